@@ -1,0 +1,163 @@
+"""Deterministic synthetic KV caches for fixtures and parity tests.
+
+Integer-only SplitMix64 stream -> uniforms with 24-bit mantissas -> an
+Irwin-Hall sum of four (approximately normal). Every step is exact IEEE
+arithmetic, so the same seed yields the same float32 bytes on any machine,
+which lets the golden fixtures store outputs only and regenerate inputs.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+_M = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+
+def splitmix64(seed: int, n: int) -> np.ndarray:
+    with np.errstate(over="ignore"):
+        i = np.arange(1, n + 1, dtype=np.uint64)
+        z = np.uint64(seed & 0xFFFFFFFFFFFFFFFF) + i * np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        z = z ^ (z >> np.uint64(31))
+    return z
+
+
+def uniform(seed: int, n: int) -> np.ndarray:
+    """Uniform in [-1, 1) with 24-bit resolution (exact float32 values)."""
+    z = splitmix64(seed, n) >> np.uint64(40)          # 24 bits
+    return (z.astype(np.float64) - 8388608.0) / 8388608.0
+
+
+def normal(seed: int, shape) -> np.ndarray:
+    n = int(np.prod(shape))
+    u = uniform(seed, 4 * n).reshape(4, n)
+    s = ((u[0] + u[1]) + u[2]) + u[3]                # exact in float64
+    return (s * 0.8660254037844386).astype(np.float32).reshape(shape)
+
+
+def kv_cache(T: int, H: int, d: int, seed: int, outliers: int = 0, channel_scale: bool = False):
+    """K, V [T x H*d] float32. outliers: that many key/value channels x8.
+    channel_scale: per-channel key scale in [0.25, 4) (log-uniform-like)."""
+    K = normal(seed * 7 + 1, (T, H * d))
+    V = normal(seed * 7 + 2, (T, H * d))
+    if channel_scale:
+        u = uniform(seed * 7 + 3, H * d)
+        scale = np.exp2(np.round(u * 8.0) / 4.0).astype(np.float32)   # 2^(k/4), k in [-8, 8]
+        K = (K * scale).astype(np.float32)
+    if outliers:
+        ch = (splitmix64(seed * 7 + 4, outliers) % np.uint64(H * d)).astype(np.int64)
+        K[:, ch] *= np.float32(8.0)
+        V[:, ch] *= np.float32(8.0)
+    return np.ascontiguousarray(K), np.ascontiguousarray(V)
+
+
+def snapkv_queries(K: np.ndarray, W: int, seed: int, noise: float = 0.1) -> np.ndarray:
+    """SnapKV window: the last W key rows plus N(0, noise^2) noise."""
+    Q = K[-W:].astype(np.float32) + (normal(seed * 7 + 5, (W, K.shape[1])) * np.float32(noise))
+    return np.ascontiguousarray(Q.astype(np.float32))
+
+
+def gen_data(n: int, seed: int) -> np.ndarray:
+    """Smooth deterministic pattern in the spirit of the reference tests'
+    sin/cos generator (tests/test-kv-compact-api.cpp:16-21), built from
+    integer arithmetic only."""
+    i = np.arange(n, dtype=np.int64)
+    a = ((i * 7 + seed) % 97).astype(np.float64) / 48.0 - 1.0
+    b = ((i * 3 + seed + 17) % 61).astype(np.float64) / 30.0 - 1.0
+    return (a + 0.3 * b).astype(np.float32)
+
+
+# --------------------------------------------------------------------------
+# Case catalogue shared by the fixture generator, the oracle tests and the
+# GPU parity tests. Each case: shape, data recipe and parameter overrides.
+# --------------------------------------------------------------------------
+
+def make_case(c: dict):
+    """Return (K, V, Q or None, n_q) for a case dict."""
+    T, H, d = c["T"], c["H"], c["d"]
+    dv = c.get("dv", d)
+    if c.get("data") == "pattern":
+        K = gen_data(T * H * d, c["seed"]).reshape(T, H * d)
+        V = gen_data(T * H * dv, c["seed"] + 500).reshape(T, H * dv)
+        nq = c.get("n_q", 0)
+        Q = gen_data(nq * H * d, c["seed"] + 900).reshape(nq, H * d) if nq else None
+        return np.ascontiguousarray(K), np.ascontiguousarray(V), Q, nq
+    K, V = kv_cache(T, H, d, c["seed"], outliers=c.get("outliers", 0),
+                    channel_scale=c.get("channel_scale", False))
+    if dv != d:
+        V = normal(c["seed"] * 7 + 9, (T, H * dv))
+    q = c.get("qref", "cheap")
+    if q == "snapkv":
+        Q = snapkv_queries(K, c.get("W", 32), c["seed"])
+        return K, V, Q, Q.shape[0]
+    if q == "random":
+        nq = c["n_q"]
+        return K, V, normal(c["seed"] * 7 + 6, (nq, H * d)), nq
+    return K, V, None, 0
+
+
+def span_classifier_spec(T: int, seed: int, frac: float = 0.3):
+    """Contiguous THINKING span [s, s + frac*T), ANSWER elsewhere."""
+    L = int(frac * T)
+    s = int(splitmix64(seed * 7 + 8, 1)[0] % np.uint64(max(T - L, 1)))
+    return s, s + L
+
+
+CASES = [
+    # name, shape, data, params
+    dict(name="cfg1_small", T=1024, H=1, d=64, seed=1, outliers=4, qref="cheap",
+         params=dict(target_ratio=0.5, use_cheap_qref=1)),
+    dict(name="cfg1_shape", T=4096, H=1, d=128, seed=2, outliers=4, qref="cheap",
+         params=dict(target_ratio=0.5, use_cheap_qref=1)),
+    dict(name="cfg2_small_div", T=1536, H=2, d=64, seed=3, channel_scale=True, qref="snapkv",
+         params=dict(target_ratio=0.2, use_diversity=1)),
+    dict(name="cfg2_small_nodiv", T=1536, H=2, d=64, seed=4, channel_scale=True, qref="snapkv",
+         params=dict(target_ratio=0.2)),
+    dict(name="unchunked_r20", T=128, H=4, d=32, seed=5, qref="random", n_q=64,
+         params=dict(target_ratio=0.2)),
+    dict(name="unchunked_r80", T=128, H=4, d=32, seed=5, qref="random", n_q=64,
+         params=dict(target_ratio=0.8)),
+    dict(name="pattern_basic", T=64, H=4, d=32, seed=1, data="pattern", n_q=32,
+         params=dict(target_ratio=0.5)),
+    dict(name="score_max", T=256, H=2, d=32, seed=6, qref="random", n_q=16,
+         params=dict(target_ratio=0.25, score_method=0)),
+    dict(name="score_mean", T=256, H=2, d=32, seed=6, qref="random", n_q=16,
+         params=dict(target_ratio=0.25, score_method=2)),
+    dict(name="prefix", T=200, H=2, d=16, seed=7, qref="random", n_q=8,
+         params=dict(target_ratio=0.3, n_shared_prefix=10)),
+    dict(name="prefix_div", T=200, H=2, d=16, seed=7, qref="random", n_q=8,
+         params=dict(target_ratio=0.3, n_shared_prefix=10, use_diversity=1)),
+    dict(name="count", T=300, H=2, d=16, seed=8, qref="random", n_q=16,
+         params=dict(target_count=40)),
+    dict(name="count_all", T=48, H=2, d=8, seed=9, qref="random", n_q=8,
+         params=dict(target_count=48)),
+    dict(name="beta_clamped", T=160, H=2, d=16, seed=10, qref="random", n_q=24,
+         params=dict(target_ratio=0.25, skip_beta=0, nnls_method=1)),
+    dict(name="beta_lh", T=160, H=2, d=16, seed=10, qref="random", n_q=24,
+         params=dict(target_ratio=0.25, skip_beta=0, nnls_method=0)),
+    dict(name="refine1", T=160, H=2, d=16, seed=11, qref="random", n_q=24,
+         params=dict(target_ratio=0.25, refine_rounds=1)),
+    dict(name="refine2_beta", T=160, H=2, d=16, seed=11, qref="random", n_q=24,
+         params=dict(target_ratio=0.25, refine_rounds=2, skip_beta=0, nnls_method=0)),
+    dict(name="chunk_explicit", T=500, H=2, d=16, seed=12, qref="random", n_q=16,
+         params=dict(target_ratio=0.5, chunk_size=200)),
+    dict(name="chunk_prefix_cheap", T=700, H=2, d=16, seed=13, qref="cheap",
+         params=dict(target_ratio=0.5, chunk_size=256, n_shared_prefix=20, use_cheap_qref=1)),
+    dict(name="rkv_span", T=640, H=2, d=32, seed=14, qref="snapkv", W=16,
+         rkv=dict(thinking=0.3, transition=0.7),
+         params=dict(target_ratio=0.5, chunk_size=256)),
+    dict(name="rkv_zero_ties", T=256, H=2, d=16, seed=15, qref="random", n_q=16,
+         rkv=dict(thinking=0.0, transition=0.0),
+         params=dict(target_ratio=0.8)),
+    dict(name="cfg5_small", T=2560, H=2, d=32, seed=16, channel_scale=True, qref="snapkv",
+         rkv=dict(thinking=0.3, transition=0.7),
+         params=dict(target_ratio=0.2, skip_beta=0, nnls_method=0, use_diversity=1, refine_rounds=1)),
+    dict(name="tiny_T1", T=1, H=1, d=4, seed=17, qref="random", n_q=2, params=dict()),
+    dict(name="tiny_T3", T=3, H=2, d=4, seed=18, qref="random", n_q=2, params=dict(target_ratio=0.9)),
+    dict(name="dv_ne_dk", T=96, H=2, d=16, dv=24, seed=19, qref="random", n_q=8,
+         params=dict(target_ratio=0.5)),
+    dict(name="unchunked_big_t", T=700, H=1, d=32, seed=20, qref="random", n_q=16,
+         params=dict(target_ratio=0.5, chunk_size=-1)),
+]
+
+CASE_BY_NAME = {c["name"]: c for c in CASES}
