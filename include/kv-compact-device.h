@@ -1,0 +1,66 @@
+/*
+ * kv-compact device-resident batch API (MI355X). Additive to the reference
+ * ABI (include/kv-compact-api.h): the reference has no counterpart; its
+ * callers loop kv_compact() over layers with host buffers (reference
+ * src/kv-compact.cpp:499-648, tests/bench-throughput-large.cpp:55-62).
+ *
+ * One call compacts L layers that share T, n_q, H, d_k, d_v and params.
+ * All pointers are device (HBM) memory. Layer l of K is K + l*ldK (elements;
+ * ldK >= T*H*d_k), likewise V/ldV and Q_ref/ldQ. Results, per layer l:
+ *   indices + l*t_total              [t_total]          kept positions, ascending
+ *   beta    + l*H*t_total            [H][t_total]
+ *   C_v     + l*H*t_total*d_v        [H][t_total][d_v]
+ *   stats   + 3*l                    avg_cosine_sim, avg_mse, avg_agreement
+ * Each layer's results equal kv_compact() on that layer bit for bit.
+ * token_weight (device float[T], may be NULL) holds the R-KV multiplier of
+ * each position; when NULL and params->reasoning has a classifier, the
+ * classifier is evaluated on the host. The call is synchronous with respect
+ * to `stream` (NULL: the library's stream). Returns the kv_compact codes.
+ */
+#pragma once
+#include "kv-compact-api.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct kvc_device_out {
+    int   * indices;
+    float * beta;
+    float * C_v;
+    float * stats;
+} kvc_device_out;
+
+/* Chunk plan of a call (same arithmetic as kv_compact): number of kept
+ * tokens per layer and number of chunks. */
+int kvc_plan(int T, int n_q, int q_ref_given, const kv_compact_params * params,
+             int * t_total, int * n_chunks);
+
+int kvc_compact_layers_device(const float * K, const float * V, const float * Q_ref,
+                              int L, int T, int n_q, int n_head_kv, int d_k, int d_v,
+                              long long ldK, long long ldV, long long ldQ,
+                              const kv_compact_params * params, const float * token_weight,
+                              kvc_device_out * out, void * stream);
+
+/* Device-resident quantized pipeline for one layer: K/V rows in the given
+ * codec (device), outputs requantized rows (device, t_total x row bytes)
+ * plus indices/beta/C_v/stats as above (L = 1). */
+int kvc_compact_quantized_device(const uint8_t * K_quant, const uint8_t * V_quant, const float * Q_ref,
+                                 int k_type, int v_type, size_t k_row_bytes, size_t v_row_bytes,
+                                 int T, int n_q, int n_head_kv, int d_k, int d_v,
+                                 const kv_compact_params * params, kvc_device_out * out,
+                                 uint8_t * K_out, uint8_t * V_out, void * stream);
+
+/* Device time in ms of each pipeline stage of the last call on the current
+ * device, measured with HIP events on that call's stream. Stages, in order:
+ * 0 scores, 1 chunk softmax + importance, 2 refit target Y = A V,
+ * 3 selection, 4 compacted softmax X, 5 normal equations, 6 elimination +
+ * back substitution, 7 quality statistics. Returns the number written. */
+int kvc_stage_times(float * out_ms, int n);
+
+/* Release the library's cached device workspace of the current device. */
+void kvc_release_workspace(void);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,74 @@
+// Shared declarations between the host orchestrator and the HIP kernels of
+// libkv-compact.so (MI355X / gfx950).
+//
+// Numerical contract: every kernel reproduces the reference CPU path's fp32
+// operation order (sequential dot products, multiply and add rounded
+// separately, the same expf/sqrtf/division semantics), so device results
+// equal the reference's bit for bit. The whole library is compiled with
+// -ffp-contract=off; division and sqrt use the correctly rounded sequences.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kvc {
+
+// How the reference queries of a chunk are obtained.
+enum QMode : int {
+    Q_PROVIDED = 0,      // caller's Q_ref rows (reference api.cpp:391-393)
+    Q_CHEAP_GLOBAL = 1,  // rows of K sampled over the whole call (api.cpp:382-390)
+    Q_CHEAP_LOCAL = 2,   // rows of K sampled inside each chunk (chunk regenerates, api.cpp:473-475)
+};
+
+// One chunk of the reference's chunk plan (api.cpp:417-499). All chunks of a
+// call share the plan; every layer of a batch uses the same plan.
+struct ChunkDesc {
+    int start;    // first token of the chunk
+    int Tc;       // tokens in the chunk
+    int tc;       // tokens kept
+    int prefix;   // forced leading positions
+    int off;      // offset of the chunk's kept tokens in the merged output
+    int nq;       // reference queries used by the chunk
+};
+
+// Geometry of a batch of layers sharing one plan.
+struct Geom {
+    int L, T, H, dk, dv;
+    int n_chunks, t_total, nq_max, tc_max, Tc_max;
+    int qmode, nq_global;       // query source; n_q of Q_CHEAP_GLOBAL/Q_PROVIDED
+    long long ldK, ldV, ldQ;    // layer strides (elements)
+    int score_method;           // 0 max, 1 rms, 2 mean
+    float inv_sqrt_dk;
+    float ridge;
+};
+
+// Device scratch for one batch (all pointers device memory).
+struct Work {
+    float * S;        // [L][H][nq_max][T]   scaled scores per chunk column range
+    float * A;        // [L][H][nq_max][T]   softmax weights
+    float * E;        // [L][H][nq_max][T]   unnormalised exp (only when beta is solved)
+    float * rowsum;   // [L][n_chunks][H][nq_max]
+    float * imp;      // [L][H][T]           per-head importance
+    float * gimp;     // [L][T]              global importance (after R-KV weights)
+    float * Y;        // [L][n_chunks][H][nq_max][dv]
+    int   * sel;      // [L][t_total]        kept token positions (layer-local), ascending
+    float * X;        // [L][H][nq_max][t_total] compacted softmax weights
+    float * aug;      // GE workspace: one [tc][tc + dv] system per (layer, chunk, head)
+    long long * aug_off; // [L][n_chunks][H] element offsets into aug
+    float * gtmp;     // [L][n_chunks][H][tc_max + tc_max + dv] GE factor / pivot-row spill
+    int   * cand;     // [L][n_chunks][Tc_max] selection candidates
+    unsigned char * flags; // [L][n_chunks][Tc_max]
+    float * wts;      // [T] R-KV weights (nullptr when disabled)
+    ChunkDesc * chunks;  // [n_chunks + 1]; the extra entry covers the whole call
+};
+
+// Statistics scratch (api.cpp:239-325 sampling: h < min(H,4), qi < min(nq,32))
+struct StatWork {
+    int mh, mq, qmode;
+    float * OS;   // [L][mh][mq][T]        original scores -> softmax
+    float * CS;   // [L][mh][mq][t_total]  compacted scores -> softmax
+    float * OO;   // [L][mh][mq][dv]
+    float * CO;   // [L][mh][mq][dv]
+};
+
+}  // namespace kvc

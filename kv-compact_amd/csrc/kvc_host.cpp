@@ -1,0 +1,1089 @@
+// Host orchestrator of libkv-compact.so: the reference's C ABI
+// (include/kv-compact-api.h, include/kv-compact-accel.h) plus the additive
+// device-resident batch API (include/kv-compact-device.h), all running on
+// the HIP kernels of kvc_kernels.hip. There is no CPU compute path: when no
+// GPU is usable the calls return KV_COMPACT_E_DEVICE.
+//
+// Call flow (reference src/kv-compact-api.cpp:360-978):
+//   validate -> params/defaults -> query source -> target count -> chunk
+//   plan -> [device] scores, chunk softmax + importance, refit target Y,
+//   global importance (+R-KV) and top-t, LS system + Gaussian elimination,
+//   quality statistics -> results.
+// Every layer of a batch and every chunk of a layer is independent, so one
+// launch of each kernel covers all (layer, chunk, head) units.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/kv-compact-api.h"
+#include "../../include/kv-compact-accel.h"
+#include "../../include/kv-compact-device.h"
+#include "kvc_common.h"
+#include "kvc_kernels.h"
+
+using namespace kvc;
+
+namespace {
+
+// ------------------------------------------------------------------ device
+
+// Pipeline stages timed with events on the call's stream (kvc_stage_times)
+enum Stage { ST_SCORES, ST_SOFTMAX, ST_REFIT, ST_SELECT, ST_LS_SOFTMAX, ST_LS_BUILD, ST_GE, ST_STATS, ST_COUNT };
+
+struct DeviceCtx {
+    std::mutex mu;
+    bool ready = false;
+    hipStream_t stream = nullptr;
+    char * arena = nullptr;
+    size_t arena_cap = 0;
+    hipEvent_t ev[ST_COUNT + 1] = {};
+    float stage_ms[ST_COUNT] = {};
+};
+
+constexpr int kMaxDevices = 64;
+DeviceCtx g_dev[kMaxDevices];
+std::mutex g_init_mu;
+
+void exp2_table(uint64_t tab[32]) {
+    // tab[i] = bits(2^(i/32) rounded to double) - (i << 47)
+    for (int i = 0; i < 32; i++) {
+        long double v = exp2l((long double)i / 32.0L);
+        double d = (double)v;
+        uint64_t b;
+        memcpy(&b, &d, 8);
+        tab[i] = b - ((uint64_t)i << 47);
+    }
+}
+
+// Returns the context of the current device, initialised, or nullptr.
+DeviceCtx * device_ctx() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    DeviceCtx * c = &g_dev[dev];
+    std::lock_guard<std::mutex> lk(g_init_mu);
+    if (!c->ready) {
+        uint64_t tab[32];
+        exp2_table(tab);
+        if (set_exp2_table(tab) != hipSuccess) return nullptr;
+        if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
+        for (int i = 0; i <= ST_COUNT; i++)
+            if (hipEventCreate(&c->ev[i]) != hipSuccess) return nullptr;
+        c->ready = true;
+    }
+    return c;
+}
+
+// Bump allocator over the device arena (256-byte aligned pieces).
+struct Carver {
+    size_t off = 0;
+    char * base = nullptr;
+    template <class T> T * take(size_t n) {
+        off = (off + 255) & ~(size_t)255;
+        T * p = base ? reinterpret_cast<T *>(base + off) : nullptr;
+        off += n * sizeof(T);
+        return p;
+    }
+};
+
+bool ensure_arena(DeviceCtx * c, size_t bytes) {
+    if (c->arena_cap >= bytes) return true;
+    if (c->arena) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(c->arena);
+        c->arena = nullptr;
+        c->arena_cap = 0;
+    }
+    size_t want = bytes + bytes / 8 + (1u << 20);
+    if (hipMalloc(&c->arena, want) != hipSuccess) {
+        (void)hipGetLastError();
+        c->arena = nullptr;
+        return false;
+    }
+    c->arena_cap = want;
+    return true;
+}
+
+bool is_device_ptr(const void * p) {
+    if (!p) return false;
+    hipPointerAttribute_t a;
+    if (hipPointerGetAttributes(&a, p) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    return a.type == hipMemoryTypeDevice;
+}
+
+double now_ms() {
+    return std::chrono::duration<double, std::milli>(
+               std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+// -------------------------------------------------------------------- plan
+
+// Reference api.cpp:382-390 (cheap query count)
+int cheap_count(int T) {
+    int n = T / 2;
+    if (n > 64) n = 64;
+    if (n < 4) n = 4;
+    if (n > T) n = T;
+    return n;
+}
+
+// Reference api.cpp:396-409 (tokens kept by one call)
+int target_count(int T, const kv_compact_params & p) {
+    int t;
+    if (p.target_count > 0) {
+        t = p.target_count < T ? p.target_count : T;
+    } else {
+        t = (int)(T * p.target_ratio);
+        if (t < 1) t = 1;
+        if (t > T) t = T;
+    }
+    if (p.n_shared_prefix > t) t = p.n_shared_prefix < T ? p.n_shared_prefix : T;
+    return t;
+}
+
+// Reference api.cpp:417-437 (auto chunk size)
+int chunk_size(int T, const kv_compact_params & p) {
+    int cs = p.chunk_size;
+    if (cs == 0) {
+        float r = (p.target_count > 0) ? (float)p.target_count / (float)T : p.target_ratio;
+        if (r <= 0.0f) r = 0.5f;
+        if (r > 1.0f) r = 1.0f;
+        int est = (int)(T * r);
+        if (est > 256) {
+            cs = (int)(256.0f / r);
+            if (cs < 64) cs = 64;
+            if (cs >= T) cs = T;
+        } else {
+            cs = T;
+        }
+    } else if (cs < 0) {
+        cs = T;
+    }
+    return cs;
+}
+
+struct Plan {
+    int T = 0, n_chunks = 0, t_total = 0, nq_max = 0, tc_max = 0, Tc_max = 0;
+    int qmode = Q_PROVIDED, nq_global = 0, stats_qmode = Q_PROVIDED;
+    std::vector<ChunkDesc> chunks;  // n_chunks + 1 (whole call last)
+};
+
+// Chunk plan of one call; the per-chunk recursion of api.cpp:466-499 is
+// unrolled here (chunk params: chunk_size -1, prefix only in chunk 0).
+void make_plan(int T, int n_q, bool q_given, const kv_compact_params & p, Plan & pl) {
+    pl.T = T;
+    const bool cheap = p.use_cheap_qref || !q_given;
+    const int nq_outer = cheap ? cheap_count(T) : n_q;
+    pl.nq_global = nq_outer;
+    pl.stats_qmode = q_given && !p.use_cheap_qref ? Q_PROVIDED : Q_CHEAP_GLOBAL;
+    const int cs = chunk_size(T, p);
+    pl.chunks.clear();
+    if (cs < T) {
+        pl.n_chunks = (T + cs - 1) / cs;
+        // inside a chunk call Q_ref is non-NULL: it regenerates only when the flag is set
+        pl.qmode = p.use_cheap_qref ? Q_CHEAP_LOCAL : (q_given ? Q_PROVIDED : Q_CHEAP_GLOBAL);
+        int off = 0;
+        for (int c = 0; c < pl.n_chunks; c++) {
+            ChunkDesc d;
+            d.start = c * cs;
+            d.Tc = std::min(T, d.start + cs) - d.start;
+            kv_compact_params cp = p;
+            cp.n_shared_prefix = (c > 0) ? 0 : std::min(p.n_shared_prefix, d.Tc);
+            d.tc = target_count(d.Tc, cp);
+            d.prefix = cp.n_shared_prefix;
+            d.nq = (pl.qmode == Q_CHEAP_LOCAL) ? cheap_count(d.Tc) : nq_outer;
+            d.off = off;
+            off += d.tc;
+            pl.chunks.push_back(d);
+        }
+        pl.t_total = off;
+    } else {
+        pl.n_chunks = 1;
+        pl.qmode = cheap ? Q_CHEAP_GLOBAL : Q_PROVIDED;
+        ChunkDesc d;
+        d.start = 0;
+        d.Tc = T;
+        d.tc = target_count(T, p);
+        d.prefix = p.n_shared_prefix;
+        d.nq = nq_outer;
+        d.off = 0;
+        pl.chunks.push_back(d);
+        pl.t_total = d.tc;
+    }
+    pl.nq_max = 0;
+    pl.tc_max = 0;
+    pl.Tc_max = 0;
+    for (const ChunkDesc & d : pl.chunks) {
+        pl.nq_max = std::max(pl.nq_max, d.nq);
+        pl.tc_max = std::max(pl.tc_max, d.tc);
+        pl.Tc_max = std::max(pl.Tc_max, d.Tc);
+    }
+    ChunkDesc whole;
+    whole.start = 0;
+    whole.Tc = T;
+    whole.tc = pl.t_total;
+    whole.prefix = 0;
+    whole.off = 0;
+    whole.nq = nq_outer;
+    pl.chunks.push_back(whole);
+}
+
+// Options this library implements; everything else is refused with -5
+// rather than computed differently.
+int check_supported(const kv_compact_params & p, int d_v) {
+    if (p.use_omp || p.use_sensitivity) return KV_COMPACT_E_UNSUPPORTED;
+    if (!p.skip_beta) return KV_COMPACT_E_UNSUPPORTED;
+    if (p.refine_rounds > 0) return KV_COMPACT_E_UNSUPPORTED;
+    if (p.use_diversity) return KV_COMPACT_E_UNSUPPORTED;
+    if (d_v > 256) return KV_COMPACT_E_UNSUPPORTED;
+    return 0;
+}
+
+// ------------------------------------------------------------ batch run
+
+struct BatchIO {
+    const float * K;   // device
+    const float * V;   // device
+    const float * Q;   // device or null
+    long long ldK, ldV, ldQ;
+    int L, T, n_q, H, dk, dv;
+    const float * wts; // device [T] or null
+    int * indices;     // device outputs
+    float * beta;
+    float * Cv;
+    float * stats;
+};
+
+struct Timing {
+    double scoring_ms = 0.0, nnls_ms = 0.0;
+};
+
+size_t workspace_bytes(const Plan & pl, const BatchIO & io, bool need_e, Carver * cv_out, Work * w, StatWork * sw) {
+    Carver cv = cv_out ? *cv_out : Carver();
+    const size_t L = io.L, H = io.H, T = io.T, nqm = pl.nq_max, nc = pl.n_chunks;
+    const size_t tt = pl.t_total, dv = io.dv;
+    Work ww{};
+    ww.S = cv.take<float>(L * H * nqm * T);
+    ww.A = cv.take<float>(L * H * nqm * T);
+    ww.E = need_e ? cv.take<float>(L * H * nqm * T) : nullptr;
+    ww.rowsum = cv.take<float>(L * nc * H * nqm);
+    ww.imp = cv.take<float>(L * H * T);
+    ww.gimp = cv.take<float>(L * T);
+    ww.Y = cv.take<float>(L * nc * H * nqm * dv);
+    ww.sel = nullptr;
+    ww.X = cv.take<float>(L * H * nqm * tt);
+    size_t aug_elems = 0;
+    for (int c = 0; c < pl.n_chunks; c++) aug_elems += (size_t)pl.chunks[c].tc * (pl.chunks[c].tc + dv);
+    ww.aug = cv.take<float>(L * H * aug_elems);
+    ww.aug_off = cv.take<long long>(L * nc * H);
+    ww.gtmp = cv.take<float>(L * nc * H * (2 * (size_t)pl.tc_max + dv));
+    ww.cand = cv.take<int>(L * nc * (size_t)pl.Tc_max);
+    ww.flags = cv.take<unsigned char>(L * nc * (size_t)pl.Tc_max);
+    ww.chunks = cv.take<ChunkDesc>(pl.chunks.size());
+    StatWork s{};
+    s.mh = std::min(io.H, 4);
+    s.mq = std::min(pl.nq_global, 32);
+    s.qmode = pl.stats_qmode;
+    s.OS = cv.take<float>(L * s.mh * s.mq * T);
+    s.CS = cv.take<float>(L * s.mh * s.mq * std::max<size_t>(tt, 1));
+    s.OO = cv.take<float>(L * s.mh * s.mq * dv);
+    s.CO = cv.take<float>(L * s.mh * s.mq * dv);
+    if (w) *w = ww;
+    if (sw) *sw = s;
+    if (cv_out) *cv_out = cv;
+    return cv.off + 256;
+}
+
+int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact_params & p,
+              const BatchIO & io, Carver & carver, Timing * tm) {
+    const bool need_e = !p.skip_beta;
+    Work w{};
+    StatWork sw{};
+    workspace_bytes(pl, io, need_e, &carver, &w, &sw);
+    w.sel = io.indices;
+    w.wts = const_cast<float *>(io.wts);
+    (void)ctx;
+
+    Geom g{};
+    g.L = io.L; g.T = io.T; g.H = io.H; g.dk = io.dk; g.dv = io.dv;
+    g.n_chunks = pl.n_chunks; g.t_total = pl.t_total; g.nq_max = pl.nq_max;
+    g.tc_max = pl.tc_max; g.Tc_max = pl.Tc_max;
+    g.qmode = pl.qmode; g.nq_global = pl.nq_global;
+    g.ldK = io.ldK; g.ldV = io.ldV; g.ldQ = io.ldQ;
+    g.score_method = p.score_method;
+    g.inv_sqrt_dk = 1.0f / sqrtf((float)io.dk);
+    g.ridge = p.ridge;
+
+    // aug offsets: [L][n_chunks][H]
+    std::vector<long long> aug_off((size_t)io.L * pl.n_chunks * io.H);
+    {
+        long long o = 0;
+        for (int l = 0; l < io.L; l++)
+            for (int c = 0; c < pl.n_chunks; c++)
+                for (int h = 0; h < io.H; h++) {
+                    aug_off[((size_t)l * pl.n_chunks + c) * io.H + h] = o;
+                    o += (long long)pl.chunks[c].tc * (pl.chunks[c].tc + io.dv);
+                }
+    }
+    if (hipMemcpyAsync(w.chunks, pl.chunks.data(), pl.chunks.size() * sizeof(ChunkDesc),
+                       hipMemcpyHostToDevice, st) != hipSuccess) return KV_COMPACT_E_DEVICE;
+    if (hipMemcpyAsync(w.aug_off, aug_off.data(), aug_off.size() * sizeof(long long),
+                       hipMemcpyHostToDevice, st) != hipSuccess) return KV_COMPACT_E_DEVICE;
+
+    hipEvent_t * ev = ctx->ev;
+    (void)hipEventRecord(ev[0], st);
+    // 1. scores for every (layer, chunk, head)
+    launch_scores(g, w.chunks, pl.n_chunks, pl.Tc_max, io.K, io.Q, w.S, io.H, pl.nq_max,
+                  (long long)io.H * pl.nq_max * io.T, (long long)pl.nq_max * io.T, io.T, pl.qmode, st);
+    (void)hipEventRecord(ev[ST_SCORES + 1], st);
+    // 2. chunk softmax + per-head importance
+    launch_chunk_softmax(g, w, st);
+    (void)hipEventRecord(ev[ST_SOFTMAX + 1], st);
+    // 3. refit target Y = A V
+    launch_refit_target(g, w, io.V, st);
+    (void)hipEventRecord(ev[ST_REFIT + 1], st);
+    // 4. global importance (+R-KV) and top-t
+    launch_select_topk(g, w, st);
+    (void)hipEventRecord(ev[ST_SELECT + 1], st);
+    // 5. beta (skip_beta: zeros), X = softmax(S[:, sel] + beta)
+    if (hipMemsetAsync(io.beta, 0, (size_t)io.L * io.H * pl.t_total * sizeof(float), st) != hipSuccess)
+        return KV_COMPACT_E_DEVICE;
+    launch_ls_softmax(g, w, io.beta, st);
+    (void)hipEventRecord(ev[ST_LS_SOFTMAX + 1], st);
+    // 6. normal equations and their solution
+    launch_ls_build(g, w, st);
+    (void)hipEventRecord(ev[ST_LS_BUILD + 1], st);
+    launch_ge(g, w, io.Cv, st);
+    (void)hipEventRecord(ev[ST_GE + 1], st);
+    // 7. quality statistics against the full call
+    launch_stats(g, w, sw, io.K, io.V, io.Q, io.beta, io.Cv, io.stats, st);
+    (void)hipEventRecord(ev[ST_STATS + 1], st);
+
+    hipError_t err = hipGetLastError();
+    if (err == hipSuccess) err = hipStreamSynchronize(st);
+    if (err != hipSuccess) {
+        fprintf(stderr, "[kv-compact] HIP error: %s\n", hipGetErrorString(err));
+        return KV_COMPACT_E_DEVICE;
+    }
+    for (int i = 0; i < ST_COUNT; i++) {
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
+        ctx->stage_ms[i] = ms;
+    }
+    if (tm) {
+        tm->scoring_ms = ctx->stage_ms[ST_SCORES] + ctx->stage_ms[ST_SOFTMAX] + ctx->stage_ms[ST_SELECT];
+        tm->nnls_ms = ctx->stage_ms[ST_REFIT] + ctx->stage_ms[ST_LS_SOFTMAX] + ctx->stage_ms[ST_LS_BUILD] +
+                      ctx->stage_ms[ST_GE];
+    }
+    return 0;
+}
+
+// Host-evaluated R-KV weights (api.cpp:668-684) for positions [0, T)
+bool rkv_weights(const kv_compact_params & p, int T, std::vector<float> & w) {
+    if (!p.reasoning || !p.reasoning->classifier) return false;
+    const kv_compact_reasoning * r = p.reasoning;
+    w.resize(T);
+    for (int j = 0; j < T; j++) {
+        int ty = r->classifier(j + r->token_offset, r->classifier_data);
+        float x = 1.0f;
+        if (ty == KV_TOKEN_THINKING) x = r->thinking_weight;
+        else if (ty == KV_TOKEN_TRANSITION) x = r->transition_weight;
+        w[j] = x;
+    }
+    return true;
+}
+
+int validate(const float * K, const float * V, const void * res, int T, int n_q, int H, int dk, int dv,
+             const float * Q, const kv_compact_params & p) {
+    if (!K || !V || !res) return -1;
+    if (T <= 0 || H <= 0 || dk <= 0 || dv <= 0) return -2;
+    if (!(p.use_cheap_qref || !Q) && n_q <= 0) return -2;
+    return 0;
+}
+
+// Device-resident outputs of one layer copied into a malloc'd host result.
+void fill_result(kv_compact_result * r, int t, int H, int dv, const std::vector<int> & idx,
+                 const std::vector<float> & beta, const std::vector<float> & cv) {
+    r->t = t;
+    r->n_head_kv = H;
+    r->selected_indices = (int *)malloc((size_t)std::max(t, 1) * sizeof(int));
+    memcpy(r->selected_indices, idx.data(), (size_t)t * sizeof(int));
+    r->beta = (float **)malloc((size_t)H * sizeof(float *));
+    r->C_v = (float **)malloc((size_t)H * sizeof(float *));
+    for (int h = 0; h < H; h++) {
+        r->beta[h] = (float *)malloc((size_t)std::max(t, 1) * sizeof(float));
+        memcpy(r->beta[h], beta.data() + (size_t)h * t, (size_t)t * sizeof(float));
+        r->C_v[h] = (float *)malloc((size_t)std::max(t, 1) * dv * sizeof(float));
+        memcpy(r->C_v[h], cv.data() + (size_t)h * t * dv, (size_t)t * dv * sizeof(float));
+    }
+}
+
+// One layer with host or device inputs; results to host (kv_compact()).
+int compact_one(const float * K, const float * V, const float * Q, int T, int n_q, int H, int dk, int dv,
+                const kv_compact_params & p, kv_compact_result * res, std::vector<float> * K_keep = nullptr) {
+    (void)K_keep;
+    const double t0 = now_ms();
+    DeviceCtx * ctx = device_ctx();
+    if (!ctx) return KV_COMPACT_E_DEVICE;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipStream_t st = ctx->stream;
+    Plan pl;
+    const bool q_given = Q != nullptr;
+    make_plan(T, n_q, q_given, p, pl);
+    const long long ek = (long long)H * dk, ev = (long long)H * dv;
+    const bool kd = is_device_ptr(K), vd = is_device_ptr(V), qd = q_given && is_device_ptr(Q);
+    const bool use_q = q_given && !p.use_cheap_qref;
+    std::vector<float> wts;
+    const bool have_w = rkv_weights(p, T, wts);
+
+    BatchIO io{};
+    io.L = 1; io.T = T; io.n_q = n_q; io.H = H; io.dk = dk; io.dv = dv;
+    io.ldK = (long long)T * ek; io.ldV = (long long)T * ev; io.ldQ = (long long)std::max(n_q, 1) * ek;
+
+    // size the arena: inputs + outputs + workspace
+    Carver sizer;
+    float * dK = kd ? nullptr : sizer.take<float>((size_t)T * ek);
+    float * dV = vd ? nullptr : sizer.take<float>((size_t)T * ev);
+    float * dQ = (use_q && !qd) ? sizer.take<float>((size_t)n_q * ek) : nullptr;
+    float * dW = have_w ? sizer.take<float>(T) : nullptr;
+    int * dI = sizer.take<int>(std::max(pl.t_total, 1));
+    float * dB = sizer.take<float>((size_t)H * std::max(pl.t_total, 1));
+    float * dC = sizer.take<float>((size_t)H * std::max(pl.t_total, 1) * dv);
+    float * dS = sizer.take<float>(3);
+    (void)dK; (void)dV; (void)dQ; (void)dW; (void)dI; (void)dB; (void)dC; (void)dS;
+    size_t need = workspace_bytes(pl, io, !p.skip_beta, &sizer, nullptr, nullptr);
+    if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
+
+    Carver cv;
+    cv.base = ctx->arena;
+    float * K_dev = kd ? const_cast<float *>(K) : cv.take<float>((size_t)T * ek);
+    float * V_dev = vd ? const_cast<float *>(V) : cv.take<float>((size_t)T * ev);
+    float * Q_dev = nullptr;
+    if (use_q) Q_dev = qd ? const_cast<float *>(Q) : cv.take<float>((size_t)n_q * ek);
+    float * W_dev = have_w ? cv.take<float>(T) : nullptr;
+    io.indices = cv.take<int>(std::max(pl.t_total, 1));
+    io.beta = cv.take<float>((size_t)H * std::max(pl.t_total, 1));
+    io.Cv = cv.take<float>((size_t)H * std::max(pl.t_total, 1) * dv);
+    io.stats = cv.take<float>(3);
+    hipError_t e = hipSuccess;
+    if (!kd) e = hipMemcpyAsync(K_dev, K, (size_t)T * ek * sizeof(float), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess && !vd) e = hipMemcpyAsync(V_dev, V, (size_t)T * ev * sizeof(float), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess && use_q && !qd) e = hipMemcpyAsync(Q_dev, Q, (size_t)n_q * ek * sizeof(float), hipMemcpyHostToDevice, st);
+    if (e == hipSuccess && have_w) e = hipMemcpyAsync(W_dev, wts.data(), (size_t)T * sizeof(float), hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
+    io.K = K_dev; io.V = V_dev; io.Q = Q_dev; io.wts = W_dev;
+
+    Timing tm;
+    int rc = run_batch(ctx, st, pl, p, io, cv, &tm);
+    if (rc != 0) return rc;
+
+    const int t = pl.t_total;
+    std::vector<int> idx(t);
+    std::vector<float> beta((size_t)H * t), cvh((size_t)H * t * dv);
+    float stats[3];
+    e = hipMemcpy(idx.data(), io.indices, (size_t)t * sizeof(int), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(beta.data(), io.beta, beta.size() * sizeof(float), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(cvh.data(), io.Cv, cvh.size() * sizeof(float), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(stats, io.stats, sizeof(stats), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
+    fill_result(res, t, H, dv, idx, beta, cvh);
+    res->stats.avg_cosine_sim = stats[0];
+    res->stats.avg_mse = stats[1];
+    res->stats.avg_agreement = stats[2];
+    res->stats.scoring_ms = tm.scoring_ms;
+    res->stats.nnls_ms = tm.nnls_ms;
+    res->stats.elapsed_ms = now_ms() - t0;
+    return 0;
+}
+
+kv_compact_params defaults() {
+    kv_compact_params p;
+    memset(&p, 0, sizeof(p));
+    p.target_ratio = 0.5f;
+    p.ridge = 1e-6f;
+    p.nnls_max_iter = 200;
+    p.diversity_strength = 0.5f;
+    p.skip_beta = 1;
+    p.score_method = 1;
+    p.omp_k_choice = 1;
+    p.omp_refit_interval = 1;
+    p.nnls_method = 1;
+    return p;
+}
+
+// Reference state.h:326-352 (row geometry of the codecs)
+int block_bytes(int type) {
+    if (type == KV_TYPE_F32) return 4;
+    if (type == KV_TYPE_F16) return 2;
+    if (type == KV_TYPE_Q8_0) return 34;
+    if (type == KV_TYPE_Q4_0) return 18;
+    if (type == KV_TYPE_Q4_1) return 20;
+    return 4;
+}
+bool is_block_type(int t) { return t == KV_TYPE_Q8_0 || t == KV_TYPE_Q4_0 || t == KV_TYPE_Q4_1; }
+bool known_type(int t) { return t == KV_TYPE_F32 || t == KV_TYPE_F16 || is_block_type(t); }
+
+}  // namespace
+
+// ======================================================================
+// Reference C ABI
+// ======================================================================
+extern "C" {
+
+kv_compact_params kv_compact_params_default(void) { return defaults(); }
+
+int kv_compact(const float * K_all, const float * V_all, const float * Q_ref_all,
+               int T, int n_q, int n_head_kv, int d_k, int d_v,
+               const kv_compact_params * params, kv_compact_result * result) {
+    kv_compact_params p = params ? *params : defaults();
+    int rc = validate(K_all, V_all, result, T, n_q, n_head_kv, d_k, d_v, Q_ref_all, p);
+    if (rc) return rc;
+    rc = check_supported(p, d_v);
+    if (rc) return rc;
+    return compact_one(K_all, V_all, Q_ref_all, T, n_q, n_head_kv, d_k, d_v, p, result);
+}
+
+void kv_compact_result_free(kv_compact_result * r) {
+    if (!r) return;
+    free(r->selected_indices);
+    r->selected_indices = NULL;
+    if (r->beta) {
+        for (int h = 0; h < r->n_head_kv; h++) free(r->beta[h]);
+        free(r->beta);
+        r->beta = NULL;
+    }
+    if (r->C_v) {
+        for (int h = 0; h < r->n_head_kv; h++) free(r->C_v[h]);
+        free(r->C_v);
+        r->C_v = NULL;
+    }
+    r->t = 0;
+    r->n_head_kv = 0;
+}
+
+// Reference api.cpp:980-1111: repeated compaction of the previous round's
+// kept keys and refitted values; indices map back to the original positions.
+int kv_compact_multi_round(const float * K_all, const float * V_all, const float * Q_ref_all,
+                           int T, int n_q, int n_head_kv, int d_k, int d_v,
+                           const kv_compact_params * params, int n_rounds,
+                           kv_compact_result * result, kv_compact_stats * per_round_stats) {
+    if (!K_all || !V_all || !result) return -1;
+    if (T <= 0 || n_head_kv <= 0 || d_k <= 0 || d_v <= 0) return -2;
+    if (n_rounds < 1) return -3;
+    kv_compact_params pc = params ? *params : defaults();
+    if (!Q_ref_all && !pc.use_cheap_qref) return -1;
+    if (Q_ref_all && n_q <= 0 && !pc.use_cheap_qref) return -2;
+    int rc = check_supported(pc, d_v);
+    if (rc) return rc;
+    const int H = n_head_kv;
+    const size_t ek = (size_t)H * d_k, ev = (size_t)H * d_v;
+    // host copies: rounds chain on small compacted caches
+    std::vector<float> Kh((size_t)T * ek), Vh((size_t)T * ev);
+    if (is_device_ptr(K_all)) {
+        if (hipMemcpy(Kh.data(), K_all, Kh.size() * 4, hipMemcpyDeviceToHost) != hipSuccess) return KV_COMPACT_E_DEVICE;
+    } else {
+        memcpy(Kh.data(), K_all, Kh.size() * 4);
+    }
+    if (is_device_ptr(V_all)) {
+        if (hipMemcpy(Vh.data(), V_all, Vh.size() * 4, hipMemcpyDeviceToHost) != hipSuccess) return KV_COMPACT_E_DEVICE;
+    } else {
+        memcpy(Vh.data(), V_all, Vh.size() * 4);
+    }
+    std::vector<float> Qh;
+    const float * Qm = Q_ref_all;
+    int nqm = n_q;
+    if (pc.use_cheap_qref || !Q_ref_all) {
+        nqm = cheap_count(T);
+        Qh.resize((size_t)nqm * ek);
+        for (int qi = 0; qi < nqm; qi++) {
+            float f = (float)(qi + 1) / (float)(nqm + 1);
+            f = f * f;
+            int pos = (int)(f * (T - 1));
+            pos = std::min(std::max(pos, 0), T - 1);
+            memcpy(Qh.data() + (size_t)qi * ek, Kh.data() + (size_t)pos * ek, ek * 4);
+        }
+        Qm = Qh.data();
+    } else if (is_device_ptr(Q_ref_all)) {
+        Qh.resize((size_t)n_q * ek);
+        if (hipMemcpy(Qh.data(), Q_ref_all, Qh.size() * 4, hipMemcpyDeviceToHost) != hipSuccess) return KV_COMPACT_E_DEVICE;
+        Qm = Qh.data();
+    }
+    std::vector<int> orig(T);
+    for (int i = 0; i < T; i++) orig[i] = i;
+    std::vector<float> cK = Kh, cV = Vh;
+    int cT = T;
+    for (int round = 0; round < n_rounds; round++) {
+        const int nqr = std::min(nqm, cT);
+        kv_compact_result rr;
+        memset(&rr, 0, sizeof(rr));
+        rc = kv_compact(cK.data(), cV.data(), Qm, cT, nqr, H, d_k, d_v, params, &rr);
+        if (rc != 0) {
+            kv_compact_result_free(&rr);
+            return rc;
+        }
+        if (per_round_stats) per_round_stats[round] = rr.stats;
+        const int nT = rr.t;
+        std::vector<int> norig(nT);
+        std::vector<float> nK((size_t)nT * ek), nV((size_t)nT * ev);
+        for (int j = 0; j < nT; j++) {
+            const int src = rr.selected_indices[j];
+            norig[j] = orig[src];
+            memcpy(nK.data() + (size_t)j * ek, cK.data() + (size_t)src * ek, ek * 4);
+            for (int h = 0; h < H; h++)
+                memcpy(nV.data() + (size_t)j * ev + (size_t)h * d_v, rr.C_v[h] + (size_t)j * d_v, (size_t)d_v * 4);
+        }
+        if (round == n_rounds - 1) {
+            std::vector<float> b((size_t)H * nT), c((size_t)H * nT * d_v);
+            for (int h = 0; h < H; h++) {
+                memcpy(b.data() + (size_t)h * nT, rr.beta[h], (size_t)nT * 4);
+                memcpy(c.data() + (size_t)h * nT * d_v, rr.C_v[h], (size_t)nT * d_v * 4);
+            }
+            fill_result(result, nT, H, d_v, norig, b, c);
+            result->stats = rr.stats;
+        }
+        kv_compact_result_free(&rr);
+        cK.swap(nK);
+        cV.swap(nV);
+        orig.swap(norig);
+        cT = nT;
+    }
+    // final statistics against the original cache, on the GPU: evaluate the
+    // result as a one-chunk call over the original data
+    {
+        DeviceCtx * ctx = device_ctx();
+        if (!ctx) return KV_COMPACT_E_DEVICE;
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        hipStream_t st = ctx->stream;
+        Plan pl;
+        kv_compact_params sp = pc;
+        sp.chunk_size = -1;
+        make_plan(T, nqm, true, sp, pl);
+        pl.t_total = result->t;
+        pl.chunks.back().tc = result->t;
+        BatchIO io{};
+        io.L = 1; io.T = T; io.n_q = nqm; io.H = H; io.dk = d_k; io.dv = d_v;
+        io.ldK = (long long)T * ek; io.ldV = (long long)T * ev; io.ldQ = (long long)nqm * ek;
+        Carver sizer;
+        sizer.take<float>((size_t)T * ek); sizer.take<float>((size_t)T * ev); sizer.take<float>((size_t)nqm * ek);
+        sizer.take<int>(std::max(result->t, 1)); sizer.take<float>((size_t)H * result->t);
+        sizer.take<float>((size_t)H * result->t * d_v); sizer.take<float>(3);
+        size_t need = workspace_bytes(pl, io, false, &sizer, nullptr, nullptr);
+        if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
+        Carver cv;
+        cv.base = ctx->arena;
+        float * dK = cv.take<float>((size_t)T * ek);
+        float * dV = cv.take<float>((size_t)T * ev);
+        float * dQ = cv.take<float>((size_t)nqm * ek);
+        int * dI = cv.take<int>(std::max(result->t, 1));
+        float * dB = cv.take<float>((size_t)H * result->t);
+        float * dC = cv.take<float>((size_t)H * result->t * d_v);
+        float * dS = cv.take<float>(3);
+        Work w{};
+        StatWork sw{};
+        workspace_bytes(pl, io, false, &cv, &w, &sw);
+        sw.qmode = Q_PROVIDED;
+        std::vector<float> b((size_t)H * result->t), c((size_t)H * result->t * d_v);
+        for (int h = 0; h < H; h++) {
+            memcpy(b.data() + (size_t)h * result->t, result->beta[h], (size_t)result->t * 4);
+            memcpy(c.data() + (size_t)h * result->t * d_v, result->C_v[h], (size_t)result->t * d_v * 4);
+        }
+        hipError_t e = hipMemcpyAsync(dK, Kh.data(), Kh.size() * 4, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(dV, Vh.data(), Vh.size() * 4, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(dQ, Qm, (size_t)nqm * ek * 4, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(dI, result->selected_indices, (size_t)result->t * 4, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(dB, b.data(), b.size() * 4, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(dC, c.data(), c.size() * 4, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(w.chunks, pl.chunks.data(), pl.chunks.size() * sizeof(ChunkDesc), hipMemcpyHostToDevice, st);
+        if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
+        Geom g{};
+        g.L = 1; g.T = T; g.H = H; g.dk = d_k; g.dv = d_v;
+        g.n_chunks = pl.n_chunks; g.t_total = result->t; g.nq_max = pl.nq_max;
+        g.tc_max = pl.tc_max; g.Tc_max = pl.Tc_max; g.qmode = Q_PROVIDED; g.nq_global = nqm;
+        g.ldK = io.ldK; g.ldV = io.ldV; g.ldQ = io.ldQ;
+        g.score_method = pc.score_method; g.inv_sqrt_dk = 1.0f / sqrtf((float)d_k); g.ridge = pc.ridge;
+        w.sel = dI;
+        launch_stats(g, w, sw, dK, dV, dQ, dB, dC, dS, st);
+        float s3[3];
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipMemcpyAsync(s3, dS, sizeof(s3), hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
+        result->stats.avg_cosine_sim = s3[0];
+        result->stats.avg_mse = s3[1];
+        result->stats.avg_agreement = s3[2];
+    }
+    return 0;
+}
+
+// ---- codec (reference api.cpp:1150-1180; state.h:326-629) ----
+
+int kv_quant_row_elements(int type, size_t row_bytes) {
+    if (type == KV_TYPE_F32) return (int)(row_bytes / 4);
+    if (type == KV_TYPE_F16) return (int)(row_bytes / 2);
+    if (is_block_type(type)) return (int)(row_bytes / (size_t)block_bytes(type)) * 32;
+    return (int)(row_bytes / 4);
+}
+
+size_t kv_quant_row_bytes(int type, int n_elements) {
+    if (type == KV_TYPE_F32) return (size_t)n_elements * 4;
+    if (type == KV_TYPE_F16) return (size_t)n_elements * 2;
+    if (is_block_type(type)) return (size_t)(n_elements / 32) * (size_t)block_bytes(type);
+    return (size_t)n_elements * 4;
+}
+
+int kv_dequantize_row(const uint8_t * src, int type, size_t row_bytes, float * dst, int max_elements) {
+    int n = kv_quant_row_elements(type, row_bytes);
+    if (n > max_elements) n = max_elements;
+    if (n <= 0) return n;
+    if (!known_type(type)) {
+        memset(dst, 0, (size_t)n * sizeof(float));
+        return n;
+    }
+    DeviceCtx * ctx = device_ctx();
+    if (!ctx) return KV_COMPACT_E_DEVICE;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const int n_conv = is_block_type(type) ? (n / 32) * 32 : n;
+    if (!ensure_arena(ctx, row_bytes + (size_t)n * 4 + 4096)) return KV_COMPACT_E_DEVICE;
+    uint8_t * ds = reinterpret_cast<uint8_t *>(ctx->arena);
+    float * dd = reinterpret_cast<float *>(ctx->arena + ((row_bytes + 255) & ~(size_t)255));
+    hipStream_t st = ctx->stream;
+    if (hipMemcpyAsync(ds, src, row_bytes, hipMemcpyHostToDevice, st) != hipSuccess) return KV_COMPACT_E_DEVICE;
+    if (n_conv > 0) launch_dequant_rows(ds, type, (long long)row_bytes, n_conv, 1, dd, st);
+    if (n_conv > 0 && hipMemcpyAsync(dst, dd, (size_t)n_conv * 4, hipMemcpyDeviceToHost, st) != hipSuccess)
+        return KV_COMPACT_E_DEVICE;
+    if (hipStreamSynchronize(st) != hipSuccess) return KV_COMPACT_E_DEVICE;
+    return n;
+}
+
+size_t kv_quantize_row(const float * src, int type, int n_elements, uint8_t * dst) {
+    if (!known_type(type) || n_elements <= 0) return 0;
+    const size_t nb = kv_quant_row_bytes(type, n_elements);
+    if (nb == 0) return 0;
+    DeviceCtx * ctx = device_ctx();
+    if (!ctx) return 0;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    if (!ensure_arena(ctx, (size_t)n_elements * 4 + nb + 4096)) return 0;
+    float * ds = reinterpret_cast<float *>(ctx->arena);
+    uint8_t * dd = reinterpret_cast<uint8_t *>(ctx->arena + (((size_t)n_elements * 4 + 255) & ~(size_t)255));
+    hipStream_t st = ctx->stream;
+    if (hipMemcpyAsync(ds, src, (size_t)n_elements * 4, hipMemcpyHostToDevice, st) != hipSuccess) return 0;
+    const int n_conv = is_block_type(type) ? (n_elements / 32) * 32 : n_elements;
+    launch_quant_rows(ds, 0, nullptr, type, n_conv, 1, dd, (long long)nb, st);
+    if (hipMemcpyAsync(dst, dd, nb, hipMemcpyDeviceToHost, st) != hipSuccess) return 0;
+    if (hipStreamSynchronize(st) != hipSuccess) return 0;
+    return nb;
+}
+
+// Reference api.cpp:1182-1257: dequantize on the device, compact, requantize
+// the kept original K rows and the refitted V rows on the device.
+int kv_compact_quantized(const uint8_t * K_quant, const uint8_t * V_quant, const float * Q_ref_all,
+                         int k_type, int v_type, size_t k_row_bytes, size_t v_row_bytes,
+                         int T, int n_q, int n_head_kv, int d_k, int d_v,
+                         const kv_compact_params * params, kv_compact_quant_result * result) {
+    if (!K_quant || !V_quant || !result) return -1;
+    if (T <= 0 || n_head_kv <= 0 || d_k <= 0 || d_v <= 0) return -2;
+    const int H = n_head_kv;
+    const int ek = H * d_k, ev = H * d_v;
+    if (kv_quant_row_elements(k_type, k_row_bytes) != ek || kv_quant_row_elements(v_type, v_row_bytes) != ev)
+        return -4;
+    kv_compact_params p = params ? *params : defaults();
+    int rc = validate((const float *)K_quant, (const float *)V_quant, result, T, n_q, H, d_k, d_v, Q_ref_all, p);
+    if (rc) return rc;
+    memset(&result->base, 0, sizeof(result->base));
+    rc = check_supported(p, d_v);
+    if (rc) return rc;
+    if (!known_type(k_type) || !known_type(v_type)) return KV_COMPACT_E_UNSUPPORTED;
+    float * dKf = nullptr;
+    float * dVf = nullptr;
+    uint8_t * dKq = nullptr;
+    uint8_t * dVq = nullptr;
+    {
+        DeviceCtx * ctx = device_ctx();
+        if (!ctx) return KV_COMPACT_E_DEVICE;
+        hipStream_t st = ctx->stream;
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        // dequantized cache lives in its own allocation for the compaction call
+        if (hipMalloc(&dKf, (size_t)T * ek * 4) != hipSuccess || hipMalloc(&dVf, (size_t)T * ev * 4) != hipSuccess ||
+            hipMalloc(&dKq, (size_t)T * k_row_bytes) != hipSuccess || hipMalloc(&dVq, (size_t)T * v_row_bytes) != hipSuccess) {
+            (void)hipGetLastError();
+            (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dKq); (void)hipFree(dVq);
+            return KV_COMPACT_E_DEVICE;
+        }
+        hipError_t e = hipMemcpyAsync(dKq, K_quant, (size_t)T * k_row_bytes, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(dVq, V_quant, (size_t)T * v_row_bytes, hipMemcpyHostToDevice, st);
+        if (e == hipSuccess) {
+            launch_dequant_rows(dKq, k_type, (long long)k_row_bytes, ek, T, dKf, st);
+            launch_dequant_rows(dVq, v_type, (long long)v_row_bytes, ev, T, dVf, st);
+            e = hipStreamSynchronize(st);
+        }
+        if (e != hipSuccess) {
+            (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dKq); (void)hipFree(dVq);
+            return KV_COMPACT_E_DEVICE;
+        }
+    }
+    rc = compact_one(dKf, dVf, Q_ref_all, T, n_q, H, d_k, d_v, p, &result->base);
+    if (rc != 0) {
+        (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dKq); (void)hipFree(dVq);
+        return rc;
+    }
+    const int t = result->base.t;
+    result->k_type = k_type;
+    result->v_type = v_type;
+    result->k_row_bytes = k_row_bytes;
+    result->v_row_bytes = v_row_bytes;
+    result->K_out = (uint8_t *)malloc((size_t)std::max(t, 1) * k_row_bytes);
+    result->V_out = (uint8_t *)malloc((size_t)std::max(t, 1) * v_row_bytes);
+    DeviceCtx * ctx = device_ctx();
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipStream_t st = ctx->stream;
+    int * dIdx = nullptr;
+    float * dCv = nullptr;
+    float * dRows = nullptr;
+    uint8_t * dKo = nullptr;
+    uint8_t * dVo = nullptr;
+    hipError_t e = hipMalloc(&dIdx, (size_t)std::max(t, 1) * 4);
+    if (e == hipSuccess) e = hipMalloc(&dCv, (size_t)std::max(t, 1) * ev * 4);
+    if (e == hipSuccess) e = hipMalloc(&dRows, (size_t)std::max(t, 1) * ev * 4);
+    if (e == hipSuccess) e = hipMalloc(&dKo, (size_t)std::max(t, 1) * k_row_bytes);
+    if (e == hipSuccess) e = hipMalloc(&dVo, (size_t)std::max(t, 1) * v_row_bytes);
+    if (e == hipSuccess) e = hipMemcpyAsync(dIdx, result->base.selected_indices, (size_t)t * 4, hipMemcpyHostToDevice, st);
+    for (int h = 0; h < H && e == hipSuccess; h++)
+        e = hipMemcpyAsync(dCv + (size_t)h * t * d_v, result->base.C_v[h], (size_t)t * d_v * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess && t > 0) {
+        launch_quant_rows(dKf, ek, dIdx, k_type, ek, t, dKo, (long long)k_row_bytes, st);
+        launch_gather_cv_rows(dCv, H, t, d_v, dRows, st);
+        launch_quant_rows(dRows, ev, nullptr, v_type, ev, t, dVo, (long long)v_row_bytes, st);
+        e = hipMemcpyAsync(result->K_out, dKo, (size_t)t * k_row_bytes, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipMemcpyAsync(result->V_out, dVo, (size_t)t * v_row_bytes, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+    }
+    (void)hipFree(dIdx); (void)hipFree(dCv); (void)hipFree(dRows); (void)hipFree(dKo); (void)hipFree(dVo);
+    (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dKq); (void)hipFree(dVq);
+    return e == hipSuccess ? 0 : KV_COMPACT_E_DEVICE;
+}
+
+void kv_compact_quant_result_free(kv_compact_quant_result * r) {
+    if (!r) return;
+    kv_compact_result_free(&r->base);
+    free(r->K_out);
+    r->K_out = NULL;
+    free(r->V_out);
+    r->V_out = NULL;
+}
+
+// ======================================================================
+// Accelerator plug-in ABI (reference include/kv-compact-accel.h)
+// ======================================================================
+
+int kv_compact_hip_available(void) { return device_ctx() ? 1 : 0; }
+
+int kv_compact_hip_mat_mul_ABt_scaled(const float * A, const float * B, float * C, int m, int n, int k,
+                                      float scale) {
+    DeviceCtx * ctx = device_ctx();
+    if (!ctx || m <= 0 || n <= 0 || k <= 0) return -1;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const size_t sa = (size_t)m * k, sb = (size_t)n * k, sc = (size_t)m * n;
+    if (!ensure_arena(ctx, (sa + sb + sc) * 4 + 1024)) return -1;
+    Carver cv;
+    cv.base = ctx->arena;
+    float * dA = cv.take<float>(sa);
+    float * dB = cv.take<float>(sb);
+    float * dC = cv.take<float>(sc);
+    hipStream_t st = ctx->stream;
+    hipError_t e = hipMemcpyAsync(dA, A, sa * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(dB, B, sb * 4, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return -1;
+    launch_gemm_abt(dA, k, dB, k, dC, n, m, n, k, scale, 0, 0, 0, 1, st);
+    e = hipMemcpyAsync(C, dC, sc * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return e == hipSuccess ? 0 : -1;
+}
+
+int kv_compact_hip_score_all_heads(const float * Q_ref, const float * K_all, float ** scores_out,
+                                   int n_q, int T, int n_head_kv, int d_k, float scale) {
+    DeviceCtx * ctx = device_ctx();
+    if (!ctx || n_q <= 0 || T <= 0 || n_head_kv <= 0 || d_k <= 0) return -1;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const size_t ek = (size_t)n_head_kv * d_k;
+    const size_t sq = (size_t)n_q * ek, sk = (size_t)T * ek, ss = (size_t)n_head_kv * n_q * T;
+    if (!ensure_arena(ctx, (sq + sk + ss) * 4 + 1024)) return -1;
+    Carver cv;
+    cv.base = ctx->arena;
+    float * dQ = cv.take<float>(sq);
+    float * dK = cv.take<float>(sk);
+    float * dS = cv.take<float>(ss);
+    hipStream_t st = ctx->stream;
+    hipError_t e = hipMemcpyAsync(dQ, Q_ref, sq * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(dK, K_all, sk * 4, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return -1;
+    launch_gemm_abt(dQ, (long long)ek, dK, (long long)ek, dS, T, n_q, T, d_k, scale, d_k, d_k,
+                    (long long)n_q * T, n_head_kv, st);
+    for (int h = 0; h < n_head_kv && e == hipSuccess; h++)
+        e = hipMemcpyAsync(scores_out[h], dS + (size_t)h * n_q * T, (size_t)n_q * T * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return e == hipSuccess ? 0 : -1;
+}
+
+int kv_compact_hip_refit_target_all_heads(const float * const * W_per_head, const float * V_all,
+                                          float ** Y_out, int n_q, int T, int n_head_kv, int d_v) {
+    DeviceCtx * ctx = device_ctx();
+    if (!ctx || n_q <= 0 || T <= 0 || n_head_kv <= 0 || d_v <= 0) return -1;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const size_t ev = (size_t)n_head_kv * d_v;
+    const size_t sw = (size_t)n_head_kv * n_q * T, sv = (size_t)T * ev, sy = (size_t)n_head_kv * n_q * d_v;
+    if (!ensure_arena(ctx, (sw + sv + sy) * 4 + 1024)) return -1;
+    Carver cv;
+    cv.base = ctx->arena;
+    float * dW = cv.take<float>(sw);
+    float * dV = cv.take<float>(sv);
+    float * dY = cv.take<float>(sy);
+    hipStream_t st = ctx->stream;
+    hipError_t e = hipSuccess;
+    for (int h = 0; h < n_head_kv && e == hipSuccess; h++)
+        e = hipMemcpyAsync(dW + (size_t)h * n_q * T, W_per_head[h], (size_t)n_q * T * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(dV, V_all, sv * 4, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return -1;
+    launch_gemm_ab(dW, T, dV, (long long)ev, dY, d_v, n_q, d_v, T, (long long)n_q * T, d_v,
+                   (long long)n_q * d_v, n_head_kv, st);
+    for (int h = 0; h < n_head_kv && e == hipSuccess; h++)
+        e = hipMemcpyAsync(Y_out[h], dY + (size_t)h * n_q * d_v, (size_t)n_q * d_v * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return e == hipSuccess ? 0 : -1;
+}
+
+void kv_compact_hip_pool_free(void) { kvc_release_workspace(); }
+
+// ======================================================================
+// Device-resident batch API (include/kv-compact-device.h)
+// ======================================================================
+
+int kvc_plan(int T, int n_q, int q_ref_given, const kv_compact_params * params, int * t_total, int * n_chunks) {
+    if (T <= 0) return -2;
+    kv_compact_params p = params ? *params : defaults();
+    Plan pl;
+    make_plan(T, n_q, q_ref_given != 0, p, pl);
+    if (t_total) *t_total = pl.t_total;
+    if (n_chunks) *n_chunks = pl.n_chunks;
+    return 0;
+}
+
+int kvc_compact_layers_device(const float * K, const float * V, const float * Q_ref, int L, int T, int n_q,
+                              int n_head_kv, int d_k, int d_v, long long ldK, long long ldV, long long ldQ,
+                              const kv_compact_params * params, const float * token_weight,
+                              kvc_device_out * out, void * stream) {
+    kv_compact_params p = params ? *params : defaults();
+    int rc = validate(K, V, out, T, n_q, n_head_kv, d_k, d_v, Q_ref, p);
+    if (rc) return rc;
+    if (L <= 0) return -2;
+    if (!out->indices || !out->beta || !out->C_v || !out->stats) return -1;
+    rc = check_supported(p, d_v);
+    if (rc) return rc;
+    DeviceCtx * ctx = device_ctx();
+    if (!ctx) return KV_COMPACT_E_DEVICE;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+    Plan pl;
+    make_plan(T, n_q, Q_ref != nullptr, p, pl);
+    BatchIO io{};
+    io.K = K; io.V = V; io.Q = (Q_ref && !p.use_cheap_qref) ? Q_ref : nullptr;
+    io.ldK = ldK; io.ldV = ldV; io.ldQ = ldQ;
+    io.L = L; io.T = T; io.n_q = n_q; io.H = n_head_kv; io.dk = d_k; io.dv = d_v;
+    io.indices = out->indices; io.beta = out->beta; io.Cv = out->C_v; io.stats = out->stats;
+    std::vector<float> wts;
+    const bool host_w = !token_weight && rkv_weights(p, T, wts);
+    Carver sizer;
+    if (host_w) sizer.take<float>(T);
+    size_t need = workspace_bytes(pl, io, !p.skip_beta, &sizer, nullptr, nullptr);
+    if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
+    Carver cv;
+    cv.base = ctx->arena;
+    io.wts = token_weight;
+    if (host_w) {
+        float * dW = cv.take<float>(T);
+        if (hipMemcpyAsync(dW, wts.data(), (size_t)T * 4, hipMemcpyHostToDevice, st) != hipSuccess)
+            return KV_COMPACT_E_DEVICE;
+        io.wts = dW;
+    }
+    return run_batch(ctx, st, pl, p, io, cv, nullptr);
+}
+
+int kvc_compact_quantized_device(const uint8_t * K_quant, const uint8_t * V_quant, const float * Q_ref,
+                                 int k_type, int v_type, size_t k_row_bytes, size_t v_row_bytes,
+                                 int T, int n_q, int n_head_kv, int d_k, int d_v,
+                                 const kv_compact_params * params, kvc_device_out * out,
+                                 uint8_t * K_out, uint8_t * V_out, void * stream) {
+    if (!K_quant || !V_quant || !out || !K_out || !V_out) return -1;
+    if (T <= 0 || n_head_kv <= 0 || d_k <= 0 || d_v <= 0) return -2;
+    const int H = n_head_kv, ek = H * d_k, ev = H * d_v;
+    if (kv_quant_row_elements(k_type, k_row_bytes) != ek || kv_quant_row_elements(v_type, v_row_bytes) != ev)
+        return -4;
+    if (!known_type(k_type) || !known_type(v_type)) return KV_COMPACT_E_UNSUPPORTED;
+    kv_compact_params p = params ? *params : defaults();
+    int rc = check_supported(p, d_v);
+    if (rc) return rc;
+    DeviceCtx * ctx = device_ctx();
+    if (!ctx) return KV_COMPACT_E_DEVICE;
+    hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+    float * dKf = nullptr;
+    float * dVf = nullptr;
+    float * dRows = nullptr;
+    int t = 0;
+    kvc_plan(T, n_q, Q_ref != nullptr, &p, &t, nullptr);
+    if (hipMalloc(&dKf, (size_t)T * ek * 4) != hipSuccess || hipMalloc(&dVf, (size_t)T * ev * 4) != hipSuccess ||
+        hipMalloc(&dRows, (size_t)std::max(t, 1) * ev * 4) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dRows);
+        return KV_COMPACT_E_DEVICE;
+    }
+    launch_dequant_rows(K_quant, k_type, (long long)k_row_bytes, ek, T, dKf, st);
+    launch_dequant_rows(V_quant, v_type, (long long)v_row_bytes, ev, T, dVf, st);
+    rc = kvc_compact_layers_device(dKf, dVf, Q_ref, 1, T, n_q, H, d_k, d_v, (long long)T * ek, (long long)T * ev,
+                                   (long long)std::max(n_q, 1) * ek, &p, nullptr, out, st);
+    if (rc == 0 && t > 0) {
+        launch_quant_rows(dKf, ek, out->indices, k_type, ek, t, K_out, (long long)k_row_bytes, st);
+        launch_gather_cv_rows(out->C_v, H, t, d_v, dRows, st);
+        launch_quant_rows(dRows, ev, nullptr, v_type, ev, t, V_out, (long long)v_row_bytes, st);
+        if (hipStreamSynchronize(st) != hipSuccess) rc = KV_COMPACT_E_DEVICE;
+    }
+    (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dRows);
+    return rc;
+}
+
+int kvc_stage_times(float * out_ms, int n) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+    DeviceCtx * c = &g_dev[dev];
+    std::lock_guard<std::mutex> lk(c->mu);
+    const int m = std::min(n, (int)ST_COUNT);
+    for (int i = 0; i < m; i++) out_ms[i] = c->stage_ms[i];
+    return m;
+}
+
+void kvc_release_workspace(void) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return;
+    DeviceCtx * c = &g_dev[dev];
+    std::lock_guard<std::mutex> lk(c->mu);
+    if (c->arena) {
+        (void)hipStreamSynchronize(c->stream);
+        (void)hipFree(c->arena);
+        c->arena = nullptr;
+        c->arena_cap = 0;
+    }
+}
+
+}  // extern "C"

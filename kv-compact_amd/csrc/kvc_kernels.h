@@ -1,0 +1,32 @@
+// Host-side launch wrappers for the kernels in kvc_kernels.hip.
+#pragma once
+#include "kvc_common.h"
+
+namespace kvc {
+
+hipError_t set_exp2_table(const uint64_t * tab32);
+
+void launch_scores(const Geom & g, const ChunkDesc * chunks, int n_chunk_units, int Tc_max,
+                   const float * K, const float * Q, float * S, int Hs, int nq_cap,
+                   long long s_layer, long long s_head, long long s_row, int qmode, hipStream_t st);
+void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st);
+void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStream_t st);
+void launch_select_topk(const Geom & g, const Work & w, hipStream_t st);
+void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st);
+void launch_ls_build(const Geom & g, const Work & w, hipStream_t st);
+void launch_ge(const Geom & g, const Work & w, float * Cv, hipStream_t st);
+void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const float * K,
+                  const float * V, const float * Q, const float * beta, const float * Cv,
+                  float * stats, hipStream_t st);
+void launch_dequant_rows(const uint8_t * src, int type, long long row_bytes, int n_el, long long rows,
+                         float * dst, hipStream_t st);
+void launch_quant_rows(const float * src, long long src_ld, const int * idx, int type, int n_el,
+                       long long rows, uint8_t * dst, long long row_bytes, hipStream_t st);
+void launch_gather_cv_rows(const float * Cv, int H, int t, int dv, float * rows, hipStream_t st);
+void launch_gemm_abt(const float * A, long long lda, const float * B, long long ldb, float * C, long long ldc,
+                     int m, int n, int k, float scale, long long sa, long long sb, long long sc, int batch,
+                     hipStream_t st);
+void launch_gemm_ab(const float * A, long long lda, const float * B, long long ldb, float * C, long long ldc,
+                    int m, int n, int k, long long sa, long long sb, long long sc, int batch, hipStream_t st);
+
+}  // namespace kvc

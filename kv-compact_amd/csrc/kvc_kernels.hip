@@ -1,0 +1,995 @@
+// HIP kernels of the attention-matching compaction path for MI355X (gfx950).
+//
+// Every kernel keeps the reference CPU path's fp32 operation order so the
+// device output equals the reference's bit for bit:
+//   * dot products accumulate sequentially over the feature index, one
+//     rounded multiply and one rounded add per term (built with
+//     -ffp-contract=off), then one multiply by 1/sqrt(d_k);
+//   * row softmax: max, e = expf(x - max) by the glibc algorithm restated
+//     below, a sequential sum, 1/(sum + 1e-12f), one multiply;
+//   * Gaussian elimination with partial pivoting in the reference's row and
+//     column order (first maximal |pivot| wins, pivots below 1e-12 skipped).
+// Parallelism comes from independent outputs (keys, queries, heads, chunks,
+// layers); a sum whose order matters always runs in one thread.
+#include "kvc_common.h"
+#include "kvc_kernels.h"
+
+#include <math.h>
+
+namespace kvc {
+
+// ---------------------------------------------------------------------------
+// expf as glibc computes it on x86-64 (FMA variant of the ARM optimized-
+// routines method): exp(x) = 2^(k/32) * 2^(r/32), k = round(x*32/ln2),
+// cubic polynomial in double. c_exp2_tab[i] = bits(2^(i/32)) - (i << 47),
+// filled by the host at start-up. Verified against libm expf over every
+// float in [-104, 0] (the softmax domain).
+// ---------------------------------------------------------------------------
+__constant__ uint64_t c_exp2_tab[32];
+
+__device__ __forceinline__ float expf_ref(float x) {
+    if (x < -0x1.9fe368p6f) return 0.0f;
+    if (x > 0x1.62e42ep6f) return __int_as_float(0x7f800000);
+    const double N = 32.0;
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * N;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / N / N / N;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / N / N;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / N;
+    double xd = (double)x;
+    double z = inv_ln2_n * xd;
+    double kd = z + shift;
+    uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    uint64_t tb = c_exp2_tab[ki % 32] + (ki << 47);
+    double s = __longlong_as_double((long long)tb);
+    double p = __builtin_fma(c0, r, c1);
+    double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(p, r2, y);
+    return (float)(y * s);
+}
+
+// cheap reference-query row (api.cpp:140-151): quadratic spacing over n rows
+__device__ __forceinline__ int cheap_pos(int qi, int n, int T) {
+    float f = (float)(qi + 1) / (float)(n + 1);
+    f = f * f;
+    int pos = (int)(f * (float)(T - 1));
+    if (pos >= T) pos = T - 1;
+    if (pos < 0) pos = 0;
+    return pos;
+}
+
+// Row of the reference queries used by chunk c for query qi (head offset 0).
+__device__ __forceinline__ const float * query_row(const Geom & g, const float * K, const float * Q,
+                                                   int layer, const ChunkDesc & c, int qi, int qmode) {
+    const long long ek = (long long)g.H * g.dk;
+    if (qmode == Q_PROVIDED) return Q + layer * g.ldQ + (long long)qi * ek;
+    if (qmode == Q_CHEAP_GLOBAL) return K + layer * g.ldK + (long long)cheap_pos(qi, g.nq_global, g.T) * ek;
+    return K + layer * g.ldK + (long long)(c.start + cheap_pos(qi, c.nq, c.Tc)) * ek;
+}
+
+__device__ __forceinline__ long long lS(const Geom & g) { return (long long)g.H * g.nq_max * g.T; }
+__device__ __forceinline__ long long hS(const Geom & g) { return (long long)g.nq_max * g.T; }
+
+// ---------------------------------------------------------------------------
+// Scores. S[l][h][qi][start + j] = (sum_d q[d] k_j[d]) * inv_sqrt_dk.
+// Block: 64 keys x up to 64 query rows (16 per thread); features staged
+// through LDS in slabs of 32. grid = (ceil(Tc_max/64), n_chunks * Hs, L)
+// ---------------------------------------------------------------------------
+constexpr int SC_KEYS = 64, SC_SLAB = 32, SC_ROWS = 64;
+
+__global__ void __launch_bounds__(256)
+k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ K,
+         const float * __restrict__ Q, float * __restrict__ S, int Hs, int nq_cap,
+         long long s_layer, long long s_head, long long s_row, int qmode) {
+    const int c_idx = blockIdx.y / Hs, h = blockIdx.y % Hs, layer = blockIdx.z;
+    const ChunkDesc c = chunks[c_idx];
+    const int key0 = blockIdx.x * SC_KEYS;
+    if (key0 >= c.Tc) return;
+    const int nq = min(c.nq, nq_cap);
+    __shared__ float ks[SC_KEYS][SC_SLAB + 1];
+    __shared__ float qs[SC_ROWS][SC_SLAB + 1];
+    __shared__ const float * qptr[SC_ROWS];
+    const int tid = threadIdx.x;
+    const int kl = tid & 63, grp = tid >> 6;
+    const long long ek = (long long)g.H * g.dk;
+    const float * Kl = K + layer * g.ldK + (long long)c.start * ek + (long long)h * g.dk;
+    float * Sl = S + layer * s_layer + h * s_head + c.start;
+    for (int q0 = 0; q0 < nq; q0 += SC_ROWS) {
+        __syncthreads();
+        if (tid < SC_ROWS) {
+            const int qi = q0 + tid;
+            qptr[tid] = (qi < nq) ? query_row(g, K, Q, layer, c, qi, qmode) + (long long)h * g.dk : nullptr;
+        }
+        float acc[SC_ROWS / 4];
+#pragma unroll
+        for (int r = 0; r < SC_ROWS / 4; r++) acc[r] = 0.0f;
+        for (int d0 = 0; d0 < g.dk; d0 += SC_SLAB) {
+            __syncthreads();
+            for (int e = tid; e < SC_KEYS * SC_SLAB; e += 256) {
+                const int kk = e / SC_SLAB, dd = e % SC_SLAB;
+                const int key = key0 + kk, dim = d0 + dd;
+                ks[kk][dd] = (key < c.Tc && dim < g.dk) ? Kl[(long long)key * ek + dim] : 0.0f;
+            }
+            for (int e = tid; e < SC_ROWS * SC_SLAB; e += 256) {
+                const int rr = e / SC_SLAB, dd = e % SC_SLAB;
+                const int dim = d0 + dd;
+                const float * qp = qptr[rr];
+                qs[rr][dd] = (qp && dim < g.dk) ? qp[dim] : 0.0f;
+            }
+            __syncthreads();
+            const int dn = min(SC_SLAB, g.dk - d0);
+            for (int dd = 0; dd < dn; dd++) {
+                const float kv = ks[kl][dd];
+#pragma unroll
+                for (int r = 0; r < SC_ROWS / 4; r++) acc[r] += qs[grp + 4 * r][dd] * kv;
+            }
+        }
+        const int key = key0 + kl;
+        if (key < c.Tc) {
+#pragma unroll
+            for (int r = 0; r < SC_ROWS / 4; r++) {
+                const int qi = q0 + grp + 4 * r;
+                if (qi < nq) Sl[(long long)qi * s_row + key] = acc[r] * g.inv_sqrt_dk;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Block reductions (blockDim.x a multiple of 64, at most 1024)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float block_max(float v, float * red) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float r = red[0];
+    for (int i = 1; i < (int)(blockDim.x >> 6); i++) r = fmaxf(r, red[i]);
+    return r;
+}
+
+// Row maximum in the reference's scan order: start from row[0], replace on
+// strictly greater. Without NaN this is the plain maximum; a NaN at row[0]
+// is kept, any other NaN is skipped.
+__device__ __forceinline__ float ref_row_max(const float * row, int n, float * red) {
+    float m = -INFINITY;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) {
+        const float v = row[j];
+        if (v == v) m = fmaxf(m, v);
+    }
+    m = block_max(m, red);
+    const float r0 = row[0];
+    if (r0 != r0) return r0;
+    return (m > r0) ? m : r0;
+}
+
+// ---------------------------------------------------------------------------
+// Chunk softmax + per-key importance (math.h:142-248).
+//   A = e * inv, e = expf(s - max), inv = 1/(sum e + 1e-12f), sum sequential
+//   imp[j] = max / rms / mean over rows, accumulated in row order
+// E/rowsum are written when beta is solved. grid = (n_chunks * H, L)
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ S,
+                     float * __restrict__ A, float * __restrict__ E, float * __restrict__ rowsum,
+                     float * __restrict__ imp) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const long long rs = g.T;
+    const float * Sh = S + layer * lS(g) + h * hS(g) + c.start;
+    float * Ah = A + layer * lS(g) + h * hS(g) + c.start;
+    float * Eh = E ? E + layer * lS(g) + h * hS(g) + c.start : nullptr;
+    __shared__ float red[16];
+    __shared__ float rmax[256], rinv[256];
+    const int nq = c.nq, n = c.Tc;
+    for (int base = 0; base < nq; base += 256) {
+        const int nb = min(256, nq - base);
+        for (int r = 0; r < nb; r++) {
+            const float m = ref_row_max(Sh + (base + r) * rs, n, red);
+            if (threadIdx.x == 0) rmax[r] = m;
+        }
+        __syncthreads();
+        for (int r = 0; r < nb; r++) {
+            const float mx = rmax[r];
+            const float * sr = Sh + (base + r) * rs;
+            float * ar = Ah + (base + r) * rs;
+            float * er = Eh ? Eh + (base + r) * rs : nullptr;
+            for (int j = threadIdx.x; j < n; j += blockDim.x) {
+                const float e = expf_ref(sr[j] - mx);
+                ar[j] = e;
+                if (er) er[j] = e;
+            }
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < nb) {
+            const int r = base + threadIdx.x;
+            const float * ar = Ah + r * rs;
+            float sum = 0.0f;
+            for (int j = 0; j < n; j++) sum += ar[j];
+            if (rowsum) rowsum[(((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max + r] = sum;
+            rinv[threadIdx.x] = 1.0f / (sum + 1e-12f);
+        }
+        __syncthreads();
+        for (int r = 0; r < nb; r++) {
+            const float iv = rinv[r];
+            float * ar = Ah + (base + r) * rs;
+            for (int j = threadIdx.x; j < n; j += blockDim.x) ar[j] = ar[j] * iv;
+        }
+        __syncthreads();
+    }
+    float * imph = imp + ((long long)layer * g.H + h) * g.T + c.start;
+    const float inv_m = 1.0f / (float)nq;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) {
+        float acc = 0.0f;
+        if (g.score_method == 0) {
+            for (int qi = 0; qi < nq; qi++) { const float a = Ah[qi * rs + j]; if (a > acc) acc = a; }
+        } else if (g.score_method == 1) {
+            for (int qi = 0; qi < nq; qi++) { const float a = Ah[qi * rs + j]; acc += a * a; }
+            acc = sqrtf(acc * inv_m);
+        } else {
+            for (int qi = 0; qi < nq; qi++) acc += Ah[qi * rs + j];
+            acc *= inv_m;
+        }
+        imph[j] = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Refit target Y = A V over the chunk (math.h:70-80), sequential over keys.
+// A pass covers QB query rows x dv outputs (<= 4096, 16 per thread); keys
+// staged through LDS 32 at a time. grid = (n_chunks * H, L); dv <= 256.
+// ---------------------------------------------------------------------------
+constexpr int Y_KT = 32;
+
+__global__ void __launch_bounds__(256)
+k_refit_target(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ A,
+               const float * __restrict__ V, float * __restrict__ Y) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const long long rs = g.T;
+    const float * Ah = A + layer * lS(g) + h * hS(g) + c.start;
+    const long long ev = (long long)g.H * g.dv;
+    const float * Vh = V + layer * g.ldV + (long long)c.start * ev + (long long)h * g.dv;
+    float * Yh = Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv;
+    const int nq = c.nq, n = c.Tc, dv = g.dv;
+    const int QB = max(1, min(64, 4096 / dv));
+    constexpr int PER = 16;
+    __shared__ float as[64][Y_KT + 1];
+    __shared__ float vs[Y_KT][257];
+    for (int q0 = 0; q0 < nq; q0 += QB) {
+        const int qn = min(QB, nq - q0);
+        const int n_out = qn * dv;
+        float acc[PER];
+#pragma unroll
+        for (int i = 0; i < PER; i++) acc[i] = 0.0f;
+        for (int j0 = 0; j0 < n; j0 += Y_KT) {
+            const int jn = min(Y_KT, n - j0);
+            __syncthreads();
+            for (int e = threadIdx.x; e < 64 * Y_KT; e += 256) {
+                const int qi = e / Y_KT, jj = e % Y_KT;
+                as[qi][jj] = (qi < qn && jj < jn) ? Ah[(q0 + qi) * rs + j0 + jj] : 0.0f;
+            }
+            for (int e = threadIdx.x; e < Y_KT * 256; e += 256) {
+                const int jj = e / 256, vv = e % 256;
+                vs[jj][vv] = (jj < jn && vv < dv) ? Vh[(long long)(j0 + jj) * ev + vv] : 0.0f;
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < PER; i++) {
+                const int o = threadIdx.x + 256 * i;
+                if (o < n_out) {
+                    const int qi = o / dv, vv = o % dv;
+                    float a = acc[i];
+                    for (int jj = 0; jj < jn; jj++) a += as[qi][jj] * vs[jj][vv];
+                    acc[i] = a;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int o = threadIdx.x + 256 * i;
+            if (o < n_out) Yh[(long long)q0 * dv + o] = acc[i];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Global importance (api.cpp:656-684): max over heads (init 0, strictly
+// greater replaces), then the R-KV weight. grid = (n_chunks, L)
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_global_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ imp,
+                    const float * __restrict__ wts, float * __restrict__ gimp) {
+    const int c_idx = blockIdx.x, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    for (int j = threadIdx.x; j < c.Tc; j += blockDim.x) {
+        float m = 0.0f;
+        for (int h = 0; h < g.H; h++) {
+            const float v = imp[((long long)layer * g.H + h) * g.T + c.start + j];
+            if (v > m) m = v;
+        }
+        if (wts) m *= wts[c.start + j];
+        gimp[(long long)layer * g.T + c.start + j] = m;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Top-t selection (api.cpp:716-744): the set std::partial_sort keeps under
+// "greater importance first" — libstdc++'s heap selection, restated here so
+// that boundary ties resolve to the same members — written ascending.
+// grid = (n_chunks, L). The heap runs on lane 0 over LDS copies (or global
+// scratch for chunks beyond the LDS budget).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool heap_less(const float * imp, int a, int b) { return imp[a] > imp[b]; }
+
+__device__ void heap_push(int * h, const float * imp, int hole, int top, int val) {
+    int parent = (hole - 1) / 2;
+    while (hole > top && heap_less(imp, h[parent], val)) {
+        h[hole] = h[parent];
+        hole = parent;
+        parent = (hole - 1) / 2;
+    }
+    h[hole] = val;
+}
+
+__device__ void heap_adjust(int * h, const float * imp, int hole, int len, int val) {
+    const int top = hole;
+    int child = hole;
+    while (child < (len - 1) / 2) {
+        child = 2 * (child + 1);
+        if (heap_less(imp, h[child], h[child - 1])) child--;
+        h[hole] = h[child];
+        hole = child;
+    }
+    if ((len & 1) == 0 && child == (len - 2) / 2) {
+        child = 2 * (child + 1);
+        h[hole] = h[child - 1];
+        hole = child - 1;
+    }
+    heap_push(h, imp, hole, top, val);
+}
+
+__device__ void heap_select(int * a, int k, int n, const float * imp) {
+    if (k >= 2) {
+        int parent = (k - 2) / 2;
+        for (;;) {
+            const int v = a[parent];
+            heap_adjust(a, imp, parent, k, v);
+            if (parent == 0) break;
+            parent--;
+        }
+    }
+    for (int i = k; i < n; i++) {
+        if (heap_less(imp, a[i], a[0])) {
+            const int v = a[i];
+            a[i] = a[0];
+            heap_adjust(a, imp, 0, k, v);
+        }
+    }
+}
+
+// ascending write-out of flagged positions: block prefix sum over flags
+__device__ void write_flagged(const unsigned char * fl, int n, int base, int * out) {
+    __shared__ int wsum[16];
+    __shared__ int carry;
+    if (threadIdx.x == 0) carry = 0;
+    __syncthreads();
+    for (int j0 = 0; j0 < n; j0 += blockDim.x) {
+        const int j = j0 + threadIdx.x;
+        const int f = (j < n) ? (int)fl[j] : 0;
+        int x = f;
+        const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(x, o);
+            if (lane >= o) x += y;
+        }
+        if (lane == 63) wsum[w] = x;
+        __syncthreads();
+        int pre = carry;
+        for (int i = 0; i < w; i++) pre += wsum[i];
+        if (f) out[pre + x - 1] = base + j;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            int tot = 0;
+            for (int i = 0; i < (int)(blockDim.x >> 6); i++) tot += wsum[i];
+            carry += tot;
+        }
+        __syncthreads();
+    }
+}
+
+__global__ void __launch_bounds__(256)
+k_select_topk(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ gimp,
+              int * __restrict__ cand_g, unsigned char * __restrict__ flags_g, int * __restrict__ sel,
+              int lds_ok) {
+    extern __shared__ unsigned char smem[];
+    const int c_idx = blockIdx.x, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const long long unit = (long long)layer * g.n_chunks + c_idx;
+    const float * im_g = gimp + (long long)layer * g.T + c.start;
+    const int pc = min(c.prefix, c.tc);
+    const int rem = c.tc - pc;
+    const int nc = c.Tc - pc;
+    float * im;
+    int * cand;
+    unsigned char * fl;
+    if (lds_ok) {
+        im = reinterpret_cast<float *>(smem);
+        cand = reinterpret_cast<int *>(smem + sizeof(float) * g.Tc_max);
+        fl = smem + (sizeof(float) + sizeof(int)) * g.Tc_max;
+        for (int j = threadIdx.x; j < c.Tc; j += blockDim.x) im[j] = im_g[j];
+    } else {
+        im = const_cast<float *>(im_g);
+        cand = cand_g + unit * g.Tc_max;
+        fl = flags_g + unit * g.Tc_max;
+    }
+    for (int j = threadIdx.x; j < nc; j += blockDim.x) cand[j] = pc + j;
+    for (int j = threadIdx.x; j < c.Tc; j += blockDim.x) fl[j] = (j < pc) ? 1 : 0;
+    __syncthreads();
+    if (threadIdx.x == 0 && rem > 0) heap_select(cand, rem, nc, im);
+    __syncthreads();
+    for (int j = threadIdx.x; j < rem; j += blockDim.x) fl[cand[j]] = 1;
+    __syncthreads();
+    write_flagged(fl, c.Tc, c.start, sel + (long long)layer * g.t_total + c.off);
+}
+
+// ---------------------------------------------------------------------------
+// Least-squares system per (chunk, head): X = softmax_rows(S[:, sel] + beta)
+// (api.cpp:833-840); aug = [X^T X + ridge I | X^T Y] (math.h:465-504),
+// both sums sequential over the query index.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ S,
+             const int * __restrict__ sel, const float * __restrict__ beta, float * __restrict__ X) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const int t = c.tc, nq = c.nq;
+    const float * Sh = S + layer * lS(g) + h * hS(g);
+    const int * sl = sel + (long long)layer * g.t_total + c.off;
+    const float * bh = beta + ((long long)layer * g.H + h) * g.t_total + c.off;
+    const long long hsX = (long long)g.nq_max * g.t_total;
+    float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
+    __shared__ float red[16];
+    __shared__ float rinv;
+    for (int qi = 0; qi < nq; qi++) {
+        float * xr = Xh + (long long)qi * g.t_total;
+        for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = Sh[(long long)qi * g.T + sl[j]] + bh[j];
+        __syncthreads();
+        const float m = ref_row_max(xr, t, red);
+        for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = expf_ref(xr[j] - m);
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float sum = 0.0f;
+            for (int j = 0; j < t; j++) sum += xr[j];
+            rinv = 1.0f / (sum + 1e-12f);
+        }
+        __syncthreads();
+        const float iv = rinv;
+        for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = xr[j] * iv;
+        __syncthreads();
+    }
+}
+
+__global__ void __launch_bounds__(256)
+k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ X,
+           const float * __restrict__ Y, float * __restrict__ aug, const long long * __restrict__ aug_off) {
+    const int c_idx = blockIdx.y / g.H, h = blockIdx.y % g.H, layer = blockIdx.z;
+    const ChunkDesc c = chunks[c_idx];
+    const int n = c.tc, p = g.dv, w = n + p, nq = c.nq;
+    float * Ag = aug + aug_off[((long long)layer * g.n_chunks + c_idx) * g.H + h];
+    const long long hsX = (long long)g.nq_max * g.t_total;
+    const float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
+    const float * Yh = Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv;
+    const long long total = (long long)n * w;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (long long)gridDim.x * blockDim.x) {
+        const int i = (int)(e / w), j = (int)(e % w);
+        float s = 0.0f;
+        if (j < n) {
+            for (int k = 0; k < nq; k++) s += Xh[(long long)k * g.t_total + i] * Xh[(long long)k * g.t_total + j];
+            if (i == j) s += g.ridge;
+        } else {
+            for (int k = 0; k < nq; k++) s += Xh[(long long)k * g.t_total + i] * Yh[(long long)k * g.dv + (j - n)];
+        }
+        Ag[e] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Gaussian elimination with partial pivoting + back substitution on
+// [M | B] (n x (n + p)), math.h:494-556; one block per system, matrix in
+// global memory. Skipped pivots give zero_val rows of x (row stride ldx).
+// ---------------------------------------------------------------------------
+__device__ void ge_solve_block(float * __restrict__ a, int n, int p, float * __restrict__ x,
+                               long long ldx, float zero_val, float * prow, float * fac) {
+    const int w = n + p;
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    __shared__ int s_mr;
+    for (int col = 0; col < n; col++) {
+        // pivot: first row with the largest |a[r][col]|, scanning r = col..n-1
+        float best = -1.0f;
+        int brow = 0x7fffffff;
+        const float a0 = fabsf(a[(long long)col * w + col]);
+        for (int r = col + 1 + threadIdx.x; r < n; r += blockDim.x) {
+            const float v = fabsf(a[(long long)r * w + col]);
+            if (v == v && v > best) { best = v; brow = r; }
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(best, o);
+            const int orow = __shfl_xor(brow, o);
+            if (ov > best || (ov == best && orow < brow)) { best = ov; brow = orow; }
+        }
+        if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = best; bi[threadIdx.x >> 6] = brow; }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            float b = bv[0];
+            int r = bi[0];
+            for (int i = 1; i < (int)(blockDim.x >> 6); i++)
+                if (bv[i] > b || (bv[i] == b && bi[i] < r)) { b = bv[i]; r = bi[i]; }
+            s_mr = (a0 == a0 && b > a0) ? r : col;
+        }
+        __syncthreads();
+        const int mr = s_mr;
+        if (mr != col) {
+            for (int j = threadIdx.x; j < w; j += blockDim.x) {
+                const float t0 = a[(long long)col * w + j];
+                a[(long long)col * w + j] = a[(long long)mr * w + j];
+                a[(long long)mr * w + j] = t0;
+            }
+        }
+        __syncthreads();
+        const float piv = a[(long long)col * w + col];
+        if (fabsf(piv) < 1e-12f) continue;
+        for (int j = col + threadIdx.x; j < w; j += blockDim.x) prow[j - col] = a[(long long)col * w + j];
+        for (int r = col + 1 + threadIdx.x; r < n; r += blockDim.x) fac[r - col - 1] = a[(long long)r * w + col] / piv;
+        __syncthreads();
+        const int rows = n - col - 1, cols = w - col;
+        const long long tot = (long long)rows * cols;
+        for (long long e = threadIdx.x; e < tot; e += blockDim.x) {
+            const int rr = (int)(e / cols), jj = (int)(e % cols);
+            float * ap = a + (long long)(col + 1 + rr) * w + col + jj;
+            *ap = *ap - fac[rr] * prow[jj];
+        }
+        __syncthreads();
+    }
+    for (int col = n - 1; col >= 0; col--) {
+        const float * arow = a + (long long)col * w;
+        const float piv = arow[col];
+        if (fabsf(piv) < 1e-12f) {
+            for (int j = threadIdx.x; j < p; j += blockDim.x) x[(long long)col * ldx + j] = zero_val;
+        } else {
+            for (int j = threadIdx.x; j < p; j += blockDim.x) {
+                float v = arow[n + j];
+                for (int r = col + 1; r < n; r++) v -= arow[r] * x[(long long)r * ldx + j];
+                x[(long long)col * ldx + j] = v / piv;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+constexpr int GE_LDS_FLOATS = 8192;
+
+__global__ void __launch_bounds__(256)
+k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__ aug,
+           const long long * __restrict__ aug_off, float * __restrict__ Cv, float * __restrict__ gtmp) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const long long sys = ((long long)layer * g.n_chunks + c_idx) * g.H + h;
+    float * Ag = aug + aug_off[sys];
+    float * x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
+    __shared__ float s_buf[GE_LDS_FLOATS];
+    const int n = c.tc, w = n + g.dv;
+    float * prow;
+    float * fac;
+    if (w + n <= GE_LDS_FLOATS) {
+        prow = s_buf;
+        fac = s_buf + w;
+    } else {
+        prow = gtmp + sys * (long long)(2 * g.tc_max + g.dv);
+        fac = prow + g.tc_max + g.dv;
+    }
+    ge_solve_block(Ag, n, g.dv, x, g.dv, 0.0f, prow, fac);
+}
+
+// ---------------------------------------------------------------------------
+// Quality statistics (api.cpp:239-325).
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_row_softmax(float * __restrict__ x, int n, long long rs, int rows, long long layer_stride) {
+    const int row = blockIdx.x, layer = blockIdx.y;
+    if (row >= rows) return;
+    float * xr = x + layer * layer_stride + row * rs;
+    __shared__ float red[16];
+    __shared__ float rinv;
+    const float m = ref_row_max(xr, n, red);
+    for (int j = threadIdx.x; j < n; j += blockDim.x) xr[j] = expf_ref(xr[j] - m);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.0f;
+        for (int j = 0; j < n; j++) sum += xr[j];
+        rinv = 1.0f / (sum + 1e-12f);
+    }
+    __syncthreads();
+    const float iv = rinv;
+    for (int j = threadIdx.x; j < n; j += blockDim.x) xr[j] = xr[j] * iv;
+}
+
+// cs[l][h][qi][j] = dot(q, K[sel_j]) * inv + beta[h][j]
+__global__ void __launch_bounds__(256)
+k_stats_comp_scores(Geom g, const ChunkDesc * __restrict__ whole, const float * __restrict__ K,
+                    const float * __restrict__ Q, int qmode, const int * __restrict__ sel,
+                    const float * __restrict__ beta, float * __restrict__ CS, int mh, int mq) {
+    const int layer = blockIdx.z, h = blockIdx.y / mq, qi = blockIdx.y % mq;
+    const long long ek = (long long)g.H * g.dk;
+    const float * q = query_row(g, K, Q, layer, whole[0], qi, qmode) + (long long)h * g.dk;
+    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < g.t_total; j += gridDim.x * blockDim.x) {
+        const int pos = sel[(long long)layer * g.t_total + j];
+        const float * k = K + layer * g.ldK + (long long)pos * ek + (long long)h * g.dk;
+        float dot = 0.0f;
+        for (int d = 0; d < g.dk; d++) dot += q[d] * k[d];
+        CS[(((long long)layer * mh + h) * mq + qi) * g.t_total + j] =
+            dot * g.inv_sqrt_dk + beta[((long long)layer * g.H + h) * g.t_total + j];
+    }
+}
+
+// out[l][h][qi][d] = sum_j a[l][h][qi][j] * val_j[d], sequential over j.
+// mode 0: val_j = V row j (head h); mode 1: val_j = C_v[h][j]
+__global__ void __launch_bounds__(128)
+k_stats_weighted_sum(Geom g, const float * __restrict__ a, int n, const float * __restrict__ V,
+                     const float * __restrict__ Cv, int mode, float * __restrict__ out, int mh, int mq) {
+    const int layer = blockIdx.z, h = blockIdx.y / mq, qi = blockIdx.y % mq;
+    const float * ar = a + (((long long)layer * mh + h) * mq + qi) * n;
+    for (int d = blockIdx.x * blockDim.x + threadIdx.x; d < g.dv; d += gridDim.x * blockDim.x) {
+        float acc = 0.0f;
+        if (mode == 0) {
+            const long long ev = (long long)g.H * g.dv;
+            const float * vb = V + layer * g.ldV + (long long)h * g.dv + d;
+            for (int j = 0; j < n; j++) acc += ar[j] * vb[(long long)j * ev];
+        } else {
+            const float * cb = Cv + ((long long)layer * g.H + h) * g.t_total * g.dv + d;
+            for (int j = 0; j < n; j++) acc += ar[j] * cb[(long long)j * g.dv];
+        }
+        out[(((long long)layer * mh + h) * mq + qi) * g.dv + d] = acc;
+    }
+}
+
+__global__ void k_stats_final(Geom g, const float * __restrict__ oo, const float * __restrict__ co,
+                              int mh, int mq, float * __restrict__ stats) {
+    const int layer = blockIdx.x;
+    if (threadIdx.x != 0) return;
+    float sum_cos = 0.0f, sum_mse = 0.0f;
+    int agree = 0, total = 0;
+    for (int h = 0; h < mh; h++) {
+        for (int qi = 0; qi < mq; qi++) {
+            const float * o = oo + (((long long)layer * mh + h) * mq + qi) * g.dv;
+            const float * c = co + (((long long)layer * mh + h) * mq + qi) * g.dv;
+            float dp = 0.0f, no = 0.0f, nc = 0.0f;
+            for (int d = 0; d < g.dv; d++) { dp += o[d] * c[d]; no += o[d] * o[d]; nc += c[d] * c[d]; }
+            sum_cos += dp / (sqrtf(no * nc) + 1e-8f);
+            float mse = 0.0f;
+            for (int d = 0; d < g.dv; d++) { const float df = o[d] - c[d]; mse += df * df; }
+            sum_mse += mse / (float)g.dv;
+            int ao = 0, ac = 0;
+            for (int d = 1; d < g.dv; d++) {
+                if (o[d] > o[ao]) ao = d;
+                if (c[d] > c[ac]) ac = d;
+            }
+            if (ao == ac) agree++;
+            total++;
+        }
+    }
+    stats[layer * 3 + 0] = sum_cos / (float)total;
+    stats[layer * 3 + 1] = sum_mse / (float)total;
+    stats[layer * 3 + 2] = (float)agree / (float)total;
+}
+
+// ---------------------------------------------------------------------------
+// Codec (state.h:326-629), bit-exact with the reference.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float f16_to_f32_ref(uint16_t hv) {
+    uint32_t sign = (uint32_t)(hv & 0x8000) << 16;
+    uint32_t e = (hv >> 10) & 0x1F;
+    uint32_t m = hv & 0x3FF;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            e = 1;
+            while (!(m & 0x400)) { m <<= 1; e--; }
+            m &= 0x3FF;
+            e = e + (127 - 15);
+            bits = sign | (e << 23) | (m << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        e = e + (127 - 15);
+        bits = sign | (e << 23) | (m << 13);
+    }
+    return __uint_as_float(bits);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16_ref(float val) {
+    const uint32_t f = __float_as_uint(val);
+    const uint32_t sign = (f >> 16) & 0x8000;
+    const int32_t e = (int32_t)((f >> 23) & 0xFF) - 127 + 15;
+    uint32_t m = (f >> 13) & 0x3FF;
+    if (e <= 0) {
+        if (e < -10) return (uint16_t)sign;
+        m = (m | 0x400) >> (1 - e);
+        return (uint16_t)(sign | m);
+    } else if (e >= 31) {
+        return (uint16_t)(sign | 0x7C00);
+    }
+    return (uint16_t)(sign | ((uint32_t)e << 10) | m);
+}
+
+__device__ __forceinline__ float fmax_std(float a, float b) { return (a < b) ? b : a; }
+__device__ __forceinline__ float fmin_std(float a, float b) { return (b < a) ? b : a; }
+__device__ __forceinline__ uint16_t load_u16(const uint8_t * p) { return (uint16_t)(p[0] | ((uint16_t)p[1] << 8)); }
+
+// one work item per 32-element block (per element for F32/F16)
+__global__ void __launch_bounds__(256)
+k_dequant_rows(const uint8_t * __restrict__ src, int type, long long row_bytes, int n_el,
+               long long rows, float * __restrict__ dst) {
+    const long long nb = (type == 0 || type == 1) ? (long long)n_el : (long long)(n_el / 32);
+    const long long total = rows * nb;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (long long)gridDim.x * blockDim.x) {
+        const long long r = e / nb, b = e % nb;
+        const uint8_t * s = src + r * row_bytes;
+        float * o = dst + r * n_el;
+        if (type == 0) {
+            o[b] = __uint_as_float((uint32_t)s[4 * b] | ((uint32_t)s[4 * b + 1] << 8) |
+                                   ((uint32_t)s[4 * b + 2] << 16) | ((uint32_t)s[4 * b + 3] << 24));
+        } else if (type == 1) {
+            o[b] = f16_to_f32_ref(load_u16(s + 2 * b));
+        } else if (type == 8) {
+            const uint8_t * bl = s + b * 34;
+            const float d = f16_to_f32_ref(load_u16(bl));
+            for (int i = 0; i < 32; i++) o[b * 32 + i] = d * (float)(int8_t)bl[2 + i];
+        } else if (type == 2) {
+            const uint8_t * bl = s + b * 18;
+            const float d = f16_to_f32_ref(load_u16(bl));
+            for (int i = 0; i < 16; i++) {
+                o[b * 32 + 2 * i] = d * ((float)(bl[2 + i] & 0xF) - 8.0f);
+                o[b * 32 + 2 * i + 1] = d * ((float)(bl[2 + i] >> 4) - 8.0f);
+            }
+        } else if (type == 3) {
+            const uint8_t * bl = s + b * 20;
+            const float d = f16_to_f32_ref(load_u16(bl)), m = f16_to_f32_ref(load_u16(bl + 2));
+            for (int i = 0; i < 16; i++) {
+                o[b * 32 + 2 * i] = d * (float)(bl[4 + i] & 0xF) + m;
+                o[b * 32 + 2 * i + 1] = d * (float)(bl[4 + i] >> 4) + m;
+            }
+        }
+    }
+}
+
+// quantize rows gathered by index (idx == nullptr: identity), src row stride src_ld
+__global__ void __launch_bounds__(256)
+k_quant_rows(const float * __restrict__ src, long long src_ld, const int * __restrict__ idx,
+             int type, int n_el, long long rows, uint8_t * __restrict__ dst, long long row_bytes) {
+    const long long nb = (type == 0 || type == 1) ? (long long)n_el : (long long)(n_el / 32);
+    const long long total = rows * nb;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (long long)gridDim.x * blockDim.x) {
+        const long long r = e / nb, b = e % nb;
+        const long long sr = idx ? (long long)idx[r] : r;
+        const float * x = src + sr * src_ld;
+        uint8_t * o = dst + r * row_bytes;
+        if (type == 0) {
+            const uint32_t u = __float_as_uint(x[b]);
+            o[4 * b] = u & 0xFF; o[4 * b + 1] = (u >> 8) & 0xFF; o[4 * b + 2] = (u >> 16) & 0xFF; o[4 * b + 3] = u >> 24;
+        } else if (type == 1) {
+            const uint16_t hv = f32_to_f16_ref(x[b]);
+            o[2 * b] = hv & 0xFF; o[2 * b + 1] = hv >> 8;
+        } else if (type == 8) {
+            const float * xb = x + b * 32;
+            uint8_t * ob = o + b * 34;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; i++) { const float a = fabsf(xb[i]); if (a > amax) amax = a; }
+            const float d = amax / 127.0f;
+            const uint16_t hv = f32_to_f16_ref(d);
+            ob[0] = hv & 0xFF; ob[1] = hv >> 8;
+            const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
+            for (int i = 0; i < 32; i++) {
+                const float v = xb[i] * id;
+                ob[2 + i] = (uint8_t)(int8_t)roundf(fmax_std(-128.0f, fmin_std(127.0f, v)));
+            }
+        } else if (type == 2) {
+            const float * xb = x + b * 32;
+            uint8_t * ob = o + b * 18;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; i++) { const float a = fabsf(xb[i]); if (a > amax) amax = a; }
+            const float d = amax / 7.0f;
+            const uint16_t hv = f32_to_f16_ref(d);
+            ob[0] = hv & 0xFF; ob[1] = hv >> 8;
+            const float id = (d != 0.0f) ? 7.0f / amax : 0.0f;
+            for (int i = 0; i < 16; i++) {
+                const float v0 = xb[2 * i] * id + 8.0f;
+                const float v1 = xb[2 * i + 1] * id + 8.0f;
+                const uint8_t q0 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v0)));
+                const uint8_t q1 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v1)));
+                ob[2 + i] = (uint8_t)(q0 | (q1 << 4));
+            }
+        } else if (type == 3) {
+            const float * xb = x + b * 32;
+            uint8_t * ob = o + b * 20;
+            float mn = xb[0], mx = xb[0];
+            for (int i = 1; i < 32; i++) { if (xb[i] < mn) mn = xb[i]; if (xb[i] > mx) mx = xb[i]; }
+            const float d = (mx - mn) / 15.0f;
+            const uint16_t hd = f32_to_f16_ref(d), hm = f32_to_f16_ref(mn);
+            ob[0] = hd & 0xFF; ob[1] = hd >> 8; ob[2] = hm & 0xFF; ob[3] = hm >> 8;
+            const float id = (d != 0.0f) ? 15.0f / (mx - mn) : 0.0f;
+            for (int i = 0; i < 16; i++) {
+                const float v0 = (xb[2 * i] - mn) * id;
+                const float v1 = (xb[2 * i + 1] - mn) * id;
+                const uint8_t q0 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v0)));
+                const uint8_t q1 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v1)));
+                ob[4 + i] = (uint8_t)(q0 | (q1 << 4));
+            }
+        }
+    }
+}
+
+// row j of the compacted V: concat over heads of C_v[h][j] (api.cpp:1243-1254)
+__global__ void __launch_bounds__(256)
+k_gather_cv_rows(const float * __restrict__ Cv, int H, int t, int dv, float * __restrict__ rows) {
+    const long long total = (long long)t * H * dv;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (long long)gridDim.x * blockDim.x) {
+        const long long j = e / ((long long)H * dv), r = e % ((long long)H * dv);
+        const int h = (int)(r / dv), d = (int)(r % dv);
+        rows[e] = Cv[((long long)h * t + j) * dv + d];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Accelerator plug-in GEMMs (accel ABI), sequential accumulation.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_gemm_abt(const float * __restrict__ A, long long lda, const float * __restrict__ B, long long ldb,
+           float * __restrict__ C, long long ldc, int m, int n, int k, float scale,
+           long long sa, long long sb, long long sc) {
+    const int bat = blockIdx.z;
+    A += bat * sa; B += bat * sb; C += bat * sc;
+    const int i = blockIdx.y * 16 + (threadIdx.x >> 4);
+    const int j = blockIdx.x * 16 + (threadIdx.x & 15);
+    if (i >= m || j >= n) return;
+    float s = 0.0f;
+    for (int l = 0; l < k; l++) s += A[(long long)i * lda + l] * B[(long long)j * ldb + l];
+    C[(long long)i * ldc + j] = s * scale;
+}
+
+__global__ void __launch_bounds__(256)
+k_gemm_ab(const float * __restrict__ A, long long lda, const float * __restrict__ B, long long ldb,
+          float * __restrict__ C, long long ldc, int m, int n, int k,
+          long long sa, long long sb, long long sc) {
+    const int bat = blockIdx.z;
+    A += bat * sa; B += bat * sb; C += bat * sc;
+    const int i = blockIdx.y * 16 + (threadIdx.x >> 4);
+    const int j = blockIdx.x * 16 + (threadIdx.x & 15);
+    if (i >= m || j >= n) return;
+    float s = 0.0f;
+    for (int l = 0; l < k; l++) s += A[(long long)i * lda + l] * B[(long long)l * ldb + j];
+    C[(long long)i * ldc + j] = s;
+}
+
+// ===========================================================================
+// Host launch wrappers
+// ===========================================================================
+static inline unsigned cdiv(long long a, long long b) { return (unsigned)((a + b - 1) / b); }
+static inline unsigned grid_cap(long long n, int bs) {
+    long long g = (n + bs - 1) / bs;
+    return (unsigned)(g < 1 ? 1 : (g > 65535 * 4 ? 65535 * 4 : g));
+}
+
+hipError_t set_exp2_table(const uint64_t * tab32) {
+    return hipMemcpyToSymbol(HIP_SYMBOL(c_exp2_tab), tab32, 32 * sizeof(uint64_t));
+}
+
+void launch_scores(const Geom & g, const ChunkDesc * chunks, int n_chunk_units, int Tc_max,
+                   const float * K, const float * Q, float * S, int Hs, int nq_cap,
+                   long long s_layer, long long s_head, long long s_row, int qmode, hipStream_t st) {
+    dim3 grid(cdiv(Tc_max, SC_KEYS), n_chunk_units * Hs, g.L);
+    hipLaunchKernelGGL(k_scores, grid, dim3(256), 0, st, g, chunks, K, Q, S, Hs, nq_cap,
+                       s_layer, s_head, s_row, qmode);
+}
+
+void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st) {
+    hipLaunchKernelGGL(k_softmax_importance, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
+                       g, w.chunks, w.S, w.A, w.E, w.E ? w.rowsum : nullptr, w.imp);
+}
+
+void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStream_t st) {
+    hipLaunchKernelGGL(k_refit_target, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
+                       g, w.chunks, w.A, V, w.Y);
+}
+
+void launch_select_topk(const Geom & g, const Work & w, hipStream_t st) {
+    hipLaunchKernelGGL(k_global_importance, dim3(g.n_chunks, g.L), dim3(256), 0, st,
+                       g, w.chunks, w.imp, w.wts, w.gimp);
+    const size_t lds = (size_t)g.Tc_max * (sizeof(float) + sizeof(int) + 1);
+    const int lds_ok = lds <= 60 * 1024 ? 1 : 0;
+    hipLaunchKernelGGL(k_select_topk, dim3(g.n_chunks, g.L), dim3(256), lds_ok ? lds : 0, st,
+                       g, w.chunks, w.gimp, w.cand, w.flags, w.sel, lds_ok);
+}
+
+void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st) {
+    hipLaunchKernelGGL(k_ls_softmax, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
+                       g, w.chunks, w.S, w.sel, beta, w.X);
+}
+
+void launch_ls_build(const Geom & g, const Work & w, hipStream_t st) {
+    const long long per = (long long)g.tc_max * (g.tc_max + g.dv);
+    const unsigned bx = (unsigned)std::min<long long>(64, (per + 255) / 256);
+    hipLaunchKernelGGL(k_ls_build, dim3(bx, g.n_chunks * g.H, g.L), dim3(256), 0, st,
+                       g, w.chunks, w.X, w.Y, w.aug, w.aug_off);
+}
+
+void launch_ge(const Geom & g, const Work & w, float * Cv, hipStream_t st) {
+    hipLaunchKernelGGL(k_ge_solve, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
+                       g, w.chunks, w.aug, w.aug_off, Cv, w.gtmp);
+}
+
+void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const float * K,
+                  const float * V, const float * Q, const float * beta, const float * Cv,
+                  float * stats, hipStream_t st) {
+    const ChunkDesc * whole = w.chunks + g.n_chunks;
+    const long long osl = (long long)sw.mh * sw.mq * g.T;
+    launch_scores(g, whole, 1, g.T, K, Q, sw.OS, sw.mh, sw.mq, osl, (long long)sw.mq * g.T, g.T, sw.qmode, st);
+    hipLaunchKernelGGL(k_row_softmax, dim3(sw.mh * sw.mq, g.L), dim3(256), 0, st,
+                       sw.OS, g.T, (long long)g.T, sw.mh * sw.mq, osl);
+    hipLaunchKernelGGL(k_stats_weighted_sum, dim3(cdiv(g.dv, 128), sw.mh * sw.mq, g.L), dim3(128), 0, st,
+                       g, sw.OS, g.T, V, Cv, 0, sw.OO, sw.mh, sw.mq);
+    hipLaunchKernelGGL(k_stats_comp_scores, dim3(cdiv(g.t_total, 256), sw.mh * sw.mq, g.L), dim3(256), 0, st,
+                       g, whole, K, Q, sw.qmode, w.sel, beta, sw.CS, sw.mh, sw.mq);
+    const long long csl = (long long)sw.mh * sw.mq * g.t_total;
+    hipLaunchKernelGGL(k_row_softmax, dim3(sw.mh * sw.mq, g.L), dim3(256), 0, st,
+                       sw.CS, g.t_total, (long long)g.t_total, sw.mh * sw.mq, csl);
+    hipLaunchKernelGGL(k_stats_weighted_sum, dim3(cdiv(g.dv, 128), sw.mh * sw.mq, g.L), dim3(128), 0, st,
+                       g, sw.CS, g.t_total, V, Cv, 1, sw.CO, sw.mh, sw.mq);
+    hipLaunchKernelGGL(k_stats_final, dim3(g.L), dim3(64), 0, st, g, sw.OO, sw.CO, sw.mh, sw.mq, stats);
+}
+
+void launch_dequant_rows(const uint8_t * src, int type, long long row_bytes, int n_el, long long rows,
+                         float * dst, hipStream_t st) {
+    const long long nb = (type == 0 || type == 1) ? (long long)n_el : (long long)(n_el / 32);
+    hipLaunchKernelGGL(k_dequant_rows, dim3(grid_cap(rows * nb, 256)), dim3(256), 0, st,
+                       src, type, row_bytes, n_el, rows, dst);
+}
+
+void launch_quant_rows(const float * src, long long src_ld, const int * idx, int type, int n_el,
+                       long long rows, uint8_t * dst, long long row_bytes, hipStream_t st) {
+    const long long nb = (type == 0 || type == 1) ? (long long)n_el : (long long)(n_el / 32);
+    hipLaunchKernelGGL(k_quant_rows, dim3(grid_cap(rows * nb, 256)), dim3(256), 0, st,
+                       src, src_ld, idx, type, n_el, rows, dst, row_bytes);
+}
+
+void launch_gather_cv_rows(const float * Cv, int H, int t, int dv, float * rows, hipStream_t st) {
+    hipLaunchKernelGGL(k_gather_cv_rows, dim3(grid_cap((long long)t * H * dv, 256)), dim3(256), 0, st,
+                       Cv, H, t, dv, rows);
+}
+
+void launch_gemm_abt(const float * A, long long lda, const float * B, long long ldb, float * C, long long ldc,
+                     int m, int n, int k, float scale, long long sa, long long sb, long long sc, int batch,
+                     hipStream_t st) {
+    hipLaunchKernelGGL(k_gemm_abt, dim3(cdiv(n, 16), cdiv(m, 16), batch), dim3(256), 0, st,
+                       A, lda, B, ldb, C, ldc, m, n, k, scale, sa, sb, sc);
+}
+
+void launch_gemm_ab(const float * A, long long lda, const float * B, long long ldb, float * C, long long ldc,
+                    int m, int n, int k, long long sa, long long sb, long long sc, int batch, hipStream_t st) {
+    hipLaunchKernelGGL(k_gemm_ab, dim3(cdiv(n, 16), cdiv(m, 16), batch), dim3(256), 0, st,
+                       A, lda, B, ldb, C, ldc, m, n, k, sa, sb, sc);
+}
+
+}  // namespace kvc

@@ -264,6 +264,39 @@ class Lib:
         return self._rb(typ, n)
 
 
+class DeviceOut(ctypes.Structure):
+    """kvc_device_out (include/kv-compact-device.h): device result buffers."""
+    _fields_ = [
+        ("indices", ctypes.c_void_p),
+        ("beta", ctypes.c_void_p),
+        ("C_v", ctypes.c_void_p),
+        ("stats", ctypes.c_void_p),
+    ]
+
+
+def bind_device_api(dll):
+    """Declare the additive device-resident entry points of libkv-compact.so."""
+    dll.kvc_plan.argtypes = [_i, _i, _i, ctypes.POINTER(Params), ctypes.POINTER(_i), ctypes.POINTER(_i)]
+    dll.kvc_plan.restype = _i
+    dll.kvc_compact_layers_device.argtypes = [_vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
+                                              ctypes.c_longlong, ctypes.c_longlong, ctypes.c_longlong,
+                                              ctypes.POINTER(Params), _vp, ctypes.POINTER(DeviceOut), _vp]
+    dll.kvc_compact_layers_device.restype = _i
+    dll.kvc_stage_times.argtypes = [ctypes.POINTER(ctypes.c_float), _i]
+    dll.kvc_stage_times.restype = _i
+    dll.kv_compact_hip_available.restype = _i
+    return dll
+
+
+def plan(dll, T, n_q, q_given, params):
+    t = _i(0)
+    nc = _i(0)
+    rc = dll.kvc_plan(T, n_q, 1 if q_given else 0, ctypes.byref(params), ctypes.byref(t), ctypes.byref(nc))
+    if rc != 0:
+        raise RuntimeError(f"kvc_plan returned {rc}")
+    return t.value, nc.value
+
+
 def product_lib_path() -> Path:
     return HERE / "libkv-compact.so"
 

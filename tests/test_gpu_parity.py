@@ -1,0 +1,172 @@
+"""GPU parity: the MI355X library against the CPU oracle, bit for bit.
+
+Every output (kept indices, beta, C_v, the three quality statistics, the
+requantized rows) must equal the oracle's exactly: the kernels keep the
+reference's fp32 operation order. Options the library does not implement yet
+must be refused with KV_COMPACT_E_UNSUPPORTED, never computed differently.
+"""
+from __future__ import annotations
+
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+from kvc_data import CASES, CASE_BY_NAME, kv_cache, make_case, snapkv_queries
+from kvc_harness import kc, load_oracle, run_case
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def supported(c):
+    p = c["params"]
+    return (p.get("skip_beta", 1) == 1 and not p.get("use_diversity") and not p.get("refine_rounds"))
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    lib = kc.load_product()
+    if not lib.dll.kv_compact_hip_available():
+        pytest.fail("no usable GPU for the GPU test tier")
+    return lib
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return load_oracle()
+
+
+def same(a, b):
+    assert a.t == b.t
+    assert np.array_equal(a.indices, b.indices), "indices"
+    assert np.array_equal(bits(a.beta), bits(b.beta)), "beta"
+    ca, cb = bits(a.C_v), bits(b.C_v)
+    if not np.array_equal(ca, cb):
+        bad = np.argwhere(ca != cb)
+        raise AssertionError(f"C_v differs at {len(bad)} of {ca.size}: first {bad[:3].tolist()}")
+    for k in ("avg_cosine_sim", "avg_mse", "avg_agreement"):
+        assert np.float32(a.stats[k]).view(np.uint32) == np.float32(b.stats[k]).view(np.uint32), k
+
+
+@pytest.mark.parametrize("name", [c["name"] for c in CASES])
+def test_case_parity(gpu, orc, name):
+    c = CASE_BY_NAME[name]
+    print(f"[case] {name}", flush=True)
+    inp = make_case(c)
+    if not supported(c):
+        from kvc_harness import case_params
+        K, V, Q, nq = inp
+        p = case_params(gpu, c, c["T"])
+        rc, r = gpu.compact_raw(K, V, Q, c["T"], nq, c["H"], c["d"], c.get("dv", c["d"]), p)
+        assert rc == kc.E_UNSUPPORTED
+        return
+    same(run_case(gpu, c, inp), run_case(orc, c, inp))
+
+
+def test_config1_shape(gpu, orc):
+    """Single head, T=4096, d=128, 4 outlier channels x8, cheap Q_ref, 50%."""
+    K, V = kv_cache(4096, 1, 128, 101, outliers=4)
+    p = dict(target_ratio=0.5, use_cheap_qref=1)
+    a = gpu.compact(K, V, None, 4096, 0, 1, 128, 128, gpu.params(**p))
+    b = orc.compact(K, V, None, 4096, 0, 1, 128, 128, orc.params(**p))
+    same(a, b)
+
+
+def test_config2_slice(gpu, orc):
+    """Llama-3-8B-shaped layer slice: H=8, d=128, T=2560, SnapKV W=32, 20%."""
+    K, V = kv_cache(2560, 8, 128, 102, channel_scale=True)
+    Q = snapkv_queries(K, 32, 102)
+    p = dict(target_ratio=0.2)
+    a = gpu.compact(K, V, Q, 2560, 32, 8, 128, 128, gpu.params(**p))
+    b = orc.compact(K, V, Q, 2560, 32, 8, 128, 128, orc.params(**p))
+    same(a, b)
+
+
+@pytest.mark.parametrize("kt,vt", [(8, 8), (2, 2), (8, 2), (1, 3)])
+def test_quantized_parity(gpu, orc, kt, vt):
+    T, H, d = 700, 2, 64
+    K, V = kv_cache(T, H, d, 60 + kt + vt)
+    Kq = np.stack([orc.quantize_row(K[i], kt) for i in range(T)])
+    Vq = np.stack([orc.quantize_row(V[i], vt) for i in range(T)])
+    args = (Kq, Vq, None, kt, vt, Kq.shape[1], Vq.shape[1], T, 0, H, d, d)
+    ra, a = gpu.quantized(*args, gpu.params(target_ratio=0.2, use_cheap_qref=1))
+    rb, b = orc.quantized(*args, orc.params(target_ratio=0.2, use_cheap_qref=1))
+    assert ra == 0 and rb == 0
+    same(a, b)
+    assert np.array_equal(a.K_out, b.K_out)
+    assert np.array_equal(a.V_out, b.V_out)
+
+
+def test_codec_rows(gpu, orc):
+    from kvc_data import normal
+    for typ in (0, 1, 2, 3, 8):
+        for s in range(3):
+            x = (normal(300 + s, (256,)) * np.float32(10.0 ** (s - 1))).astype(np.float32)
+            ea, eb = gpu.quantize_row(x, typ), orc.quantize_row(x, typ)
+            assert np.array_equal(ea, eb), typ
+            da, db = gpu.dequantize_row(ea, typ, 256), orc.dequantize_row(eb, typ, 256)
+            assert np.array_equal(bits(da), bits(db)), typ
+
+
+def test_multi_round(gpu, orc):
+    c = CASE_BY_NAME["unchunked_r80"]
+    K, V, Q, nq = make_case(c)
+    ra, a, pa = gpu.multi_round(K, V, Q, c["T"], nq, c["H"], c["d"], c["d"], gpu.params(target_ratio=0.7), 3)
+    rb, b, pb = orc.multi_round(K, V, Q, c["T"], nq, c["H"], c["d"], c["d"], orc.params(target_ratio=0.7), 3)
+    assert ra == 0 and rb == 0
+    same(a, b)
+    assert np.array_equal(bits(np.array(pa, np.float32)), bits(np.array(pb, np.float32)))
+
+
+def test_accel_plugin_scores(gpu, orc):
+    """kv_compact_hip_score_all_heads equals the CPU scoring (mat_mul_ABt then scale)."""
+    from kvc_data import normal
+    nq, T, H, d = 16, 300, 3, 40
+    Q = normal(7, (nq, H * d)); K = normal(8, (T, H * d))
+    outs = [np.zeros(nq * T, np.float32) for _ in range(H)]
+    arr = (ctypes.POINTER(ctypes.c_float) * H)(*[o.ctypes.data_as(ctypes.POINTER(ctypes.c_float)) for o in outs])
+    f = gpu.dll.kv_compact_hip_score_all_heads
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                  ctypes.c_int, ctypes.c_float]
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    assert f(Q.ctypes.data, K.ctypes.data, ctypes.cast(arr, ctypes.c_void_p), nq, T, H, d, float(scale)) == 0
+    sc = orc.dll.orc_scores
+    sc.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 5 + [ctypes.c_float]
+    for h in range(H):
+        ref = np.zeros(nq * T, np.float32)
+        sc(Q[:, h * d:].ctypes.data, K[:, h * d:].ctypes.data, ref.ctypes.data, nq, T, d, H * d, H * d, float(scale))
+        assert np.array_equal(bits(outs[h]), bits(ref)), h
+
+
+def test_device_batch_api(gpu, orc):
+    """Three layers in one device-resident call equal three oracle calls."""
+    import hiprt
+    L, T, H, d = 3, 1536, 2, 64
+    Ks, Vs, Qs = [], [], []
+    for l in range(L):
+        K, V = kv_cache(T, H, d, 200 + l, channel_scale=True)
+        Ks.append(K); Vs.append(V); Qs.append(snapkv_queries(K, 32, 200 + l))
+    dll = kc.bind_device_api(gpu.dll)
+    p = gpu.params(target_ratio=0.2)
+    t, _ = kc.plan(dll, T, 32, True, p)
+    dK, dV, dQ = (hiprt.DevBuf(L * a[0].nbytes) for a in (Ks, Vs, Qs))
+    for l in range(L):
+        dK.upload(Ks[l], l * Ks[0].nbytes); dV.upload(Vs[l], l * Vs[0].nbytes); dQ.upload(Qs[l], l * Qs[0].nbytes)
+    idx, beta, cv, st = (hiprt.DevBuf(n * 4) for n in (L * t, L * H * t, L * H * t * d, L * 3))
+    out = kc.DeviceOut(idx.value, beta.value, cv.value, st.value)
+    rc = dll.kvc_compact_layers_device(dK.value, dV.value, dQ.value, L, T, 32, H, d, d, T * H * d, T * H * d,
+                                       32 * H * d, ctypes.byref(p), None, ctypes.byref(out), None)
+    assert rc == 0
+    gi = idx.download(np.int32, L * t).reshape(L, t)
+    gc = cv.download(np.float32, L * H * t * d).reshape(L, H, t, d)
+    gs = st.download(np.float32, L * 3).reshape(L, 3)
+    for l in range(L):
+        b = orc.compact(Ks[l], Vs[l], Qs[l], T, 32, H, d, d, orc.params(target_ratio=0.2))
+        assert np.array_equal(gi[l], b.indices)
+        assert np.array_equal(bits(gc[l]), bits(b.C_v))
+        assert np.float32(gs[l, 0]).view(np.uint32) == np.float32(b.stats["avg_cosine_sim"]).view(np.uint32)
