@@ -1,0 +1,240 @@
+#!/usr/bin/env python3
+"""Compaction throughput on one MI355X.
+
+Workload (the headline configuration): a Llama-3-8B-shaped KV cache of
+32 layers x 8 KV heads x head_dim 128 at T = 100,000 tokens, fp32, compacted
+to 20% retention (t = 20,000 kept per layer) with the default parameters
+(RMS importance, skip_beta = 1, auto chunking: 79 chunks of 1280 tokens,
+256 kept per chunk). Keys ~ N(0,1) times a per-(layer, channel) scale drawn
+from LogNormal(0, 0.5); values ~ N(0,1); SnapKV reference queries = the last
+32 keys + N(0, 0.1^2) noise. Synthetic data, generated once on the host and
+resident in HBM before the timed region.
+
+One step = one device-resident call compacting all 32 layers (scoring,
+selection, value refit and the quality statistics the reference computes in
+every call). metric = T / step time (tokens of context compacted per second
+across all layers, the reference benches' definition).
+
+Prints one JSON line (driver contract) with a "roofline" object for the
+dominant kernel (from HIP events recorded by the library on its stream) and a
+"cpu_baseline" object: the reference's own CPU path compiled from its sources
+(oracle/_ref/libkvref.so, OpenMP over every host core) timed on a bounded
+sample of the same data, or the oracle port when the reference build is
+absent.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "kv-compact_amd"))
+
+import kvcompact as kc  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+FP32_PEAK_TFLOPS = 157.3       # MI355X fp32
+STAGES = ["scores", "chunk_softmax_importance", "refit_target", "selection", "compacted_softmax",
+          "normal_equations", "elimination", "quality_stats"]
+
+
+def gen_layers(L, T, H, d, W, seed):
+    """Yield (K, V, Q) float32 host arrays per layer. One pool of normals is
+    drawn once; each layer takes its own windows of it and its own channel
+    scales, so layers differ without drawing 26 GB of normals."""
+    E = H * d
+    rng = np.random.default_rng(seed)
+    pool = rng.standard_normal(3 * T * E + 4096, dtype=np.float32)
+    for l in range(L):
+        r = np.random.default_rng(seed * 1000 + l)
+        o1, o2 = (int(x) for x in r.integers(0, pool.size - T * E, size=2))
+        scale = np.exp(r.normal(0.0, 0.5, size=E)).astype(np.float32)
+        K = (pool[o1:o1 + T * E].reshape(T, E) * scale).astype(np.float32)
+        V = pool[o2:o2 + T * E].reshape(T, E)
+        Q = (K[-W:] + r.normal(0.0, 0.1, size=(W, E)).astype(np.float32)).astype(np.float32)
+        yield np.ascontiguousarray(K), np.ascontiguousarray(V), np.ascontiguousarray(Q)
+
+
+def stage_model(L, T, H, d, nq, t, n_chunks, tc):
+    """Algorithmic bytes and flops of each stage for one call (all layers).
+    Per (token, layer, head): scoring reads one key row (4d B) and does 2*nq*d
+    flops; the refit target reads one value row and does 2*nq*d flops."""
+    E = H * d
+    units = L * H * n_chunks
+    n, p = tc, d
+    elim = 2 * sum((n - 1 - c) * (n + p - c) for c in range(n))
+    back = 2 * p * sum(n - 1 - c for c in range(n))
+    m = {
+        "scores": dict(bytes=4 * L * T * E + 4 * L * H * nq * T, flops=2 * L * H * nq * T * d),
+        "chunk_softmax_importance": dict(bytes=4 * L * H * nq * T * 2 + 4 * L * H * T, flops=0),
+        "refit_target": dict(bytes=4 * L * H * nq * T + 4 * L * T * E, flops=2 * L * H * nq * T * d),
+        "selection": dict(bytes=4 * L * H * T + 4 * L * t, flops=0),
+        "compacted_softmax": dict(bytes=4 * L * H * nq * t * 2, flops=0),
+        "normal_equations": dict(bytes=4 * units * n * (n + p), flops=2 * nq * units * n * (n + p)),
+        "elimination": dict(bytes=4 * units * (2 * n * (n + p) + n * p), flops=units * (elim + back)),
+        "quality_stats": dict(bytes=4 * L * min(H, 4) * T * 2 * d, flops=2 * L * min(H, 4) * min(nq, 32) * T * 2 * d),
+    }
+    return m
+
+
+def roofline(name, model, ms):
+    b, f = model[name]["bytes"], model[name]["flops"]
+    t_hbm = b / (HBM_PEAK_GBS * 1e9)
+    t_cmp = f / (FP32_PEAK_TFLOPS * 1e12)
+    s = ms / 1e3
+    if t_cmp > t_hbm:
+        ach = f / s / 1e12
+        return dict(kernel=name, bound="mfma", achieved=round(ach, 3), peak=FP32_PEAK_TFLOPS, unit="TFLOP/s",
+                    frac=round(ach / FP32_PEAK_TFLOPS, 4), traffic=None, ms=round(ms, 3),
+                    algorithmic_flops=f, algorithmic_bytes=b)
+    ach = b / s / 1e9
+    return dict(kernel=name, bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                frac=round(ach / HBM_PEAK_GBS, 4), traffic=None, ms=round(ms, 3),
+                algorithmic_flops=f, algorithmic_bytes=b)
+
+
+def cpu_baseline(K, V, Q, T, H, d, ratio, L_total, diversity):
+    """The reference CPU path (compiled from its sources) on layer 0 at full T,
+    scaled to all layers; falls back to the oracle port."""
+    ref = REPO / "oracle" / "_ref" / "libkvref.so"
+    if ref.exists():
+        lib, kind = kc.Lib(ref), "reference"
+    else:
+        lib, kind = kc.Lib(REPO / "oracle" / "liboracle.so", prefix="orc_"), "port"
+    p = lib.params(target_ratio=ratio, use_diversity=diversity)
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or os.cpu_count()
+    t0 = time.perf_counter()
+    r = lib.compact(K, V, Q, T, Q.shape[0], H, d, d, p)
+    dt = time.perf_counter() - t0
+    per_layer = dt
+    return dict(value=round(T / (per_layer * L_total), 2), unit="tok/s", cores=threads, kind=kind,
+                sample=f"layer 0 of {L_total} at full T={T} ({dt:.1f} s, all-layer rate = T/(time*{L_total}))",
+                seconds=round(dt, 2), kept=r.t, cos=r.stats["avg_cosine_sim"])
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--T", type=int, default=100000)
+    ap.add_argument("--heads", type=int, default=8)
+    ap.add_argument("--dim", type=int, default=128)
+    ap.add_argument("--ratio", type=float, default=0.2)
+    ap.add_argument("--window", type=int, default=32)
+    ap.add_argument("--diversity", type=int, default=0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--seed", type=int, default=1234)
+    a = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if a.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (asked for {max(a.gpus, world)}); "
+              "the compaction path shards by layer or chunk with no exchange, which this build does not run",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import hiprt
+    lib = kc.load_product()
+    dll = kc.bind_device_api(lib.dll)
+    if not dll.kv_compact_hip_available():
+        raise SystemExit("no usable GPU")
+    L, T, H, d, W = a.layers, a.T, a.heads, a.dim, a.window
+    E = H * d
+    p = lib.params(target_ratio=a.ratio, use_diversity=a.diversity)
+    t, n_chunks = kc.plan(dll, T, W, True, p)
+
+    dK = hiprt.DevBuf(L * T * E * 4)
+    dV = hiprt.DevBuf(L * T * E * 4)
+    dQ = hiprt.DevBuf(L * W * E * 4)
+    first = None
+    t0 = time.perf_counter()
+    for l, (K, V, Q) in enumerate(gen_layers(L, T, H, d, W, a.seed)):
+        dK.upload(K, l * T * E * 4)
+        dV.upload(V, l * T * E * 4)
+        dQ.upload(Q, l * W * E * 4)
+        if l == 0:
+            first = (K.copy(), V.copy(), Q.copy())
+    print(f"[bench] data ready: {L} layers x T={T} x {H}x{d} ({2 * L * T * E * 4 / 1e9:.1f} GB) in "
+          f"{time.perf_counter() - t0:.1f} s; t={t} per layer, {n_chunks} chunks", file=sys.stderr, flush=True)
+    idx = hiprt.DevBuf(L * t * 4)
+    beta = hiprt.DevBuf(L * H * t * 4)
+    cv = hiprt.DevBuf(L * H * t * d * 4)
+    st = hiprt.DevBuf(L * 3 * 4)
+    out = kc.DeviceOut(idx.value, beta.value, cv.value, st.value)
+
+    def step():
+        rc = dll.kvc_compact_layers_device(dK.value, dV.value, dQ.value, L, T, W, H, d, d, T * E, T * E, W * E,
+                                           ctypes.byref(p), None, ctypes.byref(out), None)
+        if rc != 0:
+            raise RuntimeError(f"kvc_compact_layers_device returned {rc}")
+
+    stage_acc = np.zeros(len(STAGES))
+    buf = (ctypes.c_float * len(STAGES))()
+    for i in range(a.warmup):
+        ts = time.perf_counter()
+        step()
+        print(f"[bench] warmup {i}: {(time.perf_counter() - ts) * 1e3:.1f} ms", file=sys.stderr, flush=True)
+    hiprt.synchronize()
+    times = []
+    t_start = time.perf_counter()
+    for i in range(a.steps):
+        ts = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - ts)
+        dll.kvc_stage_times(buf, len(STAGES))
+        stage_acc += np.array(buf[:])
+        print(f"[bench] step {i}: {times[-1] * 1e3:.1f} ms", file=sys.stderr, flush=True)
+    hiprt.synchronize()
+    total = time.perf_counter() - t_start
+    ms = total / a.steps * 1e3
+    stage_ms = stage_acc / a.steps
+    model = stage_model(L, T, H, d, W, t, n_chunks, 256 if n_chunks > 1 else t)
+    dom = STAGES[int(np.argmax(stage_ms))]
+    roof = roofline(dom, model, float(stage_ms[int(np.argmax(stage_ms))]))
+    stats = st.download(np.float32, L * 3).reshape(L, 3)
+
+    cpu = None
+    if not a.no_cpu:
+        K0, V0, Q0 = first
+        cpu = cpu_baseline(K0, V0, Q0, T, H, d, a.ratio, L, a.diversity)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+
+    line = {
+        "metric": "compacted tok/s @100k ctx, 20% keep (32L×8H, d=128); % of MFMA/HBM peak",
+        "value": round(T / (ms / 1e3), 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{L} layers x {H} KV heads x d={d}, T={T}, fp32, keep {a.ratio:g} "
+                        f"(t={t}/layer, {n_chunks} chunks), SnapKV W={W}, RMS, skip_beta=1, "
+                        f"diversity={'on' if a.diversity else 'off'}",
+            "layers": L, "T": T, "kv_heads": H, "head_dim": d, "keep_ratio": a.ratio, "kept_per_layer": t,
+            "parallelism": "single GPU", "device": hiprt.device_name(),
+        },
+        "stage_ms": {k: round(float(v), 3) for k, v in zip(STAGES, stage_ms)},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "speedup_vs_cpu": round((T / (ms / 1e3)) / cpu["value"], 1) if cpu else None,
+        "quality": {"avg_cosine_sim_layer0": float(stats[0, 0]), "avg_cosine_sim_min": float(stats[:, 0].min())},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
