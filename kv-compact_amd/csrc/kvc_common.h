@@ -53,13 +53,16 @@ struct Work {
     float * Y;        // [L][n_chunks][H][nq_max][dv]
     int   * sel;      // [L][t_total]        kept token positions (layer-local), ascending
     float * X;        // [L][H][nq_max][t_total] compacted softmax weights
-    float * aug;      // GE workspace: one [tc][tc + dv] system per (layer, chunk, head)
+    float * aug;      // GE workspace: one column-major [tc + dv][tc] system per (layer, chunk, head)
+    int   * perm;     // [L][n_chunks][H][tc_max] pivot order of each system
+    float * Ut;       // [L][n_chunks][H][256][256] U rows by logical row (systems with tc <= 256)
+    float * Bt;       // [L][n_chunks][H][256][dv] eliminated right-hand sides by logical row
     long long * aug_off; // [L][n_chunks][H] element offsets into aug
     float * gtmp;     // [L][n_chunks][H][tc_max + tc_max + dv] GE factor / pivot-row spill
     int   * cand;     // [L][n_chunks][Tc_max] selection candidates
     unsigned char * flags; // [L][n_chunks][Tc_max]
     float * wts;      // [T] R-KV weights (nullptr when disabled)
-    ChunkDesc * chunks;  // [n_chunks + 1]; the extra entry covers the whole call
+    ChunkDesc * chunks;  // [n_chunks + 2]; then all T keys, then the kept keys (statistics)
 };
 
 // Statistics scratch (api.cpp:239-325 sampling: h < min(H,4), qi < min(nq,32))

@@ -179,7 +179,7 @@ int chunk_size(int T, const kv_compact_params & p) {
 struct Plan {
     int T = 0, n_chunks = 0, t_total = 0, nq_max = 0, tc_max = 0, Tc_max = 0;
     int qmode = Q_PROVIDED, nq_global = 0, stats_qmode = Q_PROVIDED;
-    std::vector<ChunkDesc> chunks;  // n_chunks + 1 (whole call last)
+    std::vector<ChunkDesc> chunks;  // n_chunks, then the two statistics pseudo-chunks
 };
 
 // Chunk plan of one call; the per-chunk recursion of api.cpp:466-499 is
@@ -232,6 +232,7 @@ void make_plan(int T, int n_q, bool q_given, const kv_compact_params & p, Plan &
         pl.tc_max = std::max(pl.tc_max, d.tc);
         pl.Tc_max = std::max(pl.Tc_max, d.Tc);
     }
+    // statistics pseudo-chunks: all T keys, then the t_total kept keys
     ChunkDesc whole;
     whole.start = 0;
     whole.Tc = T;
@@ -239,6 +240,8 @@ void make_plan(int T, int n_q, bool q_given, const kv_compact_params & p, Plan &
     whole.prefix = 0;
     whole.off = 0;
     whole.nq = nq_outer;
+    pl.chunks.push_back(whole);
+    whole.Tc = pl.t_total;
     pl.chunks.push_back(whole);
 }
 
@@ -290,6 +293,10 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, bool need_e, Carver 
     for (int c = 0; c < pl.n_chunks; c++) aug_elems += (size_t)pl.chunks[c].tc * (pl.chunks[c].tc + dv);
     ww.aug = cv.take<float>(L * H * aug_elems);
     ww.aug_off = cv.take<long long>(L * nc * H);
+    ww.perm = cv.take<int>(L * nc * H * (size_t)pl.tc_max);
+    const size_t ut_rows = pl.tc_max <= 256 ? 256 : 0;
+    ww.Ut = cv.take<float>(L * nc * H * ut_rows * ut_rows);
+    ww.Bt = cv.take<float>(L * nc * H * ut_rows * dv);
     ww.gtmp = cv.take<float>(L * nc * H * (2 * (size_t)pl.tc_max + dv));
     ww.cand = cv.take<int>(L * nc * (size_t)pl.Tc_max);
     ww.flags = cv.take<unsigned char>(L * nc * (size_t)pl.Tc_max);
@@ -673,7 +680,9 @@ int kv_compact_multi_round(const float * K_all, const float * V_all, const float
         sp.chunk_size = -1;
         make_plan(T, nqm, true, sp, pl);
         pl.t_total = result->t;
-        pl.chunks.back().tc = result->t;
+        pl.chunks[pl.n_chunks].tc = result->t;
+        pl.chunks[pl.n_chunks + 1].Tc = result->t;
+        pl.chunks[pl.n_chunks + 1].tc = result->t;
         BatchIO io{};
         io.L = 1; io.T = T; io.n_q = nqm; io.H = H; io.dk = d_k; io.dv = d_v;
         io.ldK = (long long)T * ek; io.ldV = (long long)T * ev; io.ldQ = (long long)nqm * ek;

@@ -83,7 +83,8 @@ constexpr int SC_KEYS = 64, SC_SLAB = 32, SC_ROWS = 64;
 __global__ void __launch_bounds__(256)
 k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ K,
          const float * __restrict__ Q, float * __restrict__ S, int Hs, int nq_cap,
-         long long s_layer, long long s_head, long long s_row, int qmode) {
+         long long s_layer, long long s_head, long long s_row, int qmode,
+         const int * __restrict__ key_idx, const float * __restrict__ beta) {
     const int c_idx = blockIdx.y / Hs, h = blockIdx.y % Hs, layer = blockIdx.z;
     const ChunkDesc c = chunks[c_idx];
     const int key0 = blockIdx.x * SC_KEYS;
@@ -95,7 +96,10 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
     const int tid = threadIdx.x;
     const int kl = tid & 63, grp = tid >> 6;
     const long long ek = (long long)g.H * g.dk;
-    const float * Kl = K + layer * g.ldK + (long long)c.start * ek + (long long)h * g.dk;
+    // key_idx: keys are rows key_idx[layer * t_total + j] (compacted statistics)
+    const float * Kl = K + layer * g.ldK + (key_idx ? 0 : (long long)c.start * ek) + (long long)h * g.dk;
+    const int * kix = key_idx ? key_idx + (long long)layer * g.t_total : nullptr;
+    const float * bh = beta ? beta + ((long long)layer * g.H + h) * g.t_total : nullptr;
     float * Sl = S + layer * s_layer + h * s_head + c.start;
     for (int q0 = 0; q0 < nq; q0 += SC_ROWS) {
         __syncthreads();
@@ -111,7 +115,8 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
             for (int e = tid; e < SC_KEYS * SC_SLAB; e += 256) {
                 const int kk = e / SC_SLAB, dd = e % SC_SLAB;
                 const int key = key0 + kk, dim = d0 + dd;
-                ks[kk][dd] = (key < c.Tc && dim < g.dk) ? Kl[(long long)key * ek + dim] : 0.0f;
+                const long long krow = kix ? (long long)(key < c.Tc ? kix[key] : 0) : (long long)key;
+                ks[kk][dd] = (key < c.Tc && dim < g.dk) ? Kl[krow * ek + dim] : 0.0f;
             }
             for (int e = tid; e < SC_ROWS * SC_SLAB; e += 256) {
                 const int rr = e / SC_SLAB, dd = e % SC_SLAB;
@@ -132,7 +137,11 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
 #pragma unroll
             for (int r = 0; r < SC_ROWS / 4; r++) {
                 const int qi = q0 + grp + 4 * r;
-                if (qi < nq) Sl[(long long)qi * s_row + key] = acc[r] * g.inv_sqrt_dk;
+                if (qi < nq) {
+                    float v = acc[r] * g.inv_sqrt_dk;
+                    if (bh) v = v + bh[key];
+                    Sl[(long long)qi * s_row + key] = v;
+                }
             }
         }
     }
@@ -239,61 +248,100 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
 }
 
 // ---------------------------------------------------------------------------
-// Refit target Y = A V over the chunk (math.h:70-80), sequential over keys.
-// A pass covers QB query rows x dv outputs (<= 4096, 16 per thread); keys
-// staged through LDS 32 at a time. grid = (n_chunks * H, L); dv <= 256.
+// Attention-weighted sums out[qi][v] = sum_j a[qi][j] * val[j][v], each
+// output accumulated sequentially over j (math.h:70-80 for the refit target
+// Y = A V; api.cpp:271-292 for the statistics' outputs). A block owns QB x vn
+// outputs (PER per thread); keys are staged through LDS 32 at a time.
+//   mode 0: refit target of a (layer, chunk, head)        grid (n_chunks*H, L)
+//   mode 1: statistics, original attention over all T      grid (mh*nvb, L)
+//   mode 2: statistics, compacted attention over t_total   grid (mh*nvb, L)
 // ---------------------------------------------------------------------------
-constexpr int Y_KT = 32;
+constexpr int AS_KT = 32;
+
+// Register-blocked tile: 256 threads as TQ x TV; thread (tq, tv) owns
+// queries tq + TQ*i (i < QR) and columns tv + TV*k (k < VR) of a QB x VB
+// output block (QB = TQ*QR, VB = TV*VR); every output is a sequential sum
+// over the keys in order.
+template <int QR, int VR, int TV>
+__device__ __forceinline__ void attn_sum_tile(const float * __restrict__ a, long long a_rs, int nq,
+                                              const float * __restrict__ val, long long val_rs, int n,
+                                              int vn, float * __restrict__ out, long long out_rs) {
+    constexpr int TQ = 256 / TV, QB = TQ * QR, VB = TV * VR;
+    __shared__ float as[QB][AS_KT + 1];
+    __shared__ float vs[AS_KT][VB + 1];
+    const int tq = threadIdx.x / TV, tv = threadIdx.x % TV;
+    for (int v0 = 0; v0 < vn; v0 += VB) {
+        const int vb = min(VB, vn - v0);
+        for (int q0 = 0; q0 < nq; q0 += QB) {
+            const int qb = min(QB, nq - q0);
+            float acc[QR][VR];
+#pragma unroll
+            for (int i = 0; i < QR; i++)
+#pragma unroll
+                for (int k = 0; k < VR; k++) acc[i][k] = 0.0f;
+            for (int j0 = 0; j0 < n; j0 += AS_KT) {
+                const int jn = min(AS_KT, n - j0);
+                __syncthreads();
+                for (int e = threadIdx.x; e < QB * AS_KT; e += 256) {
+                    const int qi = e / AS_KT, jj = e % AS_KT;
+                    as[qi][jj] = (qi < qb && jj < jn) ? a[(long long)(q0 + qi) * a_rs + j0 + jj] : 0.0f;
+                }
+                for (int e = threadIdx.x; e < AS_KT * VB; e += 256) {
+                    const int jj = e / VB, vv = e % VB;
+                    vs[jj][vv] = (jj < jn && vv < vb) ? val[(long long)(j0 + jj) * val_rs + v0 + vv] : 0.0f;
+                }
+                __syncthreads();
+                for (int jj = 0; jj < jn; jj++) {
+                    float av[QR], vv[VR];
+#pragma unroll
+                    for (int i = 0; i < QR; i++) av[i] = as[tq + TQ * i][jj];
+#pragma unroll
+                    for (int k = 0; k < VR; k++) vv[k] = vs[jj][tv + TV * k];
+#pragma unroll
+                    for (int i = 0; i < QR; i++)
+#pragma unroll
+                        for (int k = 0; k < VR; k++) acc[i][k] += av[i] * vv[k];
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < QR; i++) {
+                const int qi = tq + TQ * i;
+#pragma unroll
+                for (int k = 0; k < VR; k++) {
+                    const int vv = tv + TV * k;
+                    if (qi < qb && vv < vb) out[(long long)(q0 + qi) * out_rs + v0 + vv] = acc[i][k];
+                }
+            }
+        }
+    }
+}
 
 __global__ void __launch_bounds__(256)
 k_refit_target(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ A,
                const float * __restrict__ V, float * __restrict__ Y) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
-    const long long rs = g.T;
-    const float * Ah = A + layer * lS(g) + h * hS(g) + c.start;
     const long long ev = (long long)g.H * g.dv;
-    const float * Vh = V + layer * g.ldV + (long long)c.start * ev + (long long)h * g.dv;
-    float * Yh = Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv;
-    const int nq = c.nq, n = c.Tc, dv = g.dv;
-    const int QB = max(1, min(64, 4096 / dv));
-    constexpr int PER = 16;
-    __shared__ float as[64][Y_KT + 1];
-    __shared__ float vs[Y_KT][257];
-    for (int q0 = 0; q0 < nq; q0 += QB) {
-        const int qn = min(QB, nq - q0);
-        const int n_out = qn * dv;
-        float acc[PER];
-#pragma unroll
-        for (int i = 0; i < PER; i++) acc[i] = 0.0f;
-        for (int j0 = 0; j0 < n; j0 += Y_KT) {
-            const int jn = min(Y_KT, n - j0);
-            __syncthreads();
-            for (int e = threadIdx.x; e < 64 * Y_KT; e += 256) {
-                const int qi = e / Y_KT, jj = e % Y_KT;
-                as[qi][jj] = (qi < qn && jj < jn) ? Ah[(q0 + qi) * rs + j0 + jj] : 0.0f;
-            }
-            for (int e = threadIdx.x; e < Y_KT * 256; e += 256) {
-                const int jj = e / 256, vv = e % 256;
-                vs[jj][vv] = (jj < jn && vv < dv) ? Vh[(long long)(j0 + jj) * ev + vv] : 0.0f;
-            }
-            __syncthreads();
-#pragma unroll
-            for (int i = 0; i < PER; i++) {
-                const int o = threadIdx.x + 256 * i;
-                if (o < n_out) {
-                    const int qi = o / dv, vv = o % dv;
-                    float a = acc[i];
-                    for (int jj = 0; jj < jn; jj++) a += as[qi][jj] * vs[jj][vv];
-                    acc[i] = a;
-                }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < PER; i++) {
-            const int o = threadIdx.x + 256 * i;
-            if (o < n_out) Yh[(long long)q0 * dv + o] = acc[i];
-        }
+    attn_sum_tile<4, 4, 32>(A + layer * lS(g) + h * hS(g) + c.start, g.T, c.nq,
+                            V + layer * g.ldV + (long long)c.start * ev + (long long)h * g.dv, ev, c.Tc, g.dv,
+                            Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv, g.dv);
+}
+
+constexpr int ST_VB = 32;   // value columns per statistics block
+
+__global__ void __launch_bounds__(256)
+k_stats_sum(Geom g, const float * __restrict__ a, int n, const float * __restrict__ V,
+            const float * __restrict__ Cv, int mode, float * __restrict__ out, int mh, int mq) {
+    const int nvb = (g.dv + ST_VB - 1) / ST_VB;
+    const int h = blockIdx.x / nvb, v0 = (blockIdx.x % nvb) * ST_VB, layer = blockIdx.y;
+    const int vn = min(ST_VB, g.dv - v0);
+    const float * ar = a + (((long long)layer * mh + h) * mq) * n;
+    float * o = out + (((long long)layer * mh + h) * mq) * g.dv + v0;
+    if (mode == 1) {
+        const long long ev = (long long)g.H * g.dv;
+        attn_sum_tile<2, 2, 16>(ar, n, mq, V + layer * g.ldV + (long long)h * g.dv + v0, ev, n, vn, o, g.dv);
+    } else {
+        attn_sum_tile<2, 2, 16>(ar, n, mq, Cv + ((long long)layer * g.H + h) * g.t_total * g.dv + v0, g.dv, n, vn, o, g.dv);
     }
 }
 
@@ -454,56 +502,369 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
     const long long hsX = (long long)g.nq_max * g.t_total;
     float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
     __shared__ float red[16];
-    __shared__ float rinv;
-    for (int qi = 0; qi < nq; qi++) {
-        float * xr = Xh + (long long)qi * g.t_total;
-        for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = Sh[(long long)qi * g.T + sl[j]] + bh[j];
-        __syncthreads();
-        const float m = ref_row_max(xr, t, red);
-        for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = expf_ref(xr[j] - m);
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            float sum = 0.0f;
-            for (int j = 0; j < t; j++) sum += xr[j];
-            rinv = 1.0f / (sum + 1e-12f);
+    __shared__ float rmax[256], rinv[256];
+    for (int base = 0; base < nq; base += 256) {
+        const int nb = min(256, nq - base);
+        for (int r = 0; r < nb; r++) {
+            float * xr = Xh + (long long)(base + r) * g.t_total;
+            const float * sr = Sh + (long long)(base + r) * g.T;
+            for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = sr[sl[j]] + bh[j];
         }
         __syncthreads();
-        const float iv = rinv;
-        for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = xr[j] * iv;
+        for (int r = 0; r < nb; r++) {
+            const float m = ref_row_max(Xh + (long long)(base + r) * g.t_total, t, red);
+            if (threadIdx.x == 0) rmax[r] = m;
+        }
+        __syncthreads();
+        for (int r = 0; r < nb; r++) {
+            float * xr = Xh + (long long)(base + r) * g.t_total;
+            const float mx = rmax[r];
+            for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = expf_ref(xr[j] - mx);
+        }
+        __syncthreads();
+        if ((int)threadIdx.x < nb) {
+            const float * xr = Xh + (long long)(base + threadIdx.x) * g.t_total;
+            float sum = 0.0f;
+            for (int j = 0; j < t; j++) sum += xr[j];
+            rinv[threadIdx.x] = 1.0f / (sum + 1e-12f);
+        }
+        __syncthreads();
+        for (int r = 0; r < nb; r++) {
+            float * xr = Xh + (long long)(base + r) * g.t_total;
+            const float iv = rinv[r];
+            for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = xr[j] * iv;
+        }
         __syncthreads();
     }
 }
 
+// one block per system; X (nq x n) and Y (nq x p) staged in (dynamic) LDS
+// when they fit its budget
+constexpr int LB_LDS_FLOATS = 24576;
+
 __global__ void __launch_bounds__(256)
 k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ X,
-           const float * __restrict__ Y, float * __restrict__ aug, const long long * __restrict__ aug_off) {
-    const int c_idx = blockIdx.y / g.H, h = blockIdx.y % g.H, layer = blockIdx.z;
+           const float * __restrict__ Y, float * __restrict__ aug, const long long * __restrict__ aug_off,
+           int lds_floats) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const int n = c.tc, p = g.dv, w = n + p, nq = c.nq;
     float * Ag = aug + aug_off[((long long)layer * g.n_chunks + c_idx) * g.H + h];
     const long long hsX = (long long)g.nq_max * g.t_total;
     const float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
     const float * Yh = Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv;
+    extern __shared__ float xs[];
+    const bool staged = (long long)nq * w <= lds_floats;
+    if (staged) {
+        // xs[k][0..n) = X row k, xs[k][n..n+p) = Y row k
+        for (int e = threadIdx.x; e < nq * w; e += blockDim.x) {
+            const int k = e / w, j = e % w;
+            xs[e] = (j < n) ? Xh[(long long)k * g.t_total + j] : Yh[(long long)k * g.dv + (j - n)];
+        }
+        __syncthreads();
+    }
     const long long total = (long long)n * w;
-    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
-         e += (long long)gridDim.x * blockDim.x) {
-        const int i = (int)(e / w), j = (int)(e % w);
+    // column-major: entry (row i, column j) at Ag[j * n + i]
+    for (long long e = threadIdx.x; e < total; e += blockDim.x) {
+        const int j = (int)(e / n), i = (int)(e % n);
         float s = 0.0f;
-        if (j < n) {
+        if (staged) {
+            for (int k = 0; k < nq; k++) s += xs[k * w + i] * xs[k * w + j];
+        } else if (j < n) {
             for (int k = 0; k < nq; k++) s += Xh[(long long)k * g.t_total + i] * Xh[(long long)k * g.t_total + j];
-            if (i == j) s += g.ridge;
         } else {
             for (int k = 0; k < nq; k++) s += Xh[(long long)k * g.t_total + i] * Yh[(long long)k * g.dv + (j - n)];
         }
+        if (i == j) s += g.ridge;
         Ag[e] = s;
     }
 }
 
 // ---------------------------------------------------------------------------
-// Gaussian elimination with partial pivoting + back substitution on
-// [M | B] (n x (n + p)), math.h:494-556; one block per system, matrix in
-// global memory. Skipped pivots give zero_val rows of x (row stride ldx).
+// Gaussian elimination with partial pivoting + back substitution on [M | B]
+// (n x (n + p)), math.h:494-556. Storage is column-major: entry (r, j) at
+// a[j * n + r] (M is symmetric, B is stored transposed).
+//
+// k_ge_elim (n <= 256), phase 1: the n x n matrix lives in registers; 16
+// waves own 16-column strips, lane l owns rows l, l+64, l+128, l+192. Row
+// swaps become a logical->physical permutation. An LDS copy (panel) of the
+// strip holding the current column serves the pivot search; the multiplier
+// of each remaining row replaces that row's entry in the current column of
+// the panel (the reference never reads it again), so a retired panel is the
+// final column of the factorisation: U entries in rows already used as
+// pivots, multipliers in the others. Entries left of the current column of
+// the remaining rows are updated too and never read.
+// Phase 2 replays the same multiply-subtract sequence on the right-hand
+// sides, one 16-column strip per wave, pivot-row values read from the owning
+// lane, so B ends as the reference's eliminated right-hand side.
+// k_ge_backsub: back substitution in the reference's order, one thread per
+// right-hand side. k_ge_general: the same arithmetic for n > 256 in global
+// memory.
 // ---------------------------------------------------------------------------
+constexpr int RG_ROWS = 256, RG_STRIP = 16, RG_WAVES = 16, RG_SLOTS = 4;
+constexpr int RG_THREADS = RG_WAVES * 64;
+
+template <int S>
+__device__ __forceinline__ void rg_lane_strip(const float (&a)[RG_SLOTS][RG_STRIP], int src_lane, float (&sp)[RG_STRIP]) {
+#pragma unroll
+    for (int jj = 0; jj < RG_STRIP; jj++)
+        sp[jj] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[S][jj]), src_lane));
+}
+
+__device__ __forceinline__ void rg_pivot_values(const float (&a)[RG_SLOTS][RG_STRIP], int P, float (&sp)[RG_STRIP]) {
+    const int src = P & 63, slot = P >> 6;
+    if (slot == 0) rg_lane_strip<0>(a, src, sp);
+    else if (slot == 1) rg_lane_strip<1>(a, src, sp);
+    else if (slot == 2) rg_lane_strip<2>(a, src, sp);
+    else rg_lane_strip<3>(a, src, sp);
+}
+
+__global__ void __launch_bounds__(RG_THREADS)
+k_ge_elim(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__ aug,
+          const long long * __restrict__ aug_off, int * __restrict__ perm_out,
+          float * __restrict__ Ut_all, float * __restrict__ Bt_all) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const int n = c.tc;
+    if (n > RG_ROWS) return;
+    const long long sys = ((long long)layer * g.n_chunks + c_idx) * g.H + h;
+    float * A = aug + aug_off[sys];
+    int * perm_g = perm_out + sys * (long long)g.tc_max;
+    // U rows (row-major by logical row, n x n) and eliminated right-hand
+    // sides (row-major by logical row, n x dv) for the back substitution
+    float * Ut = Ut_all + sys * (long long)RG_ROWS * RG_ROWS;
+    float * Bt = Bt_all + sys * (long long)RG_ROWS * g.dv;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    __shared__ float panel[RG_ROWS][RG_STRIP + 1];
+    __shared__ float fac[RG_ROWS];
+    __shared__ int perm[RG_ROWS], inv[RG_ROWS], dstep[RG_ROWS], pivrow[RG_ROWS];
+    __shared__ unsigned char skip[RG_ROWS];
+    __shared__ float redv[4];
+    __shared__ int redi[4];
+
+    float a[RG_SLOTS][RG_STRIP];
+#pragma unroll
+    for (int s = 0; s < RG_SLOTS; s++) {
+        const int r = lane + 64 * s;
+#pragma unroll
+        for (int jj = 0; jj < RG_STRIP; jj++) {
+            const int j = RG_STRIP * w + jj;
+            a[s][jj] = (r < n && j < n) ? A[(long long)j * n + r] : 0.0f;
+        }
+    }
+    if (tid < RG_ROWS) {
+        perm[tid] = tid;
+        inv[tid] = tid;
+        dstep[tid] = (tid < n) ? RG_ROWS : -1;   // -1: padding row, never a pivot
+    }
+    __syncthreads();
+    for (int col = 0; col < n; col++) {
+        const int k = col & (RG_STRIP - 1);
+        if (k == 0) {
+            if (w == col / RG_STRIP) {
+#pragma unroll
+                for (int s = 0; s < RG_SLOTS; s++)
+#pragma unroll
+                    for (int kk = 0; kk < RG_STRIP; kk++) panel[lane + 64 * s][kk] = a[s][kk];
+            }
+            __syncthreads();
+        }
+        // pivot: largest |value| in column col over rows not yet used,
+        // smallest logical index on ties (the reference's first maximum)
+        float bv = -1.0f;
+        int bl = 0x7fffffff;
+        if (tid < RG_ROWS) {
+            if (dstep[tid] == RG_ROWS) {
+                const float v = fabsf(panel[tid][k]);
+                if (v == v) { bv = v; bl = inv[tid]; }
+            }
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(bv, o);
+                const int ol = __shfl_xor(bl, o);
+                if (ov > bv || (ov == bv && ol < bl)) { bv = ov; bl = ol; }
+            }
+            if (lane == 0) { redv[w] = bv; redi[w] = bl; }
+        }
+        __syncthreads();
+        float b = redv[0];
+        int bli = redi[0];
+#pragma unroll
+        for (int i = 1; i < 4; i++)
+            if (redv[i] > b || (redv[i] == b && redi[i] < bli)) { b = redv[i]; bli = redi[i]; }
+        const int Pc = perm[col];
+        const float a0 = fabsf(panel[Pc][k]);
+        const int mr = (a0 == a0 && b > a0) ? bli : col;
+        const int P = perm[mr];
+        const float piv = panel[P][k];
+        const bool elim = !(fabsf(piv) < 1e-12f);
+        // multipliers of the rows still unused (not P); they enter the panel
+        // column only after the barrier, once every wave has read its pivot
+        if (tid < RG_ROWS) {
+            float f = 0.0f;
+            if (elim && tid != P && dstep[tid] == RG_ROWS) f = panel[tid][k] / piv;
+            fac[tid] = f;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            perm[col] = P;
+            perm[mr] = Pc;
+            inv[P] = col;
+            inv[Pc] = mr;
+            dstep[P] = col;
+            pivrow[col] = P;
+            skip[col] = elim ? 0 : 1;
+        }
+        // the pivot row is final from here on: it becomes U row col (the
+        // diagonal here, the columns right of it from each live strip below)
+        if (tid == 0) Ut[(long long)col * RG_ROWS + col] = piv;
+        if (elim) {
+            if (RG_STRIP * w + RG_STRIP - 1 > col) {
+                float sp[RG_STRIP];
+                rg_pivot_values(a, P, sp);
+                if (lane == 0) {
+#pragma unroll
+                    for (int jj = 0; jj < RG_STRIP; jj++) {
+                        const int j = RG_STRIP * w + jj;
+                        if (j > col && j < n) Ut[(long long)col * RG_ROWS + j] = sp[jj];
+                    }
+                }
+#pragma unroll
+                for (int s = 0; s < RG_SLOTS; s++) {
+                    const int r = lane + 64 * s;
+                    if (r != P && dstep[r] == RG_ROWS) {
+                        const float f = fac[r];
+#pragma unroll
+                        for (int jj = 0; jj < RG_STRIP; jj++) a[s][jj] = a[s][jj] - f * sp[jj];
+                    }
+                }
+            }
+            for (int e = tid; e < RG_ROWS * RG_STRIP; e += RG_THREADS) {
+                const int r = e >> 4, kk = e & (RG_STRIP - 1);
+                if (kk >= k && r != P && dstep[r] == RG_ROWS) {
+                    if (kk == k) panel[r][kk] = fac[r];
+                    else panel[r][kk] = panel[r][kk] - fac[r] * panel[P][kk];
+                }
+            }
+        }
+        __syncthreads();
+        if (k == RG_STRIP - 1 || col == n - 1) {
+            // retire the panel: final factorisation columns [col - k, col]
+            const int c0 = col - k;
+            for (int e = tid; e < RG_ROWS * RG_STRIP; e += RG_THREADS) {
+                const int kk = e >> 8, r = e & (RG_ROWS - 1);
+                if (r < n && c0 + kk < n) A[(long long)(c0 + kk) * n + r] = panel[r][kk];
+            }
+            __syncthreads();
+        }
+    }
+    if (tid < n) perm_g[tid] = pivrow[tid];
+    __syncthreads();
+
+    // phase 2: right-hand sides, 16 columns per wave per pass
+    const int p_total = g.dv;
+    for (int v0 = 0; v0 < p_total; v0 += RG_WAVES * RG_STRIP) {
+        float bb[RG_SLOTS][RG_STRIP];
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            const int r = lane + 64 * s;
+#pragma unroll
+            for (int jj = 0; jj < RG_STRIP; jj++) {
+                const int v = v0 + RG_STRIP * w + jj;
+                bb[s][jj] = (r < n && v < p_total) ? A[(long long)(n + v) * n + r] : 0.0f;
+            }
+        }
+        if (v0 + RG_STRIP * w < p_total) {
+            for (int col = 0; col < n; col++) {
+                if (skip[col]) continue;
+                const int P = pivrow[col];
+                float sp[RG_STRIP];
+                rg_pivot_values(bb, P, sp);
+#pragma unroll
+                for (int s = 0; s < RG_SLOTS; s++) {
+                    const int r = lane + 64 * s;
+                    if (dstep[r] > col) {
+                        const float f = A[(long long)col * n + r];
+#pragma unroll
+                        for (int jj = 0; jj < RG_STRIP; jj++) bb[s][jj] = bb[s][jj] - f * sp[jj];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            const int r = lane + 64 * s;
+            if (r < n) {
+                const int lr = inv[r];
+#pragma unroll
+                for (int jj = 0; jj < RG_STRIP; jj++) {
+                    const int v = v0 + RG_STRIP * w + jj;
+                    if (v < p_total) Bt[(long long)lr * g.dv + v] = bb[s][jj];
+                }
+            }
+        }
+    }
+}
+
+// Back substitution (math.h:540-556) for n <= 256: one wave per 64 right-hand
+// sides, lane v runs x[col][v] = (b[col][v] - sum_{r>col} U[col][r] x[r][v]) / U[col][col]
+// with the sum in ascending r. Rows [hb, n) (the first solved, hb = n - 128
+// when n > 128) move from LDS into registers once solved; the remaining rows
+// then read them through a statically unrolled loop, their own earlier
+// results from LDS. U rows are uniform across the wave.
+constexpr int BS_HIGH = 128;
+
+__global__ void __launch_bounds__(64)
+k_ge_backsub(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ Ut_all,
+             const float * __restrict__ Bt_all, float * __restrict__ Cv) {
+    const int sysl = blockIdx.x;   // (layer, chunk, head)
+    const int h = sysl % g.H, c_idx = (sysl / g.H) % g.n_chunks, layer = sysl / (g.H * g.n_chunks);
+    const ChunkDesc c = chunks[c_idx];
+    const int n = c.tc, p = g.dv;
+    if (n > RG_ROWS) return;
+    const int lane = threadIdx.x;
+    const int v = blockIdx.y * 64 + lane;
+    const bool act = v < p;
+    const float * __restrict__ Ut = Ut_all + (long long)sysl * RG_ROWS * RG_ROWS;
+    const float * __restrict__ Bt = Bt_all + (long long)sysl * RG_ROWS * g.dv;
+    float * x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
+    __shared__ float xs[BS_HIGH][64];
+    const int hb = n > BS_HIGH ? n - BS_HIGH : 0;
+    // rows [hb, n): all terms among themselves, x in LDS
+    for (int col = n - 1; col >= hb; col--) {
+        const float * u = Ut + (long long)col * RG_ROWS;
+        const float piv = u[col];
+        float val = 0.0f;
+        if (!(fabsf(piv) < 1e-12f)) {
+            val = act ? Bt[(long long)col * g.dv + v] : 0.0f;
+            for (int r = col + 1; r < n; r++) val -= u[r] * xs[r - hb][lane];
+            val = val / piv;
+        }
+        xs[col - hb][lane] = val;
+        if (act) x[(long long)col * g.dv + v] = val;
+    }
+    if (hb == 0) return;
+    float xh[BS_HIGH];
+#pragma unroll
+    for (int i = 0; i < BS_HIGH; i++) xh[i] = xs[i][lane];
+    // rows [0, hb): earlier low rows from LDS, then the high rows from registers
+    for (int col = hb - 1; col >= 0; col--) {
+        const float * u = Ut + (long long)col * RG_ROWS;
+        const float piv = u[col];
+        float val = 0.0f;
+        if (!(fabsf(piv) < 1e-12f)) {
+            val = act ? Bt[(long long)col * g.dv + v] : 0.0f;
+            for (int r = col + 1; r < hb; r++) val -= u[r] * xs[r][lane];
+            const float * uh = u + hb;
+#pragma unroll
+            for (int i = 0; i < BS_HIGH; i++) val -= uh[i] * xh[i];
+            val = val / piv;
+        }
+        xs[col][lane] = val;
+        if (act) x[(long long)col * g.dv + v] = val;
+    }
+}
+
+// general size: physical row swaps in global memory, column-major storage
 __device__ void ge_solve_block(float * __restrict__ a, int n, int p, float * __restrict__ x,
                                long long ldx, float zero_val, float * prow, float * fac) {
     const int w = n + p;
@@ -511,12 +872,11 @@ __device__ void ge_solve_block(float * __restrict__ a, int n, int p, float * __r
     __shared__ int bi[16];
     __shared__ int s_mr;
     for (int col = 0; col < n; col++) {
-        // pivot: first row with the largest |a[r][col]|, scanning r = col..n-1
         float best = -1.0f;
         int brow = 0x7fffffff;
-        const float a0 = fabsf(a[(long long)col * w + col]);
+        const float a0 = fabsf(a[(long long)col * n + col]);
         for (int r = col + 1 + threadIdx.x; r < n; r += blockDim.x) {
-            const float v = fabsf(a[(long long)r * w + col]);
+            const float v = fabsf(a[(long long)col * n + r]);
             if (v == v && v > best) { best = v; brow = r; }
         }
         for (int o = 32; o > 0; o >>= 1) {
@@ -537,35 +897,34 @@ __device__ void ge_solve_block(float * __restrict__ a, int n, int p, float * __r
         const int mr = s_mr;
         if (mr != col) {
             for (int j = threadIdx.x; j < w; j += blockDim.x) {
-                const float t0 = a[(long long)col * w + j];
-                a[(long long)col * w + j] = a[(long long)mr * w + j];
-                a[(long long)mr * w + j] = t0;
+                const float t0 = a[(long long)j * n + col];
+                a[(long long)j * n + col] = a[(long long)j * n + mr];
+                a[(long long)j * n + mr] = t0;
             }
         }
         __syncthreads();
-        const float piv = a[(long long)col * w + col];
+        const float piv = a[(long long)col * n + col];
         if (fabsf(piv) < 1e-12f) continue;
-        for (int j = col + threadIdx.x; j < w; j += blockDim.x) prow[j - col] = a[(long long)col * w + j];
-        for (int r = col + 1 + threadIdx.x; r < n; r += blockDim.x) fac[r - col - 1] = a[(long long)r * w + col] / piv;
+        for (int j = col + threadIdx.x; j < w; j += blockDim.x) prow[j - col] = a[(long long)j * n + col];
+        for (int r = col + 1 + threadIdx.x; r < n; r += blockDim.x) fac[r - col - 1] = a[(long long)col * n + r] / piv;
         __syncthreads();
         const int rows = n - col - 1, cols = w - col;
         const long long tot = (long long)rows * cols;
         for (long long e = threadIdx.x; e < tot; e += blockDim.x) {
-            const int rr = (int)(e / cols), jj = (int)(e % cols);
-            float * ap = a + (long long)(col + 1 + rr) * w + col + jj;
+            const int jj = (int)(e / rows), rr = (int)(e % rows);
+            float * ap = a + (long long)(col + jj) * n + col + 1 + rr;
             *ap = *ap - fac[rr] * prow[jj];
         }
         __syncthreads();
     }
     for (int col = n - 1; col >= 0; col--) {
-        const float * arow = a + (long long)col * w;
-        const float piv = arow[col];
+        const float piv = a[(long long)col * n + col];
         if (fabsf(piv) < 1e-12f) {
             for (int j = threadIdx.x; j < p; j += blockDim.x) x[(long long)col * ldx + j] = zero_val;
         } else {
             for (int j = threadIdx.x; j < p; j += blockDim.x) {
-                float v = arow[n + j];
-                for (int r = col + 1; r < n; r++) v -= arow[r] * x[(long long)r * ldx + j];
+                float v = a[(long long)(n + j) * n + col];
+                for (int r = col + 1; r < n; r++) v -= a[(long long)r * n + col] * x[(long long)r * ldx + j];
                 x[(long long)col * ldx + j] = v / piv;
             }
         }
@@ -576,10 +935,11 @@ __device__ void ge_solve_block(float * __restrict__ a, int n, int p, float * __r
 constexpr int GE_LDS_FLOATS = 8192;
 
 __global__ void __launch_bounds__(256)
-k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__ aug,
-           const long long * __restrict__ aug_off, float * __restrict__ Cv, float * __restrict__ gtmp) {
+k_ge_general(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__ aug,
+             const long long * __restrict__ aug_off, float * __restrict__ Cv, float * __restrict__ gtmp) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
+    if (c.tc <= RG_ROWS) return;
     const long long sys = ((long long)layer * g.n_chunks + c_idx) * g.H + h;
     float * Ag = aug + aug_off[sys];
     float * x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
@@ -600,93 +960,73 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__ a
 // ---------------------------------------------------------------------------
 // Quality statistics (api.cpp:239-325).
 // ---------------------------------------------------------------------------
+// in-place row softmax (math.h:83-100), one block per row; the sequential
+// sum runs on lane 0 over LDS-staged blocks of the row
+constexpr int RS_STAGE = 4096;
+
 __global__ void __launch_bounds__(256)
 k_row_softmax(float * __restrict__ x, int n, long long rs, int rows, long long layer_stride) {
     const int row = blockIdx.x, layer = blockIdx.y;
     if (row >= rows) return;
     float * xr = x + layer * layer_stride + row * rs;
     __shared__ float red[16];
-    __shared__ float rinv;
+    __shared__ float stage[RS_STAGE];
+    __shared__ float s_sum;
     const float m = ref_row_max(xr, n, red);
-    for (int j = threadIdx.x; j < n; j += blockDim.x) xr[j] = expf_ref(xr[j] - m);
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float sum = 0.0f;
-        for (int j = 0; j < n; j++) sum += xr[j];
-        rinv = 1.0f / (sum + 1e-12f);
+    float sum = 0.0f;
+    for (int j0 = 0; j0 < n; j0 += RS_STAGE) {
+        const int jn = min(RS_STAGE, n - j0);
+        __syncthreads();
+        for (int j = threadIdx.x; j < jn; j += blockDim.x) {
+            const float e = expf_ref(xr[j0 + j] - m);
+            stage[j] = e;
+            xr[j0 + j] = e;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int j = 0; j < jn; j++) sum += stage[j];
+        }
     }
+    if (threadIdx.x == 0) s_sum = sum;
     __syncthreads();
-    const float iv = rinv;
+    const float iv = 1.0f / (s_sum + 1e-12f);
     for (int j = threadIdx.x; j < n; j += blockDim.x) xr[j] = xr[j] * iv;
 }
 
-// cs[l][h][qi][j] = dot(q, K[sel_j]) * inv + beta[h][j]
-__global__ void __launch_bounds__(256)
-k_stats_comp_scores(Geom g, const ChunkDesc * __restrict__ whole, const float * __restrict__ K,
-                    const float * __restrict__ Q, int qmode, const int * __restrict__ sel,
-                    const float * __restrict__ beta, float * __restrict__ CS, int mh, int mq) {
-    const int layer = blockIdx.z, h = blockIdx.y / mq, qi = blockIdx.y % mq;
-    const long long ek = (long long)g.H * g.dk;
-    const float * q = query_row(g, K, Q, layer, whole[0], qi, qmode) + (long long)h * g.dk;
-    for (int j = blockIdx.x * blockDim.x + threadIdx.x; j < g.t_total; j += gridDim.x * blockDim.x) {
-        const int pos = sel[(long long)layer * g.t_total + j];
-        const float * k = K + layer * g.ldK + (long long)pos * ek + (long long)h * g.dk;
-        float dot = 0.0f;
-        for (int d = 0; d < g.dk; d++) dot += q[d] * k[d];
-        CS[(((long long)layer * mh + h) * mq + qi) * g.t_total + j] =
-            dot * g.inv_sqrt_dk + beta[((long long)layer * g.H + h) * g.t_total + j];
-    }
-}
-
-// out[l][h][qi][d] = sum_j a[l][h][qi][j] * val_j[d], sequential over j.
-// mode 0: val_j = V row j (head h); mode 1: val_j = C_v[h][j]
+// per (h, qi) terms in parallel (each sequential over d), then the
+// reference's accumulation order over (h, qi) on lane 0
 __global__ void __launch_bounds__(128)
-k_stats_weighted_sum(Geom g, const float * __restrict__ a, int n, const float * __restrict__ V,
-                     const float * __restrict__ Cv, int mode, float * __restrict__ out, int mh, int mq) {
-    const int layer = blockIdx.z, h = blockIdx.y / mq, qi = blockIdx.y % mq;
-    const float * ar = a + (((long long)layer * mh + h) * mq + qi) * n;
-    for (int d = blockIdx.x * blockDim.x + threadIdx.x; d < g.dv; d += gridDim.x * blockDim.x) {
-        float acc = 0.0f;
-        if (mode == 0) {
-            const long long ev = (long long)g.H * g.dv;
-            const float * vb = V + layer * g.ldV + (long long)h * g.dv + d;
-            for (int j = 0; j < n; j++) acc += ar[j] * vb[(long long)j * ev];
-        } else {
-            const float * cb = Cv + ((long long)layer * g.H + h) * g.t_total * g.dv + d;
-            for (int j = 0; j < n; j++) acc += ar[j] * cb[(long long)j * g.dv];
-        }
-        out[(((long long)layer * mh + h) * mq + qi) * g.dv + d] = acc;
-    }
-}
-
-__global__ void k_stats_final(Geom g, const float * __restrict__ oo, const float * __restrict__ co,
-                              int mh, int mq, float * __restrict__ stats) {
+k_stats_final(Geom g, const float * __restrict__ oo, const float * __restrict__ co,
+              int mh, int mq, float * __restrict__ stats) {
     const int layer = blockIdx.x;
-    if (threadIdx.x != 0) return;
-    float sum_cos = 0.0f, sum_mse = 0.0f;
-    int agree = 0, total = 0;
-    for (int h = 0; h < mh; h++) {
-        for (int qi = 0; qi < mq; qi++) {
-            const float * o = oo + (((long long)layer * mh + h) * mq + qi) * g.dv;
-            const float * c = co + (((long long)layer * mh + h) * mq + qi) * g.dv;
-            float dp = 0.0f, no = 0.0f, nc = 0.0f;
-            for (int d = 0; d < g.dv; d++) { dp += o[d] * c[d]; no += o[d] * o[d]; nc += c[d] * c[d]; }
-            sum_cos += dp / (sqrtf(no * nc) + 1e-8f);
-            float mse = 0.0f;
-            for (int d = 0; d < g.dv; d++) { const float df = o[d] - c[d]; mse += df * df; }
-            sum_mse += mse / (float)g.dv;
-            int ao = 0, ac = 0;
-            for (int d = 1; d < g.dv; d++) {
-                if (o[d] > o[ao]) ao = d;
-                if (c[d] > c[ac]) ac = d;
-            }
-            if (ao == ac) agree++;
-            total++;
+    __shared__ float t_cos[128], t_mse[128];
+    __shared__ int t_agree[128];
+    const int nt = mh * mq;
+    for (int i = threadIdx.x; i < nt; i += blockDim.x) {
+        const float * o = oo + ((long long)layer * nt + i) * g.dv;
+        const float * c = co + ((long long)layer * nt + i) * g.dv;
+        float dp = 0.0f, no = 0.0f, nc = 0.0f;
+        for (int d = 0; d < g.dv; d++) { dp += o[d] * c[d]; no += o[d] * o[d]; nc += c[d] * c[d]; }
+        t_cos[i] = dp / (sqrtf(no * nc) + 1e-8f);
+        float mse = 0.0f;
+        for (int d = 0; d < g.dv; d++) { const float df = o[d] - c[d]; mse += df * df; }
+        t_mse[i] = mse / (float)g.dv;
+        int ao = 0, ac = 0;
+        for (int d = 1; d < g.dv; d++) {
+            if (o[d] > o[ao]) ao = d;
+            if (c[d] > c[ac]) ac = d;
         }
+        t_agree[i] = (ao == ac) ? 1 : 0;
     }
-    stats[layer * 3 + 0] = sum_cos / (float)total;
-    stats[layer * 3 + 1] = sum_mse / (float)total;
-    stats[layer * 3 + 2] = (float)agree / (float)total;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum_cos = 0.0f, sum_mse = 0.0f;
+        int agree = 0;
+        for (int i = 0; i < nt; i++) { sum_cos += t_cos[i]; sum_mse += t_mse[i]; agree += t_agree[i]; }
+        stats[layer * 3 + 0] = sum_cos / (float)nt;
+        stats[layer * 3 + 1] = sum_mse / (float)nt;
+        stats[layer * 3 + 2] = (float)agree / (float)nt;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -898,10 +1238,11 @@ hipError_t set_exp2_table(const uint64_t * tab32) {
 
 void launch_scores(const Geom & g, const ChunkDesc * chunks, int n_chunk_units, int Tc_max,
                    const float * K, const float * Q, float * S, int Hs, int nq_cap,
-                   long long s_layer, long long s_head, long long s_row, int qmode, hipStream_t st) {
+                   long long s_layer, long long s_head, long long s_row, int qmode, hipStream_t st,
+                   const int * key_idx, const float * beta) {
     dim3 grid(cdiv(Tc_max, SC_KEYS), n_chunk_units * Hs, g.L);
     hipLaunchKernelGGL(k_scores, grid, dim3(256), 0, st, g, chunks, K, Q, S, Hs, nq_cap,
-                       s_layer, s_head, s_row, qmode);
+                       s_layer, s_head, s_row, qmode, key_idx, beta);
 }
 
 void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st) {
@@ -929,35 +1270,46 @@ void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipSt
 }
 
 void launch_ls_build(const Geom & g, const Work & w, hipStream_t st) {
-    const long long per = (long long)g.tc_max * (g.tc_max + g.dv);
-    const unsigned bx = (unsigned)std::min<long long>(64, (per + 255) / 256);
-    hipLaunchKernelGGL(k_ls_build, dim3(bx, g.n_chunks * g.H, g.L), dim3(256), 0, st,
-                       g, w.chunks, w.X, w.Y, w.aug, w.aug_off);
+    const long long need = (long long)g.nq_max * (g.tc_max + g.dv);
+    const int lds_floats = need <= LB_LDS_FLOATS ? (int)need : 0;
+    hipLaunchKernelGGL(k_ls_build, dim3(g.n_chunks * g.H, g.L), dim3(256), (size_t)lds_floats * sizeof(float), st,
+                       g, w.chunks, w.X, w.Y, w.aug, w.aug_off, lds_floats);
 }
 
 void launch_ge(const Geom & g, const Work & w, float * Cv, hipStream_t st) {
-    hipLaunchKernelGGL(k_ge_solve, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
-                       g, w.chunks, w.aug, w.aug_off, Cv, w.gtmp);
+    const unsigned systems = (unsigned)(g.L * g.n_chunks * g.H);
+    hipLaunchKernelGGL(k_ge_elim, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
+                       g, w.chunks, w.aug, w.aug_off, w.perm, w.Ut, w.Bt);
+    hipLaunchKernelGGL(k_ge_backsub, dim3(systems, cdiv(g.dv, 64)), dim3(64), 0, st,
+                       g, w.chunks, w.Ut, w.Bt, Cv);
+    if (g.tc_max > RG_ROWS)
+        hipLaunchKernelGGL(k_ge_general, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
+                           g, w.chunks, w.aug, w.aug_off, Cv, w.gtmp);
 }
 
 void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const float * K,
                   const float * V, const float * Q, const float * beta, const float * Cv,
                   float * stats, hipStream_t st) {
-    const ChunkDesc * whole = w.chunks + g.n_chunks;
+    const ChunkDesc * whole = w.chunks + g.n_chunks;      // all T keys
+    const ChunkDesc * kept = w.chunks + g.n_chunks + 1;   // the t_total kept keys
     const long long osl = (long long)sw.mh * sw.mq * g.T;
-    launch_scores(g, whole, 1, g.T, K, Q, sw.OS, sw.mh, sw.mq, osl, (long long)sw.mq * g.T, g.T, sw.qmode, st);
+    const long long csl = (long long)sw.mh * sw.mq * g.t_total;
+    const int nvb = (g.dv + ST_VB - 1) / ST_VB;
+    // original attention of the sampled queries over all T
+    launch_scores(g, whole, 1, g.T, K, Q, sw.OS, sw.mh, sw.mq, osl, (long long)sw.mq * g.T, g.T, sw.qmode, st,
+                  nullptr, nullptr);
     hipLaunchKernelGGL(k_row_softmax, dim3(sw.mh * sw.mq, g.L), dim3(256), 0, st,
                        sw.OS, g.T, (long long)g.T, sw.mh * sw.mq, osl);
-    hipLaunchKernelGGL(k_stats_weighted_sum, dim3(cdiv(g.dv, 128), sw.mh * sw.mq, g.L), dim3(128), 0, st,
-                       g, sw.OS, g.T, V, Cv, 0, sw.OO, sw.mh, sw.mq);
-    hipLaunchKernelGGL(k_stats_comp_scores, dim3(cdiv(g.t_total, 256), sw.mh * sw.mq, g.L), dim3(256), 0, st,
-                       g, whole, K, Q, sw.qmode, w.sel, beta, sw.CS, sw.mh, sw.mq);
-    const long long csl = (long long)sw.mh * sw.mq * g.t_total;
+    hipLaunchKernelGGL(k_stats_sum, dim3(sw.mh * nvb, g.L), dim3(256), 0, st,
+                       g, sw.OS, g.T, V, Cv, 1, sw.OO, sw.mh, sw.mq);
+    // compacted attention over the kept keys with beta and C_v
+    launch_scores(g, kept, 1, g.t_total, K, Q, sw.CS, sw.mh, sw.mq, csl, (long long)sw.mq * g.t_total, g.t_total,
+                  sw.qmode, st, w.sel, beta);
     hipLaunchKernelGGL(k_row_softmax, dim3(sw.mh * sw.mq, g.L), dim3(256), 0, st,
                        sw.CS, g.t_total, (long long)g.t_total, sw.mh * sw.mq, csl);
-    hipLaunchKernelGGL(k_stats_weighted_sum, dim3(cdiv(g.dv, 128), sw.mh * sw.mq, g.L), dim3(128), 0, st,
-                       g, sw.CS, g.t_total, V, Cv, 1, sw.CO, sw.mh, sw.mq);
-    hipLaunchKernelGGL(k_stats_final, dim3(g.L), dim3(64), 0, st, g, sw.OO, sw.CO, sw.mh, sw.mq, stats);
+    hipLaunchKernelGGL(k_stats_sum, dim3(sw.mh * nvb, g.L), dim3(256), 0, st,
+                       g, sw.CS, g.t_total, V, Cv, 2, sw.CO, sw.mh, sw.mq);
+    hipLaunchKernelGGL(k_stats_final, dim3(g.L), dim3(128), 0, st, g, sw.OO, sw.CO, sw.mh, sw.mq, stats);
 }
 
 void launch_dequant_rows(const uint8_t * src, int type, long long row_bytes, int n_el, long long rows,
