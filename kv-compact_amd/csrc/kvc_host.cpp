@@ -295,7 +295,9 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, bool need_e, Carver 
     ww.aug_off = cv.take<long long>(L * nc * H);
     ww.perm = cv.take<int>(L * nc * H * (size_t)pl.tc_max);
     const size_t ut_rows = pl.tc_max <= 256 ? 256 : 0;
+    ww.skip = cv.take<unsigned char>(L * nc * H * (size_t)pl.tc_max);
     ww.Ut = cv.take<float>(L * nc * H * ut_rows * ut_rows);
+    ww.Lp = cv.take<float>(L * nc * H * ut_rows * ut_rows);
     ww.Bt = cv.take<float>(L * nc * H * ut_rows * dv);
     ww.gtmp = cv.take<float>(L * nc * H * (2 * (size_t)pl.tc_max + dv));
     ww.cand = cv.take<int>(L * nc * (size_t)pl.Tc_max);

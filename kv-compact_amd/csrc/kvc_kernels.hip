@@ -585,21 +585,19 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 // (n x (n + p)), math.h:494-556. Storage is column-major: entry (r, j) at
 // a[j * n + r] (M is symmetric, B is stored transposed).
 //
-// k_ge_elim (n <= 256), phase 1: the n x n matrix lives in registers; 16
-// waves own 16-column strips, lane l owns rows l, l+64, l+128, l+192. Row
-// swaps become a logical->physical permutation. An LDS copy (panel) of the
-// strip holding the current column serves the pivot search; the multiplier
-// of each remaining row replaces that row's entry in the current column of
-// the panel (the reference never reads it again), so a retired panel is the
-// final column of the factorisation: U entries in rows already used as
-// pivots, multipliers in the others. Entries left of the current column of
-// the remaining rows are updated too and never read.
-// Phase 2 replays the same multiply-subtract sequence on the right-hand
-// sides, one 16-column strip per wave, pivot-row values read from the owning
-// lane, so B ends as the reference's eliminated right-hand side.
-// k_ge_backsub: back substitution in the reference's order, one thread per
-// right-hand side. k_ge_general: the same arithmetic for n > 256 in global
-// memory.
+// k_ge_lu (n <= 256): blocked LU of the n x n matrix with the reference's
+// partial pivoting, in registers. 16 waves own 16-column strips; lane l owns
+// rows l, l+64, l+128, l+192 (physical rows; swaps are a logical<->physical
+// permutation). Panel k (strip k) is factored by wave k alone, in its own
+// registers: pivot search, multipliers, update of the panel's remaining
+// columns, step by step. After one barrier every later wave applies the
+// panel's 16 steps, in order, to its own strip. Each element therefore
+// receives exactly the reference's sequence of a -= f * u operations.
+// Outputs per system: U rows by logical row (Ut), multipliers by physical row
+// and step (Lp), the final permutation and the skipped-pivot flags.
+// The right-hand sides are not touched here: the reference's elimination of
+// them is forward substitution with the final permutation (ascending steps),
+// done with the back substitution in k_ge_solve.
 // ---------------------------------------------------------------------------
 constexpr int RG_ROWS = 256, RG_STRIP = 16, RG_WAVES = 16, RG_SLOTS = 4;
 constexpr int RG_THREADS = RG_WAVES * 64;
@@ -619,33 +617,97 @@ __device__ __forceinline__ void rg_pivot_values(const float (&a)[RG_SLOTS][RG_ST
     else rg_lane_strip<3>(a, src, sp);
 }
 
+struct LuShared {
+    float panel[RG_ROWS][RG_STRIP + 1];  // the panel being factored (one wave)
+    float fmul[2][RG_STRIP][RG_ROWS];     // multipliers of the last two panels
+    int perm[RG_ROWS], inv[RG_ROWS], pivrow[RG_ROWS];
+    unsigned char skip[RG_ROWS];
+};
+
+// Factor panel columns [c0, c0 + 16) held in sh.panel, one wave, step by
+// step in the reference's order; writes U row entries of the panel columns,
+// the multipliers (sh.fmul[buf]) and the pivot bookkeeping.
+__device__ void lu_factor_panel(LuShared & sh, bool (&live)[RG_SLOTS], int c0, int n, int lane, int buf,
+                                float * __restrict__ Ut) {
+    for (int jj = 0; jj < RG_STRIP; jj++) {
+        const int col = c0 + jj;
+        if (col >= n) break;
+        float bv = -1.0f;
+        int bl = 0x7fffffff;
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            const int r = lane + 64 * s;
+            if (live[s]) {
+                const float v = fabsf(sh.panel[r][jj]);
+                const int li = sh.inv[r];
+                if (v == v && (v > bv || (v == bv && li < bl))) { bv = v; bl = li; }
+            }
+        }
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o);
+            const int ol = __shfl_xor(bl, o);
+            if (ov > bv || (ov == bv && ol < bl)) { bv = ov; bl = ol; }
+        }
+        const int Pc = sh.perm[col];
+        const float a0 = fabsf(sh.panel[Pc][jj]);
+        const int mr = (a0 == a0 && bv > a0) ? bl : col;
+        const int P = sh.perm[mr];
+        const float piv = sh.panel[P][jj];
+        const bool elim = !(fabsf(piv) < 1e-12f);
+        float f[RG_SLOTS];
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            const int r = lane + 64 * s;
+            f[s] = (elim && live[s] && r != P) ? sh.panel[r][jj] / piv : 0.0f;
+        }
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) {
+            sh.perm[col] = P;
+            sh.perm[mr] = Pc;
+            sh.inv[P] = col;
+            sh.inv[Pc] = mr;
+            sh.pivrow[col] = P;
+            sh.skip[col] = elim ? 0 : 1;
+        }
+        // U row col over the panel's columns
+        for (int q = jj + lane; q < RG_STRIP; q += 64)
+            if (c0 + q < n) Ut[(long long)col * RG_ROWS + c0 + q] = sh.panel[P][q];
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            const int r = lane + 64 * s;
+            sh.fmul[buf][jj][r] = f[s];
+            if (elim && live[s] && r != P) {
+#pragma unroll
+                for (int q = 0; q < RG_STRIP; q++)
+                    if (q > jj) sh.panel[r][q] = sh.panel[r][q] - f[s] * sh.panel[P][q];
+            }
+            live[s] = live[s] && (r != P);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
 __global__ void __launch_bounds__(RG_THREADS)
-k_ge_elim(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__ aug,
-          const long long * __restrict__ aug_off, int * __restrict__ perm_out,
-          float * __restrict__ Ut_all, float * __restrict__ Bt_all) {
+k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
+        const long long * __restrict__ aug_off, int * __restrict__ perm_out, unsigned char * __restrict__ skip_out,
+        float * __restrict__ Ut_all, float * __restrict__ Lp_all) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const int n = c.tc;
     if (n > RG_ROWS) return;
     const long long sys = ((long long)layer * g.n_chunks + c_idx) * g.H + h;
-    float * A = aug + aug_off[sys];
-    int * perm_g = perm_out + sys * (long long)g.tc_max;
-    // U rows (row-major by logical row, n x n) and eliminated right-hand
-    // sides (row-major by logical row, n x dv) for the back substitution
+    const float * A = aug + aug_off[sys];
     float * Ut = Ut_all + sys * (long long)RG_ROWS * RG_ROWS;
-    float * Bt = Bt_all + sys * (long long)RG_ROWS * g.dv;
+    float * Lp = Lp_all + sys * (long long)RG_ROWS * RG_ROWS;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    __shared__ float panel[RG_ROWS][RG_STRIP + 1];
-    __shared__ float fac[RG_ROWS];
-    __shared__ int perm[RG_ROWS], inv[RG_ROWS], dstep[RG_ROWS], pivrow[RG_ROWS];
-    __shared__ unsigned char skip[RG_ROWS];
-    __shared__ float redv[4];
-    __shared__ int redi[4];
+    __shared__ LuShared sh;
 
     float a[RG_SLOTS][RG_STRIP];
+    bool live[RG_SLOTS];
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) {
         const int r = lane + 64 * s;
+        live[s] = r < n;
 #pragma unroll
         for (int jj = 0; jj < RG_STRIP; jj++) {
             const int j = RG_STRIP * w + jj;
@@ -653,169 +715,107 @@ k_ge_elim(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__ au
         }
     }
     if (tid < RG_ROWS) {
-        perm[tid] = tid;
-        inv[tid] = tid;
-        dstep[tid] = (tid < n) ? RG_ROWS : -1;   // -1: padding row, never a pivot
+        sh.perm[tid] = tid;
+        sh.inv[tid] = tid;
     }
     __syncthreads();
-    for (int col = 0; col < n; col++) {
-        const int k = col & (RG_STRIP - 1);
-        if (k == 0) {
-            if (w == col / RG_STRIP) {
+    const int n_panels = (n + RG_STRIP - 1) / RG_STRIP;
+    for (int k = 0; k < n_panels; k++) {
+        const int c0 = k * RG_STRIP, buf = k & 1;
+        if (w == k) {
 #pragma unroll
-                for (int s = 0; s < RG_SLOTS; s++)
+            for (int s2 = 0; s2 < RG_SLOTS; s2++)
 #pragma unroll
-                    for (int kk = 0; kk < RG_STRIP; kk++) panel[lane + 64 * s][kk] = a[s][kk];
-            }
-            __syncthreads();
-        }
-        // pivot: largest |value| in column col over rows not yet used,
-        // smallest logical index on ties (the reference's first maximum)
-        float bv = -1.0f;
-        int bl = 0x7fffffff;
-        if (tid < RG_ROWS) {
-            if (dstep[tid] == RG_ROWS) {
-                const float v = fabsf(panel[tid][k]);
-                if (v == v) { bv = v; bl = inv[tid]; }
-            }
-            for (int o = 32; o > 0; o >>= 1) {
-                const float ov = __shfl_xor(bv, o);
-                const int ol = __shfl_xor(bl, o);
-                if (ov > bv || (ov == bv && ol < bl)) { bv = ov; bl = ol; }
-            }
-            if (lane == 0) { redv[w] = bv; redi[w] = bl; }
-        }
-        __syncthreads();
-        float b = redv[0];
-        int bli = redi[0];
+                for (int q = 0; q < RG_STRIP; q++) sh.panel[lane + 64 * s2][q] = a[s2][q];
+            __builtin_amdgcn_wave_barrier();
+            lu_factor_panel(sh, live, c0, n, lane, buf, Ut);
+            // multipliers of this panel by physical row: Lp[r][c0 .. c0+15]
 #pragma unroll
-        for (int i = 1; i < 4; i++)
-            if (redv[i] > b || (redv[i] == b && redi[i] < bli)) { b = redv[i]; bli = redi[i]; }
-        const int Pc = perm[col];
-        const float a0 = fabsf(panel[Pc][k]);
-        const int mr = (a0 == a0 && b > a0) ? bli : col;
-        const int P = perm[mr];
-        const float piv = panel[P][k];
-        const bool elim = !(fabsf(piv) < 1e-12f);
-        // multipliers of the rows still unused (not P); they enter the panel
-        // column only after the barrier, once every wave has read its pivot
-        if (tid < RG_ROWS) {
-            float f = 0.0f;
-            if (elim && tid != P && dstep[tid] == RG_ROWS) f = panel[tid][k] / piv;
-            fac[tid] = f;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            perm[col] = P;
-            perm[mr] = Pc;
-            inv[P] = col;
-            inv[Pc] = mr;
-            dstep[P] = col;
-            pivrow[col] = P;
-            skip[col] = elim ? 0 : 1;
-        }
-        // the pivot row is final from here on: it becomes U row col (the
-        // diagonal here, the columns right of it from each live strip below)
-        if (tid == 0) Ut[(long long)col * RG_ROWS + col] = piv;
-        if (elim) {
-            if (RG_STRIP * w + RG_STRIP - 1 > col) {
-                float sp[RG_STRIP];
-                rg_pivot_values(a, P, sp);
-                if (lane == 0) {
+            for (int s = 0; s < RG_SLOTS; s++) {
+                const int r = lane + 64 * s;
+                if (r < n) {
 #pragma unroll
-                    for (int jj = 0; jj < RG_STRIP; jj++) {
-                        const int j = RG_STRIP * w + jj;
-                        if (j > col && j < n) Ut[(long long)col * RG_ROWS + j] = sp[jj];
-                    }
-                }
-#pragma unroll
-                for (int s = 0; s < RG_SLOTS; s++) {
-                    const int r = lane + 64 * s;
-                    if (r != P && dstep[r] == RG_ROWS) {
-                        const float f = fac[r];
-#pragma unroll
-                        for (int jj = 0; jj < RG_STRIP; jj++) a[s][jj] = a[s][jj] - f * sp[jj];
-                    }
-                }
-            }
-            for (int e = tid; e < RG_ROWS * RG_STRIP; e += RG_THREADS) {
-                const int r = e >> 4, kk = e & (RG_STRIP - 1);
-                if (kk >= k && r != P && dstep[r] == RG_ROWS) {
-                    if (kk == k) panel[r][kk] = fac[r];
-                    else panel[r][kk] = panel[r][kk] - fac[r] * panel[P][kk];
+                    for (int jj = 0; jj < RG_STRIP; jj++)
+                        if (c0 + jj < n) Lp[(long long)r * RG_ROWS + c0 + jj] = sh.fmul[buf][jj][r];
                 }
             }
         }
         __syncthreads();
-        if (k == RG_STRIP - 1 || col == n - 1) {
-            // retire the panel: final factorisation columns [col - k, col]
-            const int c0 = col - k;
-            for (int e = tid; e < RG_ROWS * RG_STRIP; e += RG_THREADS) {
-                const int kk = e >> 8, r = e & (RG_ROWS - 1);
-                if (r < n && c0 + kk < n) A[(long long)(c0 + kk) * n + r] = panel[r][kk];
-            }
-            __syncthreads();
-        }
-    }
-    if (tid < n) perm_g[tid] = pivrow[tid];
-    __syncthreads();
-
-    // phase 2: right-hand sides, 16 columns per wave per pass
-    const int p_total = g.dv;
-    for (int v0 = 0; v0 < p_total; v0 += RG_WAVES * RG_STRIP) {
-        float bb[RG_SLOTS][RG_STRIP];
-#pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++) {
-            const int r = lane + 64 * s;
-#pragma unroll
+        if (w > k && RG_STRIP * w < n) {
+            // apply the panel's steps, in order, to this strip
             for (int jj = 0; jj < RG_STRIP; jj++) {
-                const int v = v0 + RG_STRIP * w + jj;
-                bb[s][jj] = (r < n && v < p_total) ? A[(long long)(n + v) * n + r] : 0.0f;
-            }
-        }
-        if (v0 + RG_STRIP * w < p_total) {
-            for (int col = 0; col < n; col++) {
-                if (skip[col]) continue;
-                const int P = pivrow[col];
-                float sp[RG_STRIP];
-                rg_pivot_values(bb, P, sp);
+                const int col = c0 + jj;
+                if (col >= n) break;
+                const int P = sh.pivrow[col];
+                if (!sh.skip[col]) {
+                    // U row col over this strip, stored by the pivot row's owner lane
+                    // (entries past column n of a row are never read)
+                    if (lane == (P & 63)) {
+                        const int slot = P >> 6;
+                        float4 * dst = reinterpret_cast<float4 *>(Ut + (long long)col * RG_ROWS + RG_STRIP * w);
 #pragma unroll
-                for (int s = 0; s < RG_SLOTS; s++) {
-                    const int r = lane + 64 * s;
-                    if (dstep[r] > col) {
-                        const float f = A[(long long)col * n + r];
+                        for (int s2 = 0; s2 < RG_SLOTS; s2++) {
+                            if (slot == s2) {
 #pragma unroll
-                        for (int jj = 0; jj < RG_STRIP; jj++) bb[s][jj] = bb[s][jj] - f * sp[jj];
+                                for (int q4 = 0; q4 < RG_STRIP / 4; q4++)
+                                    dst[q4] = make_float4(a[s2][4 * q4], a[s2][4 * q4 + 1], a[s2][4 * q4 + 2], a[s2][4 * q4 + 3]);
+                            }
+                        }
+                    }
+                    float sp[RG_STRIP];
+                    rg_pivot_values(a, P, sp);
+#pragma unroll
+                    for (int s = 0; s < RG_SLOTS; s++) {
+                        const int r = lane + 64 * s;
+                        if (live[s] && r != P) {
+                            const float f = sh.fmul[buf][jj][r];
+#pragma unroll
+                            for (int q = 0; q < RG_STRIP; q++) a[s][q] = a[s][q] - f * sp[q];
+                        }
                     }
                 }
+#pragma unroll
+                for (int s = 0; s < RG_SLOTS; s++) live[s] = live[s] && (lane + 64 * s != P);
+            }
+        } else if (w > k) {
+            // padding strip: keep the live flags in step
+            for (int jj = 0; jj < RG_STRIP; jj++) {
+                const int col = c0 + jj;
+                if (col >= n) break;
+                const int P = sh.pivrow[col];
+#pragma unroll
+                for (int s = 0; s < RG_SLOTS; s++) live[s] = live[s] && (lane + 64 * s != P);
             }
         }
-#pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++) {
-            const int r = lane + 64 * s;
-            if (r < n) {
-                const int lr = inv[r];
-#pragma unroll
-                for (int jj = 0; jj < RG_STRIP; jj++) {
-                    const int v = v0 + RG_STRIP * w + jj;
-                    if (v < p_total) Bt[(long long)lr * g.dv + v] = bb[s][jj];
-                }
-            }
-        }
+    }
+    __syncthreads();
+    if (tid < n) {
+        perm_out[sys * (long long)g.tc_max + tid] = sh.pivrow[tid];
+        skip_out[sys * (long long)g.tc_max + tid] = sh.skip[tid];
     }
 }
 
-// Back substitution (math.h:540-556) for n <= 256: one wave per 64 right-hand
-// sides, lane v runs x[col][v] = (b[col][v] - sum_{r>col} U[col][r] x[r][v]) / U[col][col]
-// with the sum in ascending r. Rows [hb, n) (the first solved, hb = n - 128
-// when n > 128) move from LDS into registers once solved; the remaining rows
-// then read them through a statically unrolled loop, their own earlier
-// results from LDS. U rows are uniform across the wave.
+// Forward substitution y = L^-1 P b (the reference's elimination of the
+// right-hand sides: row i receives the updates of steps 0..i-1 in order,
+// skipped pivots contribute nothing), then back substitution (math.h:540-556)
+// x[i] = (y[i] - sum_{r>i} U[i][r] x[r]) / U[i][i] with r ascending. One wave
+// per 64 right-hand sides, lane v owns column v. The first 128 solved rows
+// of each sweep move from LDS into registers and are then read through a
+// statically unrolled loop; the other rows' earlier results come from LDS.
 constexpr int BS_HIGH = 128;
 
+// stage one 256-float row (uniform across the wave) into LDS
+__device__ __forceinline__ void stage_row(const float * __restrict__ src, float * dst, int lane) {
+    const float4 v4 = reinterpret_cast<const float4 *>(src)[lane];
+    reinterpret_cast<float4 *>(dst)[lane] = v4;
+    __builtin_amdgcn_wave_barrier();
+}
+
 __global__ void __launch_bounds__(64)
-k_ge_backsub(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ Ut_all,
-             const float * __restrict__ Bt_all, float * __restrict__ Cv) {
+k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
+           const long long * __restrict__ aug_off, const int * __restrict__ perm_in,
+           const unsigned char * __restrict__ skip_in, const float * __restrict__ Ut_all,
+           const float * __restrict__ Lp_all, float * __restrict__ Yt_all, float * __restrict__ Cv) {
     const int sysl = blockIdx.x;   // (layer, chunk, head)
     const int h = sysl % g.H, c_idx = (sysl / g.H) % g.n_chunks, layer = sysl / (g.H * g.n_chunks);
     const ChunkDesc c = chunks[c_idx];
@@ -825,42 +825,98 @@ k_ge_backsub(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
     const int v = blockIdx.y * 64 + lane;
     const bool act = v < p;
     const float * __restrict__ Ut = Ut_all + (long long)sysl * RG_ROWS * RG_ROWS;
-    const float * __restrict__ Bt = Bt_all + (long long)sysl * RG_ROWS * g.dv;
+    const float * __restrict__ Lp = Lp_all + (long long)sysl * RG_ROWS * RG_ROWS;
+    const float * __restrict__ B = aug + aug_off[sysl] + (long long)n * n;   // column-major RHS [v][r]
+    float * Yt = Yt_all + (long long)sysl * RG_ROWS * g.dv;
+    const int * perm = perm_in + (long long)sysl * g.tc_max;
     float * x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
     __shared__ float xs[BS_HIGH][64];
+    __shared__ __align__(16) float row[RG_ROWS];
+    __shared__ float skf[RG_ROWS];   // 1 where the step eliminated, 0 where it was skipped
+    __shared__ int any_skip;
+    if (lane == 0) any_skip = 0;
+    __builtin_amdgcn_wave_barrier();
+    for (int i = lane; i < RG_ROWS; i += 64) {
+        const int sk = (i < n) ? skip_in[(long long)sysl * g.tc_max + i] : 0;
+        skf[i] = sk ? 0.0f : 1.0f;
+        if (sk) any_skip = 1;
+    }
+    __builtin_amdgcn_wave_barrier();
+    const bool sk = any_skip != 0;
+
+    // ---- forward: rows [0, lb) from LDS, then rows [lb, n) with [0, lb) in registers
+    const int lb = n < BS_HIGH ? n : BS_HIGH;
+    for (int i = 0; i < lb; i++) {
+        const int r0 = perm[i];
+        stage_row(Lp + (long long)r0 * RG_ROWS, row, lane);
+        float val = act ? B[(long long)v * n + r0] : 0.0f;
+#pragma unroll 8
+        for (int j = 0; j < i; j++)
+            if (!sk || skf[j] != 0.0f) val -= row[j] * xs[j][lane];
+        xs[i][lane] = val;
+        if (act) Yt[(long long)i * g.dv + v] = val;
+        __builtin_amdgcn_wave_barrier();
+    }
+    if (n > BS_HIGH) {
+        float yr[BS_HIGH];
+#pragma unroll
+        for (int j = 0; j < BS_HIGH; j++) yr[j] = xs[j][lane];
+        for (int i = BS_HIGH; i < n; i++) {
+            const int r0 = perm[i];
+            stage_row(Lp + (long long)r0 * RG_ROWS, row, lane);
+            float val = act ? B[(long long)v * n + r0] : 0.0f;
+            if (!sk) {
+#pragma unroll
+                for (int j = 0; j < BS_HIGH; j++) val -= row[j] * yr[j];
+            } else {
+#pragma unroll
+                for (int j = 0; j < BS_HIGH; j++)
+                    if (skf[j] != 0.0f) val -= row[j] * yr[j];
+            }
+#pragma unroll 8
+            for (int j = BS_HIGH; j < i; j++)
+                if (!sk || skf[j] != 0.0f) val -= row[j] * xs[j - BS_HIGH][lane];
+            xs[i - BS_HIGH][lane] = val;
+            if (act) Yt[(long long)i * g.dv + v] = val;
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+
+    // ---- backward: rows [hb, n) from LDS, then rows [0, hb) with [hb, n) in registers
     const int hb = n > BS_HIGH ? n - BS_HIGH : 0;
-    // rows [hb, n): all terms among themselves, x in LDS
     for (int col = n - 1; col >= hb; col--) {
-        const float * u = Ut + (long long)col * RG_ROWS;
-        const float piv = u[col];
+        stage_row(Ut + (long long)col * RG_ROWS, row, lane);
+        const float piv = row[col];
         float val = 0.0f;
         if (!(fabsf(piv) < 1e-12f)) {
-            val = act ? Bt[(long long)col * g.dv + v] : 0.0f;
-            for (int r = col + 1; r < n; r++) val -= u[r] * xs[r - hb][lane];
+            val = act ? Yt[(long long)col * g.dv + v] : 0.0f;
+#pragma unroll 8
+            for (int r = col + 1; r < n; r++) val -= row[r] * xs[r - hb][lane];
             val = val / piv;
         }
         xs[col - hb][lane] = val;
         if (act) x[(long long)col * g.dv + v] = val;
+        __builtin_amdgcn_wave_barrier();
     }
     if (hb == 0) return;
     float xh[BS_HIGH];
 #pragma unroll
     for (int i = 0; i < BS_HIGH; i++) xh[i] = xs[i][lane];
-    // rows [0, hb): earlier low rows from LDS, then the high rows from registers
     for (int col = hb - 1; col >= 0; col--) {
-        const float * u = Ut + (long long)col * RG_ROWS;
-        const float piv = u[col];
+        stage_row(Ut + (long long)col * RG_ROWS, row, lane);
+        const float piv = row[col];
         float val = 0.0f;
         if (!(fabsf(piv) < 1e-12f)) {
-            val = act ? Bt[(long long)col * g.dv + v] : 0.0f;
-            for (int r = col + 1; r < hb; r++) val -= u[r] * xs[r][lane];
-            const float * uh = u + hb;
+            val = act ? Yt[(long long)col * g.dv + v] : 0.0f;
+#pragma unroll 8
+            for (int r = col + 1; r < hb; r++) val -= row[r] * xs[r][lane];
 #pragma unroll
-            for (int i = 0; i < BS_HIGH; i++) val -= uh[i] * xh[i];
+            for (int i = 0; i < BS_HIGH; i++) val -= row[hb + i] * xh[i];
             val = val / piv;
         }
         xs[col][lane] = val;
         if (act) x[(long long)col * g.dv + v] = val;
+        __builtin_amdgcn_wave_barrier();
     }
 }
 
@@ -1278,10 +1334,10 @@ void launch_ls_build(const Geom & g, const Work & w, hipStream_t st) {
 
 void launch_ge(const Geom & g, const Work & w, float * Cv, hipStream_t st) {
     const unsigned systems = (unsigned)(g.L * g.n_chunks * g.H);
-    hipLaunchKernelGGL(k_ge_elim, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
-                       g, w.chunks, w.aug, w.aug_off, w.perm, w.Ut, w.Bt);
-    hipLaunchKernelGGL(k_ge_backsub, dim3(systems, cdiv(g.dv, 64)), dim3(64), 0, st,
-                       g, w.chunks, w.Ut, w.Bt, Cv);
+    hipLaunchKernelGGL(k_ge_lu, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
+                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.Ut, w.Lp);
+    hipLaunchKernelGGL(k_ge_solve, dim3(systems, cdiv(g.dv, 64)), dim3(64), 0, st,
+                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.Ut, w.Lp, w.Bt, Cv);
     if (g.tc_max > RG_ROWS)
         hipLaunchKernelGGL(k_ge_general, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
                            g, w.chunks, w.aug, w.aug_off, Cv, w.gtmp);
