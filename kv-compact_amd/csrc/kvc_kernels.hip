@@ -589,9 +589,11 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 // partial pivoting, in registers. 16 waves own 16-column strips; lane l owns
 // rows l, l+64, l+128, l+192 (physical rows; swaps are a logical<->physical
 // permutation). Panel k (strip k) is factored by wave k alone, in its own
-// registers: pivot search, multipliers, update of the panel's remaining
-// columns, step by step. After one barrier every later wave applies the
-// panel's 16 steps, in order, to its own strip. Each element therefore
+// registers: pivot search (DPP reductions), multipliers, update of the
+// panel's remaining columns, step by step. Every later wave applies the
+// panel's 16 steps, in order, to its own strip one phase later, so that the
+// factorization of panel k+1 (which first applies panel k to itself) runs
+// beside the other strips' update with panel k. Each element therefore
 // receives exactly the reference's sequence of a -= f * u operations.
 // Outputs per system: U rows by logical row (Ut), multipliers by physical row
 // and step (Lp), the final permutation and the skipped-pivot flags.
@@ -617,73 +619,169 @@ __device__ __forceinline__ void rg_pivot_values(const float (&a)[RG_SLOTS][RG_ST
     else rg_lane_strip<3>(a, src, sp);
 }
 
+// Wave-wide max / min of a 32-bit unsigned value through DPP row shifts and
+// row broadcasts (the result collects in lane 63); both operations are
+// idempotent, so lanes whose DPP source is out of range keep their own value.
+template <bool MAX>
+__device__ __forceinline__ unsigned dpp_reduce_u32(unsigned x) {
+#define KVC_DPP_STEP(ctrl, rmask)                                                                  \
+    {                                                                                              \
+        const unsigned t = (unsigned)__builtin_amdgcn_update_dpp((int)x, (int)x, ctrl, rmask, 0xf, false); \
+        x = MAX ? (t > x ? t : x) : (t < x ? t : x);                                               \
+    }
+    KVC_DPP_STEP(0x111, 0xf)   // row_shr:1
+    KVC_DPP_STEP(0x112, 0xf)   // row_shr:2
+    KVC_DPP_STEP(0x114, 0xf)   // row_shr:4
+    KVC_DPP_STEP(0x118, 0xf)   // row_shr:8
+    KVC_DPP_STEP(0x142, 0xa)   // row_bcast:15
+    KVC_DPP_STEP(0x143, 0xc)   // row_bcast:31
+#undef KVC_DPP_STEP
+    return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
+}
+
 struct LuShared {
-    float panel[RG_ROWS][RG_STRIP + 1];  // the panel being factored (one wave)
     float fmul[2][RG_STRIP][RG_ROWS];     // multipliers of the last two panels
-    int perm[RG_ROWS], inv[RG_ROWS], pivrow[RG_ROWS];
+    int inv[RG_ROWS], pivrow[RG_ROWS];    // logical index of each physical row; pivot row of each step
     unsigned char skip[RG_ROWS];
 };
 
-// Factor panel columns [c0, c0 + 16) held in sh.panel, one wave, step by
-// step in the reference's order; writes U row entries of the panel columns,
-// the multipliers (sh.fmul[buf]) and the pivot bookkeeping.
-__device__ void lu_factor_panel(LuShared & sh, bool (&live)[RG_SLOTS], int c0, int n, int lane, int buf,
-                                float * __restrict__ Ut) {
+// Apply panel kp's steps (columns 16 kp .. 16 kp + 15), in order, to this
+// wave's strip; the owner lane of each pivot row stores that U row's strip.
+__device__ __forceinline__ void lu_apply_panel(const LuShared & sh, float (&a)[RG_SLOTS][RG_STRIP],
+                                               bool (&live)[RG_SLOTS], int kp, int n, int w, int lane,
+                                               float * __restrict__ Ut) {
+    const int c0 = kp * RG_STRIP, buf = kp & 1;
     for (int jj = 0; jj < RG_STRIP; jj++) {
         const int col = c0 + jj;
         if (col >= n) break;
-        float bv = -1.0f;
+        const int P = sh.pivrow[col];
+        if (!sh.skip[col]) {
+            if (lane == (P & 63)) {
+                const int slot = P >> 6;
+                float4 * dst = reinterpret_cast<float4 *>(Ut + (long long)col * RG_ROWS + RG_STRIP * w);
+#pragma unroll
+                for (int s2 = 0; s2 < RG_SLOTS; s2++) {
+                    if (slot == s2) {
+#pragma unroll
+                        for (int q4 = 0; q4 < RG_STRIP / 4; q4++)
+                            dst[q4] = make_float4(a[s2][4 * q4], a[s2][4 * q4 + 1], a[s2][4 * q4 + 2], a[s2][4 * q4 + 3]);
+                    }
+                }
+            }
+            float sp[RG_STRIP];
+            rg_pivot_values(a, P, sp);
+#pragma unroll
+            for (int s = 0; s < RG_SLOTS; s++) {
+                const int r = lane + 64 * s;
+                if (live[s] && r != P) {
+                    const float f = sh.fmul[buf][jj][r];
+#pragma unroll
+                    for (int q = 0; q < RG_STRIP; q++) a[s][q] = a[s][q] - f * sp[q];
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) live[s] = live[s] && (lane + 64 * s != P);
+    }
+}
+
+// Factor panel k (this wave's strip, in registers) step by step in the
+// reference's order: pivot = first row (logical order) of largest |a| among
+// the rows not yet used, replacing the diagonal only when strictly larger and
+// never NaN; pivots below 1e-12 in magnitude skip the step (math.h:501-523).
+__device__ __forceinline__ void lu_factor_panel(LuShared & sh, float (&a)[RG_SLOTS][RG_STRIP],
+                                                bool (&live)[RG_SLOTS], int k, int n, int lane,
+                                                float * __restrict__ Ut, float * __restrict__ Lp) {
+    const int c0 = k * RG_STRIP, buf = k & 1;
+    int li[RG_SLOTS];
+#pragma unroll
+    for (int s = 0; s < RG_SLOTS; s++) li[s] = sh.inv[lane + 64 * s];
+    int my_piv = 0, my_skip = 0;   // lane jj keeps step jj's pivot row and skip flag
+#pragma unroll
+    for (int jj = 0; jj < RG_STRIP; jj++) {
+        const int col = c0 + jj;
+        if (col >= n) break;
+        // lane candidate: largest |a| (bit pattern of a non-negative float),
+        // ties to the smallest logical index; NaN rows never qualify
+        unsigned bk = 0;
         int bl = 0x7fffffff;
+        float v0 = 0.0f;
+        bool has0 = false;
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++) {
-            const int r = lane + 64 * s;
-            if (live[s]) {
-                const float v = fabsf(sh.panel[r][jj]);
-                const int li = sh.inv[r];
-                if (v == v && (v > bv || (v == bv && li < bl))) { bv = v; bl = li; }
-            }
+            const float v = fabsf(a[s][jj]);
+            const unsigned kb = __float_as_uint(v);
+            if (live[s] && v == v && (kb > bk || (kb == bk && li[s] < bl))) { bk = kb; bl = li[s]; }
+            if (li[s] == col) { v0 = a[s][jj]; has0 = true; }
         }
-        for (int o = 32; o > 0; o >>= 1) {
-            const float ov = __shfl_xor(bv, o);
-            const int ol = __shfl_xor(bl, o);
-            if (ov > bv || (ov == bv && ol < bl)) { bv = ov; bl = ol; }
-        }
-        const int Pc = sh.perm[col];
-        const float a0 = fabsf(sh.panel[Pc][jj]);
-        const int mr = (a0 == a0 && bv > a0) ? bl : col;
-        const int P = sh.perm[mr];
-        const float piv = sh.panel[P][jj];
+        const unsigned gmax = dpp_reduce_u32<true>(bk);
+        const unsigned glo = dpp_reduce_u32<false>(bk == gmax ? (unsigned)bl : 0x7fffffffu);
+        const unsigned long long m0 = __ballot(has0);
+        const float a0 = fabsf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), __builtin_ctzll(m0))));
+        const int mr = (a0 == a0 && __uint_as_float(gmax) > a0) ? (int)glo : col;
+        int slot_l = -1;
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++)
+            if (li[s] == mr) slot_l = s;
+        const unsigned long long mp = __ballot(slot_l >= 0);
+        const int laneP = __builtin_ctzll(mp);
+        const int slotP = __builtin_amdgcn_readlane(slot_l, laneP);
+        const int P = laneP + 64 * slotP;
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) li[s] = (li[s] == col) ? mr : ((li[s] == mr) ? col : li[s]);
+        float sp[RG_STRIP];
+        rg_pivot_values(a, P, sp);
+        const float piv = sp[jj];
         const bool elim = !(fabsf(piv) < 1e-12f);
-        float f[RG_SLOTS];
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++) {
             const int r = lane + 64 * s;
-            f[s] = (elim && live[s] && r != P) ? sh.panel[r][jj] / piv : 0.0f;
-        }
-        __builtin_amdgcn_wave_barrier();
-        if (lane == 0) {
-            sh.perm[col] = P;
-            sh.perm[mr] = Pc;
-            sh.inv[P] = col;
-            sh.inv[Pc] = mr;
-            sh.pivrow[col] = P;
-            sh.skip[col] = elim ? 0 : 1;
-        }
-        // U row col over the panel's columns
-        for (int q = jj + lane; q < RG_STRIP; q += 64)
-            if (c0 + q < n) Ut[(long long)col * RG_ROWS + c0 + q] = sh.panel[P][q];
+            const bool upd = elim && live[s] && r != P;
+            const float f = upd ? a[s][jj] / piv : 0.0f;
+            if (upd) {
 #pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++) {
-            const int r = lane + 64 * s;
-            sh.fmul[buf][jj][r] = f[s];
-            if (elim && live[s] && r != P) {
-#pragma unroll
-                for (int q = 0; q < RG_STRIP; q++)
-                    if (q > jj) sh.panel[r][q] = sh.panel[r][q] - f[s] * sh.panel[P][q];
+                for (int q = jj + 1; q < RG_STRIP; q++) a[s][q] = a[s][q] - f * sp[q];
             }
-            live[s] = live[s] && (r != P);
+            sh.fmul[buf][jj][r] = f;
+            live[s] = live[s] && r != P;
         }
-        __builtin_amdgcn_wave_barrier();
+        // U row col over the panel's columns (entries left of col are never read)
+        // (a wave-uniform offset through readfirstlane: keeps the compiler from
+        // carrying one hoisted 64-bit address per unrolled step)
+        const int uoff = __builtin_amdgcn_readfirstlane(col * RG_ROWS + c0);
+        if (lane == laneP) {
+            float4 * dst = reinterpret_cast<float4 *>(Ut + uoff);
+#pragma unroll
+            for (int s2 = 0; s2 < RG_SLOTS; s2++) {
+                if (slotP == s2) {
+#pragma unroll
+                    for (int q4 = 0; q4 < RG_STRIP / 4; q4++)
+                        dst[q4] = make_float4(a[s2][4 * q4], a[s2][4 * q4 + 1], a[s2][4 * q4 + 2], a[s2][4 * q4 + 3]);
+                }
+            }
+        }
+        if (lane == jj) {
+            my_piv = P;
+            my_skip = elim ? 0 : 1;
+        }
+    }
+    if (lane < RG_STRIP && c0 + lane < n) {
+        sh.pivrow[c0 + lane] = my_piv;
+        sh.skip[c0 + lane] = (unsigned char)my_skip;
+    }
+    // multipliers of this panel by physical row: Lp[r][c0 .. c0+15] (entries
+    // past column n of a row are never read)
+#pragma unroll
+    for (int s = 0; s < RG_SLOTS; s++) {
+        const int r = lane + 64 * s;
+        if (r < n) {
+            float4 * dst = reinterpret_cast<float4 *>(Lp + (unsigned)(r * RG_ROWS + c0));
+#pragma unroll
+            for (int q4 = 0; q4 < RG_STRIP / 4; q4++)
+                dst[q4] = make_float4(sh.fmul[buf][4 * q4][r], sh.fmul[buf][4 * q4 + 1][r],
+                                      sh.fmul[buf][4 * q4 + 2][r], sh.fmul[buf][4 * q4 + 3][r]);
+        }
+        sh.inv[r] = li[s];
     }
 }
 
@@ -708,87 +806,27 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
     for (int s = 0; s < RG_SLOTS; s++) {
         const int r = lane + 64 * s;
         live[s] = r < n;
+        const int rc = r < n ? r : n - 1;
 #pragma unroll
         for (int jj = 0; jj < RG_STRIP; jj++) {
             const int j = RG_STRIP * w + jj;
-            a[s][jj] = (r < n && j < n) ? A[(long long)j * n + r] : 0.0f;
+            const float v = A[(unsigned)((j < n ? j : n - 1) * n + rc)];
+            a[s][jj] = (r < n && j < n) ? v : 0.0f;
         }
     }
-    if (tid < RG_ROWS) {
-        sh.perm[tid] = tid;
-        sh.inv[tid] = tid;
-    }
+    if (tid < RG_ROWS) sh.inv[tid] = tid;
     __syncthreads();
     const int n_panels = (n + RG_STRIP - 1) / RG_STRIP;
+    // phase k: strips w >= k apply panel k-1, then wave k factors panel k
     for (int k = 0; k < n_panels; k++) {
-        const int c0 = k * RG_STRIP, buf = k & 1;
+        if (w == k) __builtin_amdgcn_s_setprio(3);
+        if (k > 0 && w >= k && w < n_panels) lu_apply_panel(sh, a, live, k - 1, n, w, lane, Ut);
         if (w == k) {
-#pragma unroll
-            for (int s2 = 0; s2 < RG_SLOTS; s2++)
-#pragma unroll
-                for (int q = 0; q < RG_STRIP; q++) sh.panel[lane + 64 * s2][q] = a[s2][q];
-            __builtin_amdgcn_wave_barrier();
-            lu_factor_panel(sh, live, c0, n, lane, buf, Ut);
-            // multipliers of this panel by physical row: Lp[r][c0 .. c0+15]
-#pragma unroll
-            for (int s = 0; s < RG_SLOTS; s++) {
-                const int r = lane + 64 * s;
-                if (r < n) {
-#pragma unroll
-                    for (int jj = 0; jj < RG_STRIP; jj++)
-                        if (c0 + jj < n) Lp[(long long)r * RG_ROWS + c0 + jj] = sh.fmul[buf][jj][r];
-                }
-            }
+            lu_factor_panel(sh, a, live, k, n, lane, Ut, Lp);
+            __builtin_amdgcn_s_setprio(0);
         }
         __syncthreads();
-        if (w > k && RG_STRIP * w < n) {
-            // apply the panel's steps, in order, to this strip
-            for (int jj = 0; jj < RG_STRIP; jj++) {
-                const int col = c0 + jj;
-                if (col >= n) break;
-                const int P = sh.pivrow[col];
-                if (!sh.skip[col]) {
-                    // U row col over this strip, stored by the pivot row's owner lane
-                    // (entries past column n of a row are never read)
-                    if (lane == (P & 63)) {
-                        const int slot = P >> 6;
-                        float4 * dst = reinterpret_cast<float4 *>(Ut + (long long)col * RG_ROWS + RG_STRIP * w);
-#pragma unroll
-                        for (int s2 = 0; s2 < RG_SLOTS; s2++) {
-                            if (slot == s2) {
-#pragma unroll
-                                for (int q4 = 0; q4 < RG_STRIP / 4; q4++)
-                                    dst[q4] = make_float4(a[s2][4 * q4], a[s2][4 * q4 + 1], a[s2][4 * q4 + 2], a[s2][4 * q4 + 3]);
-                            }
-                        }
-                    }
-                    float sp[RG_STRIP];
-                    rg_pivot_values(a, P, sp);
-#pragma unroll
-                    for (int s = 0; s < RG_SLOTS; s++) {
-                        const int r = lane + 64 * s;
-                        if (live[s] && r != P) {
-                            const float f = sh.fmul[buf][jj][r];
-#pragma unroll
-                            for (int q = 0; q < RG_STRIP; q++) a[s][q] = a[s][q] - f * sp[q];
-                        }
-                    }
-                }
-#pragma unroll
-                for (int s = 0; s < RG_SLOTS; s++) live[s] = live[s] && (lane + 64 * s != P);
-            }
-        } else if (w > k) {
-            // padding strip: keep the live flags in step
-            for (int jj = 0; jj < RG_STRIP; jj++) {
-                const int col = c0 + jj;
-                if (col >= n) break;
-                const int P = sh.pivrow[col];
-#pragma unroll
-                for (int s = 0; s < RG_SLOTS; s++) live[s] = live[s] && (lane + 64 * s != P);
-            }
-        }
     }
-    __syncthreads();
     if (tid < n) {
         perm_out[sys * (long long)g.tc_max + tid] = sh.pivrow[tid];
         skip_out[sys * (long long)g.tc_max + tid] = sh.skip[tid];
@@ -802,13 +840,43 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
 // per 64 right-hand sides, lane v owns column v. The first 128 solved rows
 // of each sweep move from LDS into registers and are then read through a
 // statically unrolled loop; the other rows' earlier results come from LDS.
+// Each row of L / U (and its right-hand-side value) is loaded one row ahead
+// into registers, so its global-memory latency overlaps the previous row.
 constexpr int BS_HIGH = 128;
+constexpr int BS_PAD = 128;   // the row buffer holds entry k at rowb[BS_PAD - shift + k]
 
-// stage one 256-float row (uniform across the wave) into LDS
-__device__ __forceinline__ void stage_row(const float * __restrict__ src, float * dst, int lane) {
-    const float4 v4 = reinterpret_cast<const float4 *>(src)[lane];
-    reinterpret_cast<float4 *>(dst)[lane] = v4;
-    __builtin_amdgcn_wave_barrier();
+// val -= rowp[t] * xsb[t][lane] for t = 0 .. n_terms-1, ascending and
+// sequential; batches of 8 operands are loaded one batch ahead.
+__device__ __forceinline__ float dot_seq(float val, const float * rowp, const float (*xsb)[64], int n_terms,
+                                         int lane) {
+    int t = 0;
+    if (n_terms >= 8) {
+        float rc[8], xc[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) { rc[u] = rowp[u]; xc[u] = xsb[u][lane]; }
+        for (; t + 16 <= n_terms; t += 8) {
+            float rn[8], xn[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) { rn[u] = rowp[t + 8 + u]; xn[u] = xsb[t + 8 + u][lane]; }
+#pragma unroll
+            for (int u = 0; u < 8; u++) val = val - rc[u] * xc[u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) { rc[u] = rn[u]; xc[u] = xn[u]; }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) val = val - rc[u] * xc[u];
+        t += 8;
+    }
+    for (; t < n_terms; t++) val = val - rowp[t] * xsb[t][lane];
+    return val;
+}
+
+// the same sum without the terms of steps whose pivot was skipped (skp[t] == 0)
+__device__ __forceinline__ float dot_seq_skip(float val, const float * rowp, const float (*xsb)[64], int n_terms,
+                                              const float * skp, int lane) {
+    for (int t = 0; t < n_terms; t++)
+        if (skp[t] != 0.0f) val = val - rowp[t] * xsb[t][lane];
+    return val;
 }
 
 __global__ void __launch_bounds__(64)
@@ -820,41 +888,50 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     const int h = sysl % g.H, c_idx = (sysl / g.H) % g.n_chunks, layer = sysl / (g.H * g.n_chunks);
     const ChunkDesc c = chunks[c_idx];
     const int n = c.tc, p = g.dv;
-    if (n > RG_ROWS) return;
+    if (n > RG_ROWS || n < 1) return;
     const int lane = threadIdx.x;
     const int v = blockIdx.y * 64 + lane;
     const bool act = v < p;
+    const int vc = act ? v : p - 1;   // in-range column for the loads of idle lanes
     const float * __restrict__ Ut = Ut_all + (long long)sysl * RG_ROWS * RG_ROWS;
     const float * __restrict__ Lp = Lp_all + (long long)sysl * RG_ROWS * RG_ROWS;
     const float * __restrict__ B = aug + aug_off[sysl] + (long long)n * n;   // column-major RHS [v][r]
     float * Yt = Yt_all + (long long)sysl * RG_ROWS * g.dv;
-    const int * perm = perm_in + (long long)sysl * g.tc_max;
     float * x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
     __shared__ float xs[BS_HIGH][64];
-    __shared__ __align__(16) float row[RG_ROWS];
+    __shared__ __align__(16) float rowb[BS_PAD + RG_ROWS];
     __shared__ float skf[RG_ROWS];   // 1 where the step eliminated, 0 where it was skipped
+    __shared__ int permL[RG_ROWS];
     __shared__ int any_skip;
     if (lane == 0) any_skip = 0;
     __builtin_amdgcn_wave_barrier();
     for (int i = lane; i < RG_ROWS; i += 64) {
         const int sk = (i < n) ? skip_in[(long long)sysl * g.tc_max + i] : 0;
         skf[i] = sk ? 0.0f : 1.0f;
+        permL[i] = (i < n) ? perm_in[(long long)sysl * g.tc_max + i] : 0;
         if (sk) any_skip = 1;
     }
     __builtin_amdgcn_wave_barrier();
     const bool sk = any_skip != 0;
+    const float * frow = rowb + BS_PAD;   // forward rows, unshifted
+    float4 * frow4 = reinterpret_cast<float4 *>(rowb + BS_PAD);
 
     // ---- forward: rows [0, lb) from LDS, then rows [lb, n) with [0, lb) in registers
     const int lb = n < BS_HIGH ? n : BS_HIGH;
+    float4 pf = reinterpret_cast<const float4 *>(Lp + (unsigned)(permL[0] * RG_ROWS))[lane];
+    float pb = B[(unsigned)(vc * n + permL[0])];
     for (int i = 0; i < lb; i++) {
-        const int r0 = perm[i];
-        stage_row(Lp + (long long)r0 * RG_ROWS, row, lane);
-        float val = act ? B[(long long)v * n + r0] : 0.0f;
-#pragma unroll 8
-        for (int j = 0; j < i; j++)
-            if (!sk || skf[j] != 0.0f) val -= row[j] * xs[j][lane];
+        frow4[lane] = pf;
+        float val = act ? pb : 0.0f;
+        if (i + 1 < n) {
+            const int rn = permL[i + 1];
+            pf = reinterpret_cast<const float4 *>(Lp + (unsigned)(rn * RG_ROWS))[lane];
+            pb = B[(unsigned)(vc * n + rn)];
+        }
+        __builtin_amdgcn_wave_barrier();
+        val = sk ? dot_seq_skip(val, frow, xs, i, skf, lane) : dot_seq(val, frow, xs, i, lane);
         xs[i][lane] = val;
-        if (act) Yt[(long long)i * g.dv + v] = val;
+        if (act) Yt[(unsigned)(i * g.dv + v)] = val;
         __builtin_amdgcn_wave_barrier();
     }
     if (n > BS_HIGH) {
@@ -862,60 +939,86 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 #pragma unroll
         for (int j = 0; j < BS_HIGH; j++) yr[j] = xs[j][lane];
         for (int i = BS_HIGH; i < n; i++) {
-            const int r0 = perm[i];
-            stage_row(Lp + (long long)r0 * RG_ROWS, row, lane);
-            float val = act ? B[(long long)v * n + r0] : 0.0f;
+            frow4[lane] = pf;
+            float val = act ? pb : 0.0f;
+            if (i + 1 < n) {
+                const int rn = permL[i + 1];
+                pf = reinterpret_cast<const float4 *>(Lp + (unsigned)(rn * RG_ROWS))[lane];
+                pb = B[(unsigned)(vc * n + rn)];
+            }
+            __builtin_amdgcn_wave_barrier();
             if (!sk) {
 #pragma unroll
-                for (int j = 0; j < BS_HIGH; j++) val -= row[j] * yr[j];
+                for (int j = 0; j < BS_HIGH; j++) val -= frow[j] * yr[j];
+                val = dot_seq(val, frow + BS_HIGH, xs, i - BS_HIGH, lane);
             } else {
 #pragma unroll
                 for (int j = 0; j < BS_HIGH; j++)
-                    if (skf[j] != 0.0f) val -= row[j] * yr[j];
+                    if (skf[j] != 0.0f) val -= frow[j] * yr[j];
+                val = dot_seq_skip(val, frow + BS_HIGH, xs, i - BS_HIGH, skf + BS_HIGH, lane);
             }
-#pragma unroll 8
-            for (int j = BS_HIGH; j < i; j++)
-                if (!sk || skf[j] != 0.0f) val -= row[j] * xs[j - BS_HIGH][lane];
             xs[i - BS_HIGH][lane] = val;
-            if (act) Yt[(long long)i * g.dv + v] = val;
+            if (act) Yt[(unsigned)(i * g.dv + v)] = val;
             __builtin_amdgcn_wave_barrier();
         }
     }
 
-    // ---- backward: rows [hb, n) from LDS, then rows [0, hb) with [hb, n) in registers
+    // ---- backward: rows [hb, n) from LDS, then rows [0, hb) with [hb, n) in
+    // registers. Row col of U is published shifted by -hb (entry k at
+    // brow[k]), so that the register part's entries brow[hb + i] are aligned.
     const int hb = n > BS_HIGH ? n - BS_HIGH : 0;
+    float * brow = rowb + BS_PAD - hb;
+    pf = reinterpret_cast<const float4 *>(Ut + (unsigned)((n - 1) * RG_ROWS))[lane];
+    pb = Yt[(unsigned)((n - 1) * g.dv + vc)];
     for (int col = n - 1; col >= hb; col--) {
-        stage_row(Ut + (long long)col * RG_ROWS, row, lane);
-        const float piv = row[col];
+        brow[4 * lane + 0] = pf.x;
+        brow[4 * lane + 1] = pf.y;
+        brow[4 * lane + 2] = pf.z;
+        brow[4 * lane + 3] = pf.w;
+        const float yv = pb;
+        if (col > 0) {
+            pf = reinterpret_cast<const float4 *>(Ut + (unsigned)((col - 1) * RG_ROWS))[lane];
+            pb = Yt[(unsigned)((col - 1) * g.dv + vc)];
+        }
+        __builtin_amdgcn_wave_barrier();
+        const float piv = brow[col];
         float val = 0.0f;
         if (!(fabsf(piv) < 1e-12f)) {
-            val = act ? Yt[(long long)col * g.dv + v] : 0.0f;
-#pragma unroll 8
-            for (int r = col + 1; r < n; r++) val -= row[r] * xs[r - hb][lane];
+            val = act ? yv : 0.0f;
+            val = dot_seq(val, brow + col + 1, xs + (col + 1 - hb), n - col - 1, lane);
             val = val / piv;
         }
         xs[col - hb][lane] = val;
-        if (act) x[(long long)col * g.dv + v] = val;
+        if (act) x[(unsigned)(col * g.dv + v)] = val;
         __builtin_amdgcn_wave_barrier();
     }
     if (hb == 0) return;
     float xh[BS_HIGH];
 #pragma unroll
     for (int i = 0; i < BS_HIGH; i++) xh[i] = xs[i][lane];
+    const float * bhi = rowb + BS_PAD;   // == brow + hb
     for (int col = hb - 1; col >= 0; col--) {
-        stage_row(Ut + (long long)col * RG_ROWS, row, lane);
-        const float piv = row[col];
+        brow[4 * lane + 0] = pf.x;
+        brow[4 * lane + 1] = pf.y;
+        brow[4 * lane + 2] = pf.z;
+        brow[4 * lane + 3] = pf.w;
+        const float yv = pb;
+        if (col > 0) {
+            pf = reinterpret_cast<const float4 *>(Ut + (unsigned)((col - 1) * RG_ROWS))[lane];
+            pb = Yt[(unsigned)((col - 1) * g.dv + vc)];
+        }
+        __builtin_amdgcn_wave_barrier();
+        const float piv = brow[col];
         float val = 0.0f;
         if (!(fabsf(piv) < 1e-12f)) {
-            val = act ? Yt[(long long)col * g.dv + v] : 0.0f;
-#pragma unroll 8
-            for (int r = col + 1; r < hb; r++) val -= row[r] * xs[r][lane];
+            val = act ? yv : 0.0f;
+            val = dot_seq(val, brow + col + 1, xs + (col + 1), hb - col - 1, lane);
 #pragma unroll
-            for (int i = 0; i < BS_HIGH; i++) val -= row[hb + i] * xh[i];
+            for (int i = 0; i < BS_HIGH; i++) val -= bhi[i] * xh[i];
             val = val / piv;
         }
         xs[col][lane] = val;
-        if (act) x[(long long)col * g.dv + v] = val;
+        if (act) x[(unsigned)(col * g.dv + v)] = val;
         __builtin_amdgcn_wave_barrier();
     }
 }
