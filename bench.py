@@ -42,7 +42,12 @@ import kvcompact as kc  # noqa: E402
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_PEAK_TFLOPS = 157.3       # MI355X fp32
 STAGES = ["scores", "chunk_softmax_importance", "refit_target", "selection", "compacted_softmax",
-          "normal_equations", "elimination", "quality_stats"]
+          "normal_equations", "lu_factorization", "substitution", "quality_stats"]
+STAGE_KERNELS = {"scores": "k_scores", "chunk_softmax_importance": "k_softmax_importance",
+                 "refit_target": "k_refit_target", "selection": "k_global_importance + k_select_topk",
+                 "compacted_softmax": "k_ls_softmax", "normal_equations": "k_ls_build",
+                 "lu_factorization": "k_ge_lu", "substitution": "k_ge_solve",
+                 "quality_stats": "k_scores + k_row_softmax + k_stats_sum + k_stats_final"}
 
 
 def gen_layers(L, T, H, d, W, seed):
@@ -69,8 +74,12 @@ def stage_model(L, T, H, d, nq, t, n_chunks, tc):
     E = H * d
     units = L * H * n_chunks
     n, p = tc, d
-    elim = 2 * sum((n - 1 - c) * (n + p - c) for c in range(n))
-    back = 2 * p * sum(n - 1 - c for c in range(n))
+    # LU of the n x n Gram matrix: step c divides n-1-c multipliers and
+    # updates (n-1-c) x (n-1-c) entries with one multiply and one subtract
+    lu = sum(2 * (n - 1 - c) * (n - 1 - c) + (n - 1 - c) for c in range(n))
+    # forward + back substitution over p right-hand sides (one multiply and
+    # one subtract per L / U entry and column, one divide per row and column)
+    subst = p * (2 * n * (n - 1) + n)
     m = {
         "scores": dict(bytes=4 * L * T * E + 4 * L * H * nq * T, flops=2 * L * H * nq * T * d),
         "chunk_softmax_importance": dict(bytes=4 * L * H * nq * T * 2 + 4 * L * H * T, flops=0),
@@ -78,7 +87,8 @@ def stage_model(L, T, H, d, nq, t, n_chunks, tc):
         "selection": dict(bytes=4 * L * H * T + 4 * L * t, flops=0),
         "compacted_softmax": dict(bytes=4 * L * H * nq * t * 2, flops=0),
         "normal_equations": dict(bytes=4 * units * n * (n + p), flops=2 * nq * units * n * (n + p)),
-        "elimination": dict(bytes=4 * units * (2 * n * (n + p) + n * p), flops=units * (elim + back)),
+        "lu_factorization": dict(bytes=4 * units * 2 * n * n, flops=units * lu),
+        "substitution": dict(bytes=4 * units * (n * n + 3 * n * p), flops=units * subst),
         "quality_stats": dict(bytes=4 * L * min(H, 4) * T * 2 * d, flops=2 * L * min(H, 4) * min(nq, 32) * T * 2 * d),
     }
     return m
@@ -91,11 +101,11 @@ def roofline(name, model, ms):
     s = ms / 1e3
     if t_cmp > t_hbm:
         ach = f / s / 1e12
-        return dict(kernel=name, bound="mfma", achieved=round(ach, 3), peak=FP32_PEAK_TFLOPS, unit="TFLOP/s",
+        return dict(kernel=STAGE_KERNELS[name], stage=name, bound="mfma", achieved=round(ach, 3), peak=FP32_PEAK_TFLOPS, unit="TFLOP/s",
                     frac=round(ach / FP32_PEAK_TFLOPS, 4), traffic=None, ms=round(ms, 3),
                     algorithmic_flops=f, algorithmic_bytes=b)
     ach = b / s / 1e9
-    return dict(kernel=name, bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+    return dict(kernel=STAGE_KERNELS[name], stage=name, bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(ach / HBM_PEAK_GBS, 4), traffic=None, ms=round(ms, 3),
                 algorithmic_flops=f, algorithmic_bytes=b)
 

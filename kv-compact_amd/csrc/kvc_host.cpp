@@ -35,7 +35,8 @@ namespace {
 // ------------------------------------------------------------------ device
 
 // Pipeline stages timed with events on the call's stream (kvc_stage_times)
-enum Stage { ST_SCORES, ST_SOFTMAX, ST_REFIT, ST_SELECT, ST_LS_SOFTMAX, ST_LS_BUILD, ST_GE, ST_STATS, ST_COUNT };
+enum Stage { ST_SCORES, ST_SOFTMAX, ST_REFIT, ST_SELECT, ST_LS_SOFTMAX, ST_LS_BUILD, ST_LU, ST_SOLVE, ST_STATS,
+             ST_COUNT };
 
 struct DeviceCtx {
     std::mutex mu;
@@ -376,8 +377,10 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     // 6. normal equations and their solution
     launch_ls_build(g, w, st);
     (void)hipEventRecord(ev[ST_LS_BUILD + 1], st);
-    launch_ge(g, w, io.Cv, st);
-    (void)hipEventRecord(ev[ST_GE + 1], st);
+    launch_ge_lu(g, w, st);
+    (void)hipEventRecord(ev[ST_LU + 1], st);
+    launch_ge_solve(g, w, io.Cv, st);
+    (void)hipEventRecord(ev[ST_SOLVE + 1], st);
     // 7. quality statistics against the full call
     launch_stats(g, w, sw, io.K, io.V, io.Q, io.beta, io.Cv, io.stats, st);
     (void)hipEventRecord(ev[ST_STATS + 1], st);
@@ -396,7 +399,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     if (tm) {
         tm->scoring_ms = ctx->stage_ms[ST_SCORES] + ctx->stage_ms[ST_SOFTMAX] + ctx->stage_ms[ST_SELECT];
         tm->nnls_ms = ctx->stage_ms[ST_REFIT] + ctx->stage_ms[ST_LS_SOFTMAX] + ctx->stage_ms[ST_LS_BUILD] +
-                      ctx->stage_ms[ST_GE];
+                      ctx->stage_ms[ST_LU] + ctx->stage_ms[ST_SOLVE];
     }
     return 0;
 }

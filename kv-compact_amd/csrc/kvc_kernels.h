@@ -15,7 +15,8 @@ void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStr
 void launch_select_topk(const Geom & g, const Work & w, hipStream_t st);
 void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st);
 void launch_ls_build(const Geom & g, const Work & w, hipStream_t st);
-void launch_ge(const Geom & g, const Work & w, float * Cv, hipStream_t st);
+void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st);
+void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st);
 void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const float * K,
                   const float * V, const float * Q, const float * beta, const float * Cv,
                   float * stats, hipStream_t st);

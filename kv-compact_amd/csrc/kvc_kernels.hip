@@ -1435,10 +1435,13 @@ void launch_ls_build(const Geom & g, const Work & w, hipStream_t st) {
                        g, w.chunks, w.X, w.Y, w.aug, w.aug_off, lds_floats);
 }
 
-void launch_ge(const Geom & g, const Work & w, float * Cv, hipStream_t st) {
-    const unsigned systems = (unsigned)(g.L * g.n_chunks * g.H);
+void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st) {
     hipLaunchKernelGGL(k_ge_lu, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
                        g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.Ut, w.Lp);
+}
+
+void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st) {
+    const unsigned systems = (unsigned)(g.L * g.n_chunks * g.H);
     hipLaunchKernelGGL(k_ge_solve, dim3(systems, cdiv(g.dv, 64)), dim3(64), 0, st,
                        g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.Ut, w.Lp, w.Bt, Cv);
     if (g.tc_max > RG_ROWS)
