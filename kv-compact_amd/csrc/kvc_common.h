@@ -67,6 +67,22 @@ struct Work {
     ChunkDesc * chunks;  // [n_chunks + 2]; then all T keys, then the kept keys (statistics)
 };
 
+// Diversity selection scratch (api.cpp:175-233). One unit = (layer, chunk).
+// A level runs candidate pruning, the candidates' Gram matrix and the greedy
+// pass for the units whose gslot is >= 0.
+enum DivState : int { DIV_PENDING = 0, DIV_DONE = 1, DIV_RETRY = 2, DIV_SHORT = 3 };
+struct DivWork {
+    float strength;   // diversity_strength
+    float alpha;      // candidates: importance >= alpha * (t-th largest); 0 = every unused key
+    int cap;          // candidate capacity of a unit at this level (<= DIV_MAX_CAND)
+    int * state;      // [units] DivState
+    int * gslot;      // [units] Gram slot of the unit at this level, -1 = not run
+    int * count;      // [units] number of candidates
+    float * maxnc;    // [units] largest importance among the pruned keys
+    float * G;        // [slots][cap][cap] Gram matrix of the candidates' full key rows
+};
+constexpr int DIV_MAX_CAND = 1280;   // 20 candidates per lane in the greedy wave
+
 // Statistics scratch (api.cpp:239-325 sampling: h < min(H,4), qi < min(nq,32))
 struct StatWork {
     int mh, mq, qmode;

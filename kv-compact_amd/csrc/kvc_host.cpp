@@ -252,7 +252,6 @@ int check_supported(const kv_compact_params & p, int d_v) {
     if (p.use_omp || p.use_sensitivity) return KV_COMPACT_E_UNSUPPORTED;
     if (!p.skip_beta) return KV_COMPACT_E_UNSUPPORTED;
     if (p.refine_rounds > 0) return KV_COMPACT_E_UNSUPPORTED;
-    if (p.use_diversity) return KV_COMPACT_E_UNSUPPORTED;
     if (d_v > 256) return KV_COMPACT_E_UNSUPPORTED;
     return 0;
 }
@@ -276,7 +275,24 @@ struct Timing {
     double scoring_ms = 0.0, nnls_ms = 0.0;
 };
 
-size_t workspace_bytes(const Plan & pl, const BatchIO & io, bool need_e, Carver * cv_out, Work * w, StatWork * sw) {
+// candidate capacity of the first diversity level: twice the kept count
+int div_cap1(const Plan & pl) {
+    int c = std::max(2 * pl.tc_max, 256);
+    c = (c + 63) / 64 * 64;
+    return std::max(1, std::min(std::min(c, pl.Tc_max), DIV_MAX_CAND));
+}
+
+size_t div_g_floats(const Plan & pl, int L) {
+    const size_t units = (size_t)L * pl.n_chunks;
+    const size_t c1 = div_cap1(pl), cm = std::min(pl.Tc_max, DIV_MAX_CAND);
+    return std::max(units * c1 * c1, cm * cm);
+}
+
+// p == nullptr: statistics-only workspace (no exp scores, no diversity)
+size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_params * p, Carver * cv_out, Work * w,
+                       StatWork * sw, DivWork * dw = nullptr, size_t * div_floats = nullptr) {
+    const bool need_e = p && !p->skip_beta;
+    const bool div = p && p->use_diversity;
     Carver cv = cv_out ? *cv_out : Carver();
     const size_t L = io.L, H = io.H, T = io.T, nqm = pl.nq_max, nc = pl.n_chunks;
     const size_t tt = pl.t_total, dv = io.dv;
@@ -295,7 +311,10 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, bool need_e, Carver 
     ww.aug = cv.take<float>(L * H * aug_elems);
     ww.aug_off = cv.take<long long>(L * nc * H);
     ww.perm = cv.take<int>(L * nc * H * (size_t)pl.tc_max);
-    const size_t ut_rows = pl.tc_max <= 256 ? 256 : 0;
+    // register-LU systems (t_c <= 256) exist unless every chunk keeps more
+    int tc_min = pl.tc_max;
+    for (int c = 0; c < pl.n_chunks; c++) tc_min = std::min(tc_min, pl.chunks[c].tc);
+    const size_t ut_rows = tc_min <= 256 ? 256 : 0;
     ww.skip = cv.take<unsigned char>(L * nc * H * (size_t)pl.tc_max);
     ww.Ut = cv.take<float>(L * nc * H * ut_rows * ut_rows);
     ww.Lp = cv.take<float>(L * nc * H * ut_rows * ut_rows);
@@ -304,6 +323,18 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, bool need_e, Carver 
     ww.cand = cv.take<int>(L * nc * (size_t)pl.Tc_max);
     ww.flags = cv.take<unsigned char>(L * nc * (size_t)pl.Tc_max);
     ww.chunks = cv.take<ChunkDesc>(pl.chunks.size());
+    if (div) {
+        const size_t units = L * nc;
+        DivWork d{};
+        d.state = cv.take<int>(units);
+        d.gslot = cv.take<int>(units);
+        d.count = cv.take<int>(units);
+        d.maxnc = cv.take<float>(units);
+        const size_t gf = div_g_floats(pl, io.L);
+        d.G = cv.take<float>(gf);
+        if (dw) *dw = d;
+        if (div_floats) *div_floats = gf;
+    }
     StatWork s{};
     s.mh = std::min(io.H, 4);
     s.mq = std::min(pl.nq_global, 32);
@@ -318,12 +349,62 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, bool need_e, Carver 
     return cv.off + 256;
 }
 
+// Diversity selection by levels of candidate pruning (each exact; a unit
+// whose pruned greedy pass cannot certify its picks moves to the next,
+// wider level): alpha = max(0.85, safe), then the safe bound
+// (1 - 1.001 s)(1 - 1e-5), then every unused key.
+int run_diversity(hipStream_t st, const Plan & pl, const kv_compact_params & p, const Geom & g, const Work & w,
+                  DivWork dw, size_t g_floats, const float * K) {
+    const int units = g.L * pl.n_chunks;
+    const float s = p.diversity_strength;
+    float safe = 0.0f;
+    if (s >= 0.0f && s < 1.0f) safe = std::max(0.0f, (1.0f - 1.001f * s) * (1.0f - 1e-5f));
+    struct Level { float alpha; int cap; };
+    std::vector<Level> levels;
+    const int cmax = std::min(pl.Tc_max, DIV_MAX_CAND);
+    if (safe > 0.0f) {
+        const float a1 = std::max(0.85f, safe);
+        levels.push_back({a1, div_cap1(pl)});
+        if (safe < a1) levels.push_back({safe, cmax});
+    }
+    levels.push_back({0.0f, cmax});
+    dw.strength = s;
+    std::vector<int> state(units, DIV_RETRY), slot(units, -1), got(units);
+    for (const Level & lv : levels) {
+        std::vector<int> todo;
+        for (int u = 0; u < units; u++)
+            if (state[u] == DIV_RETRY) todo.push_back(u);
+        if (todo.empty()) break;
+        const size_t per = std::max<size_t>(1, g_floats / ((size_t)lv.cap * lv.cap));
+        dw.alpha = lv.alpha;
+        dw.cap = lv.cap;
+        for (size_t b0 = 0; b0 < todo.size(); b0 += per) {
+            const size_t b1 = std::min(todo.size(), b0 + per);
+            std::fill(slot.begin(), slot.end(), -1);
+            for (size_t k = b0; k < b1; k++) slot[todo[k]] = (int)(k - b0);
+            if (hipMemcpyAsync(dw.gslot, slot.data(), (size_t)units * sizeof(int), hipMemcpyHostToDevice, st) !=
+                hipSuccess)
+                return KV_COMPACT_E_DEVICE;
+            launch_div_level(g, w, dw, K, st);
+            if (hipMemcpyAsync(got.data(), dw.state, (size_t)units * sizeof(int), hipMemcpyDeviceToHost, st) !=
+                    hipSuccess ||
+                hipStreamSynchronize(st) != hipSuccess)
+                return KV_COMPACT_E_DEVICE;
+            for (size_t k = b0; k < b1; k++) state[todo[k]] = got[todo[k]];
+        }
+    }
+    for (int u = 0; u < units; u++)
+        if (state[u] != DIV_DONE) return KV_COMPACT_E_UNSUPPORTED;   // greedy stopped early or > DIV_MAX_CAND keys
+    return 0;
+}
+
 int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact_params & p,
               const BatchIO & io, Carver & carver, Timing * tm) {
-    const bool need_e = !p.skip_beta;
     Work w{};
     StatWork sw{};
-    workspace_bytes(pl, io, need_e, &carver, &w, &sw);
+    DivWork dw{};
+    size_t div_floats = 0;
+    workspace_bytes(pl, io, &p, &carver, &w, &sw, &dw, &div_floats);
     w.sel = io.indices;
     w.wts = const_cast<float *>(io.wts);
     (void)ctx;
@@ -366,8 +447,14 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     // 3. refit target Y = A V
     launch_refit_target(g, w, io.V, st);
     (void)hipEventRecord(ev[ST_REFIT + 1], st);
-    // 4. global importance (+R-KV) and top-t
-    launch_select_topk(g, w, st);
+    // 4. global importance (+R-KV), then top-t or the diversity greedy pass
+    launch_global_importance(g, w, st);
+    if (p.use_diversity) {
+        const int rc = run_diversity(st, pl, p, g, w, dw, div_floats, io.K);
+        if (rc) return rc;
+    } else {
+        launch_select_topk(g, w, st);
+    }
     (void)hipEventRecord(ev[ST_SELECT + 1], st);
     // 5. beta (skip_beta: zeros), X = softmax(S[:, sel] + beta)
     if (hipMemsetAsync(io.beta, 0, (size_t)io.L * io.H * pl.t_total * sizeof(float), st) != hipSuccess)
@@ -477,7 +564,7 @@ int compact_one(const float * K, const float * V, const float * Q, int T, int n_
     float * dC = sizer.take<float>((size_t)H * std::max(pl.t_total, 1) * dv);
     float * dS = sizer.take<float>(3);
     (void)dK; (void)dV; (void)dQ; (void)dW; (void)dI; (void)dB; (void)dC; (void)dS;
-    size_t need = workspace_bytes(pl, io, !p.skip_beta, &sizer, nullptr, nullptr);
+    size_t need = workspace_bytes(pl, io, &p, &sizer, nullptr, nullptr);
     if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
 
     Carver cv;
@@ -695,7 +782,7 @@ int kv_compact_multi_round(const float * K_all, const float * V_all, const float
         sizer.take<float>((size_t)T * ek); sizer.take<float>((size_t)T * ev); sizer.take<float>((size_t)nqm * ek);
         sizer.take<int>(std::max(result->t, 1)); sizer.take<float>((size_t)H * result->t);
         sizer.take<float>((size_t)H * result->t * d_v); sizer.take<float>(3);
-        size_t need = workspace_bytes(pl, io, false, &sizer, nullptr, nullptr);
+        size_t need = workspace_bytes(pl, io, nullptr, &sizer, nullptr, nullptr);
         if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
         Carver cv;
         cv.base = ctx->arena;
@@ -708,7 +795,7 @@ int kv_compact_multi_round(const float * K_all, const float * V_all, const float
         float * dS = cv.take<float>(3);
         Work w{};
         StatWork sw{};
-        workspace_bytes(pl, io, false, &cv, &w, &sw);
+        workspace_bytes(pl, io, nullptr, &cv, &w, &sw);
         sw.qmode = Q_PROVIDED;
         std::vector<float> b((size_t)H * result->t), c((size_t)H * result->t * d_v);
         for (int h = 0; h < H; h++) {
@@ -1021,7 +1108,7 @@ int kvc_compact_layers_device(const float * K, const float * V, const float * Q_
     const bool host_w = !token_weight && rkv_weights(p, T, wts);
     Carver sizer;
     if (host_w) sizer.take<float>(T);
-    size_t need = workspace_bytes(pl, io, !p.skip_beta, &sizer, nullptr, nullptr);
+    size_t need = workspace_bytes(pl, io, &p, &sizer, nullptr, nullptr);
     if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
     Carver cv;
     cv.base = ctx->arena;

@@ -12,7 +12,9 @@ void launch_scores(const Geom & g, const ChunkDesc * chunks, int n_chunk_units, 
                    const int * key_idx = nullptr, const float * beta = nullptr);
 void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st);
 void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStream_t st);
+void launch_global_importance(const Geom & g, const Work & w, hipStream_t st);
 void launch_select_topk(const Geom & g, const Work & w, hipStream_t st);
+void launch_div_level(const Geom & g, const Work & w, const DivWork & dw, const float * K, hipStream_t st);
 void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st);
 void launch_ls_build(const Geom & g, const Work & w, hipStream_t st);
 void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st);

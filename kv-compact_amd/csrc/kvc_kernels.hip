@@ -485,6 +485,323 @@ k_select_topk(Geom g, const ChunkDesc * __restrict__ chunks, const float * __res
     write_flagged(fl, c.Tc, c.start, sel + (long long)layer * g.t_total + c.off);
 }
 
+// Wave-wide max / min of a 32-bit unsigned value through DPP row shifts and
+// row broadcasts (the result collects in lane 63); both operations are
+// idempotent, so lanes whose DPP source is out of range keep their own value.
+template <bool MAX>
+__device__ __forceinline__ unsigned dpp_reduce_u32(unsigned x) {
+#define KVC_DPP_STEP(ctrl, rmask)                                                                  \
+    {                                                                                              \
+        const unsigned t = (unsigned)__builtin_amdgcn_update_dpp((int)x, (int)x, ctrl, rmask, 0xf, false); \
+        x = MAX ? (t > x ? t : x) : (t < x ? t : x);                                               \
+    }
+    KVC_DPP_STEP(0x111, 0xf)   // row_shr:1
+    KVC_DPP_STEP(0x112, 0xf)   // row_shr:2
+    KVC_DPP_STEP(0x114, 0xf)   // row_shr:4
+    KVC_DPP_STEP(0x118, 0xf)   // row_shr:8
+    KVC_DPP_STEP(0x142, 0xa)   // row_bcast:15
+    KVC_DPP_STEP(0x143, 0xc)   // row_bcast:31
+#undef KVC_DPP_STEP
+    return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+// ---------------------------------------------------------------------------
+// Diversity selection (api.cpp:175-233). The reference's greedy pass picks,
+// t - prefix times, the unused key of largest imp_j * (1 - s * pen_j) (first
+// index on ties, scores must beat -1e30), then raises every unused key's
+// penalty to its cosine with the pick, over the full H*d_k key row:
+//   cos = dot(k_b, k_j) / ((sqrtf(|k_b|^2) + 1e-8) * sqrtf(|k_j|^2) + 1e-8),
+// all sums sequential over the row. A sequential dot product is symmetric bit
+// for bit (a*b == b*a), and |k_j|^2 is the Gram diagonal, so every value the
+// pass needs is an entry of the candidates' Gram matrix.
+//
+// Pruning: while fewer than t keys are used, one of the t most important keys
+// is unused, so the pick's score is at least about (1 - s) I_t (I_t = t-th
+// largest importance) and at most its own importance (1 - s*pen <= 1). Keys
+// below alpha * I_t are left out; the greedy pass then checks at every step
+// that its pick beats the largest pruned importance (which bounds every pruned
+// key's score) and flags the unit for a wider level otherwise, so the result
+// is exact whatever alpha is.
+// ---------------------------------------------------------------------------
+
+// candidates of one (layer, chunk): ascending positions of the unused keys
+// with importance >= alpha * I_t; grid (n_chunks, L), 256 threads
+__global__ void __launch_bounds__(256)
+k_div_candidates(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ gimp, DivWork dw,
+                 int * __restrict__ cand_all) {
+    const int c_idx = blockIdx.x, layer = blockIdx.y;
+    const int unit = layer * g.n_chunks + c_idx;
+    if (dw.gslot[unit] < 0) return;
+    const ChunkDesc c = chunks[c_idx];
+    const float * im = gimp + (long long)layer * g.T + c.start;
+    const int pc = min(c.prefix, c.tc);
+    const int need = c.tc - pc;
+    const int tid = threadIdx.x;
+    __shared__ int s_cnt, s_bad;
+    __shared__ unsigned s_lo, s_hi;
+    __shared__ int wsum[4];
+    if (need <= 0) {   // the prefix fills the chunk: no greedy step
+        if (tid == 0) {
+            dw.maxnc[unit] = -INFINITY;
+            dw.count[unit] = 0;
+            dw.state[unit] = DIV_PENDING;
+        }
+        return;
+    }
+    if (tid == 0) s_bad = 0;
+    __syncthreads();
+    // pruning needs finite, non-negative importance and 0 <= s < 1
+    float thr = -INFINITY;
+    bool prune = dw.alpha > 0.0f && dw.strength >= 0.0f && dw.strength < 1.0f;
+    if (prune) {
+        for (int j = tid; j < c.Tc; j += blockDim.x) {
+            const float v = im[j];
+            if (!(v >= 0.0f && v <= 3.0e38f)) s_bad = 1;
+        }
+        __syncthreads();
+        prune = s_bad == 0;
+    }
+    if (prune) {
+        // I_t: the largest bit pattern x with #(imp >= x) >= tc (order of
+        // non-negative floats = order of their bits)
+        if (tid == 0) { s_lo = 0u; s_hi = 0x7f7fffffu; }
+        __syncthreads();
+        for (int it = 0; it < 32; it++) {
+            const unsigned lo = s_lo, hi = s_hi;
+            if (lo >= hi) break;
+            const unsigned mid = lo + (hi - lo + 1u) / 2u;
+            if (tid == 0) s_cnt = 0;
+            __syncthreads();
+            int cnt = 0;
+            for (int j = tid; j < c.Tc; j += blockDim.x) cnt += (__float_as_uint(im[j]) >= mid) ? 1 : 0;
+            atomicAdd(&s_cnt, cnt);
+            __syncthreads();
+            if (tid == 0) {
+                if (s_cnt >= c.tc) s_lo = mid; else s_hi = mid - 1u;
+            }
+            __syncthreads();
+        }
+        thr = __uint_as_float(s_lo) * dw.alpha;
+    }
+    // flags, the largest pruned importance, then an ascending write-out
+    int * cand = cand_all + (long long)unit * g.Tc_max;
+    __shared__ int carry;
+    if (tid == 0) carry = 0;
+    __syncthreads();
+    float mnc = -INFINITY;
+    for (int j0 = 0; j0 < c.Tc; j0 += blockDim.x) {
+        const int j = j0 + tid;
+        int f = 0;
+        if (j < c.Tc && j >= pc) {
+            const float v = im[j];
+            if (!prune || v >= thr) f = 1;
+            else if (v > mnc) mnc = v;
+        }
+        const int lane = tid & 63, w = tid >> 6;
+        const unsigned long long m = __ballot(f);
+        const int pre_l = __popcll(m & ((1ull << lane) - 1ull));
+        if (lane == 0) wsum[w] = __popcll(m);
+        __syncthreads();
+        int pre = carry;
+        for (int i = 0; i < w; i++) pre += wsum[i];
+        const int pos = pre + pre_l;
+        if (f && pos < dw.cap) cand[pos] = j;
+        __syncthreads();
+        if (tid == 0) carry += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+        __syncthreads();
+    }
+    // block max of the pruned importances (non-negative or -inf)
+    for (int o = 32; o > 0; o >>= 1) {
+        const float y = __shfl_xor(mnc, o);
+        if (y > mnc) mnc = y;
+    }
+    if ((tid & 63) == 0) wsum[tid >> 6] = __float_as_int(mnc);
+    __syncthreads();
+    if (tid == 0) {
+        float m = -INFINITY;
+        for (int i = 0; i < 4; i++) {
+            const float y = __int_as_float(wsum[i]);
+            if (y > m) m = y;
+        }
+        dw.maxnc[unit] = m;
+        dw.count[unit] = carry;
+        dw.state[unit] = (carry > dw.cap) ? DIV_RETRY : DIV_PENDING;
+    }
+}
+
+// Gram matrix of one unit's candidates over the full key row (length H*d_k),
+// each entry a sequential dot product. Tiles of 64 x 64 above the diagonal
+// (mirrored on write); 256 threads, each 4 x 4 entries. grid (units, tile pairs).
+constexpr int DG_TILE = 64, DG_SLAB = 32;
+
+__global__ void __launch_bounds__(256)
+k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ K, DivWork dw,
+           const int * __restrict__ cand_all) {
+    const int unit = blockIdx.x;
+    const int slot = dw.gslot[unit];
+    if (slot < 0 || dw.state[unit] != DIV_PENDING) return;
+    const int C = dw.count[unit];
+    // tile pair (ti <= tj) from the linear index
+    int ti = 0, rem = blockIdx.y;
+    const int nt = (dw.cap + DG_TILE - 1) / DG_TILE;
+    while (rem >= nt - ti) { rem -= nt - ti; ti++; }
+    const int tj = ti + rem;
+    if (ti * DG_TILE >= C || tj * DG_TILE >= C) return;
+    const int layer = unit / g.n_chunks, c_idx = unit % g.n_chunks;
+    const ChunkDesc c = chunks[c_idx];
+    const int E = g.H * g.dk;
+    const int * cand = cand_all + (long long)unit * g.Tc_max;
+    const float * Kl = K + (long long)layer * g.ldK + (long long)c.start * E;
+    __shared__ __align__(16) float As[DG_SLAB][DG_TILE + 4];
+    __shared__ __align__(16) float Bs[DG_SLAB][DG_TILE + 4];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    // loader: row lr of the tile, dims lq*8 .. lq*8+7 of the slab
+    const int lr = tid >> 2, lq = tid & 3;
+    const int ra = ti * DG_TILE + lr, rb = tj * DG_TILE + lr;
+    const float * pa = Kl + (long long)cand[ra < C ? ra : C - 1] * E + lq * 8;
+    const float * pb = Kl + (long long)cand[rb < C ? rb : C - 1] * E + lq * 8;
+    const bool vec = (E & 3) == 0 && (reinterpret_cast<uintptr_t>(Kl) & 15) == 0;
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
+    for (int d0 = 0; d0 < E; d0 += DG_SLAB) {
+        float va[8], vb[8];
+        if (vec && d0 + DG_SLAB <= E) {
+            const float4 a0 = *reinterpret_cast<const float4 *>(pa + d0), a1 = *reinterpret_cast<const float4 *>(pa + d0 + 4);
+            const float4 b0 = *reinterpret_cast<const float4 *>(pb + d0), b1 = *reinterpret_cast<const float4 *>(pb + d0 + 4);
+            va[0] = a0.x; va[1] = a0.y; va[2] = a0.z; va[3] = a0.w; va[4] = a1.x; va[5] = a1.y; va[6] = a1.z; va[7] = a1.w;
+            vb[0] = b0.x; vb[1] = b0.y; vb[2] = b0.z; vb[3] = b0.w; vb[4] = b1.x; vb[5] = b1.y; vb[6] = b1.z; vb[7] = b1.w;
+        } else {
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int d = d0 + lq * 8 + u;
+                va[u] = d < E ? pa[d0 + u] : 0.0f;
+                vb[u] = d < E ? pb[d0 + u] : 0.0f;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            As[lq * 8 + u][lr] = va[u];
+            Bs[lq * 8 + u][lr] = vb[u];
+        }
+        __syncthreads();
+        const int dn = min(DG_SLAB, E - d0);
+        for (int dd = 0; dd < dn; dd++) {
+            const float4 a = *reinterpret_cast<const float4 *>(&As[dd][ty * 4]);
+            const float4 b = *reinterpret_cast<const float4 *>(&Bs[dd][tx * 4]);
+            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = acc[i][j] + av[i] * bv[j];
+        }
+    }
+    float * G = dw.G + (long long)slot * dw.cap * dw.cap;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int r = ti * DG_TILE + ty * 4 + i;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int q = tj * DG_TILE + tx * 4 + j;
+            if (r < C && q < C) {
+                G[(long long)r * dw.cap + q] = acc[i][j];
+                G[(long long)q * dw.cap + r] = acc[i][j];
+            }
+        }
+    }
+}
+
+// order-preserving key of a float score (NaN never reaches it)
+__device__ __forceinline__ unsigned score_key(float x) {
+    const unsigned b = __float_as_uint(x);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// The greedy pass of one unit, one wave; candidate position p sits in lane
+// p % 64, slot p / 64. grid (units).
+constexpr int DIV_SLOTS = DIV_MAX_CAND / 64;
+
+__global__ void __launch_bounds__(64)
+k_div_greedy(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ gimp, DivWork dw,
+             const int * __restrict__ cand_all, int * __restrict__ sel) {
+    const int unit = blockIdx.x;
+    const int slot_g = dw.gslot[unit];
+    if (slot_g < 0 || dw.state[unit] != DIV_PENDING) return;
+    const int layer = unit / g.n_chunks, c_idx = unit % g.n_chunks;
+    const ChunkDesc c = chunks[c_idx];
+    const int lane = threadIdx.x;
+    const int pc = min(c.prefix, c.tc);
+    const int need = c.tc - pc;
+    const int C = dw.count[unit];
+    const float s = dw.strength, maxnc = dw.maxnc[unit];
+    const float * im = gimp + (long long)layer * g.T + c.start;
+    const int * cand = cand_all + (long long)unit * g.Tc_max;
+    const float * G = dw.G + (long long)slot_g * dw.cap * dw.cap;
+    __shared__ unsigned char taken[DIV_MAX_CAND];   // by candidate position
+    float imp[DIV_SLOTS], pen[DIV_SLOTS], sqn[DIV_SLOTS];
+    unsigned live = 0;   // bit k: slot k holds an unused candidate
+#pragma unroll
+    for (int k = 0; k < DIV_SLOTS; k++) {
+        const int p = lane + 64 * k;
+        const bool v = p < C;
+        imp[k] = v ? im[cand[p]] : 0.0f;
+        sqn[k] = v ? sqrtf(G[(long long)p * dw.cap + p]) : 0.0f;
+        pen[k] = 0.0f;
+        if (v) live |= 1u << k;
+        taken[p] = 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    int state = DIV_DONE;
+    for (int step = 0; step < need; step++) {
+        float bs = -1e30f;
+        int bp = -1;
+#pragma unroll
+        for (int k = 0; k < DIV_SLOTS; k++) {
+            if (live & (1u << k)) {
+                const float sc = imp[k] * (1.0f - s * pen[k]);
+                if (sc > bs) { bs = sc; bp = lane + 64 * k; }
+            }
+        }
+        const unsigned kmax = dpp_reduce_u32<true>(bp >= 0 ? score_key(bs) : 0u);
+        const unsigned pmin = dpp_reduce_u32<false>((bp >= 0 && score_key(bs) == kmax) ? (unsigned)bp : 0xffffffffu);
+        if (pmin == 0xffffffffu) { state = DIV_SHORT; break; }
+        const int b = (int)pmin;
+        const float best = __shfl(bs, b & 63);
+        // a pruned key could have won only if its importance reaches the pick's score
+        if (!(best > maxnc)) { state = DIV_RETRY; break; }
+        if (lane == (b & 63)) {
+            live &= ~(1u << (b >> 6));
+            taken[b] = 1;
+        }
+        const float nsel = sqrtf(G[(long long)b * dw.cap + b]) + 1e-8f;
+        const float * Gb = G + (long long)b * dw.cap;
+#pragma unroll
+        for (int k = 0; k < DIV_SLOTS; k++) {
+            if (live & (1u << k)) {
+                const float cs = Gb[lane + 64 * k] / (nsel * sqn[k] + 1e-8f);
+                if (cs > pen[k]) pen[k] = cs;
+            }
+        }
+    }
+    if (lane == 0) dw.state[unit] = state;
+    if (state != DIV_DONE) return;
+    __builtin_amdgcn_wave_barrier();
+    // kept positions ascending: the prefix, then the picks in position order
+    int * out = sel + (long long)layer * g.t_total + c.off;
+    for (int j = lane; j < pc; j += 64) out[j] = c.start + j;
+    int base = pc;
+    for (int p0 = 0; p0 < C; p0 += 64) {
+        const int p = p0 + lane;
+        const int f = (p < C) ? (int)taken[p] : 0;
+        const unsigned long long m = __ballot(f);
+        if (f) out[base + __popcll(m & ((1ull << lane) - 1ull))] = c.start + cand[p];
+        base += __popcll(m);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Least-squares system per (chunk, head): X = softmax_rows(S[:, sel] + beta)
 // (api.cpp:833-840); aug = [X^T X + ridge I | X^T Y] (math.h:465-504),
@@ -617,26 +934,6 @@ __device__ __forceinline__ void rg_pivot_values(const float (&a)[RG_SLOTS][RG_ST
     else if (slot == 1) rg_lane_strip<1>(a, src, sp);
     else if (slot == 2) rg_lane_strip<2>(a, src, sp);
     else rg_lane_strip<3>(a, src, sp);
-}
-
-// Wave-wide max / min of a 32-bit unsigned value through DPP row shifts and
-// row broadcasts (the result collects in lane 63); both operations are
-// idempotent, so lanes whose DPP source is out of range keep their own value.
-template <bool MAX>
-__device__ __forceinline__ unsigned dpp_reduce_u32(unsigned x) {
-#define KVC_DPP_STEP(ctrl, rmask)                                                                  \
-    {                                                                                              \
-        const unsigned t = (unsigned)__builtin_amdgcn_update_dpp((int)x, (int)x, ctrl, rmask, 0xf, false); \
-        x = MAX ? (t > x ? t : x) : (t < x ? t : x);                                               \
-    }
-    KVC_DPP_STEP(0x111, 0xf)   // row_shr:1
-    KVC_DPP_STEP(0x112, 0xf)   // row_shr:2
-    KVC_DPP_STEP(0x114, 0xf)   // row_shr:4
-    KVC_DPP_STEP(0x118, 0xf)   // row_shr:8
-    KVC_DPP_STEP(0x142, 0xa)   // row_bcast:15
-    KVC_DPP_STEP(0x143, 0xc)   // row_bcast:31
-#undef KVC_DPP_STEP
-    return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
 }
 
 struct LuShared {
@@ -1414,9 +1711,20 @@ void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStr
                        g, w.chunks, w.A, V, w.Y);
 }
 
-void launch_select_topk(const Geom & g, const Work & w, hipStream_t st) {
+void launch_global_importance(const Geom & g, const Work & w, hipStream_t st) {
     hipLaunchKernelGGL(k_global_importance, dim3(g.n_chunks, g.L), dim3(256), 0, st,
                        g, w.chunks, w.imp, w.wts, w.gimp);
+}
+
+void launch_div_level(const Geom & g, const Work & w, const DivWork & dw, const float * K, hipStream_t st) {
+    const unsigned units = (unsigned)(g.L * g.n_chunks);
+    const int nt = cdiv(dw.cap, DG_TILE);
+    hipLaunchKernelGGL(k_div_candidates, dim3(g.n_chunks, g.L), dim3(256), 0, st, g, w.chunks, w.gimp, dw, w.cand);
+    hipLaunchKernelGGL(k_div_gram, dim3(units, nt * (nt + 1) / 2), dim3(256), 0, st, g, w.chunks, K, dw, w.cand);
+    hipLaunchKernelGGL(k_div_greedy, dim3(units), dim3(64), 0, st, g, w.chunks, w.gimp, dw, w.cand, w.sel);
+}
+
+void launch_select_topk(const Geom & g, const Work & w, hipStream_t st) {
     const size_t lds = (size_t)g.Tc_max * (sizeof(float) + sizeof(int) + 1);
     const int lds_ok = lds <= 60 * 1024 ? 1 : 0;
     hipLaunchKernelGGL(k_select_topk, dim3(g.n_chunks, g.L), dim3(256), lds_ok ? lds : 0, st,

@@ -161,3 +161,62 @@ CASES = [
 ]
 
 CASE_BY_NAME = {c["name"]: c for c in CASES}
+
+
+# --------------------------------------------------------------------------
+# Diversity-selection variants (api.cpp:175-233): shapes and data that push
+# the GPU's candidate pruning through each of its levels.
+# --------------------------------------------------------------------------
+
+def diversity_variant_names():
+    return (["llama_chunk"] + [f"strength_{s}" for s in (0.0, 0.2, 0.8, 0.999, 1.0, 1.7, -0.5)] +
+            ["near_dup", "dup_rows", "rkv_negative", "rkv_span_div"] +
+            [f"prefix_{p}" for p in (100, 256, 400)] + ["cheap_unchunked"])
+
+
+def diversity_variant(name: str):
+    """Return (case, K, V, Q or None, n_q) for a diversity variant."""
+    if name == "llama_chunk":   # H=8, d=128: 1024-wide key rows, chunks of 1280 keeping 256
+        c = dict(name=name, T=4096, H=8, d=128, seed=31, params=dict(target_ratio=0.2, use_diversity=1))
+        K, V = kv_cache(4096, 8, 128, 31, channel_scale=True)
+        return c, K, V, snapkv_queries(K, 32, 31), 32
+    if name.startswith("strength_"):   # s >= 1 and s < 0 disable pruning
+        s = float(name.split("_", 1)[1])
+        c = dict(name=name, T=1536, H=2, d=64, seed=32,
+                 params=dict(target_ratio=0.2, use_diversity=1, diversity_strength=s))
+        K, V = kv_cache(1536, 2, 64, 32, channel_scale=True)
+        return c, K, V, snapkv_queries(K, 32, 32), 32
+    if name == "near_dup":   # one shared row + 1% noise: cosines near 1
+        T, H, d = 1280, 2, 64
+        base = normal(3301, (1, H * d))
+        K = np.ascontiguousarray((base + np.float32(0.01) * normal(3302, (T, H * d))).astype(np.float32))
+        V = normal(3303, (T, H * d))
+        Q = np.ascontiguousarray((K[-16:] + np.float32(0.5) * normal(3304, (16, H * d))).astype(np.float32))
+        c = dict(name=name, T=T, H=H, d=d, seed=33, params=dict(target_ratio=0.2, use_diversity=1))
+        return c, K, V, Q, 16
+    if name == "dup_rows":   # every key row four times: importance and cosine ties
+        T, H, d = 1024, 2, 32
+        K0, _ = kv_cache(T // 4, H, d, 34)
+        K = np.ascontiguousarray(np.repeat(K0, 4, axis=0))
+        V, _ = kv_cache(T, H, d, 35)
+        c = dict(name=name, T=T, H=H, d=d, seed=34, params=dict(target_ratio=0.25, use_diversity=1))
+        return c, K, V, normal(3401, (12, H * d)), 12
+    if name in ("rkv_negative", "rkv_span_div"):   # negative weights disable pruning
+        w = -0.5 if name == "rkv_negative" else 0.3
+        seed = 36 if name == "rkv_negative" else 37
+        c = dict(name=name, T=2560, H=2, d=32, seed=seed, rkv=dict(thinking=w, transition=0.7),
+                 params=dict(target_ratio=0.2, use_diversity=1))
+        K, V = kv_cache(2560, 2, 32, seed, channel_scale=True)
+        return c, K, V, snapkv_queries(K, 16, seed), 16
+    if name.startswith("prefix_"):   # prefix below, at and above chunk 0's kept count
+        p = int(name.split("_", 1)[1])
+        c = dict(name=name, T=2000, H=2, d=32, seed=38,
+                 params=dict(target_ratio=0.2, use_diversity=1, n_shared_prefix=p))
+        K, V = kv_cache(2000, 2, 32, 38)
+        return c, K, V, snapkv_queries(K, 16, 38), 16
+    if name == "cheap_unchunked":
+        c = dict(name=name, T=900, H=2, d=32, seed=39,
+                 params=dict(target_ratio=0.3, use_diversity=1, use_cheap_qref=1, chunk_size=-1))
+        K, V = kv_cache(900, 2, 32, 39)
+        return c, K, V, None, 0
+    raise KeyError(name)

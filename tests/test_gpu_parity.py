@@ -25,7 +25,7 @@ def bits(a):
 
 def supported(c):
     p = c["params"]
-    return (p.get("skip_beta", 1) == 1 and not p.get("use_diversity") and not p.get("refine_rounds"))
+    return p.get("skip_beta", 1) == 1 and not p.get("refine_rounds")
 
 
 @pytest.fixture(scope="module")
@@ -170,3 +170,17 @@ def test_device_batch_api(gpu, orc):
         assert np.array_equal(gi[l], b.indices)
         assert np.array_equal(bits(gc[l]), bits(b.C_v))
         assert np.float32(gs[l, 0]).view(np.uint32) == np.float32(b.stats["avg_cosine_sim"]).view(np.uint32)
+
+
+def test_mixed_chunk_sizes(gpu, orc):
+    """A shared prefix of 400 makes chunk 0 keep 400 keys (general elimination)
+    while the other chunks keep <= 256 (register LU): both solvers in one call."""
+    from kvc_harness import case_params
+    c = dict(name="mixed_chunks", T=2000, H=2, d=32, seed=40,
+             params=dict(target_ratio=0.2, n_shared_prefix=400))
+    K, V = kv_cache(2000, 2, 32, 40)
+    Q = snapkv_queries(K, 16, 40)
+    print("[case] mixed_chunks", flush=True)
+    a = gpu.compact(K, V, Q, 2000, 16, 2, 32, 32, case_params(gpu, c, 2000))
+    b = orc.compact(K, V, Q, 2000, 16, 2, 32, 32, case_params(orc, c, 2000))
+    same(a, b)

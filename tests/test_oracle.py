@@ -9,8 +9,9 @@ import hashlib
 import numpy as np
 import pytest
 
-from kvc_data import CASES, CASE_BY_NAME, kv_cache, make_case, normal, uniform
-from kvc_harness import ORACLE_SO, REF_HARNESS_SO, REF_SO, kc, load_oracle, load_ref, run_case
+from kvc_data import (CASES, CASE_BY_NAME, diversity_variant, diversity_variant_names, kv_cache, make_case,
+                      normal, uniform)
+from kvc_harness import ORACLE_SO, REF_HARNESS_SO, REF_SO, case_params, kc, load_oracle, load_ref, run_case
 from pathlib import Path
 
 GOLD = Path(__file__).resolve().parent / "golden"
@@ -91,6 +92,23 @@ def test_oracle_matches_live_reference_where_built(orc):
         a, b = run_case(orc, c, inp), run_case(ref, c, inp)
         assert np.array_equal(a.indices, b.indices)
         assert np.array_equal(bits(a.C_v), bits(b.C_v))
+
+
+@pytest.mark.parametrize("name", diversity_variant_names())
+def test_oracle_diversity_variants_match_live_reference(orc, name):
+    """The diversity variants the GPU tests use, oracle vs the compiled reference."""
+    ref = load_ref()
+    if ref is None:
+        pytest.skip("reference not compiled here (oracle/_ref)")
+    c, K, V, Q, nq = diversity_variant(name)
+    T, H, d = c["T"], c["H"], c["d"]
+    a = orc.compact(K, V, Q, T, nq, H, d, d, case_params(orc, c, T))
+    b = ref.compact(K, V, Q, T, nq, H, d, d, case_params(ref, c, T))
+    assert a.t == b.t
+    assert np.array_equal(a.indices, b.indices)
+    assert np.array_equal(bits(a.C_v), bits(b.C_v))
+    for k in ("avg_cosine_sim", "avg_mse", "avg_agreement"):
+        assert np.float32(a.stats[k]).view(np.uint32) == np.float32(b.stats[k]).view(np.uint32), k
 
 
 # ---------------------------------------------------------------- blocks ---
