@@ -3,9 +3,10 @@
 
 Workload (the headline configuration): a Llama-3-8B-shaped KV cache of
 32 layers x 8 KV heads x head_dim 128 at T = 100,000 tokens, fp32, compacted
-to 20% retention (t = 20,000 kept per layer) with the default parameters
-(RMS importance, skip_beta = 1, auto chunking: 79 chunks of 1280 tokens,
-256 kept per chunk). Keys ~ N(0,1) times a per-(layer, channel) scale drawn
+to 20% retention (t = 20,000 kept per layer) with diversity selection on
+(strength 0.5) and otherwise default parameters (RMS importance,
+skip_beta = 1, auto chunking: 79 chunks of 1280 tokens, 256 kept per chunk).
+The same data is also timed with diversity off ("other_mode"). Keys ~ N(0,1) times a per-(layer, channel) scale drawn
 from LogNormal(0, 0.5); values ~ N(0,1); SnapKV reference queries = the last
 32 keys + N(0, 0.1^2) noise. Synthetic data, generated once on the host and
 resident in HBM before the timed region.
@@ -41,10 +42,12 @@ import kvcompact as kc  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_PEAK_TFLOPS = 157.3       # MI355X fp32
-STAGES = ["scores", "chunk_softmax_importance", "refit_target", "selection", "compacted_softmax",
+STAGES = ["scores", "chunk_softmax_importance", "refit_target", "selection", "beta_fit", "compacted_softmax",
           "normal_equations", "lu_factorization", "substitution", "quality_stats"]
 STAGE_KERNELS = {"scores": "k_scores", "chunk_softmax_importance": "k_softmax_importance",
-                 "refit_target": "k_refit_target", "selection": "k_global_importance + k_select_topk",
+                 "refit_target": "k_refit_target",
+                 "selection": "k_global_importance + k_select_topk (or k_div_candidates + k_div_gram + k_div_greedy)",
+                 "beta_fit": "k_gather_exp + k_ls_build + k_ge_lu + k_ge_solve (or k_nnls_lh) + k_beta_log",
                  "compacted_softmax": "k_ls_softmax", "normal_equations": "k_ls_build",
                  "lu_factorization": "k_ge_lu", "substitution": "k_ge_solve",
                  "quality_stats": "k_scores + k_row_softmax + k_stats_sum + k_stats_final"}
@@ -85,6 +88,7 @@ def stage_model(L, T, H, d, nq, t, n_chunks, tc):
         "chunk_softmax_importance": dict(bytes=4 * L * H * nq * T * 2 + 4 * L * H * T, flops=0),
         "refit_target": dict(bytes=4 * L * H * nq * T + 4 * L * T * E, flops=2 * L * H * nq * T * d),
         "selection": dict(bytes=4 * L * H * T + 4 * L * t, flops=0),
+        "beta_fit": dict(bytes=0, flops=0),
         "compacted_softmax": dict(bytes=4 * L * H * nq * t * 2, flops=0),
         "normal_equations": dict(bytes=4 * units * n * (n + p), flops=2 * nq * units * n * (n + p)),
         "lu_factorization": dict(bytes=4 * units * 2 * n * n, flops=units * lu),
@@ -140,7 +144,10 @@ def main():
     ap.add_argument("--dim", type=int, default=128)
     ap.add_argument("--ratio", type=float, default=0.2)
     ap.add_argument("--window", type=int, default=32)
-    ap.add_argument("--diversity", type=int, default=0)
+    ap.add_argument("--diversity", type=int, default=1,
+                    help="1 (default): diversity selection on, the headline mode; the other mode is "
+                         "timed after it and reported under 'other_mode'")
+    ap.add_argument("--one-mode", action="store_true", help="time only the --diversity mode")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--seed", type=int, default=1234)
     a = ap.parse_args()
@@ -180,32 +187,39 @@ def main():
     st = hiprt.DevBuf(L * 3 * 4)
     out = kc.DeviceOut(idx.value, beta.value, cv.value, st.value)
 
-    def step():
-        rc = dll.kvc_compact_layers_device(dK.value, dV.value, dQ.value, L, T, W, H, d, d, T * E, T * E, W * E,
-                                           ctypes.byref(p), None, ctypes.byref(out), None)
-        if rc != 0:
-            raise RuntimeError(f"kvc_compact_layers_device returned {rc}")
+    def timed(params, tag):
+        """warmup, then exactly a.steps timed calls bracketed by device syncs"""
+        def step():
+            rc = dll.kvc_compact_layers_device(dK.value, dV.value, dQ.value, L, T, W, H, d, d, T * E, T * E,
+                                               W * E, ctypes.byref(params), None, ctypes.byref(out), None)
+            if rc != 0:
+                raise RuntimeError(f"kvc_compact_layers_device returned {rc}")
 
-    stage_acc = np.zeros(len(STAGES))
-    buf = (ctypes.c_float * len(STAGES))()
-    for i in range(a.warmup):
-        ts = time.perf_counter()
-        step()
-        print(f"[bench] warmup {i}: {(time.perf_counter() - ts) * 1e3:.1f} ms", file=sys.stderr, flush=True)
-    hiprt.synchronize()
-    times = []
-    t_start = time.perf_counter()
-    for i in range(a.steps):
-        ts = time.perf_counter()
-        step()
-        times.append(time.perf_counter() - ts)
-        dll.kvc_stage_times(buf, len(STAGES))
-        stage_acc += np.array(buf[:])
-        print(f"[bench] step {i}: {times[-1] * 1e3:.1f} ms", file=sys.stderr, flush=True)
-    hiprt.synchronize()
-    total = time.perf_counter() - t_start
-    ms = total / a.steps * 1e3
-    stage_ms = stage_acc / a.steps
+        acc = np.zeros(len(STAGES))
+        buf = (ctypes.c_float * len(STAGES))()
+        for i in range(a.warmup):
+            ts = time.perf_counter()
+            step()
+            print(f"[bench] {tag} warmup {i}: {(time.perf_counter() - ts) * 1e3:.1f} ms", file=sys.stderr, flush=True)
+        hiprt.synchronize()
+        t_start = time.perf_counter()
+        for i in range(a.steps):
+            ts = time.perf_counter()
+            step()
+            dll.kvc_stage_times(buf, len(STAGES))
+            acc += np.array(buf[:])
+            print(f"[bench] {tag} step {i}: {(time.perf_counter() - ts) * 1e3:.1f} ms", file=sys.stderr, flush=True)
+        hiprt.synchronize()
+        return (time.perf_counter() - t_start) / a.steps * 1e3, acc / a.steps
+
+    other = None
+    if not a.one_mode:
+        p_other = lib.params(target_ratio=a.ratio, use_diversity=0 if a.diversity else 1)
+        ms_o, stage_o = timed(p_other, "diversity " + ("off" if a.diversity else "on"))
+        other = {"diversity": "off" if a.diversity else "on", "value": round(T / (ms_o / 1e3), 1),
+                 "ms_per_step": round(ms_o, 3),
+                 "stage_ms": {k: round(float(v), 3) for k, v in zip(STAGES, stage_o)}}
+    ms, stage_ms = timed(p, "diversity " + ("on" if a.diversity else "off"))
     model = stage_model(L, T, H, d, W, t, n_chunks, 256 if n_chunks > 1 else t)
     dom = STAGES[int(np.argmax(stage_ms))]
     roof = roofline(dom, model, float(stage_ms[int(np.argmax(stage_ms))]))
@@ -238,6 +252,7 @@ def main():
             "parallelism": "single GPU", "device": hiprt.device_name(),
         },
         "stage_ms": {k: round(float(v), 3) for k, v in zip(STAGES, stage_ms)},
+        "other_mode": other,
         "roofline": roof,
         "cpu_baseline": cpu,
         "speedup_vs_cpu": round((T / (ms / 1e3)) / cpu["value"], 1) if cpu else None,

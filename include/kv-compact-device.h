@@ -54,9 +54,9 @@ int kvc_compact_quantized_device(const uint8_t * K_quant, const uint8_t * V_quan
 /* Device time in ms of each pipeline stage of the last call on the current
  * device, measured with HIP events on that call's stream. Stages, in order:
  * 0 scores, 1 chunk softmax + importance, 2 refit target Y = A V,
- * 3 selection, 4 compacted softmax X, 5 normal equations, 6 LU elimination
- * with partial pivoting, 7 forward + back substitution, 8 quality
- * statistics. Returns the number written. */
+ * 3 selection, 4 beta fit, 5 compacted softmax X, 6 normal equations,
+ * 7 LU elimination with partial pivoting, 8 forward + back substitution,
+ * 9 quality statistics. Returns the number written. */
 int kvc_stage_times(float * out_ms, int n);
 
 /* Release the library's cached device workspace of the current device. */

@@ -40,6 +40,7 @@ struct Geom {
     int score_method;           // 0 max, 1 rms, 2 mean
     float inv_sqrt_dk;
     float ridge;
+    float zero_val;             // solution value of a skipped pivot (0 for C_v, eps for the beta weights)
 };
 
 // Device scratch for one batch (all pointers device memory).
@@ -64,6 +65,7 @@ struct Work {
     int   * cand;     // [L][n_chunks][Tc_max] selection candidates
     unsigned char * flags; // [L][n_chunks][Tc_max]
     float * wts;      // [T] R-KV weights (nullptr when disabled)
+    int   * status;   // [1] nonzero: a kernel met a case this build refuses
     ChunkDesc * chunks;  // [n_chunks + 2]; then all T keys, then the kept keys (statistics)
 };
 

@@ -35,8 +35,8 @@ namespace {
 // ------------------------------------------------------------------ device
 
 // Pipeline stages timed with events on the call's stream (kvc_stage_times)
-enum Stage { ST_SCORES, ST_SOFTMAX, ST_REFIT, ST_SELECT, ST_LS_SOFTMAX, ST_LS_BUILD, ST_LU, ST_SOLVE, ST_STATS,
-             ST_COUNT };
+enum Stage { ST_SCORES, ST_SOFTMAX, ST_REFIT, ST_SELECT, ST_BETA, ST_LS_SOFTMAX, ST_LS_BUILD, ST_LU, ST_SOLVE,
+             ST_STATS, ST_COUNT };
 
 struct DeviceCtx {
     std::mutex mu;
@@ -250,7 +250,7 @@ void make_plan(int T, int n_q, bool q_given, const kv_compact_params & p, Plan &
 // rather than computed differently.
 int check_supported(const kv_compact_params & p, int d_v) {
     if (p.use_omp || p.use_sensitivity) return KV_COMPACT_E_UNSUPPORTED;
-    if (!p.skip_beta) return KV_COMPACT_E_UNSUPPORTED;
+    if (!p.skip_beta && p.nnls_method != 0 && p.nnls_pgd_iters > 0) return KV_COMPACT_E_UNSUPPORTED;
     if (p.refine_rounds > 0) return KV_COMPACT_E_UNSUPPORTED;
     if (d_v > 256) return KV_COMPACT_E_UNSUPPORTED;
     return 0;
@@ -323,6 +323,7 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     ww.cand = cv.take<int>(L * nc * (size_t)pl.Tc_max);
     ww.flags = cv.take<unsigned char>(L * nc * (size_t)pl.Tc_max);
     ww.chunks = cv.take<ChunkDesc>(pl.chunks.size());
+    ww.status = cv.take<int>(1);
     if (div) {
         const size_t units = L * nc;
         DivWork d{};
@@ -435,6 +436,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     if (hipMemcpyAsync(w.aug_off, aug_off.data(), aug_off.size() * sizeof(long long),
                        hipMemcpyHostToDevice, st) != hipSuccess) return KV_COMPACT_E_DEVICE;
 
+    if (hipMemsetAsync(w.status, 0, sizeof(int), st) != hipSuccess) return KV_COMPACT_E_DEVICE;
     hipEvent_t * ev = ctx->ev;
     (void)hipEventRecord(ev[0], st);
     // 1. scores for every (layer, chunk, head)
@@ -456,19 +458,43 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         launch_select_topk(g, w, st);
     }
     (void)hipEventRecord(ev[ST_SELECT + 1], st);
-    // 5. beta (skip_beta: zeros), X = softmax(S[:, sel] + beta)
-    if (hipMemsetAsync(io.beta, 0, (size_t)io.L * io.H * pl.t_total * sizeof(float), st) != hipSuccess)
-        return KV_COMPACT_E_DEVICE;
+    // 5. beta: zeros (skip_beta), or the NNLS mass fit on the exp scores
+    //    (api.cpp:812-831): M = exp_scores[:, sel], b = row sums
+    if (p.skip_beta) {
+        if (hipMemsetAsync(io.beta, 0, (size_t)io.L * io.H * pl.t_total * sizeof(float), st) != hipSuccess)
+            return KV_COMPACT_E_DEVICE;
+    } else {
+        launch_gather_exp(g, w, st);   // M into the X buffer
+        Geom gb = g;
+        gb.dv = 1;
+        gb.zero_val = 1e-12f;
+        Work wb = w;
+        wb.Y = w.rowsum;
+        if (p.nnls_method == 0) {
+            if (pl.tc_max > 256) return KV_COMPACT_E_UNSUPPORTED;
+            gb.ridge = 0.0f;   // Lawson-Hanson adds its own 1e-10 to each sub-problem
+            launch_ls_build(gb, wb, st);
+            launch_nnls_lh(gb, wb, io.beta, p.nnls_max_iter, w.status, st);
+        } else {
+            gb.ridge = 1e-10f;   // clamped unconstrained LS, math.h:707-745
+            launch_ls_build(gb, wb, st);
+            launch_ge_lu(gb, wb, st);
+            launch_ge_solve(gb, wb, io.beta, st);
+        }
+        launch_beta_log(io.beta, (long long)io.L * io.H * pl.t_total, st);
+    }
+    (void)hipEventRecord(ev[ST_BETA + 1], st);
+    // 6. X = softmax(S[:, sel] + beta)
     launch_ls_softmax(g, w, io.beta, st);
     (void)hipEventRecord(ev[ST_LS_SOFTMAX + 1], st);
-    // 6. normal equations and their solution
+    // 7. normal equations and their solution
     launch_ls_build(g, w, st);
     (void)hipEventRecord(ev[ST_LS_BUILD + 1], st);
     launch_ge_lu(g, w, st);
     (void)hipEventRecord(ev[ST_LU + 1], st);
     launch_ge_solve(g, w, io.Cv, st);
     (void)hipEventRecord(ev[ST_SOLVE + 1], st);
-    // 7. quality statistics against the full call
+    // 8. quality statistics against the full call
     launch_stats(g, w, sw, io.K, io.V, io.Q, io.beta, io.Cv, io.stats, st);
     (void)hipEventRecord(ev[ST_STATS + 1], st);
 
@@ -478,6 +504,9 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         fprintf(stderr, "[kv-compact] HIP error: %s\n", hipGetErrorString(err));
         return KV_COMPACT_E_DEVICE;
     }
+    int status = 0;
+    if (hipMemcpy(&status, w.status, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return KV_COMPACT_E_DEVICE;
+    if (status) return KV_COMPACT_E_UNSUPPORTED;
     for (int i = 0; i < ST_COUNT; i++) {
         float ms = 0.0f;
         (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
@@ -485,7 +514,8 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     }
     if (tm) {
         tm->scoring_ms = ctx->stage_ms[ST_SCORES] + ctx->stage_ms[ST_SOFTMAX] + ctx->stage_ms[ST_SELECT];
-        tm->nnls_ms = ctx->stage_ms[ST_REFIT] + ctx->stage_ms[ST_LS_SOFTMAX] + ctx->stage_ms[ST_LS_BUILD] +
+        tm->nnls_ms = ctx->stage_ms[ST_REFIT] + ctx->stage_ms[ST_BETA] + ctx->stage_ms[ST_LS_SOFTMAX] +
+                      ctx->stage_ms[ST_LS_BUILD] +
                       ctx->stage_ms[ST_LU] + ctx->stage_ms[ST_SOLVE];
     }
     return 0;

@@ -16,6 +16,9 @@ void launch_global_importance(const Geom & g, const Work & w, hipStream_t st);
 void launch_select_topk(const Geom & g, const Work & w, hipStream_t st);
 void launch_div_level(const Geom & g, const Work & w, const DivWork & dw, const float * K, hipStream_t st);
 void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st);
+void launch_gather_exp(const Geom & g, const Work & w, hipStream_t st);
+void launch_nnls_lh(const Geom & g, const Work & w, float * wout, int max_iter, int * status, hipStream_t st);
+void launch_beta_log(float * wb, long long n, hipStream_t st);
 void launch_ls_build(const Geom & g, const Work & w, hipStream_t st);
 void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st);
 void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st);

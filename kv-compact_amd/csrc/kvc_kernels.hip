@@ -51,6 +51,49 @@ __device__ __forceinline__ float expf_ref(float x) {
     return (float)(y * s);
 }
 
+// ---------------------------------------------------------------------------
+// logf as glibc computes it on x86-64 (FMA variant of the ARM optimized-
+// routines method): x = 2^k * z with z in [0x1.66p-1, 0x1.66p0), 16
+// subintervals with a tabulated c ~ 1/invc and log(c), then
+// log(x) = k ln2 + log(c) + log1p(r), r = z*invc - 1, with a cubic in double.
+// Verified against libm logf over every non-negative finite float (the beta
+// weights are >= 1e-12). Only finite positive normal inputs reach it here.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float logf_ref(float x) {
+    const double ln2 = 0x1.62e42fefa39efp-1;
+    const double a0 = -0x1.00ea348b88334p-2, a1 = 0x1.5575b0be00b6ap-2, a2 = -0x1.ffffef20a4123p-2;
+    const double invc_t[16] = {
+        0x1.661ec79f8f3bep+0, 0x1.571ed4aaf883dp+0, 0x1.49539f0f010bp+0, 0x1.3c995b0b80385p+0,
+        0x1.30d190c8864a5p+0, 0x1.25e227b0b8eap+0, 0x1.1bb4a4a1a343fp+0, 0x1.12358f08ae5bap+0,
+        0x1.0953f419900a7p+0, 0x1p+0, 0x1.e608cfd9a47acp-1, 0x1.ca4b31f026aap-1,
+        0x1.b2036576afce6p-1, 0x1.9c2d163a1aa2dp-1, 0x1.886e6037841edp-1, 0x1.767dcf5534862p-1};
+    const double logc_t[16] = {
+        -0x1.57bf7808caadep-2, -0x1.2bef0a7c06ddbp-2, -0x1.01eae7f513a67p-2, -0x1.b31d8a68224e9p-3,
+        -0x1.6574f0ac07758p-3, -0x1.1aa2bc79c81p-3, -0x1.a4e76ce8c0e5ep-4, -0x1.1973c5a611ccp-4,
+        -0x1.252f438e10c1ep-5, 0x0p+0, 0x1.aa5aa5df25984p-5, 0x1.c5e53aa362eb4p-4,
+        0x1.526e57720db08p-3, 0x1.bc2860d22477p-3, 0x1.1058bc8a07ee1p-2, 0x1.4043057b6ee09p-2};
+    uint32_t ix = __float_as_uint(x);
+    if (ix == 0x3f800000u) return 0.0f;
+    if (ix - 0x00800000u >= 0x7f800000u - 0x00800000u) {
+        if (ix * 2u == 0u) return -__int_as_float(0x7f800000);
+        if (ix == 0x7f800000u) return x;
+        if ((ix & 0x80000000u) || ix * 2u >= 0xff000000u) return __int_as_float(0x7fc00000);
+        ix = __float_as_uint(x * 0x1p23f) - (23u << 23);   // subnormal: normalise
+    }
+    const uint32_t tmp = ix - 0x3f330000u;
+    const int i = (int)((tmp >> 19) % 16u);
+    const int k = (int)tmp >> 23;
+    const uint32_t iz = ix - (tmp & 0xff800000u);
+    const double z = (double)__uint_as_float(iz);
+    const double r = __builtin_fma(z, invc_t[i], -1.0);
+    const double y0 = __builtin_fma((double)k, ln2, logc_t[i]);
+    const double r2 = r * r;
+    double y = __builtin_fma(a1, r, a2);
+    y = __builtin_fma(a0, r2, y);
+    y = __builtin_fma(y, r2, y0 + r);
+    return (float)y;
+}
+
 // cheap reference-query row (api.cpp:140-151): quadratic spacing over n rows
 __device__ __forceinline__ int cheap_pos(int qi, int n, int T) {
     float f = (float)(qi + 1) / (float)(n + 1);
@@ -855,6 +898,231 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
     }
 }
 
+// beta fit input (api.cpp:812-831): M[k][j] = exp_scores[k][sel[j]] per
+// (chunk, head), written in the compacted-softmax layout [L][H][nq][t_total]
+__global__ void __launch_bounds__(256)
+k_gather_exp(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ E,
+             const int * __restrict__ sel, float * __restrict__ M) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const float * Eh = E + layer * lS(g) + h * hS(g);
+    const int * sl = sel + (long long)layer * g.t_total + c.off;
+    const long long hsX = (long long)g.nq_max * g.t_total;
+    float * Mh = M + (long long)layer * g.H * hsX + h * hsX + c.off;
+    for (int e = threadIdx.x; e < c.nq * c.tc; e += blockDim.x) {
+        const int k = e / c.tc, j = e % c.tc;
+        Mh[(long long)k * g.t_total + j] = Eh[(long long)k * g.T + sl[j]];
+    }
+}
+
+// beta = logf(max(1e-12, w)) after the solvers' final clamp w < 1e-12 -> 1e-12
+// (math.h:449-451, math.h:755-757, api.cpp:829); std::max keeps 1e-12 for NaN
+__global__ void __launch_bounds__(256)
+k_beta_log(float * __restrict__ wb, long long n) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float w = wb[i];
+    if (w < 1e-12f) w = 1e-12f;
+    const float m = (1e-12f < w) ? w : 1e-12f;
+    wb[i] = logf_ref(m);
+}
+
+// ---------------------------------------------------------------------------
+// Lawson-Hanson NNLS for the beta weights (math.h:283-452), one wave per
+// (layer, chunk, head). Input: aug = [AtA | Atb] (column-major n x (n+1), no
+// ridge). The active-set loop is the reference's, step for step: the entering
+// variable is the first largest -grad over the zero set; each inner pass
+// solves the passive-set normal equations (+1e-10 on the diagonal) by
+// Gaussian elimination with partial pivoting in LDS (rows r, r + 64 in lane r),
+// interpolates back to the boundary when infeasible, and the gradient is
+// AtA w - Atb with sequential sums. Writes w (the clamp and log follow in
+// k_beta_log). Passive sets beyond LH_PMAX set *status (the host then
+// refuses the call). n <= 256: lane l owns variables l, l+64, l+128, l+192.
+// ---------------------------------------------------------------------------
+constexpr int LH_PMAX = 128;   // passive-set capacity: rows lane and lane + 64 of the sub-problem
+
+__global__ void __launch_bounds__(64)
+k_nnls_lh(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
+          const long long * __restrict__ aug_off, float * __restrict__ wout, int max_iter, int * __restrict__ status) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const int n = c.tc;
+    const int lane = threadIdx.x;
+    float * wo = wout + ((long long)layer * g.H + h) * g.t_total + c.off;
+    if (n > 256) return;   // refused on the host
+    const float * Ag = aug + aug_off[((long long)layer * g.n_chunks + c_idx) * g.H + h];
+    __shared__ float w[256], grad[256], sv[256], atb[256];
+    __shared__ unsigned char inP[256];
+    __shared__ int pidx[LH_PMAX];
+    __shared__ float sub[LH_PMAX][LH_PMAX + 2];
+    __shared__ float sP[LH_PMAX];
+    for (int i = lane; i < 256; i += 64) {
+        const float b = i < n ? Ag[(long long)n * n + i] : 0.0f;
+        atb[i] = b;
+        w[i] = 0.0f;
+        sv[i] = 0.0f;
+        grad[i] = -b;
+        inP[i] = 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+    for (int outer = 0; outer < max_iter; outer++) {
+        // entering variable: first index of the largest -grad > 0 over the zero set
+        unsigned bk = 0u;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = lane + 64 * k;
+            if (i < n && !inP[i]) {
+                const float d = -grad[i];
+                if (d > 0.0f && __float_as_uint(d) > bk) { bk = __float_as_uint(d); bi = i; }
+            }
+        }
+        const unsigned gk = dpp_reduce_u32<true>(bk);
+        const unsigned gi = dpp_reduce_u32<false>((bk == gk && bk != 0u) ? (unsigned)bi : 0xffffffffu);
+        if (gk == 0u || __uint_as_float(gk) < 1e-10f) break;
+        const int t_idx = (int)gi;
+        if (lane == 0) inP[t_idx] = 1;
+        __builtin_amdgcn_wave_barrier();
+        for (int inner = 0; inner < max_iter; inner++) {
+            // passive set, ascending
+            int pc = 0;
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int i = lane + 64 * k;
+                const bool f = i < n && inP[i];
+                const unsigned long long m = __ballot(f);
+                const int pos = pc + __popcll(m & ((1ull << lane) - 1ull));
+                if (f && pos < LH_PMAX) pidx[pos] = i;
+                pc += __popcll(m);
+            }
+            if (pc > LH_PMAX) {
+                if (lane == 0) atomicOr(status, 1);
+                return;
+            }
+            __builtin_amdgcn_wave_barrier();
+            // sub-problem [AtA_PP + 1e-10 I | Atb_P]; rows lane and lane + 64
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const int r = lane + 64 * q;
+                if (r < pc) {
+                    const int pr = pidx[r];
+                    for (int cc = 0; cc < pc; cc++) {
+                        float v = Ag[(long long)pidx[cc] * n + pr];
+                        if (cc == r) v = v + 1e-10f;
+                        sub[r][cc] = v;
+                    }
+                    sub[r][pc] = atb[pr];
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            for (int col = 0; col < pc; col++) {
+                // pivot: first row below col of largest |a| strictly above |a[col][col]|
+                const float a0 = fabsf(sub[col][col]);
+                unsigned key = 0u;
+                int kr = 0x7fffffff;
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const int r = lane + 64 * q;
+                    if (r > col && r < pc) {
+                        const float v = fabsf(sub[r][col]);
+                        if (v > a0 && __float_as_uint(v) > key) { key = __float_as_uint(v); kr = r; }
+                    }
+                }
+                const unsigned km = dpp_reduce_u32<true>(key);
+                int mr = col;
+                if (km != 0u) mr = (int)dpp_reduce_u32<false>((key == km) ? (unsigned)kr : 0xffffffffu);
+                if (mr != col) {
+                    for (int j = lane; j <= pc; j += 64) {
+                        const float t0 = sub[col][j];
+                        sub[col][j] = sub[mr][j];
+                        sub[mr][j] = t0;
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+                const float piv = sub[col][col];
+                if (fabsf(piv) < 1e-12f) continue;
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const int r = lane + 64 * q;
+                    if (r > col && r < pc) {
+                        const float f = sub[r][col] / piv;
+                        for (int j = col; j <= pc; j++) sub[r][j] = sub[r][j] - f * sub[col][j];
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+            if (lane == 0) {
+                for (int r = 0; r < pc; r++) sP[r] = 0.0f;
+                for (int col = pc - 1; col >= 0; col--) {
+                    const float piv = sub[col][col];
+                    if (fabsf(piv) < 1e-12f) continue;
+                    float val = sub[col][pc];
+                    for (int r = col + 1; r < pc; r++) val = val - sub[col][r] * sP[r];
+                    sP[col] = val / piv;
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            for (int i = lane; i < 256; i += 64) sv[i] = 0.0f;
+            __builtin_amdgcn_wave_barrier();
+            bool infeasible = false;
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const int r = lane + 64 * q;
+                if (r < pc) {
+                    sv[pidx[r]] = sP[r];
+                    infeasible = infeasible || (sP[r] <= 0.0f);
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (__ballot(infeasible) == 0ull) {
+                for (int i = lane; i < 256; i += 64) w[i] = sv[i];
+                __builtin_amdgcn_wave_barrier();
+                break;
+            }
+            // step to the boundary, in passive-set order
+            if (lane == 0) {
+                float alpha = 1.0f;
+                for (int r = 0; r < pc; r++) {
+                    const int idx = pidx[r];
+                    if (sv[idx] <= 0.0f) {
+                        const float a = w[idx] / (w[idx] - sv[idx] + 1e-30f);
+                        if (a < alpha) alpha = a;
+                    }
+                }
+                sP[0] = alpha;
+            }
+            __builtin_amdgcn_wave_barrier();
+            const float alpha = sP[0];
+            for (int i = lane; i < n; i += 64) w[i] = w[i] + alpha * (sv[i] - w[i]);
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int q = 0; q < 2; q++) {
+                const int r = lane + 64 * q;
+                if (r < pc) {
+                    const int idx = pidx[r];
+                    if (fabsf(w[idx]) < 1e-12f) {
+                        w[idx] = 0.0f;
+                        inP[idx] = 0;
+                    }
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        // grad = AtA w - Atb, sequential over j
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int i = lane + 64 * k;
+            if (i < n) {
+                float sum = 0.0f;
+                for (int j = 0; j < n; j++) sum = sum + Ag[(long long)j * n + i] * w[j];
+                grad[i] = sum - atb[i];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    for (int i = lane; i < n; i += 64) wo[i] = w[i];
+}
+
 // one block per system; X (nq x n) and Y (nq x p) staged in (dynamic) LDS
 // when they fit its budget
 constexpr int LB_LDS_FLOATS = 24576;
@@ -1279,7 +1547,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         }
         __builtin_amdgcn_wave_barrier();
         const float piv = brow[col];
-        float val = 0.0f;
+        float val = g.zero_val;
         if (!(fabsf(piv) < 1e-12f)) {
             val = act ? yv : 0.0f;
             val = dot_seq(val, brow + col + 1, xs + (col + 1 - hb), n - col - 1, lane);
@@ -1306,7 +1574,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         }
         __builtin_amdgcn_wave_barrier();
         const float piv = brow[col];
-        float val = 0.0f;
+        float val = g.zero_val;
         if (!(fabsf(piv) < 1e-12f)) {
             val = act ? yv : 0.0f;
             val = dot_seq(val, brow + col + 1, xs + (col + 1), hb - col - 1, lane);
@@ -1410,7 +1678,7 @@ k_ge_general(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__
         prow = gtmp + sys * (long long)(2 * g.tc_max + g.dv);
         fac = prow + g.tc_max + g.dv;
     }
-    ge_solve_block(Ag, n, g.dv, x, g.dv, 0.0f, prow, fac);
+    ge_solve_block(Ag, n, g.dv, x, g.dv, g.zero_val, prow, fac);
 }
 
 // ---------------------------------------------------------------------------
@@ -1734,6 +2002,20 @@ void launch_select_topk(const Geom & g, const Work & w, hipStream_t st) {
 void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st) {
     hipLaunchKernelGGL(k_ls_softmax, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
                        g, w.chunks, w.S, w.sel, beta, w.X);
+}
+
+void launch_gather_exp(const Geom & g, const Work & w, hipStream_t st) {
+    hipLaunchKernelGGL(k_gather_exp, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st, g, w.chunks, w.E, w.sel, w.X);
+}
+
+void launch_nnls_lh(const Geom & g, const Work & w, float * wout, int max_iter, int * status, hipStream_t st) {
+    hipLaunchKernelGGL(k_nnls_lh, dim3(g.n_chunks * g.H, g.L), dim3(64), 0, st, g, w.chunks, w.aug, w.aug_off,
+                       wout, max_iter, status);
+}
+
+void launch_beta_log(float * wb, long long n, hipStream_t st) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_beta_log, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, wb, n);
 }
 
 void launch_ls_build(const Geom & g, const Work & w, hipStream_t st) {

@@ -220,3 +220,41 @@ def diversity_variant(name: str):
         K, V = kv_cache(900, 2, 32, 39)
         return c, K, V, None, 0
     raise KeyError(name)
+
+
+# --------------------------------------------------------------------------
+# Beta-fit variants (api.cpp:812-831): clamped LS (nnls_method 1) and
+# Lawson-Hanson (nnls_method 0) at chunked shapes.
+# --------------------------------------------------------------------------
+
+def beta_variant_names():
+    return ["pgd_chunk", "lh_chunk", "lh_div_rkv", "lh_cheap", "pgd_unchunked_big_t", "lh_unchunked_big_t",
+            "lh_iter_cap"]
+
+
+def beta_variant(name: str):
+    """Return (case, K, V, Q or None, n_q)."""
+    if name in ("pgd_chunk", "lh_chunk", "lh_iter_cap"):
+        m = 1 if name == "pgd_chunk" else 0
+        extra = dict(nnls_max_iter=3) if name == "lh_iter_cap" else {}
+        c = dict(name=name, T=2560, H=2, d=64, seed=41,
+                 params=dict(target_ratio=0.2, skip_beta=0, nnls_method=m, **extra))
+        K, V = kv_cache(2560, 2, 64, 41, channel_scale=True)
+        return c, K, V, snapkv_queries(K, 32, 41), 32
+    if name == "lh_div_rkv":   # the 1M-token configuration's options, without refinement
+        c = dict(name=name, T=2560, H=4, d=32, seed=42, rkv=dict(thinking=0.3, transition=0.7),
+                 params=dict(target_ratio=0.2, skip_beta=0, nnls_method=0, use_diversity=1))
+        K, V = kv_cache(2560, 4, 32, 42, channel_scale=True)
+        return c, K, V, snapkv_queries(K, 32, 42), 32
+    if name == "lh_cheap":   # 64 cheap queries per chunk
+        c = dict(name=name, T=3000, H=2, d=32, seed=43,
+                 params=dict(target_ratio=0.2, skip_beta=0, nnls_method=0, use_cheap_qref=1))
+        K, V = kv_cache(3000, 2, 32, 43)
+        return c, K, V, None, 0
+    if name in ("pgd_unchunked_big_t", "lh_unchunked_big_t"):   # t = 350 > 256
+        m = 1 if name.startswith("pgd") else 0
+        c = dict(name=name, T=700, H=1, d=32, seed=44,
+                 params=dict(target_ratio=0.5, chunk_size=-1, skip_beta=0, nnls_method=m))
+        K, V = kv_cache(700, 1, 32, 44)
+        return c, K, V, normal(4401, (16, 32)), 16
+    raise KeyError(name)

@@ -25,7 +25,7 @@ def bits(a):
 
 def supported(c):
     p = c["params"]
-    return p.get("skip_beta", 1) == 1 and not p.get("refine_rounds")
+    return not p.get("refine_rounds")
 
 
 @pytest.fixture(scope="module")
