@@ -66,6 +66,7 @@ struct Work {
     unsigned char * flags; // [L][n_chunks][Tc_max]
     float * wts;      // [T] R-KV weights (nullptr when disabled)
     int   * status;   // [1] nonzero: a kernel met a case this build refuses
+    int   * refine_active; // [L][n_chunks] 1 while the unit's refinement rounds continue
     ChunkDesc * chunks;  // [n_chunks + 2]; then all T keys, then the kept keys (statistics)
 };
 

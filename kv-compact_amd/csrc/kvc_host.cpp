@@ -36,7 +36,7 @@ namespace {
 
 // Pipeline stages timed with events on the call's stream (kvc_stage_times)
 enum Stage { ST_SCORES, ST_SOFTMAX, ST_REFIT, ST_SELECT, ST_BETA, ST_LS_SOFTMAX, ST_LS_BUILD, ST_LU, ST_SOLVE,
-             ST_STATS, ST_COUNT };
+             ST_REFINE, ST_STATS, ST_COUNT };
 
 struct DeviceCtx {
     std::mutex mu;
@@ -251,7 +251,6 @@ void make_plan(int T, int n_q, bool q_given, const kv_compact_params & p, Plan &
 int check_supported(const kv_compact_params & p, int d_v) {
     if (p.use_omp || p.use_sensitivity) return KV_COMPACT_E_UNSUPPORTED;
     if (!p.skip_beta && p.nnls_method != 0 && p.nnls_pgd_iters > 0) return KV_COMPACT_E_UNSUPPORTED;
-    if (p.refine_rounds > 0) return KV_COMPACT_E_UNSUPPORTED;
     if (d_v > 256) return KV_COMPACT_E_UNSUPPORTED;
     return 0;
 }
@@ -324,6 +323,7 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     ww.flags = cv.take<unsigned char>(L * nc * (size_t)pl.Tc_max);
     ww.chunks = cv.take<ChunkDesc>(pl.chunks.size());
     ww.status = cv.take<int>(1);
+    ww.refine_active = cv.take<int>(L * nc);
     if (div) {
         const size_t units = L * nc;
         DivWork d{};
@@ -460,10 +460,11 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     (void)hipEventRecord(ev[ST_SELECT + 1], st);
     // 5. beta: zeros (skip_beta), or the NNLS mass fit on the exp scores
     //    (api.cpp:812-831): M = exp_scores[:, sel], b = row sums
-    if (p.skip_beta) {
-        if (hipMemsetAsync(io.beta, 0, (size_t)io.L * io.H * pl.t_total * sizeof(float), st) != hipSuccess)
-            return KV_COMPACT_E_DEVICE;
-    } else {
+    auto fit_beta = [&]() -> int {
+        if (p.skip_beta) {
+            const size_t bytes = (size_t)io.L * io.H * pl.t_total * sizeof(float);
+            return hipMemsetAsync(io.beta, 0, bytes, st) == hipSuccess ? 0 : KV_COMPACT_E_DEVICE;
+        }
         launch_gather_exp(g, w, st);   // M into the X buffer
         Geom gb = g;
         gb.dv = 1;
@@ -482,7 +483,10 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
             launch_ge_solve(gb, wb, io.beta, st);
         }
         launch_beta_log(io.beta, (long long)io.L * io.H * pl.t_total, st);
-    }
+        return 0;
+    };
+    int rc = fit_beta();
+    if (rc) return rc;
     (void)hipEventRecord(ev[ST_BETA + 1], st);
     // 6. X = softmax(S[:, sel] + beta)
     launch_ls_softmax(g, w, io.beta, st);
@@ -494,6 +498,22 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     (void)hipEventRecord(ev[ST_LU + 1], st);
     launch_ge_solve(g, w, io.Cv, st);
     (void)hipEventRecord(ev[ST_SOLVE + 1], st);
+    // refinement rounds (api.cpp:851-946): swap the worst kept key for the
+    // best unused one, then refit beta and C_v (units that stopped refit to
+    // the same values)
+    if (p.refine_rounds > 0) {
+        launch_fill_int(w.refine_active, 1, (long long)io.L * pl.n_chunks, st);
+        for (int r = 0; r < p.refine_rounds; r++) {
+            launch_refine_step(g, w, st);
+            rc = fit_beta();
+            if (rc) return rc;
+            launch_ls_softmax(g, w, io.beta, st);
+            launch_ls_build(g, w, st);
+            launch_ge_lu(g, w, st);
+            launch_ge_solve(g, w, io.Cv, st);
+        }
+    }
+    (void)hipEventRecord(ev[ST_REFINE + 1], st);
     // 8. quality statistics against the full call
     launch_stats(g, w, sw, io.K, io.V, io.Q, io.beta, io.Cv, io.stats, st);
     (void)hipEventRecord(ev[ST_STATS + 1], st);
@@ -516,7 +536,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         tm->scoring_ms = ctx->stage_ms[ST_SCORES] + ctx->stage_ms[ST_SOFTMAX] + ctx->stage_ms[ST_SELECT];
         tm->nnls_ms = ctx->stage_ms[ST_REFIT] + ctx->stage_ms[ST_BETA] + ctx->stage_ms[ST_LS_SOFTMAX] +
                       ctx->stage_ms[ST_LS_BUILD] +
-                      ctx->stage_ms[ST_LU] + ctx->stage_ms[ST_SOLVE];
+                      ctx->stage_ms[ST_LU] + ctx->stage_ms[ST_SOLVE] + ctx->stage_ms[ST_REFINE];
     }
     return 0;
 }

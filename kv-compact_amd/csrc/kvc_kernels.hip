@@ -846,6 +846,108 @@ k_div_greedy(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
 }
 
 // ---------------------------------------------------------------------------
+// One refinement round's decision per (layer, chunk) (api.cpp:851-903).
+// key_value[j] = sum_h (sum_qi X_h[qi][j]^2) / n_q, X = the current compacted
+// softmax (the reference recomputes it per slot: same values). The worst slot
+// is the first minimum (slot 0 when key_value[0] is NaN); the best unused
+// position is the first maximum of the global importance above -1 among the
+// unkept ones. The round stops the unit (for good) when there is none or when
+// it is not above half the worst slot's importance; otherwise the worst kept
+// position is replaced and the kept list stays ascending. grid (n_chunks, L).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void block_argbest(unsigned key, int idx, bool want_max, unsigned & k_out, int & i_out) {
+    // best key (max or min), smallest index among equal keys; 256 threads
+    __shared__ unsigned rk[4];
+    __shared__ int ri[4];
+    unsigned k = want_max ? dpp_reduce_u32<true>(key) : dpp_reduce_u32<false>(key);
+    const unsigned i = dpp_reduce_u32<false>(key == k ? (unsigned)idx : 0xffffffffu);
+    if ((threadIdx.x & 63) == 0) { rk[threadIdx.x >> 6] = k; ri[threadIdx.x >> 6] = (int)i; }
+    __syncthreads();
+    unsigned bk = rk[0];
+    int bi = ri[0];
+    for (int wv = 1; wv < (int)(blockDim.x >> 6); wv++) {
+        const bool better = want_max ? (rk[wv] > bk) : (rk[wv] < bk);
+        if (better || (rk[wv] == bk && (unsigned)ri[wv] < (unsigned)bi)) { bk = rk[wv]; bi = ri[wv]; }
+    }
+    __syncthreads();
+    k_out = bk;
+    i_out = bi;
+}
+
+__global__ void __launch_bounds__(256)
+k_refine_step(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ X,
+              const float * __restrict__ gimp, int * __restrict__ sel, unsigned char * __restrict__ flags_all,
+              int * __restrict__ active) {
+    const int c_idx = blockIdx.x, layer = blockIdx.y;
+    const int unit = layer * g.n_chunks + c_idx;
+    if (!active[unit]) return;
+    const ChunkDesc c = chunks[c_idx];
+    const int t = c.tc, nq = c.nq, tid = threadIdx.x;
+    if (t >= c.Tc || t <= 0) {
+        if (tid == 0) active[unit] = 0;
+        return;
+    }
+    int * sl = sel + (long long)layer * g.t_total + c.off;
+    const float * gi = gimp + (long long)layer * g.T;
+    unsigned char * fl = flags_all + (long long)unit * g.Tc_max;
+    const long long hsX = (long long)g.nq_max * g.t_total;
+    // worst slot
+    unsigned wk = 0xffffffffu;
+    int wi = 0x7fffffff;
+    __shared__ int s_kv0_nan;
+    for (int j = tid; j < t; j += blockDim.x) {
+        float kv = 0.0f;
+        for (int h = 0; h < g.H; h++) {
+            const float * xh = X + (long long)layer * g.H * hsX + h * hsX + c.off + j;
+            float e = 0.0f;
+            for (int qi = 0; qi < nq; qi++) {
+                const float x = xh[(long long)qi * g.t_total];
+                e = e + x * x;
+            }
+            kv = kv + e / (float)nq;
+        }
+        if (j == 0) s_kv0_nan = (kv != kv) ? 1 : 0;
+        if (kv == kv) {
+            const unsigned k = score_key(kv);
+            if (k < wk) { wk = k; wi = j; }
+        }
+    }
+    unsigned bk;
+    int worst;
+    block_argbest(wk, wi, false, bk, worst);
+    if (s_kv0_nan || worst == 0x7fffffff) worst = 0;
+    // best unused position
+    for (int j = tid; j < c.Tc; j += blockDim.x) fl[j] = 0;
+    __syncthreads();
+    for (int k = tid; k < t; k += blockDim.x) fl[sl[k] - c.start] = 1;
+    __syncthreads();
+    unsigned uk = 0u;
+    int ui = 0x7fffffff;
+    for (int j = tid; j < c.Tc; j += blockDim.x) {
+        const float v = gi[c.start + j];
+        if (!fl[j] && v > -1.0f) {
+            const unsigned k = score_key(v);
+            if (k > uk) { uk = k; ui = j; }
+        }
+    }
+    int best;
+    block_argbest(uk, ui, true, bk, best);
+    if (tid == 0) {
+        if (bk == 0u) best = -1;
+        const int wpos = sl[worst];
+        if (best < 0 || gi[c.start + best] <= gi[wpos] * 0.5f) {
+            active[unit] = 0;
+        } else {
+            const int np = c.start + best;
+            for (int k = worst; k < t - 1; k++) sl[k] = sl[k + 1];
+            int k = t - 1;
+            while (k > 0 && sl[k - 1] > np) { sl[k] = sl[k - 1]; k--; }
+            sl[k] = np;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Least-squares system per (chunk, head): X = softmax_rows(S[:, sel] + beta)
 // (api.cpp:833-840); aug = [X^T X + ridge I | X^T Y] (math.h:465-504),
 // both sums sequential over the query index.
@@ -1997,6 +2099,21 @@ void launch_select_topk(const Geom & g, const Work & w, hipStream_t st) {
     const int lds_ok = lds <= 60 * 1024 ? 1 : 0;
     hipLaunchKernelGGL(k_select_topk, dim3(g.n_chunks, g.L), dim3(256), lds_ok ? lds : 0, st,
                        g, w.chunks, w.gimp, w.cand, w.flags, w.sel, lds_ok);
+}
+
+__global__ void __launch_bounds__(256) k_fill_int(int * __restrict__ p, int v, long long n) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+void launch_fill_int(int * p, int v, long long n, hipStream_t st) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_fill_int, dim3(cdiv(n, 256)), dim3(256), 0, st, p, v, n);
+}
+
+void launch_refine_step(const Geom & g, const Work & w, hipStream_t st) {
+    hipLaunchKernelGGL(k_refine_step, dim3(g.n_chunks, g.L), dim3(256), 0, st, g, w.chunks, w.X, w.gimp, w.sel,
+                       w.flags, w.refine_active);
 }
 
 void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st) {

@@ -258,3 +258,39 @@ def beta_variant(name: str):
         K, V = kv_cache(700, 1, 32, 44)
         return c, K, V, normal(4401, (16, 32)), 16
     raise KeyError(name)
+
+
+# --------------------------------------------------------------------------
+# Refinement-round variants (api.cpp:851-946) at chunked shapes.
+# --------------------------------------------------------------------------
+
+def refine_variant_names():
+    return ["refine3_pgd", "refine2_skipbeta_div", "cfg5_chunked", "refine_full_keep", "refine_unchunked"]
+
+
+def refine_variant(name: str):
+    """Return (case, K, V, Q or None, n_q)."""
+    if name == "refine3_pgd":
+        c = dict(name=name, T=2560, H=2, d=32, seed=51,
+                 params=dict(target_ratio=0.2, skip_beta=0, nnls_method=1, refine_rounds=3))
+        K, V = kv_cache(2560, 2, 32, 51, channel_scale=True)
+        return c, K, V, snapkv_queries(K, 16, 51), 16
+    if name == "refine2_skipbeta_div":
+        c = dict(name=name, T=2560, H=2, d=32, seed=52, params=dict(target_ratio=0.2, use_diversity=1, refine_rounds=2))
+        K, V = kv_cache(2560, 2, 32, 52, channel_scale=True)
+        return c, K, V, snapkv_queries(K, 16, 52), 16
+    if name == "cfg5_chunked":   # the 1M-token configuration's options on 4 chunks of 1280
+        c = dict(name=name, T=5120, H=4, d=32, seed=53, rkv=dict(thinking=0.3, transition=0.7),
+                 params=dict(target_ratio=0.2, skip_beta=0, nnls_method=0, use_diversity=1, refine_rounds=1))
+        K, V = kv_cache(5120, 4, 32, 53, channel_scale=True)
+        return c, K, V, snapkv_queries(K, 32, 53), 32
+    if name == "refine_full_keep":   # t == T: the rounds do nothing
+        c = dict(name=name, T=200, H=2, d=16, seed=54, params=dict(target_count=200, refine_rounds=2))
+        K, V = kv_cache(200, 2, 16, 54)
+        return c, K, V, normal(5401, (8, 32)), 8
+    if name == "refine_unchunked":
+        c = dict(name=name, T=600, H=2, d=16, seed=55,
+                 params=dict(target_ratio=0.3, chunk_size=-1, refine_rounds=4, skip_beta=0, nnls_method=0))
+        K, V = kv_cache(600, 2, 16, 55)
+        return c, K, V, normal(5501, (12, 32)), 12
+    raise KeyError(name)

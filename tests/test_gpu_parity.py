@@ -2,8 +2,7 @@
 
 Every output (kept indices, beta, C_v, the three quality statistics, the
 requantized rows) must equal the oracle's exactly: the kernels keep the
-reference's fp32 operation order. Options the library does not implement yet
-must be refused with KV_COMPACT_E_UNSUPPORTED, never computed differently.
+reference's fp32 operation order.
 """
 from __future__ import annotations
 
@@ -21,11 +20,6 @@ pytestmark = pytest.mark.gpu
 
 def bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
-
-
-def supported(c):
-    p = c["params"]
-    return not p.get("refine_rounds")
 
 
 @pytest.fixture(scope="module")
@@ -58,13 +52,6 @@ def test_case_parity(gpu, orc, name):
     c = CASE_BY_NAME[name]
     print(f"[case] {name}", flush=True)
     inp = make_case(c)
-    if not supported(c):
-        from kvc_harness import case_params
-        K, V, Q, nq = inp
-        p = case_params(gpu, c, c["T"])
-        rc, r = gpu.compact_raw(K, V, Q, c["T"], nq, c["H"], c["d"], c.get("dv", c["d"]), p)
-        assert rc == kc.E_UNSUPPORTED
-        return
     same(run_case(gpu, c, inp), run_case(orc, c, inp))
 
 

@@ -10,7 +10,8 @@ import numpy as np
 import pytest
 
 from kvc_data import (CASES, CASE_BY_NAME, beta_variant, beta_variant_names, diversity_variant,
-                      diversity_variant_names, kv_cache, make_case, normal, uniform)
+                      diversity_variant_names, kv_cache, make_case, normal, refine_variant, refine_variant_names,
+                      uniform)
 from kvc_harness import ORACLE_SO, REF_HARNESS_SO, REF_SO, case_params, kc, load_oracle, load_ref, run_case
 from pathlib import Path
 
@@ -125,6 +126,25 @@ def test_oracle_beta_variants_match_live_reference(orc, name):
     assert np.array_equal(a.indices, b.indices)
     assert np.array_equal(bits(a.beta), bits(b.beta))
     assert np.array_equal(bits(a.C_v), bits(b.C_v))
+
+
+@pytest.mark.parametrize("name", refine_variant_names())
+def test_oracle_refine_variants_match_live_reference(orc, name):
+    """The refinement variants the GPU tests use, oracle vs the compiled
+    reference; each variant but the full-keep one changes the kept set."""
+    ref = load_ref()
+    if ref is None:
+        pytest.skip("reference not compiled here (oracle/_ref)")
+    c, K, V, Q, nq = refine_variant(name)
+    T, H, d = c["T"], c["H"], c["d"]
+    a = orc.compact(K, V, Q, T, nq, H, d, d, case_params(orc, c, T))
+    b = ref.compact(K, V, Q, T, nq, H, d, d, case_params(ref, c, T))
+    assert a.t == b.t
+    assert np.array_equal(a.indices, b.indices)
+    assert np.array_equal(bits(a.beta), bits(b.beta))
+    assert np.array_equal(bits(a.C_v), bits(b.C_v))
+    z = orc.compact(K, V, Q, T, nq, H, d, d, case_params(orc, c, T, refine_rounds=0))
+    assert (name == "refine_full_keep") == np.array_equal(a.indices, z.indices)
 
 
 # ---------------------------------------------------------------- blocks ---
