@@ -43,13 +43,14 @@ import kvcompact as kc  # noqa: E402
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_PEAK_TFLOPS = 157.3       # MI355X fp32
 STAGES = ["scores", "chunk_softmax_importance", "refit_target", "selection", "beta_fit", "compacted_softmax",
-          "normal_equations", "lu_factorization", "substitution", "quality_stats"]
+          "normal_equations", "lu_factorization", "substitution", "refinement", "quality_stats"]
 STAGE_KERNELS = {"scores": "k_scores", "chunk_softmax_importance": "k_softmax_importance",
                  "refit_target": "k_refit_target",
                  "selection": "k_global_importance + k_select_topk (or k_div_candidates + k_div_gram + k_div_greedy)",
                  "beta_fit": "k_gather_exp + k_ls_build + k_ge_lu + k_ge_solve (or k_nnls_lh) + k_beta_log",
                  "compacted_softmax": "k_ls_softmax", "normal_equations": "k_ls_build",
                  "lu_factorization": "k_ge_lu", "substitution": "k_ge_solve",
+                 "refinement": "k_refine_step + the beta and C_v refit per round",
                  "quality_stats": "k_scores + k_row_softmax + k_stats_sum + k_stats_final"}
 
 
@@ -89,6 +90,7 @@ def stage_model(L, T, H, d, nq, t, n_chunks, tc):
         "refit_target": dict(bytes=4 * L * H * nq * T + 4 * L * T * E, flops=2 * L * H * nq * T * d),
         "selection": dict(bytes=4 * L * H * T + 4 * L * t, flops=0),
         "beta_fit": dict(bytes=0, flops=0),
+        "refinement": dict(bytes=0, flops=0),
         "compacted_softmax": dict(bytes=4 * L * H * nq * t * 2, flops=0),
         "normal_equations": dict(bytes=4 * units * n * (n + p), flops=2 * nq * units * n * (n + p)),
         "lu_factorization": dict(bytes=4 * units * 2 * n * n, flops=units * lu),
