@@ -156,7 +156,11 @@ typedef enum {
     KV_TYPE_F16  = 1,
     KV_TYPE_Q4_0 = 2,
     KV_TYPE_Q4_1 = 3,
-    KV_TYPE_Q8_0 = 8
+    KV_TYPE_Q8_0 = 8,
+    /* Extension, no counterpart in the reference: bfloat16 rows (ggml's
+     * value for the type). Decode is exact (the upper 16 bits of the float);
+     * encode rounds to nearest, ties to even; NaN stays a quiet NaN. */
+    KV_TYPE_BF16 = 30
 } kv_data_type;
 
 #define KV_COMPACT_BLOCK_SIZE 32

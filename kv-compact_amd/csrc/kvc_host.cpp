@@ -677,14 +677,14 @@ kv_compact_params defaults() {
 // Reference state.h:326-352 (row geometry of the codecs)
 int block_bytes(int type) {
     if (type == KV_TYPE_F32) return 4;
-    if (type == KV_TYPE_F16) return 2;
+    if (type == KV_TYPE_F16 || type == KV_TYPE_BF16) return 2;
     if (type == KV_TYPE_Q8_0) return 34;
     if (type == KV_TYPE_Q4_0) return 18;
     if (type == KV_TYPE_Q4_1) return 20;
     return 4;
 }
 bool is_block_type(int t) { return t == KV_TYPE_Q8_0 || t == KV_TYPE_Q4_0 || t == KV_TYPE_Q4_1; }
-bool known_type(int t) { return t == KV_TYPE_F32 || t == KV_TYPE_F16 || is_block_type(t); }
+bool known_type(int t) { return t == KV_TYPE_F32 || t == KV_TYPE_F16 || t == KV_TYPE_BF16 || is_block_type(t); }
 
 }  // namespace
 
@@ -884,14 +884,14 @@ int kv_compact_multi_round(const float * K_all, const float * V_all, const float
 
 int kv_quant_row_elements(int type, size_t row_bytes) {
     if (type == KV_TYPE_F32) return (int)(row_bytes / 4);
-    if (type == KV_TYPE_F16) return (int)(row_bytes / 2);
+    if (type == KV_TYPE_F16 || type == KV_TYPE_BF16) return (int)(row_bytes / 2);
     if (is_block_type(type)) return (int)(row_bytes / (size_t)block_bytes(type)) * 32;
     return (int)(row_bytes / 4);
 }
 
 size_t kv_quant_row_bytes(int type, int n_elements) {
     if (type == KV_TYPE_F32) return (size_t)n_elements * 4;
-    if (type == KV_TYPE_F16) return (size_t)n_elements * 2;
+    if (type == KV_TYPE_F16 || type == KV_TYPE_BF16) return (size_t)n_elements * 2;
     if (is_block_type(type)) return (size_t)(n_elements / 32) * (size_t)block_bytes(type);
     return (size_t)n_elements * 4;
 }

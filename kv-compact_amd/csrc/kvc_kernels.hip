@@ -1905,7 +1905,7 @@ __device__ __forceinline__ uint16_t load_u16(const uint8_t * p) { return (uint16
 __global__ void __launch_bounds__(256)
 k_dequant_rows(const uint8_t * __restrict__ src, int type, long long row_bytes, int n_el,
                long long rows, float * __restrict__ dst) {
-    const long long nb = (type == 0 || type == 1) ? (long long)n_el : (long long)(n_el / 32);
+    const long long nb = (type == 0 || type == 1 || type == 30) ? (long long)n_el : (long long)(n_el / 32);
     const long long total = rows * nb;
     for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (long long)gridDim.x * blockDim.x) {
@@ -1917,6 +1917,8 @@ k_dequant_rows(const uint8_t * __restrict__ src, int type, long long row_bytes, 
                                    ((uint32_t)s[4 * b + 2] << 16) | ((uint32_t)s[4 * b + 3] << 24));
         } else if (type == 1) {
             o[b] = f16_to_f32_ref(load_u16(s + 2 * b));
+        } else if (type == 30) {
+            o[b] = __uint_as_float((uint32_t)load_u16(s + 2 * b) << 16);
         } else if (type == 8) {
             const uint8_t * bl = s + b * 34;
             const float d = f16_to_f32_ref(load_u16(bl));
@@ -1939,11 +1941,18 @@ k_dequant_rows(const uint8_t * __restrict__ src, int type, long long row_bytes, 
     }
 }
 
+// bfloat16 encode: round to nearest, ties to even; NaN -> quiet NaN
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+    const uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
 // quantize rows gathered by index (idx == nullptr: identity), src row stride src_ld
 __global__ void __launch_bounds__(256)
 k_quant_rows(const float * __restrict__ src, long long src_ld, const int * __restrict__ idx,
              int type, int n_el, long long rows, uint8_t * __restrict__ dst, long long row_bytes) {
-    const long long nb = (type == 0 || type == 1) ? (long long)n_el : (long long)(n_el / 32);
+    const long long nb = (type == 0 || type == 1 || type == 30) ? (long long)n_el : (long long)(n_el / 32);
     const long long total = rows * nb;
     for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
          e += (long long)gridDim.x * blockDim.x) {
@@ -1956,6 +1965,9 @@ k_quant_rows(const float * __restrict__ src, long long src_ld, const int * __res
             o[4 * b] = u & 0xFF; o[4 * b + 1] = (u >> 8) & 0xFF; o[4 * b + 2] = (u >> 16) & 0xFF; o[4 * b + 3] = u >> 24;
         } else if (type == 1) {
             const uint16_t hv = f32_to_f16_ref(x[b]);
+            o[2 * b] = hv & 0xFF; o[2 * b + 1] = hv >> 8;
+        } else if (type == 30) {
+            const uint16_t hv = f32_to_bf16(x[b]);
             o[2 * b] = hv & 0xFF; o[2 * b + 1] = hv >> 8;
         } else if (type == 8) {
             const float * xb = x + b * 32;
@@ -2183,14 +2195,14 @@ void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const flo
 
 void launch_dequant_rows(const uint8_t * src, int type, long long row_bytes, int n_el, long long rows,
                          float * dst, hipStream_t st) {
-    const long long nb = (type == 0 || type == 1) ? (long long)n_el : (long long)(n_el / 32);
+    const long long nb = (type == 0 || type == 1 || type == 30) ? (long long)n_el : (long long)(n_el / 32);
     hipLaunchKernelGGL(k_dequant_rows, dim3(grid_cap(rows * nb, 256)), dim3(256), 0, st,
                        src, type, row_bytes, n_el, rows, dst);
 }
 
 void launch_quant_rows(const float * src, long long src_ld, const int * idx, int type, int n_el,
                        long long rows, uint8_t * dst, long long row_bytes, hipStream_t st) {
-    const long long nb = (type == 0 || type == 1) ? (long long)n_el : (long long)(n_el / 32);
+    const long long nb = (type == 0 || type == 1 || type == 30) ? (long long)n_el : (long long)(n_el / 32);
     hipLaunchKernelGGL(k_quant_rows, dim3(grid_cap(rows * nb, 256)), dim3(256), 0, st,
                        src, src_ld, idx, type, n_el, rows, dst, row_bytes);
 }

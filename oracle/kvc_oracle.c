@@ -973,7 +973,7 @@ uint16_t orc_f32_to_f16(float val) {
 
 static int block_bytes(int type) {
     if (type == KV_TYPE_F32) return 4;
-    if (type == KV_TYPE_F16) return 2;
+    if (type == KV_TYPE_F16 || type == KV_TYPE_BF16) return 2;
     if (type == KV_TYPE_Q8_0) return 34;
     if (type == KV_TYPE_Q4_0) return 18;
     if (type == KV_TYPE_Q4_1) return 20;
@@ -986,14 +986,14 @@ static int is_block_type(int type) {
 
 int orc_quant_row_elements(int type, size_t row_bytes) {
     if (type == KV_TYPE_F32) return (int)(row_bytes / 4);
-    if (type == KV_TYPE_F16) return (int)(row_bytes / 2);
+    if (type == KV_TYPE_F16 || type == KV_TYPE_BF16) return (int)(row_bytes / 2);
     if (is_block_type(type)) return (int)(row_bytes / (size_t)block_bytes(type)) * 32;
     return (int)(row_bytes / 4);
 }
 
 size_t orc_quant_row_bytes(int type, int n) {
     if (type == KV_TYPE_F32) return (size_t)n * 4;
-    if (type == KV_TYPE_F16) return (size_t)n * 2;
+    if (type == KV_TYPE_F16 || type == KV_TYPE_BF16) return (size_t)n * 2;
     if (is_block_type(type)) return (size_t)(n / 32) * (size_t)block_bytes(type);
     return (size_t)n * 4;
 }
@@ -1005,6 +1005,13 @@ static void convert_to_f32(const uint8_t * src, int type, float * dst, size_t n)
         for (size_t i = 0; i < n; i++) {
             uint16_t h; memcpy(&h, src + 2 * i, 2);
             dst[i] = orc_f16_to_f32(h);
+        }
+    } else if (type == KV_TYPE_BF16) {
+        /* extension type (no reference counterpart): exact up-cast */
+        for (size_t i = 0; i < n; i++) {
+            uint16_t h; memcpy(&h, src + 2 * i, 2);
+            uint32_t u = (uint32_t)h << 16;
+            memcpy(dst + i, &u, 4);
         }
     } else if (type == KV_TYPE_Q8_0) {
         for (size_t b = 0; b < n / 32; b++) {
@@ -1049,6 +1056,16 @@ size_t orc_quantize_row(const float * src, int type, int n, uint8_t * dst) {
     if (type == KV_TYPE_F16) {
         for (int i = 0; i < n; i++) {
             uint16_t h = orc_f32_to_f16(src[i]);
+            memcpy(dst + 2 * i, &h, 2);
+        }
+        return (size_t)n * 2;
+    }
+    if (type == KV_TYPE_BF16) {
+        /* round to nearest, ties to even; NaN -> quiet NaN */
+        for (int i = 0; i < n; i++) {
+            uint32_t u; memcpy(&u, src + i, 4);
+            uint16_t h = ((u & 0x7fffffffu) > 0x7f800000u) ? (uint16_t)((u >> 16) | 0x40u)
+                                                          : (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
             memcpy(dst + 2 * i, &h, 2);
         }
         return (size_t)n * 2;

@@ -74,7 +74,7 @@ def test_config2_slice(gpu, orc):
     same(a, b)
 
 
-@pytest.mark.parametrize("kt,vt", [(8, 8), (2, 2), (8, 2), (1, 3)])
+@pytest.mark.parametrize("kt,vt", [(8, 8), (2, 2), (8, 2), (1, 3), (30, 30)])
 def test_quantized_parity(gpu, orc, kt, vt):
     T, H, d = 700, 2, 64
     K, V = kv_cache(T, H, d, 60 + kt + vt)
@@ -91,7 +91,7 @@ def test_quantized_parity(gpu, orc, kt, vt):
 
 def test_codec_rows(gpu, orc):
     from kvc_data import normal
-    for typ in (0, 1, 2, 3, 8):
+    for typ in (0, 1, 2, 3, 8, 30):
         for s in range(3):
             x = (normal(300 + s, (256,)) * np.float32(10.0 ** (s - 1))).astype(np.float32)
             ea, eb = gpu.quantize_row(x, typ), orc.quantize_row(x, typ)
@@ -171,3 +171,26 @@ def test_mixed_chunk_sizes(gpu, orc):
     a = gpu.compact(K, V, Q, 2000, 16, 2, 32, 32, case_params(gpu, c, 2000))
     b = orc.compact(K, V, Q, 2000, 16, 2, 32, 32, case_params(orc, c, 2000))
     same(a, b)
+
+
+def test_config3_bf16_slice(gpu, orc):
+    """Long-context shape: 4 KV heads x d=256 with bf16 storage (K/V rows
+    rounded to bf16, passed as KV_TYPE_BF16), two 1280-token chunks, keep 0.5
+    and 0.2 with SnapKV queries; the compaction runs on the exact fp32
+    up-cast, the kept K rows and C_v rows come back as bf16."""
+    from kvc_harness import kc as _kc
+    T, H, d = 2560, 4, 256
+    K, V = kv_cache(T, H, d, 70, channel_scale=True)
+    Kb = np.stack([orc.quantize_row(K[i], _kc.KV_TYPE_BF16) for i in range(T)])
+    Vb = np.stack([orc.quantize_row(V[i], _kc.KV_TYPE_BF16) for i in range(T)])
+    Kf = np.stack([orc.dequantize_row(Kb[i], _kc.KV_TYPE_BF16, H * d) for i in range(T)]).astype(np.float32)
+    Q = snapkv_queries(np.ascontiguousarray(Kf), 32, 70)
+    for ratio in (0.5, 0.2):
+        print(f"[case] config3_bf16 ratio={ratio}", flush=True)
+        args = (Kb, Vb, Q, 30, 30, Kb.shape[1], Vb.shape[1], T, 32, H, d, d)
+        ra, a = gpu.quantized(*args, gpu.params(target_ratio=ratio))
+        rb, b = orc.quantized(*args, orc.params(target_ratio=ratio))
+        assert ra == 0 and rb == 0
+        same(a, b)
+        assert np.array_equal(a.K_out, b.K_out)
+        assert np.array_equal(a.V_out, b.V_out)

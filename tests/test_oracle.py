@@ -219,6 +219,38 @@ def test_f32_to_f16_truncates(orc):
     assert np.all(np.abs(x) < nxt + 1e-30)
 
 
+def test_bf16_extension_codec(orc):
+    """KV_TYPE_BF16 (an extension, no reference counterpart): decode is the
+    exact up-cast (upper 16 bits); encode rounds to nearest, ties to even,
+    overflows to inf and keeps NaN a quiet NaN. Checked against known values,
+    every one of the 65536 bf16 patterns, and a brute-force nearest search."""
+    bf = kc.KV_TYPE_BF16
+    assert orc.row_elements(bf, 512) == 256
+    # every non-NaN bf16 pattern decodes to its float and re-encodes to itself
+    pats = np.arange(65536, dtype=np.uint32)
+    f = (pats << 16).view(np.float32)
+    keep = ~np.isnan(f)
+    enc = orc.quantize_row(f[keep], bf).view(np.uint16)
+    assert np.array_equal(enc, pats[keep].astype(np.uint16))
+    dec = orc.dequantize_row(pats[keep].astype(np.uint16).view(np.uint8), bf, int(keep.sum()))
+    assert np.array_equal(dec.view(np.uint32), (pats[keep] << 16).astype(np.uint32))
+    # known answers: ties to even, carries into the exponent, overflow, NaN
+    cases = {0x3f808000: 0x3f80, 0x3f818000: 0x3f82, 0x3f808001: 0x3f81, 0x3f7fffff: 0x3f80,
+             0x7f7fffff: 0x7f80, 0xff7fffff: 0xff80, 0x00008000: 0x0000, 0x00018000: 0x0002,
+             0x7f800001: 0x7fc0, 0xffc00000: 0xffc0, 0x80000000: 0x8000}
+    x = np.array(list(cases.keys()), np.uint32).view(np.float32)
+    got = orc.quantize_row(x, bf).view(np.uint16)
+    assert [int(v) for v in got] == list(cases.values())
+    # random floats: the encoded value is a nearest bf16 (brute force over neighbours)
+    r = (normal(91, (4000,)) * np.float32(1e3)).astype(np.float32)
+    e = orc.quantize_row(r, bf).view(np.uint16).astype(np.uint32)
+    dv = (e << 16).view(np.float32).astype(np.float64)
+    lo = ((e - 1) << 16).view(np.float32).astype(np.float64)
+    hi = ((e + 1) << 16).view(np.float32).astype(np.float64)
+    err = np.abs(dv - r)
+    assert np.all(err <= np.abs(lo - r)) and np.all(err <= np.abs(hi - r))
+
+
 def test_codec_roundtrip_bounds(orc):
     """Q8_0 error <= amax/254 + f16 truncation of the scale; Q4_0 <= amax/14 + same
     (reference round-trip bounds, tests/test-kv-compact-math.cpp:1274-1345)."""
