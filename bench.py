@@ -135,6 +135,43 @@ def cpu_baseline(K, V, Q, T, H, d, ratio, L_total, diversity):
                 seconds=round(dt, 2), kept=r.t, cos=r.stats["avg_cosine_sim"])
 
 
+def _pmc_per_dispatch(path: Path) -> dict:
+    """kernel -> (dispatches, {counter: mean value per dispatch}) from a rocprofv3 csv"""
+    import csv
+    tot, disp = {}, {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            k = r["Kernel_Name"].split("(")[0]
+            c = tot.setdefault(k, {})
+            c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+            disp.setdefault(k, set()).add(r["Dispatch_Id"])
+    return {k: (len(disp[k]), {c: v / len(disp[k]) for c, v in tot[k].items()}) for k in tot}
+
+
+def summarize_pmc(d: Path) -> dict:
+    """HBM bytes per dispatch of every kernel of one bench step: FETCH_SIZE and
+    WRITE_SIZE (KiB per dispatch) divided by what the same counter reads per
+    byte for the runtime's copy kernel moving a known number of bytes."""
+    calib = None
+    for line in (d / "cf.log").read_text().splitlines() if (d / "cf.log").exists() else []:
+        if line.startswith("{") and "copy_calibration_bytes" in line:
+            calib = json.loads(line)["copy_calibration_bytes"]
+    if calib is None:
+        raise SystemExit(f"no copy calibration log under {d}")
+    cf = _pmc_per_dispatch(d / "cf" / "run_counter_collection.csv")["__amd_rocclr_copyBuffer"][1]["FETCH_SIZE"]
+    cw = _pmc_per_dispatch(d / "cw" / "run_counter_collection.csv")["__amd_rocclr_copyBuffer"][1]["WRITE_SIZE"]
+    f_fac, w_fac = cf * 1024.0 / calib, cw * 1024.0 / calib
+    bf = _pmc_per_dispatch(d / "bf" / "run_counter_collection.csv")
+    bw = _pmc_per_dispatch(d / "bw" / "run_counter_collection.csv")
+    out = {"copy_bytes": calib, "fetch_factor": round(f_fac, 6), "write_factor": round(w_fac, 6), "kernels": {}}
+    for k, (n, c) in bf.items():
+        fk = c.get("FETCH_SIZE", 0.0)
+        wk = bw.get(k, (0, {}))[1].get("WRITE_SIZE", 0.0)
+        out["kernels"][k] = {"dispatches": n, "fetch_kib": round(fk, 1), "write_kib": round(wk, 1),
+                             "hbm_bytes": int(fk * 1024.0 / f_fac + wk * 1024.0 / w_fac)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -152,7 +189,17 @@ def main():
     ap.add_argument("--one-mode", action="store_true", help="time only the --diversity mode")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--summarize-pmc", metavar="DIR", default="",
+                    help="summarise rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE csv runs under DIR "
+                         "(cf/, cw/: copy calibration; bf/, bw/: one bench step) into per-kernel HBM "
+                         "bytes per dispatch, printed as JSON, and exit")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only copy BYTES device-to-device once (the reference kernel for scaling "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
     a = ap.parse_args()
+    if a.summarize_pmc:
+        print(json.dumps(summarize_pmc(Path(a.summarize_pmc)), indent=1))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if a.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for {max(a.gpus, world)}); "
@@ -161,6 +208,14 @@ def main():
         sys.exit(2)
 
     import hiprt
+    if a.copy_calibration:
+        src, dst = hiprt.DevBuf(a.copy_calibration), hiprt.DevBuf(a.copy_calibration)
+        src.zero()
+        hiprt.synchronize()
+        hiprt.check(hiprt.hip().hipMemcpy(dst.value, src.value, a.copy_calibration, hiprt.D2D), "hipMemcpy D2D")
+        hiprt.synchronize()
+        print(json.dumps({"copy_calibration_bytes": a.copy_calibration}), flush=True)
+        return
     lib = kc.load_product()
     dll = kc.bind_device_api(lib.dll)
     if not dll.kv_compact_hip_available():
@@ -225,6 +280,16 @@ def main():
     model = stage_model(L, T, H, d, W, t, n_chunks, 256 if n_chunks > 1 else t)
     dom = STAGES[int(np.argmax(stage_ms))]
     roof = roofline(dom, model, float(stage_ms[int(np.argmax(stage_ms))]))
+    # HBM bytes per launch of the dominant kernel from the committed rocprofv3
+    # FETCH_SIZE / WRITE_SIZE summary of this exact workload (copy-calibrated)
+    prof = REPO / "profiles" / "hbm_traffic_100k_32layer_pmc.json"
+    headline = (L, T, H, d, W, a.ratio, a.diversity) == (32, 100000, 8, 128, 32, 0.2, 1)
+    kname = "kvc::" + STAGE_KERNELS[dom]
+    if headline and prof.exists():
+        kern = json.loads(prof.read_text())["kernels"].get(kname)
+        if kern:
+            roof["traffic"] = kern["hbm_bytes"]
+            roof["traffic_source"] = str(prof.relative_to(REPO))
     stats = st.download(np.float32, L * 3).reshape(L, 3)
 
     cpu = None
