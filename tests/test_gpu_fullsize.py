@@ -1,0 +1,155 @@
+"""Parity and invariants at the full sizes of the measured configurations.
+
+* One layer of the headline workload (T = 100,000, 8 KV heads, d = 128,
+  SnapKV W = 32, keep 0.2, diversity on): every output equal to the oracle's.
+* One layer with the 1M-token configuration's options (Lawson-Hanson beta,
+  diversity, one refinement round, R-KV span weights) at T = 100,000 and
+  4 KV heads: every output equal to the oracle's.
+* The 1M-token configuration itself (10 layers x 4 KV heads x d = 128,
+  T = 1,048,576) in one device-resident call, where the oracle would take
+  minutes per layer: size-independent invariants (kept count from the chunk
+  plan, ascending in-range positions, exact per-chunk counts, finite beta >=
+  log(1e-12) and C_v, statistics in range) and the batch's layer 0 equal bit
+  for bit to a one-layer call on the same data.
+Inputs come from numpy's seeded generator (the data is made here, not read).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from kvc_harness import case_params, kc, load_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    lib = kc.load_product()
+    if not lib.dll.kv_compact_hip_available():
+        pytest.fail("no usable GPU for the GPU test tier")
+    return lib
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return load_oracle()
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+def layer(T, H, d, seed, W=32):
+    r = np.random.default_rng(seed)
+    scale = np.exp(r.normal(0.0, 0.5, size=H * d)).astype(np.float32)
+    K = (r.standard_normal((T, H * d), dtype=np.float32) * scale).astype(np.float32)
+    V = r.standard_normal((T, H * d), dtype=np.float32)
+    Q = (K[-W:] + np.float32(0.1) * r.standard_normal((W, H * d), dtype=np.float32)).astype(np.float32)
+    return np.ascontiguousarray(K), V, np.ascontiguousarray(Q)
+
+
+def span(T, seed, frac=0.3):
+    r = np.random.default_rng(seed)
+    s = int(r.integers(0, T - int(frac * T)))
+    return s, s + int(frac * T)
+
+
+def same(a, b):
+    assert a.t == b.t
+    assert np.array_equal(a.indices, b.indices), "indices"
+    assert np.array_equal(bits(a.beta), bits(b.beta)), "beta"
+    assert np.array_equal(bits(a.C_v), bits(b.C_v)), "C_v"
+    for k in ("avg_cosine_sim", "avg_mse", "avg_agreement"):
+        assert np.float32(a.stats[k]).view(np.uint32) == np.float32(b.stats[k]).view(np.uint32), k
+
+
+def test_headline_layer_exact(gpu, orc):
+    T, H, d = 100000, 8, 128
+    K, V, Q = layer(T, H, d, 7001)
+    print("[full] headline layer T=100000 H=8 d=128 diversity", flush=True)
+    a = gpu.compact(K, V, Q, T, 32, H, d, d, gpu.params(target_ratio=0.2, use_diversity=1))
+    b = orc.compact(K, V, Q, T, 32, H, d, d, orc.params(target_ratio=0.2, use_diversity=1))
+    assert a.t == 20000
+    same(a, b)
+
+
+def c5_params(lib, T, s):
+    c = dict(name="c5", T=T, H=4, d=128, seed=0, params=dict(target_ratio=0.2, skip_beta=0, nnls_method=0,
+                                                            use_diversity=1, refine_rounds=1))
+    p = case_params(lib, c, T)
+    cls = kc.CLASSIFIER(lambda pos, _d: kc.KV_TOKEN_THINKING if s[0] <= pos < s[1] else
+                        (kc.KV_TOKEN_TRANSITION if pos == s[1] else kc.KV_TOKEN_ANSWER))
+    r = kc.Reasoning(cls, None, 0.3, 0.7, 0)
+    p.reasoning = ctypes.pointer(r)
+    return p, (cls, r)
+
+
+def test_config5_options_layer_exact(gpu, orc):
+    T, H, d = 100000, 4, 128
+    K, V, Q = layer(T, H, d, 7002)
+    s = span(T, 7002)
+    print("[full] 1M-config options on one 100k layer", flush=True)
+    pg, keep_g = c5_params(gpu, T, s)
+    po, keep_o = c5_params(orc, T, s)
+    a = gpu.compact(K, V, Q, T, 32, H, d, d, pg)
+    b = orc.compact(K, V, Q, T, 32, H, d, d, po)
+    same(a, b)
+
+
+def test_config5_full_size_invariants(gpu):
+    import hiprt
+    L, T, H, d, W = 10, 1048576, 4, 128, 32
+    E = H * d
+    print("[full] 1M-token configuration, 10 layers, device batch", flush=True)
+    dll = kc.bind_device_api(gpu.dll)
+    p = gpu.params(target_ratio=0.2, skip_beta=0, nnls_method=0, use_diversity=1, refine_rounds=1)
+    t, n_chunks = kc.plan(dll, T, W, True, p)
+    assert (t, n_chunks) == (819 * 256 + 51, 820)
+    r = np.random.default_rng(7003)
+    pool = r.standard_normal(T * E + 8192 * E, dtype=np.float32)
+    dK, dV, dQ = hiprt.DevBuf(L * T * E * 4), hiprt.DevBuf(L * T * E * 4), hiprt.DevBuf(L * W * E * 4)
+    layers = []
+    for l in range(L):
+        o1, o2 = (int(x) * E for x in r.integers(0, 8192, size=2))
+        scale = np.exp(r.normal(0.0, 0.5, size=E)).astype(np.float32)
+        K = (pool[o1:o1 + T * E].reshape(T, E) * scale).astype(np.float32)
+        V = pool[o2:o2 + T * E].reshape(T, E)
+        Q = (K[-W:] + np.float32(0.1) * r.standard_normal((W, E), dtype=np.float32)).astype(np.float32)
+        dK.upload(K, l * T * E * 4)
+        dV.upload(V, l * T * E * 4)
+        dQ.upload(Q, l * W * E * 4)
+        del K
+    s0, s1 = span(T, 7003)
+    wts = np.ones(T, np.float32)
+    wts[s0:s1] = 0.3
+    wts[s1] = 0.7
+    dW = hiprt.DevBuf(T * 4)
+    dW.upload(wts)
+
+    def run(nl, k_off, v_off, q_off):
+        idx, beta, cv, st = (hiprt.DevBuf(n * 4) for n in (nl * t, nl * H * t, nl * H * t * d, nl * 3))
+        out = kc.DeviceOut(idx.value, beta.value, cv.value, st.value)
+        rc = dll.kvc_compact_layers_device(dK.value + k_off, dV.value + v_off, dQ.value + q_off, nl, T, W, H, d, d,
+                                           T * E, T * E, W * E, ctypes.byref(p), dW.value, ctypes.byref(out), None)
+        assert rc == 0
+        return (idx.download(np.int32, nl * t).reshape(nl, t), beta.download(np.float32, nl * H * t),
+                cv.download(np.float32, nl * H * t * d), st.download(np.float32, nl * 3).reshape(nl, 3))
+
+    gi, gb, gc, gs = run(L, 0, 0, 0)
+    per_chunk = np.full(n_chunks, 256)
+    per_chunk[-1] = 51
+    for l in range(L):
+        ix = gi[l]
+        assert np.all(np.diff(ix) > 0) and ix[0] >= 0 and ix[-1] < T
+        assert np.array_equal(np.bincount(ix // 1280, minlength=n_chunks), per_chunk)
+        assert 0.0 < gs[l, 0] <= 1.0 + 1e-6 and gs[l, 1] >= 0.0 and 0.0 <= gs[l, 2] <= 1.0
+    assert np.all(np.isfinite(gb)) and gb.min() >= np.float32(np.log(np.float32(1e-12))) - 1e-3
+    assert np.all(np.isfinite(gc))
+    i0, b0, c0, s0_ = run(1, 0, 0, 0)
+    assert np.array_equal(i0[0], gi[0])
+    assert np.array_equal(bits(b0), bits(gb[:H * t]))
+    assert np.array_equal(bits(c0), bits(gc[:H * t * d]))
+    assert np.array_equal(bits(s0_[0]), bits(gs[0]))
