@@ -57,8 +57,8 @@ struct Work {
     float * aug;      // GE workspace: one column-major [tc + dv][tc] system per (layer, chunk, head)
     int   * perm;     // [L][n_chunks][H][tc_max] pivot order of each system
     unsigned char * skip; // [L][n_chunks][H][tc_max] skipped-pivot flags by step
-    float * Ut;       // [L][n_chunks][H][256][256] U rows by logical row (systems with tc <= 256)
-    float * Lp;       // [L][n_chunks][H][256][256] multipliers by physical row and step
+    float * LU;       // [L][n_chunks][H][256][256] by physical row: multipliers left of the row's
+                      // pivot step, its U row from that step on (systems with tc <= 256)
     float * Bt;       // [L][n_chunks][H][256][dv] forward-substituted right-hand sides by logical row
     long long * aug_off; // [L][n_chunks][H] element offsets into aug
     float * gtmp;     // [L][n_chunks][H][tc_max + tc_max + dv] GE factor / pivot-row spill

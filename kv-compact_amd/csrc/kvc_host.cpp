@@ -315,8 +315,7 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     for (int c = 0; c < pl.n_chunks; c++) tc_min = std::min(tc_min, pl.chunks[c].tc);
     const size_t ut_rows = tc_min <= 256 ? 256 : 0;
     ww.skip = cv.take<unsigned char>(L * nc * H * (size_t)pl.tc_max);
-    ww.Ut = cv.take<float>(L * nc * H * ut_rows * ut_rows);
-    ww.Lp = cv.take<float>(L * nc * H * ut_rows * ut_rows);
+    ww.LU = cv.take<float>(L * nc * H * ut_rows * ut_rows);
     ww.Bt = cv.take<float>(L * nc * H * ut_rows * dv);
     ww.gtmp = cv.take<float>(L * nc * H * (2 * (size_t)pl.tc_max + dv));
     ww.cand = cv.take<int>(L * nc * (size_t)pl.Tc_max);

@@ -1282,8 +1282,11 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 // factorization of panel k+1 (which first applies panel k to itself) runs
 // beside the other strips' update with panel k. Each element therefore
 // receives exactly the reference's sequence of a -= f * u operations.
-// Outputs per system: U rows by logical row (Ut), multipliers by physical row
-// and step (Lp), the final permutation and the skipped-pivot flags.
+// Output per system: one 256 x 256 array by physical row r holding, left of
+// the step at which r became the pivot, r's multipliers (by step), and from
+// that step on, r's U row (a pivot row is never updated again, so the strips
+// write it once at the end); plus the final permutation and the
+// skipped-pivot flags.
 // The right-hand sides are not touched here: the reference's elimination of
 // them is forward substitution with the final permutation (ascending steps),
 // done with the back substitution in k_ge_solve.
@@ -1313,28 +1316,17 @@ struct LuShared {
 };
 
 // Apply panel kp's steps (columns 16 kp .. 16 kp + 15), in order, to this
-// wave's strip; the owner lane of each pivot row stores that U row's strip.
+// wave's strip.
 __device__ __forceinline__ void lu_apply_panel(const LuShared & sh, float (&a)[RG_SLOTS][RG_STRIP],
-                                               bool (&live)[RG_SLOTS], int kp, int n, int w, int lane,
-                                               float * __restrict__ Ut) {
+                                               bool (&live)[RG_SLOTS], int kp, int n, int lane) {
     const int c0 = kp * RG_STRIP, buf = kp & 1;
     for (int jj = 0; jj < RG_STRIP; jj++) {
         const int col = c0 + jj;
         if (col >= n) break;
-        const int P = sh.pivrow[col];
-        if (!sh.skip[col]) {
-            if (lane == (P & 63)) {
-                const int slot = P >> 6;
-                float4 * dst = reinterpret_cast<float4 *>(Ut + (long long)col * RG_ROWS + RG_STRIP * w);
-#pragma unroll
-                for (int s2 = 0; s2 < RG_SLOTS; s2++) {
-                    if (slot == s2) {
-#pragma unroll
-                        for (int q4 = 0; q4 < RG_STRIP / 4; q4++)
-                            dst[q4] = make_float4(a[s2][4 * q4], a[s2][4 * q4 + 1], a[s2][4 * q4 + 2], a[s2][4 * q4 + 3]);
-                    }
-                }
-            }
+        // wave-uniform by construction; readfirstlane lets the compiler keep the
+        // slot branch and the pivot values scalar
+        const int P = __builtin_amdgcn_readfirstlane(sh.pivrow[col]);
+        if (!__builtin_amdgcn_readfirstlane(sh.skip[col])) {
             float sp[RG_STRIP];
             rg_pivot_values(a, P, sp);
 #pragma unroll
@@ -1358,12 +1350,13 @@ __device__ __forceinline__ void lu_apply_panel(const LuShared & sh, float (&a)[R
 // never NaN; pivots below 1e-12 in magnitude skip the step (math.h:501-523).
 __device__ __forceinline__ void lu_factor_panel(LuShared & sh, float (&a)[RG_SLOTS][RG_STRIP],
                                                 bool (&live)[RG_SLOTS], int k, int n, int lane,
-                                                float * __restrict__ Ut, float * __restrict__ Lp) {
+                                                float * __restrict__ LU) {
     const int c0 = k * RG_STRIP, buf = k & 1;
     int li[RG_SLOTS];
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) li[s] = sh.inv[lane + 64 * s];
     int my_piv = 0, my_skip = 0;   // lane jj keeps step jj's pivot row and skip flag
+    unsigned lmask[RG_SLOTS] = {0u, 0u, 0u, 0u};   // bit jj: the slot's row was below the pivot at step jj
 #pragma unroll
     for (int jj = 0; jj < RG_STRIP; jj++) {
         const int col = c0 + jj;
@@ -1410,22 +1403,8 @@ __device__ __forceinline__ void lu_factor_panel(LuShared & sh, float (&a)[RG_SLO
                 for (int q = jj + 1; q < RG_STRIP; q++) a[s][q] = a[s][q] - f * sp[q];
             }
             sh.fmul[buf][jj][r] = f;
+            if (live[s] && r != P) lmask[s] |= 1u << jj;
             live[s] = live[s] && r != P;
-        }
-        // U row col over the panel's columns (entries left of col are never read)
-        // (a wave-uniform offset through readfirstlane: keeps the compiler from
-        // carrying one hoisted 64-bit address per unrolled step)
-        const int uoff = __builtin_amdgcn_readfirstlane(col * RG_ROWS + c0);
-        if (lane == laneP) {
-            float4 * dst = reinterpret_cast<float4 *>(Ut + uoff);
-#pragma unroll
-            for (int s2 = 0; s2 < RG_SLOTS; s2++) {
-                if (slotP == s2) {
-#pragma unroll
-                    for (int q4 = 0; q4 < RG_STRIP / 4; q4++)
-                        dst[q4] = make_float4(a[s2][4 * q4], a[s2][4 * q4 + 1], a[s2][4 * q4 + 2], a[s2][4 * q4 + 3]);
-                }
-            }
         }
         if (lane == jj) {
             my_piv = P;
@@ -1436,18 +1415,15 @@ __device__ __forceinline__ void lu_factor_panel(LuShared & sh, float (&a)[RG_SLO
         sh.pivrow[c0 + lane] = my_piv;
         sh.skip[c0 + lane] = (unsigned char)my_skip;
     }
-    // multipliers of this panel by physical row: Lp[r][c0 .. c0+15] (entries
-    // past column n of a row are never read)
+    // multipliers of this panel, only where the row was still below the pivot
+    // (the rest of those columns belongs to the row's U part)
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) {
         const int r = lane + 64 * s;
-        if (r < n) {
-            float4 * dst = reinterpret_cast<float4 *>(Lp + (unsigned)(r * RG_ROWS + c0));
+        float * dst = LU + (unsigned)(r * RG_ROWS + c0);
 #pragma unroll
-            for (int q4 = 0; q4 < RG_STRIP / 4; q4++)
-                dst[q4] = make_float4(sh.fmul[buf][4 * q4][r], sh.fmul[buf][4 * q4 + 1][r],
-                                      sh.fmul[buf][4 * q4 + 2][r], sh.fmul[buf][4 * q4 + 3][r]);
-        }
+        for (int jj = 0; jj < RG_STRIP; jj++)
+            if (lmask[s] & (1u << jj)) dst[jj] = sh.fmul[buf][jj][r];
         sh.inv[r] = li[s];
     }
 }
@@ -1455,15 +1431,14 @@ __device__ __forceinline__ void lu_factor_panel(LuShared & sh, float (&a)[RG_SLO
 __global__ void __launch_bounds__(RG_THREADS)
 k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
         const long long * __restrict__ aug_off, int * __restrict__ perm_out, unsigned char * __restrict__ skip_out,
-        float * __restrict__ Ut_all, float * __restrict__ Lp_all) {
+        float * __restrict__ LU_all) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const int n = c.tc;
     if (n > RG_ROWS) return;
     const long long sys = ((long long)layer * g.n_chunks + c_idx) * g.H + h;
     const float * A = aug + aug_off[sys];
-    float * Ut = Ut_all + sys * (long long)RG_ROWS * RG_ROWS;
-    float * Lp = Lp_all + sys * (long long)RG_ROWS * RG_ROWS;
+    float * LU = LU_all + sys * (long long)RG_ROWS * RG_ROWS;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     __shared__ LuShared sh;
 
@@ -1487,9 +1462,9 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
     // phase k: strips w >= k apply panel k-1, then wave k factors panel k
     for (int k = 0; k < n_panels; k++) {
         if (w == k) __builtin_amdgcn_s_setprio(3);
-        if (k > 0 && w >= k && w < n_panels) lu_apply_panel(sh, a, live, k - 1, n, w, lane, Ut);
+        if (k > 0 && w >= k && w < n_panels) lu_apply_panel(sh, a, live, k - 1, n, lane);
         if (w == k) {
-            lu_factor_panel(sh, a, live, k, n, lane, Ut, Lp);
+            lu_factor_panel(sh, a, live, k, n, lane, LU);
             __builtin_amdgcn_s_setprio(0);
         }
         __syncthreads();
@@ -1497,6 +1472,22 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
     if (tid < n) {
         perm_out[sys * (long long)g.tc_max + tid] = sh.pivrow[tid];
         skip_out[sys * (long long)g.tc_max + tid] = sh.skip[tid];
+    }
+    // U parts: row r from its pivot step on (sh.inv[r] is that step now)
+    if (RG_STRIP * w < n) {
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            const int r = lane + 64 * s;
+            if (r < n) {
+                const int st = sh.inv[r];
+                float * dst = LU + (unsigned)(r * RG_ROWS + RG_STRIP * w);
+#pragma unroll
+                for (int q = 0; q < RG_STRIP; q++) {
+                    const int c = RG_STRIP * w + q;
+                    if (c >= st && c < n) dst[q] = a[s][q];
+                }
+            }
+        }
     }
 }
 
@@ -1549,8 +1540,8 @@ __device__ __forceinline__ float dot_seq_skip(float val, const float * rowp, con
 __global__ void __launch_bounds__(64)
 k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
            const long long * __restrict__ aug_off, const int * __restrict__ perm_in,
-           const unsigned char * __restrict__ skip_in, const float * __restrict__ Ut_all,
-           const float * __restrict__ Lp_all, float * __restrict__ Yt_all, float * __restrict__ Cv) {
+           const unsigned char * __restrict__ skip_in, const float * __restrict__ LU_all,
+           float * __restrict__ Yt_all, float * __restrict__ Cv) {
     const int sysl = blockIdx.x;   // (layer, chunk, head)
     const int h = sysl % g.H, c_idx = (sysl / g.H) % g.n_chunks, layer = sysl / (g.H * g.n_chunks);
     const ChunkDesc c = chunks[c_idx];
@@ -1560,8 +1551,8 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     const int v = blockIdx.y * 64 + lane;
     const bool act = v < p;
     const int vc = act ? v : p - 1;   // in-range column for the loads of idle lanes
-    const float * __restrict__ Ut = Ut_all + (long long)sysl * RG_ROWS * RG_ROWS;
-    const float * __restrict__ Lp = Lp_all + (long long)sysl * RG_ROWS * RG_ROWS;
+    // by physical row: multipliers left of the row's pivot step, U from it on
+    const float * __restrict__ LU = LU_all + (long long)sysl * RG_ROWS * RG_ROWS;
     const float * __restrict__ B = aug + aug_off[sysl] + (long long)n * n;   // column-major RHS [v][r]
     float * Yt = Yt_all + (long long)sysl * RG_ROWS * g.dv;
     float * x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
@@ -1585,14 +1576,14 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 
     // ---- forward: rows [0, lb) from LDS, then rows [lb, n) with [0, lb) in registers
     const int lb = n < BS_HIGH ? n : BS_HIGH;
-    float4 pf = reinterpret_cast<const float4 *>(Lp + (unsigned)(permL[0] * RG_ROWS))[lane];
+    float4 pf = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[0] * RG_ROWS))[lane];
     float pb = B[(unsigned)(vc * n + permL[0])];
     for (int i = 0; i < lb; i++) {
         frow4[lane] = pf;
         float val = act ? pb : 0.0f;
         if (i + 1 < n) {
             const int rn = permL[i + 1];
-            pf = reinterpret_cast<const float4 *>(Lp + (unsigned)(rn * RG_ROWS))[lane];
+            pf = reinterpret_cast<const float4 *>(LU + (unsigned)(rn * RG_ROWS))[lane];
             pb = B[(unsigned)(vc * n + rn)];
         }
         __builtin_amdgcn_wave_barrier();
@@ -1610,7 +1601,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             float val = act ? pb : 0.0f;
             if (i + 1 < n) {
                 const int rn = permL[i + 1];
-                pf = reinterpret_cast<const float4 *>(Lp + (unsigned)(rn * RG_ROWS))[lane];
+                pf = reinterpret_cast<const float4 *>(LU + (unsigned)(rn * RG_ROWS))[lane];
                 pb = B[(unsigned)(vc * n + rn)];
             }
             __builtin_amdgcn_wave_barrier();
@@ -1635,7 +1626,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     // brow[k]), so that the register part's entries brow[hb + i] are aligned.
     const int hb = n > BS_HIGH ? n - BS_HIGH : 0;
     float * brow = rowb + BS_PAD - hb;
-    pf = reinterpret_cast<const float4 *>(Ut + (unsigned)((n - 1) * RG_ROWS))[lane];
+    pf = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[n - 1] * RG_ROWS))[lane];
     pb = Yt[(unsigned)((n - 1) * g.dv + vc)];
     for (int col = n - 1; col >= hb; col--) {
         brow[4 * lane + 0] = pf.x;
@@ -1644,7 +1635,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         brow[4 * lane + 3] = pf.w;
         const float yv = pb;
         if (col > 0) {
-            pf = reinterpret_cast<const float4 *>(Ut + (unsigned)((col - 1) * RG_ROWS))[lane];
+            pf = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[col - 1] * RG_ROWS))[lane];
             pb = Yt[(unsigned)((col - 1) * g.dv + vc)];
         }
         __builtin_amdgcn_wave_barrier();
@@ -1671,7 +1662,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         brow[4 * lane + 3] = pf.w;
         const float yv = pb;
         if (col > 0) {
-            pf = reinterpret_cast<const float4 *>(Ut + (unsigned)((col - 1) * RG_ROWS))[lane];
+            pf = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[col - 1] * RG_ROWS))[lane];
             pb = Yt[(unsigned)((col - 1) * g.dv + vc)];
         }
         __builtin_amdgcn_wave_barrier();
@@ -2156,13 +2147,13 @@ void launch_ls_build(const Geom & g, const Work & w, hipStream_t st) {
 
 void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st) {
     hipLaunchKernelGGL(k_ge_lu, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
-                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.Ut, w.Lp);
+                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU);
 }
 
 void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st) {
     const unsigned systems = (unsigned)(g.L * g.n_chunks * g.H);
     hipLaunchKernelGGL(k_ge_solve, dim3(systems, cdiv(g.dv, 64)), dim3(64), 0, st,
-                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.Ut, w.Lp, w.Bt, Cv);
+                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, w.Bt, Cv);
     if (g.tc_max > RG_ROWS)
         hipLaunchKernelGGL(k_ge_general, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
                            g, w.chunks, w.aug, w.aug_off, Cv, w.gtmp);
