@@ -291,13 +291,9 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
 }
 
 // ---------------------------------------------------------------------------
-// Attention-weighted sums out[qi][v] = sum_j a[qi][j] * val[j][v], each
-// output accumulated sequentially over j (math.h:70-80 for the refit target
-// Y = A V; api.cpp:271-292 for the statistics' outputs). A block owns QB x vn
-// outputs (PER per thread); keys are staged through LDS 32 at a time.
-//   mode 0: refit target of a (layer, chunk, head)        grid (n_chunks*H, L)
-//   mode 1: statistics, original attention over all T      grid (mh*nvb, L)
-//   mode 2: statistics, compacted attention over t_total   grid (mh*nvb, L)
+// Refit target Y = A V per (layer, chunk, head) (math.h:70-80): each output
+// accumulated sequentially over the chunk's keys; keys are staged through LDS
+// 32 at a time. grid (n_chunks*H, L)
 // ---------------------------------------------------------------------------
 constexpr int AS_KT = 32;
 
@@ -370,21 +366,126 @@ k_refit_target(Geom g, const ChunkDesc * __restrict__ chunks, const float * __re
                             Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv, g.dv);
 }
 
-constexpr int ST_VB = 32;   // value columns per statistics block
+// ---------------------------------------------------------------------------
+// Statistics attention outputs (api.cpp:270-293): out[q][v] = sum_j a[q][j] *
+// val[j][v], j ascending, for the sampled heads and queries, over all T keys
+// (original) or the t_total kept keys (compacted, val = C_v). Each output is a
+// sequential sum, so the parallelism is the outputs: a block of 128 threads
+// owns 16 queries x 64 columns, each thread 2 queries x 4 columns (8
+// independent sums); 64-key tiles of a and val are double-buffered in LDS.
+// grid (mh * ceil(mq/16) * ceil(dv/64), L)
+// ---------------------------------------------------------------------------
+constexpr int SV_QB = 16, SV_VB = 64, SV_KT = 64, SV_THREADS = 128;
 
-__global__ void __launch_bounds__(256)
-k_stats_sum(Geom g, const float * __restrict__ a, int n, const float * __restrict__ V,
-            const float * __restrict__ Cv, int mode, float * __restrict__ out, int mh, int mq) {
-    const int nvb = (g.dv + ST_VB - 1) / ST_VB;
-    const int h = blockIdx.x / nvb, v0 = (blockIdx.x % nvb) * ST_VB, layer = blockIdx.y;
-    const int vn = min(ST_VB, g.dv - v0);
-    const float * ar = a + (((long long)layer * mh + h) * mq) * n;
-    float * o = out + (((long long)layer * mh + h) * mq) * g.dv + v0;
+__global__ void __launch_bounds__(SV_THREADS)
+k_stats_values(Geom g, const float * __restrict__ a_all, int n, const float * __restrict__ V,
+               const float * __restrict__ Cv, int mode, float * __restrict__ out_all, int mh, int mq) {
+    const int nqb = (mq + SV_QB - 1) / SV_QB, nvb = (g.dv + SV_VB - 1) / SV_VB;
+    const int layer = blockIdx.y;
+    const int h = blockIdx.x / (nqb * nvb);
+    const int q0 = ((blockIdx.x / nvb) % nqb) * SV_QB, v0 = (blockIdx.x % nvb) * SV_VB;
+    const float * a = a_all + (((long long)layer * mh + h) * mq) * n;
+    const float * val;
+    long long vrs;
     if (mode == 1) {
-        const long long ev = (long long)g.H * g.dv;
-        attn_sum_tile<2, 2, 16>(ar, n, mq, V + layer * g.ldV + (long long)h * g.dv + v0, ev, n, vn, o, g.dv);
+        vrs = (long long)g.H * g.dv;
+        val = V + layer * g.ldV + (long long)h * g.dv;
     } else {
-        attn_sum_tile<2, 2, 16>(ar, n, mq, Cv + ((long long)layer * g.H + h) * g.t_total * g.dv + v0, g.dv, n, vn, o, g.dv);
+        vrs = g.dv;
+        val = Cv + ((long long)layer * g.H + h) * g.t_total * g.dv;
+    }
+    float * out = out_all + (((long long)layer * mh + h) * mq) * g.dv;
+    __shared__ float As[2][SV_QB][SV_KT + 1];
+    __shared__ __align__(16) float Vs[2][SV_KT][SV_VB];
+    const int tid = threadIdx.x, tq = tid >> 4, tv = tid & 15;
+    const int qa = q0 + 2 * tq, vc = v0 + 4 * tv;
+    // tile loaders: a: 16 x 64 (8 per thread); val: 64 x 64 (32 per thread, 8 float4)
+    const bool vvec = (g.dv & 3) == 0 && (vrs & 3) == 0 && (reinterpret_cast<uintptr_t>(val) & 15) == 0;
+    float ra[8];
+    float4 rv[8];
+    auto load = [&](int j0) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int e = tid + SV_THREADS * u, qi = e >> 6, jj = e & 63;
+            const int q = q0 + qi, j = j0 + jj;
+            ra[u] = (q < mq && j < n) ? a[(long long)q * n + j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int e = tid + SV_THREADS * u, jj = e >> 4, c4 = (e & 15) * 4;
+            const int j = j0 + jj, c = v0 + c4;
+            float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            if (j < n) {
+                const float * src = val + (long long)j * vrs + c;
+                if (vvec && c + 3 < g.dv) {
+                    x = *reinterpret_cast<const float4 *>(src);
+                } else {
+                    if (c < g.dv) x.x = src[0];
+                    if (c + 1 < g.dv) x.y = src[1];
+                    if (c + 2 < g.dv) x.z = src[2];
+                    if (c + 3 < g.dv) x.w = src[3];
+                }
+            }
+            rv[u] = x;
+        }
+    };
+    auto store = [&](int b) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int e = tid + SV_THREADS * u;
+            As[b][e >> 6][e & 63] = ra[u];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int e = tid + SV_THREADS * u;
+            *reinterpret_cast<float4 *>(&Vs[b][e >> 4][(e & 15) * 4]) = rv[u];
+        }
+    };
+    float acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) acc[i][k] = 0.0f;
+    const int ntiles = (n + SV_KT - 1) / SV_KT;
+    if (ntiles > 0) {
+        load(0);
+        store(0);
+    }
+    __syncthreads();
+    for (int t = 0; t < ntiles; t++) {
+        const int b = t & 1;
+        if (t + 1 < ntiles) load((t + 1) * SV_KT);
+        const int jn = min(SV_KT, n - t * SV_KT);
+        if (jn == SV_KT) {
+#pragma unroll 8
+            for (int jj = 0; jj < SV_KT; jj++) {
+                const float a0 = As[b][2 * tq][jj], a1 = As[b][2 * tq + 1][jj];
+                const float4 x = *reinterpret_cast<const float4 *>(&Vs[b][jj][4 * tv]);
+                acc[0][0] = acc[0][0] + a0 * x.x; acc[0][1] = acc[0][1] + a0 * x.y;
+                acc[0][2] = acc[0][2] + a0 * x.z; acc[0][3] = acc[0][3] + a0 * x.w;
+                acc[1][0] = acc[1][0] + a1 * x.x; acc[1][1] = acc[1][1] + a1 * x.y;
+                acc[1][2] = acc[1][2] + a1 * x.z; acc[1][3] = acc[1][3] + a1 * x.w;
+            }
+        } else {
+            for (int jj = 0; jj < jn; jj++) {
+                const float a0 = As[b][2 * tq][jj], a1 = As[b][2 * tq + 1][jj];
+                const float4 x = *reinterpret_cast<const float4 *>(&Vs[b][jj][4 * tv]);
+                acc[0][0] = acc[0][0] + a0 * x.x; acc[0][1] = acc[0][1] + a0 * x.y;
+                acc[0][2] = acc[0][2] + a0 * x.z; acc[0][3] = acc[0][3] + a0 * x.w;
+                acc[1][0] = acc[1][0] + a1 * x.x; acc[1][1] = acc[1][1] + a1 * x.y;
+                acc[1][2] = acc[1][2] + a1 * x.z; acc[1][3] = acc[1][3] + a1 * x.w;
+            }
+        }
+        if (t + 1 < ntiles) store(b ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int q = qa + i;
+        if (q >= mq) continue;
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            if (vc + k < g.dv) out[(long long)q * g.dv + vc + k] = acc[i][k];
     }
 }
 
@@ -529,13 +630,15 @@ k_select_topk(Geom g, const ChunkDesc * __restrict__ chunks, const float * __res
 }
 
 // Wave-wide max / min of a 32-bit unsigned value through DPP row shifts and
-// row broadcasts (the result collects in lane 63); both operations are
-// idempotent, so lanes whose DPP source is out of range keep their own value.
+// row broadcasts (the result collects in lane 63).
 template <bool MAX>
 __device__ __forceinline__ unsigned dpp_reduce_u32(unsigned x) {
+    // lanes without a source (row edge, masked row) see the identity, which
+    // lets the move and the min/max fold into one DPP instruction
+    constexpr int ident = MAX ? 0 : -1;
 #define KVC_DPP_STEP(ctrl, rmask)                                                                  \
     {                                                                                              \
-        const unsigned t = (unsigned)__builtin_amdgcn_update_dpp((int)x, (int)x, ctrl, rmask, 0xf, false); \
+        const unsigned t = (unsigned)__builtin_amdgcn_update_dpp(ident, (int)x, ctrl, rmask, 0xf, false); \
         x = MAX ? (t > x ? t : x) : (t < x ? t : x);                                               \
     }
     KVC_DPP_STEP(0x111, 0xf)   // row_shr:1
@@ -1320,13 +1423,13 @@ struct LuShared {
 __device__ __forceinline__ void lu_apply_panel(const LuShared & sh, float (&a)[RG_SLOTS][RG_STRIP],
                                                bool (&live)[RG_SLOTS], int kp, int n, int lane) {
     const int c0 = kp * RG_STRIP, buf = kp & 1;
-    for (int jj = 0; jj < RG_STRIP; jj++) {
-        const int col = c0 + jj;
-        if (col >= n) break;
-        // wave-uniform by construction; readfirstlane lets the compiler keep the
-        // slot branch and the pivot values scalar
-        const int P = __builtin_amdgcn_readfirstlane(sh.pivrow[col]);
-        if (!__builtin_amdgcn_readfirstlane(sh.skip[col])) {
+    const int steps = min(RG_STRIP, n - c0);
+    // lane q holds step q's pivot row and skip flag (read once per panel)
+    const int pv = (lane < steps) ? sh.pivrow[c0 + lane] : 0;
+    const int sk = (lane < steps) ? (int)sh.skip[c0 + lane] : 1;
+    for (int jj = 0; jj < steps; jj++) {
+        const int P = __builtin_amdgcn_readlane(pv, jj);
+        if (!__builtin_amdgcn_readlane(sk, jj)) {
             float sp[RG_STRIP];
             rg_pivot_values(a, P, sp);
 #pragma unroll
@@ -2166,20 +2269,20 @@ void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const flo
     const ChunkDesc * kept = w.chunks + g.n_chunks + 1;   // the t_total kept keys
     const long long osl = (long long)sw.mh * sw.mq * g.T;
     const long long csl = (long long)sw.mh * sw.mq * g.t_total;
-    const int nvb = (g.dv + ST_VB - 1) / ST_VB;
     // original attention of the sampled queries over all T
     launch_scores(g, whole, 1, g.T, K, Q, sw.OS, sw.mh, sw.mq, osl, (long long)sw.mq * g.T, g.T, sw.qmode, st,
                   nullptr, nullptr);
     hipLaunchKernelGGL(k_row_softmax, dim3(sw.mh * sw.mq, g.L), dim3(256), 0, st,
                        sw.OS, g.T, (long long)g.T, sw.mh * sw.mq, osl);
-    hipLaunchKernelGGL(k_stats_sum, dim3(sw.mh * nvb, g.L), dim3(256), 0, st,
+    const unsigned sv_blocks = (unsigned)(sw.mh * cdiv(sw.mq, SV_QB) * cdiv(g.dv, SV_VB));
+    hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), 0, st,
                        g, sw.OS, g.T, V, Cv, 1, sw.OO, sw.mh, sw.mq);
     // compacted attention over the kept keys with beta and C_v
     launch_scores(g, kept, 1, g.t_total, K, Q, sw.CS, sw.mh, sw.mq, csl, (long long)sw.mq * g.t_total, g.t_total,
                   sw.qmode, st, w.sel, beta);
     hipLaunchKernelGGL(k_row_softmax, dim3(sw.mh * sw.mq, g.L), dim3(256), 0, st,
                        sw.CS, g.t_total, (long long)g.t_total, sw.mh * sw.mq, csl);
-    hipLaunchKernelGGL(k_stats_sum, dim3(sw.mh * nvb, g.L), dim3(256), 0, st,
+    hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), 0, st,
                        g, sw.CS, g.t_total, V, Cv, 2, sw.CO, sw.mh, sw.mq);
     hipLaunchKernelGGL(k_stats_final, dim3(g.L), dim3(128), 0, st, g, sw.OO, sw.CO, sw.mh, sw.mq, stats);
 }
