@@ -117,11 +117,15 @@ __device__ __forceinline__ long long lS(const Geom & g) { return (long long)g.H 
 __device__ __forceinline__ long long hS(const Geom & g) { return (long long)g.nq_max * g.T; }
 
 // ---------------------------------------------------------------------------
-// Scores. S[l][h][qi][start + j] = (sum_d q[d] k_j[d]) * inv_sqrt_dk.
-// Block: 64 keys x up to 64 query rows (16 per thread); features staged
-// through LDS in slabs of 32. grid = (ceil(Tc_max/64), n_chunks * Hs, L)
+// Scores. S[l][h][qi][start + j] = (sum_d q[d] k_j[d]) * inv_sqrt_dk, the dot
+// product sequential over d (math.h:44-54; the product a*b is symmetric).
+// Block: 128 keys x 32 query rows; thread (tk, tr) owns keys 4 tk .. 4 tk + 3
+// and rows 4 tr .. 4 tr + 3 (16 sums). Features are staged through LDS in
+// slabs of 32, transposed (dimension-major) so each thread reads its 4 keys
+// and its 4 rows as one 16-byte load each. grid = (ceil(Tc_max/128),
+// n_chunks * Hs, L); query rows beyond 32 loop.
 // ---------------------------------------------------------------------------
-constexpr int SC_KEYS = 64, SC_SLAB = 32, SC_ROWS = 64;
+constexpr int SC_KEYS = 128, SC_SLAB = 32, SC_ROWS = 32;
 
 __global__ void __launch_bounds__(256)
 k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ K,
@@ -133,55 +137,96 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
     const int key0 = blockIdx.x * SC_KEYS;
     if (key0 >= c.Tc) return;
     const int nq = min(c.nq, nq_cap);
-    __shared__ float ks[SC_KEYS][SC_SLAB + 1];
-    __shared__ float qs[SC_ROWS][SC_SLAB + 1];
+    __shared__ __align__(16) float ks[SC_SLAB][SC_KEYS + 4];
+    __shared__ __align__(16) float qs[SC_SLAB][SC_ROWS + 4];
     __shared__ const float * qptr[SC_ROWS];
     const int tid = threadIdx.x;
-    const int kl = tid & 63, grp = tid >> 6;
+    const int tk = tid & 31, tr = tid >> 5;
     const long long ek = (long long)g.H * g.dk;
     // key_idx: keys are rows key_idx[layer * t_total + j] (compacted statistics)
     const float * Kl = K + layer * g.ldK + (key_idx ? 0 : (long long)c.start * ek) + (long long)h * g.dk;
     const int * kix = key_idx ? key_idx + (long long)layer * g.t_total : nullptr;
     const float * bh = beta ? beta + ((long long)layer * g.H + h) * g.t_total : nullptr;
     float * Sl = S + layer * s_layer + h * s_head + c.start;
+    // tile loaders: 8 threads per key row (4 dims each, 16-byte loads when
+    // aligned), keys (tid >> 3) + 32 u; query rows likewise
+    const int ld = (tid & 7) * 4, lr = tid >> 3;
+    const float * kp[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int key = key0 + lr + 32 * u;
+        const long long row = (key < c.Tc) ? (kix ? (long long)kix[key] : (long long)key) : -1;
+        kp[u] = (row >= 0) ? Kl + row * ek : nullptr;
+    }
+    const bool vec = (g.dk & 3) == 0 && (ek & 3) == 0 && (reinterpret_cast<uintptr_t>(Kl) & 15) == 0 &&
+                     (qmode != Q_PROVIDED || ((reinterpret_cast<uintptr_t>(Q) & 15) == 0 && (g.ldQ & 3) == 0));
     for (int q0 = 0; q0 < nq; q0 += SC_ROWS) {
         __syncthreads();
         if (tid < SC_ROWS) {
             const int qi = q0 + tid;
             qptr[tid] = (qi < nq) ? query_row(g, K, Q, layer, c, qi, qmode) + (long long)h * g.dk : nullptr;
         }
-        float acc[SC_ROWS / 4];
+        float acc[4][4];
 #pragma unroll
-        for (int r = 0; r < SC_ROWS / 4; r++) acc[r] = 0.0f;
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
         for (int d0 = 0; d0 < g.dk; d0 += SC_SLAB) {
             __syncthreads();
-            for (int e = tid; e < SC_KEYS * SC_SLAB; e += 256) {
-                const int kk = e / SC_SLAB, dd = e % SC_SLAB;
-                const int key = key0 + kk, dim = d0 + dd;
-                const long long krow = kix ? (long long)(key < c.Tc ? kix[key] : 0) : (long long)key;
-                ks[kk][dd] = (key < c.Tc && dim < g.dk) ? Kl[krow * ek + dim] : 0.0f;
+            const int dim = d0 + ld;
+            const bool full = vec && dim + 3 < g.dk;
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (kp[u]) {
+                    if (full) {
+                        x = *reinterpret_cast<const float4 *>(kp[u] + dim);
+                    } else {
+                        if (dim < g.dk) x.x = kp[u][dim];
+                        if (dim + 1 < g.dk) x.y = kp[u][dim + 1];
+                        if (dim + 2 < g.dk) x.z = kp[u][dim + 2];
+                        if (dim + 3 < g.dk) x.w = kp[u][dim + 3];
+                    }
+                }
+                const int kk = lr + 32 * u;
+                ks[ld][kk] = x.x; ks[ld + 1][kk] = x.y; ks[ld + 2][kk] = x.z; ks[ld + 3][kk] = x.w;
             }
-            for (int e = tid; e < SC_ROWS * SC_SLAB; e += 256) {
-                const int rr = e / SC_SLAB, dd = e % SC_SLAB;
-                const int dim = d0 + dd;
-                const float * qp = qptr[rr];
-                qs[rr][dd] = (qp && dim < g.dk) ? qp[dim] : 0.0f;
+            {
+                const float * qp = qptr[lr];
+                float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (qp) {
+                    if (full) {
+                        x = *reinterpret_cast<const float4 *>(qp + dim);
+                    } else {
+                        if (dim < g.dk) x.x = qp[dim];
+                        if (dim + 1 < g.dk) x.y = qp[dim + 1];
+                        if (dim + 2 < g.dk) x.z = qp[dim + 2];
+                        if (dim + 3 < g.dk) x.w = qp[dim + 3];
+                    }
+                }
+                qs[ld][lr] = x.x; qs[ld + 1][lr] = x.y; qs[ld + 2][lr] = x.z; qs[ld + 3][lr] = x.w;
             }
             __syncthreads();
             const int dn = min(SC_SLAB, g.dk - d0);
             for (int dd = 0; dd < dn; dd++) {
-                const float kv = ks[kl][dd];
+                const float4 kv = *reinterpret_cast<const float4 *>(&ks[dd][4 * tk]);
+                const float4 qv = *reinterpret_cast<const float4 *>(&qs[dd][4 * tr]);
+                const float kk[4] = {kv.x, kv.y, kv.z, kv.w}, qq[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
-                for (int r = 0; r < SC_ROWS / 4; r++) acc[r] += qs[grp + 4 * r][dd] * kv;
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) acc[i][j] = acc[i][j] + qq[i] * kk[j];
             }
         }
-        const int key = key0 + kl;
-        if (key < c.Tc) {
 #pragma unroll
-            for (int r = 0; r < SC_ROWS / 4; r++) {
-                const int qi = q0 + grp + 4 * r;
-                if (qi < nq) {
-                    float v = acc[r] * g.inv_sqrt_dk;
+        for (int i = 0; i < 4; i++) {
+            const int qi = q0 + 4 * tr + i;
+            if (qi >= nq) continue;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int key = key0 + 4 * tk + j;
+                if (key < c.Tc) {
+                    float v = acc[i][j] * g.inv_sqrt_dk;
                     if (bh) v = v + bh[key];
                     Sl[(long long)qi * s_row + key] = v;
                 }
