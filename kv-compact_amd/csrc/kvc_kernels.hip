@@ -1375,8 +1375,13 @@ k_nnls_lh(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restric
 
 // one block per system; X (nq x n) and Y (nq x p) staged in (dynamic) LDS
 // when they fit its budget
-constexpr int LB_LDS_FLOATS = 24576;
+constexpr int LB_LDS_FLOATS = 40960;   // 160 KB
 
+// Staged X | Y (rows of width wp = round_up(n + p, 4)): 4 x 4 output tiles per
+// thread over the block tile grid, upper-triangular tiles only for X^T X
+// (a sequential dot product is symmetric bit for bit: the mirror entry is
+// written from the same sum). Without staging (too large for LDS): one
+// output per thread straight from global memory.
 __global__ void __launch_bounds__(256)
 k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ X,
            const float * __restrict__ Y, float * __restrict__ aug, const long long * __restrict__ aug_off,
@@ -1388,30 +1393,66 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     const long long hsX = (long long)g.nq_max * g.t_total;
     const float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
     const float * Yh = Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv;
-    extern __shared__ float xs[];
-    const bool staged = (long long)nq * w <= lds_floats;
-    if (staged) {
-        // xs[k][0..n) = X row k, xs[k][n..n+p) = Y row k
-        for (int e = threadIdx.x; e < nq * w; e += blockDim.x) {
-            const int k = e / w, j = e % w;
-            xs[e] = (j < n) ? Xh[(long long)k * g.t_total + j] : Yh[(long long)k * g.dv + (j - n)];
+    extern __shared__ __align__(16) float xs[];
+    const int wp = (w + 3) & ~3;
+    if ((long long)nq * wp > lds_floats) {
+        // column-major: entry (row i, column j) at Ag[j * n + i]
+        const long long total = (long long)n * w;
+        for (long long e = threadIdx.x; e < total; e += blockDim.x) {
+            const int j = (int)(e / n), i = (int)(e % n);
+            float s = 0.0f;
+            if (j < n) {
+                for (int k = 0; k < nq; k++) s += Xh[(long long)k * g.t_total + i] * Xh[(long long)k * g.t_total + j];
+            } else {
+                for (int k = 0; k < nq; k++) s += Xh[(long long)k * g.t_total + i] * Yh[(long long)k * g.dv + (j - n)];
+            }
+            if (i == j) s += g.ridge;
+            Ag[e] = s;
         }
-        __syncthreads();
+        return;
     }
-    const long long total = (long long)n * w;
-    // column-major: entry (row i, column j) at Ag[j * n + i]
-    for (long long e = threadIdx.x; e < total; e += blockDim.x) {
-        const int j = (int)(e / n), i = (int)(e % n);
-        float s = 0.0f;
-        if (staged) {
-            for (int k = 0; k < nq; k++) s += xs[k * w + i] * xs[k * w + j];
-        } else if (j < n) {
-            for (int k = 0; k < nq; k++) s += Xh[(long long)k * g.t_total + i] * Xh[(long long)k * g.t_total + j];
-        } else {
-            for (int k = 0; k < nq; k++) s += Xh[(long long)k * g.t_total + i] * Yh[(long long)k * g.dv + (j - n)];
+    // xs[k][0..n) = X row k, xs[k][n..n+p) = Y row k, zero padding to wp
+    for (int e = threadIdx.x; e < nq * wp; e += blockDim.x) {
+        const int k = e / wp, j = e % wp;
+        float v = 0.0f;
+        if (j < n) v = Xh[(long long)k * g.t_total + j];
+        else if (j < w) v = Yh[(long long)k * g.dv + (j - n)];
+        xs[e] = v;
+    }
+    __syncthreads();
+    const int nbi = (n + 3) >> 2, nbw = wp >> 2;
+    for (int e = threadIdx.x; e < nbi * nbw; e += blockDim.x) {
+        const int jb = e / nbi, ib = e % nbi;   // consecutive threads: consecutive row blocks
+        if (ib > jb) continue;
+        const int i0 = 4 * ib, j0 = 4 * jb;
+        float acc[4][4];
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
+        for (int k = 0; k < nq; k++) {
+            const float4 xi = *reinterpret_cast<const float4 *>(&xs[k * wp + i0]);
+            const float4 xj = *reinterpret_cast<const float4 *>(&xs[k * wp + j0]);
+            const float vi[4] = {xi.x, xi.y, xi.z, xi.w}, vj[4] = {xj.x, xj.y, xj.z, xj.w};
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) acc[a][b] = acc[a][b] + vi[a] * vj[b];
         }
-        if (i == j) s += g.ridge;
-        Ag[e] = s;
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+            const int i = i0 + a;
+            if (i >= n) continue;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const int j = j0 + b;
+                if (j >= w) continue;
+                float v = acc[a][b];
+                if (i == j) v += g.ridge;
+                Ag[(long long)j * n + i] = v;
+                if (j < n && j > i) Ag[(long long)i * n + j] = v;   // mirror (j, i)
+            }
+        }
     }
 }
 
@@ -2287,8 +2328,15 @@ void launch_beta_log(float * wb, long long n, hipStream_t st) {
 }
 
 void launch_ls_build(const Geom & g, const Work & w, hipStream_t st) {
-    const long long need = (long long)g.nq_max * (g.tc_max + g.dv);
-    const int lds_floats = need <= LB_LDS_FLOATS ? (int)need : 0;
+    // dynamic LDS beyond 64 KB needs the kernel attribute (once per process)
+    static int lds_cap = -1;
+    if (lds_cap < 0)
+        lds_cap = hipFuncSetAttribute(reinterpret_cast<const void *>(k_ls_build),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      LB_LDS_FLOATS * (int)sizeof(float)) == hipSuccess
+                      ? LB_LDS_FLOATS : 16384;
+    const long long need = (long long)g.nq_max * ((g.tc_max + g.dv + 3) & ~3);
+    const int lds_floats = need <= lds_cap ? (int)need : 0;
     hipLaunchKernelGGL(k_ls_build, dim3(g.n_chunks * g.H, g.L), dim3(256), (size_t)lds_floats * sizeof(float), st,
                        g, w.chunks, w.X, w.Y, w.aug, w.aug_off, lds_floats);
 }
