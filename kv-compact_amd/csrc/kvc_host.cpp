@@ -400,6 +400,7 @@ int run_diversity(hipStream_t st, const Plan & pl, const kv_compact_params & p, 
 
 int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact_params & p,
               const BatchIO & io, Carver & carver, Timing * tm) {
+    if (pl.nq_max > 256) return KV_COMPACT_E_UNSUPPORTED;   // chunk softmax keeps <= 256 row sums on chip
     Work w{};
     StatWork sw{};
     DivWork dw{};

@@ -113,6 +113,34 @@ __device__ __forceinline__ const float * query_row(const Geom & g, const float *
     return K + layer * g.ldK + (long long)(c.start + cheap_pos(qi, c.nq, c.Tc)) * ek;
 }
 
+// order-preserving key of a float score (unsigned order = float order; NaN excluded by callers)
+__device__ __forceinline__ unsigned score_key(float x) {
+    const unsigned b = __float_as_uint(x);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Wave-wide max / min of a 32-bit unsigned value through DPP row shifts and
+// row broadcasts (the result collects in lane 63).
+template <bool MAX>
+__device__ __forceinline__ unsigned dpp_reduce_u32(unsigned x) {
+    // lanes without a source (row edge, masked row) see the identity, which
+    // lets the move and the min/max fold into one DPP instruction
+    constexpr int ident = MAX ? 0 : -1;
+#define KVC_DPP_STEP(ctrl, rmask)                                                                  \
+    {                                                                                              \
+        const unsigned t = (unsigned)__builtin_amdgcn_update_dpp(ident, (int)x, ctrl, rmask, 0xf, false); \
+        x = MAX ? (t > x ? t : x) : (t < x ? t : x);                                               \
+    }
+    KVC_DPP_STEP(0x111, 0xf)   // row_shr:1
+    KVC_DPP_STEP(0x112, 0xf)   // row_shr:2
+    KVC_DPP_STEP(0x114, 0xf)   // row_shr:4
+    KVC_DPP_STEP(0x118, 0xf)   // row_shr:8
+    KVC_DPP_STEP(0x142, 0xa)   // row_bcast:15
+    KVC_DPP_STEP(0x143, 0xc)   // row_bcast:31
+#undef KVC_DPP_STEP
+    return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
+}
+
 __device__ __forceinline__ long long lS(const Geom & g) { return (long long)g.H * g.nq_max * g.T; }
 __device__ __forceinline__ long long hS(const Geom & g) { return (long long)g.nq_max * g.T; }
 
@@ -270,6 +298,32 @@ __device__ __forceinline__ float ref_row_max(const float * row, int n, float * r
 //   imp[j] = max / rms / mean over rows, accumulated in row order
 // E/rowsum are written when beta is solved. grid = (n_chunks * H, L)
 // ---------------------------------------------------------------------------
+// Row maximum in the reference's scan order for one row held by a wave:
+// the largest non-NaN value (or -inf), unless row[0] is NaN (then NaN);
+// every lane gets the result.
+__device__ __forceinline__ float wave_ref_row_max(const float * row, int n, int lane) {
+    float m = -INFINITY;
+    for (int j = lane; j < n; j += 64) {
+        const float v = row[j];
+        if (v == v && v > m) m = v;
+    }
+    const unsigned k = dpp_reduce_u32<true>(score_key(m));
+    const unsigned b = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;   // inverse of score_key
+    const float mm = __uint_as_float(b);
+    const float r0 = row[0];
+    if (r0 != r0) return r0;
+    return (mm > r0) ? mm : r0;
+}
+
+// Chunk softmax + per-key importance (math.h:142-248), for up to SM_MAXQ rows:
+//  1. row maxima, one wave per row;
+//  2. e = expf(s - max) over 64-key tiles: written unnormalised to A (and E),
+//     staged in LDS so that one thread per row adds its tile in key order;
+//  3. one thread per key: A = e * inv row by row, importance accumulated in
+//     row order (max / sum of squares / sum), finalised as the reference.
+// grid = (n_chunks * H, L)
+constexpr int SM_MAXQ = 256, SM_TILE = 64, SM_TROWS = 32;
+
 __global__ void __launch_bounds__(256)
 k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ S,
                      float * __restrict__ A, float * __restrict__ E, float * __restrict__ rowsum,
@@ -280,57 +334,63 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
     const float * Sh = S + layer * lS(g) + h * hS(g) + c.start;
     float * Ah = A + layer * lS(g) + h * hS(g) + c.start;
     float * Eh = E ? E + layer * lS(g) + h * hS(g) + c.start : nullptr;
-    __shared__ float red[16];
-    __shared__ float rmax[256], rinv[256];
+    __shared__ float rmax[SM_MAXQ], rinv[SM_MAXQ];
+    __shared__ float eb[SM_TROWS][SM_TILE + 1];
     const int nq = c.nq, n = c.Tc;
-    for (int base = 0; base < nq; base += 256) {
-        const int nb = min(256, nq - base);
-        for (int r = 0; r < nb; r++) {
-            const float m = ref_row_max(Sh + (base + r) * rs, n, red);
-            if (threadIdx.x == 0) rmax[r] = m;
-        }
-        __syncthreads();
-        for (int r = 0; r < nb; r++) {
-            const float mx = rmax[r];
-            const float * sr = Sh + (base + r) * rs;
-            float * ar = Ah + (base + r) * rs;
-            float * er = Eh ? Eh + (base + r) * rs : nullptr;
-            for (int j = threadIdx.x; j < n; j += blockDim.x) {
-                const float e = expf_ref(sr[j] - mx);
-                ar[j] = e;
-                if (er) er[j] = e;
-            }
-        }
-        __syncthreads();
-        if ((int)threadIdx.x < nb) {
-            const int r = base + threadIdx.x;
-            const float * ar = Ah + r * rs;
-            float sum = 0.0f;
-            for (int j = 0; j < n; j++) sum += ar[j];
-            if (rowsum) rowsum[(((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max + r] = sum;
-            rinv[threadIdx.x] = 1.0f / (sum + 1e-12f);
-        }
-        __syncthreads();
-        for (int r = 0; r < nb; r++) {
-            const float iv = rinv[r];
-            float * ar = Ah + (base + r) * rs;
-            for (int j = threadIdx.x; j < n; j += blockDim.x) ar[j] = ar[j] * iv;
-        }
-        __syncthreads();
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // 1. row maxima
+    for (int r = wv; r < nq; r += 4) {
+        const float m = wave_ref_row_max(Sh + r * rs, n, lane);
+        if (lane == 0) rmax[r] = m;
     }
+    __syncthreads();
+    // 2. exponentials and ordered row sums, 32 rows at a time
+    for (int r0 = 0; r0 < nq; r0 += SM_TROWS) {
+        const int nr = min(SM_TROWS, nq - r0);
+        float sum = 0.0f;   // row r0 + tid for tid < nr
+        for (int t0 = 0; t0 < n; t0 += SM_TILE) {
+            const int jn = min(SM_TILE, n - t0);
+            const int kk = tid & 63;
+            if (kk < jn) {
+                for (int rr = wv; rr < nr; rr += 4) {
+                    const int r = r0 + rr;
+                    const float e = expf_ref(Sh[r * rs + t0 + kk] - rmax[r]);
+                    eb[rr][kk] = e;
+                    Ah[r * rs + t0 + kk] = e;
+                    if (Eh) Eh[r * rs + t0 + kk] = e;
+                }
+            }
+            __syncthreads();
+            if (tid < nr) {
+                for (int j = 0; j < jn; j++) sum += eb[tid][j];
+            }
+            __syncthreads();
+        }
+        if (tid < nr) {
+            const int r = r0 + tid;
+            if (rowsum) rowsum[(((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max + r] = sum;
+            rinv[r] = 1.0f / (sum + 1e-12f);
+        }
+    }
+    __syncthreads();
+    // 3. normalise and aggregate per key in row order
     float * imph = imp + ((long long)layer * g.H + h) * g.T + c.start;
     const float inv_m = 1.0f / (float)nq;
-    for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    for (int j = tid; j < n; j += blockDim.x) {
         float acc = 0.0f;
-        if (g.score_method == 0) {
-            for (int qi = 0; qi < nq; qi++) { const float a = Ah[qi * rs + j]; if (a > acc) acc = a; }
-        } else if (g.score_method == 1) {
-            for (int qi = 0; qi < nq; qi++) { const float a = Ah[qi * rs + j]; acc += a * a; }
-            acc = sqrtf(acc * inv_m);
-        } else {
-            for (int qi = 0; qi < nq; qi++) acc += Ah[qi * rs + j];
-            acc *= inv_m;
+        for (int qi = 0; qi < nq; qi++) {
+            const float a = Ah[qi * rs + j] * rinv[qi];
+            Ah[qi * rs + j] = a;
+            if (g.score_method == 0) {
+                if (a > acc) acc = a;
+            } else if (g.score_method == 1) {
+                acc += a * a;
+            } else {
+                acc += a;
+            }
         }
+        if (g.score_method == 1) acc = sqrtf(acc * inv_m);
+        else if (g.score_method == 2) acc *= inv_m;
         imph[j] = acc;
     }
 }
@@ -674,27 +734,6 @@ k_select_topk(Geom g, const ChunkDesc * __restrict__ chunks, const float * __res
     write_flagged(fl, c.Tc, c.start, sel + (long long)layer * g.t_total + c.off);
 }
 
-// Wave-wide max / min of a 32-bit unsigned value through DPP row shifts and
-// row broadcasts (the result collects in lane 63).
-template <bool MAX>
-__device__ __forceinline__ unsigned dpp_reduce_u32(unsigned x) {
-    // lanes without a source (row edge, masked row) see the identity, which
-    // lets the move and the min/max fold into one DPP instruction
-    constexpr int ident = MAX ? 0 : -1;
-#define KVC_DPP_STEP(ctrl, rmask)                                                                  \
-    {                                                                                              \
-        const unsigned t = (unsigned)__builtin_amdgcn_update_dpp(ident, (int)x, ctrl, rmask, 0xf, false); \
-        x = MAX ? (t > x ? t : x) : (t < x ? t : x);                                               \
-    }
-    KVC_DPP_STEP(0x111, 0xf)   // row_shr:1
-    KVC_DPP_STEP(0x112, 0xf)   // row_shr:2
-    KVC_DPP_STEP(0x114, 0xf)   // row_shr:4
-    KVC_DPP_STEP(0x118, 0xf)   // row_shr:8
-    KVC_DPP_STEP(0x142, 0xa)   // row_bcast:15
-    KVC_DPP_STEP(0x143, 0xc)   // row_bcast:31
-#undef KVC_DPP_STEP
-    return (unsigned)__builtin_amdgcn_readlane((int)x, 63);
-}
 
 // ---------------------------------------------------------------------------
 // Diversity selection (api.cpp:175-233). The reference's greedy pass picks,
@@ -903,12 +942,6 @@ k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             }
         }
     }
-}
-
-// order-preserving key of a float score (NaN never reaches it)
-__device__ __forceinline__ unsigned score_key(float x) {
-    const unsigned b = __float_as_uint(x);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
 // The greedy pass of one unit, one wave; candidate position p sits in lane
