@@ -1751,6 +1751,35 @@ __device__ __forceinline__ float dot_seq(float val, const float * rowp, const fl
     return val;
 }
 
+// Four rows at once: val[t] -= lt[j][t] * xsb[j - j1][lane] for j = j1 .. j2-1,
+// each row's terms in ascending j (four independent sequential sums);
+// lt holds the four rows' entries interleaved (16 bytes per j).
+__device__ __forceinline__ void dot4_seq(float (&val)[4], const float4 * lt, const float (*xsb)[64], int j1, int j2,
+                                         int lane) {
+    int j = j1;
+    for (; j + 8 <= j2; j += 8) {
+        float4 l[8];
+        float y[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) { l[u] = lt[j + u]; y[u] = xsb[j - j1 + u][lane]; }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            val[0] = val[0] - l[u].x * y[u];
+            val[1] = val[1] - l[u].y * y[u];
+            val[2] = val[2] - l[u].z * y[u];
+            val[3] = val[3] - l[u].w * y[u];
+        }
+    }
+    for (; j < j2; j++) {
+        const float4 l = lt[j];
+        const float y = xsb[j - j1][lane];
+        val[0] = val[0] - l.x * y;
+        val[1] = val[1] - l.y * y;
+        val[2] = val[2] - l.z * y;
+        val[3] = val[3] - l.w * y;
+    }
+}
+
 // the same sum without the terms of steps whose pivot was skipped (skp[t] == 0)
 __device__ __forceinline__ float dot_seq_skip(float val, const float * rowp, const float (*xsb)[64], int n_terms,
                                               const float * skp, int lane) {
@@ -1796,10 +1825,78 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     const float * frow = rowb + BS_PAD;   // forward rows, unshifted
     float4 * frow4 = reinterpret_cast<float4 *>(rowb + BS_PAD);
 
+    float4 pf;
+    float pb;
+    if (!sk) {
+        // ---- forward, four rows at a time (no skipped pivots): the rows'
+        // multipliers sit interleaved in LDS; earlier results come from LDS
+        // (rows below 128 until row 128, then from registers) and the four
+        // sums run side by side; the 4 x 4 triangle finishes them in order.
+        __shared__ __align__(16) float4 lt[RG_ROWS];
+        float yr[BS_HIGH];
+        float4 qf[4];
+        float qb[4];
+        auto fetch = [&](int i0) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int r = permL[(i0 + t < n) ? i0 + t : i0];
+                qf[t] = reinterpret_cast<const float4 *>(LU + (unsigned)(r * RG_ROWS))[lane];
+                qb[t] = B[(unsigned)(vc * n + r)];
+            }
+        };
+        fetch(0);
+        for (int i0 = 0; i0 < n; i0 += 4) {
+            const int nr = min(4, n - i0);
+            lt[4 * lane + 0] = make_float4(qf[0].x, qf[1].x, qf[2].x, qf[3].x);
+            lt[4 * lane + 1] = make_float4(qf[0].y, qf[1].y, qf[2].y, qf[3].y);
+            lt[4 * lane + 2] = make_float4(qf[0].z, qf[1].z, qf[2].z, qf[3].z);
+            lt[4 * lane + 3] = make_float4(qf[0].w, qf[1].w, qf[2].w, qf[3].w);
+            float val[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) val[t] = act ? qb[t] : 0.0f;
+            if (i0 + 4 < n) fetch(i0 + 4);
+            __builtin_amdgcn_wave_barrier();
+            if (i0 <= BS_HIGH) {
+                dot4_seq(val, lt, xs, 0, i0, lane);
+            } else {
+#pragma unroll
+                for (int j = 0; j < BS_HIGH; j++) {
+                    const float4 l = lt[j];
+                    val[0] = val[0] - l.x * yr[j];
+                    val[1] = val[1] - l.y * yr[j];
+                    val[2] = val[2] - l.z * yr[j];
+                    val[3] = val[3] - l.w * yr[j];
+                }
+                dot4_seq(val, lt + BS_HIGH, xs, 0, i0 - BS_HIGH, lane);
+            }
+            // the block's own triangle, row by row
+            float yn[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (q < t) val[t] = val[t] - reinterpret_cast<const float *>(&lt[i0 + q])[t] * yn[q];
+                yn[t] = val[t];
+            }
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                if (t >= nr) break;
+                const int i = i0 + t;
+                xs[i < BS_HIGH ? i : i - BS_HIGH][lane] = yn[t];
+                if (act) Yt[(unsigned)(i * g.dv + v)] = yn[t];
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (i0 + 4 == BS_HIGH && n > BS_HIGH) {
+#pragma unroll
+                for (int j = 0; j < BS_HIGH; j++) yr[j] = xs[j][lane];
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
+    } else {
     // ---- forward: rows [0, lb) from LDS, then rows [lb, n) with [0, lb) in registers
     const int lb = n < BS_HIGH ? n : BS_HIGH;
-    float4 pf = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[0] * RG_ROWS))[lane];
-    float pb = B[(unsigned)(vc * n + permL[0])];
+    pf = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[0] * RG_ROWS))[lane];
+    pb = B[(unsigned)(vc * n + permL[0])];
     for (int i = 0; i < lb; i++) {
         frow4[lane] = pf;
         float val = act ? pb : 0.0f;
@@ -1841,6 +1938,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             if (act) Yt[(unsigned)(i * g.dv + v)] = val;
             __builtin_amdgcn_wave_barrier();
         }
+    }
     }
 
     // ---- backward: rows [hb, n) from LDS, then rows [0, hb) with [hb, n) in
