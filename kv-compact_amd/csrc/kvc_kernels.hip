@@ -1585,22 +1585,23 @@ __device__ __forceinline__ void lu_factor_panel(LuShared & sh, float (&a)[RG_SLO
         if (col >= n) break;
         // lane candidate: largest |a| (bit pattern of a non-negative float),
         // ties to the smallest logical index; NaN rows never qualify
+        // The row at logical col is itself a candidate with the smallest
+        // logical index, so "first maximum, replacing only on strictly greater"
+        // is the first-index maximum over the live rows, except that a NaN on
+        // the diagonal keeps col (every comparison against it fails).
         unsigned bk = 0;
         int bl = 0x7fffffff;
-        float v0 = 0.0f;
-        bool has0 = false;
+        bool nan0 = false;
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++) {
             const float v = fabsf(a[s][jj]);
             const unsigned kb = __float_as_uint(v);
             if (live[s] && v == v && (kb > bk || (kb == bk && li[s] < bl))) { bk = kb; bl = li[s]; }
-            if (li[s] == col) { v0 = a[s][jj]; has0 = true; }
+            nan0 = nan0 || (li[s] == col && v != v);
         }
         const unsigned gmax = dpp_reduce_u32<true>(bk);
         const unsigned glo = dpp_reduce_u32<false>(bk == gmax ? (unsigned)bl : 0x7fffffffu);
-        const unsigned long long m0 = __ballot(has0);
-        const float a0 = fabsf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v0), __builtin_ctzll(m0))));
-        const int mr = (a0 == a0 && __uint_as_float(gmax) > a0) ? (int)glo : col;
+        const int mr = __ballot(nan0) ? col : (int)glo;
         int slot_l = -1;
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++)
