@@ -526,6 +526,10 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     }
     int status = 0;
     if (hipMemcpy(&status, w.status, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return KV_COMPACT_E_DEVICE;
+    if (status & 2) {
+        fprintf(stderr, "[kv-compact] LU step wait exceeded its bound\n");
+        return KV_COMPACT_E_DEVICE;
+    }
     if (status) return KV_COMPACT_E_UNSUPPORTED;
     for (int i = 0; i < ST_COUNT; i++) {
         float ms = 0.0f;

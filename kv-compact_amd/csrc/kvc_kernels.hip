@@ -1494,178 +1494,234 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 // (n x (n + p)), math.h:494-556. Storage is column-major: entry (r, j) at
 // a[j * n + r] (M is symmetric, B is stored transposed).
 //
-// k_ge_lu (n <= 256): blocked LU of the n x n matrix with the reference's
-// partial pivoting, in registers. 16 waves own 16-column strips; lane l owns
-// rows l, l+64, l+128, l+192 (physical rows; swaps are a logical<->physical
-// permutation). Panel k (strip k) is factored by wave k alone, in its own
-// registers: pivot search (DPP reductions), multipliers, update of the
-// panel's remaining columns, step by step. Every later wave applies the
-// panel's 16 steps, in order, to its own strip one phase later, so that the
-// factorization of panel k+1 (which first applies panel k to itself) runs
-// beside the other strips' update with panel k. Each element therefore
-// receives exactly the reference's sequence of a -= f * u operations.
+// k_ge_lu (n <= 256): LU of the n x n matrix with the reference's partial
+// pivoting, in registers, as a column-cyclic dataflow. Wave w owns columns
+// w, w + 16, ..., w + 240; lane l owns rows l, l+64, l+128, l+192 (physical
+// rows; swaps are a logical<->physical permutation kept in LDS). Step c is
+// produced by the owner of column c: pivot search on that column (DPP
+// reductions), the multipliers a[r][c] / pivot, which it publishes through a
+// 32-slot LDS ring with a per-slot step flag. Every wave consumes the steps
+// in order, applying step c to each of its columns j > c (a -= f * u, the
+// pivot row's u read from its own registers), so each element receives
+// exactly the reference's sequence of updates. The owner of column c + 1
+// applies step c to that column first and publishes step c + 1 before it
+// updates its other columns, so the serial chain per step is one column's
+// update, one pivot search and one division per row; everything else runs
+// beside it. A wave can be at most 17 steps behind the newest published step
+// (it owns one of any 16 consecutive columns and publishes that step only
+// after consuming the step before), so the 32-slot ring is never overwritten
+// before every wave has read it, and every flag a wave waits for is
+// published by a wave that only waits for earlier flags.
 // Output per system: one 256 x 256 array by physical row r holding, left of
-// the step at which r became the pivot, r's multipliers (by step), and from
-// that step on, r's U row (a pivot row is never updated again, so the strips
-// write it once at the end); plus the final permutation and the
-// skipped-pivot flags.
-// The right-hand sides are not touched here: the reference's elimination of
-// them is forward substitution with the final permutation (ascending steps),
-// done with the back substitution in k_ge_solve.
+// the step at which r became the pivot, r's multipliers (by step; the
+// producer stores them over the eliminated column in registers), and from
+// that step on, r's U row; plus the final permutation and the skipped-pivot
+// flags. The right-hand sides are not touched here: the reference's
+// elimination of them is forward substitution with the final permutation
+// (ascending steps), done with the back substitution in k_ge_solve.
 // ---------------------------------------------------------------------------
-constexpr int RG_ROWS = 256, RG_STRIP = 16, RG_WAVES = 16, RG_SLOTS = 4;
+constexpr int RG_ROWS = 256, RG_WAVES = 16, RG_COLS = 16, RG_SLOTS = 4;
 constexpr int RG_THREADS = RG_WAVES * 64;
-
-template <int S>
-__device__ __forceinline__ void rg_lane_strip(const float (&a)[RG_SLOTS][RG_STRIP], int src_lane, float (&sp)[RG_STRIP]) {
-#pragma unroll
-    for (int jj = 0; jj < RG_STRIP; jj++)
-        sp[jj] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[S][jj]), src_lane));
-}
-
-__device__ __forceinline__ void rg_pivot_values(const float (&a)[RG_SLOTS][RG_STRIP], int P, float (&sp)[RG_STRIP]) {
-    const int src = P & 63, slot = P >> 6;
-    if (slot == 0) rg_lane_strip<0>(a, src, sp);
-    else if (slot == 1) rg_lane_strip<1>(a, src, sp);
-    else if (slot == 2) rg_lane_strip<2>(a, src, sp);
-    else rg_lane_strip<3>(a, src, sp);
-}
+constexpr int LU_RING = 32;          // > 17 outstanding steps
+constexpr int LU_TROWS = 32;         // rows per pass of the transposed output write
+constexpr int LU_SPIN_LIMIT = 1 << 22;   // polls per wave over the whole factorization
 
 struct LuShared {
-    float fmul[2][RG_STRIP][RG_ROWS];     // multipliers of the last two panels
-    int inv[RG_ROWS], pivrow[RG_ROWS];    // logical index of each physical row; pivot row of each step
+    union {
+        struct {
+            float4 fm[LU_RING][64];  // step c's multipliers in slot c % LU_RING: lane l's four rows
+            int piv[LU_RING];        // step's pivot row; +256 when the step was skipped
+            int flag[LU_RING];       // step number published in the slot
+        } ring;
+        float tile[LU_TROWS][RG_ROWS + 1];   // output staging at the end
+    } u;
+    union {
+        unsigned w[64];              // logical index of rows l, l+64, l+128, l+192 as bytes of w[l]
+        unsigned char b[RG_ROWS];
+    } inv;
+    int phys[RG_ROWS];               // physical row of each logical index
+    int pivrow[RG_ROWS];
     unsigned char skip[RG_ROWS];
 };
 
-// Apply panel kp's steps (columns 16 kp .. 16 kp + 15), in order, to this
-// wave's strip.
-__device__ __forceinline__ void lu_apply_panel(const LuShared & sh, float (&a)[RG_SLOTS][RG_STRIP],
-                                               bool (&live)[RG_SLOTS], int kp, int n, int lane) {
-    const int c0 = kp * RG_STRIP, buf = kp & 1;
-    const int steps = min(RG_STRIP, n - c0);
-    // lane q holds step q's pivot row and skip flag (read once per panel)
-    const int pv = (lane < steps) ? sh.pivrow[c0 + lane] : 0;
-    const int sk = (lane < steps) ? (int)sh.skip[c0 + lane] : 1;
-    for (int jj = 0; jj < steps; jj++) {
-        const int P = __builtin_amdgcn_readlane(pv, jj);
-        if (!__builtin_amdgcn_readlane(sk, jj)) {
-            float sp[RG_STRIP];
-            rg_pivot_values(a, P, sp);
-#pragma unroll
-            for (int s = 0; s < RG_SLOTS; s++) {
-                const int r = lane + 64 * s;
-                if (live[s] && r != P) {
-                    const float f = sh.fmul[buf][jj][r];
-#pragma unroll
-                    for (int q = 0; q < RG_STRIP; q++) a[s][q] = a[s][q] - f * sp[q];
-                }
-            }
-        }
-#pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++) live[s] = live[s] && (lane + 64 * s != P);
-    }
+__device__ __forceinline__ int lu_inv_byte(int r) { return (r & 63) * 4 + (r >> 6); }
+
+__device__ __forceinline__ float lu_pick(const float (&v)[RG_SLOTS], int s) {
+    return s == 0 ? v[0] : (s == 1 ? v[1] : (s == 2 ? v[2] : v[3]));
 }
 
-// Factor panel k (this wave's strip, in registers) step by step in the
-// reference's order: pivot = first row (logical order) of largest |a| among
-// the rows not yet used, replacing the diagonal only when strictly larger and
-// never NaN; pivots below 1e-12 in magnitude skip the step (math.h:501-523).
-__device__ __forceinline__ void lu_factor_panel(LuShared & sh, float (&a)[RG_SLOTS][RG_STRIP],
-                                                bool (&live)[RG_SLOTS], int k, int n, int lane,
-                                                float * __restrict__ LU) {
-    const int c0 = k * RG_STRIP, buf = k & 1;
+// Publish step c1 from its column's values col[] (steps < c1 applied): pivot =
+// first row in logical order of largest |a| among the rows not yet used,
+// replacing the diagonal only when strictly larger and never NaN (a NaN
+// diagonal keeps the diagonal, every comparison against it failing); pivots
+// below 1e-12 in magnitude skip the step (math.h:507-527). The rows still
+// below the pivot get their multipliers (0 for a skipped step) in col[].
+__device__ __forceinline__ void lu_produce(LuShared & sh, float (&col)[RG_SLOTS], const bool (&live)[RG_SLOTS],
+                                           int c1, int lane) {
+    const unsigned ivw = sh.inv.w[lane];
+    const int physc = __builtin_amdgcn_readfirstlane(sh.phys[c1]);
     int li[RG_SLOTS];
-#pragma unroll
-    for (int s = 0; s < RG_SLOTS; s++) li[s] = sh.inv[lane + 64 * s];
-    int my_piv = 0, my_skip = 0;   // lane jj keeps step jj's pivot row and skip flag
-    unsigned lmask[RG_SLOTS] = {0u, 0u, 0u, 0u};   // bit jj: the slot's row was below the pivot at step jj
-#pragma unroll
-    for (int jj = 0; jj < RG_STRIP; jj++) {
-        const int col = c0 + jj;
-        if (col >= n) break;
-        // lane candidate: largest |a| (bit pattern of a non-negative float),
-        // ties to the smallest logical index; NaN rows never qualify
-        // The row at logical col is itself a candidate with the smallest
-        // logical index, so "first maximum, replacing only on strictly greater"
-        // is the first-index maximum over the live rows, except that a NaN on
-        // the diagonal keeps col (every comparison against it fails).
-        unsigned bk = 0;
-        int bl = 0x7fffffff;
-        bool nan0 = false;
-#pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++) {
-            const float v = fabsf(a[s][jj]);
-            const unsigned kb = __float_as_uint(v);
-            if (live[s] && v == v && (kb > bk || (kb == bk && li[s] < bl))) { bk = kb; bl = li[s]; }
-            nan0 = nan0 || (li[s] == col && v != v);
-        }
-        const unsigned gmax = dpp_reduce_u32<true>(bk);
-        const unsigned glo = dpp_reduce_u32<false>(bk == gmax ? (unsigned)bl : 0x7fffffffu);
-        const int mr = __ballot(nan0) ? col : (int)glo;
-        int slot_l = -1;
-#pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++)
-            if (li[s] == mr) slot_l = s;
-        const unsigned long long mp = __ballot(slot_l >= 0);
-        const int laneP = __builtin_ctzll(mp);
-        const int slotP = __builtin_amdgcn_readlane(slot_l, laneP);
-        const int P = laneP + 64 * slotP;
-#pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++) li[s] = (li[s] == col) ? mr : ((li[s] == mr) ? col : li[s]);
-        float sp[RG_STRIP];
-        rg_pivot_values(a, P, sp);
-        const float piv = sp[jj];
-        const bool elim = !(fabsf(piv) < 1e-12f);
-#pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++) {
-            const int r = lane + 64 * s;
-            const bool upd = elim && live[s] && r != P;
-            const float f = upd ? a[s][jj] / piv : 0.0f;
-            if (upd) {
-#pragma unroll
-                for (int q = jj + 1; q < RG_STRIP; q++) a[s][q] = a[s][q] - f * sp[q];
-            }
-            sh.fmul[buf][jj][r] = f;
-            if (live[s] && r != P) lmask[s] |= 1u << jj;
-            live[s] = live[s] && r != P;
-        }
-        if (lane == jj) {
-            my_piv = P;
-            my_skip = elim ? 0 : 1;
-        }
-    }
-    if (lane < RG_STRIP && c0 + lane < n) {
-        sh.pivrow[c0 + lane] = my_piv;
-        sh.skip[c0 + lane] = (unsigned char)my_skip;
-    }
-    // multipliers of this panel, only where the row was still below the pivot
-    // (the rest of those columns belongs to the row's U part)
+    unsigned key[RG_SLOTS];
+    bool nanc = false;
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) {
-        const int r = lane + 64 * s;
-        float * dst = LU + (unsigned)(r * RG_ROWS + c0);
-#pragma unroll
-        for (int jj = 0; jj < RG_STRIP; jj++)
-            if (lmask[s] & (1u << jj)) dst[jj] = sh.fmul[buf][jj][r];
-        sh.inv[r] = li[s];
+        li[s] = (int)((ivw >> (8 * s)) & 255u);
+        const float v = fabsf(col[s]);
+        key[s] = (live[s] && v == v) ? __float_as_uint(v) : 0u;
+        nanc = nanc || (li[s] == c1 && v != v);
     }
+    const unsigned kmax = max(max(key[0], key[1]), max(key[2], key[3]));
+    const unsigned gmax = dpp_reduce_u32<true>(kmax);
+    int mr, P;
+    if (__ballot(nanc) || gmax == 0u) {
+        // every live row is +-0 or NaN, or the diagonal is NaN: the diagonal stays
+        mr = c1;
+        P = physc;
+    } else {
+        // first logical index among the rows at the maximum, with its physical row
+        unsigned cand = 0xffffu;
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            const unsigned e = ((unsigned)li[s] << 8) | (unsigned)(lane + 64 * s);
+            cand = min(cand, key[s] == gmax ? e : 0xffffu);
+        }
+        const unsigned long long m = __ballot(cand != 0xffffu);
+        unsigned v;
+        if ((m & (m - 1)) == 0ull) v = (unsigned)__builtin_amdgcn_readlane((int)cand, __builtin_ctzll(m));
+        else v = dpp_reduce_u32<false>(cand);
+        mr = (int)(v >> 8);
+        P = (int)(v & 255u);
+    }
+    const float piv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lu_pick(col, P >> 6)), P & 63));
+    const bool elim = !(fabsf(piv) < 1e-12f);
+    float f[RG_SLOTS];
+#pragma unroll
+    for (int s = 0; s < RG_SLOTS; s++) {
+        const bool below = live[s] && (lane + 64 * s) != P;
+        const float q = col[s] / piv;
+        f[s] = (elim && below) ? q : 0.0f;
+        if (below) col[s] = f[s];
+    }
+    const int slot = c1 & (LU_RING - 1);
+    sh.u.ring.fm[slot][lane] = make_float4(f[0], f[1], f[2], f[3]);
+    if (lane == 0) {
+        sh.u.ring.piv[slot] = P | (elim ? 0 : 256);
+        sh.inv.b[lu_inv_byte(P)] = (unsigned char)c1;
+        sh.inv.b[lu_inv_byte(physc)] = (unsigned char)mr;   // P == physc when mr == c1
+        sh.phys[c1] = P;
+        sh.phys[mr] = physc;
+        sh.pivrow[c1] = P;
+        sh.skip[c1] = elim ? 0 : 1;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    if (lane == 0) __hip_atomic_store(&sh.u.ring.flag[slot], c1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// The owner of column c + 1 (register column Q): apply step c to it, then
+// publish step c + 1.
+template <int Q>
+__device__ __forceinline__ void lu_next_column(LuShared & sh, float (&a)[RG_SLOTS][RG_COLS],
+                                               const bool (&live)[RG_SLOTS], const float (&f)[RG_SLOTS],
+                                               bool skip, int P, int c1, int lane) {
+    float col[RG_SLOTS];
+#pragma unroll
+    for (int s = 0; s < RG_SLOTS; s++) col[s] = a[s][Q];
+    if (!skip) {
+        const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lu_pick(col, P >> 6)), P & 63));
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++)
+            if (live[s]) col[s] = col[s] - f[s] * u;
+    }
+    lu_produce(sh, col, live, c1, lane);
+#pragma unroll
+    for (int s = 0; s < RG_SLOTS; s++) a[s][Q] = col[s];
+}
+
+template <int S>
+__device__ __forceinline__ void lu_pivot_row(const float (&a)[RG_SLOTS][RG_COLS], int lP, unsigned act,
+                                             float (&u)[RG_COLS]) {
+#pragma unroll
+    for (int q = 0; q < RG_COLS; q++)
+        if (act & (1u << q)) u[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[S][q]), lP));
+}
+
+// Steps 16 B .. 16 B + 15 (register column B is the wave's column in that
+// range). Columns j = w + 16 q receive step c when j >= c + 2 (column c + 1
+// was updated by its owner before publishing step c + 1).
+template <int B>
+__device__ __forceinline__ void lu_steps(LuShared & sh, float (&a)[RG_SLOTS][RG_COLS], bool (&live)[RG_SLOTS],
+                                         int n, int w, int lane, int & spins, int * __restrict__ status) {
+    for (int i = 0; i < RG_COLS; i++) {
+        const int c = RG_COLS * B + i;
+        if (c >= n) break;   // (a break, not a return: one exit path keeps the register assignment)
+        const int slot = c & (LU_RING - 1);
+        // bounded wait: past the limit the wave stops waiting and reports
+        // through *status (the host turns that into a device error)
+        while (__hip_atomic_load(&sh.u.ring.flag[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != c) {
+            if (++spins > LU_SPIN_LIMIT) {
+                if (lane == 0) atomicOr(status, 2);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        const int pv = __builtin_amdgcn_readfirstlane(sh.u.ring.piv[slot]);
+        const float4 f4 = sh.u.ring.fm[slot][lane];
+        const float f[RG_SLOTS] = {f4.x, f4.y, f4.z, f4.w};
+        const int P = pv & 255;
+        const bool skip = (pv & 256) != 0;
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) live[s] = live[s] && (lane + 64 * s) != P;
+        if (c + 1 < n && w == ((c + 1) & (RG_COLS - 1))) {
+            __builtin_amdgcn_s_setprio(3);
+            if (w != 0) lu_next_column<B>(sh, a, live, f, skip, P, c + 1, lane);
+            else if constexpr (B + 1 < RG_COLS) lu_next_column<B + 1>(sh, a, live, f, skip, P, c + 1, lane);
+            __builtin_amdgcn_s_setprio(0);
+        }
+        if (skip) continue;
+        // active register columns of this step (uniform)
+        unsigned act = 0;
+#pragma unroll
+        for (int q = B + 2; q < RG_COLS; q++) act |= 1u << q;
+        if constexpr (B + 1 < RG_COLS)
+            if (!(i == RG_COLS - 1 && w == 0)) act |= 1u << (B + 1);
+        if (w >= i + 2) act |= 1u << B;
+        if (act == 0) continue;
+        float u[RG_COLS];
+        const int lP = P & 63;
+        switch (P >> 6) {
+            case 0: lu_pivot_row<0>(a, lP, act, u); break;
+            case 1: lu_pivot_row<1>(a, lP, act, u); break;
+            case 2: lu_pivot_row<2>(a, lP, act, u); break;
+            default: lu_pivot_row<3>(a, lP, act, u); break;
+        }
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            if (live[s]) {
+#pragma unroll
+                for (int q = B; q < RG_COLS; q++)
+                    if (act & (1u << q)) a[s][q] = a[s][q] - f[s] * u[q];
+            }
+        }
+    }
+    if constexpr (B + 1 < RG_COLS) lu_steps<B + 1>(sh, a, live, n, w, lane, spins, status);
 }
 
 __global__ void __launch_bounds__(RG_THREADS)
 k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
         const long long * __restrict__ aug_off, int * __restrict__ perm_out, unsigned char * __restrict__ skip_out,
-        float * __restrict__ LU_all) {
+        float * __restrict__ LU_all, int * __restrict__ status) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const int n = c.tc;
-    if (n > RG_ROWS) return;
+    if (n > RG_ROWS || n < 1) return;
     const long long sys = ((long long)layer * g.n_chunks + c_idx) * g.H + h;
     const float * A = aug + aug_off[sys];
     float * LU = LU_all + sys * (long long)RG_ROWS * RG_ROWS;
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     __shared__ LuShared sh;
 
-    float a[RG_SLOTS][RG_STRIP];
+    float a[RG_SLOTS][RG_COLS];
     bool live[RG_SLOTS];
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) {
@@ -1673,43 +1729,53 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
         live[s] = r < n;
         const int rc = r < n ? r : n - 1;
 #pragma unroll
-        for (int jj = 0; jj < RG_STRIP; jj++) {
-            const int j = RG_STRIP * w + jj;
+        for (int q = 0; q < RG_COLS; q++) {
+            const int j = w + RG_WAVES * q;
             const float v = A[(unsigned)((j < n ? j : n - 1) * n + rc)];
-            a[s][jj] = (r < n && j < n) ? v : 0.0f;
+            a[s][q] = (r < n && j < n) ? v : 0.0f;
         }
     }
-    if (tid < RG_ROWS) sh.inv[tid] = tid;
+    if (tid < RG_ROWS) {
+        sh.phys[tid] = tid;
+        sh.inv.b[lu_inv_byte(tid)] = (unsigned char)tid;
+    }
+    if (tid < LU_RING) sh.u.ring.flag[tid] = -1;
     __syncthreads();
-    const int n_panels = (n + RG_STRIP - 1) / RG_STRIP;
-    // phase k: strips w >= k apply panel k-1, then wave k factors panel k
-    for (int k = 0; k < n_panels; k++) {
-        if (w == k) __builtin_amdgcn_s_setprio(3);
-        if (k > 0 && w >= k && w < n_panels) lu_apply_panel(sh, a, live, k - 1, n, lane);
-        if (w == k) {
-            lu_factor_panel(sh, a, live, k, n, lane, LU);
-            __builtin_amdgcn_s_setprio(0);
-        }
-        __syncthreads();
+    if (w == 0) {
+        float col[RG_SLOTS];
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) col[s] = a[s][0];
+        lu_produce(sh, col, live, 0, lane);
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) a[s][0] = col[s];
     }
+    int spins = 0;
+    lu_steps<0>(sh, a, live, n, w, lane, spins, status);
+    __syncthreads();
     if (tid < n) {
         perm_out[sys * (long long)g.tc_max + tid] = sh.pivrow[tid];
         skip_out[sys * (long long)g.tc_max + tid] = sh.skip[tid];
     }
-    // U parts: row r from its pivot step on (sh.inv[r] is that step now)
-    if (RG_STRIP * w < n) {
+    // every entry is final in registers: multipliers left of each row's pivot
+    // step, U from it on; rows go out through LDS, LU_TROWS at a time, as
+    // contiguous row segments
 #pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++) {
-            const int r = lane + 64 * s;
-            if (r < n) {
-                const int st = sh.inv[r];
-                float * dst = LU + (unsigned)(r * RG_ROWS + RG_STRIP * w);
+    for (int s = 0; s < RG_SLOTS; s++) {
 #pragma unroll
-                for (int q = 0; q < RG_STRIP; q++) {
-                    const int c = RG_STRIP * w + q;
-                    if (c >= st && c < n) dst[q] = a[s][q];
-                }
+        for (int half = 0; half < 64 / LU_TROWS; half++) {
+            const int r0 = 64 * s + LU_TROWS * half;
+            if (r0 >= n) break;
+            const int lr = lane - LU_TROWS * half;
+            if (lr >= 0 && lr < LU_TROWS) {
+#pragma unroll
+                for (int q = 0; q < RG_COLS; q++) sh.u.tile[lr][w + RG_WAVES * q] = a[s][q];
             }
+            __syncthreads();
+            for (int e = tid; e < LU_TROWS * RG_ROWS; e += RG_THREADS) {
+                const int rr = e / RG_ROWS, j = e % RG_ROWS;
+                if (r0 + rr < n && j < n) LU[(unsigned)((r0 + rr) * RG_ROWS + j)] = sh.u.tile[rr][j];
+            }
+            __syncthreads();
         }
     }
 }
@@ -2475,7 +2541,7 @@ void launch_ls_build(const Geom & g, const Work & w, hipStream_t st) {
 
 void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st) {
     hipLaunchKernelGGL(k_ge_lu, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
-                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU);
+                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, w.status);
 }
 
 void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st) {
