@@ -67,6 +67,7 @@ struct Work {
     float * wts;      // [T] R-KV weights (nullptr when disabled)
     int   * status;   // [1] nonzero: a kernel met a case this build refuses
     int   * refine_active; // [L][n_chunks] 1 while the unit's refinement rounds continue
+    int   * lu_redo;  // [L][n_chunks][H] 1: the system's LU is redone with masked updates
     ChunkDesc * chunks;  // [n_chunks + 2]; then all T keys, then the kept keys (statistics)
 };
 

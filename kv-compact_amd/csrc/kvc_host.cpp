@@ -323,6 +323,7 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     ww.chunks = cv.take<ChunkDesc>(pl.chunks.size());
     ww.status = cv.take<int>(1);
     ww.refine_active = cv.take<int>(L * nc);
+    ww.lu_redo = cv.take<int>(L * nc * H);
     if (div) {
         const size_t units = L * nc;
         DivWork d{};

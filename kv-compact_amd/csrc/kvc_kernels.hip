@@ -1512,6 +1512,17 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 // after consuming the step before), so the 32-slot ring is never overwritten
 // before every wave has read it, and every flag a wave waits for is
 // published by a wave that only waits for earlier flags.
+//
+// Two variants. The unmasked one applies each step to every row with the
+// published multiplier, which is 0 for the rows no longer below the pivot, so
+// those rows (already final) see a -= 0 * u. That leaves them unchanged
+// whenever u is finite and a is not -0: the input is checked for -0 and
+// non-finite entries, and no entry ever becomes -0 (x - y is -0 only for
+// x = -0), and a non-finite u would leave a non-finite final entry in its
+// pivot row, so a system whose final entries are all finite was factored
+// exactly. Any other system is flagged and redone by the masked variant,
+// which skips the rows no longer below the pivot.
+//
 // Output per system: one 256 x 256 array by physical row r holding, left of
 // the step at which r became the pivot, r's multipliers (by step; the
 // producer stores them over the eliminated column in registers), and from
@@ -1550,22 +1561,30 @@ __device__ __forceinline__ float lu_pick(const float (&v)[RG_SLOTS], int s) {
     return s == 0 ? v[0] : (s == 1 ? v[1] : (s == 2 ? v[2] : v[3]));
 }
 
+// -0, +-inf or NaN
+__device__ __forceinline__ bool lu_unsafe(float x) {
+    const unsigned b = __float_as_uint(x);
+    return b == 0x80000000u || (b & 0x7f800000u) == 0x7f800000u;
+}
+
 // Publish step c1 from its column's values col[] (steps < c1 applied): pivot =
-// first row in logical order of largest |a| among the rows not yet used,
-// replacing the diagonal only when strictly larger and never NaN (a NaN
-// diagonal keeps the diagonal, every comparison against it failing); pivots
-// below 1e-12 in magnitude skip the step (math.h:507-527). The rows still
-// below the pivot get their multipliers (0 for a skipped step) in col[].
-__device__ __forceinline__ void lu_produce(LuShared & sh, float (&col)[RG_SLOTS], const bool (&live)[RG_SLOTS],
-                                           int c1, int lane) {
+// first row in logical order of largest |a| among the rows not yet used
+// (logical index >= c1), replacing the diagonal only when strictly larger and
+// never NaN (a NaN diagonal keeps the diagonal, every comparison against it
+// failing); pivots below 1e-12 in magnitude skip the step (math.h:507-527).
+// The rows still below the pivot get their multipliers (0 for a skipped step)
+// in col[]; every other row's published multiplier is 0.
+__device__ __forceinline__ void lu_produce(LuShared & sh, float (&col)[RG_SLOTS], int c1, int n, int lane) {
     const unsigned ivw = sh.inv.w[lane];
     const int physc = __builtin_amdgcn_readfirstlane(sh.phys[c1]);
     int li[RG_SLOTS];
+    bool live[RG_SLOTS];
     unsigned key[RG_SLOTS];
     bool nanc = false;
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) {
         li[s] = (int)((ivw >> (8 * s)) & 255u);
+        live[s] = li[s] >= c1 && lane + 64 * s < n;
         const float v = fabsf(col[s]);
         key[s] = (live[s] && v == v) ? __float_as_uint(v) : 0u;
         nanc = nanc || (li[s] == c1 && v != v);
@@ -1617,38 +1636,70 @@ __device__ __forceinline__ void lu_produce(LuShared & sh, float (&col)[RG_SLOTS]
     if (lane == 0) __hip_atomic_store(&sh.u.ring.flag[slot], c1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// The owner of column c + 1 (register column Q): apply step c to it, then
-// publish step c + 1.
-template <int Q>
-__device__ __forceinline__ void lu_next_column(LuShared & sh, float (&a)[RG_SLOTS][RG_COLS],
+// The owner of column c + 1 (register column Q): a copy of that column with
+// step c applied, from which step c + 1 is published; the copy (multipliers
+// below the new pivot) replaces the column after the wave's own update with
+// step c, which computes the same values for it.
+template <int Q, bool MASKED>
+__device__ __forceinline__ void lu_next_column(LuShared & sh, const float (&a)[RG_SLOTS][RG_COLS],
                                                const bool (&live)[RG_SLOTS], const float (&f)[RG_SLOTS],
-                                               bool skip, int P, int c1, int lane) {
-    float col[RG_SLOTS];
+                                               bool skip, int P, int c1, int n, int lane, float (&col)[RG_SLOTS]) {
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) col[s] = a[s][Q];
     if (!skip) {
         const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lu_pick(col, P >> 6)), P & 63));
 #pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++)
-            if (live[s]) col[s] = col[s] - f[s] * u;
+        for (int s = 0; s < RG_SLOTS; s++) {
+            if (MASKED) {
+                if (live[s]) col[s] = col[s] - f[s] * u;
+            } else {
+                col[s] = col[s] - f[s] * u;
+            }
+        }
     }
-    lu_produce(sh, col, live, c1, lane);
-#pragma unroll
-    for (int s = 0; s < RG_SLOTS; s++) a[s][Q] = col[s];
+    lu_produce(sh, col, c1, n, lane);
 }
 
-template <int S>
-__device__ __forceinline__ void lu_pivot_row(const float (&a)[RG_SLOTS][RG_COLS], int lP, unsigned act,
-                                             float (&u)[RG_COLS]) {
+// u[q] = a[P][q] for the register columns q >= Q0 (pivot row in slot S, lane lP)
+template <int S, int Q0>
+__device__ __forceinline__ void lu_read_row(const float (&a)[RG_SLOTS][RG_COLS], int lP, float (&u)[RG_COLS]) {
 #pragma unroll
-    for (int q = 0; q < RG_COLS; q++)
-        if (act & (1u << q)) u[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[S][q]), lP));
+    for (int q = Q0; q < RG_COLS; q++) u[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[S][q]), lP));
+}
+
+// Apply one step to the register columns q >= Q0: a[r][q] -= f[r] * a[P][q],
+// for every row (f = 0 off the rows below) or, MASKED, for the rows below.
+template <int Q0, bool MASKED>
+__device__ __forceinline__ void lu_apply_any(float (&a)[RG_SLOTS][RG_COLS], const bool (&live)[RG_SLOTS],
+                                             const float (&f)[RG_SLOTS], int P) {
+    if constexpr (Q0 < RG_COLS) {
+        const int lP = P & 63;
+        float u[RG_COLS];
+        switch (P >> 6) {
+            case 0: lu_read_row<0, Q0>(a, lP, u); break;
+            case 1: lu_read_row<1, Q0>(a, lP, u); break;
+            case 2: lu_read_row<2, Q0>(a, lP, u); break;
+            default: lu_read_row<3, Q0>(a, lP, u); break;
+        }
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            if (MASKED) {
+                if (live[s]) {
+#pragma unroll
+                    for (int q = Q0; q < RG_COLS; q++) a[s][q] = a[s][q] - f[s] * u[q];
+                }
+            } else {
+#pragma unroll
+                for (int q = Q0; q < RG_COLS; q++) a[s][q] = a[s][q] - f[s] * u[q];
+            }
+        }
+    }
 }
 
 // Steps 16 B .. 16 B + 15 (register column B is the wave's column in that
-// range). Columns j = w + 16 q receive step c when j >= c + 2 (column c + 1
-// was updated by its owner before publishing step c + 1).
-template <int B>
+// range). Step c goes to the columns j = w + 16 q > c: q > B always, q = B
+// when w > i.
+template <int B, bool MASKED>
 __device__ __forceinline__ void lu_steps(LuShared & sh, float (&a)[RG_SLOTS][RG_COLS], bool (&live)[RG_SLOTS],
                                          int n, int w, int lane, int & spins, int * __restrict__ status) {
     for (int i = 0; i < RG_COLS; i++) {
@@ -1670,69 +1721,68 @@ __device__ __forceinline__ void lu_steps(LuShared & sh, float (&a)[RG_SLOTS][RG_
         const float f[RG_SLOTS] = {f4.x, f4.y, f4.z, f4.w};
         const int P = pv & 255;
         const bool skip = (pv & 256) != 0;
+        if (MASKED) {
 #pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++) live[s] = live[s] && (lane + 64 * s) != P;
-        if (c + 1 < n && w == ((c + 1) & (RG_COLS - 1))) {
+            for (int s = 0; s < RG_SLOTS; s++) live[s] = live[s] && (lane + 64 * s) != P;
+        }
+        const bool prod = c + 1 < n && w == ((c + 1) & (RG_COLS - 1));
+        float col[RG_SLOTS];
+        if (prod) {
             __builtin_amdgcn_s_setprio(3);
-            if (w != 0) lu_next_column<B>(sh, a, live, f, skip, P, c + 1, lane);
-            else if constexpr (B + 1 < RG_COLS) lu_next_column<B + 1>(sh, a, live, f, skip, P, c + 1, lane);
+            if (w != 0) lu_next_column<B, MASKED>(sh, a, live, f, skip, P, c + 1, n, lane, col);
+            else if constexpr (B + 1 < RG_COLS)
+                lu_next_column<B + 1, MASKED>(sh, a, live, f, skip, P, c + 1, n, lane, col);
             __builtin_amdgcn_s_setprio(0);
         }
-        if (skip) continue;
-        // active register columns of this step (uniform)
-        unsigned act = 0;
-#pragma unroll
-        for (int q = B + 2; q < RG_COLS; q++) act |= 1u << q;
-        if constexpr (B + 1 < RG_COLS)
-            if (!(i == RG_COLS - 1 && w == 0)) act |= 1u << (B + 1);
-        if (w >= i + 2) act |= 1u << B;
-        if (act == 0) continue;
-        float u[RG_COLS];
-        const int lP = P & 63;
-        switch (P >> 6) {
-            case 0: lu_pivot_row<0>(a, lP, act, u); break;
-            case 1: lu_pivot_row<1>(a, lP, act, u); break;
-            case 2: lu_pivot_row<2>(a, lP, act, u); break;
-            default: lu_pivot_row<3>(a, lP, act, u); break;
+        if (!skip) {
+            if (w > i) lu_apply_any<B, MASKED>(a, live, f, P);
+            else lu_apply_any<B + 1, MASKED>(a, live, f, P);
         }
+        if (prod) {
+            if (w != 0) {
 #pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++) {
-            if (live[s]) {
+                for (int s = 0; s < RG_SLOTS; s++) a[s][B] = col[s];
+            } else if constexpr (B + 1 < RG_COLS) {
 #pragma unroll
-                for (int q = B; q < RG_COLS; q++)
-                    if (act & (1u << q)) a[s][q] = a[s][q] - f[s] * u[q];
+                for (int s = 0; s < RG_SLOTS; s++) a[s][B + 1] = col[s];
             }
         }
     }
-    if constexpr (B + 1 < RG_COLS) lu_steps<B + 1>(sh, a, live, n, w, lane, spins, status);
+    if constexpr (B + 1 < RG_COLS) lu_steps<B + 1, MASKED>(sh, a, live, n, w, lane, spins, status);
 }
 
+// grid (n_chunks * H, L), 1024 threads. MASKED = false: every system, sets
+// redo[sys]; MASKED = true: only the systems with redo[sys] set.
+template <bool MASKED>
 __global__ void __launch_bounds__(RG_THREADS)
 k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
         const long long * __restrict__ aug_off, int * __restrict__ perm_out, unsigned char * __restrict__ skip_out,
-        float * __restrict__ LU_all, int * __restrict__ status) {
+        float * __restrict__ LU_all, int * __restrict__ redo, int * __restrict__ status) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const int n = c.tc;
     if (n > RG_ROWS || n < 1) return;
     const long long sys = ((long long)layer * g.n_chunks + c_idx) * g.H + h;
+    if (MASKED && redo[sys] == 0) return;
     const float * A = aug + aug_off[sys];
     float * LU = LU_all + sys * (long long)RG_ROWS * RG_ROWS;
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
     __shared__ LuShared sh;
 
+    // rows and columns past n hold copies of row / column n - 1: those rows
+    // are never live and those columns are never published or written out
     float a[RG_SLOTS][RG_COLS];
     bool live[RG_SLOTS];
+    bool unsafe = false;
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) {
         const int r = lane + 64 * s;
         live[s] = r < n;
-        const int rc = r < n ? r : n - 1;
+        const int rc = min(r, n - 1);
 #pragma unroll
         for (int q = 0; q < RG_COLS; q++) {
-            const int j = w + RG_WAVES * q;
-            const float v = A[(unsigned)((j < n ? j : n - 1) * n + rc)];
-            a[s][q] = (r < n && j < n) ? v : 0.0f;
+            a[s][q] = A[(unsigned)(min(w + RG_WAVES * q, n - 1) * n + rc)];
+            if (!MASKED) unsafe = unsafe || lu_unsafe(a[s][q]);
         }
     }
     if (tid < RG_ROWS) {
@@ -1740,18 +1790,39 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
         sh.inv.b[lu_inv_byte(tid)] = (unsigned char)tid;
     }
     if (tid < LU_RING) sh.u.ring.flag[tid] = -1;
-    __syncthreads();
+    if (!MASKED) {
+        if (__syncthreads_or(unsafe)) {
+            if (tid == 0) redo[sys] = 1;
+            return;
+        }
+    } else {
+        __syncthreads();
+    }
     if (w == 0) {
         float col[RG_SLOTS];
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++) col[s] = a[s][0];
-        lu_produce(sh, col, live, 0, lane);
+        lu_produce(sh, col, 0, n, lane);
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++) a[s][0] = col[s];
     }
     int spins = 0;
-    lu_steps<0>(sh, a, live, n, w, lane, spins, status);
-    __syncthreads();
+    lu_steps<0, MASKED>(sh, a, live, n, w, lane, spins, status);
+    if (!MASKED) {
+        // a non-finite final entry: some step may have changed a finished row
+        bool bad = false;
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++)
+#pragma unroll
+            for (int q = 0; q < RG_COLS; q++)
+                bad = bad || (lane + 64 * s < n && w + RG_WAVES * q < n &&
+                              (__float_as_uint(a[s][q]) & 0x7f800000u) == 0x7f800000u);
+        const bool redo_sys = __syncthreads_or(bad);
+        if (tid == 0) redo[sys] = redo_sys ? 1 : 0;
+        if (redo_sys) return;
+    } else {
+        __syncthreads();
+    }
     if (tid < n) {
         perm_out[sys * (long long)g.tc_max + tid] = sh.pivrow[tid];
         skip_out[sys * (long long)g.tc_max + tid] = sh.skip[tid];
@@ -2540,8 +2611,11 @@ void launch_ls_build(const Geom & g, const Work & w, hipStream_t st) {
 }
 
 void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st) {
-    hipLaunchKernelGGL(k_ge_lu, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
-                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, w.status);
+    // unmasked pass over every system, then the masked pass over the flagged ones
+    hipLaunchKernelGGL(k_ge_lu<false>, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
+                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, w.lu_redo, w.status);
+    hipLaunchKernelGGL(k_ge_lu<true>, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
+                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, w.lu_redo, w.status);
 }
 
 void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st) {
