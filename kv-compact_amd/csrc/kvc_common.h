@@ -41,6 +41,7 @@ struct Geom {
     float inv_sqrt_dk;
     float ridge;
     float zero_val;             // solution value of a skipped pivot (0 for C_v, eps for the beta weights)
+    int lu_masked;              // 1: every register LU takes the masked variant (KVC_LU_MASKED=1, for tests)
 };
 
 // Device scratch for one batch (all pointers device memory).

@@ -420,6 +420,10 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     g.score_method = p.score_method;
     g.inv_sqrt_dk = 1.0f / sqrtf((float)io.dk);
     g.ridge = p.ridge;
+    {
+        const char * e = getenv("KVC_LU_MASKED");
+        g.lu_masked = (e && e[0] == '1') ? 1 : 0;
+    }
 
     // aug offsets: [L][n_chunks][H]
     std::vector<long long> aug_off((size_t)io.L * pl.n_chunks * io.H);

@@ -1199,14 +1199,16 @@ k_gather_exp(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
 }
 
 // beta = logf(max(1e-12, w)) after the solvers' final clamp w < 1e-12 -> 1e-12
-// (math.h:449-451, math.h:755-757, api.cpp:829); std::max keeps 1e-12 for NaN
+// (math.h:449-451, math.h:755-757, api.cpp:829). The clamp keeps NaN and
+// std::max then returns 1e-12 for it, so together: w >= 1e-12 ? w : 1e-12.
+// (Written as one comparison: the two selects in sequence were folded into
+// the first alone, which keeps NaN.)
 __global__ void __launch_bounds__(256)
 k_beta_log(float * __restrict__ wb, long long n) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    float w = wb[i];
-    if (w < 1e-12f) w = 1e-12f;
-    const float m = (1e-12f < w) ? w : 1e-12f;
+    const float w = wb[i];
+    const float m = (w >= 1e-12f) ? w : 1e-12f;
     wb[i] = logf_ref(m);
 }
 
@@ -1764,6 +1766,10 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
     if (n > RG_ROWS || n < 1) return;
     const long long sys = ((long long)layer * g.n_chunks + c_idx) * g.H + h;
     if (MASKED && redo[sys] == 0) return;
+    if (!MASKED && g.lu_masked) {
+        if (threadIdx.x == 0) redo[sys] = 1;
+        return;
+    }
     const float * A = aug + aug_off[sys];
     float * LU = LU_all + sys * (long long)RG_ROWS * RG_ROWS;
     const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);

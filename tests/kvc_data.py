@@ -294,3 +294,25 @@ def refine_variant(name: str):
         K, V = kv_cache(600, 2, 16, 55)
         return c, K, V, normal(5501, (12, 32)), 12
     raise KeyError(name)
+
+
+def nonfinite_variant_names():
+    return ["nan_k", "inf_k", "nan_v", "negzero_k_row"]
+
+
+def nonfinite_variant(name: str):
+    """Return (case, K, V, Q, n_q): one NaN / inf / -0 planted in an otherwise
+    ordinary cache (the reference's arithmetic carries them through)."""
+    T, H, d = 600, 2, 32
+    K, V = kv_cache(T, H, d, 77)
+    Q = snapkv_queries(K, 16, 77)
+    if name == "nan_k":
+        K[123, 5] = np.nan
+    elif name == "inf_k":
+        K[321, 40] = np.inf
+    elif name == "nan_v":
+        V[50, 3] = np.nan
+    elif name == "negzero_k_row":
+        K[10, :] = -0.0
+    c = dict(name=name, T=T, H=H, d=d, seed=77, params=dict(target_ratio=0.3))
+    return c, K, V, Q, 16

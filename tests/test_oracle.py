@@ -10,8 +10,8 @@ import numpy as np
 import pytest
 
 from kvc_data import (CASES, CASE_BY_NAME, beta_variant, beta_variant_names, diversity_variant,
-                      diversity_variant_names, kv_cache, make_case, normal, refine_variant, refine_variant_names,
-                      uniform)
+                      diversity_variant_names, kv_cache, make_case, nonfinite_variant, nonfinite_variant_names,
+                      normal, refine_variant, refine_variant_names, uniform)
 from kvc_harness import ORACLE_SO, REF_HARNESS_SO, REF_SO, case_params, kc, load_oracle, load_ref, run_case
 from pathlib import Path
 
@@ -145,6 +145,26 @@ def test_oracle_refine_variants_match_live_reference(orc, name):
     assert np.array_equal(bits(a.C_v), bits(b.C_v))
     z = orc.compact(K, V, Q, T, nq, H, d, d, case_params(orc, c, T, refine_rounds=0))
     assert (name == "refine_full_keep") == np.array_equal(a.indices, z.indices)
+
+
+@pytest.mark.parametrize("pgd", [0, 1])
+@pytest.mark.parametrize("name", nonfinite_variant_names())
+def test_oracle_nonfinite_inputs_match_live_reference(orc, name, pgd):
+    """A NaN, inf or -0 in K or V: the oracle follows the compiled reference
+    bit for bit, NaN patterns included (zero-beta and clamped-LS beta fits)."""
+    ref = load_ref()
+    if ref is None:
+        pytest.skip("reference not compiled here (oracle/_ref)")
+    c, K, V, Q, nq = nonfinite_variant(name)
+    T, H, d = c["T"], c["H"], c["d"]
+    extra = dict(skip_beta=0, nnls_method=1) if pgd else {}
+    a = orc.compact(K, V, Q, T, nq, H, d, d, case_params(orc, c, T, **extra))
+    b = ref.compact(K, V, Q, T, nq, H, d, d, case_params(ref, c, T, **extra))
+    assert np.array_equal(a.indices, b.indices)
+    assert np.array_equal(bits(a.beta), bits(b.beta))
+    assert np.array_equal(bits(a.C_v), bits(b.C_v))
+    for k in ("avg_cosine_sim", "avg_mse", "avg_agreement"):
+        assert np.float32(a.stats[k]).view(np.uint32) == np.float32(b.stats[k]).view(np.uint32), k
 
 
 # ---------------------------------------------------------------- blocks ---
