@@ -1541,23 +1541,47 @@ constexpr int LU_SPIN_LIMIT = 1 << 22;   // polls per wave over the whole factor
 
 struct LuShared {
     union {
-        struct {
-            float4 fm[LU_RING][64];  // step c's multipliers in slot c % LU_RING: lane l's four rows
-            int piv[LU_RING];        // step's pivot row; +256 when the step was skipped
-            int flag[LU_RING];       // step number published in the slot
-        } ring;
+        float4 fm[LU_RING][64];      // step c's multipliers in slot c % LU_RING: lane l's four rows
         float tile[LU_TROWS][RG_ROWS + 1];   // output staging at the end
     } u;
+    int plog[RG_ROWS];               // step c's pivot row (+256: skipped); -1 until published
     union {
-        unsigned w[64];              // logical index of rows l, l+64, l+128, l+192 as bytes of w[l]
-        unsigned char b[RG_ROWS];
+        int4 v[64];                  // logical index of rows l, l+64, l+128, l+192 in v[l]
+        int e[RG_ROWS];
     } inv;
     int phys[RG_ROWS];               // physical row of each logical index
-    int pivrow[RG_ROWS];
-    unsigned char skip[RG_ROWS];
 };
 
-__device__ __forceinline__ int lu_inv_byte(int r) { return (r & 63) * 4 + (r >> 6); }
+__device__ __forceinline__ int lu_inv_elem(int r) { return (r & 63) * 4 + (r >> 6); }
+
+// LDS byte offset of a __shared__ object
+template <typename T>
+__device__ __forceinline__ unsigned lu_lds(const T * p) {
+    return (unsigned)(size_t)(const __attribute__((address_space(3))) T *)p;
+}
+
+// Four LDS reads issued back to back, in this order, then one wait: an entry
+// of plog, then (same pass) a step's multipliers, this lane's logical indices
+// and one entry of phys. A wave's LDS accesses execute in order, so when the
+// plog entry reads as published, the other three read what its producer
+// wrote before it.
+__device__ __forceinline__ void lu_poll_read(unsigned a_plog, unsigned a_fm, unsigned a_inv, unsigned a_phys,
+                                             int & pl, float4 & f4, int4 & iv, int & ph) {
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    v4f x;
+    v4i y;
+    asm volatile("ds_read_b32 %0, %4\n\t"
+                 "ds_read_b128 %1, %5\n\t"
+                 "ds_read_b128 %2, %6\n\t"
+                 "ds_read_b32 %3, %7\n\t"
+                 "s_waitcnt lgkmcnt(0)"
+                 : "=&v"(pl), "=&v"(x), "=&v"(y), "=&v"(ph)
+                 : "v"(a_plog), "v"(a_fm), "v"(a_inv), "v"(a_phys)
+                 : "memory");
+    f4 = make_float4(x[0], x[1], x[2], x[3]);
+    iv = make_int4(y[0], y[1], y[2], y[3]);
+}
 
 __device__ __forceinline__ float lu_pick(const float (&v)[RG_SLOTS], int s) {
     return s == 0 ? v[0] : (s == 1 ? v[1] : (s == 2 ? v[2] : v[3]));
@@ -1569,43 +1593,48 @@ __device__ __forceinline__ bool lu_unsafe(float x) {
     return b == 0x80000000u || (b & 0x7f800000u) == 0x7f800000u;
 }
 
-// Publish step c1 from its column's values col[] (steps < c1 applied): pivot =
-// first row in logical order of largest |a| among the rows not yet used
-// (logical index >= c1), replacing the diagonal only when strictly larger and
-// never NaN (a NaN diagonal keeps the diagonal, every comparison against it
-// failing); pivots below 1e-12 in magnitude skip the step (math.h:507-527).
-// The rows still below the pivot get their multipliers (0 for a skipped step)
-// in col[]; every other row's published multiplier is 0.
-__device__ __forceinline__ void lu_produce(LuShared & sh, float (&col)[RG_SLOTS], int c1, int n, int lane) {
-    const unsigned ivw = sh.inv.w[lane];
-    const int physc = __builtin_amdgcn_readfirstlane(sh.phys[c1]);
-    int li[RG_SLOTS];
+// Publish step c1 from its column's values col[] (steps < c1 applied), given
+// the logical indices iv of this lane's rows (negative for rows past n) and
+// the physical row physc at logical c1: pivot = first row in logical order of
+// largest |a| among the rows not yet used (logical index >= c1), replacing the
+// diagonal only when strictly larger and never NaN (a NaN diagonal keeps the
+// diagonal, every comparison against it failing); pivots below 1e-12 in
+// magnitude skip the step (math.h:507-527). The rows still below the pivot
+// get their multipliers (0 for a skipped step) in col[]; every other row's
+// published multiplier is 0. The multipliers and the permutation update go
+// to LDS before the step's entry in plog, which consumers wait for.
+// Unmasked (MASKED = false), NaN needs no handling: a system that meets one
+// ends with a non-finite entry and is redone masked.
+template <bool MASKED>
+__device__ __forceinline__ void lu_produce(LuShared & sh, float (&col)[RG_SLOTS], int4 iv, int physc, int c1,
+                                           int lane) {
+    const int li[RG_SLOTS] = {iv.x, iv.y, iv.z, iv.w};
     bool live[RG_SLOTS];
     unsigned key[RG_SLOTS];
     bool nanc = false;
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) {
-        li[s] = (int)((ivw >> (8 * s)) & 255u);
-        live[s] = li[s] >= c1 && lane + 64 * s < n;
+        live[s] = li[s] >= c1;
         const float v = fabsf(col[s]);
-        key[s] = (live[s] && v == v) ? __float_as_uint(v) : 0u;
-        nanc = nanc || (li[s] == c1 && v != v);
+        if (MASKED) {
+            key[s] = (live[s] && v == v) ? __float_as_uint(v) : 0u;
+            nanc = nanc || (li[s] == c1 && v != v);
+        } else {
+            key[s] = live[s] ? __float_as_uint(v) : 0u;
+        }
     }
-    const unsigned kmax = max(max(key[0], key[1]), max(key[2], key[3]));
-    const unsigned gmax = dpp_reduce_u32<true>(kmax);
+    const unsigned gmax = dpp_reduce_u32<true>(max(max(key[0], key[1]), max(key[2], key[3])));
     int mr, P;
-    if (__ballot(nanc) || gmax == 0u) {
-        // every live row is +-0 or NaN, or the diagonal is NaN: the diagonal stays
+    if ((MASKED && __ballot(nanc)) || gmax == 0u) {
+        // every live row is +-0 (or NaN), or the diagonal is NaN: the diagonal stays
         mr = c1;
         P = physc;
     } else {
         // first logical index among the rows at the maximum, with its physical row
         unsigned cand = 0xffffu;
 #pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++) {
-            const unsigned e = ((unsigned)li[s] << 8) | (unsigned)(lane + 64 * s);
-            cand = min(cand, key[s] == gmax ? e : 0xffffu);
-        }
+        for (int s = 0; s < RG_SLOTS; s++)
+            cand = min(cand, key[s] == gmax ? (((unsigned)li[s] << 8) | (unsigned)(lane + 64 * s)) : 0xffffu);
         const unsigned long long m = __ballot(cand != 0xffffu);
         unsigned v;
         if ((m & (m - 1)) == 0ull) v = (unsigned)__builtin_amdgcn_readlane((int)cand, __builtin_ctzll(m));
@@ -1623,19 +1652,18 @@ __device__ __forceinline__ void lu_produce(LuShared & sh, float (&col)[RG_SLOTS]
         f[s] = (elim && below) ? q : 0.0f;
         if (below) col[s] = f[s];
     }
-    const int slot = c1 & (LU_RING - 1);
-    sh.u.ring.fm[slot][lane] = make_float4(f[0], f[1], f[2], f[3]);
-    if (lane == 0) {
-        sh.u.ring.piv[slot] = P | (elim ? 0 : 256);
-        sh.inv.b[lu_inv_byte(P)] = (unsigned char)c1;
-        sh.inv.b[lu_inv_byte(physc)] = (unsigned char)mr;   // P == physc when mr == c1
-        sh.phys[c1] = P;
-        sh.phys[mr] = physc;
-        sh.pivrow[c1] = P;
-        sh.skip[c1] = elim ? 0 : 1;
+    sh.u.fm[c1 & (LU_RING - 1)][lane] = make_float4(f[0], f[1], f[2], f[3]);
+    // swap logical c1 and mr: lanes 0-3 write inv[P], inv[physc], phys[c1],
+    // phys[mr] in one instruction (equal addresses carry equal values when
+    // mr == c1)
+    if (lane < 4) {
+        int * dst = lane == 0 ? &sh.inv.e[lu_inv_elem(P)]
+                  : lane == 1 ? &sh.inv.e[lu_inv_elem(physc)]
+                  : lane == 2 ? &sh.phys[c1] : &sh.phys[mr];
+        *dst = lane == 0 ? c1 : lane == 1 ? mr : lane == 2 ? P : physc;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    if (lane == 0) __hip_atomic_store(&sh.u.ring.flag[slot], c1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (lane == 0) __hip_atomic_store(&sh.plog[c1], P | (elim ? 0 : 256), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // The owner of column c + 1 (register column Q): a copy of that column with
@@ -1645,7 +1673,8 @@ __device__ __forceinline__ void lu_produce(LuShared & sh, float (&col)[RG_SLOTS]
 template <int Q, bool MASKED>
 __device__ __forceinline__ void lu_next_column(LuShared & sh, const float (&a)[RG_SLOTS][RG_COLS],
                                                const bool (&live)[RG_SLOTS], const float (&f)[RG_SLOTS],
-                                               bool skip, int P, int c1, int n, int lane, float (&col)[RG_SLOTS]) {
+                                               bool skip, int P, int4 iv, int physc, int c1, int n, int lane,
+                                               float (&col)[RG_SLOTS]) {
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) col[s] = a[s][Q];
     if (!skip) {
@@ -1659,7 +1688,7 @@ __device__ __forceinline__ void lu_next_column(LuShared & sh, const float (&a)[R
             }
         }
     }
-    lu_produce(sh, col, c1, n, lane);
+    lu_produce<MASKED>(sh, col, iv, physc, c1, lane);
 }
 
 // u[q] = a[P][q] for the register columns q >= Q0 (pivot row in slot S, lane lP)
@@ -1708,18 +1737,49 @@ __device__ __forceinline__ void lu_steps(LuShared & sh, float (&a)[RG_SLOTS][RG_
         const int c = RG_COLS * B + i;
         if (c >= n) break;   // (a break, not a return: one exit path keeps the register assignment)
         const int slot = c & (LU_RING - 1);
-        // bounded wait: past the limit the wave stops waiting and reports
-        // through *status (the host turns that into a device error)
-        while (__hip_atomic_load(&sh.u.ring.flag[slot], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != c) {
-            if (++spins > LU_SPIN_LIMIT) {
-                if (lane == 0) atomicOr(status, 2);
-                break;
+        const bool prod = c + 1 < n && w == ((c + 1) & (RG_COLS - 1));
+        // the owners of columns c + 1 and c + 2 run ahead of the others on
+        // their SIMDs: the first publishes step c + 1 now, the second must be
+        // through step c by the time step c + 1 appears
+        if (prod || w == ((c + 2) & (RG_COLS - 1))) __builtin_amdgcn_s_setprio(2);
+        else __builtin_amdgcn_s_setprio(0);
+        // wait for step c (bounded: past the limit the wave stops waiting and
+        // reports through *status, which the host turns into a device error).
+        // The next producer polls without sleeping and reads the step's
+        // multipliers, its rows' logical indices and the row at logical c + 1
+        // in the same pass: LDS accesses of one wave execute in order, and
+        // the producer wrote them before the plog entry.
+        int pv;
+        float4 f4;
+        int4 iv = make_int4(0, 0, 0, 0);
+        int physc = 0;
+        if (prod) {
+            for (;;) {
+                int pl;
+                lu_poll_read(lu_lds(&sh.plog[c]), lu_lds(&sh.u.fm[slot][lane]), lu_lds(&sh.inv.v[lane]),
+                             lu_lds(&sh.phys[c + 1]), pl, f4, iv, physc);
+                pv = __builtin_amdgcn_readfirstlane(pl);
+                if (pv >= 0) break;
+                if (++spins > LU_SPIN_LIMIT) {
+                    if (lane == 0) atomicOr(status, 2);
+                    break;
+                }
             }
-            __builtin_amdgcn_s_sleep(1);
+        } else {
+            for (;;) {
+                pv = __builtin_amdgcn_readfirstlane(
+                    __hip_atomic_load(&sh.plog[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+                if (pv >= 0) break;
+                if (++spins > LU_SPIN_LIMIT) {
+                    if (lane == 0) atomicOr(status, 2);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+            f4 = sh.u.fm[slot][lane];
         }
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-        const int pv = __builtin_amdgcn_readfirstlane(sh.u.ring.piv[slot]);
-        const float4 f4 = sh.u.ring.fm[slot][lane];
+        physc = __builtin_amdgcn_readfirstlane(physc);
         const float f[RG_SLOTS] = {f4.x, f4.y, f4.z, f4.w};
         const int P = pv & 255;
         const bool skip = (pv & 256) != 0;
@@ -1727,14 +1787,13 @@ __device__ __forceinline__ void lu_steps(LuShared & sh, float (&a)[RG_SLOTS][RG_
 #pragma unroll
             for (int s = 0; s < RG_SLOTS; s++) live[s] = live[s] && (lane + 64 * s) != P;
         }
-        const bool prod = c + 1 < n && w == ((c + 1) & (RG_COLS - 1));
         float col[RG_SLOTS];
         if (prod) {
             __builtin_amdgcn_s_setprio(3);
-            if (w != 0) lu_next_column<B, MASKED>(sh, a, live, f, skip, P, c + 1, n, lane, col);
+            if (w != 0) lu_next_column<B, MASKED>(sh, a, live, f, skip, P, iv, physc, c + 1, n, lane, col);
             else if constexpr (B + 1 < RG_COLS)
-                lu_next_column<B + 1, MASKED>(sh, a, live, f, skip, P, c + 1, n, lane, col);
-            __builtin_amdgcn_s_setprio(0);
+                lu_next_column<B + 1, MASKED>(sh, a, live, f, skip, P, iv, physc, c + 1, n, lane, col);
+            __builtin_amdgcn_s_setprio(2);
         }
         if (!skip) {
             if (w > i) lu_apply_any<B, MASKED>(a, live, f, P);
@@ -1793,9 +1852,9 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
     }
     if (tid < RG_ROWS) {
         sh.phys[tid] = tid;
-        sh.inv.b[lu_inv_byte(tid)] = (unsigned char)tid;
+        sh.inv.e[lu_inv_elem(tid)] = tid < n ? tid : -1;   // rows past n are never live
+        sh.plog[tid] = -1;
     }
-    if (tid < LU_RING) sh.u.ring.flag[tid] = -1;
     if (!MASKED) {
         if (__syncthreads_or(unsafe)) {
             if (tid == 0) redo[sys] = 1;
@@ -1808,7 +1867,7 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
         float col[RG_SLOTS];
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++) col[s] = a[s][0];
-        lu_produce(sh, col, 0, n, lane);
+        lu_produce<MASKED>(sh, col, sh.inv.v[lane], 0, 0, lane);
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++) a[s][0] = col[s];
     }
@@ -1830,8 +1889,9 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
         __syncthreads();
     }
     if (tid < n) {
-        perm_out[sys * (long long)g.tc_max + tid] = sh.pivrow[tid];
-        skip_out[sys * (long long)g.tc_max + tid] = sh.skip[tid];
+        const int pl = sh.plog[tid];
+        perm_out[sys * (long long)g.tc_max + tid] = pl & 255;
+        skip_out[sys * (long long)g.tc_max + tid] = (unsigned char)(pl >> 8);
     }
     // every entry is final in registers: multipliers left of each row's pivot
     // step, U from it on; rows go out through LDS, LU_TROWS at a time, as
