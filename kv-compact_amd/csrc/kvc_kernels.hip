@@ -1546,13 +1546,16 @@ struct LuShared {
     } u;
     int plog[RG_ROWS];               // step c's pivot row (+256: skipped); -1 until published
     union {
-        int4 v[64];                  // logical index of rows l, l+64, l+128, l+192 in v[l]
-        int e[RG_ROWS];
-    } inv;
-    int phys[RG_ROWS];               // physical row of each logical index
+        struct {
+            int4 inv[64];            // logical index of rows l, l+64, l+128, l+192 in inv[l]
+            int phys[RG_ROWS];       // physical row of each logical index
+        } p;
+        int e[2 * RG_ROWS];          // the same as one array: inv entries, then phys
+    } m;
 };
 
 __device__ __forceinline__ int lu_inv_elem(int r) { return (r & 63) * 4 + (r >> 6); }
+constexpr int LU_PHYS0 = RG_ROWS;    // index of phys[0] in LuShared::m.e
 
 // LDS byte offset of a __shared__ object
 template <typename T>
@@ -1583,8 +1586,11 @@ __device__ __forceinline__ void lu_poll_read(unsigned a_plog, unsigned a_fm, uns
     iv = make_int4(y[0], y[1], y[2], y[3]);
 }
 
+// v[s] for a uniform s, as selects (no branches)
 __device__ __forceinline__ float lu_pick(const float (&v)[RG_SLOTS], int s) {
-    return s == 0 ? v[0] : (s == 1 ? v[1] : (s == 2 ? v[2] : v[3]));
+    const float lo = (s & 1) ? v[1] : v[0];
+    const float hi = (s & 1) ? v[3] : v[2];
+    return (s & 2) ? hi : lo;
 }
 
 // -0, +-inf or NaN
@@ -1642,6 +1648,16 @@ __device__ __forceinline__ void lu_produce(LuShared & sh, float (&col)[RG_SLOTS]
         mr = (int)(v >> 8);
         P = (int)(v & 255u);
     }
+    // swap logical c1 and mr: lanes 0-3 write inv[P], inv[physc], phys[c1],
+    // phys[mr] in one instruction (equal addresses carry equal values when
+    // mr == c1), issued before the division so that it completes beside it
+    {
+        const int e01 = lane == 0 ? lu_inv_elem(P) : lu_inv_elem(physc);
+        const int e23 = LU_PHYS0 + (lane == 2 ? c1 : mr);
+        const int v01 = lane == 0 ? c1 : mr;
+        const int v23 = lane == 2 ? P : physc;
+        if (lane < 4) sh.m.e[lane < 2 ? e01 : e23] = lane < 2 ? v01 : v23;
+    }
     const float piv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lu_pick(col, P >> 6)), P & 63));
     const bool elim = !(fabsf(piv) < 1e-12f);
     float f[RG_SLOTS];
@@ -1653,15 +1669,6 @@ __device__ __forceinline__ void lu_produce(LuShared & sh, float (&col)[RG_SLOTS]
         if (below) col[s] = f[s];
     }
     sh.u.fm[c1 & (LU_RING - 1)][lane] = make_float4(f[0], f[1], f[2], f[3]);
-    // swap logical c1 and mr: lanes 0-3 write inv[P], inv[physc], phys[c1],
-    // phys[mr] in one instruction (equal addresses carry equal values when
-    // mr == c1)
-    if (lane < 4) {
-        int * dst = lane == 0 ? &sh.inv.e[lu_inv_elem(P)]
-                  : lane == 1 ? &sh.inv.e[lu_inv_elem(physc)]
-                  : lane == 2 ? &sh.phys[c1] : &sh.phys[mr];
-        *dst = lane == 0 ? c1 : lane == 1 ? mr : lane == 2 ? P : physc;
-    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
     if (lane == 0) __hip_atomic_store(&sh.plog[c1], P | (elim ? 0 : 256), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
@@ -1756,8 +1763,8 @@ __device__ __forceinline__ void lu_steps(LuShared & sh, float (&a)[RG_SLOTS][RG_
         if (prod) {
             for (;;) {
                 int pl;
-                lu_poll_read(lu_lds(&sh.plog[c]), lu_lds(&sh.u.fm[slot][lane]), lu_lds(&sh.inv.v[lane]),
-                             lu_lds(&sh.phys[c + 1]), pl, f4, iv, physc);
+                lu_poll_read(lu_lds(&sh.plog[c]), lu_lds(&sh.u.fm[slot][lane]), lu_lds(&sh.m.p.inv[lane]),
+                             lu_lds(&sh.m.p.phys[c + 1]), pl, f4, iv, physc);
                 pv = __builtin_amdgcn_readfirstlane(pl);
                 if (pv >= 0) break;
                 if (++spins > LU_SPIN_LIMIT) {
@@ -1851,8 +1858,8 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
         }
     }
     if (tid < RG_ROWS) {
-        sh.phys[tid] = tid;
-        sh.inv.e[lu_inv_elem(tid)] = tid < n ? tid : -1;   // rows past n are never live
+        sh.m.p.phys[tid] = tid;
+        sh.m.e[lu_inv_elem(tid)] = tid < n ? tid : -1;   // rows past n are never live
         sh.plog[tid] = -1;
     }
     if (!MASKED) {
@@ -1867,7 +1874,7 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
         float col[RG_SLOTS];
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++) col[s] = a[s][0];
-        lu_produce<MASKED>(sh, col, sh.inv.v[lane], 0, 0, lane);
+        lu_produce<MASKED>(sh, col, sh.m.p.inv[lane], 0, 0, lane);
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++) a[s][0] = col[s];
     }
