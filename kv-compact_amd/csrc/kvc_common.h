@@ -55,7 +55,8 @@ struct Work {
     float * Y;        // [L][n_chunks][H][nq_max][dv]
     int   * sel;      // [L][t_total]        kept token positions (layer-local), ascending
     float * X;        // [L][H][nq_max][t_total] compacted softmax weights
-    float * aug;      // GE workspace: one column-major [tc + dv][tc] system per (layer, chunk, head)
+    float * aug;      // GE workspace per (layer, chunk, head): M column-major [tc][tc], then B
+                      // (tc x dv: row-major when tc <= 256, else column-major)
     int   * perm;     // [L][n_chunks][H][tc_max] pivot order of each system
     unsigned char * skip; // [L][n_chunks][H][tc_max] skipped-pivot flags by step
     float * LU;       // [L][n_chunks][H][256][256] by physical row: multipliers left of the row's

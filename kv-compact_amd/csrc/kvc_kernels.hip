@@ -1408,6 +1408,15 @@ k_nnls_lh(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restric
     for (int i = lane; i < n; i += 64) wo[i] = w[i];
 }
 
+// Right-hand side entry (row i, column v) of a system's [M | B] storage:
+// row-major for the register-LU systems (n <= 256), whose solve reads one row
+// of B across 64 columns at a time; column-major (B transposed) for larger
+// ones, whose general elimination swaps rows in place. For p == 1 both are
+// the same.
+__device__ __forceinline__ long long rhs_at(int n, int p, int i, int v) {
+    return (long long)n * n + (n <= 256 ? (long long)i * p + v : (long long)v * n + i);
+}
+
 // one block per system; X (nq x n) and Y (nq x p) staged in (dynamic) LDS
 // when they fit its budget
 constexpr int LB_LDS_FLOATS = 40960;   // 160 KB
@@ -1442,7 +1451,7 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
                 for (int k = 0; k < nq; k++) s += Xh[(long long)k * g.t_total + i] * Yh[(long long)k * g.dv + (j - n)];
             }
             if (i == j) s += g.ridge;
-            Ag[e] = s;
+            Ag[j < n ? e : rhs_at(n, p, i, j - n)] = s;
         }
         return;
     }
@@ -1456,9 +1465,8 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     }
     __syncthreads();
     const int nbi = (n + 3) >> 2, nbw = wp >> 2;
-    for (int e = threadIdx.x; e < nbi * nbw; e += blockDim.x) {
-        const int jb = e / nbi, ib = e % nbi;   // consecutive threads: consecutive row blocks
-        if (ib > jb) continue;
+    // one 4 x 4 output tile; the sums run over k ascending
+    auto tile = [&](int ib, int jb) {
         const int i0 = 4 * ib, j0 = 4 * jb;
         float acc[4][4];
 #pragma unroll
@@ -1484,17 +1492,29 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
                 if (j >= w) continue;
                 float v = acc[a][b];
                 if (i == j) v += g.ridge;
-                Ag[(long long)j * n + i] = v;
+                Ag[j < n ? (long long)j * n + i : rhs_at(n, p, i, j - n)] = v;
                 if (j < n && j > i) Ag[(long long)i * n + j] = v;   // mirror (j, i)
             }
         }
+    };
+    // tiles holding columns of M (upper triangle only): consecutive threads
+    // take consecutive row blocks (column-major stores)
+    const int nbm = nbi;   // column blocks that hold at least one column of M
+    for (int e = threadIdx.x; e < nbi * nbm; e += blockDim.x) {
+        const int jb = e / nbi, ib = e % nbi;
+        if (ib > jb) continue;
+        tile(ib, jb);
     }
+    // tiles of B alone: consecutive threads take consecutive column blocks
+    // (row-major stores when n <= 256)
+    const int nbr = nbw - nbm;
+    for (int e = threadIdx.x; e < nbi * nbr; e += blockDim.x) tile(e / nbr, nbm + e % nbr);
 }
 
 // ---------------------------------------------------------------------------
 // Gaussian elimination with partial pivoting + back substitution on [M | B]
-// (n x (n + p)), math.h:494-556. Storage is column-major: entry (r, j) at
-// a[j * n + r] (M is symmetric, B is stored transposed).
+// (n x (n + p)), math.h:494-556. M is stored column-major (entry (r, j) at
+// a[j * n + r]; M is symmetric), B after it as given by rhs_at.
 //
 // k_ge_lu (n <= 256): LU of the n x n matrix with the reference's partial
 // pivoting, in registers, as a column-cyclic dataflow. Wave w owns columns
@@ -1935,6 +1955,7 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
 // into registers, so its global-memory latency overlaps the previous row.
 constexpr int BS_HIGH = 128;
 constexpr int BS_PAD = 128;   // the row buffer holds entry k at rowb[BS_PAD - shift + k]
+constexpr int BS_AHEAD = 8;   // backward rows in flight
 
 // val -= rowp[t] * xsb[t][lane] for t = 0 .. n_terms-1, ascending and
 // sequential; batches of 8 operands are loaded one batch ahead.
@@ -2015,7 +2036,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     const int vc = act ? v : p - 1;   // in-range column for the loads of idle lanes
     // by physical row: multipliers left of the row's pivot step, U from it on
     const float * __restrict__ LU = LU_all + (long long)sysl * RG_ROWS * RG_ROWS;
-    const float * __restrict__ B = aug + aug_off[sysl] + (long long)n * n;   // column-major RHS [v][r]
+    const float * __restrict__ B = aug + aug_off[sysl] + (long long)n * n;   // row-major RHS [r][v]
     float * Yt = Yt_all + (long long)sysl * RG_ROWS * g.dv;
     float * x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
     __shared__ float xs[BS_HIGH][64];
@@ -2052,7 +2073,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             for (int t = 0; t < 4; t++) {
                 const int r = permL[(i0 + t < n) ? i0 + t : i0];
                 qf[t] = reinterpret_cast<const float4 *>(LU + (unsigned)(r * RG_ROWS))[lane];
-                qb[t] = B[(unsigned)(vc * n + r)];
+                qb[t] = B[(unsigned)(r * p + vc)];
             }
         };
         fetch(0);
@@ -2107,14 +2128,14 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     // ---- forward: rows [0, lb) from LDS, then rows [lb, n) with [0, lb) in registers
     const int lb = n < BS_HIGH ? n : BS_HIGH;
     pf = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[0] * RG_ROWS))[lane];
-    pb = B[(unsigned)(vc * n + permL[0])];
+    pb = B[(unsigned)(permL[0] * p + vc)];
     for (int i = 0; i < lb; i++) {
         frow4[lane] = pf;
         float val = act ? pb : 0.0f;
         if (i + 1 < n) {
             const int rn = permL[i + 1];
             pf = reinterpret_cast<const float4 *>(LU + (unsigned)(rn * RG_ROWS))[lane];
-            pb = B[(unsigned)(vc * n + rn)];
+            pb = B[(unsigned)(rn * p + vc)];
         }
         __builtin_amdgcn_wave_barrier();
         val = sk ? dot_seq_skip(val, frow, xs, i, skf, lane) : dot_seq(val, frow, xs, i, lane);
@@ -2132,7 +2153,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             if (i + 1 < n) {
                 const int rn = permL[i + 1];
                 pf = reinterpret_cast<const float4 *>(LU + (unsigned)(rn * RG_ROWS))[lane];
-                pb = B[(unsigned)(vc * n + rn)];
+                pb = B[(unsigned)(rn * p + vc)];
             }
             __builtin_amdgcn_wave_barrier();
             if (!sk) {
@@ -2155,60 +2176,59 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     // ---- backward: rows [hb, n) from LDS, then rows [0, hb) with [hb, n) in
     // registers. Row col of U is published shifted by -hb (entry k at
     // brow[k]), so that the register part's entries brow[hb + i] are aligned.
+    // U rows and y values are loaded BS_AHEAD rows ahead through a register
+    // ring, so that their latency overlaps the short sums of the last rows.
     const int hb = n > BS_HIGH ? n - BS_HIGH : 0;
     float * brow = rowb + BS_PAD - hb;
-    pf = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[n - 1] * RG_ROWS))[lane];
-    pb = Yt[(unsigned)((n - 1) * g.dv + vc)];
-    for (int col = n - 1; col >= hb; col--) {
-        brow[4 * lane + 0] = pf.x;
-        brow[4 * lane + 1] = pf.y;
-        brow[4 * lane + 2] = pf.z;
-        brow[4 * lane + 3] = pf.w;
-        const float yv = pb;
-        if (col > 0) {
-            pf = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[col - 1] * RG_ROWS))[lane];
-            pb = Yt[(unsigned)((col - 1) * g.dv + vc)];
-        }
-        __builtin_amdgcn_wave_barrier();
-        const float piv = brow[col];
-        float val = g.zero_val;
-        if (!(fabsf(piv) < 1e-12f)) {
-            val = act ? yv : 0.0f;
-            val = dot_seq(val, brow + col + 1, xs + (col + 1 - hb), n - col - 1, lane);
-            val = val / piv;
-        }
-        xs[col - hb][lane] = val;
-        if (act) x[(unsigned)(col * g.dv + v)] = val;
-        __builtin_amdgcn_wave_barrier();
-    }
-    if (hb == 0) return;
-    float xh[BS_HIGH];
-#pragma unroll
-    for (int i = 0; i < BS_HIGH; i++) xh[i] = xs[i][lane];
     const float * bhi = rowb + BS_PAD;   // == brow + hb
-    for (int col = hb - 1; col >= 0; col--) {
-        brow[4 * lane + 0] = pf.x;
-        brow[4 * lane + 1] = pf.y;
-        brow[4 * lane + 2] = pf.z;
-        brow[4 * lane + 3] = pf.w;
-        const float yv = pb;
-        if (col > 0) {
-            pf = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[col - 1] * RG_ROWS))[lane];
-            pb = Yt[(unsigned)((col - 1) * g.dv + vc)];
-        }
-        __builtin_amdgcn_wave_barrier();
-        const float piv = brow[col];
-        float val = g.zero_val;
-        if (!(fabsf(piv) < 1e-12f)) {
-            val = act ? yv : 0.0f;
-            val = dot_seq(val, brow + col + 1, xs + (col + 1), hb - col - 1, lane);
+    float xh[BS_HIGH];
+    float4 rf[BS_AHEAD];
+    float rb[BS_AHEAD];
 #pragma unroll
-            for (int i = 0; i < BS_HIGH; i++) val -= bhi[i] * xh[i];
-            val = val / piv;
+    for (int k = 0; k < BS_AHEAD; k++) {
+        const int r = max(n - 1 - k, 0);
+        rf[k] = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[r] * RG_ROWS))[lane];
+        rb[k] = Yt[(unsigned)(r * g.dv + vc)];
+    }
+    for (int col0 = n - 1; col0 >= 0; col0 -= BS_AHEAD) {
+#pragma unroll
+        for (int k = 0; k < BS_AHEAD; k++) {
+            const int col = col0 - k;
+            if (col < 0) break;
+            if (col == hb - 1) {
+                // entering the rows below hb: rows [hb, n) move to registers
+#pragma unroll
+                for (int i = 0; i < BS_HIGH; i++) xh[i] = xs[i][lane];
+                __builtin_amdgcn_wave_barrier();
+            }
+            brow[4 * lane + 0] = rf[k].x;
+            brow[4 * lane + 1] = rf[k].y;
+            brow[4 * lane + 2] = rf[k].z;
+            brow[4 * lane + 3] = rf[k].w;
+            const float yv = rb[k];
+            if (col - BS_AHEAD >= 0) {
+                const int r = col - BS_AHEAD;
+                rf[k] = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[r] * RG_ROWS))[lane];
+                rb[k] = Yt[(unsigned)(r * g.dv + vc)];
+            }
+            __builtin_amdgcn_wave_barrier();
+            const float piv = brow[col];
+            float val = g.zero_val;
+            if (!(fabsf(piv) < 1e-12f)) {
+                val = act ? yv : 0.0f;
+                if (col >= hb) {
+                    val = dot_seq(val, brow + col + 1, xs + (col + 1 - hb), n - col - 1, lane);
+                } else {
+                    val = dot_seq(val, brow + col + 1, xs + (col + 1), hb - col - 1, lane);
+#pragma unroll
+                    for (int i = 0; i < BS_HIGH; i++) val -= bhi[i] * xh[i];
+                }
+                val = val / piv;
+            }
+            xs[col >= hb ? col - hb : col][lane] = val;
+            if (act) x[(unsigned)(col * g.dv + v)] = val;
+            __builtin_amdgcn_wave_barrier();
         }
-        xs[col][lane] = val;
-        if (act) x[(unsigned)(col * g.dv + v)] = val;
-        __builtin_amdgcn_wave_barrier();
     }
 }
 
