@@ -340,7 +340,8 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     s.mh = std::min(io.H, 4);
     s.mq = std::min(pl.nq_global, 32);
     s.qmode = pl.stats_qmode;
-    s.OS = cv.take<float>(L * s.mh * s.mq * T);
+    // the original scores reuse S when the statistics share the main query set
+    s.OS = (p && pl.qmode == pl.stats_qmode) ? nullptr : cv.take<float>(L * s.mh * s.mq * T);
     s.CS = cv.take<float>(L * s.mh * s.mq * std::max<size_t>(tt, 1));
     s.OO = cv.take<float>(L * s.mh * s.mq * dv);
     s.CO = cv.take<float>(L * s.mh * s.mq * dv);
@@ -520,7 +521,9 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     }
     (void)hipEventRecord(ev[ST_REFINE + 1], st);
     // 8. quality statistics against the full call
-    launch_stats(g, w, sw, io.K, io.V, io.Q, io.beta, io.Cv, io.stats, st);
+    // the statistics' original scores are rows of S when both use one query set
+    launch_stats(g, w, sw, io.K, io.V, io.Q, io.beta, io.Cv, io.stats, st,
+                 pl.qmode == pl.stats_qmode ? w.S : nullptr);
     (void)hipEventRecord(ev[ST_STATS + 1], st);
 
     hipError_t err = hipGetLastError();

@@ -24,9 +24,11 @@ void launch_beta_log(float * wb, long long n, hipStream_t st);
 void launch_ls_build(const Geom & g, const Work & w, hipStream_t st);
 void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st);
 void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st);
+// S_main: the main path's scores [L][H][nq_max][T], used (and overwritten by
+// the sampled rows' softmax) when the statistics share its query set; else null
 void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const float * K,
                   const float * V, const float * Q, const float * beta, const float * Cv,
-                  float * stats, hipStream_t st);
+                  float * stats, hipStream_t st, float * S_main = nullptr);
 void launch_dequant_rows(const uint8_t * src, int type, long long row_bytes, int n_el, long long rows,
                          float * dst, hipStream_t st);
 void launch_quant_rows(const float * src, long long src_ld, const int * idx, int type, int n_el,

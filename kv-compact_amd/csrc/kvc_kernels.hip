@@ -483,13 +483,14 @@ k_refit_target(Geom g, const ChunkDesc * __restrict__ chunks, const float * __re
 constexpr int SV_QB = 16, SV_VB = 64, SV_KT = 64, SV_THREADS = 128;
 
 __global__ void __launch_bounds__(SV_THREADS)
-k_stats_values(Geom g, const float * __restrict__ a_all, int n, const float * __restrict__ V,
-               const float * __restrict__ Cv, int mode, float * __restrict__ out_all, int mh, int mq) {
+k_stats_values(Geom g, const float * __restrict__ a_all, long long a_ls, long long a_hs, long long a_rs, int n,
+               const float * __restrict__ V, const float * __restrict__ Cv, int mode, float * __restrict__ out_all,
+               int mh, int mq) {
     const int nqb = (mq + SV_QB - 1) / SV_QB, nvb = (g.dv + SV_VB - 1) / SV_VB;
     const int layer = blockIdx.y;
     const int h = blockIdx.x / (nqb * nvb);
     const int q0 = ((blockIdx.x / nvb) % nqb) * SV_QB, v0 = (blockIdx.x % nvb) * SV_VB;
-    const float * a = a_all + (((long long)layer * mh + h) * mq) * n;
+    const float * a = a_all + layer * a_ls + h * a_hs;   // row q at a + q * a_rs
     const float * val;
     long long vrs;
     if (mode == 1) {
@@ -513,7 +514,7 @@ k_stats_values(Geom g, const float * __restrict__ a_all, int n, const float * __
         for (int u = 0; u < 8; u++) {
             const int e = tid + SV_THREADS * u, qi = e >> 6, jj = e & 63;
             const int q = q0 + qi, j = j0 + jj;
-            ra[u] = (q < mq && j < n) ? a[(long long)q * n + j] : 0.0f;
+            ra[u] = (q < mq && j < n) ? a[(long long)q * a_rs + j] : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < 8; u++) {
@@ -2328,37 +2329,114 @@ k_ge_general(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__
 // ---------------------------------------------------------------------------
 // Quality statistics (api.cpp:239-325).
 // ---------------------------------------------------------------------------
-// in-place row softmax (math.h:83-100), one block per row; the sequential
-// sum runs on lane 0 over LDS-staged blocks of the row
-constexpr int RS_STAGE = 4096;
+// In-place row softmax (math.h:83-100) of the statistics rows: row r of a
+// layer is (h = r / mq, q = r % mq) at x + layer * ls + h * hs + q * rs. A
+// block owns RSM_ROWS rows and sweeps them together, one column per thread,
+// so that every row's load of a column is in flight at once:
+//  1. maxima: the largest non-NaN value of each row (NaN when row[0] is NaN;
+//     the reference's scan keeps row[0] otherwise unless a value exceeds it);
+//  2. RSM_TILE-column tiles, double-buffered in LDS: threads 64.. compute
+//     expf(x - max) (written back in place) while lane r of wave 0 adds row
+//     r's previous tile in column order, the reference's sequential sum;
+//  3. x *= 1 / (sum + 1e-12f).
+// grid (ceil(mh * mq / RSM_ROWS), L), RSM_THREADS threads.
+constexpr int RSM_ROWS = 16, RSM_TILE = 256, RSM_THREADS = 64 + RSM_TILE;
 
-__global__ void __launch_bounds__(256)
-k_row_softmax(float * __restrict__ x, int n, long long rs, int rows, long long layer_stride) {
-    const int row = blockIdx.x, layer = blockIdx.y;
-    if (row >= rows) return;
-    float * xr = x + layer * layer_stride + row * rs;
-    __shared__ float red[16];
-    __shared__ float stage[RS_STAGE];
-    __shared__ float s_sum;
-    const float m = ref_row_max(xr, n, red);
-    float sum = 0.0f;
-    for (int j0 = 0; j0 < n; j0 += RS_STAGE) {
-        const int jn = min(RS_STAGE, n - j0);
-        __syncthreads();
-        for (int j = threadIdx.x; j < jn; j += blockDim.x) {
-            const float e = expf_ref(xr[j0 + j] - m);
-            stage[j] = e;
-            xr[j0 + j] = e;
-        }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            for (int j = 0; j < jn; j++) sum += stage[j];
-        }
+__global__ void __launch_bounds__(RSM_THREADS)
+k_row_softmax(float * __restrict__ x, int n, long long ls, long long hs, long long rs, int mh, int mq) {
+    const int layer = blockIdx.y, r0 = blockIdx.x * RSM_ROWS;
+    const int nrows = min(RSM_ROWS, mh * mq - r0);
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    __shared__ float mx[RSM_ROWS], inv[RSM_ROWS];
+    __shared__ float tile[2][RSM_ROWS][RSM_TILE + 1];
+    __shared__ unsigned red[RSM_THREADS / 64][RSM_ROWS];
+    float * rowp[RSM_ROWS];
+#pragma unroll
+    for (int r = 0; r < RSM_ROWS; r++) {
+        const int rr = r0 + min(r, nrows - 1);
+        rowp[r] = x + layer * ls + (long long)(rr / mq) * hs + (long long)(rr % mq) * rs;
     }
-    if (threadIdx.x == 0) s_sum = sum;
+    // 1. maxima
+    {
+        float m[RSM_ROWS];
+#pragma unroll
+        for (int r = 0; r < RSM_ROWS; r++) m[r] = -INFINITY;
+        for (int j = tid; j < n; j += RSM_THREADS) {
+            float v[RSM_ROWS];
+#pragma unroll
+            for (int r = 0; r < RSM_ROWS; r++) v[r] = rowp[r][j];
+#pragma unroll
+            for (int r = 0; r < RSM_ROWS; r++)
+                if (v[r] == v[r] && v[r] > m[r]) m[r] = v[r];
+        }
+#pragma unroll
+        for (int r = 0; r < RSM_ROWS; r++) {
+            const unsigned k = dpp_reduce_u32<true>(score_key(m[r]));
+            if (lane == 0) red[w][r] = k;
+        }
+        __syncthreads();
+        if (tid < nrows) {
+            unsigned k = red[0][tid];
+            for (int i = 1; i < RSM_THREADS / 64; i++) k = max(k, red[i][tid]);
+            const float mm = __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+            const float a0 = rowp[tid][0];
+            mx[tid] = (a0 != a0) ? a0 : ((mm > a0) ? mm : a0);
+        }
+        __syncthreads();
+    }
+    // 2. exponentials and the sequential sums
+    const int ntiles = (n + RSM_TILE - 1) / RSM_TILE;
+    auto compute = [&](int t, int b) {   // threads 64 .. 64 + RSM_TILE - 1
+        const int c = tid - 64, j = t * RSM_TILE + c;
+        if (j >= n) return;
+        float v[RSM_ROWS];
+#pragma unroll
+        for (int r = 0; r < RSM_ROWS; r++) v[r] = rowp[r][j];
+#pragma unroll
+        for (int r = 0; r < RSM_ROWS; r++) {
+            if (r < nrows) {
+                const float e = expf_ref(v[r] - mx[r]);
+                rowp[r][j] = e;
+                tile[b][r][c] = e;
+            }
+        }
+    };
+    float sum = 0.0f;
+    if (w > 0) compute(0, 0);
     __syncthreads();
-    const float iv = 1.0f / (s_sum + 1e-12f);
-    for (int j = threadIdx.x; j < n; j += blockDim.x) xr[j] = xr[j] * iv;
+    for (int t = 0; t < ntiles; t++) {
+        const int b = t & 1;
+        if (w > 0) {
+            if (t + 1 < ntiles) compute(t + 1, b ^ 1);
+        } else if (lane < nrows) {
+            const int jn = min(RSM_TILE, n - t * RSM_TILE);
+            const float * tr = &tile[b][lane][0];
+            int c = 0;
+            for (; c + 16 <= jn; c += 16) {   // 16 reads in flight, then the adds in order
+                float e[16];
+#pragma unroll
+                for (int k = 0; k < 16; k++) e[k] = tr[c + k];
+#pragma unroll
+                for (int k = 0; k < 16; k++) sum += e[k];
+            }
+            for (; c < jn; c++) sum += tr[c];
+        }
+        __syncthreads();
+    }
+    if (w == 0 && lane < nrows) inv[lane] = 1.0f / (sum + 1e-12f);
+    __syncthreads();
+    // 3. normalisation
+    float iv[RSM_ROWS];
+#pragma unroll
+    for (int r = 0; r < RSM_ROWS; r++) iv[r] = inv[min(r, nrows - 1)];
+    for (int j = tid; j < n; j += RSM_THREADS) {
+        float v[RSM_ROWS];
+#pragma unroll
+        for (int r = 0; r < RSM_ROWS; r++) v[r] = rowp[r][j];
+#pragma unroll
+        for (int r = 0; r < RSM_ROWS; r++)
+            if (r < nrows) rowp[r][j] = v[r] * iv[r];
+    }
 }
 
 // per (h, qi) terms in parallel (each sequential over d), then the
@@ -2722,26 +2800,38 @@ void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st)
 
 void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const float * K,
                   const float * V, const float * Q, const float * beta, const float * Cv,
-                  float * stats, hipStream_t st) {
+                  float * stats, hipStream_t st, float * S_main) {
     const ChunkDesc * whole = w.chunks + g.n_chunks;      // all T keys
     const ChunkDesc * kept = w.chunks + g.n_chunks + 1;   // the t_total kept keys
     const long long osl = (long long)sw.mh * sw.mq * g.T;
     const long long csl = (long long)sw.mh * sw.mq * g.t_total;
-    // original attention of the sampled queries over all T
-    launch_scores(g, whole, 1, g.T, K, Q, sw.OS, sw.mh, sw.mq, osl, (long long)sw.mq * g.T, g.T, sw.qmode, st,
-                  nullptr, nullptr);
-    hipLaunchKernelGGL(k_row_softmax, dim3(sw.mh * sw.mq, g.L), dim3(256), 0, st,
-                       sw.OS, g.T, (long long)g.T, sw.mh * sw.mq, osl);
+    const unsigned rsm_blocks = (unsigned)cdiv(sw.mh * sw.mq, RSM_ROWS);
     const unsigned sv_blocks = (unsigned)(sw.mh * cdiv(sw.mq, SV_QB) * cdiv(g.dv, SV_VB));
+    // original attention of the sampled queries over all T: the main path's
+    // scores S [L][H][nq_max][T] hold exactly these rows when the statistics
+    // use the main query set (they are not read again), else computed here
+    float * os = sw.OS;
+    long long o_ls = osl, o_hs = (long long)sw.mq * g.T;
+    if (S_main) {
+        os = S_main;
+        o_ls = (long long)g.H * g.nq_max * g.T;
+        o_hs = (long long)g.nq_max * g.T;
+    } else {
+        launch_scores(g, whole, 1, g.T, K, Q, sw.OS, sw.mh, sw.mq, osl, (long long)sw.mq * g.T, g.T, sw.qmode, st,
+                      nullptr, nullptr);
+    }
+    hipLaunchKernelGGL(k_row_softmax, dim3(rsm_blocks, g.L), dim3(RSM_THREADS), 0, st,
+                       os, g.T, o_ls, o_hs, (long long)g.T, sw.mh, sw.mq);
     hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), 0, st,
-                       g, sw.OS, g.T, V, Cv, 1, sw.OO, sw.mh, sw.mq);
+                       g, os, o_ls, o_hs, (long long)g.T, g.T, V, Cv, 1, sw.OO, sw.mh, sw.mq);
     // compacted attention over the kept keys with beta and C_v
     launch_scores(g, kept, 1, g.t_total, K, Q, sw.CS, sw.mh, sw.mq, csl, (long long)sw.mq * g.t_total, g.t_total,
                   sw.qmode, st, w.sel, beta);
-    hipLaunchKernelGGL(k_row_softmax, dim3(sw.mh * sw.mq, g.L), dim3(256), 0, st,
-                       sw.CS, g.t_total, (long long)g.t_total, sw.mh * sw.mq, csl);
+    hipLaunchKernelGGL(k_row_softmax, dim3(rsm_blocks, g.L), dim3(RSM_THREADS), 0, st,
+                       sw.CS, g.t_total, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, sw.mh, sw.mq);
     hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), 0, st,
-                       g, sw.CS, g.t_total, V, Cv, 2, sw.CO, sw.mh, sw.mq);
+                       g, sw.CS, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, g.t_total, V, Cv, 2,
+                       sw.CO, sw.mh, sw.mq);
     hipLaunchKernelGGL(k_stats_final, dim3(g.L), dim3(128), 0, st, g, sw.OO, sw.CO, sw.mh, sw.mq, stats);
 }
 
