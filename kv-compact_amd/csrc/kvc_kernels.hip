@@ -475,12 +475,13 @@ k_refit_target(Geom g, const ChunkDesc * __restrict__ chunks, const float * __re
 // Statistics attention outputs (api.cpp:270-293): out[q][v] = sum_j a[q][j] *
 // val[j][v], j ascending, for the sampled heads and queries, over all T keys
 // (original) or the t_total kept keys (compacted, val = C_v). Each output is a
-// sequential sum, so the parallelism is the outputs: a block of 128 threads
-// owns 16 queries x 64 columns, each thread 2 queries x 4 columns (8
-// independent sums); 64-key tiles of a and val are double-buffered in LDS.
+// sequential sum, so the parallelism is the outputs: a block of 256 threads
+// owns 16 queries x 64 columns, each thread one query x 4 columns (4
+// independent sums; four waves per block keep two per SIMD busy); 64-key
+// tiles of a and val are double-buffered in LDS.
 // grid (mh * ceil(mq/16) * ceil(dv/64), L)
 // ---------------------------------------------------------------------------
-constexpr int SV_QB = 16, SV_VB = 64, SV_KT = 64, SV_THREADS = 128;
+constexpr int SV_QB = 16, SV_VB = 64, SV_KT = 64, SV_THREADS = 256;
 
 __global__ void __launch_bounds__(SV_THREADS)
 k_stats_values(Geom g, const float * __restrict__ a_all, long long a_ls, long long a_hs, long long a_rs, int n,
@@ -504,20 +505,20 @@ k_stats_values(Geom g, const float * __restrict__ a_all, long long a_ls, long lo
     __shared__ float As[2][SV_QB][SV_KT + 1];
     __shared__ __align__(16) float Vs[2][SV_KT][SV_VB];
     const int tid = threadIdx.x, tq = tid >> 4, tv = tid & 15;
-    const int qa = q0 + 2 * tq, vc = v0 + 4 * tv;
-    // tile loaders: a: 16 x 64 (8 per thread); val: 64 x 64 (32 per thread, 8 float4)
+    const int qa = q0 + tq, vc = v0 + 4 * tv;
+    // tile loaders: a: 16 x 64 (4 per thread); val: 64 x 64 (16 per thread, 4 float4)
     const bool vvec = (g.dv & 3) == 0 && (vrs & 3) == 0 && (reinterpret_cast<uintptr_t>(val) & 15) == 0;
-    float ra[8];
-    float4 rv[8];
+    float ra[4];
+    float4 rv[4];
     auto load = [&](int j0) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < 4; u++) {
             const int e = tid + SV_THREADS * u, qi = e >> 6, jj = e & 63;
             const int q = q0 + qi, j = j0 + jj;
             ra[u] = (q < mq && j < n) ? a[(long long)q * a_rs + j] : 0.0f;
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < 4; u++) {
             const int e = tid + SV_THREADS * u, jj = e >> 4, c4 = (e & 15) * 4;
             const int j = j0 + jj, c = v0 + c4;
             float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -537,21 +538,17 @@ k_stats_values(Geom g, const float * __restrict__ a_all, long long a_ls, long lo
     };
     auto store = [&](int b) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < 4; u++) {
             const int e = tid + SV_THREADS * u;
             As[b][e >> 6][e & 63] = ra[u];
         }
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+        for (int u = 0; u < 4; u++) {
             const int e = tid + SV_THREADS * u;
             *reinterpret_cast<float4 *>(&Vs[b][e >> 4][(e & 15) * 4]) = rv[u];
         }
     };
-    float acc[2][4];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int k = 0; k < 4; k++) acc[i][k] = 0.0f;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     const int ntiles = (n + SV_KT - 1) / SV_KT;
     if (ntiles > 0) {
         load(0);
@@ -565,33 +562,26 @@ k_stats_values(Geom g, const float * __restrict__ a_all, long long a_ls, long lo
         if (jn == SV_KT) {
 #pragma unroll 8
             for (int jj = 0; jj < SV_KT; jj++) {
-                const float a0 = As[b][2 * tq][jj], a1 = As[b][2 * tq + 1][jj];
+                const float a0 = As[b][tq][jj];
                 const float4 x = *reinterpret_cast<const float4 *>(&Vs[b][jj][4 * tv]);
-                acc[0][0] = acc[0][0] + a0 * x.x; acc[0][1] = acc[0][1] + a0 * x.y;
-                acc[0][2] = acc[0][2] + a0 * x.z; acc[0][3] = acc[0][3] + a0 * x.w;
-                acc[1][0] = acc[1][0] + a1 * x.x; acc[1][1] = acc[1][1] + a1 * x.y;
-                acc[1][2] = acc[1][2] + a1 * x.z; acc[1][3] = acc[1][3] + a1 * x.w;
+                acc[0] = acc[0] + a0 * x.x; acc[1] = acc[1] + a0 * x.y;
+                acc[2] = acc[2] + a0 * x.z; acc[3] = acc[3] + a0 * x.w;
             }
         } else {
             for (int jj = 0; jj < jn; jj++) {
-                const float a0 = As[b][2 * tq][jj], a1 = As[b][2 * tq + 1][jj];
+                const float a0 = As[b][tq][jj];
                 const float4 x = *reinterpret_cast<const float4 *>(&Vs[b][jj][4 * tv]);
-                acc[0][0] = acc[0][0] + a0 * x.x; acc[0][1] = acc[0][1] + a0 * x.y;
-                acc[0][2] = acc[0][2] + a0 * x.z; acc[0][3] = acc[0][3] + a0 * x.w;
-                acc[1][0] = acc[1][0] + a1 * x.x; acc[1][1] = acc[1][1] + a1 * x.y;
-                acc[1][2] = acc[1][2] + a1 * x.z; acc[1][3] = acc[1][3] + a1 * x.w;
+                acc[0] = acc[0] + a0 * x.x; acc[1] = acc[1] + a0 * x.y;
+                acc[2] = acc[2] + a0 * x.z; acc[3] = acc[3] + a0 * x.w;
             }
         }
         if (t + 1 < ntiles) store(b ^ 1);
         __syncthreads();
     }
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int q = qa + i;
-        if (q >= mq) continue;
+    if (qa < mq) {
 #pragma unroll
         for (int k = 0; k < 4; k++)
-            if (vc + k < g.dv) out[(long long)q * g.dv + vc + k] = acc[i][k];
+            if (vc + k < g.dv) out[(long long)qa * g.dv + vc + k] = acc[k];
     }
 }
 
