@@ -1456,6 +1456,8 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     }
     __syncthreads();
     const int nbi = (n + 3) >> 2, nbw = wp >> 2;
+    // 16-byte stores need n, p multiples of 4, B row-major and an aligned base
+    const bool vec = (n & 3) == 0 && (p & 3) == 0 && n <= 256 && (reinterpret_cast<uintptr_t>(Ag) & 15) == 0;
     // one 4 x 4 output tile; the sums run over k ascending
     auto tile = [&](int ib, int jb) {
         const int i0 = 4 * ib, j0 = 4 * jb;
@@ -1472,6 +1474,31 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             for (int a = 0; a < 4; a++)
 #pragma unroll
                 for (int b = 0; b < 4; b++) acc[a][b] = acc[a][b] + vi[a] * vj[b];
+        }
+        if (vec && i0 + 3 < n && j0 + 3 < w && (j0 + 3 < n || j0 >= n)) {
+            // whole tile inside M or inside B: 16-byte stores
+            if (j0 < n) {
+                if (ib == jb) {
+#pragma unroll
+                    for (int a = 0; a < 4; a++) acc[a][a] = acc[a][a] + g.ridge;
+                }
+#pragma unroll
+                for (int b = 0; b < 4; b++)   // column j0 + b, rows i0 .. i0 + 3
+                    *reinterpret_cast<float4 *>(&Ag[(long long)(j0 + b) * n + i0]) =
+                        make_float4(acc[0][b], acc[1][b], acc[2][b], acc[3][b]);
+                if (ib < jb) {
+#pragma unroll
+                    for (int a = 0; a < 4; a++)   // mirror: column i0 + a, rows j0 .. j0 + 3
+                        *reinterpret_cast<float4 *>(&Ag[(long long)(i0 + a) * n + j0]) =
+                            make_float4(acc[a][0], acc[a][1], acc[a][2], acc[a][3]);
+                }
+            } else {
+#pragma unroll
+                for (int a = 0; a < 4; a++)   // row i0 + a of B, columns j0 - n ..
+                    *reinterpret_cast<float4 *>(&Ag[rhs_at(n, p, i0 + a, j0 - n)]) =
+                        make_float4(acc[a][0], acc[a][1], acc[a][2], acc[a][3]);
+            }
+            return;
         }
 #pragma unroll
         for (int a = 0; a < 4; a++) {
