@@ -303,7 +303,16 @@ __device__ __forceinline__ float ref_row_max(const float * row, int n, float * r
 // every lane gets the result.
 __device__ __forceinline__ float wave_ref_row_max(const float * row, int n, int lane) {
     float m = -INFINITY;
-    for (int j = lane; j < n; j += 64) {
+    int j = lane;
+    for (; j + 192 < n; j += 256) {   // four loads in flight
+        float v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) v[u] = row[j + 64 * u];
+#pragma unroll
+        for (int u = 0; u < 4; u++)
+            if (v[u] == v[u] && v[u] > m) m = v[u];
+    }
+    for (; j < n; j += 64) {
         const float v = row[j];
         if (v == v && v > m) m = v;
     }
@@ -352,17 +361,36 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
             const int jn = min(SM_TILE, n - t0);
             const int kk = tid & 63;
             if (kk < jn) {
-                for (int rr = wv; rr < nr; rr += 4) {
-                    const int r = r0 + rr;
-                    const float e = expf_ref(Sh[r * rs + t0 + kk] - rmax[r]);
-                    eb[rr][kk] = e;
-                    Ah[r * rs + t0 + kk] = e;
-                    if (Eh) Eh[r * rs + t0 + kk] = e;
+                // this thread's rows wv, wv + 4, ...: every load in flight first
+                float sv[SM_TROWS / 4];
+#pragma unroll
+                for (int u = 0; u < SM_TROWS / 4; u++) {
+                    const int rr = wv + 4 * u;
+                    if (rr < nr) sv[u] = Sh[(r0 + rr) * rs + t0 + kk];
+                }
+#pragma unroll
+                for (int u = 0; u < SM_TROWS / 4; u++) {
+                    const int rr = wv + 4 * u;
+                    if (rr < nr) {
+                        const int r = r0 + rr;
+                        const float e = expf_ref(sv[u] - rmax[r]);
+                        eb[rr][kk] = e;
+                        Ah[r * rs + t0 + kk] = e;
+                        if (Eh) Eh[r * rs + t0 + kk] = e;
+                    }
                 }
             }
             __syncthreads();
             if (tid < nr) {
-                for (int j = 0; j < jn; j++) sum += eb[tid][j];
+                int j = 0;
+                for (; j + 16 <= jn; j += 16) {   // 16 reads in flight, then the adds in order
+                    float e[16];
+#pragma unroll
+                    for (int k = 0; k < 16; k++) e[k] = eb[tid][j + k];
+#pragma unroll
+                    for (int k = 0; k < 16; k++) sum += e[k];
+                }
+                for (; j < jn; j++) sum += eb[tid][j];
             }
             __syncthreads();
         }
@@ -378,15 +406,27 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
     const float inv_m = 1.0f / (float)nq;
     for (int j = tid; j < n; j += blockDim.x) {
         float acc = 0.0f;
-        for (int qi = 0; qi < nq; qi++) {
-            const float a = Ah[qi * rs + j] * rinv[qi];
-            Ah[qi * rs + j] = a;
-            if (g.score_method == 0) {
-                if (a > acc) acc = a;
-            } else if (g.score_method == 1) {
-                acc += a * a;
-            } else {
-                acc += a;
+        for (int q0 = 0; q0 < nq; q0 += 16) {
+            // sixteen rows' loads in flight, then the row-ordered aggregation
+            const int qn = min(16, nq - q0);
+            float ev[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (u < qn) ev[u] = Ah[(q0 + u) * rs + j];
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                if (u < qn) {
+                    const int qi = q0 + u;
+                    const float a = ev[u] * rinv[qi];
+                    Ah[qi * rs + j] = a;
+                    if (g.score_method == 0) {
+                        if (a > acc) acc = a;
+                    } else if (g.score_method == 1) {
+                        acc += a * a;
+                    } else {
+                        acc += a;
+                    }
+                }
             }
         }
         if (g.score_method == 1) acc = sqrtf(acc * inv_m);
