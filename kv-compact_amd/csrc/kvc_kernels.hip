@@ -1164,6 +1164,11 @@ k_refine_step(Geom g, const ChunkDesc * __restrict__ chunks, const float * __res
 // (api.cpp:833-840); aug = [X^T X + ridge I | X^T Y] (math.h:465-504),
 // both sums sequential over the query index.
 // ---------------------------------------------------------------------------
+// 32 rows x t_c columns at a time in LDS: gather S[:, sel] + beta, row maxima
+// (one wave per row, the reference's scan semantics), exponentials, the
+// sequential row sums (one thread per row over LDS), then X = e * inv.
+constexpr int LSX_ROWS = 32, LSX_COLS = 256;
+
 __global__ void __launch_bounds__(256)
 k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ S,
              const int * __restrict__ sel, const float * __restrict__ beta, float * __restrict__ X) {
@@ -1175,38 +1180,95 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
     const float * bh = beta + ((long long)layer * g.H + h) * g.t_total + c.off;
     const long long hsX = (long long)g.nq_max * g.t_total;
     float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
-    __shared__ float red[16];
-    __shared__ float rmax[256], rinv[256];
-    for (int base = 0; base < nq; base += 256) {
-        const int nb = min(256, nq - base);
-        for (int r = 0; r < nb; r++) {
-            float * xr = Xh + (long long)(base + r) * g.t_total;
-            const float * sr = Sh + (long long)(base + r) * g.T;
-            for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = sr[sl[j]] + bh[j];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    if (t > LSX_COLS) {
+        // large chunks: row by row through global memory
+        __shared__ float red[16];
+        __shared__ float rmax1, rinv1;
+        for (int r = 0; r < nq; r++) {
+            float * xr = Xh + (long long)r * g.t_total;
+            const float * sr = Sh + (long long)r * g.T;
+            for (int j = tid; j < t; j += blockDim.x) xr[j] = sr[sl[j]] + bh[j];
+            __syncthreads();
+            const float m = ref_row_max(xr, t, red);
+            if (tid == 0) rmax1 = m;
+            __syncthreads();
+            for (int j = tid; j < t; j += blockDim.x) xr[j] = expf_ref(xr[j] - rmax1);
+            __syncthreads();
+            if (tid == 0) {
+                float sum = 0.0f;
+                for (int j = 0; j < t; j++) sum += xr[j];
+                rinv1 = 1.0f / (sum + 1e-12f);
+            }
+            __syncthreads();
+            for (int j = tid; j < t; j += blockDim.x) xr[j] = xr[j] * rinv1;
+            __syncthreads();
+        }
+        return;
+    }
+    __shared__ float xs[LSX_ROWS][LSX_COLS + 1];
+    __shared__ float rmax[LSX_ROWS], rinv[LSX_ROWS];
+    __shared__ int sls[LSX_COLS];
+    __shared__ float bs[LSX_COLS];
+    for (int j = tid; j < t; j += blockDim.x) {
+        sls[j] = sl[j];
+        bs[j] = bh[j];
+    }
+    __syncthreads();
+    for (int r0 = 0; r0 < nq; r0 += LSX_ROWS) {
+        const int nr = min(LSX_ROWS, nq - r0);
+        // gather: eight rows' loads per thread in flight
+        for (int j = tid; j < t; j += blockDim.x) {
+            const int sj = sls[j];
+            const float bj = bs[j];
+            for (int rb = 0; rb < nr; rb += 8) {
+                float v[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (rb + u < nr) v[u] = Sh[(long long)(r0 + rb + u) * g.T + sj];
+#pragma unroll
+                for (int u = 0; u < 8; u++)
+                    if (rb + u < nr) xs[rb + u][j] = v[u] + bj;
+            }
         }
         __syncthreads();
-        for (int r = 0; r < nb; r++) {
-            const float m = ref_row_max(Xh + (long long)(base + r) * g.t_total, t, red);
-            if (threadIdx.x == 0) rmax[r] = m;
+        // maxima: largest non-NaN value, NaN when the first entry is NaN,
+        // else the first entry unless a value exceeds it
+        for (int r = wv; r < nr; r += 4) {
+            float m = -INFINITY;
+            for (int j = lane; j < t; j += 64) {
+                const float v = xs[r][j];
+                if (v == v && v > m) m = v;
+            }
+            const unsigned k = dpp_reduce_u32<true>(score_key(m));
+            const float mm = __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+            const float a0 = xs[r][0];
+            if (lane == 0) rmax[r] = (a0 != a0) ? a0 : ((mm > a0) ? mm : a0);
         }
         __syncthreads();
-        for (int r = 0; r < nb; r++) {
-            float * xr = Xh + (long long)(base + r) * g.t_total;
-            const float mx = rmax[r];
-            for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = expf_ref(xr[j] - mx);
+        for (int e = tid; e < nr * LSX_COLS; e += blockDim.x) {
+            const int r = e / LSX_COLS, j = e % LSX_COLS;
+            if (j < t) xs[r][j] = expf_ref(xs[r][j] - rmax[r]);
         }
         __syncthreads();
-        if ((int)threadIdx.x < nb) {
-            const float * xr = Xh + (long long)(base + threadIdx.x) * g.t_total;
+        if (tid < nr) {
             float sum = 0.0f;
-            for (int j = 0; j < t; j++) sum += xr[j];
-            rinv[threadIdx.x] = 1.0f / (sum + 1e-12f);
+            int j = 0;
+            for (; j + 16 <= t; j += 16) {   // 16 reads in flight, then the adds in order
+                float e[16];
+#pragma unroll
+                for (int k = 0; k < 16; k++) e[k] = xs[tid][j + k];
+#pragma unroll
+                for (int k = 0; k < 16; k++) sum += e[k];
+            }
+            for (; j < t; j++) sum += xs[tid][j];
+            rinv[tid] = 1.0f / (sum + 1e-12f);
         }
         __syncthreads();
-        for (int r = 0; r < nb; r++) {
-            float * xr = Xh + (long long)(base + r) * g.t_total;
+        for (int r = 0; r < nr; r++) {
             const float iv = rinv[r];
-            for (int j = threadIdx.x; j < t; j += blockDim.x) xr[j] = xr[j] * iv;
+            float * xr = Xh + (long long)(r0 + r) * g.t_total;
+            for (int j = tid; j < t; j += blockDim.x) xr[j] = xs[r][j] * iv;
         }
         __syncthreads();
     }
