@@ -2076,6 +2076,7 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
 constexpr int BS_HIGH = 128;
 constexpr int BS_PAD = 128;   // the row buffer holds entry k at rowb[BS_PAD - shift + k]
 constexpr int BS_AHEAD = 8;   // backward rows in flight
+constexpr int BS_FAHEAD = 4;  // forward 4-row blocks in flight
 
 // val -= rowp[t] * xsb[t][lane] for t = 0 .. n_terms-1, ascending and
 // sequential; batches of 8 operands are loaded one batch ahead.
@@ -2186,27 +2187,34 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         // sums run side by side; the 4 x 4 triangle finishes them in order.
         __shared__ __align__(16) float4 lt[RG_ROWS];
         float yr[BS_HIGH];
-        float4 qf[4];
-        float qb[4];
-        auto fetch = [&](int i0) {
+        // rows and right-hand sides of the next BS_FAHEAD blocks in flight
+        float4 qf[BS_FAHEAD][4];
+        float qb[BS_FAHEAD][4];
+        auto fetch = [&](int i0, float4 (&f)[4], float (&bb)[4]) {
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const int r = permL[(i0 + t < n) ? i0 + t : i0];
-                qf[t] = reinterpret_cast<const float4 *>(LU + (unsigned)(r * RG_ROWS))[lane];
-                qb[t] = B[(unsigned)(r * p + vc)];
+                f[t] = reinterpret_cast<const float4 *>(LU + (unsigned)(r * RG_ROWS))[lane];
+                bb[t] = B[(unsigned)(r * p + vc)];
             }
         };
-        fetch(0);
-        for (int i0 = 0; i0 < n; i0 += 4) {
+#pragma unroll
+        for (int k = 0; k < BS_FAHEAD; k++)
+            if (4 * k < n) fetch(4 * k, qf[k], qb[k]);
+        for (int ib = 0; ib < n; ib += 4 * BS_FAHEAD) {
+#pragma unroll
+        for (int k = 0; k < BS_FAHEAD; k++) {
+            const int i0 = ib + 4 * k;
+            if (i0 >= n) break;
             const int nr = min(4, n - i0);
-            lt[4 * lane + 0] = make_float4(qf[0].x, qf[1].x, qf[2].x, qf[3].x);
-            lt[4 * lane + 1] = make_float4(qf[0].y, qf[1].y, qf[2].y, qf[3].y);
-            lt[4 * lane + 2] = make_float4(qf[0].z, qf[1].z, qf[2].z, qf[3].z);
-            lt[4 * lane + 3] = make_float4(qf[0].w, qf[1].w, qf[2].w, qf[3].w);
+            lt[4 * lane + 0] = make_float4(qf[k][0].x, qf[k][1].x, qf[k][2].x, qf[k][3].x);
+            lt[4 * lane + 1] = make_float4(qf[k][0].y, qf[k][1].y, qf[k][2].y, qf[k][3].y);
+            lt[4 * lane + 2] = make_float4(qf[k][0].z, qf[k][1].z, qf[k][2].z, qf[k][3].z);
+            lt[4 * lane + 3] = make_float4(qf[k][0].w, qf[k][1].w, qf[k][2].w, qf[k][3].w);
             float val[4];
 #pragma unroll
-            for (int t = 0; t < 4; t++) val[t] = act ? qb[t] : 0.0f;
-            if (i0 + 4 < n) fetch(i0 + 4);
+            for (int t = 0; t < 4; t++) val[t] = act ? qb[k][t] : 0.0f;
+            if (i0 + 4 * BS_FAHEAD < n) fetch(i0 + 4 * BS_FAHEAD, qf[k], qb[k]);
             __builtin_amdgcn_wave_barrier();
             if (i0 <= BS_HIGH) {
                 dot4_seq(val, lt, xs, 0, i0, lane);
@@ -2243,6 +2251,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
                 for (int j = 0; j < BS_HIGH; j++) yr[j] = xs[j][lane];
                 __builtin_amdgcn_wave_barrier();
             }
+        }
         }
     } else {
     // ---- forward: rows [0, lb) from LDS, then rows [lb, n) with [0, lb) in registers
