@@ -2077,59 +2077,194 @@ constexpr int BS_HIGH = 128;
 constexpr int BS_PAD = 128;   // the row buffer holds entry k at rowb[BS_PAD - shift + k]
 constexpr int BS_AHEAD = 8;   // backward rows in flight
 constexpr int BS_FAHEAD = 4;  // forward 4-row blocks in flight
+constexpr int BS_LQ = 6;      // forward: multipliers read ahead in the register part
+constexpr int BS_UQ = 6;      // backward: float4 of U read ahead in the register part
 
 // val -= rowp[t] * xsb[t][lane] for t = 0 .. n_terms-1, ascending and
-// sequential; batches of 8 operands are loaded one batch ahead.
+// sequential. Sums of DS_B terms or more run in batches of DS_B: the first
+// batch is read at term 0 and applies its first (n_terms % DS_B, else DS_B)
+// terms, each later batch starts where the previous one stopped, and every
+// batch is read while the one before it is applied (two register sets
+// used in turn; a batch past the end is read at the last in-range start
+// n_terms - DS_B and not applied, so no read leaves [0, n_terms) and the
+// reads need no branches around them). The scheduling fences keep the
+// reads ahead of the arithmetic, so the LDS latency overlaps a batch of
+// the chain.
+constexpr int DS_B = 16;
+// val - r[0] * x[0] - r[1] * x[1] - ... in order: the products first, then
+// the subtractions back to back (a subtraction issued right after the one
+// it depends on waits less than one separated from it by a product).
+template <int B>
+__device__ __forceinline__ float sub_products(float val, const float (&r)[B], const float (&x)[B]) {
+    float p[B];
+#pragma unroll
+    for (int u = 0; u < B; u++) p[u] = r[u] * x[u];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < B; u++) val = val - p[u];
+    __builtin_amdgcn_sched_barrier(0);
+    return val;
+}
+__device__ __forceinline__ void ds_load(float (&r)[DS_B], float (&x)[DS_B], const float * rowp,
+                                        const float (*xsb)[64], int t0, int lane) {
+#pragma unroll
+    for (int u = 0; u < DS_B; u++) { r[u] = rowp[t0 + u]; x[u] = xsb[t0 + u][lane]; }
+}
+// the same batch with rowp + t0 16-byte aligned (float4 reads of rowp)
+__device__ __forceinline__ void ds_load4(float (&r)[DS_B], float (&x)[DS_B], const float * rowp,
+                                         const float (*xsb)[64], int t0, int lane) {
+    const float4 * r4 = reinterpret_cast<const float4 *>(rowp + t0);
+#pragma unroll
+    for (int q = 0; q < DS_B / 4; q++) {
+        const float4 a = r4[q];
+        r[4 * q + 0] = a.x; r[4 * q + 1] = a.y; r[4 * q + 2] = a.z; r[4 * q + 3] = a.w;
+    }
+#pragma unroll
+    for (int u = 0; u < DS_B; u++) x[u] = xsb[t0 + u][lane];
+}
 __device__ __forceinline__ float dot_seq(float val, const float * rowp, const float (*xsb)[64], int n_terms,
                                          int lane) {
-    int t = 0;
-    if (n_terms >= 8) {
-        float rc[8], xc[8];
+    if (n_terms < DS_B) {
+        float r[DS_B - 1], x[DS_B - 1];
 #pragma unroll
-        for (int u = 0; u < 8; u++) { rc[u] = rowp[u]; xc[u] = xsb[u][lane]; }
-        for (; t + 16 <= n_terms; t += 8) {
-            float rn[8], xn[8];
+        for (int u = 0; u < DS_B - 1; u++)
+            if (u < n_terms) { r[u] = rowp[u]; x[u] = xsb[u][lane]; }
 #pragma unroll
-            for (int u = 0; u < 8; u++) { rn[u] = rowp[t + 8 + u]; xn[u] = xsb[t + 8 + u][lane]; }
-#pragma unroll
-            for (int u = 0; u < 8; u++) val = val - rc[u] * xc[u];
-#pragma unroll
-            for (int u = 0; u < 8; u++) { rc[u] = rn[u]; xc[u] = xn[u]; }
-        }
-#pragma unroll
-        for (int u = 0; u < 8; u++) val = val - rc[u] * xc[u];
-        t += 8;
+        for (int u = 0; u < DS_B - 1; u++)
+            if (u < n_terms) val = val - r[u] * x[u];
+        return val;
     }
-    for (; t < n_terms; t++) val = val - rowp[t] * xsb[t][lane];
+    const int rem = n_terms & (DS_B - 1);
+    const int first = rem ? rem : DS_B;
+    const int lastb = n_terms - DS_B;
+    float ra[DS_B], xa[DS_B], rb[DS_B], xb[DS_B];
+    ds_load(ra, xa, rowp, xsb, 0, lane);
+    int t = first;
+    ds_load(rb, xb, rowp, xsb, min(t, lastb), lane);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < DS_B; u++)
+        if (u < first) val = val - ra[u] * xa[u];
+    __builtin_amdgcn_sched_barrier(0);
+    while (t < n_terms) {
+        ds_load(ra, xa, rowp, xsb, min(t + DS_B, lastb), lane);
+        __builtin_amdgcn_sched_barrier(0);
+        val = sub_products(val, rb, xb);
+        t += DS_B;
+        if (t >= n_terms) break;
+        ds_load(rb, xb, rowp, xsb, min(t + DS_B, lastb), lane);
+        __builtin_amdgcn_sched_barrier(0);
+        val = sub_products(val, ra, xa);
+        t += DS_B;
+    }
+    return val;
+}
+
+// dot_seq for a number of terms n8 that is a multiple of 8, with rowp
+// 16-byte aligned: an odd eighth first, then batches of DS_B read one batch
+// ahead as in dot_seq (no partial batch, so no per-term selection).
+__device__ __forceinline__ float dot_seq8(float val, const float * rowp, const float (*xsb)[64], int n8,
+                                          int lane) {
+    if (n8 <= 0) return val;
+    const float4 * r4 = reinterpret_cast<const float4 *>(rowp);
+    float r8[8], x8[8];
+    if (n8 == 8) {
+        const float4 a = r4[0], b = r4[1];
+        r8[0] = a.x; r8[1] = a.y; r8[2] = a.z; r8[3] = a.w;
+        r8[4] = b.x; r8[5] = b.y; r8[6] = b.z; r8[7] = b.w;
+#pragma unroll
+        for (int u = 0; u < 8; u++) x8[u] = xsb[u][lane];
+        return sub_products(val, r8, x8);
+    }
+    float ra[DS_B], xa[DS_B], rb[DS_B], xb[DS_B];
+    int t;
+    if (n8 & 8) {
+        const float4 a = r4[0], b = r4[1];
+        r8[0] = a.x; r8[1] = a.y; r8[2] = a.z; r8[3] = a.w;
+        r8[4] = b.x; r8[5] = b.y; r8[6] = b.z; r8[7] = b.w;
+#pragma unroll
+        for (int u = 0; u < 8; u++) x8[u] = xsb[u][lane];
+        ds_load4(rb, xb, rowp, xsb, 8, lane);
+        __builtin_amdgcn_sched_barrier(0);
+        val = sub_products(val, r8, x8);
+        t = 8;
+    } else {
+        ds_load4(rb, xb, rowp, xsb, 0, lane);
+        t = 0;
+    }
+    const int lastb = n8 - DS_B;
+    while (true) {
+        ds_load4(ra, xa, rowp, xsb, min(t + DS_B, lastb), lane);
+        __builtin_amdgcn_sched_barrier(0);
+        val = sub_products(val, rb, xb);
+        t += DS_B;
+        if (t >= n8) break;
+        ds_load4(rb, xb, rowp, xsb, min(t + DS_B, lastb), lane);
+        __builtin_amdgcn_sched_barrier(0);
+        val = sub_products(val, ra, xa);
+        t += DS_B;
+        if (t >= n8) break;
+    }
     return val;
 }
 
 // Four rows at once: val[t] -= lt[j][t] * xsb[j - j1][lane] for j = j1 .. j2-1,
 // each row's terms in ascending j (four independent sequential sums);
-// lt holds the four rows' entries interleaved (16 bytes per j).
-__device__ __forceinline__ void dot4_seq(float (&val)[4], const float4 * lt, const float (*xsb)[64], int j1, int j2,
-                                         int lane) {
-    int j = j1;
-    for (; j + 8 <= j2; j += 8) {
-        float4 l[8];
-        float y[8];
+// lt holds the four rows' entries interleaved (16 bytes per j). Batches of
+// D4_B steps, arranged and read ahead as in dot_seq.
+constexpr int D4_B = 8;
+__device__ __forceinline__ void d4_load(float4 (&l)[D4_B], float (&y)[D4_B], const float4 * lp,
+                                        const float (*xsb)[64], int t0, int lane) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) { l[u] = lt[j + u]; y[u] = xsb[j - j1 + u][lane]; }
+    for (int u = 0; u < D4_B; u++) { l[u] = lp[t0 + u]; y[u] = xsb[t0 + u][lane]; }
+}
+__device__ __forceinline__ void d4_apply(float (&val)[4], const float4 (&l)[D4_B], const float (&y)[D4_B], int cnt) {
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
+    for (int u = 0; u < D4_B; u++) {
+        if (u < cnt) {
             val[0] = val[0] - l[u].x * y[u];
             val[1] = val[1] - l[u].y * y[u];
             val[2] = val[2] - l[u].z * y[u];
             val[3] = val[3] - l[u].w * y[u];
         }
     }
-    for (; j < j2; j++) {
-        const float4 l = lt[j];
-        const float y = xsb[j - j1][lane];
-        val[0] = val[0] - l.x * y;
-        val[1] = val[1] - l.y * y;
-        val[2] = val[2] - l.z * y;
-        val[3] = val[3] - l.w * y;
+}
+__device__ __forceinline__ void dot4_seq(float (&val)[4], const float4 * lt, const float (*xsb)[64], int j1, int j2,
+                                         int lane) {
+    const int n_terms = j2 - j1;
+    const float4 * lp = lt + j1;
+    if (n_terms < D4_B) {
+        float4 l[D4_B];
+        float y[D4_B];
+#pragma unroll
+        for (int u = 0; u < D4_B - 1; u++)
+            if (u < n_terms) { l[u] = lp[u]; y[u] = xsb[u][lane]; }
+        d4_apply(val, l, y, n_terms);
+        return;
+    }
+    const int rem = n_terms & (D4_B - 1);
+    const int first = rem ? rem : D4_B;
+    const int lastb = n_terms - D4_B;
+    float4 la[D4_B], lb[D4_B];
+    float ya[D4_B], yb[D4_B];
+    d4_load(la, ya, lp, xsb, 0, lane);
+    int t = first;
+    d4_load(lb, yb, lp, xsb, min(t, lastb), lane);
+    __builtin_amdgcn_sched_barrier(0);
+    d4_apply(val, la, ya, first);
+    __builtin_amdgcn_sched_barrier(0);
+    while (t < n_terms) {
+        d4_load(la, ya, lp, xsb, min(t + D4_B, lastb), lane);
+        __builtin_amdgcn_sched_barrier(0);
+        d4_apply(val, lb, yb, D4_B);
+        __builtin_amdgcn_sched_barrier(0);
+        t += D4_B;
+        if (t >= n_terms) break;
+        d4_load(lb, yb, lp, xsb, min(t + D4_B, lastb), lane);
+        __builtin_amdgcn_sched_barrier(0);
+        d4_apply(val, la, ya, D4_B);
+        __builtin_amdgcn_sched_barrier(0);
+        t += D4_B;
     }
 }
 
@@ -2214,18 +2349,24 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             float val[4];
 #pragma unroll
             for (int t = 0; t < 4; t++) val[t] = act ? qb[k][t] : 0.0f;
-            if (i0 + 4 * BS_FAHEAD < n) fetch(i0 + 4 * BS_FAHEAD, qf[k], qb[k]);
+            fetch(min(i0 + 4 * BS_FAHEAD, n - 1), qf[k], qb[k]);   // unconditional, as in the backward ring
             __builtin_amdgcn_wave_barrier();
             if (i0 <= BS_HIGH) {
                 dot4_seq(val, lt, xs, 0, i0, lane);
             } else {
+                // entries read BS_LQ steps ahead of their use
+                float4 lq[BS_HIGH];
+#pragma unroll
+                for (int j = 0; j < BS_LQ; j++) lq[j] = lt[j];
 #pragma unroll
                 for (int j = 0; j < BS_HIGH; j++) {
-                    const float4 l = lt[j];
-                    val[0] = val[0] - l.x * yr[j];
-                    val[1] = val[1] - l.y * yr[j];
-                    val[2] = val[2] - l.z * yr[j];
-                    val[3] = val[3] - l.w * yr[j];
+                    if (j + BS_LQ < BS_HIGH) lq[j + BS_LQ] = lt[j + BS_LQ];
+                    __builtin_amdgcn_sched_barrier(0);
+                    val[0] = val[0] - lq[j].x * yr[j];
+                    val[1] = val[1] - lq[j].y * yr[j];
+                    val[2] = val[2] - lq[j].z * yr[j];
+                    val[3] = val[3] - lq[j].w * yr[j];
+                    __builtin_amdgcn_sched_barrier(0);
                 }
                 dot4_seq(val, lt + BS_HIGH, xs, 0, i0 - BS_HIGH, lane);
             }
@@ -2302,15 +2443,21 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     }
     }
 
-    // ---- backward: rows [hb, n) from LDS, then rows [0, hb) with [hb, n) in
-    // registers. Row col of U is published shifted by -hb (entry k at
-    // brow[k]), so that the register part's entries brow[hb + i] are aligned.
-    // U rows and y values are loaded BS_AHEAD rows ahead through a register
-    // ring, so that their latency overlaps the short sums of the last rows.
+    // ---- backward: rows [hb, n) first, then rows [0, hb) with [hb, n) in
+    // registers (xh). Rows run in groups of BS_AHEAD from the top of each
+    // part (n - hb is a multiple of BS_AHEAD), so a row's sum splits into
+    // the rows above it in its own group (kept in registers, w), the earlier
+    // groups of its part (from LDS, a multiple of 8 terms) and, below hb,
+    // the register part; each piece ascends, in that order. Row col of U is
+    // published at brow, placed so that the entries of the earlier groups
+    // start 16-byte aligned (brow + col0 + 1) and, when hb > 0, the
+    // register part's entries brow[hb + i] are too. U rows and y values are
+    // loaded BS_AHEAD rows ahead through a register ring.
     const int hb = n > BS_HIGH ? n - BS_HIGH : 0;
-    float * brow = rowb + BS_PAD - hb;
-    const float * bhi = rowb + BS_PAD;   // == brow + hb
+    float * brow = rowb + BS_PAD - hb - (hb > 0 ? 0 : (n & 3));
+    const float * bhi = rowb + BS_PAD;   // == brow + hb when hb > 0
     float xh[BS_HIGH];
+    float w[BS_AHEAD];
     float4 rf[BS_AHEAD];
     float rb[BS_AHEAD];
 #pragma unroll
@@ -2320,6 +2467,9 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         rb[k] = Yt[(unsigned)(r * g.dv + vc)];
     }
     for (int col0 = n - 1; col0 >= 0; col0 -= BS_AHEAD) {
+        const bool upper = col0 >= hb;            // the whole group is on one side of hb
+        const int xoff = upper ? hb : 0;           // row r's result sits at xs[r - xoff]
+        const int n8 = (upper ? n : hb) - col0 - 1;   // earlier groups of this part
 #pragma unroll
         for (int k = 0; k < BS_AHEAD; k++) {
             const int col = col0 - k;
@@ -2335,28 +2485,66 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             brow[4 * lane + 2] = rf[k].z;
             brow[4 * lane + 3] = rf[k].w;
             const float yv = rb[k];
-            if (col - BS_AHEAD >= 0) {
-                const int r = col - BS_AHEAD;
+            __builtin_amdgcn_wave_barrier();
+            const float piv = brow[col];
+            float ug[BS_AHEAD];   // U entries of the rows above col in the group
+#pragma unroll
+            for (int j = 0; j < k; j++) ug[j] = brow[col + 1 + j];
+            float val = g.zero_val;
+            if (!(fabsf(piv) < 1e-12f)) {
+                val = act ? yv : 0.0f;
+                if (k > 0) {
+                    float pg[BS_AHEAD];
+#pragma unroll
+                    for (int j = 0; j < k; j++) pg[j] = ug[j] * w[k - 1 - j];
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int j = 0; j < k; j++) val = val - pg[j];
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                val = dot_seq8(val, brow + col0 + 1, xs + (col0 + 1 - xoff), n8, lane);
+                if (!upper) {
+                    // U entries read BS_UQ float4 ahead of their use
+                    const float4 * bhi4 = reinterpret_cast<const float4 *>(bhi);
+                    float4 uq[BS_HIGH / 4];
+#pragma unroll
+                    for (int q = 0; q < BS_UQ; q++) uq[q] = bhi4[q];
+#pragma unroll
+                    for (int q = 0; q < BS_HIGH / 4; q += 2) {
+                        if (q + BS_UQ < BS_HIGH / 4) uq[q + BS_UQ] = bhi4[q + BS_UQ];
+                        if (q + 1 + BS_UQ < BS_HIGH / 4) uq[q + 1 + BS_UQ] = bhi4[q + 1 + BS_UQ];
+                        __builtin_amdgcn_sched_barrier(0);
+                        const float r8[8] = {uq[q].x, uq[q].y, uq[q].z, uq[q].w,
+                                             uq[q + 1].x, uq[q + 1].y, uq[q + 1].z, uq[q + 1].w};
+                        const float x8[8] = {xh[4 * q + 0], xh[4 * q + 1], xh[4 * q + 2], xh[4 * q + 3],
+                                             xh[4 * q + 4], xh[4 * q + 5], xh[4 * q + 6], xh[4 * q + 7]};
+                        val = sub_products(val, r8, x8);
+                    }
+                }
+                val = val / piv;
+            }
+            w[k] = val;
+            xs[col - xoff][lane] = val;
+            {
+                // the slot's next row, refilled once its values are dead and
+                // unconditionally (row 0 again near the end): otherwise the
+                // slot holds two live values, and the copy that merges them
+                // waits for every load in flight
+                const int r = max(col - BS_AHEAD, 0);
                 rf[k] = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[r] * RG_ROWS))[lane];
                 rb[k] = Yt[(unsigned)(r * g.dv + vc)];
             }
             __builtin_amdgcn_wave_barrier();
-            const float piv = brow[col];
-            float val = g.zero_val;
-            if (!(fabsf(piv) < 1e-12f)) {
-                val = act ? yv : 0.0f;
-                if (col >= hb) {
-                    val = dot_seq(val, brow + col + 1, xs + (col + 1 - hb), n - col - 1, lane);
-                } else {
-                    val = dot_seq(val, brow + col + 1, xs + (col + 1), hb - col - 1, lane);
+        }
+    }
+    // the solution goes out after the sweep (stores inside it would make
+    // the waits for the row loads drain every access in flight): rows
+    // [0, hb) from LDS, rows [hb, n) from registers when n > BS_HIGH
+    if (act) {
+        for (int i = 0; i < (hb > 0 ? hb : n); i++) x[(unsigned)(i * g.dv + v)] = xs[i][lane];
+        if (hb > 0) {
 #pragma unroll
-                    for (int i = 0; i < BS_HIGH; i++) val -= bhi[i] * xh[i];
-                }
-                val = val / piv;
-            }
-            xs[col >= hb ? col - hb : col][lane] = val;
-            if (act) x[(unsigned)(col * g.dv + v)] = val;
-            __builtin_amdgcn_wave_barrier();
+            for (int i = 0; i < BS_HIGH; i++) x[(unsigned)((hb + i) * g.dv + v)] = xh[i];
         }
     }
 }
