@@ -2296,7 +2296,14 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     float * Yt = Yt_all + (long long)sysl * RG_ROWS * g.dv;
     float * x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
     __shared__ float xs[BS_HIGH][64];
-    __shared__ __align__(16) float rowb[BS_PAD + RG_ROWS];
+    // the forward's interleaved multipliers and the row buffers share LDS:
+    // rowb[0] holds the forward's rows when pivots were skipped, and the
+    // backward alternates U rows between rowb[0] and rowb[1]
+    __shared__ __align__(16) union {
+        float4 lt[RG_ROWS];
+        float rowb[2][BS_PAD + RG_ROWS];
+    } srows;
+    float * const rowb = srows.rowb[0];
     __shared__ float skf[RG_ROWS];   // 1 where the step eliminated, 0 where it was skipped
     __shared__ int permL[RG_ROWS];
     __shared__ int any_skip;
@@ -2320,7 +2327,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         // multipliers sit interleaved in LDS; earlier results come from LDS
         // (rows below 128 until row 128, then from registers) and the four
         // sums run side by side; the 4 x 4 triangle finishes them in order.
-        __shared__ __align__(16) float4 lt[RG_ROWS];
+        float4 * const lt = srows.lt;
         float yr[BS_HIGH];
         // rows and right-hand sides of the next BS_FAHEAD blocks in flight
         float4 qf[BS_FAHEAD][4];
@@ -2448,14 +2455,14 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     // part (n - hb is a multiple of BS_AHEAD), so a row's sum splits into
     // the rows above it in its own group (kept in registers, w), the earlier
     // groups of its part (from LDS, a multiple of 8 terms) and, below hb,
-    // the register part; each piece ascends, in that order. Row col of U is
-    // published at brow, placed so that the entries of the earlier groups
-    // start 16-byte aligned (brow + col0 + 1) and, when hb > 0, the
-    // register part's entries brow[hb + i] are too. U rows and y values are
-    // loaded BS_AHEAD rows ahead through a register ring.
+    // the register part; each piece ascends, in that order. Row col of U
+    // sits at rowb[k & 1] + bsh (k = the row's place in its group), written
+    // while the row before it runs; bsh places the entries of the earlier
+    // groups (col0 + 1 on) 16-byte aligned and, when hb > 0, the register
+    // part's entries (hb on) too. U rows and y values are loaded BS_AHEAD
+    // rows ahead through a register ring.
     const int hb = n > BS_HIGH ? n - BS_HIGH : 0;
-    float * brow = rowb + BS_PAD - hb - (hb > 0 ? 0 : (n & 3));
-    const float * bhi = rowb + BS_PAD;   // == brow + hb when hb > 0
+    const int bsh = BS_PAD - hb - (hb > 0 ? 0 : (n & 3));
     float xh[BS_HIGH];
     float w[BS_AHEAD];
     float4 rf[BS_AHEAD];
@@ -2466,10 +2473,19 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         rf[k] = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[r] * RG_ROWS))[lane];
         rb[k] = Yt[(unsigned)(r * g.dv + vc)];
     }
+    {
+        float * b0 = srows.rowb[0] + bsh;
+        b0[4 * lane + 0] = rf[0].x;
+        b0[4 * lane + 1] = rf[0].y;
+        b0[4 * lane + 2] = rf[0].z;
+        b0[4 * lane + 3] = rf[0].w;
+    }
     for (int col0 = n - 1; col0 >= 0; col0 -= BS_AHEAD) {
         const bool upper = col0 >= hb;            // the whole group is on one side of hb
         const int xoff = upper ? hb : 0;           // row r's result sits at xs[r - xoff]
         const int n8 = (upper ? n : hb) - col0 - 1;   // earlier groups of this part
+        // physical rows of the next group, lane k holding row col0 - BS_AHEAD - k
+        const int pnext = permL[max(col0 - BS_AHEAD - (lane & (BS_AHEAD - 1)), 0)];
 #pragma unroll
         for (int k = 0; k < BS_AHEAD; k++) {
             const int col = col0 - k;
@@ -2480,12 +2496,18 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
                 for (int i = 0; i < BS_HIGH; i++) xh[i] = xs[i][lane];
                 __builtin_amdgcn_wave_barrier();
             }
-            brow[4 * lane + 0] = rf[k].x;
-            brow[4 * lane + 1] = rf[k].y;
-            brow[4 * lane + 2] = rf[k].z;
-            brow[4 * lane + 3] = rf[k].w;
+            const float * brow = srows.rowb[k & 1] + bsh;
+            const float * bhi = srows.rowb[k & 1] + BS_PAD;   // == brow + hb when hb > 0
+            {
+                // the next row's U (ring slot k + 1) into the other buffer
+                float * bn = srows.rowb[(k + 1) & 1] + bsh;
+                const float4 f = rf[(k + 1) % BS_AHEAD];
+                bn[4 * lane + 0] = f.x;
+                bn[4 * lane + 1] = f.y;
+                bn[4 * lane + 2] = f.z;
+                bn[4 * lane + 3] = f.w;
+            }
             const float yv = rb[k];
-            __builtin_amdgcn_wave_barrier();
             const float piv = brow[col];
             float ug[BS_AHEAD];   // U entries of the rows above col in the group
 #pragma unroll
@@ -2531,7 +2553,8 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
                 // slot holds two live values, and the copy that merges them
                 // waits for every load in flight
                 const int r = max(col - BS_AHEAD, 0);
-                rf[k] = reinterpret_cast<const float4 *>(LU + (unsigned)(permL[r] * RG_ROWS))[lane];
+                const int pr = __builtin_amdgcn_readlane(pnext, k);
+                rf[k] = reinterpret_cast<const float4 *>(LU + (unsigned)(pr * RG_ROWS))[lane];
                 rb[k] = Yt[(unsigned)(r * g.dv + vc)];
             }
             __builtin_amdgcn_wave_barrier();
