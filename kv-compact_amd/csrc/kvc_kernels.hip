@@ -168,6 +168,7 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
     __shared__ __align__(16) float ks[SC_SLAB][SC_KEYS + 4];
     __shared__ __align__(16) float qs[SC_SLAB][SC_ROWS + 4];
     __shared__ const float * qptr[SC_ROWS];
+    __shared__ long long qoff[SC_ROWS];
     const int tid = threadIdx.x;
     const int tk = tid & 31, tr = tid >> 5;
     const long long ek = (long long)g.H * g.dk;
@@ -188,6 +189,90 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
     }
     const bool vec = (g.dk & 3) == 0 && (ek & 3) == 0 && (reinterpret_cast<uintptr_t>(Kl) & 15) == 0 &&
                      (qmode != Q_PROVIDED || ((reinterpret_cast<uintptr_t>(Q) & 15) == 0 && (g.ldQ & 3) == 0));
+    if (vec && g.dk % SC_SLAB == 0) {
+        // whole 16-byte slabs: every thread loads rows that exist (keys past
+        // the chunk read its last key, query rows past nq read row 0; their
+        // sums are not stored), with no branch around the loads, and the next
+        // slab is loaded while this one is summed
+        const float * kq[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int key = min(key0 + lr + 32 * u, c.Tc - 1);
+            kq[u] = Kl + (kix ? (long long)kix[key] : (long long)key) * ek + ld;
+        }
+        // query rows as element offsets from qbase (a pointer kept in LDS
+        // would make the row loads flat ones, which every LDS wait waits for)
+        const float * qbase = qmode == Q_PROVIDED ? Q : K;
+        for (int q0 = 0; q0 < nq; q0 += SC_ROWS) {
+            __syncthreads();
+            if (tid < SC_ROWS) {
+                const int qi = q0 + tid;
+                qoff[tid] = (query_row(g, K, Q, layer, c, qi < nq ? qi : 0, qmode) - qbase) + (long long)h * g.dk;
+            }
+            __syncthreads();
+            const float * qp = qbase + qoff[lr] + ld;
+            float acc[4][4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
+            float4 kx[4], qx;
+#pragma unroll
+            for (int u = 0; u < 4; u++) kx[u] = *reinterpret_cast<const float4 *>(kq[u]);
+            qx = *reinterpret_cast<const float4 *>(qp);
+            for (int d0 = 0; d0 < g.dk; d0 += SC_SLAB) {
+                __syncthreads();
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int kk = lr + 32 * u;
+                    ks[ld][kk] = kx[u].x; ks[ld + 1][kk] = kx[u].y; ks[ld + 2][kk] = kx[u].z; ks[ld + 3][kk] = kx[u].w;
+                }
+                qs[ld][lr] = qx.x; qs[ld + 1][lr] = qx.y; qs[ld + 2][lr] = qx.z; qs[ld + 3][lr] = qx.w;
+                __syncthreads();
+                // the next slab (the last one again at the end: no branch)
+                const int dn = min(d0 + SC_SLAB, g.dk - SC_SLAB);
+#pragma unroll
+                for (int u = 0; u < 4; u++) kx[u] = *reinterpret_cast<const float4 *>(kq[u] + dn);
+                qx = *reinterpret_cast<const float4 *>(qp + dn);
+                asm volatile("" ::: "memory");   // keeps the loads ahead of the sums, not sunk to their use
+                // dimension dd + 1 is read from LDS while dd is summed
+                float4 kv = *reinterpret_cast<const float4 *>(&ks[0][4 * tk]);
+                float4 qv = *reinterpret_cast<const float4 *>(&qs[0][4 * tr]);
+#pragma unroll
+                for (int dd = 0; dd < SC_SLAB; dd++) {
+                    float4 kn = kv, qn = qv;
+                    if (dd + 1 < SC_SLAB) {
+                        kn = *reinterpret_cast<const float4 *>(&ks[dd + 1][4 * tk]);
+                        qn = *reinterpret_cast<const float4 *>(&qs[dd + 1][4 * tr]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    const float kk[4] = {kv.x, kv.y, kv.z, kv.w}, qq[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+                    for (int i = 0; i < 4; i++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++) acc[i][j] = acc[i][j] + qq[i] * kk[j];
+                    __builtin_amdgcn_sched_barrier(0);
+                    kv = kn;
+                    qv = qn;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int qi = q0 + 4 * tr + i;
+                if (qi >= nq) continue;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int key = key0 + 4 * tk + j;
+                    if (key < c.Tc) {
+                        float v = acc[i][j] * g.inv_sqrt_dk;
+                        if (bh) v = v + bh[key];
+                        Sl[(long long)qi * s_row + key] = v;
+                    }
+                }
+            }
+        }
+        return;
+    }
     for (int q0 = 0; q0 < nq; q0 += SC_ROWS) {
         __syncthreads();
         if (tid < SC_ROWS) {
