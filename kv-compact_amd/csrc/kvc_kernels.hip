@@ -585,9 +585,107 @@ __device__ __forceinline__ void attn_sum_tile(const float * __restrict__ a, long
     }
 }
 
+// The same sums for vn == 128 with 16-byte aligned value rows: a 32 x 128
+// output block, thread (tq, tv) = (tid / 32, tid % 32) owning queries
+// 4 tq .. 4 tq + 3 and columns 4 tv .. 4 tv + 3, both read from LDS as one
+// 16-byte load per key; the weights are staged key-major. Tile loads read
+// rows that exist (clamped) and put zeros in registers for keys past n and
+// queries past nq, with no branch around the loads; the next tile is loaded
+// while this one is summed. A zero term leaves a sum unchanged: a sum that
+// starts at +0 never becomes -0 (x + y is -0 only when both are -0), and
+// x + (+0) = x for every other x.
+__device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, long long a_rs, int nq,
+                                             const float * __restrict__ val, long long val_rs, int n,
+                                             float * __restrict__ out, long long out_rs) {
+    __shared__ __align__(16) float as[AS_KT][32];
+    __shared__ __align__(16) float vs[AS_KT][128];
+    const int tid = threadIdx.x, tq = tid >> 5, tv = tid & 31;
+    // loaders: weights, thread -> query lq, keys 4 lk .. 4 lk + 3;
+    // values, thread -> keys vk + 8 u, columns 4 vc .. 4 vc + 3
+    const int lq = tid >> 3, lk = (tid & 7) * 4;
+    const int vk = tid >> 5, vc = (tid & 31) * 4;
+    for (int q0 = 0; q0 < nq; q0 += 32) {
+        const bool qok = q0 + lq < nq;
+        const float * arow = a + (long long)min(q0 + lq, nq - 1) * a_rs;
+        float ra[4];
+        float4 rv[4];
+        auto load = [&](int j0) {
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int j = j0 + lk + u;
+                const float x = arow[min(j, n - 1)];
+                ra[u] = (qok && j < n) ? x : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int j = j0 + vk + 8 * u;
+                const float4 x = *reinterpret_cast<const float4 *>(val + (long long)min(j, n - 1) * val_rs + vc);
+                rv[u] = j < n ? x : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+        };
+        float acc[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) acc[i][k] = 0.0f;
+        load(0);
+        for (int j0 = 0; j0 < n; j0 += AS_KT) {
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < 4; u++) as[lk + u][lq] = ra[u];
+#pragma unroll
+            for (int u = 0; u < 4; u++) *reinterpret_cast<float4 *>(&vs[vk + 8 * u][vc]) = rv[u];
+            __syncthreads();
+            load(j0 + AS_KT);   // past the end: clamped rows, zeros (not used)
+            asm volatile("" ::: "memory");   // keeps the loads ahead of the sums
+            float4 av = *reinterpret_cast<const float4 *>(&as[0][4 * tq]);
+            float4 vv = *reinterpret_cast<const float4 *>(&vs[0][4 * tv]);
+#pragma unroll
+            for (int jj = 0; jj < AS_KT; jj++) {
+                float4 an = av, vn = vv;
+                if (jj + 1 < AS_KT) {
+                    an = *reinterpret_cast<const float4 *>(&as[jj + 1][4 * tq]);
+                    vn = *reinterpret_cast<const float4 *>(&vs[jj + 1][4 * tv]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                const float aa[4] = {av.x, av.y, av.z, av.w}, vx[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int k = 0; k < 4; k++) acc[i][k] = acc[i][k] + aa[i] * vx[k];
+                __builtin_amdgcn_sched_barrier(0);
+                av = an;
+                vv = vn;
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int qi = q0 + 4 * tq + i;
+            if (qi < nq)
+                *reinterpret_cast<float4 *>(out + (long long)qi * out_rs + 4 * tv) =
+                    make_float4(acc[i][0], acc[i][1], acc[i][2], acc[i][3]);
+        }
+    }
+}
+
+// Two kernels, so that each holds only its own LDS tiles: k_refit_target
+// for d_v = 128 with 16-byte aligned value rows (chosen on the host), and
+// k_refit_target_any for every other shape.
 __global__ void __launch_bounds__(256)
 k_refit_target(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ A,
                const float * __restrict__ V, float * __restrict__ Y) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const long long ev = (long long)g.H * g.dv;
+    if (c.nq <= 0 || c.Tc <= 0) return;
+    attn_sum_128(A + layer * lS(g) + h * hS(g) + c.start, g.T, c.nq,
+                 V + layer * g.ldV + (long long)c.start * ev + (long long)h * g.dv, ev, c.Tc,
+                 Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv, g.dv);
+}
+
+__global__ void __launch_bounds__(256)
+k_refit_target_any(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ A,
+                   const float * __restrict__ V, float * __restrict__ Y) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const long long ev = (long long)g.H * g.dv;
@@ -3133,8 +3231,16 @@ void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st) {
 }
 
 void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStream_t st) {
-    hipLaunchKernelGGL(k_refit_target, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
-                       g, w.chunks, w.A, V, w.Y);
+    // every (layer, chunk, head) value row starts 16-byte aligned when V does
+    // and the layer, token and head strides are multiples of four floats
+    const bool v128 = g.dv == 128 && (reinterpret_cast<uintptr_t>(V) & 15) == 0 && (g.ldV & 3) == 0 &&
+                      (((long long)g.H * g.dv) & 3) == 0;
+    if (v128)
+        hipLaunchKernelGGL(k_refit_target, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
+                           g, w.chunks, w.A, V, w.Y);
+    else
+        hipLaunchKernelGGL(k_refit_target_any, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
+                           g, w.chunks, w.A, V, w.Y);
 }
 
 void launch_global_importance(const Geom & g, const Work & w, hipStream_t st) {
