@@ -42,6 +42,10 @@ struct DeviceCtx {
     std::mutex mu;
     bool ready = false;
     hipStream_t stream = nullptr;
+    // second stream for the original-attention statistics, which overlap the
+    // normal equations and factorizations (default priority, like stream)
+    hipStream_t stream2 = nullptr;
+    hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     char * arena = nullptr;
     size_t arena_cap = 0;
     hipEvent_t ev[ST_COUNT + 1] = {};
@@ -79,6 +83,9 @@ DeviceCtx * device_ctx() {
         exp2_table(tab);
         if (set_exp2_table(tab) != hipSuccess) return nullptr;
         if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
+        if (hipStreamCreateWithFlags(&c->stream2, hipStreamNonBlocking) != hipSuccess) return nullptr;
+        if (hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming) != hipSuccess) return nullptr;
+        if (hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming) != hipSuccess) return nullptr;
         for (int i = 0; i <= ST_COUNT; i++)
             if (hipEventCreate(&c->ev[i]) != hipSuccess) return nullptr;
         c->ready = true;
@@ -497,6 +504,18 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     // 6. X = softmax(S[:, sel] + beta)
     launch_ls_softmax(g, w, io.beta, st);
     (void)hipEventRecord(ev[ST_LS_SOFTMAX + 1], st);
+    // The original-attention statistics read S and V only and rewrite the rows
+    // of S they use; without refinement rounds the main path reads S no more,
+    // so they run from here on the second stream, beside the normal
+    // equations, factorizations and substitutions.
+    float * s_main = pl.qmode == pl.stats_qmode ? w.S : nullptr;
+    const bool fork = p.refine_rounds <= 0 && ctx->stream2;
+    if (fork) {
+        if (hipEventRecord(ctx->fork_ev, st) != hipSuccess ||
+            hipStreamWaitEvent(ctx->stream2, ctx->fork_ev, 0) != hipSuccess) return KV_COMPACT_E_DEVICE;
+        launch_stats_original(g, w, sw, io.K, io.V, io.Q, ctx->stream2, s_main);
+        if (hipEventRecord(ctx->join_ev, ctx->stream2) != hipSuccess) return KV_COMPACT_E_DEVICE;
+    }
     // 7. normal equations and their solution
     launch_ls_build(g, w, st);
     (void)hipEventRecord(ev[ST_LS_BUILD + 1], st);
@@ -522,8 +541,10 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     (void)hipEventRecord(ev[ST_REFINE + 1], st);
     // 8. quality statistics against the full call
     // the statistics' original scores are rows of S when both use one query set
-    launch_stats(g, w, sw, io.K, io.V, io.Q, io.beta, io.Cv, io.stats, st,
-                 pl.qmode == pl.stats_qmode ? w.S : nullptr);
+    if (!fork) launch_stats_original(g, w, sw, io.K, io.V, io.Q, st, s_main);
+    launch_stats_compacted(g, w, sw, io.K, io.V, io.Q, io.beta, io.Cv, io.stats, st);
+    if (fork && hipStreamWaitEvent(st, ctx->join_ev, 0) != hipSuccess) return KV_COMPACT_E_DEVICE;
+    launch_stats_final(g, sw, io.stats, st);
     (void)hipEventRecord(ev[ST_STATS + 1], st);
 
     hipError_t err = hipGetLastError();

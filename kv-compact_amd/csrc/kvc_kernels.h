@@ -29,6 +29,14 @@ void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st)
 void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const float * K,
                   const float * V, const float * Q, const float * beta, const float * Cv,
                   float * stats, hipStream_t st, float * S_main = nullptr);
+// the same in parts: original attention (needs S and V only), compacted
+// attention, then the statistics (needs both)
+void launch_stats_original(const Geom & g, const Work & w, const StatWork & sw, const float * K,
+                           const float * V, const float * Q, hipStream_t st, float * S_main);
+void launch_stats_compacted(const Geom & g, const Work & w, const StatWork & sw, const float * K,
+                            const float * V, const float * Q, const float * beta, const float * Cv,
+                            float * stats, hipStream_t st);
+void launch_stats_final(const Geom & g, const StatWork & sw, float * stats, hipStream_t st);
 void launch_dequant_rows(const uint8_t * src, int type, long long row_bytes, int n_el, long long rows,
                          float * dst, hipStream_t st);
 void launch_quant_rows(const float * src, long long src_ld, const int * idx, int type, int n_el,

@@ -706,7 +706,16 @@ k_refit_target_any(Geom g, const ChunkDesc * __restrict__ chunks, const float * 
 // ---------------------------------------------------------------------------
 constexpr int SV_QB = 16, SV_VB = 64, SV_KT = 64, SV_THREADS = 256;
 
-__global__ void __launch_bounds__(SV_THREADS)
+// at most 96 VGPRs (five waves per SIMD), so that a block fits on a CU
+// beside a k_ge_lu block (four waves per SIMD at up to 104 VGPRs) while the
+// original-attention statistics overlap the factorizations
+// LDS: As[2][SV_QB][SV_KT + 1] then Vs[2][SV_KT][SV_VB] (SV_LDS bytes), given
+// at launch, so that the compiler holds the kernel to 96 VGPRs (five waves
+// per SIMD): a block then fits on a CU beside a k_ge_lu block (four waves per
+// SIMD at 104 VGPRs) while the original-attention statistics overlap the
+// factorizations
+constexpr int SV_LDS = (2 * SV_QB * (SV_KT + 1) + 2 * SV_KT * SV_VB) * 4;
+__global__ void __launch_bounds__(SV_THREADS) __attribute__((amdgpu_waves_per_eu(5, 8)))
 k_stats_values(Geom g, const float * __restrict__ a_all, long long a_ls, long long a_hs, long long a_rs, int n,
                const float * __restrict__ V, const float * __restrict__ Cv, int mode, float * __restrict__ out_all,
                int mh, int mq) {
@@ -725,8 +734,9 @@ k_stats_values(Geom g, const float * __restrict__ a_all, long long a_ls, long lo
         val = Cv + ((long long)layer * g.H + h) * g.t_total * g.dv;
     }
     float * out = out_all + (((long long)layer * mh + h) * mq) * g.dv;
-    __shared__ float As[2][SV_QB][SV_KT + 1];
-    __shared__ __align__(16) float Vs[2][SV_KT][SV_VB];
+    extern __shared__ __align__(16) float sv_lds[];
+    float (*As)[SV_QB][SV_KT + 1] = reinterpret_cast<float (*)[SV_QB][SV_KT + 1]>(sv_lds);
+    float (*Vs)[SV_KT][SV_VB] = reinterpret_cast<float (*)[SV_KT][SV_VB]>(sv_lds + 2 * SV_QB * (SV_KT + 1));
     const int tid = threadIdx.x, tq = tid >> 4, tv = tid & 15;
     const int qa = q0 + tq, vc = v0 + 4 * tv;
     // tile loaders: a: 16 x 64 (4 per thread); val: 64 x 64 (16 per thread, 4 float4)
@@ -783,7 +793,7 @@ k_stats_values(Geom g, const float * __restrict__ a_all, long long a_ls, long lo
         if (t + 1 < ntiles) load((t + 1) * SV_KT);
         const int jn = min(SV_KT, n - t * SV_KT);
         if (jn == SV_KT) {
-#pragma unroll 8
+#pragma unroll 4
             for (int jj = 0; jj < SV_KT; jj++) {
                 const float a0 = As[b][tq][jj];
                 const float4 x = *reinterpret_cast<const float4 *>(&Vs[b][jj][4 * tv]);
@@ -3328,18 +3338,18 @@ void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st)
                            g, w.chunks, w.aug, w.aug_off, Cv, w.gtmp);
 }
 
-void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const float * K,
-                  const float * V, const float * Q, const float * beta, const float * Cv,
-                  float * stats, hipStream_t st, float * S_main) {
+// Original attention of the sampled queries over all T (outputs OO): needs
+// only the main scores (or the statistics' own) and V, so it may run beside
+// the compaction once the main path no longer reads S (row softmax rewrites
+// the rows of S it uses in place).
+void launch_stats_original(const Geom & g, const Work & w, const StatWork & sw, const float * K,
+                           const float * V, const float * Q, hipStream_t st, float * S_main) {
     const ChunkDesc * whole = w.chunks + g.n_chunks;      // all T keys
-    const ChunkDesc * kept = w.chunks + g.n_chunks + 1;   // the t_total kept keys
     const long long osl = (long long)sw.mh * sw.mq * g.T;
-    const long long csl = (long long)sw.mh * sw.mq * g.t_total;
     const unsigned rsm_blocks = (unsigned)cdiv(sw.mh * sw.mq, RSM_ROWS);
     const unsigned sv_blocks = (unsigned)(sw.mh * cdiv(sw.mq, SV_QB) * cdiv(g.dv, SV_VB));
-    // original attention of the sampled queries over all T: the main path's
-    // scores S [L][H][nq_max][T] hold exactly these rows when the statistics
-    // use the main query set (they are not read again), else computed here
+    // the main path's scores S [L][H][nq_max][T] hold exactly these rows when
+    // the statistics use the main query set, else they are computed here
     float * os = sw.OS;
     long long o_ls = osl, o_hs = (long long)sw.mq * g.T;
     if (S_main) {
@@ -3352,17 +3362,38 @@ void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const flo
     }
     hipLaunchKernelGGL(k_row_softmax, dim3(rsm_blocks, g.L), dim3(RSM_THREADS), 0, st,
                        os, g.T, o_ls, o_hs, (long long)g.T, sw.mh, sw.mq);
-    hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), 0, st,
-                       g, os, o_ls, o_hs, (long long)g.T, g.T, V, Cv, 1, sw.OO, sw.mh, sw.mq);
-    // compacted attention over the kept keys with beta and C_v
+    hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), SV_LDS, st,
+                       g, os, o_ls, o_hs, (long long)g.T, g.T, V, nullptr, 1, sw.OO, sw.mh, sw.mq);
+}
+
+// Compacted attention over the kept keys with beta and C_v (outputs CO), then
+// the statistics from OO and CO.
+void launch_stats_compacted(const Geom & g, const Work & w, const StatWork & sw, const float * K,
+                            const float * V, const float * Q, const float * beta, const float * Cv,
+                            float * stats, hipStream_t st) {
+    const ChunkDesc * kept = w.chunks + g.n_chunks + 1;   // the t_total kept keys
+    const long long csl = (long long)sw.mh * sw.mq * g.t_total;
+    const unsigned rsm_blocks = (unsigned)cdiv(sw.mh * sw.mq, RSM_ROWS);
+    const unsigned sv_blocks = (unsigned)(sw.mh * cdiv(sw.mq, SV_QB) * cdiv(g.dv, SV_VB));
     launch_scores(g, kept, 1, g.t_total, K, Q, sw.CS, sw.mh, sw.mq, csl, (long long)sw.mq * g.t_total, g.t_total,
                   sw.qmode, st, w.sel, beta);
     hipLaunchKernelGGL(k_row_softmax, dim3(rsm_blocks, g.L), dim3(RSM_THREADS), 0, st,
                        sw.CS, g.t_total, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, sw.mh, sw.mq);
-    hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), 0, st,
+    hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), SV_LDS, st,
                        g, sw.CS, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, g.t_total, V, Cv, 2,
                        sw.CO, sw.mh, sw.mq);
+}
+
+void launch_stats_final(const Geom & g, const StatWork & sw, float * stats, hipStream_t st) {
     hipLaunchKernelGGL(k_stats_final, dim3(g.L), dim3(128), 0, st, g, sw.OO, sw.CO, sw.mh, sw.mq, stats);
+}
+
+void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const float * K,
+                  const float * V, const float * Q, const float * beta, const float * Cv,
+                  float * stats, hipStream_t st, float * S_main) {
+    launch_stats_original(g, w, sw, K, V, Q, st, S_main);
+    launch_stats_compacted(g, w, sw, K, V, Q, beta, Cv, stats, st);
+    launch_stats_final(g, sw, stats, st);
 }
 
 void launch_dequant_rows(const uint8_t * src, int type, long long row_bytes, int n_el, long long rows,
