@@ -1742,12 +1742,31 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         return;
     }
     // xs[k][0..n) = X row k, xs[k][n..n+p) = Y row k, zero padding to wp
-    for (int e = threadIdx.x; e < nq * wp; e += blockDim.x) {
-        const int k = e / wp, j = e % wp;
-        float v = 0.0f;
-        if (j < n) v = Xh[(long long)k * g.t_total + j];
-        else if (j < w) v = Yh[(long long)k * g.dv + (j - n)];
-        xs[e] = v;
+    const bool v4 = (n & 3) == 0 && (p & 3) == 0 && (g.t_total & 3) == 0 && (g.dv & 3) == 0 &&
+                    (reinterpret_cast<uintptr_t>(Xh) & 15) == 0 && (reinterpret_cast<uintptr_t>(Yh) & 15) == 0;
+    if (v4) {
+        // 16-byte pieces with no branch around the loads (w = wp here)
+        const int n4 = n >> 2, p4 = p >> 2;
+#pragma unroll 4
+        for (int q = threadIdx.x; q < nq * n4; q += blockDim.x) {
+            const int k = q / n4, j4 = q - k * n4;
+            *reinterpret_cast<float4 *>(&xs[k * wp + 4 * j4]) =
+                *reinterpret_cast<const float4 *>(Xh + (long long)k * g.t_total + 4 * j4);
+        }
+#pragma unroll 4
+        for (int q = threadIdx.x; q < nq * p4; q += blockDim.x) {
+            const int k = q / p4, j4 = q - k * p4;
+            *reinterpret_cast<float4 *>(&xs[k * wp + n + 4 * j4]) =
+                *reinterpret_cast<const float4 *>(Yh + (long long)k * g.dv + 4 * j4);
+        }
+    } else {
+        for (int e = threadIdx.x; e < nq * wp; e += blockDim.x) {
+            const int k = e / wp, j = e % wp;
+            float v = 0.0f;
+            if (j < n) v = Xh[(long long)k * g.t_total + j];
+            else if (j < w) v = Yh[(long long)k * g.dv + (j - n)];
+            xs[e] = v;
+        }
     }
     __syncthreads();
     const int nbi = (n + 3) >> 2, nbw = wp >> 2;
@@ -1761,14 +1780,24 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         for (int a = 0; a < 4; a++)
 #pragma unroll
             for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
+        // row k + 1 is read from LDS while row k is summed (the last row
+        // again at the end: no branch around the reads)
+        float4 xi = *reinterpret_cast<const float4 *>(&xs[i0]);
+        float4 xj = *reinterpret_cast<const float4 *>(&xs[j0]);
+#pragma unroll 4
         for (int k = 0; k < nq; k++) {
-            const float4 xi = *reinterpret_cast<const float4 *>(&xs[k * wp + i0]);
-            const float4 xj = *reinterpret_cast<const float4 *>(&xs[k * wp + j0]);
+            const int kn = min(k + 1, nq - 1);
+            const float4 xin = *reinterpret_cast<const float4 *>(&xs[kn * wp + i0]);
+            const float4 xjn = *reinterpret_cast<const float4 *>(&xs[kn * wp + j0]);
+            __builtin_amdgcn_sched_barrier(0);
             const float vi[4] = {xi.x, xi.y, xi.z, xi.w}, vj[4] = {xj.x, xj.y, xj.z, xj.w};
 #pragma unroll
             for (int a = 0; a < 4; a++)
 #pragma unroll
                 for (int b = 0; b < 4; b++) acc[a][b] = acc[a][b] + vi[a] * vj[b];
+            __builtin_amdgcn_sched_barrier(0);
+            xi = xin;
+            xj = xjn;
         }
         if (vec && i0 + 3 < n && j0 + 3 < w && (j0 + 3 < n || j0 >= n)) {
             // whole tile inside M or inside B: 16-byte stores
