@@ -1747,13 +1747,11 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     if (v4) {
         // 16-byte pieces with no branch around the loads (w = wp here)
         const int n4 = n >> 2, p4 = p >> 2;
-#pragma unroll 4
         for (int q = threadIdx.x; q < nq * n4; q += blockDim.x) {
             const int k = q / n4, j4 = q - k * n4;
             *reinterpret_cast<float4 *>(&xs[k * wp + 4 * j4]) =
                 *reinterpret_cast<const float4 *>(Xh + (long long)k * g.t_total + 4 * j4);
         }
-#pragma unroll 4
         for (int q = threadIdx.x; q < nq * p4; q += blockDim.x) {
             const int k = q / p4, j4 = q - k * p4;
             *reinterpret_cast<float4 *>(&xs[k * wp + n + 4 * j4]) =
@@ -1784,7 +1782,6 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         // again at the end: no branch around the reads)
         float4 xi = *reinterpret_cast<const float4 *>(&xs[i0]);
         float4 xj = *reinterpret_cast<const float4 *>(&xs[j0]);
-#pragma unroll 4
         for (int k = 0; k < nq; k++) {
             const int kn = min(k + 1, nq - 1);
             const float4 xin = *reinterpret_cast<const float4 *>(&xs[kn * wp + i0]);
