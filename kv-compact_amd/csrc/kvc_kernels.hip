@@ -27,7 +27,11 @@ namespace kvc {
 // ---------------------------------------------------------------------------
 __constant__ uint64_t c_exp2_tab[32];
 
-__device__ __forceinline__ float expf_ref(float x) {
+// tab: c_exp2_tab, or a copy of it in LDS. Kernels that store results
+// between exponentials use the LDS copy: a lane-indexed lookup in constant
+// memory is a vector memory load, and waiting for it also waits for every
+// store in flight.
+__device__ __forceinline__ float expf_ref(float x, const uint64_t * tab = c_exp2_tab) {
     if (x < -0x1.9fe368p6f) return 0.0f;
     if (x > 0x1.62e42ep6f) return __int_as_float(0x7f800000);
     const double N = 32.0;
@@ -42,7 +46,7 @@ __device__ __forceinline__ float expf_ref(float x) {
     uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= shift;
     double r = __builtin_fma(inv_ln2_n, xd, -kd);
-    uint64_t tb = c_exp2_tab[ki % 32] + (ki << 47);
+    uint64_t tb = tab[ki % 32] + (ki << 47);
     double s = __longlong_as_double((long long)tb);
     double p = __builtin_fma(c0, r, c1);
     double r2 = r * r;
@@ -430,8 +434,10 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
     float * Eh = E ? E + layer * lS(g) + h * hS(g) + c.start : nullptr;
     __shared__ float rmax[SM_MAXQ], rinv[SM_MAXQ];
     __shared__ float eb[SM_TROWS][SM_TILE + 1];
+    __shared__ uint64_t etab[32];
     const int nq = c.nq, n = c.Tc;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    if (tid < 32) etab[tid] = c_exp2_tab[tid];   // visible after the barrier below
     // 1. row maxima
     for (int r = wv; r < nq; r += 4) {
         const float m = wave_ref_row_max(Sh + r * rs, n, lane);
@@ -458,7 +464,7 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
                     const int rr = wv + 4 * u;
                     if (rr < nr) {
                         const int r = r0 + rr;
-                        const float e = expf_ref(sv[u] - rmax[r]);
+                        const float e = expf_ref(sv[u] - rmax[r], etab);
                         eb[rr][kk] = e;
                         Ah[r * rs + t0 + kk] = e;
                         if (Eh) Eh[r * rs + t0 + kk] = e;
@@ -1374,6 +1380,8 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
     const long long hsX = (long long)g.nq_max * g.t_total;
     float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    __shared__ uint64_t etab[32];
+    if (tid < 32) etab[tid] = c_exp2_tab[tid];   // visible after the barriers below
     if (t > LSX_COLS) {
         // large chunks: row by row through global memory
         __shared__ float red[16];
@@ -1386,7 +1394,7 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
             const float m = ref_row_max(xr, t, red);
             if (tid == 0) rmax1 = m;
             __syncthreads();
-            for (int j = tid; j < t; j += blockDim.x) xr[j] = expf_ref(xr[j] - rmax1);
+            for (int j = tid; j < t; j += blockDim.x) xr[j] = expf_ref(xr[j] - rmax1, etab);
             __syncthreads();
             if (tid == 0) {
                 float sum = 0.0f;
@@ -1441,7 +1449,7 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
         __syncthreads();
         for (int e = tid; e < nr * LSX_COLS; e += blockDim.x) {
             const int r = e / LSX_COLS, j = e % LSX_COLS;
-            if (j < t) xs[r][j] = expf_ref(xs[r][j] - rmax[r]);
+            if (j < t) xs[r][j] = expf_ref(xs[r][j] - rmax[r], etab);
         }
         __syncthreads();
         if (tid < nr) {
@@ -2908,6 +2916,8 @@ k_row_softmax(float * __restrict__ x, int n, long long ls, long long hs, long lo
     __shared__ float mx[RSM_ROWS], inv[RSM_ROWS];
     __shared__ float tile[2][RSM_ROWS][RSM_TILE + 1];
     __shared__ unsigned red[RSM_THREADS / 64][RSM_ROWS];
+    __shared__ uint64_t etab[32];
+    if (tid < 32) etab[tid] = c_exp2_tab[tid];   // visible after the barriers below
     float * rowp[RSM_ROWS];
 #pragma unroll
     for (int r = 0; r < RSM_ROWS; r++) {
@@ -2953,7 +2963,7 @@ k_row_softmax(float * __restrict__ x, int n, long long ls, long long hs, long lo
 #pragma unroll
         for (int r = 0; r < RSM_ROWS; r++) {
             if (r < nrows) {
-                const float e = expf_ref(v[r] - mx[r]);
+                const float e = expf_ref(v[r] - mx[r], etab);
                 rowp[r][j] = e;
                 tile[b][r][c] = e;
             }
