@@ -42,10 +42,14 @@ struct DeviceCtx {
     std::mutex mu;
     bool ready = false;
     hipStream_t stream = nullptr;
-    // second stream for the original-attention statistics, which overlap the
-    // normal equations and factorizations (default priority, like stream)
+    // second stream (default priority, like stream) for work that runs beside
+    // the main chain: the refit target during the selection, and the
+    // original-attention statistics during the normal equations and
+    // factorizations
     hipStream_t stream2 = nullptr;
     hipEvent_t fork_ev = nullptr, join_ev = nullptr;
+    hipEvent_t refit_fork = nullptr, refit_join = nullptr;
+    hipEvent_t refit_t[2] = {};   // timing of the refit target on the second stream
     char * arena = nullptr;
     size_t arena_cap = 0;
     hipEvent_t ev[ST_COUNT + 1] = {};
@@ -86,6 +90,10 @@ DeviceCtx * device_ctx() {
         if (hipStreamCreateWithFlags(&c->stream2, hipStreamNonBlocking) != hipSuccess) return nullptr;
         if (hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming) != hipSuccess) return nullptr;
         if (hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming) != hipSuccess) return nullptr;
+        if (hipEventCreateWithFlags(&c->refit_fork, hipEventDisableTiming) != hipSuccess) return nullptr;
+        if (hipEventCreateWithFlags(&c->refit_join, hipEventDisableTiming) != hipSuccess) return nullptr;
+        for (int i = 0; i < 2; i++)
+            if (hipEventCreate(&c->refit_t[i]) != hipSuccess) return nullptr;
         for (int i = 0; i <= ST_COUNT; i++)
             if (hipEventCreate(&c->ev[i]) != hipSuccess) return nullptr;
         c->ready = true;
@@ -449,6 +457,9 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     if (hipMemcpyAsync(w.aug_off, aug_off.data(), aug_off.size() * sizeof(long long),
                        hipMemcpyHostToDevice, st) != hipSuccess) return KV_COMPACT_E_DEVICE;
 
+    // second-stream work of an earlier call that ended early may still use the workspace
+    if (ctx->stream2 && (hipEventRecord(ctx->refit_join, ctx->stream2) != hipSuccess ||
+                         hipStreamWaitEvent(st, ctx->refit_join, 0) != hipSuccess)) return KV_COMPACT_E_DEVICE;
     if (hipMemsetAsync(w.status, 0, sizeof(int), st) != hipSuccess) return KV_COMPACT_E_DEVICE;
     hipEvent_t * ev = ctx->ev;
     (void)hipEventRecord(ev[0], st);
@@ -459,8 +470,20 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     // 2. chunk softmax + per-head importance
     launch_chunk_softmax(g, w, st);
     (void)hipEventRecord(ev[ST_SOFTMAX + 1], st);
-    // 3. refit target Y = A V
-    launch_refit_target(g, w, io.V, st);
+    // 3. refit target Y = A V. Only the normal equations read Y, so it runs
+    //    on the second stream beside the selection (whose greedy pass is one
+    //    short serial chain per unit and leaves the chip mostly idle).
+    const bool refit_fork = ctx->stream2 != nullptr;
+    if (refit_fork) {
+        if (hipEventRecord(ctx->refit_fork, st) != hipSuccess ||
+            hipStreamWaitEvent(ctx->stream2, ctx->refit_fork, 0) != hipSuccess) return KV_COMPACT_E_DEVICE;
+        (void)hipEventRecord(ctx->refit_t[0], ctx->stream2);
+        launch_refit_target(g, w, io.V, ctx->stream2);
+        (void)hipEventRecord(ctx->refit_t[1], ctx->stream2);
+        if (hipEventRecord(ctx->refit_join, ctx->stream2) != hipSuccess) return KV_COMPACT_E_DEVICE;
+    } else {
+        launch_refit_target(g, w, io.V, st);
+    }
     (void)hipEventRecord(ev[ST_REFIT + 1], st);
     // 4. global importance (+R-KV), then top-t or the diversity greedy pass
     launch_global_importance(g, w, st);
@@ -517,6 +540,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         if (hipEventRecord(ctx->join_ev, ctx->stream2) != hipSuccess) return KV_COMPACT_E_DEVICE;
     }
     // 7. normal equations and their solution
+    if (refit_fork && hipStreamWaitEvent(st, ctx->refit_join, 0) != hipSuccess) return KV_COMPACT_E_DEVICE;
     launch_ls_build(g, w, st);
     (void)hipEventRecord(ev[ST_LS_BUILD + 1], st);
     launch_ge_lu(g, w, st);
@@ -564,6 +588,12 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         float ms = 0.0f;
         (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
         ctx->stage_ms[i] = ms;
+    }
+    if (refit_fork) {
+        // the refit target's own time on the second stream (it overlaps the selection)
+        float ms = 0.0f;
+        (void)hipEventElapsedTime(&ms, ctx->refit_t[0], ctx->refit_t[1]);
+        ctx->stage_ms[ST_REFIT] = ms;
     }
     if (tm) {
         tm->scoring_ms = ctx->stage_ms[ST_SCORES] + ctx->stage_ms[ST_SOFTMAX] + ctx->stage_ms[ST_SELECT];
