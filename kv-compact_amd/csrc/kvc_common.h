@@ -47,6 +47,7 @@ struct Geom {
 // Device scratch for one batch (all pointers device memory).
 struct Work {
     float * S;        // [L][H][nq_max][T]   scaled scores per chunk column range
+    unsigned * smax;  // [L][H][nq_max][n_chunks][ceil(Tc_max/128)] order keys of the scoring tiles' row maxima
     float * A;        // [L][H][nq_max][T]   softmax weights
     float * E;        // [L][H][nq_max][T]   unnormalised exp (only when beta is solved)
     float * rowsum;   // [L][n_chunks][H][nq_max]

@@ -312,6 +312,7 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     const size_t tt = pl.t_total, dv = io.dv;
     Work ww{};
     ww.S = cv.take<float>(L * H * nqm * T);
+    ww.smax = cv.take<unsigned>(L * H * nqm * nc * (((size_t)pl.Tc_max + 127) / 128));
     ww.A = cv.take<float>(L * H * nqm * T);
     ww.E = need_e ? cv.take<float>(L * H * nqm * T) : nullptr;
     ww.rowsum = cv.take<float>(L * nc * H * nqm);
@@ -465,7 +466,8 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     (void)hipEventRecord(ev[0], st);
     // 1. scores for every (layer, chunk, head)
     launch_scores(g, w.chunks, pl.n_chunks, pl.Tc_max, io.K, io.Q, w.S, io.H, pl.nq_max,
-                  (long long)io.H * pl.nq_max * io.T, (long long)pl.nq_max * io.T, io.T, pl.qmode, st);
+                  (long long)io.H * pl.nq_max * io.T, (long long)pl.nq_max * io.T, io.T, pl.qmode, st,
+                  nullptr, nullptr, w.smax);
     (void)hipEventRecord(ev[ST_SCORES + 1], st);
     // 2. chunk softmax + per-head importance
     launch_chunk_softmax(g, w, st);

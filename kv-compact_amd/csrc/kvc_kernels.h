@@ -9,7 +9,7 @@ hipError_t set_exp2_table(const uint64_t * tab32);
 void launch_scores(const Geom & g, const ChunkDesc * chunks, int n_chunk_units, int Tc_max,
                    const float * K, const float * Q, float * S, int Hs, int nq_cap,
                    long long s_layer, long long s_head, long long s_row, int qmode, hipStream_t st,
-                   const int * key_idx = nullptr, const float * beta = nullptr);
+                   const int * key_idx = nullptr, const float * beta = nullptr, unsigned * tmax = nullptr);
 void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st);
 void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStream_t st);
 void launch_global_importance(const Geom & g, const Work & w, hipStream_t st);

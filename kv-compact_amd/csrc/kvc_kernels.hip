@@ -156,14 +156,34 @@ __device__ __forceinline__ long long hS(const Geom & g) { return (long long)g.nq
 // slabs of 32, transposed (dimension-major) so each thread reads its 4 keys
 // and its 4 rows as one 16-byte load each. grid = (ceil(Tc_max/128),
 // n_chunks * Hs, L); query rows beyond 32 loop.
+// tmax (optional): each block also writes, per query row, the order key
+// (score_key) of its largest non-NaN stored score, or of -inf, at
+// tmax[(((layer * Hs + h) * nq_max + qi) * n_chunks + chunk) * gridDim.x + blockIdx.x];
+// the chunk softmax takes its row maxima from these instead of re-reading S.
 // ---------------------------------------------------------------------------
 constexpr int SC_KEYS = 128, SC_SLAB = 32, SC_ROWS = 32;
+
+// max of x over lanes 0-31 in lane 31 and over lanes 32-63 in lane 63
+__device__ __forceinline__ unsigned dpp_half_max_u32(unsigned x) {
+#define KVC_DPP_STEP(ctrl, rmask)                                                                  \
+    {                                                                                              \
+        const unsigned t = (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, ctrl, rmask, 0xf, false); \
+        x = t > x ? t : x;                                                                         \
+    }
+    KVC_DPP_STEP(0x111, 0xf)   // row_shr:1
+    KVC_DPP_STEP(0x112, 0xf)   // row_shr:2
+    KVC_DPP_STEP(0x114, 0xf)   // row_shr:4
+    KVC_DPP_STEP(0x118, 0xf)   // row_shr:8
+    KVC_DPP_STEP(0x142, 0xa)   // row_bcast:15
+#undef KVC_DPP_STEP
+    return x;
+}
 
 __global__ void __launch_bounds__(256)
 k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ K,
          const float * __restrict__ Q, float * __restrict__ S, int Hs, int nq_cap,
          long long s_layer, long long s_head, long long s_row, int qmode,
-         const int * __restrict__ key_idx, const float * __restrict__ beta) {
+         const int * __restrict__ key_idx, const float * __restrict__ beta, unsigned * __restrict__ tmax) {
     const int c_idx = blockIdx.y / Hs, h = blockIdx.y % Hs, layer = blockIdx.z;
     const ChunkDesc c = chunks[c_idx];
     const int key0 = blockIdx.x * SC_KEYS;
@@ -181,6 +201,35 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
     const int * kix = key_idx ? key_idx + (long long)layer * g.t_total : nullptr;
     const float * bh = beta ? beta + ((long long)layer * g.H + h) * g.t_total : nullptr;
     float * Sl = S + layer * s_layer + h * s_head + c.start;
+    // scaled (+ beta) scores of rows q0 + 4 tr .. + 3 out to S, and each row's tile maximum to tmax
+    auto store_tile = [&](const float (&acc)[4][4], int q0) {
+        unsigned mk[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int qi = q0 + 4 * tr + i;
+            mk[i] = score_key(-INFINITY);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int key = key0 + 4 * tk + j;
+                if (key < c.Tc) {
+                    float v = acc[i][j] * g.inv_sqrt_dk;
+                    if (bh) v = v + bh[key];
+                    if (qi < nq) Sl[(long long)qi * s_row + key] = v;
+                    if (v == v && score_key(v) > mk[i]) mk[i] = score_key(v);
+                }
+            }
+        }
+        if (tmax) {
+            const long long nt = gridDim.x, ncu = gridDim.y / Hs;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const unsigned m = dpp_half_max_u32(mk[i]);
+                const int qi = q0 + 4 * tr + i;
+                if ((tid & 31) == 31 && qi < nq)
+                    tmax[((((long long)layer * Hs + h) * g.nq_max + qi) * ncu + c_idx) * nt + blockIdx.x] = m;
+            }
+        }
+    };
     // tile loaders: 8 threads per key row (4 dims each, 16-byte loads when
     // aligned), keys (tid >> 3) + 32 u; query rows likewise
     const int ld = (tid & 7) * 4, lr = tid >> 3;
@@ -260,20 +309,7 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
                     qv = qn;
                 }
             }
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int qi = q0 + 4 * tr + i;
-                if (qi >= nq) continue;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int key = key0 + 4 * tk + j;
-                    if (key < c.Tc) {
-                        float v = acc[i][j] * g.inv_sqrt_dk;
-                        if (bh) v = v + bh[key];
-                        Sl[(long long)qi * s_row + key] = v;
-                    }
-                }
-            }
+            store_tile(acc, q0);
         }
         return;
     }
@@ -335,20 +371,7 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
                     for (int j = 0; j < 4; j++) acc[i][j] = acc[i][j] + qq[i] * kk[j];
             }
         }
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int qi = q0 + 4 * tr + i;
-            if (qi >= nq) continue;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int key = key0 + 4 * tk + j;
-                if (key < c.Tc) {
-                    float v = acc[i][j] * g.inv_sqrt_dk;
-                    if (bh) v = v + bh[key];
-                    Sl[(long long)qi * s_row + key] = v;
-                }
-            }
-        }
+        store_tile(acc, q0);
     }
 }
 
@@ -424,7 +447,7 @@ constexpr int SM_MAXQ = 256, SM_TILE = 64, SM_TROWS = 32;
 
 __global__ void __launch_bounds__(256)
 k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ S,
-                     float * __restrict__ A, float * __restrict__ E, float * __restrict__ rowsum,
+                     const unsigned * __restrict__ smax, float * __restrict__ A, float * __restrict__ E, float * __restrict__ rowsum,
                      float * __restrict__ imp) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
@@ -438,10 +461,23 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
     const int nq = c.nq, n = c.Tc;
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     if (tid < 32) etab[tid] = c_exp2_tab[tid];   // visible after the barrier below
-    // 1. row maxima
-    for (int r = wv; r < nq; r += 4) {
-        const float m = wave_ref_row_max(Sh + r * rs, n, lane);
-        if (lane == 0) rmax[r] = m;
+    // 1. row maxima: from the scoring tiles' maxima (smax, see k_scores), or
+    //    one wave per row over S
+    if (smax) {
+        const int nt = (g.Tc_max + SC_KEYS - 1) / SC_KEYS, ntc = (n + SC_KEYS - 1) / SC_KEYS;
+        for (int r = tid; r < nq; r += blockDim.x) {
+            const unsigned * sm = smax + ((((long long)layer * g.H + h) * g.nq_max + r) * g.n_chunks + c_idx) * nt;
+            unsigned k = sm[0];
+            for (int t = 1; t < ntc; t++) k = max(k, sm[t]);
+            const float mm = __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+            const float r0 = Sh[r * rs];
+            rmax[r] = (r0 != r0) ? r0 : ((mm > r0) ? mm : r0);
+        }
+    } else {
+        for (int r = wv; r < nq; r += 4) {
+            const float m = wave_ref_row_max(Sh + r * rs, n, lane);
+            if (lane == 0) rmax[r] = m;
+        }
     }
     __syncthreads();
     // 2. exponentials and ordered row sums, 32 rows at a time
@@ -3265,15 +3301,15 @@ hipError_t set_exp2_table(const uint64_t * tab32) {
 void launch_scores(const Geom & g, const ChunkDesc * chunks, int n_chunk_units, int Tc_max,
                    const float * K, const float * Q, float * S, int Hs, int nq_cap,
                    long long s_layer, long long s_head, long long s_row, int qmode, hipStream_t st,
-                   const int * key_idx, const float * beta) {
+                   const int * key_idx, const float * beta, unsigned * tmax) {
     dim3 grid(cdiv(Tc_max, SC_KEYS), n_chunk_units * Hs, g.L);
     hipLaunchKernelGGL(k_scores, grid, dim3(256), 0, st, g, chunks, K, Q, S, Hs, nq_cap,
-                       s_layer, s_head, s_row, qmode, key_idx, beta);
+                       s_layer, s_head, s_row, qmode, key_idx, beta, tmax);
 }
 
 void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st) {
     hipLaunchKernelGGL(k_softmax_importance, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
-                       g, w.chunks, w.S, w.A, w.E, w.E ? w.rowsum : nullptr, w.imp);
+                       g, w.chunks, w.S, w.smax, w.A, w.E, w.E ? w.rowsum : nullptr, w.imp);
 }
 
 void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStream_t st) {
