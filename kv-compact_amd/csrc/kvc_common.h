@@ -48,9 +48,10 @@ struct Geom {
 struct Work {
     float * S;        // [L][H][nq_max][T]   scaled scores per chunk column range
     unsigned * smax;  // [L][H][nq_max][n_chunks][ceil(Tc_max/128)] order keys of the scoring tiles' row maxima
-    float * A;        // [L][H][nq_max][T]   softmax weights
-    float * E;        // [L][H][nq_max][T]   unnormalised exp (only when beta is solved)
+    float * A;        // [L][H][nq_max][T]   unnormalised exponentials e; the softmax weights are e * ainv[row]
+    float * E;        // == A when beta is solved (the exp scores), else nullptr
     float * rowsum;   // [L][n_chunks][H][nq_max]
+    float * ainv;     // [L][n_chunks][H][nq_max] 1 / (row sum + 1e-12f) of the chunk softmax
     float * imp;      // [L][H][T]           per-head importance
     float * gimp;     // [L][T]              global importance (after R-KV weights)
     float * Y;        // [L][n_chunks][H][nq_max][dv]

@@ -314,8 +314,9 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     ww.S = cv.take<float>(L * H * nqm * T);
     ww.smax = cv.take<unsigned>(L * H * nqm * nc * (((size_t)pl.Tc_max + 127) / 128));
     ww.A = cv.take<float>(L * H * nqm * T);
-    ww.E = need_e ? cv.take<float>(L * H * nqm * T) : nullptr;
+    ww.E = need_e ? ww.A : nullptr;   // A keeps the unnormalised exponentials
     ww.rowsum = cv.take<float>(L * nc * H * nqm);
+    ww.ainv = cv.take<float>(L * nc * H * nqm);
     ww.imp = cv.take<float>(L * H * T);
     ww.gimp = cv.take<float>(L * T);
     ww.Y = cv.take<float>(L * nc * H * nqm * dv);

@@ -203,11 +203,14 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
     float * Sl = S + layer * s_layer + h * s_head + c.start;
     // scaled (+ beta) scores of rows q0 + 4 tr .. + 3 out to S, and each row's tile maximum to tmax
     auto store_tile = [&](const float (&acc)[4][4], int q0) {
-        unsigned mk[4];
+        // fmaxf returns the other operand for a NaN, so mx is the largest
+        // non-NaN score or -inf (a zero's sign may differ from a scan's
+        // first-found zero, which leaves every s - max unchanged)
+        float mx[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int qi = q0 + 4 * tr + i;
-            mk[i] = score_key(-INFINITY);
+            mx[i] = -INFINITY;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int key = key0 + 4 * tk + j;
@@ -215,7 +218,7 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
                     float v = acc[i][j] * g.inv_sqrt_dk;
                     if (bh) v = v + bh[key];
                     if (qi < nq) Sl[(long long)qi * s_row + key] = v;
-                    if (v == v && score_key(v) > mk[i]) mk[i] = score_key(v);
+                    mx[i] = fmaxf(mx[i], v);
                 }
             }
         }
@@ -223,7 +226,7 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
             const long long nt = gridDim.x, ncu = gridDim.y / Hs;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const unsigned m = dpp_half_max_u32(mk[i]);
+                const unsigned m = dpp_half_max_u32(score_key(mx[i]));
                 const int qi = q0 + 4 * tr + i;
                 if ((tid & 31) == 31 && qi < nq)
                     tmax[((((long long)layer * Hs + h) * g.nq_max + qi) * ncu + c_idx) * nt + blockIdx.x] = m;
@@ -438,23 +441,25 @@ __device__ __forceinline__ float wave_ref_row_max(const float * row, int n, int 
 
 // Chunk softmax + per-key importance (math.h:142-248), for up to SM_MAXQ rows:
 //  1. row maxima, one wave per row;
-//  2. e = expf(s - max) over 64-key tiles: written unnormalised to A (and E),
-//     staged in LDS so that one thread per row adds its tile in key order;
-//  3. one thread per key: A = e * inv row by row, importance accumulated in
-//     row order (max / sum of squares / sum), finalised as the reference.
+//  2. e = expf(s - max) over 64-key tiles: written unnormalised to A, staged
+//     in LDS so that one thread per row adds its tile in key order; the row's
+//     inv = 1 / (sum + 1e-12f) goes to ainv (and the sum to rowsum, if given);
+//  3. one thread per key: the weights a = e * inv row by row, importance
+//     accumulated in row order (max / sum of squares / sum), finalised as the
+//     reference. A keeps e: its consumers form a = e * inv themselves (the
+//     same single rounding), and e itself is the beta fit's exp scores.
 // grid = (n_chunks * H, L)
 constexpr int SM_MAXQ = 256, SM_TILE = 64, SM_TROWS = 32;
 
 __global__ void __launch_bounds__(256)
 k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ S,
-                     const unsigned * __restrict__ smax, float * __restrict__ A, float * __restrict__ E, float * __restrict__ rowsum,
-                     float * __restrict__ imp) {
+                     const unsigned * __restrict__ smax, float * __restrict__ A, float * __restrict__ rowsum,
+                     float * __restrict__ ainv, float * __restrict__ imp) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const long long rs = g.T;
     const float * Sh = S + layer * lS(g) + h * hS(g) + c.start;
     float * Ah = A + layer * lS(g) + h * hS(g) + c.start;
-    float * Eh = E ? E + layer * lS(g) + h * hS(g) + c.start : nullptr;
     __shared__ float rmax[SM_MAXQ], rinv[SM_MAXQ];
     __shared__ float eb[SM_TROWS][SM_TILE + 1];
     __shared__ uint64_t etab[32];
@@ -503,7 +508,6 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
                         const float e = expf_ref(sv[u] - rmax[r], etab);
                         eb[rr][kk] = e;
                         Ah[r * rs + t0 + kk] = e;
-                        if (Eh) Eh[r * rs + t0 + kk] = e;
                     }
                 }
             }
@@ -523,12 +527,15 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
         }
         if (tid < nr) {
             const int r = r0 + tid;
-            if (rowsum) rowsum[(((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max + r] = sum;
-            rinv[r] = 1.0f / (sum + 1e-12f);
+            const long long ro = (((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max + r;
+            if (rowsum) rowsum[ro] = sum;
+            const float iv = 1.0f / (sum + 1e-12f);
+            rinv[r] = iv;
+            ainv[ro] = iv;
         }
     }
     __syncthreads();
-    // 3. normalise and aggregate per key in row order
+    // 3. the weights per key, aggregated in row order
     float * imph = imp + ((long long)layer * g.H + h) * g.T + c.start;
     const float inv_m = 1.0f / (float)nq;
     for (int j = tid; j < n; j += blockDim.x) {
@@ -545,7 +552,6 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
                 if (u < qn) {
                     const int qi = q0 + u;
                     const float a = ev[u] * rinv[qi];
-                    Ah[qi * rs + j] = a;
                     if (g.score_method == 0) {
                         if (a > acc) acc = a;
                     } else if (g.score_method == 1) {
@@ -565,7 +571,9 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
 // ---------------------------------------------------------------------------
 // Refit target Y = A V per (layer, chunk, head) (math.h:70-80): each output
 // accumulated sequentially over the chunk's keys; keys are staged through LDS
-// 32 at a time. grid (n_chunks*H, L)
+// 32 at a time. The weights are formed on the way in as a = e * ascale[row]
+// (the unnormalised exponentials times the row's 1 / (sum + 1e-12f), the
+// chunk softmax's own product). grid (n_chunks*H, L)
 // ---------------------------------------------------------------------------
 constexpr int AS_KT = 32;
 
@@ -574,7 +582,8 @@ constexpr int AS_KT = 32;
 // output block (QB = TQ*QR, VB = TV*VR); every output is a sequential sum
 // over the keys in order.
 template <int QR, int VR, int TV>
-__device__ __forceinline__ void attn_sum_tile(const float * __restrict__ a, long long a_rs, int nq,
+__device__ __forceinline__ void attn_sum_tile(const float * __restrict__ a, const float * __restrict__ ascale,
+                                              long long a_rs, int nq,
                                               const float * __restrict__ val, long long val_rs, int n,
                                               int vn, float * __restrict__ out, long long out_rs) {
     constexpr int TQ = 256 / TV, QB = TQ * QR, VB = TV * VR;
@@ -595,7 +604,7 @@ __device__ __forceinline__ void attn_sum_tile(const float * __restrict__ a, long
                 __syncthreads();
                 for (int e = threadIdx.x; e < QB * AS_KT; e += 256) {
                     const int qi = e / AS_KT, jj = e % AS_KT;
-                    as[qi][jj] = (qi < qb && jj < jn) ? a[(long long)(q0 + qi) * a_rs + j0 + jj] : 0.0f;
+                    as[qi][jj] = (qi < qb && jj < jn) ? a[(long long)(q0 + qi) * a_rs + j0 + jj] * ascale[q0 + qi] : 0.0f;
                 }
                 for (int e = threadIdx.x; e < AS_KT * VB; e += 256) {
                     const int jj = e / VB, vv = e % VB;
@@ -636,7 +645,8 @@ __device__ __forceinline__ void attn_sum_tile(const float * __restrict__ a, long
 // while this one is summed. A zero term leaves a sum unchanged: a sum that
 // starts at +0 never becomes -0 (x + y is -0 only when both are -0), and
 // x + (+0) = x for every other x.
-__device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, long long a_rs, int nq,
+__device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, const float * __restrict__ ascale,
+                                             long long a_rs, int nq,
                                              const float * __restrict__ val, long long val_rs, int n,
                                              float * __restrict__ out, long long out_rs) {
     __shared__ __align__(16) float as[AS_KT][32];
@@ -649,13 +659,14 @@ __device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, long 
     for (int q0 = 0; q0 < nq; q0 += 32) {
         const bool qok = q0 + lq < nq;
         const float * arow = a + (long long)min(q0 + lq, nq - 1) * a_rs;
+        const float sc = ascale[min(q0 + lq, nq - 1)];
         float ra[4];
         float4 rv[4];
         auto load = [&](int j0) {
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int j = j0 + lk + u;
-                const float x = arow[min(j, n - 1)];
+                const float x = arow[min(j, n - 1)] * sc;
                 ra[u] = (qok && j < n) ? x : 0.0f;
             }
 #pragma unroll
@@ -715,23 +726,25 @@ __device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, long 
 // k_refit_target_any for every other shape.
 __global__ void __launch_bounds__(256)
 k_refit_target(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ A,
-               const float * __restrict__ V, float * __restrict__ Y) {
+               const float * __restrict__ ainv, const float * __restrict__ V, float * __restrict__ Y) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const long long ev = (long long)g.H * g.dv;
     if (c.nq <= 0 || c.Tc <= 0) return;
-    attn_sum_128(A + layer * lS(g) + h * hS(g) + c.start, g.T, c.nq,
+    const float * sc = ainv + (((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max;
+    attn_sum_128(A + layer * lS(g) + h * hS(g) + c.start, sc, g.T, c.nq,
                  V + layer * g.ldV + (long long)c.start * ev + (long long)h * g.dv, ev, c.Tc,
                  Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv, g.dv);
 }
 
 __global__ void __launch_bounds__(256)
 k_refit_target_any(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ A,
-                   const float * __restrict__ V, float * __restrict__ Y) {
+                   const float * __restrict__ ainv, const float * __restrict__ V, float * __restrict__ Y) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const long long ev = (long long)g.H * g.dv;
-    attn_sum_tile<4, 4, 32>(A + layer * lS(g) + h * hS(g) + c.start, g.T, c.nq,
+    const float * sc = ainv + (((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max;
+    attn_sum_tile<4, 4, 32>(A + layer * lS(g) + h * hS(g) + c.start, sc, g.T, c.nq,
                             V + layer * g.ldV + (long long)c.start * ev + (long long)h * g.dv, ev, c.Tc, g.dv,
                             Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv, g.dv);
 }
@@ -3309,7 +3322,7 @@ void launch_scores(const Geom & g, const ChunkDesc * chunks, int n_chunk_units, 
 
 void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st) {
     hipLaunchKernelGGL(k_softmax_importance, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
-                       g, w.chunks, w.S, w.smax, w.A, w.E, w.E ? w.rowsum : nullptr, w.imp);
+                       g, w.chunks, w.S, w.smax, w.A, w.E ? w.rowsum : nullptr, w.ainv, w.imp);
 }
 
 void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStream_t st) {
@@ -3319,10 +3332,10 @@ void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStr
                       (((long long)g.H * g.dv) & 3) == 0;
     if (v128)
         hipLaunchKernelGGL(k_refit_target, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
-                           g, w.chunks, w.A, V, w.Y);
+                           g, w.chunks, w.A, w.ainv, V, w.Y);
     else
         hipLaunchKernelGGL(k_refit_target_any, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
-                           g, w.chunks, w.A, V, w.Y);
+                           g, w.chunks, w.A, w.ainv, V, w.Y);
 }
 
 void launch_global_importance(const Geom & g, const Work & w, hipStream_t st) {
