@@ -94,8 +94,10 @@ constexpr int DIV_MAX_CAND = 1280;   // 20 candidates per lane in the greedy wav
 // Statistics scratch (api.cpp:239-325 sampling: h < min(H,4), qi < min(nq,32))
 struct StatWork {
     int mh, mq, qmode;
-    float * OS;   // [L][mh][mq][T]        original scores -> softmax
-    float * CS;   // [L][mh][mq][t_total]  compacted scores -> softmax
+    float * OS;   // [L][mh][mq][T]        original scores -> unnormalised softmax
+    float * CS;   // [L][mh][mq][t_total]  compacted scores -> unnormalised softmax
+    float * OI;   // [L][mh][mq]           1 / (row sum + 1e-12f) of the original rows
+    float * CI;   // [L][mh][mq]           the same for the compacted rows
     float * OO;   // [L][mh][mq][dv]
     float * CO;   // [L][mh][mq][dv]
 };

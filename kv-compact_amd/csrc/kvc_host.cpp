@@ -360,6 +360,8 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     // the original scores reuse S when the statistics share the main query set
     s.OS = (p && pl.qmode == pl.stats_qmode) ? nullptr : cv.take<float>(L * s.mh * s.mq * T);
     s.CS = cv.take<float>(L * s.mh * s.mq * std::max<size_t>(tt, 1));
+    s.OI = cv.take<float>(L * s.mh * s.mq);
+    s.CI = cv.take<float>(L * s.mh * s.mq);
     s.OO = cv.take<float>(L * s.mh * s.mq * dv);
     s.CO = cv.take<float>(L * s.mh * s.mq * dv);
     if (w) *w = ww;

@@ -771,7 +771,8 @@ constexpr int SV_QB = 16, SV_VB = 64, SV_KT = 64, SV_THREADS = 256;
 // factorizations
 constexpr int SV_LDS = (2 * SV_QB * (SV_KT + 1) + 2 * SV_KT * SV_VB) * 4;
 __global__ void __launch_bounds__(SV_THREADS) __attribute__((amdgpu_waves_per_eu(5, 8)))
-k_stats_values(Geom g, const float * __restrict__ a_all, long long a_ls, long long a_hs, long long a_rs, int n,
+k_stats_values(Geom g, const float * __restrict__ a_all, const float * __restrict__ ascale, long long a_ls,
+               long long a_hs, long long a_rs, int n,
                const float * __restrict__ V, const float * __restrict__ Cv, int mode, float * __restrict__ out_all,
                int mh, int mq) {
     const int nqb = (mq + SV_QB - 1) / SV_QB, nvb = (g.dv + SV_VB - 1) / SV_VB;
@@ -798,6 +799,15 @@ k_stats_values(Geom g, const float * __restrict__ a_all, long long a_ls, long lo
     const bool vvec = (g.dv & 3) == 0 && (vrs & 3) == 0 && (reinterpret_cast<uintptr_t>(val) & 15) == 0;
     float ra[4];
     float4 rv[4];
+    // row scales (the weights are a * ascale[row] when ascale is given),
+    // applied at the LDS store: a product at the load would make each load
+    // wait for its data before the next is issued
+    float sc[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int q = q0 + ((tid + SV_THREADS * u) >> 6);
+        sc[u] = ascale ? ascale[((long long)layer * mh + h) * mq + min(q, mq - 1)] : 1.0f;
+    }
     auto load = [&](int j0) {
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -828,7 +838,7 @@ k_stats_values(Geom g, const float * __restrict__ a_all, long long a_ls, long lo
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int e = tid + SV_THREADS * u;
-            As[b][e >> 6][e & 63] = ra[u];
+            As[b][e >> 6][e & 63] = ra[u] * sc[u];
         }
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -2949,16 +2959,31 @@ k_ge_general(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__
 // block owns RSM_ROWS rows and sweeps them together, one column per thread,
 // so that every row's load of a column is in flight at once:
 //  1. maxima: the largest non-NaN value of each row (NaN when row[0] is NaN;
-//     the reference's scan keeps row[0] otherwise unless a value exceeds it);
+//     the reference's scan keeps row[0] otherwise unless a value exceeds it),
+//     from the scoring tiles' maxima when the rows are the main scores (ms.tm),
+//     else over the row;
 //  2. RSM_TILE-column tiles, double-buffered in LDS: threads 64.. compute
 //     expf(x - max) (written back in place) while lane r of wave 0 adds row
 //     r's previous tile in column order, the reference's sequential sum;
-//  3. x *= 1 / (sum + 1e-12f).
+//  3. inv = 1 / (sum + 1e-12f): to inv_out[layer][r] when given (the rows stay
+//     unnormalised and their reader forms x * inv, the same product), else
+//     x *= inv in place.
 // grid (ceil(mh * mq / RSM_ROWS), L), RSM_THREADS threads.
 constexpr int RSM_ROWS = 16, RSM_TILE = 256, RSM_THREADS = 64 + RSM_TILE;
 
+// tile maxima of the main scores (k_scores' tmax), for rows that are rows of S:
+// row (h, q) of a layer at tm + layer * ls + h * hs + q * rs, chunk c's tiles
+// from c * nt on, ceil(chunks[c].Tc / SC_KEYS) of them
+struct RowMaxSrc {
+    const unsigned * tm;
+    const ChunkDesc * chunks;
+    int nc, nt;
+    long long ls, hs, rs;
+};
+
 __global__ void __launch_bounds__(RSM_THREADS)
-k_row_softmax(float * __restrict__ x, int n, long long ls, long long hs, long long rs, int mh, int mq) {
+k_row_softmax(float * __restrict__ x, int n, long long ls, long long hs, long long rs, int mh, int mq,
+              RowMaxSrc ms, float * __restrict__ inv_out) {
     const int layer = blockIdx.y, r0 = blockIdx.x * RSM_ROWS;
     const int nrows = min(RSM_ROWS, mh * mq - r0);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -2974,7 +2999,21 @@ k_row_softmax(float * __restrict__ x, int n, long long ls, long long hs, long lo
         rowp[r] = x + layer * ls + (long long)(rr / mq) * hs + (long long)(rr % mq) * rs;
     }
     // 1. maxima
-    {
+    if (ms.tm) {
+        if (tid < nrows) {
+            const int rr = r0 + tid;
+            const unsigned * p = ms.tm + layer * ms.ls + (long long)(rr / mq) * ms.hs + (long long)(rr % mq) * ms.rs;
+            unsigned k = 0;
+            for (int c = 0; c < ms.nc; c++) {
+                const int ntc = (ms.chunks[c].Tc + SC_KEYS - 1) / SC_KEYS;
+                for (int t = 0; t < ntc; t++) k = max(k, p[(long long)c * ms.nt + t]);
+            }
+            const float mm = __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+            const float a0 = rowp[tid][0];
+            mx[tid] = (a0 != a0) ? a0 : ((mm > a0) ? mm : a0);
+        }
+        __syncthreads();
+    } else {
         float m[RSM_ROWS];
 #pragma unroll
         for (int r = 0; r < RSM_ROWS; r++) m[r] = -INFINITY;
@@ -3040,7 +3079,12 @@ k_row_softmax(float * __restrict__ x, int n, long long ls, long long hs, long lo
         }
         __syncthreads();
     }
-    if (w == 0 && lane < nrows) inv[lane] = 1.0f / (sum + 1e-12f);
+    if (w == 0 && lane < nrows) {
+        const float iv = 1.0f / (sum + 1e-12f);
+        inv[lane] = iv;
+        if (inv_out) inv_out[(long long)layer * mh * mq + r0 + lane] = iv;
+    }
+    if (inv_out) return;
     __syncthreads();
     // 3. normalisation
     float iv[RSM_ROWS];
@@ -3437,18 +3481,28 @@ void launch_stats_original(const Geom & g, const Work & w, const StatWork & sw, 
     // the statistics use the main query set, else they are computed here
     float * os = sw.OS;
     long long o_ls = osl, o_hs = (long long)sw.mq * g.T;
+    RowMaxSrc ms{};
     if (S_main) {
         os = S_main;
         o_ls = (long long)g.H * g.nq_max * g.T;
         o_hs = (long long)g.nq_max * g.T;
+        if (w.smax) {
+            ms.tm = w.smax;
+            ms.chunks = w.chunks;
+            ms.nc = g.n_chunks;
+            ms.nt = cdiv(g.Tc_max, SC_KEYS);
+            ms.rs = (long long)ms.nc * ms.nt;
+            ms.hs = (long long)g.nq_max * ms.rs;
+            ms.ls = (long long)g.H * ms.hs;
+        }
     } else {
         launch_scores(g, whole, 1, g.T, K, Q, sw.OS, sw.mh, sw.mq, osl, (long long)sw.mq * g.T, g.T, sw.qmode, st,
                       nullptr, nullptr);
     }
     hipLaunchKernelGGL(k_row_softmax, dim3(rsm_blocks, g.L), dim3(RSM_THREADS), 0, st,
-                       os, g.T, o_ls, o_hs, (long long)g.T, sw.mh, sw.mq);
+                       os, g.T, o_ls, o_hs, (long long)g.T, sw.mh, sw.mq, ms, sw.OI);
     hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), SV_LDS, st,
-                       g, os, o_ls, o_hs, (long long)g.T, g.T, V, nullptr, 1, sw.OO, sw.mh, sw.mq);
+                       g, os, sw.OI, o_ls, o_hs, (long long)g.T, g.T, V, nullptr, 1, sw.OO, sw.mh, sw.mq);
 }
 
 // Compacted attention over the kept keys with beta and C_v (outputs CO), then
@@ -3463,9 +3517,10 @@ void launch_stats_compacted(const Geom & g, const Work & w, const StatWork & sw,
     launch_scores(g, kept, 1, g.t_total, K, Q, sw.CS, sw.mh, sw.mq, csl, (long long)sw.mq * g.t_total, g.t_total,
                   sw.qmode, st, w.sel, beta);
     hipLaunchKernelGGL(k_row_softmax, dim3(rsm_blocks, g.L), dim3(RSM_THREADS), 0, st,
-                       sw.CS, g.t_total, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, sw.mh, sw.mq);
+                       sw.CS, g.t_total, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, sw.mh, sw.mq,
+                       RowMaxSrc{}, sw.CI);
     hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), SV_LDS, st,
-                       g, sw.CS, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, g.t_total, V, Cv, 2,
+                       g, sw.CS, sw.CI, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, g.t_total, V, Cv, 2,
                        sw.CO, sw.mh, sw.mq);
 }
 
