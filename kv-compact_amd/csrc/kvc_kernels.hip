@@ -1150,7 +1150,10 @@ k_div_candidates(Geom g, const ChunkDesc * __restrict__ chunks, const float * __
 
 // Gram matrix of one unit's candidates over the full key row (length H*d_k),
 // each entry a sequential dot product. Tiles of 64 x 64 above the diagonal
-// (mirrored on write); 256 threads, each 4 x 4 entries. grid (units, tile pairs).
+// (mirrored on write); 256 threads, each 4 x 4 entries. A diagonal tile needs
+// only its 136 sub-tiles on or above the diagonal: there threads 0..135 take
+// them in order and the others only help stage the slabs (a wave with no
+// sub-tile skips the sums). grid (units, tile pairs).
 constexpr int DG_TILE = 64, DG_SLAB = 32;
 
 __global__ void __launch_bounds__(256)
@@ -1173,7 +1176,18 @@ k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     const float * Kl = K + (long long)layer * g.ldK + (long long)c.start * E;
     __shared__ __align__(16) float As[DG_SLAB][DG_TILE + 4];
     __shared__ __align__(16) float Bs[DG_SLAB][DG_TILE + 4];
-    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int tid = threadIdx.x;
+    int tx = tid & 15, ty = tid >> 4;
+    bool work = true;
+    if (ti == tj) {
+        // sub-tile k = tid of the upper triangle, row by row: row y holds 16 - y
+        int k = tid, y = 0;
+        while (y < 16 && k >= 16 - y) { k -= 16 - y; y++; }
+        work = y < 16;
+        ty = work ? y : 0;
+        tx = work ? y + k : 0;
+    }
+    const bool wave_work = __builtin_amdgcn_readfirstlane(__ballot(work) != 0ull) != 0;
     // loader: row lr of the tile, dims lq*8 .. lq*8+7 of the slab
     const int lr = tid >> 2, lq = tid & 3;
     const int ra = ti * DG_TILE + lr, rb = tj * DG_TILE + lr;
@@ -1207,7 +1221,7 @@ k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             Bs[lq * 8 + u][lr] = vb[u];
         }
         __syncthreads();
-        const int dn = min(DG_SLAB, E - d0);
+        const int dn = wave_work ? min(DG_SLAB, E - d0) : 0;
         for (int dd = 0; dd < dn; dd++) {
             const float4 a = *reinterpret_cast<const float4 *>(&As[dd][ty * 4]);
             const float4 b = *reinterpret_cast<const float4 *>(&Bs[dd][tx * 4]);
@@ -1225,7 +1239,7 @@ k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int q = tj * DG_TILE + tx * 4 + j;
-            if (r < C && q < C) {
+            if (work && r < C && q < C) {
                 G[(long long)r * dw.cap + q] = acc[i][j];
                 G[(long long)q * dw.cap + r] = acc[i][j];
             }
