@@ -1176,6 +1176,11 @@ k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     const float * Kl = K + (long long)layer * g.ldK + (long long)c.start * E;
     __shared__ __align__(16) float As[DG_SLAB][DG_TILE + 4];
     __shared__ __align__(16) float Bs[DG_SLAB][DG_TILE + 4];
+    // rows from tile ta, columns from tile tb: the partial last tile, if in
+    // the pair, gives the rows, so that a wave whose rows are all past C
+    // skips the sums (the entries go out both ways, so the orientation is free)
+    const bool swp = ti < tj && (tj + 1) * DG_TILE > C;
+    const int ta = swp ? tj : ti, tb = swp ? ti : tj;
     const int tid = threadIdx.x;
     int tx = tid & 15, ty = tid >> 4;
     bool work = true;
@@ -1187,10 +1192,11 @@ k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         ty = work ? y : 0;
         tx = work ? y + k : 0;
     }
+    work = work && ta * DG_TILE + 4 * ty < C;
     const bool wave_work = __builtin_amdgcn_readfirstlane(__ballot(work) != 0ull) != 0;
     // loader: row lr of the tile, dims lq*8 .. lq*8+7 of the slab
     const int lr = tid >> 2, lq = tid & 3;
-    const int ra = ti * DG_TILE + lr, rb = tj * DG_TILE + lr;
+    const int ra = ta * DG_TILE + lr, rb = tb * DG_TILE + lr;
     const float * pa = Kl + (long long)cand[ra < C ? ra : C - 1] * E + lq * 8;
     const float * pb = Kl + (long long)cand[rb < C ? rb : C - 1] * E + lq * 8;
     const bool vec = (E & 3) == 0 && (reinterpret_cast<uintptr_t>(Kl) & 15) == 0;
@@ -1235,10 +1241,10 @@ k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     float * G = dw.G + (long long)slot * dw.cap * dw.cap;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const int r = ti * DG_TILE + ty * 4 + i;
+        const int r = ta * DG_TILE + ty * 4 + i;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            const int q = tj * DG_TILE + tx * 4 + j;
+            const int q = tb * DG_TILE + tx * 4 + j;
             if (work && r < C && q < C) {
                 G[(long long)r * dw.cap + q] = acc[i][j];
                 G[(long long)q * dw.cap + r] = acc[i][j];
