@@ -519,8 +519,8 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
             launch_nnls_lh(gb, wb, io.beta, p.nnls_max_iter, w.status, st);
         } else {
             gb.ridge = 1e-10f;   // clamped unconstrained LS, math.h:707-745
-            launch_ls_build(gb, wb, st);
-            launch_ge_lu(gb, wb, st);
+            launch_ls_build(gb, wb, st, true);
+            launch_ge_lu(gb, wb, st, true);
             launch_ge_solve(gb, wb, io.beta, st);
         }
         launch_beta_log(io.beta, (long long)io.L * io.H * pl.t_total, st);
@@ -546,9 +546,9 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     }
     // 7. normal equations and their solution
     if (refit_fork && hipStreamWaitEvent(st, ctx->refit_join, 0) != hipSuccess) return KV_COMPACT_E_DEVICE;
-    launch_ls_build(g, w, st);
+    launch_ls_build(g, w, st, true);
     (void)hipEventRecord(ev[ST_LS_BUILD + 1], st);
-    launch_ge_lu(g, w, st);
+    launch_ge_lu(g, w, st, true);
     (void)hipEventRecord(ev[ST_LU + 1], st);
     launch_ge_solve(g, w, io.Cv, st);
     (void)hipEventRecord(ev[ST_SOLVE + 1], st);
@@ -562,8 +562,8 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
             rc = fit_beta();
             if (rc) return rc;
             launch_ls_softmax(g, w, io.beta, st);
-            launch_ls_build(g, w, st);
-            launch_ge_lu(g, w, st);
+            launch_ls_build(g, w, st, true);
+            launch_ge_lu(g, w, st, true);
             launch_ge_solve(g, w, io.Cv, st);
         }
     }

@@ -21,8 +21,11 @@ void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipSt
 void launch_gather_exp(const Geom & g, const Work & w, hipStream_t st);
 void launch_nnls_lh(const Geom & g, const Work & w, float * wout, int max_iter, int * status, hipStream_t st);
 void launch_beta_log(float * wb, long long n, hipStream_t st);
-void launch_ls_build(const Geom & g, const Work & w, hipStream_t st);
-void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st);
+// m_by_lu: k_ls_build leaves M = X^T X out where k_ge_lu can form it from X
+// (the register LU's systems with nq * n <= 8192); launch_ge_lu must then
+// be given the same flag
+void launch_ls_build(const Geom & g, const Work & w, hipStream_t st, bool m_by_lu = false);
+void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st, bool m_by_lu = false);
 void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st);
 // S_main: the main path's scores [L][H][nq_max][T], used (and overwritten by
 // the sampled rows' softmax) when the statistics share its query set; else null

@@ -1786,6 +1786,10 @@ k_nnls_lh(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restric
 // of B across 64 columns at a time; column-major (B transposed) for larger
 // ones, whose general elimination swaps rows in place. For p == 1 both are
 // the same.
+// The register LU forms M = X^T X from X itself when X (nq x n) fits the LDS
+// of its step ring: then k_ls_build writes B only.
+__device__ __forceinline__ bool lu_x_fits(int n, int nq) { return n <= 256 && nq >= 1 && nq * n <= 8192; }
+
 __device__ __forceinline__ long long rhs_at(int n, int p, int i, int v) {
     return (long long)n * n + (n <= 256 ? (long long)i * p + v : (long long)v * n + i);
 }
@@ -1802,10 +1806,12 @@ constexpr int LB_LDS_FLOATS = 40960;   // 160 KB
 __global__ void __launch_bounds__(256)
 k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ X,
            const float * __restrict__ Y, float * __restrict__ aug, const long long * __restrict__ aug_off,
-           int lds_floats) {
+           int lds_floats, int m_by_lu) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const int n = c.tc, p = g.dv, w = n + p, nq = c.nq;
+    // M is left to k_ge_lu, which forms it from X itself (lu_x_fits)
+    const bool skip_m = m_by_lu && lu_x_fits(n, nq);
     float * Ag = aug + aug_off[((long long)layer * g.n_chunks + c_idx) * g.H + h];
     const long long hsX = (long long)g.nq_max * g.t_total;
     const float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
@@ -1815,7 +1821,7 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     if ((long long)nq * wp > lds_floats) {
         // column-major: entry (row i, column j) at Ag[j * n + i]
         const long long total = (long long)n * w;
-        for (long long e = threadIdx.x; e < total; e += blockDim.x) {
+        for (long long e = skip_m ? (long long)n * n + threadIdx.x : threadIdx.x; e < total; e += blockDim.x) {
             const int j = (int)(e / n), i = (int)(e % n);
             float s = 0.0f;
             if (j < n) {
@@ -1886,6 +1892,7 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         if (vec && i0 + 3 < n && j0 + 3 < w && (j0 + 3 < n || j0 >= n)) {
             // whole tile inside M or inside B: 16-byte stores
             if (j0 < n) {
+                if (skip_m) return;
                 if (ib == jb) {
 #pragma unroll
                     for (int a = 0; a < 4; a++) acc[a][a] = acc[a][a] + g.ridge;
@@ -1915,7 +1922,7 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 const int j = j0 + b;
-                if (j >= w) continue;
+                if (j >= w || (skip_m && j < n)) continue;
                 float v = acc[a][b];
                 if (i == j) v += g.ridge;
                 Ag[j < n ? (long long)j * n + i : rhs_at(n, p, i, j - n)] = v;
@@ -1926,10 +1933,15 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     // tiles holding columns of M (upper triangle only): consecutive threads
     // take consecutive row blocks (column-major stores)
     const int nbm = nbi;   // column blocks that hold at least one column of M
-    for (int e = threadIdx.x; e < nbi * nbm; e += blockDim.x) {
-        const int jb = e / nbi, ib = e % nbi;
-        if (ib > jb) continue;
-        tile(ib, jb);
+    if (!skip_m) {
+        for (int e = threadIdx.x; e < nbi * nbm; e += blockDim.x) {
+            const int jb = e / nbi, ib = e % nbi;
+            if (ib > jb) continue;
+            tile(ib, jb);
+        }
+    } else if (n & 3) {
+        // the last M column block also holds the first columns of B
+        for (int ib = threadIdx.x; ib < nbi; ib += blockDim.x) tile(ib, nbm - 1);
     }
     // tiles of B alone: consecutive threads take consecutive column blocks
     // (row-major stores when n <= 256)
@@ -1984,11 +1996,13 @@ constexpr int RG_THREADS = RG_WAVES * 64;
 constexpr int LU_RING = 32;          // > 17 outstanding steps
 constexpr int LU_TROWS = 32;         // rows per pass of the transposed output write
 constexpr int LU_SPIN_LIMIT = 1 << 22;   // polls per wave over the whole factorization
+constexpr int LU_X_FLOATS = LU_RING * 64 * 4;   // X staged in the ring's LDS: nq * n <= 8192
 
 struct LuShared {
     union {
         float4 fm[LU_RING][64];      // step c's multipliers in slot c % LU_RING: lane l's four rows
         float tile[LU_TROWS][RG_ROWS + 1];   // output staging at the end
+        float xs[LU_X_FLOATS];       // X (nq x n) while the matrix is formed, when M comes from X
     } u;
     int plog[RG_ROWS];               // step c's pivot row (+256: skipped); -1 until published
     union {
@@ -2270,8 +2284,9 @@ __device__ __forceinline__ void lu_steps(LuShared & sh, float (&a)[RG_SLOTS][RG_
 template <bool MASKED>
 __global__ void __launch_bounds__(RG_THREADS)
 k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
-        const long long * __restrict__ aug_off, int * __restrict__ perm_out, unsigned char * __restrict__ skip_out,
-        float * __restrict__ LU_all, int * __restrict__ redo, int * __restrict__ status) {
+        const long long * __restrict__ aug_off, const float * __restrict__ X, int * __restrict__ perm_out,
+        unsigned char * __restrict__ skip_out, float * __restrict__ LU_all, int * __restrict__ redo,
+        int * __restrict__ status) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const int n = c.tc;
@@ -2292,15 +2307,61 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
     float a[RG_SLOTS][RG_COLS];
     bool live[RG_SLOTS];
     bool unsafe = false;
+    if (X && lu_x_fits(n, c.nq)) {
+        // M = X^T X (+ ridge on the diagonal) formed here, k_ls_build having
+        // left it out: each entry the same sequential sum over the rows of X
+        // (k ascending from +0), the ridge added after it, X staged in LDS
+        const int nq = c.nq;
+        const long long hsX = (long long)g.nq_max * g.t_total;
+        const float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
+        for (int e = tid; e < nq * n; e += RG_THREADS) {
+            const int k = e / n, i = e - k * n;
+            sh.u.xs[e] = Xh[(long long)k * g.t_total + i];
+        }
+        __syncthreads();
+        int cc[RG_COLS];
 #pragma unroll
-    for (int s = 0; s < RG_SLOTS; s++) {
-        const int r = lane + 64 * s;
-        live[s] = r < n;
-        const int rc = min(r, n - 1);
+        for (int q = 0; q < RG_COLS; q++) cc[q] = min(w + RG_WAVES * q, n - 1);
 #pragma unroll
-        for (int q = 0; q < RG_COLS; q++) {
-            a[s][q] = A[(unsigned)(min(w + RG_WAVES * q, n - 1) * n + rc)];
-            if (!MASKED) unsafe = unsafe || lu_unsafe(a[s][q]);
+        for (int s = 0; s < RG_SLOTS; s++) {
+            const int r = lane + 64 * s;
+            live[s] = r < n;
+#pragma unroll
+            for (int q = 0; q < RG_COLS; q++) a[s][q] = 0.0f;
+        }
+        for (int k = 0; k < nq; k++) {
+            const float * xk = sh.u.xs + k * n;
+            float xr[RG_SLOTS], xc[RG_COLS];
+#pragma unroll
+            for (int s = 0; s < RG_SLOTS; s++) xr[s] = xk[min(lane + 64 * s, n - 1)];
+#pragma unroll
+            for (int q = 0; q < RG_COLS; q++) xc[q] = xk[cc[q]];
+#pragma unroll
+            for (int s = 0; s < RG_SLOTS; s++)
+#pragma unroll
+                for (int q = 0; q < RG_COLS; q++) a[s][q] = a[s][q] + xr[s] * xc[q];
+        }
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            const int rc = min(lane + 64 * s, n - 1);
+#pragma unroll
+            for (int q = 0; q < RG_COLS; q++) {
+                if (rc == cc[q]) a[s][q] = a[s][q] + g.ridge;
+                if (!MASKED) unsafe = unsafe || lu_unsafe(a[s][q]);
+            }
+        }
+        __syncthreads();   // X is dead: the LDS becomes the step ring
+    } else {
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            const int r = lane + 64 * s;
+            live[s] = r < n;
+            const int rc = min(r, n - 1);
+#pragma unroll
+            for (int q = 0; q < RG_COLS; q++) {
+                a[s][q] = A[(unsigned)(min(w + RG_WAVES * q, n - 1) * n + rc)];
+                if (!MASKED) unsafe = unsafe || lu_unsafe(a[s][q]);
+            }
         }
     }
     if (tid < RG_ROWS) {
@@ -3456,7 +3517,7 @@ void launch_beta_log(float * wb, long long n, hipStream_t st) {
     hipLaunchKernelGGL(k_beta_log, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, wb, n);
 }
 
-void launch_ls_build(const Geom & g, const Work & w, hipStream_t st) {
+void launch_ls_build(const Geom & g, const Work & w, hipStream_t st, bool m_by_lu) {
     // dynamic LDS beyond 64 KB needs the kernel attribute (once per process)
     static int lds_cap = -1;
     if (lds_cap < 0)
@@ -3467,15 +3528,16 @@ void launch_ls_build(const Geom & g, const Work & w, hipStream_t st) {
     const long long need = (long long)g.nq_max * ((g.tc_max + g.dv + 3) & ~3);
     const int lds_floats = need <= lds_cap ? (int)need : 0;
     hipLaunchKernelGGL(k_ls_build, dim3(g.n_chunks * g.H, g.L), dim3(256), (size_t)lds_floats * sizeof(float), st,
-                       g, w.chunks, w.X, w.Y, w.aug, w.aug_off, lds_floats);
+                       g, w.chunks, w.X, w.Y, w.aug, w.aug_off, lds_floats, m_by_lu ? 1 : 0);
 }
 
-void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st) {
+void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st, bool m_by_lu) {
     // unmasked pass over every system, then the masked pass over the flagged ones
+    const float * X = m_by_lu ? w.X : nullptr;
     hipLaunchKernelGGL(k_ge_lu<false>, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
-                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, w.lu_redo, w.status);
+                       g, w.chunks, w.aug, w.aug_off, X, w.perm, w.skip, w.LU, w.lu_redo, w.status);
     hipLaunchKernelGGL(k_ge_lu<true>, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
-                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, w.lu_redo, w.status);
+                       g, w.chunks, w.aug, w.aug_off, X, w.perm, w.skip, w.LU, w.lu_redo, w.status);
 }
 
 void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st) {
