@@ -92,8 +92,11 @@ def stage_model(L, T, H, d, nq, t, n_chunks, tc):
         "beta_fit": dict(bytes=0, flops=0),
         "refinement": dict(bytes=0, flops=0),
         "compacted_softmax": dict(bytes=4 * L * H * nq * t * 2, flops=0),
-        "normal_equations": dict(bytes=4 * units * n * (n + p), flops=2 * nq * units * n * (n + p)),
-        "lu_factorization": dict(bytes=4 * units * 2 * n * n, flops=units * lu),
+        # the normal equations write B = X^T Y only; the register LU forms
+        # M = X^T X (one triangle's worth of sums) from X, then factors it
+        "normal_equations": dict(bytes=4 * units * (nq * (n + p) + n * p), flops=2 * nq * units * n * p),
+        "lu_factorization": dict(bytes=4 * units * (nq * n + n * n),
+                                 flops=units * (lu + nq * n * (n + 1))),
         "substitution": dict(bytes=4 * units * (n * n + 3 * n * p), flops=units * subst),
         "quality_stats": dict(bytes=4 * L * min(H, 4) * T * 2 * d, flops=2 * L * min(H, 4) * min(nq, 32) * T * 2 * d),
     }
