@@ -15,6 +15,9 @@
 #include "kvc_kernels.h"
 
 #include <math.h>
+#include <stdlib.h>
+
+#include <utility>
 
 namespace kvc {
 
@@ -2409,7 +2412,8 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
     }
     // every entry is final in registers: multipliers left of each row's pivot
     // step, U from it on; rows go out through LDS, LU_TROWS at a time, as
-    // contiguous row segments
+    // contiguous row segments of 256 entries, zero past column n (the
+    // substitution reads whole blocks of a row without guards)
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) {
 #pragma unroll
@@ -2424,7 +2428,7 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
             __syncthreads();
             for (int e = tid; e < LU_TROWS * RG_ROWS; e += RG_THREADS) {
                 const int rr = e / RG_ROWS, j = e % RG_ROWS;
-                if (r0 + rr < n && j < n) LU[(unsigned)((r0 + rr) * RG_ROWS + j)] = sh.u.tile[rr][j];
+                if (r0 + rr < n) LU[(unsigned)((r0 + rr) * RG_ROWS + j)] = j < n ? sh.u.tile[rr][j] : 0.0f;
             }
             __syncthreads();
         }
@@ -2647,7 +2651,7 @@ __global__ void __launch_bounds__(64)
 k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
            const long long * __restrict__ aug_off, const int * __restrict__ perm_in,
            const unsigned char * __restrict__ skip_in, const float * __restrict__ LU_all,
-           float * __restrict__ Yt_all, float * __restrict__ Cv) {
+           float * __restrict__ Yt_all, float * __restrict__ Cv, int only_skip) {
     const int sysl = blockIdx.x;   // (layer, chunk, head)
     const int h = sysl % g.H, c_idx = (sysl / g.H) % g.n_chunks, layer = sysl / (g.H * g.n_chunks);
     const ChunkDesc c = chunks[c_idx];
@@ -2684,6 +2688,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     }
     __builtin_amdgcn_wave_barrier();
     const bool sk = any_skip != 0;
+    if (only_skip && !sk) return;         // k_ge_subst solved this system
     const float * frow = rowb + BS_PAD;   // forward rows, unshifted
     float4 * frow4 = reinterpret_cast<float4 *>(rowb + BS_PAD);
 
@@ -2936,6 +2941,397 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 #pragma unroll
             for (int i = 0; i < BS_HIGH; i++) x[(unsigned)((hb + i) * g.dv + v)] = xh[i];
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Forward and back substitution of the register-LU systems (n <= 256). The
+// forward pass is the reference's elimination of the right-hand-side columns
+// (math.h:531-537): the row that ends at logical position i receives the
+// updates of steps 0 .. i-1 in step order, y_i = b - f_0 y_0 - f_1 y_1 - ...,
+// and a skipped step updates no row. The backward pass is math.h:540-556:
+// x_i = (y_i - U[i][i+1] x_{i+1} - U[i][i+2] x_{i+2} - ...) / U[i][i], the
+// solution value of a skipped pivot (|U[i][i]| < 1e-12) being zero_val.
+//
+// One wave per 64 right-hand-side columns (lane = column), the waves of a
+// system in one block, two waves per SIMD. A column's 256 values sit in 32
+// groups of eight rows: 24 groups in registers, 8 in LDS. Registers are only
+// indexed statically, so they form a stack: a new group enters at block 0 and
+// the others move down one block. Each pass reads the stack in a fixed order
+// with a uniform guard per block:
+//  - forward: block m holds group cnt-1-m (cnt = groups in registers), read
+//    oldest first; groups 24-31 go to LDS (the earliest rows, read by every
+//    later row, stay in registers);
+//  - backward: block m holds the solution of group gb+1+m, read newest first,
+//    and the bottom blocks hold the y groups still to be consumed, the next
+//    one in block 23; once 24 solved groups fill the stack the oldest moves
+//    to the LDS slot of the y group just consumed.
+// Between the passes the blocks are permuted statically into the backward's
+// order. Rows of L and U are the same for every lane of a wave and come
+// through scalar loads. The forward pass sums four rows side by side
+// (independent chains); the backward pass is one chain per column (each row's
+// sum starts with the row solved just before it). Rows past n are processed
+// as zero rows: their values stay zero and the factor array holds zeros in
+// their columns, so their terms (0 * 0 subtracted from a sum that is never -0)
+// change nothing and the sums need no guards.
+// ---------------------------------------------------------------------------
+constexpr int SB_G = 8;                     // rows per group (and entries per block)
+constexpr int SB_NG = RG_ROWS / SB_G;       // groups of a column
+constexpr int SB_RG = 24;                   // groups held in registers
+constexpr int SB_LG = SB_NG - SB_RG;        // groups held in LDS
+constexpr int SB_LDS = SB_LG * SB_G;        // stored LDS rows per lane (plus an eight-row window)
+
+// N consecutive entries of a row of the factor array (uniform address: scalar loads)
+template <int N>
+__device__ __forceinline__ void sb_load(float (&u)[N], const float * __restrict__ row, int k0) {
+#pragma unroll
+    for (int j = 0; j < N; j++) u[j] = row[k0 + j];
+}
+
+// Scalar loads return out of order, so a wait covers every load in flight:
+// the next block's loads are issued after the wait for the current block's
+// and before its arithmetic.
+__device__ __forceinline__ void sb_wait_scalar() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0), vmcnt and expcnt unchanged
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// perm[i] for a uniform i, from the lanes' entries (perm[l + 64 s] in slot s)
+__device__ __forceinline__ int sb_perm(const int (&pv)[4], int i) {
+    const int s = i >> 6;
+    const int v = s == 0 ? pv[0] : s == 1 ? pv[1] : s == 2 ? pv[2] : pv[3];
+    return __builtin_amdgcn_readlane(v, i & 63);
+}
+
+// push a group onto the register stack
+__device__ __forceinline__ void sb_push(float (&R)[SB_RG][SB_G], const float (&g)[SB_G]) {
+#pragma unroll
+    for (int m = SB_RG - 1; m > 0; m--)
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) R[m][j] = R[m - 1][j];
+#pragma unroll
+    for (int j = 0; j < SB_G; j++) R[0][j] = g[j];
+}
+
+// val[t] -= l[t][j] * y[j] for the four rows t, j ascending
+__device__ __forceinline__ void sb_fterms(float (&val)[4], const float (&l)[4][4], const float * y) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        float pr[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) pr[t] = l[t][j] * y[j];
+#pragma unroll
+        for (int t = 0; t < 4; t++) val[t] = val[t] - pr[t];
+    }
+}
+
+// Forward pass for four rows r0 .. r0+3 of group gi (r0 = 8 gi, or 8 gi + 4
+// for the second half): the steps of every earlier group, then (second half)
+// the first half's four steps, then the half's own steps. ya: the first
+// half's results.
+template <bool SECOND>
+__device__ __forceinline__ void sb_fhalf(float (&val)[4], const float (&R)[SB_RG][SB_G], float (*zl)[64],
+                                         const float * const (&lr)[4], const float (&ya)[4], int gi, int lane) {
+    int cnt = min(gi, SB_RG);
+    // (opaque to the compiler, so that each half tests its own copy rather
+    // than keeping the other half's test results alive)
+    asm volatile("" : "+s"(cnt));
+    // register groups, oldest first: block m holds group cnt - 1 - m
+    float lc[4][4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) sb_load(lc[t], lr[t], 0);
+#pragma unroll
+    for (int m = SB_RG - 1; m >= 0; m--) {
+        if (m >= cnt) continue;
+        const int k0 = SB_G * (cnt - 1 - m);
+        // steps k0 .. k0 + 3 (lc), then k0 + 4 .. k0 + 7
+        sb_wait_scalar();
+        float ln[4][4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) sb_load(ln[t], lr[t], k0 + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        sb_fterms(val, lc, &R[m][0]);
+        sb_wait_scalar();
+#pragma unroll
+        for (int t = 0; t < 4; t++) sb_load(lc[t], lr[t], k0 + 8);   // the next group's steps
+        __builtin_amdgcn_sched_barrier(0);
+        sb_fterms(val, ln, &R[m][4]);
+    }
+    // LDS groups 24 .. gi - 1 (lc holds steps 192 .. 195 when there are any)
+    for (int G = SB_RG; G < gi; G++) {
+        const int k0 = SB_G * G;
+        float y[SB_G];
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) y[j] = zl[SB_G * (G - SB_RG) + j][lane];
+        sb_wait_scalar();
+        float ln[4][4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) sb_load(ln[t], lr[t], k0 + 4);
+        __builtin_amdgcn_sched_barrier(0);
+        sb_fterms(val, lc, y);
+        sb_wait_scalar();
+#pragma unroll
+        for (int t = 0; t < 4; t++) sb_load(lc[t], lr[t], min(k0 + 8, RG_ROWS - 4));
+        __builtin_amdgcn_sched_barrier(0);
+        sb_fterms(val, ln, y + 4);
+    }
+    // this group's steps: the first half's rows (second half only), then the
+    // half's own rows in order; lc holds the entries of steps 8 gi .. 8 gi + 3
+    sb_wait_scalar();
+    const int g0 = SB_G * gi;
+    if (SECOND) {
+        sb_fterms(val, lc, ya);
+#pragma unroll
+        for (int t = 0; t < 4; t++) sb_load(lc[t], lr[t], g0 + 4);
+        sb_wait_scalar();
+    }
+    const int h0 = SECOND ? g0 + 4 : g0;
+#pragma unroll
+    for (int t = 1; t < 4; t++) {
+#pragma unroll
+        for (int r = 0; r < t; r++) val[t] = val[t] - lc[t][r] * val[r];
+    }
+}
+
+// one group of the forward pass: its eight results in yg (zero past n)
+__device__ __forceinline__ void sb_fgroup(float (&yg)[SB_G], const float (&R)[SB_RG][SB_G], float (*zl)[64],
+                                          const float * __restrict__ LU, const float * __restrict__ B,
+                                          const int (&pv)[4], int gi, int n, int p, int vc, int lane, float & pf) {
+    if (SB_G * gi < n) {
+        // the next group's eight L rows into the caches (lane l: line l & 15
+        // of row l >> 4 of each half; the value only feeds the sink)
+        {
+            const int r = min(SB_G * (gi + 1) + (lane >> 4), n - 1);
+            const int r2 = min(SB_G * (gi + 1) + 4 + (lane >> 4), n - 1);
+            const int pr = __builtin_amdgcn_ds_bpermute(4 * (r & 63), r < 64 ? pv[0] : r < 128 ? pv[1] : r < 192 ? pv[2] : pv[3]);
+            const int pr2 = __builtin_amdgcn_ds_bpermute(4 * (r2 & 63), r2 < 64 ? pv[0] : r2 < 128 ? pv[1] : r2 < 192 ? pv[2] : pv[3]);
+            pf = fmaxf(pf, LU[(unsigned)(pr * RG_ROWS + 16 * (lane & 15))]);
+            pf = fmaxf(pf, LU[(unsigned)(pr2 * RG_ROWS + 16 * (lane & 15))]);
+        }
+        float ya[4], yb[4];
+        const float * lr[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int pr = sb_perm(pv, min(SB_G * gi + t, n - 1));
+            lr[t] = LU + (unsigned)(pr * RG_ROWS);
+            ya[t] = B[(unsigned)(pr * p + vc)];
+        }
+        sb_fhalf<false>(ya, R, zl, lr, ya, gi, lane);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int pr = sb_perm(pv, min(SB_G * gi + 4 + t, n - 1));
+            lr[t] = LU + (unsigned)(pr * RG_ROWS);
+            yb[t] = B[(unsigned)(pr * p + vc)];
+        }
+        sb_fhalf<true>(yb, R, zl, lr, ya, gi, lane);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            yg[t] = SB_G * gi + t < n ? ya[t] : 0.0f;
+            yg[4 + t] = SB_G * gi + 4 + t < n ? yb[t] : 0.0f;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) yg[j] = 0.0f;
+    }
+}
+
+__device__ __forceinline__ void sb_forward(float (&R)[SB_RG][SB_G], float (*zl)[64], const float * __restrict__ LU,
+                                           const float * __restrict__ B, const int (&pv)[4], int n, int p, int vc,
+                                           int lane, float & pf) {
+    // groups 0-23 onto the register stack, groups 24-31 into LDS
+    for (int gi = 0; gi < SB_RG; gi++) {
+        float yg[SB_G];
+        sb_fgroup(yg, R, zl, LU, B, pv, gi, n, p, vc, lane, pf);
+        sb_push(R, yg);
+    }
+    for (int gi = SB_RG; gi < SB_NG; gi++) {
+        float yg[SB_G];
+        sb_fgroup(yg, R, zl, LU, B, pv, gi, n, p, vc, lane, pf);
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) zl[SB_G * (gi - SB_RG) + j][lane] = yg[j];
+    }
+}
+
+// Backward pass. On entry block m holds y group 8 + m and LDS slot s y group
+// s; on exit block m holds x group m and LDS slot s x group 24 + s.
+// lane L of each 16-lane row of v, in every lane (DPP row_newbcast, folded
+// into the instruction that uses it)
+template <int L>
+__device__ __forceinline__ float sb_bc(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xf, 0xf, false));
+}
+
+// backward pass: a U row from its group's first column g0, sixteen entries
+// per register (register i: entries g0 + 16 i + 0..15, each in every 16-lane
+// row), far enough for the register blocks (entries g0 .. g0 + 207)
+constexpr int SB_US = (SB_G * (SB_RG + 2) + 15) / 16;
+
+// products of register block M (entries g0 + 8 (M + 1) + J) with its results
+template <int M, int... J>
+__device__ __forceinline__ void sb_bprod(float (&pr)[SB_G], const float (&us)[SB_US], const float (&R)[SB_RG][SB_G],
+                                         std::integer_sequence<int, J...>) {
+    ((pr[J] = sb_bc<(SB_G * (M + 1) + J) % 16>(us[(SB_G * (M + 1) + J) / 16]) * R[M][J]), ...);
+}
+template <int M>
+__device__ __forceinline__ void sb_bblock(float & val, const float (&us)[SB_US], const float (&R)[SB_RG][SB_G],
+                                          int nxr) {
+    if (M < nxr) {
+        float pr[SB_G];
+        sb_bprod<M>(pr, us, R, std::make_integer_sequence<int, SB_G>{});
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) val = val - pr[j];
+    }
+}
+template <int... M>
+__device__ __forceinline__ void sb_bblocks(float & val, const float (&us)[SB_US], const float (&R)[SB_RG][SB_G],
+                                           int nxr, std::integer_sequence<int, M...>) {
+    (sb_bblock<M>(val, us, R, nxr), ...);
+}
+// the rows above col in its group (entries g0 + J, J > k), ascending
+template <int... J>
+__device__ __forceinline__ void sb_bgroup_terms(float & val, float us0, const float (&xw)[SB_G], int k,
+                                                std::integer_sequence<int, J...>) {
+    ((val = J > k ? val - sb_bc<J>(us0) * xw[J] : val), ...);
+}
+
+// one group of the backward pass: its results xw from its y values yw
+__device__ __forceinline__ void sb_bgroup(float (&xw)[SB_G], const float (&yw)[SB_G], const float (&R)[SB_RG][SB_G],
+                                          float (*zl)[64], const float * __restrict__ LU, const int (&pv)[4],
+                                          int gb, int n, float zero_val, int lane, float & pf) {
+        const int nx = min(SB_NG - 1 - gb, SB_RG);   // solved groups in registers
+        // the group's y values, read by row through the LDS window after the
+        // stored rows
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) zl[SB_LDS + j][lane] = yw[j];
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) xw[j] = 0.0f;
+        const int g0 = SB_G * gb;
+        for (int col = min(g0 + SB_G, n) - 1; col >= g0; col--) {
+            const int k = col - g0;
+            const float * __restrict__ ur = LU + (unsigned)(sb_perm(pv, col) * RG_ROWS);
+            // the next row's sixteen 64-byte lines into the caches while
+            // this row runs (one load; the value only feeds the sink)
+            pf = fmaxf(pf, LU[(unsigned)(sb_perm(pv, max(col - 1, 0)) * RG_ROWS + 16 * (lane & 15))]);
+            float us[SB_US];
+#pragma unroll
+            for (int i = 0; i < SB_US; i++) us[i] = ur[min(g0 + 16 * i + (lane & 15), RG_ROWS - 1)];
+            const float yk = zl[SB_LDS + k][lane];
+            const float piv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(us[0]), k));
+            float val = zero_val;
+            if (!(fabsf(piv) < 1e-12f)) {
+                val = yk;
+                sb_bgroup_terms(val, us[0], xw, k, std::make_integer_sequence<int, SB_G>{});
+                // solved groups in registers, newest (lowest rows) first (nx
+                // opaque: tested per row, not kept from the row before)
+                int nxr = nx;
+                asm volatile("" : "+s"(nxr));
+                sb_bblocks(val, us, R, nxr, std::make_integer_sequence<int, SB_RG>{});
+                // solved groups gb + 25 .. 31 in LDS slots gb + 1 .. 7
+                for (int s = gb + 1; s < SB_LG; s++) {
+                    float uc[SB_G];
+                    sb_load(uc, ur, SB_G * (s + SB_RG));
+                    sb_wait_scalar();
+#pragma unroll
+                    for (int j = 0; j < SB_G; j++) val = val - uc[j] * zl[SB_G * s + j][lane];
+                }
+                val = val / piv;
+            }
+#pragma unroll
+            for (int j = 0; j < SB_G; j++) xw[j] = k == j ? val : xw[j];
+        }
+}
+
+__device__ __forceinline__ void sb_backward(float (&R)[SB_RG][SB_G], float (*zl)[64], const float * __restrict__ LU,
+                                            const int (&pv)[4], int n, float zero_val, int lane, float & pf) {
+    // groups 31-8: y from the bottom block, which the pushed result replaces
+    for (int gb = SB_NG - 1; gb >= SB_LG; gb--) {
+        float yw[SB_G], xw[SB_G];
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) yw[j] = R[SB_RG - 1][j];
+        sb_bgroup(xw, yw, R, zl, LU, pv, gb, n, zero_val, lane, pf);
+        sb_push(R, xw);
+    }
+    // groups 7-0: y from LDS; the oldest solved group moves to its slot
+    for (int gb = SB_LG - 1; gb >= 0; gb--) {
+        float yw[SB_G], xw[SB_G];
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) yw[j] = zl[SB_G * gb + j][lane];
+        sb_bgroup(xw, yw, R, zl, LU, pv, gb, n, zero_val, lane, pf);
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) zl[SB_G * gb + j][lane] = R[SB_RG - 1][j];
+        sb_push(R, xw);
+    }
+}
+
+// grid (systems), block 64 * ceil(p / 64); dynamic LDS SB_LDS + SB_G rows x
+// 64 lanes per wave
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+k_ge_subst(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
+           const long long * __restrict__ aug_off, const int * __restrict__ perm_in,
+           const unsigned char * __restrict__ skip_in, const float * __restrict__ LU_all, float * __restrict__ Cv) {
+    const int sysl = blockIdx.x;   // (layer, chunk, head)
+    const int h = sysl % g.H, c_idx = (sysl / g.H) % g.n_chunks, layer = sysl / (g.H * g.n_chunks);
+    const ChunkDesc c = chunks[c_idx];
+    const int n = c.tc, p = g.dv;
+    if (n > RG_ROWS || n < 1) return;
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int v = wv * 64 + lane;
+    const bool act = v < p;
+    const int vc = act ? v : p - 1;
+    const float * __restrict__ LU = LU_all + (long long)sysl * RG_ROWS * RG_ROWS;
+    const float * __restrict__ B = aug + aug_off[sysl] + (long long)n * n;   // row-major RHS [r][v]
+    float * __restrict__ x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
+    extern __shared__ float sb_lds[];
+    float (*zl)[64] = reinterpret_cast<float (*)[64]>(sb_lds + (size_t)wv * (SB_LDS + SB_G) * 64);
+    // permutation by logical row (lane l holds rows l, l + 64, ...); a system
+    // with a skipped step is left to k_ge_solve
+    int pv[4];
+    bool sk = false;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        const int i = lane + 64 * s;
+        pv[s] = i < n ? perm_in[(long long)sysl * g.tc_max + i] : 0;
+        sk = sk || (i < n && skip_in[(long long)sysl * g.tc_max + i] != 0);
+    }
+    if (__ballot(sk) != 0ull) return;
+    float R[SB_RG][SB_G];
+#pragma unroll
+    for (int m = 0; m < SB_RG; m++)
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) R[m][j] = 0.0f;
+    float pf = 0.0f;   // sink of the cache warm-up loads
+    sb_forward(R, zl, LU, B, pv, n, p, vc, lane, pf);
+    // forward layout: block m = group 23 - m, LDS slot s = group 24 + s;
+    // backward layout: block m = group 8 + m, LDS slot s = group s
+    {
+        float Q[SB_RG][SB_G];
+#pragma unroll
+        for (int m = 0; m < 16; m++)
+#pragma unroll
+            for (int j = 0; j < SB_G; j++) Q[m][j] = R[15 - m][j];
+#pragma unroll
+        for (int m = 16; m < SB_RG; m++)
+#pragma unroll
+            for (int j = 0; j < SB_G; j++) Q[m][j] = zl[SB_G * (m - 16) + j][lane];
+#pragma unroll
+        for (int s = 0; s < SB_LG; s++)
+#pragma unroll
+            for (int j = 0; j < SB_G; j++) zl[SB_G * s + j][lane] = R[SB_RG - 1 - s][j];
+#pragma unroll
+        for (int m = 0; m < SB_RG; m++)
+#pragma unroll
+            for (int j = 0; j < SB_G; j++) R[m][j] = Q[m][j];
+    }
+    sb_backward(R, zl, LU, pv, n, g.zero_val, lane, pf);
+    zl[SB_LDS][lane] = pf;   // (the window row is dead by now)
+    // block m = x group m, LDS slot s = x group 24 + s
+    if (act) {
+#pragma unroll
+        for (int m = 0; m < SB_RG; m++)
+#pragma unroll
+            for (int j = 0; j < SB_G; j++)
+                if (SB_G * m + j < n) x[(unsigned)((SB_G * m + j) * g.dv + v)] = R[m][j];
+        for (int r = SB_G * SB_RG; r < n; r++) x[(unsigned)(r * g.dv + v)] = zl[r - SB_G * SB_RG][lane];
     }
 }
 
@@ -3542,8 +3938,25 @@ void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st, bool m_by_lu) 
 
 void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st) {
     const unsigned systems = (unsigned)(g.L * g.n_chunks * g.H);
+    // k_ge_subst solves every system without a skipped pivot step, k_ge_solve
+    // the others (KVC_SOLVE_OLD=1: k_ge_solve all of them)
+    static const bool old_solve = [] {
+        const char * e = getenv("KVC_SOLVE_OLD");
+        return e && e[0] == '1';
+    }();
+    if (!old_solve) {
+        const unsigned nw = cdiv(g.dv, 64);
+        const size_t lds = (size_t)nw * (SB_LDS + SB_G) * 64 * sizeof(float);
+        static int lds_ok = -1;
+        if (lds_ok < 0)
+            lds_ok = hipFuncSetAttribute(reinterpret_cast<const void *>(k_ge_subst),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         4 * (SB_LDS + SB_G) * 64 * (int)sizeof(float)) == hipSuccess;
+        hipLaunchKernelGGL(k_ge_subst, dim3(systems), dim3(64 * nw), lds, st,
+                           g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, Cv);
+    }
     hipLaunchKernelGGL(k_ge_solve, dim3(systems, cdiv(g.dv, 64)), dim3(64), 0, st,
-                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, w.Bt, Cv);
+                       g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, w.Bt, Cv, old_solve ? 0 : 1);
     if (g.tc_max > RG_ROWS)
         hipLaunchKernelGGL(k_ge_general, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
                            g, w.chunks, w.aug, w.aug_off, Cv, w.gtmp);
