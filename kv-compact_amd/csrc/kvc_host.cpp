@@ -113,10 +113,21 @@ struct Carver {
     }
 };
 
+// Work an earlier call left on the second stream (it ended early, after the
+// refit target or the statistics were launched there) may still read or
+// write the workspace: the call's stream waits for it before any workspace
+// write.
+bool drain_second_stream(DeviceCtx * ctx, hipStream_t st) {
+    if (!ctx->stream2) return true;
+    return hipEventRecord(ctx->refit_join, ctx->stream2) == hipSuccess &&
+           hipStreamWaitEvent(st, ctx->refit_join, 0) == hipSuccess;
+}
+
 bool ensure_arena(DeviceCtx * c, size_t bytes) {
     if (c->arena_cap >= bytes) return true;
     if (c->arena) {
         (void)hipStreamSynchronize(c->stream);
+        (void)hipStreamSynchronize(c->stream2);
         (void)hipFree(c->arena);
         c->arena = nullptr;
         c->arena_cap = 0;
@@ -422,6 +433,10 @@ int run_diversity(hipStream_t st, const Plan & pl, const kv_compact_params & p, 
 int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact_params & p,
               const BatchIO & io, Carver & carver, Timing * tm) {
     if (pl.nq_max > 256) return KV_COMPACT_E_UNSUPPORTED;   // chunk softmax keeps <= 256 row sums on chip
+    // Lawson-Hanson keeps a system's passive set on one wave: refused before
+    // anything is launched
+    if (!p.skip_beta && p.nnls_method == 0 && pl.tc_max > 256) return KV_COMPACT_E_UNSUPPORTED;
+    if (!drain_second_stream(ctx, st)) return KV_COMPACT_E_DEVICE;
     Work w{};
     StatWork sw{};
     DivWork dw{};
@@ -461,10 +476,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     if (hipMemcpyAsync(w.aug_off, aug_off.data(), aug_off.size() * sizeof(long long),
                        hipMemcpyHostToDevice, st) != hipSuccess) return KV_COMPACT_E_DEVICE;
 
-    // second-stream work of an earlier call that ended early may still use the workspace
-    if (ctx->stream2 && (hipEventRecord(ctx->refit_join, ctx->stream2) != hipSuccess ||
-                         hipStreamWaitEvent(st, ctx->refit_join, 0) != hipSuccess)) return KV_COMPACT_E_DEVICE;
-    if (hipMemsetAsync(w.status, 0, sizeof(int), st) != hipSuccess) return KV_COMPACT_E_DEVICE;
+    launch_fill_int(w.status, 0, 1, st);
     hipEvent_t * ev = ctx->ev;
     (void)hipEventRecord(ev[0], st);
     // 1. scores for every (layer, chunk, head)
@@ -503,8 +515,8 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     //    (api.cpp:812-831): M = exp_scores[:, sel], b = row sums
     auto fit_beta = [&]() -> int {
         if (p.skip_beta) {
-            const size_t bytes = (size_t)io.L * io.H * pl.t_total * sizeof(float);
-            return hipMemsetAsync(io.beta, 0, bytes, st) == hipSuccess ? 0 : KV_COMPACT_E_DEVICE;
+            launch_fill_f32(io.beta, 0.0f, (long long)io.L * io.H * pl.t_total, st);
+            return 0;
         }
         launch_gather_exp(g, w, st);   // M into the X buffer
         Geom gb = g;
@@ -513,7 +525,6 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         Work wb = w;
         wb.Y = w.rowsum;
         if (p.nnls_method == 0) {
-            if (pl.tc_max > 256) return KV_COMPACT_E_UNSUPPORTED;
             gb.ridge = 0.0f;   // Lawson-Hanson adds its own 1e-10 to each sub-problem
             launch_ls_build(gb, wb, st);
             launch_nnls_lh(gb, wb, io.beta, p.nnls_max_iter, w.status, st);
@@ -658,6 +669,7 @@ int compact_one(const float * K, const float * V, const float * Q, int T, int n_
     if (!ctx) return KV_COMPACT_E_DEVICE;
     std::lock_guard<std::mutex> lk(ctx->mu);
     hipStream_t st = ctx->stream;
+    if (!drain_second_stream(ctx, st)) return KV_COMPACT_E_DEVICE;
     Plan pl;
     const bool q_given = Q != nullptr;
     make_plan(T, n_q, q_given, p, pl);
@@ -885,6 +897,7 @@ int kv_compact_multi_round(const float * K_all, const float * V_all, const float
         if (!ctx) return KV_COMPACT_E_DEVICE;
         std::lock_guard<std::mutex> lk(ctx->mu);
         hipStream_t st = ctx->stream;
+        if (!drain_second_stream(ctx, st)) return KV_COMPACT_E_DEVICE;
         Plan pl;
         kv_compact_params sp = pc;
         sp.chunk_size = -1;
@@ -976,7 +989,8 @@ int kv_dequantize_row(const uint8_t * src, int type, size_t row_bytes, float * d
     if (!ctx) return KV_COMPACT_E_DEVICE;
     std::lock_guard<std::mutex> lk(ctx->mu);
     const int n_conv = is_block_type(type) ? (n / 32) * 32 : n;
-    if (!ensure_arena(ctx, row_bytes + (size_t)n * 4 + 4096)) return KV_COMPACT_E_DEVICE;
+    if (!drain_second_stream(ctx, ctx->stream) || !ensure_arena(ctx, row_bytes + (size_t)n * 4 + 4096))
+        return KV_COMPACT_E_DEVICE;
     uint8_t * ds = reinterpret_cast<uint8_t *>(ctx->arena);
     float * dd = reinterpret_cast<float *>(ctx->arena + ((row_bytes + 255) & ~(size_t)255));
     hipStream_t st = ctx->stream;
@@ -995,7 +1009,7 @@ size_t kv_quantize_row(const float * src, int type, int n_elements, uint8_t * ds
     DeviceCtx * ctx = device_ctx();
     if (!ctx) return 0;
     std::lock_guard<std::mutex> lk(ctx->mu);
-    if (!ensure_arena(ctx, (size_t)n_elements * 4 + nb + 4096)) return 0;
+    if (!drain_second_stream(ctx, ctx->stream) || !ensure_arena(ctx, (size_t)n_elements * 4 + nb + 4096)) return 0;
     float * ds = reinterpret_cast<float *>(ctx->arena);
     uint8_t * dd = reinterpret_cast<uint8_t *>(ctx->arena + (((size_t)n_elements * 4 + 255) & ~(size_t)255));
     hipStream_t st = ctx->stream;
@@ -1116,7 +1130,7 @@ int kv_compact_hip_mat_mul_ABt_scaled(const float * A, const float * B, float * 
     if (!ctx || m <= 0 || n <= 0 || k <= 0) return -1;
     std::lock_guard<std::mutex> lk(ctx->mu);
     const size_t sa = (size_t)m * k, sb = (size_t)n * k, sc = (size_t)m * n;
-    if (!ensure_arena(ctx, (sa + sb + sc) * 4 + 1024)) return -1;
+    if (!drain_second_stream(ctx, ctx->stream) || !ensure_arena(ctx, (sa + sb + sc) * 4 + 1024)) return -1;
     Carver cv;
     cv.base = ctx->arena;
     float * dA = cv.take<float>(sa);
@@ -1139,7 +1153,7 @@ int kv_compact_hip_score_all_heads(const float * Q_ref, const float * K_all, flo
     std::lock_guard<std::mutex> lk(ctx->mu);
     const size_t ek = (size_t)n_head_kv * d_k;
     const size_t sq = (size_t)n_q * ek, sk = (size_t)T * ek, ss = (size_t)n_head_kv * n_q * T;
-    if (!ensure_arena(ctx, (sq + sk + ss) * 4 + 1024)) return -1;
+    if (!drain_second_stream(ctx, ctx->stream) || !ensure_arena(ctx, (sq + sk + ss) * 4 + 1024)) return -1;
     Carver cv;
     cv.base = ctx->arena;
     float * dQ = cv.take<float>(sq);
@@ -1164,7 +1178,7 @@ int kv_compact_hip_refit_target_all_heads(const float * const * W_per_head, cons
     std::lock_guard<std::mutex> lk(ctx->mu);
     const size_t ev = (size_t)n_head_kv * d_v;
     const size_t sw = (size_t)n_head_kv * n_q * T, sv = (size_t)T * ev, sy = (size_t)n_head_kv * n_q * d_v;
-    if (!ensure_arena(ctx, (sw + sv + sy) * 4 + 1024)) return -1;
+    if (!drain_second_stream(ctx, ctx->stream) || !ensure_arena(ctx, (sw + sv + sy) * 4 + 1024)) return -1;
     Carver cv;
     cv.base = ctx->arena;
     float * dW = cv.take<float>(sw);
@@ -1200,10 +1214,15 @@ int kvc_plan(int T, int n_q, int q_ref_given, const kv_compact_params * params, 
     return 0;
 }
 
-int kvc_compact_layers_device(const float * K, const float * V, const float * Q_ref, int L, int T, int n_q,
-                              int n_head_kv, int d_k, int d_v, long long ldK, long long ldV, long long ldQ,
-                              const kv_compact_params * params, const float * token_weight,
-                              kvc_device_out * out, void * stream) {
+}  // extern "C"
+
+namespace {
+
+// kvc_compact_layers_device: the workspace is the device arena (grown with
+// hipMalloc when needed).
+int layers_device(const float * K, const float * V, const float * Q_ref, int L, int T, int n_q, int n_head_kv,
+                  int d_k, int d_v, long long ldK, long long ldV, long long ldQ, const kv_compact_params * params,
+                  const float * token_weight, kvc_device_out * out, void * stream) {
     kv_compact_params p = params ? *params : defaults();
     int rc = validate(K, V, out, T, n_q, n_head_kv, d_k, d_v, Q_ref, p);
     if (rc) return rc;
@@ -1226,9 +1245,10 @@ int kvc_compact_layers_device(const float * K, const float * V, const float * Q_
     const bool host_w = !token_weight && rkv_weights(p, T, wts);
     Carver sizer;
     if (host_w) sizer.take<float>(T);
-    size_t need = workspace_bytes(pl, io, &p, &sizer, nullptr, nullptr);
-    if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
+    const size_t need = workspace_bytes(pl, io, &p, &sizer, nullptr, nullptr);
+    if (!drain_second_stream(ctx, st)) return KV_COMPACT_E_DEVICE;
     Carver cv;
+    if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
     cv.base = ctx->arena;
     io.wts = token_weight;
     if (host_w) {
@@ -1238,6 +1258,18 @@ int kvc_compact_layers_device(const float * K, const float * V, const float * Q_
         io.wts = dW;
     }
     return run_batch(ctx, st, pl, p, io, cv, nullptr);
+}
+
+}  // namespace
+
+extern "C" {
+
+int kvc_compact_layers_device(const float * K, const float * V, const float * Q_ref, int L, int T, int n_q,
+                              int n_head_kv, int d_k, int d_v, long long ldK, long long ldV, long long ldQ,
+                              const kv_compact_params * params, const float * token_weight,
+                              kvc_device_out * out, void * stream) {
+    return layers_device(K, V, Q_ref, L, T, n_q, n_head_kv, d_k, d_v, ldK, ldV, ldQ, params, token_weight, out,
+                         stream);
 }
 
 int kvc_compact_quantized_device(const uint8_t * K_quant, const uint8_t * V_quant, const float * Q_ref,

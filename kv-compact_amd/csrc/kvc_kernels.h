@@ -16,6 +16,8 @@ void launch_global_importance(const Geom & g, const Work & w, hipStream_t st);
 void launch_select_topk(const Geom & g, const Work & w, hipStream_t st);
 void launch_div_level(const Geom & g, const Work & w, const DivWork & dw, const float * K, hipStream_t st);
 void launch_fill_int(int * p, int v, long long n, hipStream_t st);
+// fill kernels stand in for hipMemsetAsync (a caller may capture the call in a graph)
+void launch_fill_f32(float * p, float v, long long n, hipStream_t st);
 void launch_refine_step(const Geom & g, const Work & w, hipStream_t st);
 void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st);
 void launch_gather_exp(const Geom & g, const Work & w, hipStream_t st);

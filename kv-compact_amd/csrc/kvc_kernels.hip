@@ -1790,8 +1790,9 @@ k_nnls_lh(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restric
 // ones, whose general elimination swaps rows in place. For p == 1 both are
 // the same.
 // The register LU forms M = X^T X from X itself when X (nq x n) fits the LDS
-// of its step ring: then k_ls_build writes B only.
-__device__ __forceinline__ bool lu_x_fits(int n, int nq) { return n <= 256 && nq >= 1 && nq * n <= 8192; }
+// of its step ring (lu_x_fits, defined with the LU's constants below): then
+// k_ls_build writes B only.
+__device__ __forceinline__ bool lu_x_fits(int n, int nq);
 
 __device__ __forceinline__ long long rhs_at(int n, int p, int i, int v) {
     return (long long)n * n + (n <= 256 ? (long long)i * p + v : (long long)v * n + i);
@@ -1999,7 +2000,10 @@ constexpr int RG_THREADS = RG_WAVES * 64;
 constexpr int LU_RING = 32;          // > 17 outstanding steps
 constexpr int LU_TROWS = 32;         // rows per pass of the transposed output write
 constexpr int LU_SPIN_LIMIT = 1 << 22;   // polls per wave over the whole factorization
-constexpr int LU_X_FLOATS = LU_RING * 64 * 4;   // X staged in the ring's LDS: nq * n <= 8192
+constexpr int LU_X_FLOATS = LU_RING * 64 * 4;   // X staged in the ring's LDS: nq * n <= LU_X_FLOATS
+
+// X (nq x n) fits the ring's LDS, and the system the register LU
+__device__ __forceinline__ bool lu_x_fits(int n, int nq) { return n <= RG_ROWS && nq >= 1 && nq * n <= LU_X_FLOATS; }
 
 struct LuShared {
     union {
@@ -2007,6 +2011,7 @@ struct LuShared {
         float tile[LU_TROWS][RG_ROWS + 1];   // output staging at the end
         float xs[LU_X_FLOATS];       // X (nq x n) while the matrix is formed, when M comes from X
     } u;
+    static_assert(sizeof(float) * LU_X_FLOATS <= sizeof(float4) * LU_RING * 64, "X staging exceeds the ring");
     int plog[RG_ROWS];               // step c's pivot row (+256: skipped); -1 until published
     union {
         struct {
@@ -2428,10 +2433,15 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
             __syncthreads();
             for (int e = tid; e < LU_TROWS * RG_ROWS; e += RG_THREADS) {
                 const int rr = e / RG_ROWS, j = e % RG_ROWS;
-                if (r0 + rr < n) LU[(unsigned)((r0 + rr) * RG_ROWS + j)] = j < n ? sh.u.tile[rr][j] : 0.0f;
+                if (r0 + rr < n && j < n) LU[(unsigned)((r0 + rr) * RG_ROWS + j)] = sh.u.tile[rr][j];
             }
             __syncthreads();
         }
+    }
+    // zeros past column n
+    for (int e = tid; e < n * (RG_ROWS - n); e += RG_THREADS) {
+        const int r = e / (RG_ROWS - n), j = n + e % (RG_ROWS - n);
+        LU[(unsigned)(r * RG_ROWS + j)] = 0.0f;
     }
 }
 
@@ -2955,17 +2965,19 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 //
 // One wave per 64 right-hand-side columns (lane = column), the waves of a
 // system in one block, two waves per SIMD. A column's 256 values sit in 32
-// groups of eight rows: 24 groups in registers, 8 in LDS. Registers are only
+// groups of eight rows: 23 groups in registers, 9 in LDS (the most that lets
+// two waves share a SIMD with nothing spilled: the 23 groups take 184 of 256
+// registers, and four blocks' LDS fill the CU's 160 KB). Registers are only
 // indexed statically, so they form a stack: a new group enters at block 0 and
 // the others move down one block. Each pass reads the stack in a fixed order
 // with a uniform guard per block:
 //  - forward: block m holds group cnt-1-m (cnt = groups in registers), read
-//    oldest first; groups 24-31 go to LDS (the earliest rows, read by every
+//    oldest first; groups 23-31 go to LDS (the earliest rows, read by every
 //    later row, stay in registers);
 //  - backward: block m holds the solution of group gb+1+m, read newest first,
 //    and the bottom blocks hold the y groups still to be consumed, the next
-//    one in block 23; once 24 solved groups fill the stack the oldest moves
-//    to the LDS slot of the y group just consumed.
+//    one in the last block; once solved groups fill the stack the oldest
+//    moves to the LDS slot of the y group just consumed.
 // Between the passes the blocks are permuted statically into the backward's
 // order. Rows of L and U are the same for every lane of a wave and come
 // through scalar loads. The forward pass sums four rows side by side
@@ -2977,7 +2989,7 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 // ---------------------------------------------------------------------------
 constexpr int SB_G = 8;                     // rows per group (and entries per block)
 constexpr int SB_NG = RG_ROWS / SB_G;       // groups of a column
-constexpr int SB_RG = 24;                   // groups held in registers
+constexpr int SB_RG = 23;                   // groups held in registers
 constexpr int SB_LG = SB_NG - SB_RG;        // groups held in LDS
 constexpr int SB_LDS = SB_LG * SB_G;        // stored LDS rows per lane (plus an eight-row window)
 
@@ -3057,7 +3069,7 @@ __device__ __forceinline__ void sb_fhalf(float (&val)[4], const float (&R)[SB_RG
         __builtin_amdgcn_sched_barrier(0);
         sb_fterms(val, ln, &R[m][4]);
     }
-    // LDS groups 24 .. gi - 1 (lc holds steps 192 .. 195 when there are any)
+    // LDS groups SB_RG .. gi - 1 (lc holds their first four steps when there are any)
     for (int G = SB_RG; G < gi; G++) {
         const int k0 = SB_G * G;
         float y[SB_G];
@@ -3085,7 +3097,7 @@ __device__ __forceinline__ void sb_fhalf(float (&val)[4], const float (&R)[SB_RG
         for (int t = 0; t < 4; t++) sb_load(lc[t], lr[t], g0 + 4);
         sb_wait_scalar();
     }
-    const int h0 = SECOND ? g0 + 4 : g0;
+    // (lc: the entries of the half's own steps)
 #pragma unroll
     for (int t = 1; t < 4; t++) {
 #pragma unroll
@@ -3138,7 +3150,7 @@ __device__ __forceinline__ void sb_fgroup(float (&yg)[SB_G], const float (&R)[SB
 __device__ __forceinline__ void sb_forward(float (&R)[SB_RG][SB_G], float (*zl)[64], const float * __restrict__ LU,
                                            const float * __restrict__ B, const int (&pv)[4], int n, int p, int vc,
                                            int lane, float & pf) {
-    // groups 0-23 onto the register stack, groups 24-31 into LDS
+    // groups 0 .. SB_RG - 1 onto the register stack, the rest into LDS
     for (int gi = 0; gi < SB_RG; gi++) {
         float yg[SB_G];
         sb_fgroup(yg, R, zl, LU, B, pv, gi, n, p, vc, lane, pf);
@@ -3152,8 +3164,8 @@ __device__ __forceinline__ void sb_forward(float (&R)[SB_RG][SB_G], float (*zl)[
     }
 }
 
-// Backward pass. On entry block m holds y group 8 + m and LDS slot s y group
-// s; on exit block m holds x group m and LDS slot s x group 24 + s.
+// Backward pass. On entry block m holds y group SB_LG + m and LDS slot s y
+// group s; on exit block m holds x group m and LDS slot s x group SB_RG + s.
 // lane L of each 16-lane row of v, in every lane (DPP row_newbcast, folded
 // into the instruction that uses it)
 template <int L>
@@ -3226,7 +3238,7 @@ __device__ __forceinline__ void sb_bgroup(float (&xw)[SB_G], const float (&yw)[S
                 int nxr = nx;
                 asm volatile("" : "+s"(nxr));
                 sb_bblocks(val, us, R, nxr, std::make_integer_sequence<int, SB_RG>{});
-                // solved groups gb + 25 .. 31 in LDS slots gb + 1 .. 7
+                // solved groups gb + SB_RG + 1 .. 31 in LDS slots gb + 1 .. SB_LG - 1
                 for (int s = gb + 1; s < SB_LG; s++) {
                     float uc[SB_G];
                     sb_load(uc, ur, SB_G * (s + SB_RG));
@@ -3243,7 +3255,7 @@ __device__ __forceinline__ void sb_bgroup(float (&xw)[SB_G], const float (&yw)[S
 
 __device__ __forceinline__ void sb_backward(float (&R)[SB_RG][SB_G], float (*zl)[64], const float * __restrict__ LU,
                                             const int (&pv)[4], int n, float zero_val, int lane, float & pf) {
-    // groups 31-8: y from the bottom block, which the pushed result replaces
+    // groups 31 .. SB_LG: y from the bottom block, which the pushed result replaces
     for (int gb = SB_NG - 1; gb >= SB_LG; gb--) {
         float yw[SB_G], xw[SB_G];
 #pragma unroll
@@ -3251,7 +3263,7 @@ __device__ __forceinline__ void sb_backward(float (&R)[SB_RG][SB_G], float (*zl)
         sb_bgroup(xw, yw, R, zl, LU, pv, gb, n, zero_val, lane, pf);
         sb_push(R, xw);
     }
-    // groups 7-0: y from LDS; the oldest solved group moves to its slot
+    // groups SB_LG - 1 .. 0: y from LDS; the oldest solved group moves to its slot
     for (int gb = SB_LG - 1; gb >= 0; gb--) {
         float yw[SB_G], xw[SB_G];
 #pragma unroll
@@ -3301,22 +3313,29 @@ k_ge_subst(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         for (int j = 0; j < SB_G; j++) R[m][j] = 0.0f;
     float pf = 0.0f;   // sink of the cache warm-up loads
     sb_forward(R, zl, LU, B, pv, n, p, vc, lane, pf);
-    // forward layout: block m = group 23 - m, LDS slot s = group 24 + s;
-    // backward layout: block m = group 8 + m, LDS slot s = group s
+    // forward layout: block m = group SB_RG - 1 - m, LDS slot s = group
+    // SB_RG + s; backward layout: block m = group SB_LG + m, LDS slot s =
+    // group s
     {
+        // one group at a time (a group's LDS slot is read before the
+        // register group that replaces it is stored), so that no more than
+        // one group is in flight beside the stack
         float Q[SB_RG][SB_G];
 #pragma unroll
-        for (int m = 0; m < 16; m++)
+        for (int s = 0; s < SB_LG; s++) {
+            float t[SB_G];
 #pragma unroll
-            for (int j = 0; j < SB_G; j++) Q[m][j] = R[15 - m][j];
-#pragma unroll
-        for (int m = 16; m < SB_RG; m++)
-#pragma unroll
-            for (int j = 0; j < SB_G; j++) Q[m][j] = zl[SB_G * (m - 16) + j][lane];
-#pragma unroll
-        for (int s = 0; s < SB_LG; s++)
+            for (int j = 0; j < SB_G; j++) t[j] = zl[SB_G * s + j][lane];
 #pragma unroll
             for (int j = 0; j < SB_G; j++) zl[SB_G * s + j][lane] = R[SB_RG - 1 - s][j];
+#pragma unroll
+            for (int j = 0; j < SB_G; j++) Q[SB_RG - SB_LG + s][j] = t[j];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int m = 0; m < SB_RG - SB_LG; m++)
+#pragma unroll
+            for (int j = 0; j < SB_G; j++) Q[m][j] = R[SB_RG - SB_LG - 1 - m][j];
 #pragma unroll
         for (int m = 0; m < SB_RG; m++)
 #pragma unroll
@@ -3887,6 +3906,16 @@ __global__ void __launch_bounds__(256) k_fill_int(int * __restrict__ p, int v, l
 void launch_fill_int(int * p, int v, long long n, hipStream_t st) {
     if (n <= 0) return;
     hipLaunchKernelGGL(k_fill_int, dim3(cdiv(n, 256)), dim3(256), 0, st, p, v, n);
+}
+
+__global__ void __launch_bounds__(256) k_fill_f32(float * __restrict__ p, float v, long long n) {
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+void launch_fill_f32(float * p, float v, long long n, hipStream_t st) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_fill_f32, dim3(grid_cap(n, 256)), dim3(256), 0, st, p, v, n);
 }
 
 void launch_refine_step(const Geom & g, const Work & w, hipStream_t st) {
