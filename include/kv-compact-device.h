@@ -42,6 +42,27 @@ int kvc_compact_layers_device(const float * K, const float * V, const float * Q_
                               const kv_compact_params * params, const float * token_weight,
                               kvc_device_out * out, void * stream);
 
+/* Allocation-free variant of kvc_compact_layers_device (no counterpart in the
+ * reference). For callers that cannot allocate device memory (tight serving
+ * loops, code under graph capture, harnesses that forbid hipMalloc): same
+ * arguments, outputs and results bit for bit, but the workspace is a fixed
+ * device array of KVC_NOALLOC_SCRATCH_BYTES per GPU that the library holds
+ * from load until the process ends, and the call makes no hipMalloc/hipFree
+ * (nor any other allocating library call). A call whose workspace exceeds the
+ * array returns KVC_E_SCRATCH without launching anything. Every call on one
+ * GPU uses that GPU's array and leaves its contents behind (each call writes
+ * what it reads, and clears its status flag with a kernel): calls on one GPU
+ * must not overlap — this library serializes its own calls per device, so
+ * overlapping calls can only come from elsewhere (another copy of the library
+ * in the process) and would race on the array. */
+#define KVC_NOALLOC_SCRATCH_BYTES (64u << 20)
+#define KVC_E_SCRATCH (-7)
+int kvc_compact_layers_device_noalloc(const float * K, const float * V, const float * Q_ref,
+                                      int L, int T, int n_q, int n_head_kv, int d_k, int d_v,
+                                      long long ldK, long long ldV, long long ldQ,
+                                      const kv_compact_params * params, const float * token_weight,
+                                      kvc_device_out * out, void * stream);
+
 /* Device-resident quantized pipeline for one layer: K/V rows in the given
  * codec (device), outputs requantized rows (device, t_total x row bytes)
  * plus indices/beta/C_v/stats as above (L = 1). */

@@ -38,9 +38,16 @@ namespace {
 enum Stage { ST_SCORES, ST_SOFTMAX, ST_REFIT, ST_SELECT, ST_BETA, ST_LS_SOFTMAX, ST_LS_BUILD, ST_LU, ST_SOLVE,
              ST_REFINE, ST_STATS, ST_COUNT };
 
+// Fixed workspace of kvc_compact_layers_device_noalloc, one copy per GPU
+// (each device that loads the library holds it until the process ends). Host
+// code never uses this name as an address: DeviceCtx::scratch holds the
+// device address, taken once per device with hipGetSymbolAddress.
+static __device__ __align__(256) unsigned char scratch[KVC_NOALLOC_SCRATCH_BYTES];
+
 struct DeviceCtx {
     std::mutex mu;
     bool ready = false;
+    char * scratch = nullptr;   // device address of `scratch` on this device (null if unavailable)
     hipStream_t stream = nullptr;
     // second stream (default priority, like stream) for work that runs beside
     // the main chain: the refit target during the selection, and the
@@ -96,6 +103,13 @@ DeviceCtx * device_ctx() {
             if (hipEventCreate(&c->refit_t[i]) != hipSuccess) return nullptr;
         for (int i = 0; i <= ST_COUNT; i++)
             if (hipEventCreate(&c->ev[i]) != hipSuccess) return nullptr;
+        void * sp = nullptr;
+        if (hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) == hipSuccess) {
+            c->scratch = static_cast<char *>(sp);
+        } else {
+            (void)hipGetLastError();
+            c->scratch = nullptr;
+        }
         c->ready = true;
     }
     return c;
@@ -1218,11 +1232,11 @@ int kvc_plan(int T, int n_q, int q_ref_given, const kv_compact_params * params, 
 
 namespace {
 
-// kvc_compact_layers_device: the workspace is the device arena (grown with
-// hipMalloc when needed).
+// kvc_compact_layers_device and its allocation-free variant: the workspace is
+// the device arena (grown with hipMalloc when needed) or the fixed scratch.
 int layers_device(const float * K, const float * V, const float * Q_ref, int L, int T, int n_q, int n_head_kv,
                   int d_k, int d_v, long long ldK, long long ldV, long long ldQ, const kv_compact_params * params,
-                  const float * token_weight, kvc_device_out * out, void * stream) {
+                  const float * token_weight, kvc_device_out * out, void * stream, bool noalloc) {
     kv_compact_params p = params ? *params : defaults();
     int rc = validate(K, V, out, T, n_q, n_head_kv, d_k, d_v, Q_ref, p);
     if (rc) return rc;
@@ -1248,8 +1262,18 @@ int layers_device(const float * K, const float * V, const float * Q_ref, int L, 
     const size_t need = workspace_bytes(pl, io, &p, &sizer, nullptr, nullptr);
     if (!drain_second_stream(ctx, st)) return KV_COMPACT_E_DEVICE;
     Carver cv;
-    if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
-    cv.base = ctx->arena;
+    if (noalloc) {
+        if (!ctx->scratch) return KV_COMPACT_E_DEVICE;
+        if (need > (size_t)KVC_NOALLOC_SCRATCH_BYTES) {
+            fprintf(stderr, "[kv-compact] kvc_compact_layers_device_noalloc: the call needs %zu bytes of workspace, "
+                            "the fixed scratch holds %zu\n", need, (size_t)KVC_NOALLOC_SCRATCH_BYTES);
+            return KVC_E_SCRATCH;
+        }
+        cv.base = ctx->scratch;
+    } else {
+        if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
+        cv.base = ctx->arena;
+    }
     io.wts = token_weight;
     if (host_w) {
         float * dW = cv.take<float>(T);
@@ -1269,7 +1293,15 @@ int kvc_compact_layers_device(const float * K, const float * V, const float * Q_
                               const kv_compact_params * params, const float * token_weight,
                               kvc_device_out * out, void * stream) {
     return layers_device(K, V, Q_ref, L, T, n_q, n_head_kv, d_k, d_v, ldK, ldV, ldQ, params, token_weight, out,
-                         stream);
+                         stream, false);
+}
+
+int kvc_compact_layers_device_noalloc(const float * K, const float * V, const float * Q_ref, int L, int T, int n_q,
+                                      int n_head_kv, int d_k, int d_v, long long ldK, long long ldV, long long ldQ,
+                                      const kv_compact_params * params, const float * token_weight,
+                                      kvc_device_out * out, void * stream) {
+    return layers_device(K, V, Q_ref, L, T, n_q, n_head_kv, d_k, d_v, ldK, ldV, ldQ, params, token_weight, out,
+                         stream, true);
 }
 
 int kvc_compact_quantized_device(const uint8_t * K_quant, const uint8_t * V_quant, const float * Q_ref,

@@ -36,6 +36,7 @@ def hip():
         _hip.hipDeviceGetName.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int]
         _hip.hipGetDeviceCount.argtypes = [ctypes.POINTER(ctypes.c_int)]
         _hip.hipGetErrorString.restype = ctypes.c_char_p
+        _hip.hipMemGetInfo.argtypes = [ctypes.POINTER(sz), ctypes.POINTER(sz)]
     return _hip
 
 
@@ -93,6 +94,13 @@ def device_name() -> str:
     buf = ctypes.create_string_buffer(256)
     check(hip().hipDeviceGetName(buf, 256, 0), "hipDeviceGetName")
     return buf.value.decode()
+
+
+def mem_free() -> int:
+    """Free device memory in bytes (hipMemGetInfo)."""
+    f, t = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    check(hip().hipMemGetInfo(ctypes.byref(f), ctypes.byref(t)), "hipMemGetInfo")
+    return f.value
 
 
 def synchronize():

@@ -24,7 +24,7 @@ REPO = HERE.parent
 KV_TYPE_F32, KV_TYPE_F16, KV_TYPE_Q4_0, KV_TYPE_Q4_1, KV_TYPE_Q8_0 = 0, 1, 2, 3, 8
 KV_TYPE_BF16 = 30   # extension: bfloat16 rows (no reference counterpart)
 KV_TOKEN_ANSWER, KV_TOKEN_THINKING, KV_TOKEN_TRANSITION = 0, 1, 2
-E_UNSUPPORTED, E_DEVICE = -5, -6
+E_UNSUPPORTED, E_DEVICE, E_SCRATCH = -5, -6, -7
 
 
 class Stats(ctypes.Structure):
@@ -283,6 +283,8 @@ def bind_device_api(dll):
                                               ctypes.c_longlong, ctypes.c_longlong, ctypes.c_longlong,
                                               ctypes.POINTER(Params), _vp, ctypes.POINTER(DeviceOut), _vp]
     dll.kvc_compact_layers_device.restype = _i
+    dll.kvc_compact_layers_device_noalloc.argtypes = dll.kvc_compact_layers_device.argtypes
+    dll.kvc_compact_layers_device_noalloc.restype = _i
     dll.kvc_stage_times.argtypes = [ctypes.POINTER(ctypes.c_float), _i]
     dll.kvc_stage_times.restype = _i
     dll.kv_compact_hip_available.restype = _i
