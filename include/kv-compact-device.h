@@ -63,9 +63,22 @@ int kvc_compact_layers_device_noalloc(const float * K, const float * V, const fl
                                       const kv_compact_params * params, const float * token_weight,
                                       kvc_device_out * out, void * stream);
 
-/* Device-resident quantized pipeline for one layer: K/V rows in the given
- * codec (device), outputs requantized rows (device, t_total x row bytes)
- * plus indices/beta/C_v/stats as above (L = 1). */
+/* Device-resident quantized pipeline (reference api.cpp:1182-1257 for each
+ * layer): L layers of K/V rows in the given codecs (device; layer l of K at
+ * K_quant + l * ldKq bytes, likewise V; Q_ref layers ldQ floats apart) are
+ * dequantized into the library's workspace, compacted as by
+ * kvc_compact_layers_device, and the kept K rows and refitted V rows
+ * requantized into K_out / V_out (device, [L][t_total][row bytes]); indices,
+ * beta, C_v and stats as above. Each layer's outputs equal
+ * kv_compact_quantized() on that layer bit for bit. */
+int kvc_compact_quantized_layers_device(const uint8_t * K_quant, const uint8_t * V_quant, const float * Q_ref,
+                                        int L, int k_type, int v_type, size_t k_row_bytes, size_t v_row_bytes,
+                                        int T, int n_q, int n_head_kv, int d_k, int d_v,
+                                        long long ldKq, long long ldVq, long long ldQ,
+                                        const kv_compact_params * params, kvc_device_out * out,
+                                        uint8_t * K_out, uint8_t * V_out, void * stream);
+
+/* The same for one layer (L = 1). */
 int kvc_compact_quantized_device(const uint8_t * K_quant, const uint8_t * V_quant, const float * Q_ref,
                                  int k_type, int v_type, size_t k_row_bytes, size_t v_row_bytes,
                                  int T, int n_q, int n_head_kv, int d_k, int d_v,

@@ -780,6 +780,62 @@ int block_bytes(int type) {
 bool is_block_type(int t) { return t == KV_TYPE_Q8_0 || t == KV_TYPE_Q4_0 || t == KV_TYPE_Q4_1; }
 bool known_type(int t) { return t == KV_TYPE_F32 || t == KV_TYPE_F16 || t == KV_TYPE_BF16 || is_block_type(t); }
 
+// Quantized caches of L layers (device memory; layer strides in bytes).
+struct QuantIO {
+    const uint8_t * Kq = nullptr;
+    const uint8_t * Vq = nullptr;
+    long long lsKq = 0, lsVq = 0;
+    int k_type = 0, v_type = 0;
+    size_t k_rb = 0, v_rb = 0;
+    uint8_t * Kout = nullptr;   // [L][t][k_rb]
+    uint8_t * Vout = nullptr;   // [L][t][v_rb]
+};
+
+// rows [L][T] of a codec into fp32 [L][T][n_el]
+void dequant_cache(const uint8_t * src, int type, size_t rb, long long ls, int n_el, int T, int L, float * dst,
+                   hipStream_t st) {
+    if (codec8_ok(type, n_el)) {
+        launch_dequant8(src, type, (long long)rb, ls, n_el, T, L, dst, st);
+        return;
+    }
+    for (int l = 0; l < L; l++)
+        launch_dequant_rows(src + (long long)l * ls, type, (long long)rb, n_el, T, dst + (long long)l * T * n_el, st);
+}
+
+// Scratch the requantization of L layers may need (value rows gathered from
+// C_v when the coalesced kernel does not apply).
+size_t requant_floats(const QuantIO & qi, int t, int H, int dv) {
+    const bool v8 = codec8_ok(qi.v_type, H * dv) && dv % 8 == 0;
+    return v8 ? 0 : (size_t)t * H * dv;
+}
+
+// K_out: the kept rows of the dequantized K (api.cpp:1234-1241); V_out: the
+// refitted rows assembled over heads from C_v (api.cpp:1243-1254).
+void requant_outputs(const QuantIO & qi, const float * Kf, const int * idx, const float * Cv, int L, int T, int t,
+                     int H, int dk, int dv, float * rows_tmp, hipStream_t st) {
+    if (t <= 0) return;
+    const int ek = H * dk, ev = H * dv;
+    const bool cv_al = (reinterpret_cast<uintptr_t>(Cv) & 15) == 0;
+    if (codec8_ok(qi.k_type, ek)) {
+        launch_requant8(Kf, (long long)T * ek, ek, idx, t, 0, H, dk, qi.k_type, ek, t, L, qi.Kout,
+                        (long long)qi.k_rb, (long long)t * qi.k_rb, st);
+    } else {
+        for (int l = 0; l < L; l++)
+            launch_quant_rows(Kf + (long long)l * T * ek, ek, idx + (long long)l * t, qi.k_type, ek, t,
+                              qi.Kout + (long long)l * t * qi.k_rb, (long long)qi.k_rb, st);
+    }
+    if (codec8_ok(qi.v_type, ev) && dv % 8 == 0 && cv_al) {
+        launch_requant8(Cv, 0, 0, nullptr, 0, 1, H, dv, qi.v_type, ev, t, L, qi.Vout, (long long)qi.v_rb,
+                        (long long)t * qi.v_rb, st);
+    } else {
+        for (int l = 0; l < L; l++) {
+            launch_gather_cv_rows(Cv + (long long)l * H * t * dv, H, t, dv, rows_tmp, st);
+            launch_quant_rows(rows_tmp, ev, nullptr, qi.v_type, ev, t, qi.Vout + (long long)l * t * qi.v_rb,
+                              (long long)qi.v_rb, st);
+        }
+    }
+}
+
 }  // namespace
 
 // ======================================================================
@@ -1035,8 +1091,9 @@ size_t kv_quantize_row(const float * src, int type, int n_elements, uint8_t * ds
     return nb;
 }
 
-// Reference api.cpp:1182-1257: dequantize on the device, compact, requantize
-// the kept original K rows and the refitted V rows on the device.
+// Reference api.cpp:1182-1257: the quantized rows are uploaded into the
+// workspace, dequantized there, compacted, and the kept K rows and refitted V
+// rows requantized there; the host receives the results only.
 int kv_compact_quantized(const uint8_t * K_quant, const uint8_t * V_quant, const float * Q_ref_all,
                          int k_type, int v_type, size_t k_row_bytes, size_t v_row_bytes,
                          int T, int n_q, int n_head_kv, int d_k, int d_v,
@@ -1054,73 +1111,96 @@ int kv_compact_quantized(const uint8_t * K_quant, const uint8_t * V_quant, const
     rc = check_supported(p, d_v);
     if (rc) return rc;
     if (!known_type(k_type) || !known_type(v_type)) return KV_COMPACT_E_UNSUPPORTED;
-    float * dKf = nullptr;
-    float * dVf = nullptr;
-    uint8_t * dKq = nullptr;
-    uint8_t * dVq = nullptr;
-    {
-        DeviceCtx * ctx = device_ctx();
-        if (!ctx) return KV_COMPACT_E_DEVICE;
-        hipStream_t st = ctx->stream;
-        std::lock_guard<std::mutex> lk(ctx->mu);
-        // dequantized cache lives in its own allocation for the compaction call
-        if (hipMalloc(&dKf, (size_t)T * ek * 4) != hipSuccess || hipMalloc(&dVf, (size_t)T * ev * 4) != hipSuccess ||
-            hipMalloc(&dKq, (size_t)T * k_row_bytes) != hipSuccess || hipMalloc(&dVq, (size_t)T * v_row_bytes) != hipSuccess) {
-            (void)hipGetLastError();
-            (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dKq); (void)hipFree(dVq);
-            return KV_COMPACT_E_DEVICE;
-        }
-        hipError_t e = hipMemcpyAsync(dKq, K_quant, (size_t)T * k_row_bytes, hipMemcpyHostToDevice, st);
-        if (e == hipSuccess) e = hipMemcpyAsync(dVq, V_quant, (size_t)T * v_row_bytes, hipMemcpyHostToDevice, st);
-        if (e == hipSuccess) {
-            launch_dequant_rows(dKq, k_type, (long long)k_row_bytes, ek, T, dKf, st);
-            launch_dequant_rows(dVq, v_type, (long long)v_row_bytes, ev, T, dVf, st);
-            e = hipStreamSynchronize(st);
-        }
-        if (e != hipSuccess) {
-            (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dKq); (void)hipFree(dVq);
-            return KV_COMPACT_E_DEVICE;
-        }
+    const double t0 = now_ms();
+    DeviceCtx * ctx = device_ctx();
+    if (!ctx) return KV_COMPACT_E_DEVICE;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipStream_t st = ctx->stream;
+    if (!drain_second_stream(ctx, st)) return KV_COMPACT_E_DEVICE;
+    Plan pl;
+    const bool q_given = Q_ref_all != nullptr;
+    make_plan(T, n_q, q_given, p, pl);
+    const bool use_q = q_given && !p.use_cheap_qref;
+    const bool qd = use_q && is_device_ptr(Q_ref_all);
+    std::vector<float> wts;
+    const bool have_w = rkv_weights(p, T, wts);
+    const int t = pl.t_total;
+    QuantIO qi;
+    qi.k_type = k_type; qi.v_type = v_type; qi.k_rb = k_row_bytes; qi.v_rb = v_row_bytes;
+    qi.lsKq = (long long)T * k_row_bytes; qi.lsVq = (long long)T * v_row_bytes;
+    BatchIO io{};
+    io.L = 1; io.T = T; io.n_q = n_q; io.H = H; io.dk = d_k; io.dv = d_v;
+    io.ldK = (long long)T * ek; io.ldV = (long long)T * ev; io.ldQ = (long long)std::max(n_q, 1) * ek;
+    // workspace: quantized rows, fp32 cache, query rows, weights, outputs, requantized rows, batch workspace
+    auto carve = [&](Carver & cv, uint8_t *& dKq, uint8_t *& dVq, float *& dK, float *& dV, float *& dQ,
+                     float *& dW, float *& tmp) {
+        dKq = cv.take<uint8_t>((size_t)T * k_row_bytes);
+        dVq = cv.take<uint8_t>((size_t)T * v_row_bytes);
+        dK = cv.take<float>((size_t)T * ek);
+        dV = cv.take<float>((size_t)T * ev);
+        dQ = (use_q && !qd) ? cv.take<float>((size_t)n_q * ek) : nullptr;
+        dW = have_w ? cv.take<float>(T) : nullptr;
+        io.indices = cv.take<int>(std::max(t, 1));
+        io.beta = cv.take<float>((size_t)H * std::max(t, 1));
+        io.Cv = cv.take<float>((size_t)H * std::max(t, 1) * d_v);
+        io.stats = cv.take<float>(3);
+        qi.Kout = cv.take<uint8_t>((size_t)std::max(t, 1) * k_row_bytes);
+        qi.Vout = cv.take<uint8_t>((size_t)std::max(t, 1) * v_row_bytes);
+        tmp = cv.take<float>(std::max<size_t>(requant_floats(qi, t, H, d_v), 1));
+    };
+    uint8_t * dKq; uint8_t * dVq; float * dK; float * dV; float * dQ; float * dW; float * tmp;
+    Carver sizer;
+    carve(sizer, dKq, dVq, dK, dV, dQ, dW, tmp);
+    const size_t need = workspace_bytes(pl, io, &p, &sizer, nullptr, nullptr);
+    if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
+    Carver cv;
+    cv.base = ctx->arena;
+    carve(cv, dKq, dVq, dK, dV, dQ, dW, tmp);
+    hipError_t e = hipMemcpyAsync(dKq, K_quant, (size_t)T * k_row_bytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(dVq, V_quant, (size_t)T * v_row_bytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess && dQ) e = hipMemcpyAsync(dQ, Q_ref_all, (size_t)n_q * ek * 4, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess && dW) e = hipMemcpyAsync(dW, wts.data(), (size_t)T * 4, hipMemcpyHostToDevice, st);
+    if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
+    dequant_cache(dKq, k_type, k_row_bytes, qi.lsKq, ek, T, 1, dK, st);
+    dequant_cache(dVq, v_type, v_row_bytes, qi.lsVq, ev, T, 1, dV, st);
+    io.K = dK; io.V = dV; io.Q = use_q ? (qd ? Q_ref_all : dQ) : nullptr; io.wts = dW;
+    Timing tm;
+    rc = run_batch(ctx, st, pl, p, io, cv, &tm);
+    if (rc != 0) return rc;
+    requant_outputs(qi, dK, io.indices, io.Cv, 1, T, t, H, d_k, d_v, tmp, st);
+    std::vector<int> idx(t);
+    std::vector<float> beta((size_t)H * t), cvh((size_t)H * t * d_v);
+    float stats[3];
+    result->K_out = (uint8_t *)malloc((size_t)std::max(t, 1) * k_row_bytes);
+    result->V_out = (uint8_t *)malloc((size_t)std::max(t, 1) * v_row_bytes);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipMemcpyAsync(idx.data(), io.indices, (size_t)t * sizeof(int), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(beta.data(), io.beta, beta.size() * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(cvh.data(), io.Cv, cvh.size() * 4, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(stats, io.stats, sizeof(stats), hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess && t > 0)
+        e = hipMemcpyAsync(result->K_out, qi.Kout, (size_t)t * k_row_bytes, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess && t > 0)
+        e = hipMemcpyAsync(result->V_out, qi.Vout, (size_t)t * v_row_bytes, hipMemcpyDeviceToHost, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e != hipSuccess) {
+        free(result->K_out);
+        free(result->V_out);
+        result->K_out = result->V_out = NULL;
+        return KV_COMPACT_E_DEVICE;
     }
-    rc = compact_one(dKf, dVf, Q_ref_all, T, n_q, H, d_k, d_v, p, &result->base);
-    if (rc != 0) {
-        (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dKq); (void)hipFree(dVq);
-        return rc;
-    }
-    const int t = result->base.t;
+    fill_result(&result->base, t, H, d_v, idx, beta, cvh);
+    result->base.stats.avg_cosine_sim = stats[0];
+    result->base.stats.avg_mse = stats[1];
+    result->base.stats.avg_agreement = stats[2];
+    result->base.stats.scoring_ms = tm.scoring_ms;
+    result->base.stats.nnls_ms = tm.nnls_ms;
+    result->base.stats.elapsed_ms = now_ms() - t0;
     result->k_type = k_type;
     result->v_type = v_type;
     result->k_row_bytes = k_row_bytes;
     result->v_row_bytes = v_row_bytes;
-    result->K_out = (uint8_t *)malloc((size_t)std::max(t, 1) * k_row_bytes);
-    result->V_out = (uint8_t *)malloc((size_t)std::max(t, 1) * v_row_bytes);
-    DeviceCtx * ctx = device_ctx();
-    std::lock_guard<std::mutex> lk(ctx->mu);
-    hipStream_t st = ctx->stream;
-    int * dIdx = nullptr;
-    float * dCv = nullptr;
-    float * dRows = nullptr;
-    uint8_t * dKo = nullptr;
-    uint8_t * dVo = nullptr;
-    hipError_t e = hipMalloc(&dIdx, (size_t)std::max(t, 1) * 4);
-    if (e == hipSuccess) e = hipMalloc(&dCv, (size_t)std::max(t, 1) * ev * 4);
-    if (e == hipSuccess) e = hipMalloc(&dRows, (size_t)std::max(t, 1) * ev * 4);
-    if (e == hipSuccess) e = hipMalloc(&dKo, (size_t)std::max(t, 1) * k_row_bytes);
-    if (e == hipSuccess) e = hipMalloc(&dVo, (size_t)std::max(t, 1) * v_row_bytes);
-    if (e == hipSuccess) e = hipMemcpyAsync(dIdx, result->base.selected_indices, (size_t)t * 4, hipMemcpyHostToDevice, st);
-    for (int h = 0; h < H && e == hipSuccess; h++)
-        e = hipMemcpyAsync(dCv + (size_t)h * t * d_v, result->base.C_v[h], (size_t)t * d_v * 4, hipMemcpyHostToDevice, st);
-    if (e == hipSuccess && t > 0) {
-        launch_quant_rows(dKf, ek, dIdx, k_type, ek, t, dKo, (long long)k_row_bytes, st);
-        launch_gather_cv_rows(dCv, H, t, d_v, dRows, st);
-        launch_quant_rows(dRows, ev, nullptr, v_type, ev, t, dVo, (long long)v_row_bytes, st);
-        e = hipMemcpyAsync(result->K_out, dKo, (size_t)t * k_row_bytes, hipMemcpyDeviceToHost, st);
-        if (e == hipSuccess) e = hipMemcpyAsync(result->V_out, dVo, (size_t)t * v_row_bytes, hipMemcpyDeviceToHost, st);
-        if (e == hipSuccess) e = hipStreamSynchronize(st);
-    }
-    (void)hipFree(dIdx); (void)hipFree(dCv); (void)hipFree(dRows); (void)hipFree(dKo); (void)hipFree(dVo);
-    (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dKq); (void)hipFree(dVq);
-    return e == hipSuccess ? 0 : KV_COMPACT_E_DEVICE;
+    return 0;
 }
 
 void kv_compact_quant_result_free(kv_compact_quant_result * r) {
@@ -1304,46 +1384,80 @@ int kvc_compact_layers_device_noalloc(const float * K, const float * V, const fl
                          stream, true);
 }
 
+int kvc_compact_quantized_layers_device(const uint8_t * K_quant, const uint8_t * V_quant, const float * Q_ref,
+                                        int L, int k_type, int v_type, size_t k_row_bytes, size_t v_row_bytes,
+                                        int T, int n_q, int n_head_kv, int d_k, int d_v,
+                                        long long ldKq, long long ldVq, long long ldQ,
+                                        const kv_compact_params * params, kvc_device_out * out,
+                                        uint8_t * K_out, uint8_t * V_out, void * stream) {
+    if (!K_quant || !V_quant || !out || !K_out || !V_out) return -1;
+    if (T <= 0 || n_head_kv <= 0 || d_k <= 0 || d_v <= 0 || L <= 0) return -2;
+    const int H = n_head_kv, ek = H * d_k, ev = H * d_v;
+    if (kv_quant_row_elements(k_type, k_row_bytes) != ek || kv_quant_row_elements(v_type, v_row_bytes) != ev)
+        return -4;
+    if (!known_type(k_type) || !known_type(v_type)) return KV_COMPACT_E_UNSUPPORTED;
+    if (!out->indices || !out->beta || !out->C_v || !out->stats) return -1;
+    kv_compact_params p = params ? *params : defaults();
+    int rc = validate((const float *)K_quant, (const float *)V_quant, out, T, n_q, H, d_k, d_v, Q_ref, p);
+    if (rc) return rc;
+    rc = check_supported(p, d_v);
+    if (rc) return rc;
+    DeviceCtx * ctx = device_ctx();
+    if (!ctx) return KV_COMPACT_E_DEVICE;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
+    if (!drain_second_stream(ctx, st)) return KV_COMPACT_E_DEVICE;
+    Plan pl;
+    make_plan(T, n_q, Q_ref != nullptr, p, pl);
+    const int t = pl.t_total;
+    QuantIO qi;
+    qi.Kq = K_quant; qi.Vq = V_quant; qi.lsKq = ldKq; qi.lsVq = ldVq;
+    qi.k_type = k_type; qi.v_type = v_type; qi.k_rb = k_row_bytes; qi.v_rb = v_row_bytes;
+    qi.Kout = K_out; qi.Vout = V_out;
+    BatchIO io{};
+    io.Q = (Q_ref && !p.use_cheap_qref) ? Q_ref : nullptr;
+    io.ldK = (long long)T * ek; io.ldV = (long long)T * ev; io.ldQ = ldQ;
+    io.L = L; io.T = T; io.n_q = n_q; io.H = H; io.dk = d_k; io.dv = d_v;
+    io.indices = out->indices; io.beta = out->beta; io.Cv = out->C_v; io.stats = out->stats;
+    std::vector<float> wts;
+    const bool host_w = rkv_weights(p, T, wts);
+    auto carve = [&](Carver & cv, float *& dK, float *& dV, float *& dW, float *& tmp) {
+        dK = cv.take<float>((size_t)L * T * ek);
+        dV = cv.take<float>((size_t)L * T * ev);
+        dW = host_w ? cv.take<float>(T) : nullptr;
+        tmp = cv.take<float>(std::max<size_t>(requant_floats(qi, t, H, d_v), 1));
+    };
+    float * dK; float * dV; float * dW; float * tmp;
+    Carver sizer;
+    carve(sizer, dK, dV, dW, tmp);
+    const size_t need = workspace_bytes(pl, io, &p, &sizer, nullptr, nullptr);
+    if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
+    Carver cv;
+    cv.base = ctx->arena;
+    carve(cv, dK, dV, dW, tmp);
+    if (dW && hipMemcpyAsync(dW, wts.data(), (size_t)T * 4, hipMemcpyHostToDevice, st) != hipSuccess)
+        return KV_COMPACT_E_DEVICE;
+    dequant_cache(K_quant, k_type, k_row_bytes, ldKq, ek, T, L, dK, st);
+    dequant_cache(V_quant, v_type, v_row_bytes, ldVq, ev, T, L, dV, st);
+    io.K = dK; io.V = dV; io.wts = dW;
+    rc = run_batch(ctx, st, pl, p, io, cv, nullptr);
+    if (rc != 0) return rc;
+    requant_outputs(qi, dK, io.indices, io.Cv, L, T, t, H, d_k, d_v, tmp, st);
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    return e == hipSuccess ? 0 : KV_COMPACT_E_DEVICE;
+}
+
 int kvc_compact_quantized_device(const uint8_t * K_quant, const uint8_t * V_quant, const float * Q_ref,
                                  int k_type, int v_type, size_t k_row_bytes, size_t v_row_bytes,
                                  int T, int n_q, int n_head_kv, int d_k, int d_v,
                                  const kv_compact_params * params, kvc_device_out * out,
                                  uint8_t * K_out, uint8_t * V_out, void * stream) {
-    if (!K_quant || !V_quant || !out || !K_out || !V_out) return -1;
-    if (T <= 0 || n_head_kv <= 0 || d_k <= 0 || d_v <= 0) return -2;
-    const int H = n_head_kv, ek = H * d_k, ev = H * d_v;
-    if (kv_quant_row_elements(k_type, k_row_bytes) != ek || kv_quant_row_elements(v_type, v_row_bytes) != ev)
-        return -4;
-    if (!known_type(k_type) || !known_type(v_type)) return KV_COMPACT_E_UNSUPPORTED;
-    kv_compact_params p = params ? *params : defaults();
-    int rc = check_supported(p, d_v);
-    if (rc) return rc;
-    DeviceCtx * ctx = device_ctx();
-    if (!ctx) return KV_COMPACT_E_DEVICE;
-    hipStream_t st = stream ? (hipStream_t)stream : ctx->stream;
-    float * dKf = nullptr;
-    float * dVf = nullptr;
-    float * dRows = nullptr;
-    int t = 0;
-    kvc_plan(T, n_q, Q_ref != nullptr, &p, &t, nullptr);
-    if (hipMalloc(&dKf, (size_t)T * ek * 4) != hipSuccess || hipMalloc(&dVf, (size_t)T * ev * 4) != hipSuccess ||
-        hipMalloc(&dRows, (size_t)std::max(t, 1) * ev * 4) != hipSuccess) {
-        (void)hipGetLastError();
-        (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dRows);
-        return KV_COMPACT_E_DEVICE;
-    }
-    launch_dequant_rows(K_quant, k_type, (long long)k_row_bytes, ek, T, dKf, st);
-    launch_dequant_rows(V_quant, v_type, (long long)v_row_bytes, ev, T, dVf, st);
-    rc = kvc_compact_layers_device(dKf, dVf, Q_ref, 1, T, n_q, H, d_k, d_v, (long long)T * ek, (long long)T * ev,
-                                   (long long)std::max(n_q, 1) * ek, &p, nullptr, out, st);
-    if (rc == 0 && t > 0) {
-        launch_quant_rows(dKf, ek, out->indices, k_type, ek, t, K_out, (long long)k_row_bytes, st);
-        launch_gather_cv_rows(out->C_v, H, t, d_v, dRows, st);
-        launch_quant_rows(dRows, ev, nullptr, v_type, ev, t, V_out, (long long)v_row_bytes, st);
-        if (hipStreamSynchronize(st) != hipSuccess) rc = KV_COMPACT_E_DEVICE;
-    }
-    (void)hipFree(dKf); (void)hipFree(dVf); (void)hipFree(dRows);
-    return rc;
+    return kvc_compact_quantized_layers_device(K_quant, V_quant, Q_ref, 1, k_type, v_type, k_row_bytes, v_row_bytes,
+                                               T, n_q, n_head_kv, d_k, d_v, (long long)T * k_row_bytes,
+                                               (long long)T * v_row_bytes,
+                                               (long long)std::max(n_q, 1) * n_head_kv * d_k, params, out, K_out,
+                                               V_out, stream);
 }
 
 int kvc_stage_times(float * out_ms, int n) {

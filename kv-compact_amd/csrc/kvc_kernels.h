@@ -47,6 +47,15 @@ void launch_dequant_rows(const uint8_t * src, int type, long long row_bytes, int
 void launch_quant_rows(const float * src, long long src_ld, const int * idx, int type, int n_el,
                        long long rows, uint8_t * dst, long long row_bytes, hipStream_t st);
 void launch_gather_cv_rows(const float * Cv, int H, int t, int dv, float * rows, hipStream_t st);
+// whole-cache codec kernels (coalesced; Q8_0, Q4_0, F16, BF16, F32 when codec8_ok)
+bool codec8_ok(int type, int n_el);
+void launch_dequant8(const uint8_t * src, int type, long long row_bytes, long long src_ls, int n_el, int T, int L,
+                     float * dst, hipStream_t st);
+// mode 0: kept rows idx[l * idx_ls + j] of src (row stride src_ld, layer stride
+// src_ls floats); mode 1: value rows assembled from C_v [L][H][rows][dv]
+void launch_requant8(const float * src, long long src_ls, long long src_ld, const int * idx, long long idx_ls,
+                     int mode, int H, int dv, int type, int n_el, int rows, int L, uint8_t * dst, long long row_bytes,
+                     long long dst_ls, hipStream_t st);
 void launch_gemm_abt(const float * A, long long lda, const float * B, long long ldb, float * C, long long ldc,
                      int m, int n, int k, float scale, long long sa, long long sb, long long sc, int batch,
                      hipStream_t st);

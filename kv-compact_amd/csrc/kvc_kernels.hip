@@ -3808,6 +3808,159 @@ k_gather_cv_rows(const float * __restrict__ Cv, int H, int t, int dv, float * __
 }
 
 // ---------------------------------------------------------------------------
+// Whole-cache codec kernels (state.h:355-375, 528-567): eight elements per
+// work item, the floats moved as 16-byte pieces, so a wave reads and writes
+// contiguous memory. Quantization gives the four work items of a 32-element
+// block to the four lanes of a quad, which reduce the block's largest
+// magnitude between them (the largest non-NaN |x| from 0: one value in any
+// order). Results equal k_dequant_rows / k_quant_rows bit for bit; Q4_1 and
+// rows whose element count is not a multiple of 32 stay on those.
+// ---------------------------------------------------------------------------
+
+// rows [L][T] of codec `type` (row stride row_bytes, layer stride src_ls
+// bytes) into dst [L][T][n_el] fp32
+__global__ void __launch_bounds__(256)
+k_dequant8(const uint8_t * __restrict__ src, int type, long long row_bytes, long long src_ls, int n_el, int T,
+           int L, float * __restrict__ dst) {
+    const int n8 = n_el >> 3;
+    const long long total = (long long)L * T * n8;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (long long)gridDim.x * blockDim.x) {
+        const long long rr = e / n8;
+        const int q = (int)(e - rr * n8);
+        const long long l = rr / T, r = rr - l * T;
+        const uint8_t * s = src + l * src_ls + r * row_bytes;
+        float v[8];
+        if (type == 8) {          // Q8_0: d * q
+            const uint8_t * bl = s + (q >> 2) * 34;
+            const float d = f16_to_f32_ref(load_u16(bl));
+            const uint8_t * qs = bl + 2 + 8 * (q & 3);
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = d * (float)(int8_t)qs[i];
+        } else if (type == 2) {   // Q4_0: d * (nibble - 8), adjacent-pair nibbles
+            const uint8_t * bl = s + (q >> 2) * 18;
+            const float d = f16_to_f32_ref(load_u16(bl));
+            const uint8_t * qs = bl + 2 + 4 * (q & 3);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[2 * i] = d * ((float)(qs[i] & 0xF) - 8.0f);
+                v[2 * i + 1] = d * ((float)(qs[i] >> 4) - 8.0f);
+            }
+        } else if (type == 1) {   // F16
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = f16_to_f32_ref(load_u16(s + 2 * (8 * q + i)));
+        } else if (type == 30) {  // BF16
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = __uint_as_float((uint32_t)load_u16(s + 2 * (8 * q + i)) << 16);
+        } else {                  // F32 (byte-assembled: rows need not be aligned)
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint8_t * b = s + 4 * (8 * q + i);
+                v[i] = __uint_as_float((uint32_t)b[0] | ((uint32_t)b[1] << 8) | ((uint32_t)b[2] << 16) |
+                                       ((uint32_t)b[3] << 24));
+            }
+        }
+        float4 * o = reinterpret_cast<float4 *>(dst + rr * n_el + 8 * q);
+        o[0] = make_float4(v[0], v[1], v[2], v[3]);
+        o[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+}
+
+// Quantize rows (l, j), j < rows, of L layers into codec `type` (row stride
+// row_bytes, layer stride dst_ls bytes). Source row:
+//   mode 0: src + l * src_ls + idx[l * idx_ls + j] * src_ld (kept rows of a cache)
+//   mode 1: the concatenation over heads h of Cv[((l * H + h) * rows + j) * dv ..]
+//           (a refitted value row, api.cpp:1243-1254; dv a multiple of 8)
+__global__ void __launch_bounds__(256)
+k_requant8(const float * __restrict__ src, long long src_ls, long long src_ld, const int * __restrict__ idx,
+           long long idx_ls, int mode, int H, int dv, int type, int n_el, int rows, int L,
+           uint8_t * __restrict__ dst, long long row_bytes, long long dst_ls) {
+    const int n8 = n_el >> 3;
+    const long long total = (long long)L * rows * n8;   // a multiple of 4: quads stay whole
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (long long)gridDim.x * blockDim.x) {
+        const long long rr = e / n8;
+        const int q = (int)(e - rr * n8);
+        const long long l = rr / rows, j = rr - l * rows;
+        const float * x;
+        if (mode == 0) {
+            x = src + l * src_ls + (long long)idx[l * idx_ls + j] * src_ld + 8 * q;
+        } else {
+            const int h = (8 * q) / dv, v = 8 * q - h * dv;
+            x = src + (((l * H + h) * rows + j) * dv + v);
+        }
+        const float4 a = reinterpret_cast<const float4 *>(x)[0], b = reinterpret_cast<const float4 *>(x)[1];
+        const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        uint8_t * o = dst + l * dst_ls + j * row_bytes;
+        if (type == 8 || type == 2) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float t = fabsf(xv[i]);
+                if (t > amax) amax = t;
+            }
+            const float o1 = __shfl_xor(amax, 1);
+            amax = o1 > amax ? o1 : amax;
+            const float o2 = __shfl_xor(amax, 2);
+            amax = o2 > amax ? o2 : amax;
+            const int kq = q & 3;
+            if (type == 8) {
+                uint8_t * ob = o + (q >> 2) * 34;
+                const float d = amax / 127.0f;
+                const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
+                if (kq == 0) {
+                    const uint16_t hv = f32_to_f16_ref(d);
+                    ob[0] = hv & 0xFF;
+                    ob[1] = hv >> 8;
+                }
+                uint16_t * q16 = reinterpret_cast<uint16_t *>(ob + 2 + 8 * kq);   // 2-byte aligned
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint8_t q0 = (uint8_t)(int8_t)roundf(fmax_std(-128.0f, fmin_std(127.0f, xv[2 * i] * id)));
+                    const uint8_t q1 =
+                        (uint8_t)(int8_t)roundf(fmax_std(-128.0f, fmin_std(127.0f, xv[2 * i + 1] * id)));
+                    q16[i] = (uint16_t)(q0 | ((uint16_t)q1 << 8));
+                }
+            } else {
+                uint8_t * ob = o + (q >> 2) * 18;
+                const float d = amax / 7.0f;
+                const float id = (d != 0.0f) ? 7.0f / amax : 0.0f;
+                if (kq == 0) {
+                    const uint16_t hv = f32_to_f16_ref(d);
+                    ob[0] = hv & 0xFF;
+                    ob[1] = hv >> 8;
+                }
+                uint16_t * q16 = reinterpret_cast<uint16_t *>(ob + 2 + 4 * kq);
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    uint8_t by[2];
+#pragma unroll
+                    for (int u = 0; u < 2; u++) {
+                        const float v0 = xv[4 * i + 2 * u] * id + 8.0f;
+                        const float v1 = xv[4 * i + 2 * u + 1] * id + 8.0f;
+                        const uint8_t q0 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v0)));
+                        const uint8_t q1 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v1)));
+                        by[u] = (uint8_t)(q0 | (q1 << 4));
+                    }
+                    q16[i] = (uint16_t)(by[0] | ((uint16_t)by[1] << 8));
+                }
+            }
+        } else if (type == 1 || type == 30) {
+            uint16_t * o16 = reinterpret_cast<uint16_t *>(o) + 8 * q;   // rows of 2-byte elements
+#pragma unroll
+            for (int i = 0; i < 8; i++) o16[i] = type == 1 ? f32_to_f16_ref(xv[i]) : f32_to_bf16(xv[i]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t u = __float_as_uint(xv[i]);
+                uint8_t * b4 = o + 4 * (8 * q + i);
+                b4[0] = u & 0xFF; b4[1] = (u >> 8) & 0xFF; b4[2] = (u >> 16) & 0xFF; b4[3] = u >> 24;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Accelerator plug-in GEMMs (accel ABI), sequential accumulation.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
@@ -4072,6 +4225,27 @@ void launch_quant_rows(const float * src, long long src_ld, const int * idx, int
     const long long nb = (type == 0 || type == 1 || type == 30) ? (long long)n_el : (long long)(n_el / 32);
     hipLaunchKernelGGL(k_quant_rows, dim3(grid_cap(rows * nb, 256)), dim3(256), 0, st,
                        src, src_ld, idx, type, n_el, rows, dst, row_bytes);
+}
+
+bool codec8_ok(int type, int n_el) {
+    if (type == 8 || type == 2) return n_el % 32 == 0;
+    return (type == 0 || type == 1 || type == 30) && n_el % 8 == 0;
+}
+
+void launch_dequant8(const uint8_t * src, int type, long long row_bytes, long long src_ls, int n_el, int T, int L,
+                     float * dst, hipStream_t st) {
+    const long long total = (long long)L * T * (n_el / 8);
+    hipLaunchKernelGGL(k_dequant8, dim3(grid_cap(total, 256)), dim3(256), 0, st,
+                       src, type, row_bytes, src_ls, n_el, T, L, dst);
+}
+
+void launch_requant8(const float * src, long long src_ls, long long src_ld, const int * idx, long long idx_ls,
+                     int mode, int H, int dv, int type, int n_el, int rows, int L, uint8_t * dst, long long row_bytes,
+                     long long dst_ls, hipStream_t st) {
+    const long long total = (long long)L * rows * (n_el / 8);
+    if (total <= 0) return;
+    hipLaunchKernelGGL(k_requant8, dim3(grid_cap(total, 256)), dim3(256), 0, st,
+                       src, src_ls, src_ld, idx, idx_ls, mode, H, dv, type, n_el, rows, L, dst, row_bytes, dst_ls);
 }
 
 void launch_gather_cv_rows(const float * Cv, int H, int t, int dv, float * rows, hipStream_t st) {

@@ -285,6 +285,15 @@ def bind_device_api(dll):
     dll.kvc_compact_layers_device.restype = _i
     dll.kvc_compact_layers_device_noalloc.argtypes = dll.kvc_compact_layers_device.argtypes
     dll.kvc_compact_layers_device_noalloc.restype = _i
+    dll.kvc_compact_quantized_layers_device.argtypes = [_vp, _vp, _vp, _i, _i, _i, ctypes.c_size_t, ctypes.c_size_t,
+                                                        _i, _i, _i, _i, _i, ctypes.c_longlong, ctypes.c_longlong,
+                                                        ctypes.c_longlong, ctypes.POINTER(Params),
+                                                        ctypes.POINTER(DeviceOut), _vp, _vp, _vp]
+    dll.kvc_compact_quantized_layers_device.restype = _i
+    dll.kvc_compact_quantized_device.argtypes = [_vp, _vp, _vp, _i, _i, ctypes.c_size_t, ctypes.c_size_t,
+                                                 _i, _i, _i, _i, _i, ctypes.POINTER(Params),
+                                                 ctypes.POINTER(DeviceOut), _vp, _vp, _vp]
+    dll.kvc_compact_quantized_device.restype = _i
     dll.kvc_stage_times.argtypes = [ctypes.POINTER(ctypes.c_float), _i]
     dll.kvc_stage_times.restype = _i
     dll.kv_compact_hip_available.restype = _i

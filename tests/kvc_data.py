@@ -316,3 +316,55 @@ def nonfinite_variant(name: str):
         K[10, :] = -0.0
     c = dict(name=name, T=T, H=H, d=d, seed=77, params=dict(target_ratio=0.3))
     return c, K, V, Q, 16
+
+
+# ---------------------------------------------------------------------------
+# Vectorized reference-codec quantizers (state.h:508-567) for building large
+# synthetic Q8_0 / Q4_0 caches quickly. test_oracle.py pins them byte for byte
+# against the oracle's row quantizer.
+# ---------------------------------------------------------------------------
+def f32_to_f16_trunc(x: np.ndarray) -> np.ndarray:
+    """The reference's f32 -> f16: mantissa truncated, NaN -> Inf (state.h:508-525)."""
+    f = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.int64)
+    sign = (f >> 16) & 0x8000
+    e = ((f >> 23) & 0xFF) - 127 + 15
+    m = (f >> 13) & 0x3FF
+    sub = np.where(e < -10, 0, ((m | 0x400) >> np.clip(1 - e, 0, 31)))
+    out = np.where(e <= 0, sign | sub, np.where(e >= 31, sign | 0x7C00, sign | (np.clip(e, 0, 31) << 10) | m))
+    return out.astype(np.uint16)
+
+
+def roundf(v: np.ndarray) -> np.ndarray:
+    """C roundf (half away from zero) for float32 values."""
+    r = np.trunc(v)
+    frac = np.abs(v - r)   # exact for |v| < 2^23
+    return (r + np.where(frac >= np.float32(0.5), np.sign(v), 0)).astype(np.float32)
+
+
+def quantize_rows(x: np.ndarray, typ: int) -> np.ndarray:
+    """Rows of float32 (n a multiple of 32) -> reference Q8_0 (typ 8) or Q4_0 (typ 2) bytes."""
+    x = np.ascontiguousarray(x, np.float32)
+    rows, n = x.shape
+    b = x.reshape(rows, n // 32, 32)
+    amax = np.max(np.abs(b), axis=2)   # the blocks here hold no NaN
+    if typ == 8:
+        d = (amax / np.float32(127.0)).astype(np.float32)
+        with np.errstate(divide="ignore"):
+            idv = np.where(d != 0, np.float32(127.0) / amax, np.float32(0.0)).astype(np.float32)
+        v = (b * idv[:, :, None]).astype(np.float32)
+        q = roundf(np.maximum(np.float32(-128.0), np.minimum(np.float32(127.0), v))).astype(np.int8)
+        out = np.empty((rows, n // 32, 34), np.uint8)
+        out[:, :, 0:2] = f32_to_f16_trunc(d).view(np.uint8).reshape(rows, n // 32, 2)
+        out[:, :, 2:] = q.view(np.uint8)
+    elif typ == 2:
+        d = (amax / np.float32(7.0)).astype(np.float32)
+        with np.errstate(divide="ignore"):
+            idv = np.where(d != 0, np.float32(7.0) / amax, np.float32(0.0)).astype(np.float32)
+        v = ((b * idv[:, :, None]).astype(np.float32) + np.float32(8.0)).astype(np.float32)
+        q = np.maximum(np.float32(0.0), np.minimum(np.float32(15.0), roundf(v))).astype(np.uint8)
+        out = np.empty((rows, n // 32, 18), np.uint8)
+        out[:, :, 0:2] = f32_to_f16_trunc(d).view(np.uint8).reshape(rows, n // 32, 2)
+        out[:, :, 2:] = q[:, :, 0::2] | (q[:, :, 1::2] << 4)
+    else:
+        raise ValueError(typ)
+    return out.reshape(rows, -1)

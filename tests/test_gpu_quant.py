@@ -1,0 +1,186 @@
+"""GPU parity of the quantized pipeline (dequantize -> compact -> requantize,
+reference api.cpp:1182-1257) at the Q8_0 / Q4_0 configuration's shape:
+8 KV heads x d = 128, cheap reference queries, keep 0.2, chunked (1280-token
+chunks). Every output, the requantized K and V rows included, must equal the
+oracle's bit for bit, through the host entry (kv_compact_quantized), the
+one-layer device entry and the multi-layer device entry. At the full
+configuration (32 layers x T = 32,768) the multi-layer call is checked by
+size-independent properties, against a one-layer call on the same data, and
+row by row against the reference codec applied to its own outputs.
+Inputs are quantized here from seeded N(0,1) data (kvc_data.quantize_rows,
+which test_oracle.py pins against the oracle's row quantizer).
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+from kvc_data import kv_cache, quantize_rows
+from kvc_harness import kc, load_oracle
+
+pytestmark = pytest.mark.gpu
+
+ROW_BYTES = {8: 34, 2: 18}
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    lib = kc.load_product()
+    if not lib.dll.kv_compact_hip_available():
+        pytest.fail("no usable GPU for the GPU test tier")
+    kc.bind_device_api(lib.dll)
+    return lib
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return load_oracle()
+
+
+def same(a, b):
+    assert a.t == b.t
+    assert np.array_equal(a.indices, b.indices), "indices"
+    assert np.array_equal(bits(a.beta), bits(b.beta)), "beta"
+    assert np.array_equal(bits(a.C_v), bits(b.C_v)), "C_v"
+    for k in ("avg_cosine_sim", "avg_mse", "avg_agreement"):
+        assert np.float32(a.stats[k]).view(np.uint32) == np.float32(b.stats[k]).view(np.uint32), k
+
+
+def dequant_q(rows, typ):
+    """Reference codec decode (state.h:355-375) of Q8_0 / Q4_0 rows, numpy."""
+    nb = rows.shape[1] // ROW_BYTES[typ]
+    bl = rows.reshape(rows.shape[0], nb, ROW_BYTES[typ])
+    d = bl[:, :, 0:2].copy().view(np.float16).astype(np.float32)
+    if typ == 8:
+        q = bl[:, :, 2:].view(np.int8).astype(np.float32)
+    else:
+        by = bl[:, :, 2:]
+        q = np.empty((rows.shape[0], nb, 32), np.float32)
+        q[:, :, 0::2] = (by & 0xF).astype(np.float32) - np.float32(8.0)
+        q[:, :, 1::2] = (by >> 4).astype(np.float32) - np.float32(8.0)
+    return (d * q).astype(np.float32).reshape(rows.shape[0], -1)
+
+
+def device_call(gpu, Kq, Vq, kt, vt, L, T, H, d, p):
+    """kvc_compact_quantized_layers_device on L layers (Kq/Vq [L][T][row bytes])."""
+    import hiprt
+    dll = gpu.dll
+    t, _ = kc.plan(dll, T, 0, False, p)
+    krb, vrb = Kq.shape[-1], Vq.shape[-1]
+    dKq, dVq = hiprt.DevBuf(Kq.nbytes), hiprt.DevBuf(Vq.nbytes)
+    dKq.upload(Kq)
+    dVq.upload(Vq)
+    idx, beta, cv, st = (hiprt.DevBuf(n * 4) for n in (L * t, L * H * t, L * H * t * d, L * 3))
+    ko, vo = hiprt.DevBuf(L * t * krb), hiprt.DevBuf(L * t * vrb)
+    out = kc.DeviceOut(idx.value, beta.value, cv.value, st.value)
+    if L == 1:
+        rc = dll.kvc_compact_quantized_device(dKq.value, dVq.value, None, kt, vt, krb, vrb, T, 0, H, d, d,
+                                              ctypes.byref(p), ctypes.byref(out), ko.value, vo.value, None)
+    else:
+        rc = dll.kvc_compact_quantized_layers_device(dKq.value, dVq.value, None, L, kt, vt, krb, vrb, T, 0, H, d, d,
+                                                     T * krb, T * vrb, 0, ctypes.byref(p), ctypes.byref(out),
+                                                     ko.value, vo.value, None)
+    assert rc == 0
+    return dict(t=t, indices=idx.download(np.int32, L * t).reshape(L, t),
+                beta=beta.download(np.float32, L * H * t).reshape(L, H, t),
+                C_v=cv.download(np.float32, L * H * t * d).reshape(L, H, t, d),
+                stats=st.download(np.float32, L * 3).reshape(L, 3),
+                K_out=ko.download(np.uint8, L * t * krb).reshape(L, t, krb),
+                V_out=vo.download(np.uint8, L * t * vrb).reshape(L, t, vrb))
+
+
+def same_device(dv, l, ref, H, d):
+    t = ref.t
+    assert dv["t"] == t
+    assert np.array_equal(dv["indices"][l], ref.indices), "indices"
+    assert np.array_equal(bits(dv["beta"][l]), bits(np.asarray(ref.beta).reshape(H, t))), "beta"
+    assert np.array_equal(bits(dv["C_v"][l]), bits(np.asarray(ref.C_v).reshape(H, t, d))), "C_v"
+    st = np.array([ref.stats["avg_cosine_sim"], ref.stats["avg_mse"], ref.stats["avg_agreement"]], np.float32)
+    assert np.array_equal(bits(dv["stats"][l]), bits(st)), "stats"
+    assert np.array_equal(dv["K_out"][l], ref.K_out), "K_out"
+    assert np.array_equal(dv["V_out"][l], ref.V_out), "V_out"
+
+
+@pytest.mark.parametrize("kt,vt", [(8, 8), (2, 2), (2, 8)])
+def test_config4_chunked(gpu, orc, kt, vt):
+    """8 heads x d = 128, T = 2560 (two 1280-token chunks), both device entries and the host entry."""
+    T, H, d = 2560, 8, 128
+    print(f"[quant] config-4 shape T={T} k_type={kt} v_type={vt}", flush=True)
+    K, V = kv_cache(T, H, d, 4000 + kt * 10 + vt)
+    Kq, Vq = quantize_rows(K, kt), quantize_rows(V, vt)
+    pk = dict(target_ratio=0.2, use_cheap_qref=1)
+    args = (Kq, Vq, None, kt, vt, Kq.shape[1], Vq.shape[1], T, 0, H, d, d)
+    rb, b = orc.quantized(*args, orc.params(**pk))
+    ra, a = gpu.quantized(*args, gpu.params(**pk))
+    assert ra == 0 and rb == 0
+    same(a, b)
+    assert np.array_equal(a.K_out, b.K_out) and np.array_equal(a.V_out, b.V_out)
+    dv = device_call(gpu, Kq[None], Vq[None], kt, vt, 1, T, H, d, gpu.params(**pk))
+    same_device(dv, 0, b, H, d)
+
+
+def test_quantized_layers_device(gpu, orc):
+    """Three layers (Q4_0 keys, Q8_0 values) in one call: each layer equals the oracle's one-layer result."""
+    L, T, H, d, kt, vt = 3, 2560, 8, 128, 2, 8
+    print(f"[quant] layers L={L} T={T}", flush=True)
+    Kq = np.empty((L, T, H * d // 32 * ROW_BYTES[kt]), np.uint8)
+    Vq = np.empty((L, T, H * d // 32 * ROW_BYTES[vt]), np.uint8)
+    for l in range(L):
+        K, V = kv_cache(T, H, d, 4100 + l)
+        Kq[l], Vq[l] = quantize_rows(K, kt), quantize_rows(V, vt)
+    pk = dict(target_ratio=0.2, use_cheap_qref=1)
+    dv = device_call(gpu, Kq, Vq, kt, vt, L, T, H, d, gpu.params(**pk))
+    for l in range(L):
+        rb, b = orc.quantized(Kq[l], Vq[l], None, kt, vt, Kq.shape[2], Vq.shape[2], T, 0, H, d, d, orc.params(**pk))
+        assert rb == 0
+        same_device(dv, l, b, H, d)
+
+
+@pytest.mark.parametrize("typ", [8, 2])
+def test_config4_full_size(gpu, typ):
+    """32 layers x 8 heads x d = 128, T = 32,768 in one device call (Q8_0 or Q4_0 keys and values)."""
+    L, T, H, d = 32, 32768, 8, 128
+    E = H * d
+    print(f"[quant] full configuration L={L} T={T} type={typ}", flush=True)
+    r = np.random.default_rng(4200 + typ)
+    pool = quantize_rows(r.standard_normal((T + 4096, E), dtype=np.float32), typ)
+    rb = pool.shape[1]
+    Kq = np.empty((L, T, rb), np.uint8)
+    Vq = np.empty((L, T, rb), np.uint8)
+    for l in range(L):
+        o1, o2 = (int(x) for x in r.integers(0, 4096, size=2))
+        Kq[l] = pool[o1:o1 + T]
+        Vq[l] = pool[o2:o2 + T]
+    p = gpu.params(target_ratio=0.2, use_cheap_qref=1)
+    dv = device_call(gpu, Kq, Vq, typ, typ, L, T, H, d, p)
+    t = dv["t"]
+    assert t == 25 * 256 + 153
+    per_chunk = np.full(26, 256)
+    per_chunk[-1] = 153
+    for l in range(L):
+        ix = dv["indices"][l]
+        assert np.all(np.diff(ix) > 0) and ix[0] >= 0 and ix[-1] < T
+        assert np.array_equal(np.bincount(ix // 1280, minlength=26), per_chunk)
+        s = dv["stats"][l]
+        assert 0.0 < s[0] <= 1.0 + 1e-6 and s[1] >= 0.0 and 0.0 <= s[2] <= 1.0
+    assert np.all(dv["beta"] == 0.0) and np.all(np.isfinite(dv["C_v"]))
+    # layer 0 alone gives the same outputs
+    d1 = device_call(gpu, Kq[:1], Vq[:1], typ, typ, 1, T, H, d, p)
+    for k in ("indices", "K_out", "V_out"):
+        assert np.array_equal(d1[k][0], dv[k][0]), k
+    for k in ("beta", "C_v", "stats"):
+        assert np.array_equal(bits(d1[k][0]), bits(dv[k][0])), k
+    # requantized rows: the reference codec of the kept dequantized K rows and
+    # of the refitted value rows (sampled rows of two layers)
+    for l in (0, L - 1):
+        j = np.unique(r.integers(0, t, size=64))
+        kept = dequant_q(Kq[l][dv["indices"][l][j]], typ)
+        assert np.array_equal(quantize_rows(kept, typ), dv["K_out"][l][j])
+        vrows = dv["C_v"][l][:, j, :].transpose(1, 0, 2).reshape(len(j), E)
+        assert np.array_equal(quantize_rows(vrows, typ), dv["V_out"][l][j])

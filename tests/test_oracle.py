@@ -405,3 +405,18 @@ def test_error_codes(orc):
     x = np.ones(4, np.float32)
     assert orc.compact_raw(x, x, x, 0, 1, 1, 1, 1, None)[0] == -2
     assert orc.compact_raw(x, x, x, 1, 0, 1, 1, 1, None)[0] == -2
+
+
+def test_numpy_quantizers_match_oracle(orc):
+    """kvc_data.quantize_rows (used to build large Q8_0 / Q4_0 caches) equals the
+    oracle's row quantizer byte for byte, zeros, -0 and tiny/huge scales included."""
+    from kvc_data import normal, quantize_rows
+    for typ in (8, 2):
+        for s in range(4):
+            x = (normal(500 + s, (48, 256)) * np.float32(10.0 ** (2 * s - 4))).astype(np.float32)
+            x[3, :32] = 0.0
+            x[5, 40] = -0.0
+            x[7, 64:96] = np.float32(1e-30)
+            a = quantize_rows(x, typ)
+            b = np.stack([orc.quantize_row(x[i], typ) for i in range(x.shape[0])])
+            assert np.array_equal(a, b), (typ, s)
