@@ -41,15 +41,20 @@ sys.path.insert(0, str(REPO / "kv-compact_amd"))
 import kvcompact as kc  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
-FP32_PEAK_TFLOPS = 157.3       # MI355X fp32
+FP32_PEAK_TFLOPS = 157.3       # MI355X fp32 (published)
+# fp32 multiply and add issued separately on the vector ALUs (the reference's
+# rounding: no FMA, no packed fp32), two or more waves per SIMD: 256 CUs x 4
+# SIMDs x 32 lanes x 2.4 GHz, measured with s_memtime microbenchmarks
+VALU_CEILING_TOPS = 78.6
 STAGES = ["scores", "chunk_softmax_importance", "refit_target", "selection", "beta_fit", "compacted_softmax",
           "normal_equations", "lu_factorization", "substitution", "refinement", "quality_stats"]
+QSTAGES = STAGES + ["dequantize", "requantize"]
 STAGE_KERNELS = {"scores": "k_scores", "chunk_softmax_importance": "k_softmax_importance",
                  "refit_target": "k_refit_target",
                  "selection": "k_global_importance + k_select_topk (or k_div_candidates + k_div_gram + k_div_greedy)",
                  "beta_fit": "k_gather_exp + k_ls_build + k_ge_lu + k_ge_solve (or k_nnls_lh) + k_beta_log",
                  "compacted_softmax": "k_ls_softmax", "normal_equations": "k_ls_build",
-                 "lu_factorization": "k_ge_lu", "substitution": "k_ge_solve",
+                 "lu_factorization": "k_ge_lu", "substitution": "k_ge_subst",
                  "refinement": "k_refine_step + the beta and C_v refit per round",
                  "quality_stats": "k_scores + k_row_softmax + k_stats_sum + k_stats_final"}
 
@@ -109,14 +114,51 @@ def roofline(name, model, ms):
     t_cmp = f / (FP32_PEAK_TFLOPS * 1e12)
     s = ms / 1e3
     if t_cmp > t_hbm:
+        # fp32 arithmetic on the vector ALUs in the reference's operation
+        # order (no MFMA: a reordered or fused sum would change the results)
         ach = f / s / 1e12
-        return dict(kernel=STAGE_KERNELS[name], stage=name, bound="mfma", achieved=round(ach, 3), peak=FP32_PEAK_TFLOPS, unit="TFLOP/s",
-                    frac=round(ach / FP32_PEAK_TFLOPS, 4), traffic=None, ms=round(ms, 3),
+        return dict(kernel=STAGE_KERNELS[name], stage=name, bound="valu", achieved=round(ach, 3), peak=FP32_PEAK_TFLOPS,
+                    unit="TFLOP/s", frac=round(ach / FP32_PEAK_TFLOPS, 4), traffic=None, ms=round(ms, 3),
+                    valu_ceiling=VALU_CEILING_TOPS, frac_of_valu_ceiling=round(ach / VALU_CEILING_TOPS, 4),
                     algorithmic_flops=f, algorithmic_bytes=b)
     ach = b / s / 1e9
     return dict(kernel=STAGE_KERNELS[name], stage=name, bound="hbm", achieved=round(ach, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                 frac=round(ach / HBM_PEAK_GBS, 4), traffic=None, ms=round(ms, 3),
                 algorithmic_flops=f, algorithmic_bytes=b)
+
+
+def host_info() -> dict:
+    """Device and host descriptions for the record, as the box's own tools
+    print them (rocminfo and rocm-smi run as their own processes)."""
+    import subprocess
+    arch, model = "", ""
+    try:
+        out = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=60).stdout
+        for line in out.splitlines():
+            t = line.strip()
+            if t.startswith("Name:") and "gfx" in t and not arch:
+                arch = t.split(":", 1)[1].strip()
+    except Exception:  # noqa: BLE001
+        pass
+    try:
+        out = subprocess.run(["rocm-smi", "--showproductname"], capture_output=True, text=True, timeout=60).stdout
+        for line in out.splitlines():
+            if "Card Model:" in line:
+                model = line.split("Card Model:", 1)[1].strip()
+                break
+    except Exception:  # noqa: BLE001
+        pass
+    cpu = ""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    dev = f"AMD Instinct {arch}" + (f" (PCI device {model})" if model else "")
+    return {"device": dev, "cpu_model": cpu, "host_cpus": os.cpu_count(),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS", "")}
 
 
 def cpu_baseline(K, V, Q, T, H, d, ratio, L_total, diversity):
@@ -133,6 +175,8 @@ def cpu_baseline(K, V, Q, T, H, d, ratio, L_total, diversity):
     r = lib.compact(K, V, Q, T, Q.shape[0], H, d, d, p)
     dt = time.perf_counter() - t0
     per_layer = dt
+    if r is None:
+        raise RuntimeError("CPU baseline call failed")
     return dict(value=round(T / (per_layer * L_total), 2), unit="tok/s", cores=threads, kind=kind,
                 sample=f"layer 0 of {L_total} at full T={T} ({dt:.1f} s, all-layer rate = T/(time*{L_total}))",
                 seconds=round(dt, 2), kept=r.t, cos=r.stats["avg_cosine_sim"])
@@ -175,6 +219,118 @@ def summarize_pmc(d: Path) -> dict:
     return out
 
 
+def config1_point(lib, seed):
+    """The single-head configuration (T = 4096, d = 128, four outlier channels
+    x8, cheap reference queries, keep 0.5): the GPU library through the host
+    entry point, and the reference CPU path on one thread and on every core."""
+    sys.path.insert(0, str(REPO / "tests"))
+    from kvc_data import kv_cache
+    T, H, d = 4096, 1, 128
+    K, V = kv_cache(T, H, d, seed, outliers=4)
+    out = {"workload": "1 layer x 1 KV head x d=128, T=4096, fp32, 4 outlier channels x8, cheap Q_ref, keep 0.5"}
+    p = lib.params(target_ratio=0.5, use_cheap_qref=1)
+    lib.compact(K, V, None, T, 0, H, d, d, p)   # warm
+    ts = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        lib.compact(K, V, None, T, 0, H, d, d, p)
+        ts.append(time.perf_counter() - t0)
+    out["gpu_host_entry_tok_s"] = round(T / float(np.median(ts)), 1)
+    ref = REPO / "oracle" / "_ref" / "libkvref.so"
+    if ref.exists():
+        rl = kc.Lib(ref)
+        for threads in (1, 0):
+            pr = rl.params(target_ratio=0.5, use_cheap_qref=1, n_threads=threads)
+            ts = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                rl.compact(K, V, None, T, 0, H, d, d, pr)
+                ts.append(time.perf_counter() - t0)
+            key = "cpu_reference_1_thread_tok_s" if threads == 1 else "cpu_reference_all_threads_tok_s"
+            out[key] = round(T / float(np.median(ts)), 1)
+    return out
+
+
+def drop_in_mode(lib, L, T, H, d, W, ratio, diversity, seed):
+    """Drop-in mode: the reference's own host-pointer kv_compact() once per
+    layer (host buffers in, malloc'd results out), every layer of the
+    workload; the time counts the calls only (data generation excluded)."""
+    p = lib.params(target_ratio=ratio, use_diversity=diversity)
+    total = 0.0
+    for l, (K, V, Q) in enumerate(gen_layers(L, T, H, d, W, seed)):
+        t0 = time.perf_counter()
+        r = lib.compact(K, V, Q, T, W, H, d, d, p)
+        total += time.perf_counter() - t0
+        if r is None:
+            raise RuntimeError("kv_compact failed")
+    bytes_in = 2 * L * T * H * d * 4
+    return {"value": round(T / total, 1), "unit": "tok/s", "seconds": round(total, 3),
+            "host_to_device_gb": round(bytes_in / 1e9, 2),
+            "host_link_bound_tok_s": round(T / (bytes_in / 64e9), 1),
+            "note": f"{L} kv_compact calls with pageable host buffers (one layer each), results copied back"}
+
+
+def quantized_mode(dll, lib, hiprt, L, T, H, d, ratio, steps, warmup, seed):
+    """Q8_0 and Q4_0 caches of N(0,1) data: the multi-layer quantized device
+    entry (dequantize, compact, requantize) on all layers, inputs resident."""
+    sys.path.insert(0, str(REPO / "tests"))
+    from kvc_data import quantize_rows
+    E = H * d
+    p = lib.params(target_ratio=ratio, use_cheap_qref=1)
+    t, n_chunks = kc.plan(dll, T, 0, False, p)
+    res = {"workload": f"{L} layers x {H} KV heads x d={d}, T={T}, keep {ratio:g} (t={t}/layer, {n_chunks} chunks), "
+                       f"cheap Q_ref, K and V in the codec"}
+    rng = np.random.default_rng(seed)
+    for typ, name in ((8, "q8_0"), (2, "q4_0")):
+        pool = quantize_rows(rng.standard_normal((T + 4096, E), dtype=np.float32), typ)
+        rb = pool.shape[1]
+        dKq, dVq = hiprt.DevBuf(L * T * rb), hiprt.DevBuf(L * T * rb)
+        for l in range(L):
+            o1, o2 = (int(x) for x in rng.integers(0, 4096, size=2))
+            dKq.upload(pool[o1:o1 + T], l * T * rb)
+            dVq.upload(pool[o2:o2 + T], l * T * rb)
+        bufs = [hiprt.DevBuf(n * 4) for n in (L * t, L * H * t, L * H * t * d, L * 3)]
+        ko, vo = hiprt.DevBuf(L * t * rb), hiprt.DevBuf(L * t * rb)
+        out = kc.DeviceOut(*(b.value for b in bufs))
+
+        def step():
+            rc = dll.kvc_compact_quantized_layers_device(dKq.value, dVq.value, None, L, typ, typ, rb, rb, T, 0, H, d,
+                                                         d, T * rb, T * rb, 0, ctypes.byref(p), ctypes.byref(out),
+                                                         ko.value, vo.value, None)
+            if rc != 0:
+                raise RuntimeError(f"kvc_compact_quantized_layers_device returned {rc}")
+        for _ in range(warmup):
+            step()
+        hiprt.synchronize()
+        acc = np.zeros(len(QSTAGES))
+        buf = (ctypes.c_float * len(QSTAGES))()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+            dll.kvc_stage_times(buf, len(QSTAGES))
+            acc += np.array(buf[:])
+        hiprt.synchronize()
+        ms = (time.perf_counter() - t0) / steps * 1e3
+        acc /= steps
+        dq_bytes = 2 * L * T * (rb + E * 4)                     # read the rows, write fp32
+        rq_bytes = 2 * L * t * (E * 4 + rb)                     # read kept K rows and C_v, write the rows
+        st = dict(zip(QSTAGES, acc))
+        res[name] = {"value": round(T / (ms / 1e3), 1), "unit": "tok/s", "ms_per_step": round(ms, 3),
+                     "row_bytes": rb,
+                     "stage_ms": {k: round(float(v), 3) for k, v in st.items()},
+                     "dequantize_gb_s": round(dq_bytes / (st["dequantize"] / 1e3) / 1e9, 1) if st["dequantize"] else None,
+                     "dequantize_frac_hbm": round(dq_bytes / (st["dequantize"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
+                     if st["dequantize"] else None,
+                     "requantize_gb_s": round(rq_bytes / (st["requantize"] / 1e3) / 1e9, 1) if st["requantize"] else None,
+                     "requantize_frac_hbm": round(rq_bytes / (st["requantize"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
+                     if st["requantize"] else None,
+                     "dequantize_bytes": dq_bytes, "requantize_bytes": rq_bytes}
+        print(f"[bench] quantized {name}: {ms:.1f} ms per step, dequantize {st['dequantize']:.2f} ms, "
+              f"requantize {st['requantize']:.2f} ms", file=sys.stderr, flush=True)
+        del dKq, dVq, bufs, ko, vo
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -191,6 +347,8 @@ def main():
                          "timed after it and reported under 'other_mode'")
     ap.add_argument("--one-mode", action="store_true", help="time only the --diversity mode")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the extra records (config-1 point, drop-in mode, quantized caches)")
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--summarize-pmc", metavar="DIR", default="",
                     help="summarise rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE csv runs under DIR "
@@ -296,6 +454,15 @@ def main():
             roof["traffic"] = kern["hbm_bytes"]
             roof["traffic_source"] = str(prof.relative_to(REPO))
     stats = st.download(np.float32, L * 3).reshape(L, 3)
+    del dK, dV, dQ, idx, beta, cv, st
+
+    extras = {}
+    if not a.no_extras:
+        extras["quantized"] = quantized_mode(dll, lib, hiprt, 32, 32768, H, d, a.ratio, a.steps, a.warmup, a.seed + 7)
+        extras["drop_in_host_pointers"] = drop_in_mode(lib, L, T, H, d, W, a.ratio, a.diversity, a.seed)
+        print(f"[bench] drop-in mode: {extras['drop_in_host_pointers']}", file=sys.stderr, flush=True)
+        extras["config1"] = config1_point(lib, 101)
+        print(f"[bench] config 1: {extras['config1']}", file=sys.stderr, flush=True)
 
     cpu = None
     if not a.no_cpu:
@@ -321,7 +488,7 @@ def main():
                         f"(t={t}/layer, {n_chunks} chunks), SnapKV W={W}, RMS, skip_beta=1, "
                         f"diversity={'on' if a.diversity else 'off'}",
             "layers": L, "T": T, "kv_heads": H, "head_dim": d, "keep_ratio": a.ratio, "kept_per_layer": t,
-            "parallelism": "single GPU", "device": hiprt.device_name(),
+            "parallelism": "single GPU", **host_info(),
         },
         "stage_ms": {k: round(float(v), 3) for k, v in zip(STAGES, stage_ms)},
         "other_mode": other,
@@ -329,6 +496,7 @@ def main():
         "cpu_baseline": cpu,
         "speedup_vs_cpu": round((T / (ms / 1e3)) / cpu["value"], 1) if cpu else None,
         "quality": {"avg_cosine_sim_layer0": float(stats[0, 0]), "avg_cosine_sim_min": float(stats[:, 0].min())},
+        **extras,
     }
     print(json.dumps(line), flush=True)
 

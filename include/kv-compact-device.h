@@ -90,7 +90,10 @@ int kvc_compact_quantized_device(const uint8_t * K_quant, const uint8_t * V_quan
  * 0 scores, 1 chunk softmax + importance, 2 refit target Y = A V,
  * 3 selection, 4 beta fit, 5 compacted softmax X, 6 normal equations,
  * 7 LU elimination with partial pivoting, 8 forward + back substitution,
- * 9 refinement rounds, 10 quality statistics. Returns the number written. */
+ * 9 refinement rounds, 10 quality statistics, and for the quantized entries
+ * 11 dequantization of the K and V rows, 12 requantization of the kept K
+ * rows and refitted V rows (0 after an unquantized call). Returns the number
+ * written. */
 int kvc_stage_times(float * out_ms, int n);
 
 /* Release the library's cached device workspace of the current device. */

@@ -36,7 +36,9 @@ namespace {
 
 // Pipeline stages timed with events on the call's stream (kvc_stage_times)
 enum Stage { ST_SCORES, ST_SOFTMAX, ST_REFIT, ST_SELECT, ST_BETA, ST_LS_SOFTMAX, ST_LS_BUILD, ST_LU, ST_SOLVE,
-             ST_REFINE, ST_STATS, ST_COUNT };
+             ST_REFINE, ST_STATS, ST_BATCH_END,
+             // the quantized entries' codec phases, around the batch
+             ST_DEQUANT = ST_BATCH_END, ST_REQUANT, ST_COUNT };
 
 // Fixed workspace of kvc_compact_layers_device_noalloc, one copy per GPU
 // (each device that loads the library holds it until the process ends). Host
@@ -59,7 +61,8 @@ struct DeviceCtx {
     hipEvent_t refit_t[2] = {};   // timing of the refit target on the second stream
     char * arena = nullptr;
     size_t arena_cap = 0;
-    hipEvent_t ev[ST_COUNT + 1] = {};
+    hipEvent_t ev[ST_BATCH_END + 1] = {};
+    hipEvent_t q_ev[4] = {};      // dequantization and requantization phases
     float stage_ms[ST_COUNT] = {};
 };
 
@@ -101,8 +104,10 @@ DeviceCtx * device_ctx() {
         if (hipEventCreateWithFlags(&c->refit_join, hipEventDisableTiming) != hipSuccess) return nullptr;
         for (int i = 0; i < 2; i++)
             if (hipEventCreate(&c->refit_t[i]) != hipSuccess) return nullptr;
-        for (int i = 0; i <= ST_COUNT; i++)
+        for (int i = 0; i <= ST_BATCH_END; i++)
             if (hipEventCreate(&c->ev[i]) != hipSuccess) return nullptr;
+        for (int i = 0; i < 4; i++)
+            if (hipEventCreate(&c->q_ev[i]) != hipSuccess) return nullptr;
         void * sp = nullptr;
         if (hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) == hipSuccess) {
             c->scratch = static_cast<char *>(sp);
@@ -614,11 +619,12 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         return KV_COMPACT_E_DEVICE;
     }
     if (status) return KV_COMPACT_E_UNSUPPORTED;
-    for (int i = 0; i < ST_COUNT; i++) {
+    for (int i = 0; i < ST_BATCH_END; i++) {
         float ms = 0.0f;
         (void)hipEventElapsedTime(&ms, ev[i], ev[i + 1]);
         ctx->stage_ms[i] = ms;
     }
+    ctx->stage_ms[ST_DEQUANT] = ctx->stage_ms[ST_REQUANT] = 0.0f;
     if (refit_fork) {
         // the refit target's own time on the second stream (it overlaps the selection)
         float ms = 0.0f;
@@ -790,6 +796,15 @@ struct QuantIO {
     uint8_t * Kout = nullptr;   // [L][t][k_rb]
     uint8_t * Vout = nullptr;   // [L][t][v_rb]
 };
+
+// times of the dequantization and requantization phases of the last quantized call
+void record_codec_times(DeviceCtx * ctx) {
+    float a = 0.0f, b = 0.0f;
+    (void)hipEventElapsedTime(&a, ctx->q_ev[0], ctx->q_ev[1]);
+    (void)hipEventElapsedTime(&b, ctx->q_ev[2], ctx->q_ev[3]);
+    ctx->stage_ms[ST_DEQUANT] = a;
+    ctx->stage_ms[ST_REQUANT] = b;
+}
 
 // rows [L][T] of a codec into fp32 [L][T][n_el]
 void dequant_cache(const uint8_t * src, int type, size_t rb, long long ls, int n_el, int T, int L, float * dst,
@@ -1161,13 +1176,17 @@ int kv_compact_quantized(const uint8_t * K_quant, const uint8_t * V_quant, const
     if (e == hipSuccess && dQ) e = hipMemcpyAsync(dQ, Q_ref_all, (size_t)n_q * ek * 4, hipMemcpyHostToDevice, st);
     if (e == hipSuccess && dW) e = hipMemcpyAsync(dW, wts.data(), (size_t)T * 4, hipMemcpyHostToDevice, st);
     if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
+    (void)hipEventRecord(ctx->q_ev[0], st);
     dequant_cache(dKq, k_type, k_row_bytes, qi.lsKq, ek, T, 1, dK, st);
     dequant_cache(dVq, v_type, v_row_bytes, qi.lsVq, ev, T, 1, dV, st);
+    (void)hipEventRecord(ctx->q_ev[1], st);
     io.K = dK; io.V = dV; io.Q = use_q ? (qd ? Q_ref_all : dQ) : nullptr; io.wts = dW;
     Timing tm;
     rc = run_batch(ctx, st, pl, p, io, cv, &tm);
     if (rc != 0) return rc;
+    (void)hipEventRecord(ctx->q_ev[2], st);
     requant_outputs(qi, dK, io.indices, io.Cv, 1, T, t, H, d_k, d_v, tmp, st);
+    (void)hipEventRecord(ctx->q_ev[3], st);
     std::vector<int> idx(t);
     std::vector<float> beta((size_t)H * t), cvh((size_t)H * t * d_v);
     float stats[3];
@@ -1183,6 +1202,7 @@ int kv_compact_quantized(const uint8_t * K_quant, const uint8_t * V_quant, const
     if (e == hipSuccess && t > 0)
         e = hipMemcpyAsync(result->V_out, qi.Vout, (size_t)t * v_row_bytes, hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e == hipSuccess) record_codec_times(ctx);
     if (e != hipSuccess) {
         free(result->K_out);
         free(result->V_out);
@@ -1437,14 +1457,19 @@ int kvc_compact_quantized_layers_device(const uint8_t * K_quant, const uint8_t *
     carve(cv, dK, dV, dW, tmp);
     if (dW && hipMemcpyAsync(dW, wts.data(), (size_t)T * 4, hipMemcpyHostToDevice, st) != hipSuccess)
         return KV_COMPACT_E_DEVICE;
+    (void)hipEventRecord(ctx->q_ev[0], st);
     dequant_cache(K_quant, k_type, k_row_bytes, ldKq, ek, T, L, dK, st);
     dequant_cache(V_quant, v_type, v_row_bytes, ldVq, ev, T, L, dV, st);
+    (void)hipEventRecord(ctx->q_ev[1], st);
     io.K = dK; io.V = dV; io.wts = dW;
     rc = run_batch(ctx, st, pl, p, io, cv, nullptr);
     if (rc != 0) return rc;
+    (void)hipEventRecord(ctx->q_ev[2], st);
     requant_outputs(qi, dK, io.indices, io.Cv, L, T, t, H, d_k, d_v, tmp, st);
+    (void)hipEventRecord(ctx->q_ev[3], st);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (e == hipSuccess) record_codec_times(ctx);
     return e == hipSuccess ? 0 : KV_COMPACT_E_DEVICE;
 }
 
