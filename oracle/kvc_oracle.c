@@ -358,9 +358,10 @@ static void gram_and_rhs(const float * A, const float * b, int m, int n, float *
     }
 }
 
-/* clamped unconstrained LS (default NNLS method with 0 PGD iterations),
- * math.h:683-752 */
-void orc_nnls_clamped(const float * A, const float * b, float * w, int m, int n, float eps) {
+/* the default NNLS method, math.h:683-806: clamped unconstrained LS (GE with
+ * a 1e-10 ridge, skipped pivots give eps), then `iters` projected-gradient
+ * steps of size 1 / L, L = u^T (A^T A) u after three power-iteration steps */
+void orc_nnls_pgd(const float * A, const float * b, float * w, int m, int n, float eps, int iters) {
     float * AtA = (float *)malloc((size_t)n * n * sizeof(float));
     float * Atb = (float *)malloc((size_t)n * sizeof(float));
     gram_and_rhs(A, b, m, n, AtA, Atb);
@@ -372,7 +373,162 @@ void orc_nnls_clamped(const float * A, const float * b, float * w, int m, int n,
     }
     ge_solve(aug, n, 1, w, eps);
     for (int i = 0; i < n; i++) if (w[i] < eps) w[i] = eps;
-    free(aug); free(AtA); free(Atb);
+    free(aug);
+    if (iters > 0) {
+        float * u = (float *)malloc((size_t)n * sizeof(float));
+        float * v = (float *)malloc((size_t)(m > 0 ? m : 1) * sizeof(float));
+        float * grad = (float *)malloc((size_t)n * sizeof(float));
+        for (int i = 0; i < n; i++) u[i] = 1.0f / sqrtf((float)n);
+        for (int pw = 0; pw < 3; pw++) {
+            for (int i = 0; i < m; i++) {
+                float acc = 0.0f;
+                for (int j = 0; j < n; j++) acc += A[(size_t)i * n + j] * u[j];
+                v[i] = acc;
+            }
+            float vn = 0.0f;
+            for (int i = 0; i < m; i++) vn += v[i] * v[i];
+            vn = sqrtf(vn);
+            if (vn < 1e-12f) break;
+            for (int i = 0; i < m; i++) v[i] /= vn;
+            for (int j = 0; j < n; j++) {
+                float acc = 0.0f;
+                for (int i = 0; i < m; i++) acc += A[(size_t)i * n + j] * v[i];
+                u[j] = acc;
+            }
+            float un = 0.0f;
+            for (int j = 0; j < n; j++) un += u[j] * u[j];
+            un = sqrtf(un);
+            if (un < 1e-12f) break;
+            for (int j = 0; j < n; j++) u[j] /= un;
+        }
+        float L = 0.0f;
+        for (int i = 0; i < n; i++) {
+            float acc = 0.0f;
+            for (int j = 0; j < n; j++) acc += AtA[(size_t)i * n + j] * u[j];
+            L += u[i] * acc;
+        }
+        if (L < 1e-6f) L = 1e-6f;
+        const float eta = 1.0f / L;
+        for (int it = 0; it < iters; it++) {
+            for (int i = 0; i < n; i++) {
+                float acc = 0.0f;
+                for (int j = 0; j < n; j++) acc += AtA[(size_t)i * n + j] * w[j];
+                grad[i] = acc - Atb[i];
+            }
+            for (int i = 0; i < n; i++) {
+                w[i] -= eta * grad[i];
+                if (w[i] < eps) w[i] = eps;
+            }
+        }
+        free(u); free(v); free(grad);
+    }
+    free(AtA); free(Atb);
+}
+
+void orc_nnls_clamped(const float * A, const float * b, float * w, int m, int n, float eps) {
+    orc_nnls_pgd(A, b, w, m, n, eps, 0);
+}
+
+/* sensitivity of one head, math.h:579-594: largest over keys of the largest
+ * weight over queries, over its mean */
+float orc_head_sensitivity(const float * attn, int n_q, int T) {
+    float sum_imp = 0.0f, max_imp = 0.0f;
+    for (int j = 0; j < T; j++) {
+        float max_w = 0.0f;
+        for (int qi = 0; qi < n_q; qi++) {
+            const float w = attn[(size_t)qi * T + j];
+            if (w > max_w) max_w = w;
+        }
+        sum_imp += max_w;
+        if (max_w > max_imp) max_imp = max_w;
+    }
+    const float mean_imp = sum_imp / (float)T;
+    return max_imp / (mean_imp + 1e-12f);
+}
+
+static int cmp_sel_pair(const void * a, const void * b) {
+    const int x = ((const int *)a)[0], y = ((const int *)b)[0];
+    return (x > y) - (x < y);
+}
+
+/* OMP key selection, math.h:832-950: greedy picks by correlation with the
+ * mass residual, NNLS refit (orc_nnls_pgd) every refit_interval iterations;
+ * out sorted ascending with its weights; fewer than t picks are padded with
+ * index 0 / weight 1e-12 */
+void orc_omp_select(const float * E, const float * rs, int T, int n_q, int t, int * sel_out, float * w_out,
+                    int k_choice, int refit_interval, int nnls_iters) {
+    unsigned char * mask = (unsigned char *)calloc((size_t)T, 1);
+    float * cur = (float *)calloc((size_t)(n_q > 0 ? n_q : 1), sizeof(float));
+    float * res = (float *)malloc((size_t)(n_q > 0 ? n_q : 1) * sizeof(float));
+    float * corr = (float *)malloc((size_t)T * sizeof(float));
+    int * order = (int *)malloc((size_t)(t > 0 ? t : 1) * sizeof(int));
+    float * prev_w = (float *)malloc((size_t)(t > 0 ? t : 1) * sizeof(float));
+    float * M = (float *)malloc((size_t)(n_q > 0 ? n_q : 1) * (t > 0 ? t : 1) * sizeof(float));
+    float * w = (float *)malloc((size_t)(t > 0 ? t : 1) * sizeof(float));
+    int ns = 0, n_prev = 0, iteration = 0;
+    while (ns < t) {
+        for (int i = 0; i < n_q; i++) res[i] = rs[i] - cur[i];
+        for (int j = 0; j < T; j++) {
+            corr[j] = 0.0f;
+            if (mask[j]) continue;
+            float c = 0.0f;
+            for (int i = 0; i < n_q; i++) c += E[(size_t)i * T + j] * res[i];
+            corr[j] = c;
+        }
+        const int remaining = t - ns;
+        int k_sel = k_choice < remaining ? k_choice : remaining;
+        const int available = T - ns;
+        if (k_sel > available) k_sel = available;
+        if (k_sel <= 0) break;
+        for (int k = 0; k < k_sel; k++) {
+            int best = -1;
+            float best_c = -1e30f;
+            for (int j = 0; j < T; j++) {
+                if (mask[j]) continue;
+                if (corr[j] > best_c) { best_c = corr[j]; best = j; }
+            }
+            if (best < 0) break;
+            order[ns++] = best;
+            mask[best] = 1;
+            corr[best] = -1e30f;
+        }
+        const int ct = ns;
+        const int solve = (refit_interval <= 1) || (iteration % refit_interval == 0) || (ct == t);
+        if (solve) {
+            for (int i = 0; i < n_q; i++)
+                for (int j = 0; j < ct; j++) M[(size_t)i * ct + j] = E[(size_t)i * T + order[j]];
+            orc_nnls_pgd(M, rs, w, n_q, ct, 1e-12f, nnls_iters);
+            for (int j = 0; j < ct; j++) prev_w[j] = w[j];
+            n_prev = ct;
+            for (int i = 0; i < n_q; i++) {
+                float acc = 0.0f;
+                for (int j = 0; j < ct; j++) acc += M[(size_t)i * ct + j] * w[j];
+                cur[i] = acc;
+            }
+        } else {
+            for (int j = n_prev; j < ct; j++) prev_w[j] = 1e-12f;
+            n_prev = ct;
+            for (int i = 0; i < n_q; i++) {
+                float acc = 0.0f;
+                for (int j = 0; j < ct; j++) acc += E[(size_t)i * T + order[j]] * prev_w[j];
+                cur[i] = acc;
+            }
+        }
+        iteration++;
+    }
+    /* sort by index, weights along (indices are distinct: a stable order is not needed) */
+    int * pairs = (int *)malloc((size_t)(ns > 0 ? ns : 1) * 2 * sizeof(int));
+    for (int j = 0; j < ns; j++) { pairs[2 * j] = order[j]; pairs[2 * j + 1] = j; }
+    qsort(pairs, (size_t)ns, 2 * sizeof(int), cmp_sel_pair);
+    for (int j = 0; j < ns; j++) {
+        sel_out[j] = pairs[2 * j];
+        if (w_out) w_out[j] = pairs[2 * j + 1] < n_prev ? prev_w[pairs[2 * j + 1]] : 1e-12f;
+    }
+    for (int j = ns; j < t; j++) {
+        sel_out[j] = 0;
+        if (w_out) w_out[j] = 1e-12f;
+    }
+    free(pairs); free(mask); free(cur); free(res); free(corr); free(order); free(prev_w); free(M); free(w);
 }
 
 /* Lawson-Hanson active set, math.h:283-452 */
@@ -586,7 +742,7 @@ static void solve_beta(const float * expS, const float * row_sums, const int * s
     for (int qi = 0; qi < n_q; qi++)
         for (int j = 0; j < t; j++) M[(size_t)qi * t + j] = expS[(size_t)qi * T + sel[j]];
     if (p->nnls_method == 0) orc_nnls_lh(M, row_sums, w, n_q, t, p->nnls_max_iter);
-    else orc_nnls_clamped(M, row_sums, w, n_q, t, 1e-12f);
+    else orc_nnls_pgd(M, row_sums, w, n_q, t, 1e-12f, p->nnls_pgd_iters);
     for (int j = 0; j < t; j++) {
         float v = (1e-12f < w[j]) ? w[j] : 1e-12f;   /* std::max(1e-12f, w) */
         beta[j] = logf(v);
@@ -612,21 +768,28 @@ static int compact_body(const float * K, const float * V, const float * Q, int T
     double t0 = now_ms();
     const int ek = H * d_k, ev = H * d_v;
     const float inv_sqrt = 1.0f / sqrtf((float)d_k);
-    const int need_exp = !p->skip_beta;
+    const int need_exp = !p->skip_beta || p->use_omp;   /* OMP reads the exp scores (api.cpp:634-643) */
     float * S = (float *)malloc((size_t)H * n_q * T * sizeof(float));
     float * A = (float *)malloc((size_t)H * n_q * T * sizeof(float));
     float * E = need_exp ? (float *)malloc((size_t)H * n_q * T * sizeof(float)) : NULL;
     float * RS = need_exp ? (float *)malloc((size_t)H * n_q * sizeof(float)) : NULL;
     float * gimp = (float *)calloc((size_t)T, sizeof(float));
-    float * himp = (float *)malloc((size_t)T * sizeof(float));
+    float * himp = (float *)malloc((size_t)T * H * sizeof(float));
+    float * sens = (float *)malloc((size_t)H * sizeof(float));
     for (int h = 0; h < H; h++) {
         float * Sh = S + (size_t)h * n_q * T;
+        float * ih = himp + (size_t)h * T;
         orc_scores(Q + (size_t)h * d_k, K + (size_t)h * d_k, Sh, n_q, T, d_k, ek, ek, inv_sqrt);
-        orc_softmax_importance(Sh, A + (size_t)h * n_q * T, himp,
+        orc_softmax_importance(Sh, A + (size_t)h * n_q * T, ih,
                                E ? E + (size_t)h * n_q * T : NULL,
                                RS ? RS + (size_t)h * n_q : NULL, n_q, T, p->score_method);
-        for (int j = 0; j < T; j++) if (himp[j] > gimp[j]) gimp[j] = himp[j];
+        if (p->use_sensitivity) sens[h] = orc_head_sensitivity(A + (size_t)h * n_q * T, n_q, T);
+        else for (int j = 0; j < T; j++) if (ih[j] > gimp[j]) gimp[j] = ih[j];
     }
+    /* sensitivity weighting, math.h:605-618: out[j] += s_h * imp_h[j], heads in order */
+    if (p->use_sensitivity)
+        for (int h = 0; h < H; h++)
+            for (int j = 0; j < T; j++) gimp[j] += sens[h] * himp[(size_t)h * T + j];
     if (p->reasoning && p->reasoning->classifier) {
         const kv_compact_reasoning * rk = p->reasoning;
         for (int j = 0; j < T; j++) {
@@ -638,10 +801,21 @@ static int compact_body(const float * K, const float * V, const float * Q, int T
         }
     }
     int * sel = (int *)malloc((size_t)t * sizeof(int));
-    if (p->use_diversity)
+    if (p->use_omp) {
+        /* OMP on the exp scores and row sums summed over heads, api.cpp:690-711 */
+        float * ce = (float *)calloc((size_t)n_q * T, sizeof(float));
+        float * cs = (float *)calloc((size_t)(n_q > 0 ? n_q : 1), sizeof(float));
+        for (int h = 0; h < H; h++) {
+            for (size_t i = 0; i < (size_t)n_q * T; i++) ce[i] += E[(size_t)h * n_q * T + i];
+            for (int i = 0; i < n_q; i++) cs[i] += RS[(size_t)h * n_q + i];
+        }
+        orc_omp_select(ce, cs, T, n_q, t, sel, NULL, p->omp_k_choice, p->omp_refit_interval, p->nnls_pgd_iters);
+        free(ce); free(cs);
+    } else if (p->use_diversity) {
         t = orc_select_diverse(gimp, K, T, t, ek, p->diversity_strength, p->n_shared_prefix, sel, NULL);
-    else
+    } else {
         orc_select_topk(gimp, T, t, p->n_shared_prefix, sel);
+    }
     double scoring_ms = now_ms() - t0;
     double t1 = now_ms();
 
@@ -724,7 +898,7 @@ static int compact_body(const float * K, const float * V, const float * Q, int T
     res->stats.elapsed_ms = now_ms() - t0;
     res->stats.scoring_ms = scoring_ms;
     res->stats.nnls_ms = nnls_ms;
-    free(S); free(A); free(E); free(RS); free(gimp); free(himp); free(Y); free(beta); free(Cv);
+    free(S); free(A); free(E); free(RS); free(gimp); free(himp); free(sens); free(Y); free(beta); free(Cv);
     return 0;
 }
 
@@ -814,8 +988,6 @@ static int compact_impl(const float * K, const float * V, const float * Q, int T
     if (!K || !V || !res) return -1;
     if (T <= 0 || H <= 0 || d_k <= 0 || d_v <= 0) return -2;
     kv_compact_params p = params ? *params : orc_params_default();
-    if (p.use_omp || p.use_sensitivity || (p.nnls_pgd_iters > 0 && !p.skip_beta && p.nnls_method != 0))
-        return KV_COMPACT_E_UNSUPPORTED;
     const int ek = H * d_k;
     float * cheap = NULL;
     const float * Qu = Q;

@@ -62,6 +62,10 @@ int   orc_select_diverse(const float * imp, const float * K, int T, int t, int n
 void  orc_ls_solve(const float * A, const float * b, float * x, int m, int n, int p, float ridge);
 void  orc_nnls_lh(const float * A, const float * b, float * w, int m, int n, int max_iter);
 void  orc_nnls_clamped(const float * A, const float * b, float * w, int m, int n, float eps);
+void  orc_nnls_pgd(const float * A, const float * b, float * w, int m, int n, float eps, int iters);
+float orc_head_sensitivity(const float * attn, int n_q, int T);
+void  orc_omp_select(const float * E, const float * rs, int T, int n_q, int t, int * sel_out, float * w_out,
+                     int k_choice, int refit_interval, int nnls_iters);
 void  orc_quality_stats(const float * K, const float * V, const float * Q, int T, int n_q,
                         int H, int d_k, int d_v, const kv_compact_result * r,
                         kv_compact_stats * st);

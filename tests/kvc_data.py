@@ -368,3 +368,50 @@ def quantize_rows(x: np.ndarray, typ: int) -> np.ndarray:
     else:
         raise ValueError(typ)
     return out.reshape(rows, -1)
+
+
+# --------------------------------------------------------------------------
+# Options past the defaults: sensitivity weighting (math.h:579-618,
+# api.cpp:651-666), projected-gradient NNLS iterations (math.h:752-805) and
+# OMP key selection (math.h:832-950, api.cpp:690-711).
+# --------------------------------------------------------------------------
+
+def option_variant_names():
+    return ["sens_chunk", "sens_max_div", "sens_mean_cheap", "pgd_iters_chunk", "pgd_iters_unchunked",
+            "omp_k1", "omp_k4_r2_beta_pgd", "omp_lh_beta", "omp_refine", "omp_cheap_chunk"]
+
+
+def option_variant(name: str):
+    """Return (case, K, V, Q or None, n_q)."""
+    def snap(T, H, d, seed, **params):
+        c = dict(name=name, T=T, H=H, d=d, seed=seed, params=params)
+        K, V = kv_cache(T, H, d, seed, channel_scale=True)
+        return c, K, V, snapkv_queries(K, 32, seed), 32
+
+    def cheap(T, H, d, seed, **params):
+        c = dict(name=name, T=T, H=H, d=d, seed=seed, params=dict(use_cheap_qref=1, **params))
+        K, V = kv_cache(T, H, d, seed)
+        return c, K, V, None, 0
+
+    if name == "sens_chunk":
+        return snap(2560, 4, 64, 51, target_ratio=0.2, use_sensitivity=1)
+    if name == "sens_max_div":
+        return snap(2000, 3, 32, 52, target_ratio=0.2, use_sensitivity=1, score_method=0, use_diversity=1)
+    if name == "sens_mean_cheap":
+        return cheap(3000, 2, 32, 53, target_ratio=0.2, use_sensitivity=1, score_method=2)
+    if name == "pgd_iters_chunk":
+        return snap(2560, 2, 64, 54, target_ratio=0.2, skip_beta=0, nnls_method=1, nnls_pgd_iters=20)
+    if name == "pgd_iters_unchunked":
+        return snap(700, 1, 32, 55, target_ratio=0.3, chunk_size=-1, skip_beta=0, nnls_method=1, nnls_pgd_iters=5)
+    if name == "omp_k1":
+        return snap(1000, 2, 32, 56, target_ratio=0.2, use_omp=1)
+    if name == "omp_k4_r2_beta_pgd":
+        return snap(2560, 2, 32, 57, target_ratio=0.2, use_omp=1, omp_k_choice=4, omp_refit_interval=2,
+                    skip_beta=0, nnls_method=1, nnls_pgd_iters=3)
+    if name == "omp_lh_beta":
+        return snap(1500, 2, 32, 58, target_ratio=0.15, use_omp=1, omp_k_choice=2, skip_beta=0, nnls_method=0)
+    if name == "omp_refine":
+        return snap(1200, 2, 32, 59, target_ratio=0.2, use_omp=1, refine_rounds=1, skip_beta=0)
+    if name == "omp_cheap_chunk":
+        return cheap(1800, 2, 32, 60, target_ratio=0.2, use_omp=1, omp_k_choice=3, use_sensitivity=1)
+    raise KeyError(name)

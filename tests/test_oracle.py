@@ -11,7 +11,7 @@ import pytest
 
 from kvc_data import (CASES, CASE_BY_NAME, beta_variant, beta_variant_names, diversity_variant,
                       diversity_variant_names, kv_cache, make_case, nonfinite_variant, nonfinite_variant_names,
-                      normal, refine_variant, refine_variant_names, uniform)
+                      normal, option_variant, option_variant_names, refine_variant, refine_variant_names, uniform)
 from kvc_harness import ORACLE_SO, REF_HARNESS_SO, REF_SO, case_params, kc, load_oracle, load_ref, run_case
 from pathlib import Path
 
@@ -126,6 +126,24 @@ def test_oracle_beta_variants_match_live_reference(orc, name):
     assert np.array_equal(a.indices, b.indices)
     assert np.array_equal(bits(a.beta), bits(b.beta))
     assert np.array_equal(bits(a.C_v), bits(b.C_v))
+
+
+@pytest.mark.parametrize("name", option_variant_names())
+def test_oracle_option_variants_match_live_reference(orc, name):
+    """Sensitivity weighting, PGD iterations and OMP selection: oracle vs the compiled reference."""
+    ref = load_ref()
+    if ref is None:
+        pytest.skip("reference not compiled here (oracle/_ref)")
+    c, K, V, Q, nq = option_variant(name)
+    T, H, d = c["T"], c["H"], c["d"]
+    a = orc.compact(K, V, Q, T, nq, H, d, d, case_params(orc, c, T))
+    b = ref.compact(K, V, Q, T, nq, H, d, d, case_params(ref, c, T))
+    assert a.t == b.t
+    assert np.array_equal(a.indices, b.indices)
+    assert np.array_equal(bits(a.beta), bits(b.beta))
+    assert np.array_equal(bits(a.C_v), bits(b.C_v))
+    for k in ("avg_cosine_sim", "avg_mse", "avg_agreement"):
+        assert np.float32(a.stats[k]).view(np.uint32) == np.float32(b.stats[k]).view(np.uint32), k
 
 
 @pytest.mark.parametrize("name", refine_variant_names())
