@@ -53,6 +53,9 @@ struct Work {
     float * rowsum;   // [L][n_chunks][H][nq_max]
     float * ainv;     // [L][n_chunks][H][nq_max] 1 / (row sum + 1e-12f) of the chunk softmax
     float * imp;      // [L][H][T]           per-head importance
+    float * amax;     // [L][H][T]           per-key maxima over queries of the softmax weights
+                      //                     (sensitivity under the rms and mean score methods), or nullptr
+    float * sens;     // [L][n_chunks][H]    head sensitivities (nullptr: max over heads)
     float * gimp;     // [L][T]              global importance (after R-KV weights)
     float * Y;        // [L][n_chunks][H][nq_max][dv]
     int   * sel;      // [L][t_total]        kept token positions (layer-local), ascending
@@ -90,6 +93,22 @@ struct DivWork {
     float * G;        // [slots][cap][cap] Gram matrix of the candidates' full key rows
 };
 constexpr int DIV_MAX_CAND = 1280;   // 20 candidates per lane in the greedy wave
+
+// OMP key selection scratch (math.h:832-950). One unit = (layer, chunk).
+struct OmpWork {
+    float * ce;       // [L][nq_max][T]      exp scores summed over heads
+    float * cs;       // [L][n_chunks][nq_max] row sums summed over heads
+    float * corr;     // [L][T]              correlations with the residual
+    unsigned char * mask; // [L][T]          1: key picked
+    int * order;      // [L][t_total]        picks in pick order
+    float * w;        // [L][t_total]        latest NNLS solution
+    float * prev_w;   // [L][t_total]        weights of the residual (padded with 1e-12f between refits)
+    float * G;        // [units][tc_max][tc_max] Gram matrix of the picked columns, pick order
+    float * Atb;      // [units][tc_max]
+    float * aug;      // [units][tc_max][tc_max + 1] the regularised system, solved in place
+    float * vec;      // [units][4 tc_max + 1 + nq_max] PGD vectors (u, grad, v), GE pivot row and factors
+    int k_choice, refit_interval, pgd_iters;
+};
 
 // Statistics scratch (api.cpp:239-325 sampling: h < min(H,4), qi < min(nq,32))
 struct StatWork {

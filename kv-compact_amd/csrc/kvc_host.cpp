@@ -294,8 +294,6 @@ void make_plan(int T, int n_q, bool q_given, const kv_compact_params & p, Plan &
 // Options this library implements; everything else is refused with -5
 // rather than computed differently.
 int check_supported(const kv_compact_params & p, int d_v) {
-    if (p.use_omp || p.use_sensitivity) return KV_COMPACT_E_UNSUPPORTED;
-    if (!p.skip_beta && p.nnls_method != 0 && p.nnls_pgd_iters > 0) return KV_COMPACT_E_UNSUPPORTED;
     if (d_v > 256) return KV_COMPACT_E_UNSUPPORTED;
     return 0;
 }
@@ -334,9 +332,12 @@ size_t div_g_floats(const Plan & pl, int L) {
 
 // p == nullptr: statistics-only workspace (no exp scores, no diversity)
 size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_params * p, Carver * cv_out, Work * w,
-                       StatWork * sw, DivWork * dw = nullptr, size_t * div_floats = nullptr) {
-    const bool need_e = p && !p->skip_beta;
-    const bool div = p && p->use_diversity;
+                       StatWork * sw, DivWork * dw = nullptr, size_t * div_floats = nullptr, OmpWork * ow = nullptr) {
+    // OMP reads the exp scores and row sums even when beta is skipped (api.cpp:634-643)
+    const bool omp = p && p->use_omp;
+    const bool need_e = p && (!p->skip_beta || omp);
+    const bool div = p && p->use_diversity && !omp;
+    const bool sens = p && p->use_sensitivity;
     Carver cv = cv_out ? *cv_out : Carver();
     const size_t L = io.L, H = io.H, T = io.T, nqm = pl.nq_max, nc = pl.n_chunks;
     const size_t tt = pl.t_total, dv = io.dv;
@@ -348,6 +349,8 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     ww.rowsum = cv.take<float>(L * nc * H * nqm);
     ww.ainv = cv.take<float>(L * nc * H * nqm);
     ww.imp = cv.take<float>(L * H * T);
+    ww.sens = sens ? cv.take<float>(L * nc * H) : nullptr;
+    ww.amax = sens && p->score_method != 0 ? cv.take<float>(L * H * T) : nullptr;
     ww.gimp = cv.take<float>(L * T);
     ww.Y = cv.take<float>(L * nc * H * nqm * dv);
     ww.sel = nullptr;
@@ -371,6 +374,25 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     ww.status = cv.take<int>(1);
     ww.refine_active = cv.take<int>(L * nc);
     ww.lu_redo = cv.take<int>(L * nc * H);
+    if (omp) {
+        const size_t units = L * nc, tm = pl.tc_max;
+        OmpWork o{};
+        o.ce = cv.take<float>(L * nqm * T);
+        o.cs = cv.take<float>(units * nqm);
+        o.corr = cv.take<float>(L * T);
+        o.mask = cv.take<unsigned char>(L * T);
+        o.order = cv.take<int>(L * tt);
+        o.w = cv.take<float>(L * tt);
+        o.prev_w = cv.take<float>(L * tt);
+        o.G = cv.take<float>(units * tm * tm);
+        o.Atb = cv.take<float>(units * tm);
+        o.aug = cv.take<float>(units * tm * (tm + 1));
+        o.vec = cv.take<float>(units * (4 * tm + 1 + nqm));
+        o.k_choice = p->omp_k_choice;
+        o.refit_interval = p->omp_refit_interval;
+        o.pgd_iters = p->nnls_pgd_iters;
+        if (ow) *ow = o;
+    }
     if (div) {
         const size_t units = L * nc;
         DivWork d{};
@@ -455,12 +477,16 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     // Lawson-Hanson keeps a system's passive set on one wave: refused before
     // anything is launched
     if (!p.skip_beta && p.nnls_method == 0 && pl.tc_max > 256) return KV_COMPACT_E_UNSUPPORTED;
+    // the beta fit's PGD steps keep their vectors in LDS
+    const bool pgd = !p.skip_beta && p.nnls_method != 0 && p.nnls_pgd_iters > 0;
+    if (pgd && 3 * pl.tc_max + pl.nq_max > PGD_LDS_FLOATS) return KV_COMPACT_E_UNSUPPORTED;
     if (!drain_second_stream(ctx, st)) return KV_COMPACT_E_DEVICE;
     Work w{};
     StatWork sw{};
     DivWork dw{};
+    OmpWork ow{};
     size_t div_floats = 0;
-    workspace_bytes(pl, io, &p, &carver, &w, &sw, &dw, &div_floats);
+    workspace_bytes(pl, io, &p, &carver, &w, &sw, &dw, &div_floats, &ow);
     w.sel = io.indices;
     w.wts = const_cast<float *>(io.wts);
     (void)ctx;
@@ -521,9 +547,12 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         launch_refit_target(g, w, io.V, st);
     }
     (void)hipEventRecord(ev[ST_REFIT + 1], st);
-    // 4. global importance (+R-KV), then top-t or the diversity greedy pass
+    // 4. global importance (+R-KV), then OMP, the diversity greedy pass or top-t
+    //    (api.cpp:686-716)
     launch_global_importance(g, w, st);
-    if (p.use_diversity) {
+    if (p.use_omp) {
+        launch_omp_select(g, w, ow, st);
+    } else if (p.use_diversity) {
         const int rc = run_diversity(st, pl, p, g, w, dw, div_floats, io.K);
         if (rc) return rc;
     } else {
@@ -552,6 +581,12 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
             launch_ls_build(gb, wb, st, true);
             launch_ge_lu(gb, wb, st, true);
             launch_ge_solve(gb, wb, io.beta, st);
+            if (pgd) {
+                // projected-gradient steps (math.h:752-805) on [AtA | Atb] without the ridge
+                gb.ridge = 0.0f;
+                launch_ls_build(gb, wb, st);
+                launch_nnls_pgd(gb, wb, io.beta, p.nnls_pgd_iters, st);
+            }
         }
         launch_beta_log(io.beta, (long long)io.L * io.H * pl.t_total, st);
         return 0;
@@ -618,6 +653,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         fprintf(stderr, "[kv-compact] LU step wait exceeded its bound\n");
         return KV_COMPACT_E_DEVICE;
     }
+    if (status & 4) fprintf(stderr, "[kv-compact] OMP selection found no pickable key (non-finite correlations)\n");
     if (status) return KV_COMPACT_E_UNSUPPORTED;
     for (int i = 0; i < ST_BATCH_END; i++) {
         float ms = 0.0f;

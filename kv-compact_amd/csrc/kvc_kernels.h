@@ -23,6 +23,12 @@ void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipSt
 void launch_gather_exp(const Geom & g, const Work & w, hipStream_t st);
 void launch_nnls_lh(const Geom & g, const Work & w, float * wout, int max_iter, int * status, hipStream_t st);
 void launch_beta_log(float * wb, long long n, hipStream_t st);
+// PGD steps of the beta fit on [AtA | Atb] in aug and M in X (wb refined in
+// place; 3 tc_max + nq_max <= PGD_LDS_FLOATS)
+constexpr int PGD_LDS_FLOATS = 40960 - 64;
+void launch_nnls_pgd(const Geom & g, const Work & w, float * wb, int iters, hipStream_t st);
+// OMP selection into w.sel (rows of w.A and w.rowsum as the exp scores)
+void launch_omp_select(const Geom & g, const Work & w, const OmpWork & ow, hipStream_t st);
 // m_by_lu: k_ls_build leaves M = X^T X out where k_ge_lu can form it from X
 // (the register LU's systems with nq * n <= 8192); launch_ge_lu must then
 // be given the same flag

@@ -459,7 +459,7 @@ constexpr int SM_MAXQ = 256, SM_TILE = 64, SM_TROWS = 32;
 __global__ void __launch_bounds__(256)
 k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ S,
                      const unsigned * __restrict__ smax, float * __restrict__ A, float * __restrict__ rowsum,
-                     float * __restrict__ ainv, float * __restrict__ imp) {
+                     float * __restrict__ ainv, float * __restrict__ imp, float * __restrict__ amax) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const long long rs = g.T;
@@ -543,8 +543,9 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
     // 3. the weights per key, aggregated in row order
     float * imph = imp + ((long long)layer * g.H + h) * g.T + c.start;
     const float inv_m = 1.0f / (float)nq;
+    float * amaxh = amax ? amax + ((long long)layer * g.H + h) * g.T + c.start : nullptr;
     for (int j = tid; j < n; j += blockDim.x) {
-        float acc = 0.0f;
+        float acc = 0.0f, mx = 0.0f;
         for (int q0 = 0; q0 < nq; q0 += 16) {
             // sixteen rows' loads in flight, then the row-ordered aggregation
             const int qn = min(16, nq - q0);
@@ -564,12 +565,14 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
                     } else {
                         acc += a;
                     }
+                    if (amaxh && a > mx) mx = a;
                 }
             }
         }
         if (g.score_method == 1) acc = sqrtf(acc * inv_m);
         else if (g.score_method == 2) acc *= inv_m;
         imph[j] = acc;
+        if (amaxh) amaxh[j] = mx;
     }
 }
 
@@ -889,19 +892,55 @@ k_stats_values(Geom g, const float * __restrict__ a_all, const float * __restric
 }
 
 // ---------------------------------------------------------------------------
+// Head sensitivity (math.h:579-594) of one (layer, chunk, head): over the
+// chunk's keys, the largest of the per-key maxima over queries of the softmax
+// weights (0 start, strictly greater replaces), over their mean (the sum runs
+// in key order) plus 1e-12f. amax holds those per-key maxima [L][H][T] (the
+// importance itself under the max score method). The wave walks the keys 64
+// at a time and every lane adds the broadcast values in key order.
+// grid = (n_chunks * H, L), 64 threads
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(64)
+k_head_sensitivity(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ amax,
+                   float * __restrict__ sens) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const float * src = amax + ((long long)layer * g.H + h) * g.T + c.start;
+    const int n = c.Tc, lane = threadIdx.x;
+    float sum = 0.0f, mx = 0.0f;
+    for (int j0 = 0; j0 < n; j0 += 64) {
+        const float x = (j0 + lane < n) ? src[j0 + lane] : 0.0f;
+        const int cnt = min(64, n - j0);
+        for (int k = 0; k < cnt; k++) {
+            const float y = __shfl(x, k);
+            sum += y;
+            if (y > mx) mx = y;
+        }
+    }
+    if (lane == 0) {
+        const float mean = sum / (float)n;
+        sens[((long long)layer * g.n_chunks + c_idx) * g.H + h] = mx / (mean + 1e-12f);
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Global importance (api.cpp:656-684): max over heads (init 0, strictly
-// greater replaces), then the R-KV weight. grid = (n_chunks, L)
+// greater replaces), or with sensitivity weighting (math.h:605-618) the sum
+// over heads in order of sens_h * imp_h[j] from 0; then the R-KV weight.
+// grid = (n_chunks, L)
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
 k_global_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ imp,
-                    const float * __restrict__ wts, float * __restrict__ gimp) {
+                    const float * __restrict__ wts, const float * __restrict__ sens, float * __restrict__ gimp) {
     const int c_idx = blockIdx.x, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
+    const float * sh = sens ? sens + ((long long)layer * g.n_chunks + c_idx) * g.H : nullptr;
     for (int j = threadIdx.x; j < c.Tc; j += blockDim.x) {
         float m = 0.0f;
         for (int h = 0; h < g.H; h++) {
             const float v = imp[((long long)layer * g.H + h) * g.T + c.start + j];
-            if (v > m) m = v;
+            if (sh) m = m + sh[h] * v;
+            else if (v > m) m = v;
         }
         if (wts) m *= wts[c.start + j];
         gimp[(long long)layer * g.T + c.start + j] = m;
@@ -3450,6 +3489,304 @@ k_ge_general(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__
 }
 
 // ---------------------------------------------------------------------------
+// Projected-gradient NNLS (math.h:752-805), after the clamped least-squares
+// solution: w < eps -> eps; then, for iters > 0, three power-iteration steps
+// on M from u = 1 / sqrtf(n) (each stopped when a norm falls below 1e-12f),
+// L = u^T (M^T M) u clamped to 1e-6f, eta = 1 / L, and iters steps
+// w <- max(eps, w - eta (M^T M w - M^T b)). Every sum runs in index order
+// (one thread per output, or thread 0 for the norms and L). One block; the
+// vectors u (n), v (m) and grad (n) are the caller's scratch.
+// ---------------------------------------------------------------------------
+struct MatRows {    // M(i, j) = p[i * rs + j]
+    const float * p;
+    long long rs;
+    __device__ __forceinline__ float operator()(int i, int j) const { return p[(long long)i * rs + j]; }
+};
+struct MatPicked {  // M(i, j) = p[i * rs + col[j]]
+    const float * p;
+    long long rs;
+    const int * col;
+    __device__ __forceinline__ float operator()(int i, int j) const { return p[(long long)i * rs + col[j]]; }
+};
+
+// AtA(i, j) at AtA[j * lda + i] (symmetric); w, u, v, grad visible to the block
+template <class Mat>
+__device__ void pgd_block(const Mat & M, int m, int n, const float * AtA, long long lda, const float * Atb,
+                          float * w, float eps, int iters, float * u, float * v, float * grad) {
+    __shared__ float s_val;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int i = tid; i < n; i += nt) {
+        const float x = w[i];
+        w[i] = (x < eps) ? eps : x;
+    }
+    __syncthreads();
+    if (iters <= 0) return;
+    const float u0 = 1.0f / sqrtf((float)n);
+    for (int j = tid; j < n; j += nt) u[j] = u0;
+    __syncthreads();
+    for (int pw = 0; pw < 3; pw++) {
+        for (int i = tid; i < m; i += nt) {
+            float acc = 0.0f;
+            for (int j = 0; j < n; j++) acc += M(i, j) * u[j];
+            v[i] = acc;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float s = 0.0f;
+            for (int i = 0; i < m; i++) s += v[i] * v[i];
+            s_val = sqrtf(s);
+        }
+        __syncthreads();
+        const float vn = s_val;
+        if (vn < 1e-12f) break;
+        for (int i = tid; i < m; i += nt) v[i] = v[i] / vn;
+        __syncthreads();
+        for (int j = tid; j < n; j += nt) {
+            float acc = 0.0f;
+            for (int i = 0; i < m; i++) acc += M(i, j) * v[i];
+            u[j] = acc;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float s = 0.0f;
+            for (int j = 0; j < n; j++) s += u[j] * u[j];
+            s_val = sqrtf(s);
+        }
+        __syncthreads();
+        const float un = s_val;
+        if (un < 1e-12f) break;
+        for (int j = tid; j < n; j += nt) u[j] = u[j] / un;
+        __syncthreads();
+    }
+    for (int i = tid; i < n; i += nt) {
+        float acc = 0.0f;
+        for (int j = 0; j < n; j++) acc += AtA[(long long)j * lda + i] * u[j];
+        grad[i] = acc;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float L = 0.0f;
+        for (int i = 0; i < n; i++) L += u[i] * grad[i];
+        if (L < 1e-6f) L = 1e-6f;
+        s_val = 1.0f / L;
+    }
+    __syncthreads();
+    const float eta = s_val;
+    for (int it = 0; it < iters; it++) {
+        for (int i = tid; i < n; i += nt) {
+            float acc = 0.0f;
+            for (int j = 0; j < n; j++) acc += AtA[(long long)j * lda + i] * w[j];
+            grad[i] = acc - Atb[i];
+        }
+        __syncthreads();
+        for (int i = tid; i < n; i += nt) {
+            const float x = w[i] - eta * grad[i];
+            w[i] = (x < eps) ? eps : x;
+        }
+        __syncthreads();
+    }
+}
+
+// The beta fit's PGD steps (api.cpp:826 with nnls_pgd_iters > 0): per
+// (layer, chunk, head), M = the gathered exp scores in X, [AtA | Atb] in aug
+// (k_ls_build without ridge), w = the clamped LS solution in wb, refined in
+// place. Dynamic LDS: w, u, grad (tc_max each), v (nq_max).
+// grid = (n_chunks * H, L), 256 threads
+__global__ void __launch_bounds__(256)
+k_nnls_pgd(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ X,
+           const float * __restrict__ aug, const long long * __restrict__ aug_off, float * __restrict__ wb,
+           int iters) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const int n = c.tc, m = c.nq;
+    const long long sys = ((long long)layer * g.n_chunks + c_idx) * g.H + h;
+    const float * Ag = aug + aug_off[sys];
+    const long long hsX = (long long)g.nq_max * g.t_total;
+    const float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
+    float * wg = wb + ((long long)layer * g.H + h) * g.t_total + c.off;
+    extern __shared__ float pv[];
+    float * w = pv;
+    float * u = pv + g.tc_max;
+    float * grad = pv + 2 * g.tc_max;
+    float * v = pv + 3 * g.tc_max;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) w[i] = wg[i];
+    __syncthreads();
+    pgd_block(MatRows{Xh, g.t_total}, m, n, Ag, n, Ag + (long long)n * n, w, 1e-12f, iters, u, v, grad);
+    for (int i = threadIdx.x; i < n; i += blockDim.x) wg[i] = w[i];
+}
+
+// ---------------------------------------------------------------------------
+// OMP key selection (math.h:832-950; api.cpp:690-711) of one (layer, chunk)
+// on the exp scores and row sums summed over heads (in head order from 0):
+// while fewer than t keys are picked, the residual r = b - cur, the
+// correlations corr_j = sum_i E[i][j] r_i of the unpicked keys, then up to
+// k_choice picks of the largest correlation (first index on ties; it must
+// beat -1e30f). On refit iterations (every refit_interval-th, and the last)
+// the NNLS of the picked columns in pick order (ridge 1e-10f, GE with partial
+// pivoting, skipped pivots and the clamp at 1e-12f, then the PGD steps) gives
+// the weights and cur = M w; between refits the new picks weigh 1e-12f. The
+// Gram matrix grows by the new columns only (every entry is its own sum over
+// the queries, the same whenever it is formed). Output: the picks ascending
+// (fewer than t picks are padded with the chunk's first position). An
+// iteration without a pick (every correlation NaN) sets status bit 4 and
+// stops, where the reference would not return.
+// grid = (n_chunks, L), 256 threads
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(256)
+k_omp_select(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ E,
+             const float * __restrict__ rowsum, OmpWork ow, int * __restrict__ sel, int * __restrict__ status) {
+    const int c_idx = blockIdx.x, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const int T = c.Tc, nq = c.nq, t = c.tc, tid = threadIdx.x, nt = blockDim.x;
+    const long long unit = (long long)layer * g.n_chunks + c_idx;
+    const long long tm = g.tc_max;
+    float * ce = ow.ce + (long long)layer * g.nq_max * g.T + c.start;   // row k at k * g.T
+    float * corr = ow.corr + (long long)layer * g.T + c.start;
+    unsigned char * mask = ow.mask + (long long)layer * g.T + c.start;
+    int * order = ow.order + (long long)layer * g.t_total + c.off;
+    float * w = ow.w + (long long)layer * g.t_total + c.off;
+    float * prev_w = ow.prev_w + (long long)layer * g.t_total + c.off;
+    float * G = ow.G + unit * tm * tm;            // column j at G + j * t
+    float * Atb = ow.Atb + unit * tm;
+    float * aug = ow.aug + unit * tm * (tm + 1);
+    float * u = ow.vec + unit * (4 * tm + 1 + g.nq_max);
+    float * grad = u + tm;
+    float * v = grad + tm;
+    float * prow = v + g.nq_max;
+    float * fac = prow + tm + 1;
+    __shared__ float cs[SM_MAXQ], res[SM_MAXQ], cur[SM_MAXQ];
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    __shared__ int s_best;
+    for (long long e = tid; e < (long long)nq * T; e += nt) {
+        const int k = (int)(e / T), j = (int)(e % T);
+        float s = 0.0f;
+        for (int h = 0; h < g.H; h++) s += E[layer * lS(g) + h * hS(g) + (long long)k * g.T + c.start + j];
+        ce[(long long)k * g.T + j] = s;
+    }
+    for (int k = tid; k < nq; k += nt) {
+        float s = 0.0f;
+        for (int h = 0; h < g.H; h++) s += rowsum[(unit * g.H + h) * g.nq_max + k];
+        cs[k] = s;
+        cur[k] = 0.0f;
+    }
+    for (int j = tid; j < T; j += nt) mask[j] = 0;
+    __syncthreads();
+    const MatPicked M{ce, g.T, order};
+    int ns = 0, n_prev = 0, ng = 0, iteration = 0;
+    while (ns < t) {
+        for (int i = tid; i < nq; i += nt) res[i] = cs[i] - cur[i];
+        __syncthreads();
+        for (int j = tid; j < T; j += nt) {
+            float cc = 0.0f;
+            if (!mask[j])
+                for (int i = 0; i < nq; i++) cc += ce[(long long)i * g.T + j] * res[i];
+            corr[j] = cc;
+        }
+        __syncthreads();
+        int k_sel = min(ow.k_choice, t - ns);
+        k_sel = min(k_sel, T - ns);
+        if (k_sel <= 0) break;
+        const int ns0 = ns;
+        for (int k = 0; k < k_sel; k++) {
+            float bv = -1e30f;
+            int bi = -1;
+            for (int j = tid; j < T; j += nt)
+                if (!mask[j]) {
+                    const float x = corr[j];
+                    if (x > bv) { bv = x; bi = j; }
+                }
+            // largest value, then smallest index (-1, no candidate, ranks last)
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(bv, o);
+                const int oi = __shfl_xor(bi, o);
+                if (ov > bv || (ov == bv && (unsigned)oi < (unsigned)bi)) { bv = ov; bi = oi; }
+            }
+            if ((tid & 63) == 0) { rv[tid >> 6] = bv; ri[tid >> 6] = bi; }
+            __syncthreads();
+            if (tid == 0) {
+                float b = rv[0];
+                int r = ri[0];
+                for (int q = 1; q < (nt >> 6); q++)
+                    if (rv[q] > b || (rv[q] == b && (unsigned)ri[q] < (unsigned)r)) { b = rv[q]; r = ri[q]; }
+                s_best = r;
+                if (r >= 0) {
+                    order[ns] = r;
+                    mask[r] = 1;
+                }
+            }
+            __syncthreads();
+            if (s_best < 0) break;
+            ns++;
+        }
+        if (ns == ns0) {
+            if (tid == 0) atomicOr(status, 4);
+            return;
+        }
+        const int ct = ns;
+        const bool solve = ow.refit_interval <= 1 || iteration % ow.refit_interval == 0 || ct == t;
+        if (solve) {
+            // Gram entries (i, jn) of the new columns jn, i <= jn, mirrored
+            for (long long e = tid; e < (long long)(ct - ng) * ct; e += nt) {
+                const int jn = ng + (int)(e / ct), i = (int)(e % ct);
+                if (i > jn) continue;
+                const int ci = order[i], cj = order[jn];
+                float s = 0.0f;
+                for (int k = 0; k < nq; k++) s += ce[(long long)k * g.T + ci] * ce[(long long)k * g.T + cj];
+                G[(long long)jn * t + i] = s;
+                G[(long long)i * t + jn] = s;
+            }
+            for (int jn = ng + tid; jn < ct; jn += nt) {
+                const int cj = order[jn];
+                float s = 0.0f;
+                for (int k = 0; k < nq; k++) s += ce[(long long)k * g.T + cj] * cs[k];
+                Atb[jn] = s;
+            }
+            ng = ct;
+            __syncthreads();
+            // [G + 1e-10 I | A^T b], column-major ct x (ct + 1)
+            for (long long e = tid; e < (long long)ct * ct; e += nt) {
+                const int j = (int)(e / ct), i = (int)(e % ct);
+                float a = G[(long long)j * t + i];
+                if (i == j) a += 1e-10f;
+                aug[e] = a;
+            }
+            for (int i = tid; i < ct; i += nt) aug[(long long)ct * ct + i] = Atb[i];
+            __syncthreads();
+            ge_solve_block(aug, ct, 1, w, 1, 1e-12f, prow, fac);
+            pgd_block(M, nq, ct, G, t, Atb, w, 1e-12f, ow.pgd_iters, u, v, grad);
+            for (int j = tid; j < ct; j += nt) prev_w[j] = w[j];
+            n_prev = ct;
+            for (int i = tid; i < nq; i += nt) {
+                float acc = 0.0f;
+                for (int j = 0; j < ct; j++) acc += M(i, j) * w[j];
+                cur[i] = acc;
+            }
+        } else {
+            for (int j = n_prev + tid; j < ct; j += nt) prev_w[j] = 1e-12f;
+            n_prev = ct;
+            __syncthreads();
+            for (int i = tid; i < nq; i += nt) {
+                float acc = 0.0f;
+                for (int j = 0; j < ct; j++) acc += M(i, j) * prev_w[j];
+                cur[i] = acc;
+            }
+        }
+        __syncthreads();
+        iteration++;
+    }
+    // ascending (the picks are distinct: rank = number of smaller picks)
+    int * out = sel + (long long)layer * g.t_total + c.off;
+    for (int j = tid; j < ns; j += nt) {
+        const int x = order[j];
+        int r = 0;
+        for (int k = 0; k < ns; k++) r += order[k] < x ? 1 : 0;
+        out[r] = c.start + x;
+    }
+    for (int j = ns + tid; j < t; j += nt) out[j] = c.start;
+}
+
+// ---------------------------------------------------------------------------
 // Quality statistics (api.cpp:239-325).
 // ---------------------------------------------------------------------------
 // In-place row softmax (math.h:83-100) of the statistics rows: row r of a
@@ -4027,7 +4364,13 @@ void launch_scores(const Geom & g, const ChunkDesc * chunks, int n_chunk_units, 
 
 void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st) {
     hipLaunchKernelGGL(k_softmax_importance, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
-                       g, w.chunks, w.S, w.smax, w.A, w.E ? w.rowsum : nullptr, w.ainv, w.imp);
+                       g, w.chunks, w.S, w.smax, w.A, w.E ? w.rowsum : nullptr, w.ainv, w.imp,
+                       w.sens && g.score_method != 0 ? w.amax : nullptr);
+    // sensitivity per (layer, chunk, head) from the per-key maxima over
+    // queries (the importance itself under the max score method)
+    if (w.sens)
+        hipLaunchKernelGGL(k_head_sensitivity, dim3(g.n_chunks * g.H, g.L), dim3(64), 0, st,
+                           g, w.chunks, g.score_method != 0 ? w.amax : w.imp, w.sens);
 }
 
 void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStream_t st) {
@@ -4045,7 +4388,7 @@ void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStr
 
 void launch_global_importance(const Geom & g, const Work & w, hipStream_t st) {
     hipLaunchKernelGGL(k_global_importance, dim3(g.n_chunks, g.L), dim3(256), 0, st,
-                       g, w.chunks, w.imp, w.wts, w.gimp);
+                       g, w.chunks, w.imp, w.wts, w.sens, w.gimp);
 }
 
 void launch_div_level(const Geom & g, const Work & w, const DivWork & dw, const float * K, hipStream_t st) {
@@ -4100,6 +4443,24 @@ void launch_gather_exp(const Geom & g, const Work & w, hipStream_t st) {
 void launch_nnls_lh(const Geom & g, const Work & w, float * wout, int max_iter, int * status, hipStream_t st) {
     hipLaunchKernelGGL(k_nnls_lh, dim3(g.n_chunks * g.H, g.L), dim3(64), 0, st, g, w.chunks, w.aug, w.aug_off,
                        wout, max_iter, status);
+}
+
+void launch_nnls_pgd(const Geom & g, const Work & w, float * wb, int iters, hipStream_t st) {
+    const size_t lds = (size_t)(3 * g.tc_max + g.nq_max) * sizeof(float);
+    // beyond 64 KB of dynamic LDS the kernel needs the attribute (set once;
+    // PGD_LDS_FLOATS leaves room for the kernel's static LDS)
+    static bool lds_set = false;
+    if (lds > 65536 && !lds_set)
+        lds_set = hipFuncSetAttribute(reinterpret_cast<const void *>(k_nnls_pgd),
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      PGD_LDS_FLOATS * (int)sizeof(float)) == hipSuccess;
+    hipLaunchKernelGGL(k_nnls_pgd, dim3(g.n_chunks * g.H, g.L), dim3(256), lds, st,
+                       g, w.chunks, w.X, w.aug, w.aug_off, wb, iters);
+}
+
+void launch_omp_select(const Geom & g, const Work & w, const OmpWork & ow, hipStream_t st) {
+    hipLaunchKernelGGL(k_omp_select, dim3(g.n_chunks, g.L), dim3(256), 0, st,
+                       g, w.chunks, w.A, w.rowsum, ow, w.sel, w.status);
 }
 
 void launch_beta_log(float * wb, long long n, hipStream_t st) {
