@@ -318,3 +318,90 @@ def load_product() -> "Lib":
     if not p.exists():
         raise FileNotFoundError(f"{p} not built: run __graft_entry__.build()")
     return Lib(p)
+
+
+# -- llama.cpp state blob compaction (include/kv-compact-state.h) ---------------
+LayerFilterFn = ctypes.CFUNCTYPE(_i, _i, _i, _vp)
+
+
+class StateParams(ctypes.Structure):
+    """kvc_state_params (include/kv-compact-state.h)."""
+    _fields_ = [
+        ("compact_ratio", ctypes.c_float),
+        ("n_ref_queries", ctypes.c_int32),
+        ("n_head_kv", ctypes.c_int32),
+        ("n_pos_per_embd", ctypes.c_uint32),
+        ("sensitivity_budget", ctypes.c_int32),
+        ("layer_filter", LayerFilterFn),
+        ("layer_filter_data", _vp),
+    ]
+
+
+class StateInfo(ctypes.Structure):
+    """kvc_state_info (include/kv-compact-state.h)."""
+    _fields_ = [
+        ("n_stream", ctypes.c_uint32),
+        ("cell_count", ctypes.c_uint32),
+        ("v_trans", ctypes.c_uint32),
+        ("n_layer", ctypes.c_uint32),
+        ("n_embd_k", ctypes.c_int32),
+        ("n_embd_v", ctypes.c_int32),
+        ("kv_bytes", ctypes.c_uint64),
+        ("trailing_bytes", ctypes.c_uint64),
+    ]
+
+
+def state_params(ratio, n_head_kv, n_ref=0, n_pos=1, sens=0, layers=None):
+    """kvc_state_params; layers: explicit list of compacted layers (None: all).
+    Returns (params, keepalive) - keep the second alive while the call runs."""
+    p = StateParams()
+    p.compact_ratio = ratio
+    p.n_ref_queries = n_ref
+    p.n_head_kv = n_head_kv
+    p.n_pos_per_embd = n_pos
+    p.sensitivity_budget = sens
+    keep = None
+    if layers is not None:
+        allowed = set(int(x) for x in layers)
+        keep = LayerFilterFn(lambda layer, n, data: 1 if layer in allowed else 0)
+        p.layer_filter = keep
+    return p, keep
+
+
+def bind_state(dll, prefix):
+    """prefix 'kvc_' (the library) or 'orc_' (the oracle): parse_info and compact."""
+    info = getattr(dll, prefix + "state_parse_info")
+    info.argtypes = [_vp, ctypes.c_size_t, ctypes.c_uint32, ctypes.POINTER(StateInfo)]
+    info.restype = _i
+    comp = getattr(dll, prefix + "state_compact")
+    comp.argtypes = [_vp, ctypes.c_size_t, ctypes.POINTER(StateParams), ctypes.POINTER(_vp),
+                     ctypes.POINTER(ctypes.c_size_t), _vp]
+    comp.restype = _i
+    free = getattr(dll, prefix + "state_free")
+    free.argtypes = [_vp]
+    free.restype = None
+    return info, comp, free
+
+
+def state_info(dll, prefix, blob: bytes, n_pos=1):
+    info, _, _ = bind_state(dll, prefix)
+    si = StateInfo()
+    b = np.frombuffer(blob, np.uint8)
+    rc = info(b.ctypes.data if b.size else None, b.size, n_pos, ctypes.byref(si))
+    return rc, si
+
+
+def state_compact(dll, prefix, blob: bytes, params: StateParams, t_max: int):
+    """(rc, out bytes or None, selected int32[t] or None)."""
+    _, comp, free = bind_state(dll, prefix)
+    b = np.frombuffer(blob, np.uint8)
+    out = _vp()
+    n = ctypes.c_size_t(0)
+    sel = np.full(max(t_max, 1), -1, np.int32)
+    rc = comp(b.ctypes.data if b.size else None, b.size, ctypes.byref(params), ctypes.byref(out), ctypes.byref(n),
+              sel.ctypes.data)
+    if rc != 0:
+        return rc, None, None
+    data = ctypes.string_at(out.value, n.value) if n.value else b""
+    free(out)
+    return 0, data, sel

@@ -1356,3 +1356,331 @@ void orc_quant_result_free(kv_compact_quant_result * r) {
     free(r->K_out); r->K_out = NULL;
     free(r->V_out); r->V_out = NULL;
 }
+
+/* ------------------------------------------------------------------------ */
+/* llama.cpp state blob: parse (state.h:104-222), the CLI's cross-layer      */
+/* selection and refit (kv-compact.cpp:380-690), and the compacted blob      */
+/* (build_compacted_state, state.h:645-810).                                 */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    int32_t k_type, v_type;
+    uint64_t k_size_row, v_size_row;
+    uint32_t v_size_el, n_embd_v_hdr;
+    int nk, nv;                /* elements per K / V row (V: [cell][nv] after the transpose) */
+    float * K;                 /* [cell][nk] */
+    float * V;                 /* [cell][nv] */
+} orc_layer;
+
+typedef struct {
+    uint32_t n_stream, cell_count, v_trans, n_layer;
+    int32_t * pos;             /* [cell] */
+    int32_t * ext;             /* [cell][2] (n_pos_per_embd > 1) */
+    uint32_t * n_seq;          /* [cell] */
+    int32_t ** seq;            /* [cell][n_seq] */
+    orc_layer * layers;
+    size_t kv_end;             /* offset of the trailing bytes */
+} orc_state;
+
+static void orc_state_release(orc_state * s) {
+    if (s->seq)
+        for (uint32_t c = 0; c < s->cell_count; c++) free(s->seq[c]);
+    if (s->layers)
+        for (uint32_t l = 0; l < s->n_layer; l++) { free(s->layers[l].K); free(s->layers[l].V); }
+    free(s->pos); free(s->ext); free(s->n_seq); free(s->seq); free(s->layers);
+    memset(s, 0, sizeof(*s));
+}
+
+static int rd(const uint8_t ** p, const uint8_t * end, void * v, size_t n) {
+    if ((size_t)(end - *p) < n) return 0;
+    memcpy(v, *p, n);
+    *p += n;
+    return 1;
+}
+
+/* parsed_kv_state::parse (state.h:104-222). Returns 1 on success. Streams
+ * after the first must be empty (only stream 0 is kept here); a non-empty one
+ * sets *extra_streams. */
+static int orc_state_parse(const uint8_t * data, size_t size, uint32_t n_pos, orc_state * s, int * extra_streams) {
+    const uint8_t * p = data;
+    const uint8_t * end = data + size;
+    memset(s, 0, sizeof(*s));
+    *extra_streams = 0;
+    if (!rd(&p, end, &s->n_stream, 4)) return 0;
+    for (uint32_t st = 0; st < s->n_stream; st++) {
+        uint32_t cc;
+        if (!rd(&p, end, &cc, 4)) return 0;
+        if (cc == 0) continue;
+        if (st > 0) { *extra_streams = 1; return 1; }   /* only stream 0 may hold cells */
+        s->cell_count = cc;
+        s->pos = (int32_t *)calloc(cc, 4);
+        s->ext = (int32_t *)calloc((size_t)cc * 2, 4);
+        s->n_seq = (uint32_t *)calloc(cc, 4);
+        s->seq = (int32_t **)calloc(cc, sizeof(int32_t *));
+        for (uint32_t c = 0; c < cc; c++) {
+            if (!rd(&p, end, &s->pos[c], 4)) return 0;
+            if (!rd(&p, end, &s->n_seq[c], 4)) return 0;
+            if (n_pos > 1) {
+                if (!rd(&p, end, &s->ext[2 * c], 4)) return 0;
+                if (!rd(&p, end, &s->ext[2 * c + 1], 4)) return 0;
+            }
+            /* each id needs 4 bytes: a count beyond the blob fails below */
+            if ((size_t)(end - p) / 4 < s->n_seq[c]) return 0;
+            s->seq[c] = (int32_t *)malloc((size_t)(s->n_seq[c] ? s->n_seq[c] : 1) * 4);
+            for (uint32_t i = 0; i < s->n_seq[c]; i++)
+                if (!rd(&p, end, &s->seq[c][i], 4)) return 0;
+        }
+        if (!rd(&p, end, &s->v_trans, 4)) return 0;
+        if (!rd(&p, end, &s->n_layer, 4)) return 0;
+        s->layers = (orc_layer *)calloc(s->n_layer ? s->n_layer : 1, sizeof(orc_layer));
+        for (uint32_t l = 0; l < s->n_layer; l++) {
+            orc_layer * ld = &s->layers[l];
+            if (!rd(&p, end, &ld->k_type, 4)) return 0;
+            if (!rd(&p, end, &ld->k_size_row, 8)) return 0;
+            const uint64_t bytes = (uint64_t)cc * ld->k_size_row;
+            if ((uint64_t)(end - p) < bytes) return 0;
+            ld->nk = orc_quant_row_elements(ld->k_type, (size_t)ld->k_size_row);
+            ld->K = (float *)malloc(((size_t)cc * ld->nk + 1) * sizeof(float));
+            for (uint32_t c = 0; c < cc; c++)
+                convert_to_f32(p + (size_t)c * ld->k_size_row, ld->k_type, ld->K + (size_t)c * ld->nk, (size_t)ld->nk);
+            p += bytes;
+        }
+        for (uint32_t l = 0; l < s->n_layer; l++) {
+            orc_layer * ld = &s->layers[l];
+            if (!rd(&p, end, &ld->v_type, 4)) return 0;
+            if (!s->v_trans) {
+                if (!rd(&p, end, &ld->v_size_row, 8)) return 0;
+                const uint64_t bytes = (uint64_t)cc * ld->v_size_row;
+                if ((uint64_t)(end - p) < bytes) return 0;
+                ld->nv = orc_quant_row_elements(ld->v_type, (size_t)ld->v_size_row);
+                ld->V = (float *)malloc(((size_t)cc * ld->nv + 1) * sizeof(float));
+                for (uint32_t c = 0; c < cc; c++)
+                    convert_to_f32(p + (size_t)c * ld->v_size_row, ld->v_type, ld->V + (size_t)c * ld->nv,
+                                   (size_t)ld->nv);
+                p += bytes;
+            } else {
+                /* [embd][cell] storage: decoded as one flat run of
+                 * n_embd * cell values, then transposed (state.h:425-462) */
+                if (!rd(&p, end, &ld->v_size_el, 4)) return 0;
+                if (!rd(&p, end, &ld->n_embd_v_hdr, 4)) return 0;
+                const uint64_t bytes = (uint64_t)ld->n_embd_v_hdr * cc * ld->v_size_el;
+                if ((uint64_t)(end - p) < bytes) return 0;
+                const size_t n = (size_t)ld->n_embd_v_hdr * cc;
+                ld->nv = (int)ld->n_embd_v_hdr;
+                float * tmp = (float *)calloc(n + 1, sizeof(float));
+                convert_to_f32(p, ld->v_type, tmp, n);
+                ld->V = (float *)malloc((n + 1) * sizeof(float));
+                for (uint32_t d = 0; d < ld->n_embd_v_hdr; d++)
+                    for (uint32_t c = 0; c < cc; c++) ld->V[(size_t)c * ld->nv + d] = tmp[(size_t)d * cc + c];
+                free(tmp);
+                p += bytes;
+            }
+        }
+    }
+    s->kv_end = (size_t)(p - data);
+    return 1;
+}
+
+int orc_state_parse_info(const uint8_t * blob, size_t size, uint32_t n_pos, kvc_state_info * info) {
+    if (!blob || !info) return -1;
+    orc_state s;
+    int extra = 0;
+    if (!orc_state_parse(blob, size, n_pos, &s, &extra)) { orc_state_release(&s); return -2; }
+    memset(info, 0, sizeof(*info));
+    if (extra) { orc_state_release(&s); return KV_COMPACT_E_UNSUPPORTED; }
+    info->n_stream = s.n_stream;
+    info->cell_count = s.cell_count;
+    info->v_trans = s.v_trans;
+    info->n_layer = s.n_layer;
+    if (s.n_layer > 0) { info->n_embd_k = s.layers[0].nk; info->n_embd_v = s.layers[0].nv; }
+    info->kv_bytes = s.kv_end;
+    info->trailing_bytes = size - s.kv_end;
+    orc_state_release(&s);
+    return 0;
+}
+
+typedef struct { uint8_t * p; size_t n, cap; } orc_buf;
+
+static void put(orc_buf * b, const void * v, size_t n) {
+    if (b->n + n > b->cap) {
+        size_t c = b->cap ? b->cap : 4096;
+        while (c < b->n + n) c *= 2;
+        b->p = (uint8_t *)realloc(b->p, c);
+        b->cap = c;
+    }
+    memcpy(b->p + b->n, v, n);
+    b->n += n;
+}
+
+static int state_type_ok(int32_t t) {
+    return t == KV_TYPE_F32 || t == KV_TYPE_F16 || t == KV_TYPE_Q8_0 || t == KV_TYPE_Q4_0 || t == KV_TYPE_Q4_1;
+}
+
+/* The CLI's compaction of stream 0 (kv-compact.cpp:380-690) and the blob
+ * writer (state.h:645-810). beta is 0 for every kept cell (the CLI never fits
+ * it, kv-compact.cpp:611) but the writer still adds (beta * sqrtf(d_k)) *
+ * direction to each kept key, so the directions are computed. */
+int orc_state_compact(const uint8_t * blob, size_t size, const kvc_state_params * sp,
+                      uint8_t ** out, size_t * out_size, int32_t * sel_out) {
+    if (!blob || !sp || !out || !out_size) return -1;
+    orc_state s;
+    int extra = 0;
+    if (!orc_state_parse(blob, size, sp->n_pos_per_embd, &s, &extra)) { orc_state_release(&s); return -2; }
+    if (extra) { orc_state_release(&s); return KV_COMPACT_E_UNSUPPORTED; }
+    if (s.cell_count == 0 || s.n_layer == 0) { orc_state_release(&s); return -2; }
+    const int T = (int)s.cell_count, L = (int)s.n_layer, H = sp->n_head_kv;
+    const int nk = s.layers[0].nk, nv = s.layers[0].nv;
+    if (H <= 0 || nk <= 0 || nv <= 0 || nk % H || nv % H) { orc_state_release(&s); return -2; }
+    for (int l = 0; l < L; l++) {
+        const orc_layer * ld = &s.layers[l];
+        if (!state_type_ok(ld->k_type) || !state_type_ok(ld->v_type) || ld->nk != nk || ld->nv != nv) {
+            orc_state_release(&s);
+            return KV_COMPACT_E_UNSUPPORTED;
+        }
+    }
+    const int dk = nk / H, dv = nv / H;
+    int t = (int)(T * sp->compact_ratio);   /* kv-compact.cpp:269 */
+    if (t < 1) t = 1;
+    int nq = sp->n_ref_queries;             /* kv-compact.cpp:274-277 */
+    if (nq <= 0) nq = T / 4 > 16 ? T / 4 : 16;
+    if (nq > T) nq = T;
+    if (t > T) { orc_state_release(&s); return -2; }
+    if (nq > 8192) { orc_state_release(&s); return KV_COMPACT_E_UNSUPPORTED; }
+    const int ref_start = T - nq;
+    const float inv_sqrt = 1.0f / sqrtf((float)dk);
+    unsigned char * on = (unsigned char *)malloc((size_t)L);
+    for (int l = 0; l < L; l++) on[l] = sp->layer_filter ? (sp->layer_filter(l, L, sp->layer_filter_data) != 0) : 1;
+
+    /* scores, softmax and importance per (layer, head); global importance as
+     * the max over all of them (0 start) or the sensitivity-weighted sum in
+     * (layer, head) order (kv-compact.cpp:500-571) */
+    float * S = (float *)malloc((size_t)L * H * nq * T * sizeof(float));
+    float * A = (float *)malloc((size_t)L * H * nq * T * sizeof(float));
+    float * himp = (float *)malloc((size_t)L * H * T * sizeof(float));
+    float * sens = (float *)malloc((size_t)L * H * sizeof(float));
+    float * gimp = (float *)calloc((size_t)T, sizeof(float));
+    int n_heads = 0;
+    for (int l = 0; l < L; l++) {
+        if (!on[l]) continue;
+        const float * K = s.layers[l].K;
+        for (int h = 0; h < H; h++) {
+            const size_t o = ((size_t)l * H + h) * nq * T;
+            float * ih = himp + (size_t)n_heads * T;
+            orc_scores(K + (size_t)ref_start * nk + (size_t)h * dk, K + (size_t)h * dk, S + o, nq, T, dk, nk, nk,
+                       inv_sqrt);
+            orc_softmax_importance(S + o, A + o, ih, NULL, NULL, nq, T, 0);
+            if (sp->sensitivity_budget) sens[n_heads] = orc_head_sensitivity(A + o, nq, T);
+            else for (int j = 0; j < T; j++) if (ih[j] > gimp[j]) gimp[j] = ih[j];
+            n_heads++;
+        }
+    }
+    if (sp->sensitivity_budget)
+        for (int k = 0; k < n_heads; k++)
+            for (int j = 0; j < T; j++) gimp[j] += sens[k] * himp[(size_t)k * T + j];
+    int * sel = (int *)malloc((size_t)t * sizeof(int));
+    orc_select_topk(gimp, T, t, 0, sel);   /* partial_sort + sort, kv-compact.cpp:573-582 */
+    if (sel_out) for (int j = 0; j < t; j++) sel_out[j] = sel[j];
+
+    /* values (kv-compact.cpp:594-635) and beta directions (kv-compact.cpp:659-685) */
+    float * cv = (float *)malloc((size_t)L * H * t * dv * sizeof(float));
+    float * dir = (float *)calloc((size_t)L * H * dk, sizeof(float));
+    float * X = (float *)malloc((size_t)nq * t * sizeof(float));
+    float * Y = (float *)malloc((size_t)nq * dv * sizeof(float));
+    float * Qh = (float *)malloc((size_t)nq * dk * sizeof(float));
+    float * ones = (float *)malloc((size_t)nq * sizeof(float));
+    for (int i = 0; i < nq; i++) ones[i] = 1.0f;
+    for (int l = 0; l < L; l++) {
+        const orc_layer * ld = &s.layers[l];
+        for (int h = 0; h < H; h++) {
+            float * c = cv + ((size_t)l * H + h) * t * dv;
+            if (!on[l]) {
+                for (int j = 0; j < t; j++)
+                    memcpy(c + (size_t)j * dv, ld->V + (size_t)sel[j] * nv + (size_t)h * dv, (size_t)dv * 4);
+                continue;
+            }
+            const size_t o = ((size_t)l * H + h) * nq * T;
+            for (int i = 0; i < nq; i++)
+                for (int j = 0; j < t; j++) X[(size_t)i * t + j] = S[o + (size_t)i * T + sel[j]] + 0.0f;
+            orc_softmax_rows(X, nq, t);
+            for (int i = 0; i < nq; i++)
+                for (int e = 0; e < dv; e++) {
+                    float acc = 0.0f;
+                    for (int j = 0; j < T; j++)
+                        acc += A[o + (size_t)i * T + j] * ld->V[(size_t)j * nv + (size_t)h * dv + e];
+                    Y[(size_t)i * dv + e] = acc;
+                }
+            orc_ls_solve(X, Y, c, nq, t, dv, 1e-6f);
+            for (int i = 0; i < nq; i++)
+                memcpy(Qh + (size_t)i * dk, ld->K + (size_t)(ref_start + i) * nk + (size_t)h * dk, (size_t)dk * 4);
+            orc_ls_solve(Qh, ones, dir + ((size_t)l * H + h) * dk, nq, dk, 1, 1e-6f);
+        }
+    }
+
+    /* the compacted blob, state.h:645-810 */
+    orc_buf b = {0};
+    put(&b, &s.n_stream, 4);
+    const uint32_t tc = (uint32_t)t;
+    put(&b, &tc, 4);
+    for (int j = 0; j < t; j++) {
+        const int c = sel[j];
+        put(&b, &s.pos[c], 4);
+        put(&b, &s.n_seq[c], 4);
+        if (sp->n_pos_per_embd > 1) put(&b, &s.ext[2 * c], 8);
+        put(&b, s.seq[c], (size_t)s.n_seq[c] * 4);
+    }
+    put(&b, &s.v_trans, 4);
+    put(&b, &s.n_layer, 4);
+    const float scale = sqrtf((float)dk);
+    float * row = (float *)malloc((size_t)(nk > nv ? nk : nv) * sizeof(float) + 4);
+    uint8_t * rb = (uint8_t *)malloc((size_t)(nk > nv ? nk : nv) * 4 + (size_t)t * 4 + 64);
+    for (int l = 0; l < L; l++) {
+        const orc_layer * ld = &s.layers[l];
+        put(&b, &ld->k_type, 4);
+        put(&b, &ld->k_size_row, 8);
+        for (int j = 0; j < t; j++) {
+            memcpy(row, ld->K + (size_t)sel[j] * nk, (size_t)nk * 4);
+            for (int h = 0; h < H; h++) {
+                const float bs = 0.0f * scale;
+                const float * dh = dir + ((size_t)l * H + h) * dk;
+                for (int d = 0; d < dk; d++) row[h * dk + d] += bs * dh[d];
+            }
+            put(&b, rb, orc_quantize_row(row, ld->k_type, nk, rb));
+        }
+    }
+    for (int l = 0; l < L; l++) {
+        const orc_layer * ld = &s.layers[l];
+        put(&b, &ld->v_type, 4);
+        if (!s.v_trans) {
+            put(&b, &ld->v_size_row, 8);
+            for (int j = 0; j < t; j++) {
+                for (int h = 0; h < H; h++)
+                    memcpy(row + (size_t)h * dv, cv + (((size_t)l * H + h) * t + j) * dv, (size_t)dv * 4);
+                put(&b, rb, orc_quantize_row(row, ld->v_type, nv, rb));
+            }
+        } else {
+            put(&b, &ld->v_size_el, 4);
+            const uint32_t ne = (uint32_t)(H * dv);
+            put(&b, &ne, 4);
+            float * col = (float *)malloc((size_t)t * sizeof(float));
+            for (uint32_t d = 0; d < ne; d++) {
+                const int h = (int)d / dv, e = (int)d % dv;
+                for (int j = 0; j < t; j++) col[j] = cv[(((size_t)l * H + h) * t + j) * dv + e];
+                if (ld->v_type == KV_TYPE_F32 || ld->v_type == KV_TYPE_F16 || ld->v_type == KV_TYPE_Q8_0 ||
+                    ld->v_type == KV_TYPE_Q4_0 || ld->v_type == KV_TYPE_Q4_1)
+                    put(&b, rb, orc_quantize_row(col, ld->v_type, t, rb));
+            }
+            free(col);
+        }
+    }
+    const uint32_t zero = 0;   /* the other (empty) streams */
+    for (uint32_t st = 1; st < s.n_stream; st++) put(&b, &zero, 4);
+    if (size > s.kv_end) put(&b, blob + s.kv_end, size - s.kv_end);
+    *out = b.p;
+    *out_size = b.n;
+    free(row); free(rb); free(on); free(S); free(A); free(himp); free(sens); free(gimp); free(sel);
+    free(cv); free(dir); free(X); free(Y); free(Qh); free(ones);
+    orc_state_release(&s);
+    return 0;
+}
+
+void orc_state_free(uint8_t * p) { free(p); }

@@ -19,6 +19,7 @@
 #include <stddef.h>
 #include <stdint.h>
 #include "../include/kv-compact-api.h"
+#include "../include/kv-compact-state.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -73,6 +74,12 @@ void  orc_quality_stats(const float * K, const float * V, const float * Q, int T
  * by orc_chunk_t(); exact float arithmetic of reference api.cpp:396-437 */
 int   orc_chunk_plan(int T, const kv_compact_params * p, int * chunk_size_out);
 int   orc_target_count(int T, const kv_compact_params * p);
+
+/* llama.cpp state blob compaction (state.h:104-222, 645-810; kv-compact.cpp:380-690) */
+int  orc_state_parse_info(const uint8_t * blob, size_t size, uint32_t n_pos_per_embd, kvc_state_info * info);
+int  orc_state_compact(const uint8_t * blob, size_t size, const kvc_state_params * sp,
+                       uint8_t ** out, size_t * out_size, int32_t * selected);
+void orc_state_free(uint8_t * p);
 
 #ifdef __cplusplus
 }

@@ -3,7 +3,8 @@
 Run in the container that holds the reference checkout, after
 `make -C oracle ref` has compiled it into oracle/_ref/:
 
-    python tests/golden/gen_golden.py
+    python tests/golden/gen_golden.py          (everything)
+    python tests/golden/gen_golden.py state    (the state blob cases only)
 
 Inputs are regenerated from seeds by tests/kvc_data.py (integer-only
 generator), so each fixture stores only the reference's outputs plus an
@@ -69,7 +70,31 @@ def codec_vectors():
     return np.stack(rows).astype(np.float32)
 
 
+def write_state_fixtures():
+    """llama.cpp state blob cases through the reference's own parse/build
+    (oracle/_ref harness, the CLI's call sequence): kept cells, output size and
+    SHA-256 of the compacted blob (the inputs regenerate from their seeds)."""
+    import hashlib
+
+    from kvc_data import STATE_CASES, state_blob
+    from kvc_harness import ref_state_compact
+    out = {}
+    for c in STATE_CASES:
+        blob = state_blob(c)
+        rc, data, sel = ref_state_compact(blob, c)
+        assert rc == 0, c["name"]
+        out[c["name"] + "_sel"] = sel.astype(np.int32)
+        out[c["name"] + "_size"] = np.int64(len(data))
+        out[c["name"] + "_sha256"] = np.array(hashlib.sha256(data).hexdigest())
+        out[c["name"] + "_input_sha256"] = np.array(hashlib.sha256(blob).hexdigest())
+    np.savez_compressed(HERE / "state_cases.npz", **out)
+    print("wrote", len(STATE_CASES), "state cases")
+
+
 def main():
+    if len(sys.argv) > 1 and sys.argv[1] == "state":
+        write_state_fixtures()
+        return
     ref = load_ref()
     if ref is None:
         raise SystemExit("oracle/_ref/libkvref.so missing: run `make -C oracle ref` first")
@@ -147,6 +172,7 @@ def main():
     blocks["f32_to_f16_in"] = probe
     blocks["f32_to_f16_out"] = np.array([h.ref_f32_to_f16(float(v)) for v in probe], np.uint16)
     np.savez_compressed(HERE / "blocks.npz", **blocks)
+    write_state_fixtures()
     print("wrote", len(out), "cases,", len(QUANT_CASES), "quantized cases, multi-round and blocks")
 
 

@@ -415,3 +415,109 @@ def option_variant(name: str):
     if name == "omp_cheap_chunk":
         return cheap(1800, 2, 32, 60, target_ratio=0.2, use_omp=1, omp_k_choice=3, use_sensitivity=1)
     raise KeyError(name)
+
+
+# -- llama.cpp state blobs (include/kv-compact-state.h layout) -------------------
+# Synthetic blobs in the format llama_state_seq_get_data writes, built from the
+# seeded generator: encoded payloads are drawn directly (random int8 / nibbles
+# with positive f16 scales for the block codecs, f16 / f32 of normal values
+# with some exact -0 and +0 entries), so every decode path is exercised.
+T_F32, T_F16, T_Q4_0, T_Q4_1, T_Q8_0 = 0, 1, 2, 3, 8
+_BLOCK = {T_Q8_0: 34, T_Q4_0: 18, T_Q4_1: 20}
+
+
+def _u8(seed, n):
+    return (splitmix64(seed, n) & 0xFF).astype(np.uint8)
+
+
+def _payload(typ: int, n_el: int, rows: int, seed: int) -> bytes:
+    """rows x n_el values of `typ`, row-major bytes."""
+    if typ in (T_F32, T_F16):
+        x = normal(seed, (rows, n_el))
+        z = _u8(seed + 1, rows * n_el).reshape(rows, n_el)
+        x = np.where(z < 6, np.float32(-0.0), np.where(z < 9, np.float32(0.0), x)).astype(np.float32)
+        return (x if typ == T_F32 else x.astype(np.float16)).tobytes()
+    nb = n_el // 32
+    bb = _BLOCK[typ]
+    raw = _u8(seed, rows * nb * bb).reshape(rows * nb, bb)
+    d = (np.abs(normal(seed + 2, (rows * nb,))) * 0.05 + 0.01).astype(np.float16)
+    raw[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    if typ == T_Q4_1:
+        m = (normal(seed + 3, (rows * nb,)) * 0.3).astype(np.float16)
+        raw[:, 2:4] = m.view(np.uint8).reshape(-1, 2)
+    return raw.tobytes()
+
+
+def state_blob(c: dict) -> bytes:
+    """Blob for a state case dict: T, L, H, dk, dv, kt, vt, vtrans, n_pos, seed,
+    optional n_stream (extra streams empty unless extra_cells), trailing."""
+    import struct
+    T, L, H, dk, dv = c["T"], c["L"], c["H"], c["dk"], c["dv"]
+    seed, n_pos = c["seed"], c.get("n_pos", 1)
+    nk, nv = H * dk, H * dv
+    out = bytearray()
+    n_stream = c.get("n_stream", 1)
+    out += struct.pack("<I", n_stream)
+    out += struct.pack("<I", T)
+    z = splitmix64(seed * 7 + 1, 4 * T)
+    for i in range(T):
+        ns = 1 + int(z[i] % 3)
+        out += struct.pack("<iI", i + int(c.get("pos0", 0)), ns)
+        if n_pos > 1:
+            out += struct.pack("<ii", int(z[T + i] % 64), int(z[2 * T + i] % 64))
+        for k in range(ns):
+            out += struct.pack("<i", int((z[3 * T + i] >> (8 * k)) % 8))
+    out += struct.pack("<II", int(c["vtrans"]), L)
+    for l in range(L):
+        kt = c["kt"][l] if isinstance(c["kt"], (list, tuple)) else c["kt"]
+        rb = nk * 4 if kt == T_F32 else nk * 2 if kt == T_F16 else nk // 32 * _BLOCK[kt]
+        out += struct.pack("<iQ", kt, rb)
+        out += _payload(kt, nk, T, seed * 101 + l)
+    for l in range(L):
+        vt = c["vt"][l] if isinstance(c["vt"], (list, tuple)) else c["vt"]
+        if not c["vtrans"]:
+            rb = nv * 4 if vt == T_F32 else nv * 2 if vt == T_F16 else nv // 32 * _BLOCK[vt]
+            out += struct.pack("<iQ", vt, rb)
+            out += _payload(vt, nv, T, seed * 211 + l)
+        else:
+            # [embd][cell]: v_size_el is the element size (f32 / f16) or, for
+            # block codecs, the block size (as llama.cpp's ggml_type_size)
+            el = 4 if vt == T_F32 else 2 if vt == T_F16 else _BLOCK[vt]
+            out += struct.pack("<iII", vt, el, nv)
+            if vt in (T_F32, T_F16):
+                out += _payload(vt, T, nv, seed * 307 + l)
+            else:
+                body = bytearray(nv * T * el)
+                enc = _payload(vt, nv * T // 32 * 32, 1, seed * 307 + l) if nv * T >= 32 else b""
+                body[:len(enc)] = enc
+                out += bytes(body)
+    for s in range(1, n_stream):
+        ec = c.get("extra_cells", 0) if s == 1 else 0
+        out += struct.pack("<I", ec)
+        if ec:
+            for i in range(ec):
+                out += struct.pack("<iIi", i, 1, 0)
+            out += struct.pack("<II", 0, 0)
+    out += bytes(c.get("trailing", b""))
+    return bytes(out)
+
+
+STATE_CASES = [
+    dict(name="f16_basic", T=300, L=3, H=2, dk=32, dv=32, kt=T_F16, vt=T_F16, vtrans=0, seed=61, ratio=0.2),
+    dict(name="q8_vtrans_f16", T=257, L=2, H=2, dk=64, dv=64, kt=T_Q8_0, vt=T_F16, vtrans=1, seed=62, ratio=0.3),
+    dict(name="imrope_q4_trailing", T=200, L=2, H=4, dk=32, dv=32, kt=T_Q4_0, vt=T_Q4_1, vtrans=0, n_pos=4,
+         seed=63, ratio=0.25, trailing=bytes(range(37))),
+    dict(name="f32_sens_nref", T=240, L=3, H=2, dk=32, dv=32, kt=T_F32, vt=T_F32, vtrans=0, seed=64, ratio=0.2,
+         sens=1, n_ref=40),
+    dict(name="q8_filter", T=220, L=3, H=2, dk=64, dv=64, kt=T_Q8_0, vt=T_Q8_0, vtrans=0, seed=65, ratio=0.2,
+         layers=[0, 2]),
+    dict(name="vtrans_q8_flat", T=160, L=2, H=1, dk=32, dv=32, kt=T_F16, vt=T_Q8_0, vtrans=1, seed=66, ratio=0.3),
+    dict(name="two_streams_dk_ne_dv", T=180, L=2, H=2, dk=64, dv=32, kt=T_F16, vt=T_F32, vtrans=1, seed=67,
+         ratio=0.2, n_stream=2),
+    dict(name="mixed_types_sens", T=260, L=4, H=2, dk=32, dv=32, kt=[T_F16, T_Q8_0, T_Q4_1, T_F32],
+         vt=[T_Q4_0, T_F16, T_Q8_0, T_F32], vtrans=0, seed=68, ratio=0.15, sens=1),
+    dict(name="t1_small", T=20, L=1, H=1, dk=32, dv=32, kt=T_F16, vt=T_F16, vtrans=1, seed=69, ratio=0.01),
+    dict(name="large_nref", T=1200, L=2, H=2, dk=64, dv=64, kt=T_F16, vt=T_F16, vtrans=0, seed=70, ratio=0.1,
+         n_ref=300),
+]
+STATE_CASE_BY_NAME = {c["name"]: c for c in STATE_CASES}

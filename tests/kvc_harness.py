@@ -67,3 +67,42 @@ def load_ref():
     if not REF_SO.exists():
         return None
     return kc.Lib(REF_SO)
+
+
+def state_case_params(c):
+    """(StateParams, keepalive) for a state case dict."""
+    return kc.state_params(c["ratio"], c["H"], n_ref=c.get("n_ref", 0), n_pos=c.get("n_pos", 1),
+                           sens=c.get("sens", 0), layers=c.get("layers"))
+
+
+def state_t(c):
+    """Kept cells of a state case: max(1, (int)(T * ratio)) in float32."""
+    return max(1, int(np.float32(c["T"]) * np.float32(c["ratio"])))
+
+
+def ref_state_compact(blob: bytes, c):
+    """The reference's own parse/build driven by the harness (CLI sequence)."""
+    if not REF_HARNESS_SO.exists():
+        return None
+    dll = ctypes.CDLL(str(REF_HARNESS_SO))
+    f = dll.ref_state_compact
+    f.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_int, ctypes.c_float, ctypes.c_int,
+                  ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.POINTER(ctypes.c_void_p),
+                  ctypes.POINTER(ctypes.c_size_t), ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    dll.ref_free.argtypes = [ctypes.c_void_p]
+    b = np.frombuffer(blob, np.uint8)
+    layers = c.get("layers")
+    la = np.asarray(layers if layers is not None else [0], np.int32)
+    out = ctypes.c_void_p()
+    n = ctypes.c_size_t(0)
+    t = state_t(c)
+    sel = np.full(t, -1, np.int32)
+    rc = f(b.ctypes.data, b.size, c.get("n_pos", 1), c["H"], c["ratio"], c.get("n_ref", 0), c.get("sens", 0),
+           la.ctypes.data, len(layers) if layers is not None else -1, ctypes.byref(out), ctypes.byref(n),
+           sel.ctypes.data)
+    if rc != 0:
+        return rc, None, None
+    data = ctypes.string_at(out.value, n.value)
+    dll.ref_free(out)
+    return 0, data, sel
