@@ -25,6 +25,7 @@
 #include "../../include/kv-compact-api.h"
 #include "../../include/kv-compact-accel.h"
 #include "../../include/kv-compact-device.h"
+#include "../../include/kv-compact-state.h"
 #include "kvc_common.h"
 #include "kvc_kernels.h"
 
@@ -473,7 +474,8 @@ int run_diversity(hipStream_t st, const Plan & pl, const kv_compact_params & p, 
 
 int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact_params & p,
               const BatchIO & io, Carver & carver, Timing * tm) {
-    if (pl.nq_max > 256) return KV_COMPACT_E_UNSUPPORTED;   // chunk softmax keeps <= 256 row sums on chip
+    // the chunk softmax keeps each row's maximum and scale in LDS, OMP its residuals
+    if (pl.nq_max > SOFTMAX_MAXQ || (p.use_omp && pl.nq_max > OMP_MAXQ)) return KV_COMPACT_E_UNSUPPORTED;
     // Lawson-Hanson keeps a system's passive set on one wave: refused before
     // anything is launched
     if (!p.skip_beta && p.nnls_method == 0 && pl.tc_max > 256) return KV_COMPACT_E_UNSUPPORTED;
@@ -1543,5 +1545,619 @@ void kvc_release_workspace(void) {
         c->arena_cap = 0;
     }
 }
+
+}  // extern "C"
+
+// ------------------------------------------------------- llama.cpp state blobs
+//
+// kvc_state_compact / _device: the reference CLI's compaction of a sequence
+// state (src/kv-compact.cpp:380-690) and its write-back blob
+// (build_compacted_state, include/kv-compact-state.h:645-810). The blob's
+// headers and cell records are walked on the host (parsed_kv_state::parse,
+// state.h:104-222); every K/V payload is decoded, compacted and re-encoded on
+// the device.
+namespace {
+
+// Reads of a blob in host or device memory; device reads go through a host
+// window so that the walk over headers and cell records costs few copies.
+struct BlobReader {
+    const uint8_t * p = nullptr;
+    size_t size = 0;
+    bool dev = false;
+    bool dev_err = false;
+    std::vector<uint8_t> win;
+    size_t win_off = 0, win_len = 0;
+    bool read(size_t off, void * dst, size_t n) {
+        if (off > size || n > size - off) return false;
+        if (!dev) {
+            memcpy(dst, p + off, n);
+            return true;
+        }
+        if (off < win_off || off + n > win_off + win_len) {
+            const size_t len = std::min(size - off, std::max(n, (size_t)1 << 20));
+            win.resize(len);
+            if (hipMemcpy(win.data(), p + off, len, hipMemcpyDeviceToHost) != hipSuccess) {
+                (void)hipGetLastError();
+                dev_err = true;
+                return false;
+            }
+            win_off = off;
+            win_len = len;
+        }
+        memcpy(dst, win.data() + (off - win_off), n);
+        return true;
+    }
+};
+
+struct StateLayer {
+    int32_t k_type = 0, v_type = 0;
+    uint64_t k_rb = 0, v_rb = 0;   // row bytes (V: row-major layout)
+    uint32_t v_el = 0, v_ne = 0;   // transposed V: element size, n_embd_v_gqa
+    size_t k_off = 0, v_off = 0;   // payload offsets in the blob
+    int nk = 0, nv = 0;            // elements per K / V row
+};
+
+struct StateLayout {
+    uint32_t n_stream = 0, cells = 0, v_trans = 0, n_layer = 0;
+    std::vector<size_t> cell_at;    // offset of each cell record
+    std::vector<uint32_t> cell_len; // its bytes: pos, n_seq_id, [x, y], seq ids
+    std::vector<StateLayer> layers;
+    size_t kv_end = 0;
+    bool extra_streams = false;     // a stream after the first holds cells
+};
+
+// elements per row of a stored type (state.h:342-352)
+int state_row_elements(int32_t type, uint64_t rb) {
+    if (type == KV_TYPE_F32) return (int)(rb / 4);
+    if (type == KV_TYPE_F16) return (int)(rb / 2);
+    if (is_block_type(type)) return (int)(rb / (uint64_t)block_bytes(type)) * 32;
+    return (int)(rb / 4);
+}
+
+bool state_type_ok(int32_t t) {
+    return t == KV_TYPE_F32 || t == KV_TYPE_F16 || is_block_type(t);
+}
+
+// parsed_kv_state::parse (state.h:104-222) without the payload decode.
+// 0, -2 malformed, -6 device read failed. Stops at a second stream that holds
+// cells (extra_streams).
+int parse_state(BlobReader & r, uint32_t n_pos, StateLayout & s) {
+    size_t off = 0;
+    auto rd = [&](void * v, size_t n) {
+        if (!r.read(off, v, n)) return false;
+        off += n;
+        return true;
+    };
+    auto fail = [&]() { return r.dev_err ? KV_COMPACT_E_DEVICE : -2; };
+    if (!rd(&s.n_stream, 4)) return fail();
+    for (uint32_t st = 0; st < s.n_stream; st++) {
+        uint32_t cc = 0;
+        if (!rd(&cc, 4)) return fail();
+        if (cc == 0) continue;
+        if (st > 0) {
+            s.extra_streams = true;
+            return 0;
+        }
+        s.cells = cc;
+        s.cell_at.resize(cc);
+        s.cell_len.resize(cc);
+        for (uint32_t c = 0; c < cc; c++) {
+            s.cell_at[c] = off;
+            int32_t pos = 0;
+            uint32_t ns = 0;
+            if (!rd(&pos, 4) || !rd(&ns, 4)) return fail();
+            if (n_pos > 1) off += 8;
+            if (off > r.size || (r.size - off) / 4 < ns) return fail();
+            off += (size_t)ns * 4;
+            s.cell_len[c] = (uint32_t)(off - s.cell_at[c]);
+        }
+        if (!rd(&s.v_trans, 4) || !rd(&s.n_layer, 4)) return fail();
+        s.layers.assign(s.n_layer, StateLayer());
+        for (uint32_t l = 0; l < s.n_layer; l++) {
+            StateLayer & ld = s.layers[l];
+            if (!rd(&ld.k_type, 4) || !rd(&ld.k_rb, 8)) return fail();
+            const uint64_t bytes = (uint64_t)cc * ld.k_rb;
+            if (ld.k_rb != 0 && bytes / ld.k_rb != cc) return -2;
+            if (bytes > r.size - off) return -2;
+            ld.nk = state_row_elements(ld.k_type, ld.k_rb);
+            ld.k_off = off;
+            off += bytes;
+        }
+        for (uint32_t l = 0; l < s.n_layer; l++) {
+            StateLayer & ld = s.layers[l];
+            if (!rd(&ld.v_type, 4)) return fail();
+            if (!s.v_trans) {
+                if (!rd(&ld.v_rb, 8)) return fail();
+                const uint64_t bytes = (uint64_t)cc * ld.v_rb;
+                if (ld.v_rb != 0 && bytes / ld.v_rb != cc) return -2;
+                if (bytes > r.size - off) return -2;
+                ld.nv = state_row_elements(ld.v_type, ld.v_rb);
+                ld.v_off = off;
+                off += bytes;
+            } else {
+                if (!rd(&ld.v_el, 4) || !rd(&ld.v_ne, 4)) return fail();
+                const uint64_t bytes = (uint64_t)ld.v_ne * cc * ld.v_el;
+                if (bytes > r.size - off) return -2;
+                // the flat decode must stay inside the section (a smaller
+                // v_size_el would make the reference read past it)
+                if ((uint64_t)ld.v_ne * cc >= (1ULL << 31) ||
+                    (uint64_t)kv_quant_row_bytes(ld.v_type, (int)((uint64_t)ld.v_ne * cc)) > bytes)
+                    return -2;
+                ld.nv = (int)ld.v_ne;
+                ld.v_off = off;
+                off += bytes;
+            }
+        }
+    }
+    s.kv_end = off;
+    return 0;
+}
+
+size_t row_written(int32_t type, int n) { return (size_t)kv_quant_row_bytes(type, n); }
+
+// The output blob's sections (state.h:660-808), laid out from the parse and
+// the kept cells.
+struct StateOut {
+    size_t cells_off = 0, total = 0;
+    std::vector<size_t> k_hdr, k_pay, v_hdr, v_pay;   // per layer
+    std::vector<size_t> k_w, v_w;                     // bytes per written row (V transposed: per column)
+    size_t tail_off = 0;                              // empty streams, then the trailing bytes
+};
+
+StateOut plan_state_out(const StateLayout & s, const std::vector<int> & sel, int t, int H, int dv, size_t size) {
+    StateOut o;
+    size_t off = 8;   // n_stream, t
+    o.cells_off = off;
+    for (int j = 0; j < t; j++) off += s.cell_len[sel[j]];
+    off += 8;         // v_trans, n_layer
+    const int L = (int)s.n_layer;
+    o.k_hdr.resize(L); o.k_pay.resize(L); o.v_hdr.resize(L); o.v_pay.resize(L);
+    o.k_w.resize(L); o.v_w.resize(L);
+    for (int l = 0; l < L; l++) {
+        const StateLayer & ld = s.layers[l];
+        o.k_hdr[l] = off;
+        o.k_pay[l] = off + 12;
+        o.k_w[l] = row_written(ld.k_type, ld.nk);
+        off += 12 + (size_t)t * o.k_w[l];
+    }
+    for (int l = 0; l < L; l++) {
+        const StateLayer & ld = s.layers[l];
+        o.v_hdr[l] = off;
+        o.v_pay[l] = off + 12;
+        if (!s.v_trans) {
+            o.v_w[l] = row_written(ld.v_type, ld.nv);
+            off += 12 + (size_t)t * o.v_w[l];
+        } else {
+            o.v_w[l] = row_written(ld.v_type, t);
+            off += 12 + (size_t)H * dv * o.v_w[l];
+        }
+    }
+    o.tail_off = off;
+    off += (size_t)(s.n_stream - 1) * 4 + (size - s.kv_end);
+    o.total = off;
+    return o;
+}
+
+// Decode one stored section into fp32 rows [T][n] (rows of rb bytes, or the
+// transposed [n][T] run decoded flat and transposed through tmp).
+void decode_rows(const uint8_t * src, int32_t type, uint64_t rb, int n, int T, float * dst, hipStream_t st) {
+    const bool even = ((reinterpret_cast<uintptr_t>(src) | rb) & 1) == 0;
+    if (codec8_ok(type, n) && even)
+        launch_dequant8(src, type, (long long)rb, 0, n, T, 1, dst, st);
+    else
+        launch_dequant_rows(src, type, (long long)rb, n, T, dst, st);
+}
+
+// rows [t][n] fp32 (gathered by idx, or in order when idx is null) into a
+// section of rows of w bytes
+void encode_rows(const float * src, long long ld, const int * idx, const int * iota, int32_t type, int n, int t,
+                 uint8_t * dst, size_t w, hipStream_t st) {
+    const bool even = ((reinterpret_cast<uintptr_t>(dst) | w) & 1) == 0;
+    const bool al = (reinterpret_cast<uintptr_t>(src) & 15) == 0 && (ld & 3) == 0;
+    if (codec8_ok(type, n) && even && al)
+        launch_requant8(src, 0, ld, idx ? idx : iota, 0, 0, 0, 1, type, n, t, 1, dst, (long long)w, 0, st);
+    else
+        launch_quant_rows(src, ld, idx, type, n, t, dst, (long long)w, st);
+}
+
+struct StateRun {
+    int rc = 0;
+    std::vector<int> sel;
+    size_t out_size = 0;
+};
+
+// The whole call: blob (host or device, `dev`), output to a host buffer
+// (*host_out, malloc'd) or to device memory (d_out, out_cap).
+StateRun state_compact_impl(const uint8_t * blob, size_t size, bool dev, const kvc_state_params & sp,
+                            void ** host_out, uint8_t * d_out, size_t out_cap, hipStream_t user_st) {
+    StateRun run;
+    auto done = [&](int rc) { run.rc = rc; return run; };
+    DeviceCtx * ctx = device_ctx();
+    if (!ctx) return done(KV_COMPACT_E_DEVICE);
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    hipStream_t st = user_st ? user_st : ctx->stream;
+    BlobReader rd;
+    rd.p = blob; rd.size = size; rd.dev = dev;
+    StateLayout s;
+    int rc = parse_state(rd, sp.n_pos_per_embd, s);
+    if (rc) return done(rc);
+    if (s.extra_streams) return done(KV_COMPACT_E_UNSUPPORTED);
+    if (s.cells == 0 || s.n_layer == 0) return done(-2);
+    const int T = (int)s.cells, L = (int)s.n_layer, H = sp.n_head_kv;
+    const int nk = s.layers[0].nk, nv = s.layers[0].nv;
+    if (H <= 0 || nk <= 0 || nv <= 0 || nk % H || nv % H) return done(-2);
+    for (const StateLayer & ld : s.layers)
+        if (!state_type_ok(ld.k_type) || !state_type_ok(ld.v_type) || ld.nk != nk || ld.nv != nv)
+            return done(KV_COMPACT_E_UNSUPPORTED);
+    const int dk = nk / H, dv = nv / H;
+    int t = (int)(T * sp.compact_ratio);
+    if (t < 1) t = 1;
+    int nq = sp.n_ref_queries;
+    if (nq <= 0) nq = std::max(16, T / 4);
+    nq = std::min(nq, T);
+    if (t > T) return done(-2);
+    if (nq > SOFTMAX_MAXQ) return done(KV_COMPACT_E_UNSUPPORTED);
+    if (s.v_trans && (long long)nv * T >= (1LL << 31)) return done(KV_COMPACT_E_UNSUPPORTED);
+    const int q0 = T - nq;
+    // compacted layers take the first slots of the fp32 caches, kept layers the rest
+    std::vector<int> slot(L), order;
+    for (int l = 0; l < L; l++)
+        if (!sp.layer_filter || sp.layer_filter(l, L, sp.layer_filter_data)) order.push_back(l);
+    const int Lc = (int)order.size();
+    for (int l = 0; l < L; l++)
+        if (!(!sp.layer_filter || sp.layer_filter(l, L, sp.layer_filter_data))) order.push_back(l);
+    for (int i = 0; i < L; i++) slot[order[i]] = i;
+
+    // plans: the compaction (one chunk of all T cells keeping t, nq queries)
+    // and the direction fits (d_k unknowns, nq rows, one right-hand side)
+    kv_compact_params p = defaults();
+    p.skip_beta = 1;
+    p.score_method = 0;
+    p.use_sensitivity = sp.sensitivity_budget ? 1 : 0;
+    Plan pl;
+    {
+        pl.T = T; pl.n_chunks = 1; pl.t_total = t; pl.nq_max = nq; pl.tc_max = t; pl.Tc_max = T;
+        pl.qmode = Q_PROVIDED; pl.nq_global = nq; pl.stats_qmode = Q_PROVIDED;
+        ChunkDesc d;
+        d.start = 0; d.Tc = T; d.tc = t; d.prefix = 0; d.nq = nq; d.off = 0;
+        pl.chunks = {d, d, d};
+        pl.chunks[2].Tc = t;
+    }
+    Plan pd;
+    {
+        pd.T = dk; pd.n_chunks = 1; pd.t_total = dk; pd.nq_max = nq; pd.tc_max = dk; pd.Tc_max = dk;
+        pd.qmode = Q_PROVIDED; pd.nq_global = nq; pd.stats_qmode = Q_PROVIDED;
+        ChunkDesc d;
+        d.start = 0; d.Tc = dk; d.tc = dk; d.prefix = 0; d.nq = nq; d.off = 0;
+        pd.chunks = {d, d, d};
+    }
+    BatchIO io{};
+    io.L = Lc; io.T = T; io.n_q = nq; io.H = H; io.dk = dk; io.dv = dv;
+    io.ldK = (long long)T * nk; io.ldV = (long long)T * nv; io.ldQ = (long long)T * nk;
+    BatchIO iod{};
+    iod.L = Lc; iod.T = dk; iod.n_q = nq; iod.H = H; iod.dk = dk; iod.dv = 1;
+    kv_compact_params pdp = defaults();
+    pdp.skip_beta = 1;
+
+    // arena: blob copy (host input), fp32 caches, outputs, then the two
+    // workspaces (the same carving sizes the arena and places the buffers)
+    struct Bufs {
+        uint8_t * blob = nullptr;
+        float * Kf = nullptr, * Vf = nullptr, * vt_tmp = nullptr;
+        int * idx = nullptr, * iota = nullptr;
+        float * zbeta = nullptr, * beta_c = nullptr, * Cv = nullptr, * stats = nullptr, * dirs = nullptr;
+        float * rows = nullptr, * cols = nullptr;
+        uint8_t * stage = nullptr;
+        Work w{}, wd{};
+    };
+    auto carve = [&](Carver & c, Bufs & b) {
+        if (!dev) b.blob = c.take<uint8_t>(size);
+        b.Kf = c.take<float>((size_t)L * T * nk);
+        b.Vf = c.take<float>((size_t)L * T * nv);
+        b.vt_tmp = s.v_trans ? c.take<float>((size_t)nv * T) : nullptr;
+        b.idx = c.take<int>((size_t)std::max(Lc, 1) * t);
+        b.iota = c.take<int>((size_t)t);
+        b.zbeta = c.take<float>((size_t)H * t);
+        b.beta_c = c.take<float>((size_t)std::max(Lc, 1) * H * t);
+        b.Cv = c.take<float>((size_t)std::max(Lc, 1) * H * t * dv);
+        b.stats = c.take<float>((size_t)std::max(Lc, 1) * 3);
+        b.dirs = c.take<float>((size_t)L * H * dk);
+        b.rows = c.take<float>((size_t)t * std::max(nk, nv));
+        b.cols = c.take<float>((size_t)nv * t);
+        b.stage = c.take<uint8_t>(size);   // the compacted blob is never larger than the input
+        if (Lc > 0) {
+            StatWork sw{};
+            workspace_bytes(pl, io, &p, &c, &b.w, &sw);
+            workspace_bytes(pd, iod, &pdp, &c, &b.wd, &sw);
+        }
+    };
+    Bufs b;
+    {
+        Carver sz;
+        Bufs dummy;
+        carve(sz, dummy);
+        if (!drain_second_stream(ctx, st)) return done(KV_COMPACT_E_DEVICE);
+        if (!ensure_arena(ctx, sz.off + 256)) return done(KV_COMPACT_E_DEVICE);
+        Carver c;
+        c.base = ctx->arena;
+        carve(c, b);
+    }
+    const uint8_t * dblob = blob;
+    if (!dev) {
+        if (hipMemcpyAsync(b.blob, blob, size, hipMemcpyHostToDevice, st) != hipSuccess)
+            return done(KV_COMPACT_E_DEVICE);
+        dblob = b.blob;
+    }
+    float * Kf = b.Kf, * Vf = b.Vf, * vt_tmp = b.vt_tmp, * zbeta = b.zbeta, * Cv = b.Cv, * dirs = b.dirs;
+    float * rows = b.rows, * cols = b.cols;
+    int * idx = b.idx, * iota = b.iota;
+    uint8_t * stage = b.stage;
+
+    // 1. decode every layer's K and V into fp32 rows (slot order)
+    (void)hipEventRecord(ctx->q_ev[0], st);
+    for (int l = 0; l < L; l++) {
+        const StateLayer & ld = s.layers[l];
+        float * kd = Kf + (size_t)slot[l] * T * nk;
+        float * vd = Vf + (size_t)slot[l] * T * nv;
+        decode_rows(dblob + ld.k_off, ld.k_type, ld.k_rb, nk, T, kd, st);
+        if (!s.v_trans) {
+            decode_rows(dblob + ld.v_off, ld.v_type, ld.v_rb, nv, T, vd, st);
+        } else {
+            // [nv][T] decoded as one flat run (state.h:447-453; a block-coded
+            // run leaves its last n % 32 values 0), then transposed
+            launch_fill_f32(vt_tmp, 0.0f, (long long)nv * T, st);
+            launch_dequant_rows(dblob + ld.v_off, ld.v_type, 0, nv * T, 1, vt_tmp, st);
+            launch_transpose(vt_tmp, nv, T, vd, st);
+        }
+    }
+    (void)hipEventRecord(ctx->q_ev[1], st);
+    launch_fill_f32(zbeta, 0.0f, (long long)H * t, st);
+    launch_fill_f32(dirs, 0.0f, (long long)L * H * dk, st);
+    launch_iota(iota, t, st);
+
+    // 2. scores, softmax and importance of the compacted layers; one global
+    //    importance over all their heads; top-t; values and directions
+    if (Lc > 0) {
+        io.K = Kf; io.V = Vf; io.Q = Kf + (size_t)q0 * nk;
+        io.indices = idx; io.Cv = Cv; io.stats = b.stats; io.beta = b.beta_c;
+        Work & w = b.w;
+        Work & wd = b.wd;
+        w.sel = idx;
+        w.wts = nullptr;
+        Geom g{};
+        g.L = Lc; g.T = T; g.H = H; g.dk = dk; g.dv = dv;
+        g.n_chunks = 1; g.t_total = t; g.nq_max = nq; g.tc_max = t; g.Tc_max = T;
+        g.qmode = Q_PROVIDED; g.nq_global = nq;
+        g.ldK = io.ldK; g.ldV = io.ldV; g.ldQ = io.ldQ;
+        g.score_method = 0;
+        g.inv_sqrt_dk = 1.0f / sqrtf((float)dk);
+        g.ridge = 1e-6f;   // least_squares_solve's default (math.h:463-464)
+        g.zero_val = 0.0f;
+        {
+            const char * e = getenv("KVC_LU_MASKED");
+            g.lu_masked = (e && e[0] == '1') ? 1 : 0;
+        }
+        std::vector<long long> aoff((size_t)Lc * H), doff((size_t)Lc * H);
+        for (size_t i = 0; i < aoff.size(); i++) {
+            aoff[i] = (long long)i * t * (t + dv);
+            doff[i] = (long long)i * dk * (dk + 1);
+        }
+        if (hipMemcpyAsync(w.chunks, pl.chunks.data(), pl.chunks.size() * sizeof(ChunkDesc), hipMemcpyHostToDevice,
+                           st) != hipSuccess ||
+            hipMemcpyAsync(w.aug_off, aoff.data(), aoff.size() * 8, hipMemcpyHostToDevice, st) != hipSuccess ||
+            hipMemcpyAsync(wd.chunks, pd.chunks.data(), pd.chunks.size() * sizeof(ChunkDesc), hipMemcpyHostToDevice,
+                           st) != hipSuccess ||
+            hipMemcpyAsync(wd.aug_off, doff.data(), doff.size() * 8, hipMemcpyHostToDevice, st) != hipSuccess)
+            return done(KV_COMPACT_E_DEVICE);
+        launch_fill_int(w.status, 0, 1, st);
+        launch_fill_int(wd.status, 0, 1, st);
+        launch_scores(g, w.chunks, 1, T, io.K, io.Q, w.S, H, nq, (long long)H * nq * T, (long long)nq * T, T,
+                      Q_PROVIDED, st, nullptr, nullptr, w.smax);
+        launch_chunk_softmax(g, w, st);
+        // every (layer, head) of the compacted layers as one head list
+        Geom gg = g;
+        gg.L = 1;
+        gg.H = Lc * H;
+        launch_global_importance(gg, w, st);
+        launch_select_topk(gg, w, st);
+        for (int l = 1; l < Lc; l++)
+            if (hipMemcpyAsync(idx + (size_t)l * t, idx, (size_t)t * 4, hipMemcpyDeviceToDevice, st) != hipSuccess)
+                return done(KV_COMPACT_E_DEVICE);
+        launch_refit_target(g, w, io.V, st);
+        launch_fill_f32(b.beta_c, 0.0f, (long long)Lc * H * t, st);
+        launch_ls_softmax(g, w, b.beta_c, st);
+        launch_ls_build(g, w, st, true);
+        launch_ge_lu(g, w, st, true);
+        launch_ge_solve(g, w, Cv, st);
+        // beta directions: ridge LS of each head's reference queries against 1
+        Geom gd{};
+        gd.L = Lc; gd.T = dk; gd.H = H; gd.dk = dk; gd.dv = 1;
+        gd.n_chunks = 1; gd.t_total = dk; gd.nq_max = nq; gd.tc_max = dk; gd.Tc_max = dk;
+        gd.qmode = Q_PROVIDED; gd.nq_global = nq;
+        gd.ridge = 1e-6f;
+        gd.zero_val = 0.0f;
+        gd.lu_masked = g.lu_masked;
+        launch_gather_qref(Kf, io.ldK, nk, q0, nq, H, dk, Lc, wd.X, st);
+        launch_fill_f32(wd.Y, 1.0f, (long long)Lc * H * nq, st);
+        launch_ls_build(gd, wd, st, true);
+        launch_ge_lu(gd, wd, st, true);
+        launch_ge_solve(gd, wd, dirs, st);   // slots 0 .. Lc - 1 are the compacted layers
+        int status[2] = {0, 0};
+        if (hipStreamSynchronize(st) != hipSuccess ||
+            hipMemcpy(&status[0], w.status, 4, hipMemcpyDeviceToHost) != hipSuccess ||
+            hipMemcpy(&status[1], wd.status, 4, hipMemcpyDeviceToHost) != hipSuccess) {
+            (void)hipGetLastError();
+            return done(KV_COMPACT_E_DEVICE);
+        }
+        if ((status[0] | status[1]) & 2) {
+            fprintf(stderr, "[kv-compact] LU step wait exceeded its bound\n");
+            return done(KV_COMPACT_E_DEVICE);
+        }
+        if (status[0] | status[1]) return done(KV_COMPACT_E_UNSUPPORTED);
+    } else {
+        // no layer compacted: the importance is 0 everywhere, and partial_sort
+        // over equal keys keeps the first t positions (its heap moves never
+        // bring in an element that does not compare greater)
+        run.sel.resize(t);
+        for (int j = 0; j < t; j++) run.sel[j] = j;
+        if (hipMemcpyAsync(idx, run.sel.data(), (size_t)t * 4, hipMemcpyHostToDevice, st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess)
+            return done(KV_COMPACT_E_DEVICE);
+    }
+    if (run.sel.empty()) {
+        run.sel.resize(t);
+        if (hipMemcpyAsync(run.sel.data(), idx, (size_t)t * 4, hipMemcpyDeviceToHost, st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess)
+            return done(KV_COMPACT_E_DEVICE);
+    }
+
+    // 3. the output blob, staged in device memory with the final offsets
+    const StateOut o = plan_state_out(s, run.sel, t, H, dv, size);
+    run.out_size = o.total;
+    if (o.total > size) return done(-2);   // not reached: every section shrinks or keeps its size
+    if (!host_out && o.total > out_cap) return done(KVC_E_CAPACITY);
+    std::vector<uint8_t> hdr(o.k_hdr.empty() ? 16 : o.k_hdr[0]);
+    {
+        uint32_t v2[2] = {s.n_stream, (uint32_t)t};
+        memcpy(hdr.data(), v2, 8);
+        size_t off = o.cells_off;
+        BlobReader cr;
+        cr.p = blob; cr.size = size; cr.dev = dev;
+        for (int j = 0; j < t; j++) {
+            const int c = run.sel[j];
+            if (!cr.read(s.cell_at[c], hdr.data() + off, s.cell_len[c])) return done(KV_COMPACT_E_DEVICE);
+            off += s.cell_len[c];
+        }
+        v2[0] = s.v_trans;
+        v2[1] = s.n_layer;
+        memcpy(hdr.data() + off, v2, 8);
+    }
+    if (hipMemcpyAsync(stage, hdr.data(), hdr.size(), hipMemcpyHostToDevice, st) != hipSuccess)
+        return done(KV_COMPACT_E_DEVICE);
+    std::vector<uint8_t> lh((size_t)2 * L * 16);
+    (void)hipEventRecord(ctx->q_ev[2], st);
+    const float scale = sqrtf((float)dk);
+    for (int l = 0; l < L; l++) {
+        const StateLayer & ld = s.layers[l];
+        uint8_t * kh = lh.data() + (size_t)l * 16;
+        memcpy(kh, &ld.k_type, 4);
+        memcpy(kh + 4, &ld.k_rb, 8);
+        if (hipMemcpyAsync(stage + o.k_hdr[l], kh, 12, hipMemcpyHostToDevice, st) != hipSuccess)
+            return done(KV_COMPACT_E_DEVICE);
+        const int sl = slot[l];
+        const int * sidx = idx;   // row 0: every layer keeps the same cells
+        launch_fold_rows(Kf + (size_t)sl * T * nk, nk, sidx, t, zbeta, dirs + (size_t)sl * H * dk, H, dk, scale,
+                         rows, st);
+        encode_rows(rows, nk, nullptr, iota, ld.k_type, nk, t, stage + o.k_pay[l], o.k_w[l], st);
+        // the fold reads `rows` before the value rows overwrite it: same stream
+    }
+    for (int l = 0; l < L; l++) {
+        const StateLayer & ld = s.layers[l];
+        uint8_t * vh = lh.data() + (size_t)(L + l) * 16;
+        memcpy(vh, &ld.v_type, 4);
+        const int sl = slot[l];
+        const bool comp = sl < Lc;
+        const float * cvl = comp ? Cv + (size_t)sl * H * t * dv : nullptr;
+        const float * vl = Vf + (size_t)sl * T * nv;
+        if (!s.v_trans) {
+            memcpy(vh + 4, &ld.v_rb, 8);
+            if (comp) {
+                launch_gather_cv_rows(cvl, H, t, dv, rows, st);
+                encode_rows(rows, nv, nullptr, iota, ld.v_type, nv, t, stage + o.v_pay[l], o.v_w[l], st);
+            } else {
+                encode_rows(vl, nv, idx, iota, ld.v_type, nv, t, stage + o.v_pay[l], o.v_w[l], st);
+            }
+        } else {
+            const uint32_t ne = (uint32_t)(H * dv);
+            memcpy(vh + 4, &ld.v_el, 4);
+            memcpy(vh + 8, &ne, 4);
+            launch_value_columns(cvl, vl, nv, idx, H, dv, t, cols, st);
+            launch_quant_rows(cols, t, nullptr, ld.v_type, t, (long long)ne, stage + o.v_pay[l],
+                              (long long)o.v_w[l], st);
+        }
+        if (hipMemcpyAsync(stage + o.v_hdr[l], vh, 12, hipMemcpyHostToDevice, st) != hipSuccess)
+            return done(KV_COMPACT_E_DEVICE);
+    }
+    (void)hipEventRecord(ctx->q_ev[3], st);
+    // empty streams and the trailing bytes
+    std::vector<uint8_t> zeros((size_t)(s.n_stream - 1) * 4, 0);
+    if (!zeros.empty() &&
+        hipMemcpyAsync(stage + o.tail_off, zeros.data(), zeros.size(), hipMemcpyHostToDevice, st) != hipSuccess)
+        return done(KV_COMPACT_E_DEVICE);
+    const size_t trail = size - s.kv_end;
+    if (trail && hipMemcpyAsync(stage + o.tail_off + zeros.size(), dblob + s.kv_end, trail,
+                                hipMemcpyDeviceToDevice, st) != hipSuccess)
+        return done(KV_COMPACT_E_DEVICE);
+    if (host_out) {
+        uint8_t * out = (uint8_t *)malloc(std::max<size_t>(o.total, 1));
+        if (!out) return done(-1);
+        if (hipMemcpyAsync(out, stage, o.total, hipMemcpyDeviceToHost, st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess) {
+            free(out);
+            return done(KV_COMPACT_E_DEVICE);
+        }
+        *host_out = out;
+    } else {
+        if (hipMemcpyAsync(d_out, stage, o.total, hipMemcpyDeviceToDevice, st) != hipSuccess ||
+            hipStreamSynchronize(st) != hipSuccess)
+            return done(KV_COMPACT_E_DEVICE);
+    }
+    record_codec_times(ctx);
+    return done(0);
+}
+
+}  // namespace
+
+extern "C" {
+
+int kvc_state_parse_info(const void * blob, size_t size, uint32_t n_pos_per_embd, kvc_state_info * info) {
+    if (!blob || !info) return -1;
+    BlobReader rd;
+    rd.p = static_cast<const uint8_t *>(blob);
+    rd.size = size;
+    rd.dev = is_device_ptr(blob);
+    StateLayout s;
+    const int rc = parse_state(rd, n_pos_per_embd, s);
+    memset(info, 0, sizeof(*info));
+    if (rc) return rc;
+    if (s.extra_streams) return KV_COMPACT_E_UNSUPPORTED;
+    info->n_stream = s.n_stream;
+    info->cell_count = s.cells;
+    info->v_trans = s.v_trans;
+    info->n_layer = s.n_layer;
+    if (s.n_layer > 0) {
+        info->n_embd_k = s.layers[0].nk;
+        info->n_embd_v = s.layers[0].nv;
+    }
+    info->kv_bytes = s.kv_end;
+    info->trailing_bytes = size - s.kv_end;
+    return 0;
+}
+
+int kvc_state_compact(const void * blob, size_t size, const kvc_state_params * sp, void ** out, size_t * out_size,
+                      int32_t * selected) {
+    if (!blob || !sp || !out || !out_size) return -1;
+    *out = nullptr;
+    *out_size = 0;
+    StateRun r = state_compact_impl(static_cast<const uint8_t *>(blob), size, false, *sp, out, nullptr, 0, nullptr);
+    if (r.rc) return r.rc;
+    *out_size = r.out_size;
+    if (selected) memcpy(selected, r.sel.data(), r.sel.size() * sizeof(int32_t));
+    return 0;
+}
+
+int kvc_state_compact_device(const void * d_blob, size_t size, const kvc_state_params * sp, void * d_out,
+                             size_t out_cap, size_t * out_size, int32_t * selected, void * stream) {
+    if (!d_blob || !sp || !d_out || !out_size) return -1;
+    if (!is_device_ptr(d_blob) || !is_device_ptr(d_out)) return -1;
+    StateRun r = state_compact_impl(static_cast<const uint8_t *>(d_blob), size, true, *sp, nullptr,
+                                    static_cast<uint8_t *>(d_out), out_cap, (hipStream_t)stream);
+    *out_size = r.out_size;
+    if (r.rc) return r.rc;
+    if (selected) memcpy(selected, r.sel.data(), r.sel.size() * sizeof(int32_t));
+    return 0;
+}
+
+void kvc_state_free(void * out) { free(out); }
 
 }  // extern "C"

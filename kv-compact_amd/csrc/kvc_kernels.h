@@ -27,6 +27,8 @@ void launch_beta_log(float * wb, long long n, hipStream_t st);
 // place; 3 tc_max + nq_max <= PGD_LDS_FLOATS)
 constexpr int PGD_LDS_FLOATS = 40960 - 64;
 void launch_nnls_pgd(const Geom & g, const Work & w, float * wb, int iters, hipStream_t st);
+// query rows: the chunk softmax keeps two floats per row in LDS, OMP three
+constexpr int SOFTMAX_MAXQ = 8192, OMP_MAXQ = 256;
 // OMP selection into w.sel (rows of w.A and w.rowsum as the exp scores)
 void launch_omp_select(const Geom & g, const Work & w, const OmpWork & ow, hipStream_t st);
 // m_by_lu: k_ls_build leaves M = X^T X out where k_ge_lu can form it from X
@@ -62,6 +64,16 @@ void launch_dequant8(const uint8_t * src, int type, long long row_bytes, long lo
 void launch_requant8(const float * src, long long src_ls, long long src_ld, const int * idx, long long idx_ls,
                      int mode, int H, int dv, int type, int n_el, int rows, int L, uint8_t * dst, long long row_bytes,
                      long long dst_ls, hipStream_t st);
+// state blobs: [rows][cols] -> [cols][rows]; kept key rows with the beta
+// fold; transposed value columns; the reference-query rows of each head
+void launch_transpose(const float * src, long long rows, long long cols, float * dst, hipStream_t st);
+void launch_fold_rows(const float * K, int nk, const int * sel, int t, const float * beta, const float * dir, int H,
+                      int dk, float scale, float * out, hipStream_t st);
+void launch_value_columns(const float * Cv, const float * V, int nv, const int * sel, int H, int dv, int t,
+                          float * col, hipStream_t st);
+void launch_gather_qref(const float * K, long long ldK, int nk, int q0, int nq, int H, int dk, int L, float * out,
+                        hipStream_t st);
+void launch_iota(int * p, long long n, hipStream_t st);
 void launch_gemm_abt(const float * A, long long lda, const float * B, long long ldb, float * C, long long ldc,
                      int m, int n, int k, float scale, long long sa, long long sb, long long sc, int batch,
                      hipStream_t st);

@@ -444,7 +444,8 @@ __device__ __forceinline__ float wave_ref_row_max(const float * row, int n, int 
     return (mm > r0) ? mm : r0;
 }
 
-// Chunk softmax + per-key importance (math.h:142-248), for up to SM_MAXQ rows:
+// Chunk softmax + per-key importance (math.h:142-248), for up to SOFTMAX_MAXQ rows
+// (two floats per row in dynamic LDS):
 //  1. row maxima, one wave per row;
 //  2. e = expf(s - max) over 64-key tiles: written unnormalised to A, staged
 //     in LDS so that one thread per row adds its tile in key order; the row's
@@ -454,7 +455,7 @@ __device__ __forceinline__ float wave_ref_row_max(const float * row, int n, int 
 //     reference. A keeps e: its consumers form a = e * inv themselves (the
 //     same single rounding), and e itself is the beta fit's exp scores.
 // grid = (n_chunks * H, L)
-constexpr int SM_MAXQ = 256, SM_TILE = 64, SM_TROWS = 32;
+constexpr int SM_TILE = 64, SM_TROWS = 32;
 
 __global__ void __launch_bounds__(256)
 k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ S,
@@ -465,7 +466,9 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
     const long long rs = g.T;
     const float * Sh = S + layer * lS(g) + h * hS(g) + c.start;
     float * Ah = A + layer * lS(g) + h * hS(g) + c.start;
-    __shared__ float rmax[SM_MAXQ], rinv[SM_MAXQ];
+    extern __shared__ float sm_rows[];   // row maxima, then 1 / (row sum + 1e-12f): nq_max each
+    float * rmax = sm_rows;
+    float * rinv = sm_rows + g.nq_max;
     __shared__ float eb[SM_TROWS][SM_TILE + 1];
     __shared__ uint64_t etab[32];
     const int nq = c.nq, n = c.Tc;
@@ -3654,7 +3657,7 @@ k_omp_select(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
     float * v = grad + tm;
     float * prow = v + g.nq_max;
     float * fac = prow + tm + 1;
-    __shared__ float cs[SM_MAXQ], res[SM_MAXQ], cur[SM_MAXQ];
+    __shared__ float cs[OMP_MAXQ], res[OMP_MAXQ], cur[OMP_MAXQ];
     __shared__ float rv[4];
     __shared__ int ri[4];
     __shared__ int s_best;
@@ -4310,6 +4313,84 @@ k_requant8(const float * __restrict__ src, long long src_ls, long long src_ld, c
 }
 
 // ---------------------------------------------------------------------------
+// llama.cpp state blobs (state.h:425-462, 645-810; kv-compact.cpp:659-685):
+// the layout moves around the compaction itself.
+// ---------------------------------------------------------------------------
+// [rows][cols] -> [cols][rows], 32 x 32 tiles through LDS; grid (ceil(cols/32),
+// ceil(rows/32)), 32 x 8 threads
+__global__ void __launch_bounds__(256)
+k_transpose(const float * __restrict__ src, long long rows, long long cols, float * __restrict__ dst) {
+    __shared__ float tile[32][33];
+    const long long r0 = (long long)blockIdx.y * 32, c0 = (long long)blockIdx.x * 32;
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+    for (int i = ty; i < 32; i += 8) {
+        const long long r = r0 + i, c = c0 + tx;
+        tile[i][tx] = (r < rows && c < cols) ? src[r * cols + c] : 0.0f;
+    }
+    __syncthreads();
+    for (int i = ty; i < 32; i += 8) {
+        const long long c = c0 + i, r = r0 + tx;
+        if (c < cols && r < rows) dst[c * rows + r] = tile[tx][i];
+    }
+}
+
+// Kept key rows with the beta fold of the blob writer (state.h:714-728):
+// out[j][h * dk + d] = K[sel[j]][h * dk + d] + (beta[h][j] * scale) * dir[h][d],
+// other columns copied. grid (ceil(t * nk / 256))
+__global__ void __launch_bounds__(256)
+k_fold_rows(const float * __restrict__ K, int nk, const int * __restrict__ sel, int t, const float * __restrict__ beta,
+            const float * __restrict__ dir, int H, int dk, float scale, float * __restrict__ out) {
+    const long long total = (long long)t * nk;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (long long)gridDim.x * blockDim.x) {
+        const int j = (int)(e / nk), c = (int)(e % nk);
+        float x = K[(long long)sel[j] * nk + c];
+        if (c < H * dk) {
+            const int h = c / dk, d = c - h * dk;
+            const float bs = beta[(long long)h * t + j] * scale;
+            x = x + bs * dir[(long long)h * dk + d];
+        }
+        out[e] = x;
+    }
+}
+
+// Transposed value columns of the blob writer (state.h:770-800): col[d][j] for
+// d < H * dv, j < t, from C_v [H][t][dv] (Cv != nullptr) or, for a layer the
+// filter keeps as is, from the original rows V[sel[j]][d] (row width nv).
+__global__ void __launch_bounds__(256)
+k_value_columns(const float * __restrict__ Cv, const float * __restrict__ V, int nv, const int * __restrict__ sel,
+                int H, int dv, int t, float * __restrict__ col) {
+    const long long total = (long long)H * dv * t;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (long long)gridDim.x * blockDim.x) {
+        const int d = (int)(e / t), j = (int)(e % t);
+        const int h = d / dv, c = d - h * dv;
+        col[e] = Cv ? Cv[((long long)h * t + j) * dv + c] : V[(long long)sel[j] * nv + d];
+    }
+}
+
+// Reference queries of the direction fit (kv-compact.cpp:674-681): rows
+// q0 .. q0 + nq - 1 of each layer's keys, per head: out[l][h][i][d] =
+// K[l][q0 + i][h * dk + d]. grid (ceil(H * nq * dk / 256), L)
+__global__ void __launch_bounds__(256)
+k_gather_qref(const float * __restrict__ K, long long ldK, int nk, int q0, int nq, int H, int dk,
+              float * __restrict__ out) {
+    const int l = blockIdx.y;
+    const long long total = (long long)H * nq * dk;
+    for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (long long)gridDim.x * blockDim.x) {
+        const int h = (int)(e / ((long long)nq * dk)), r = (int)(e % ((long long)nq * dk));
+        const int i = r / dk, d = r - i * dk;
+        out[(long long)l * total + e] = K[(long long)l * ldK + (long long)(q0 + i) * nk + h * dk + d];
+    }
+}
+
+__global__ void __launch_bounds__(256) k_iota(int * __restrict__ p, long long n) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = (int)i;
+}
+
+// ---------------------------------------------------------------------------
 // Accelerator plug-in GEMMs (accel ABI), sequential accumulation.
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(256)
@@ -4363,7 +4444,8 @@ void launch_scores(const Geom & g, const ChunkDesc * chunks, int n_chunk_units, 
 }
 
 void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st) {
-    hipLaunchKernelGGL(k_softmax_importance, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
+    hipLaunchKernelGGL(k_softmax_importance, dim3(g.n_chunks * g.H, g.L), dim3(256),
+                       (size_t)2 * g.nq_max * sizeof(float), st,
                        g, w.chunks, w.S, w.smax, w.A, w.E ? w.rowsum : nullptr, w.ainv, w.imp,
                        w.sens && g.score_method != 0 ? w.amax : nullptr);
     // sensitivity per (layer, chunk, head) from the per-key maxima over
@@ -4623,6 +4705,37 @@ void launch_requant8(const float * src, long long src_ls, long long src_ld, cons
     const long long blocks = std::min<long long>((total + 255) / 256, 1LL << 30);
     hipLaunchKernelGGL(k_requant8, dim3((unsigned)blocks), dim3(256), 0, st,
                        src, src_ls, src_ld, idx, idx_ls, mode, H, dv, type, n_el, rows, L, dst, row_bytes, dst_ls);
+}
+
+void launch_transpose(const float * src, long long rows, long long cols, float * dst, hipStream_t st) {
+    if (rows <= 0 || cols <= 0) return;
+    hipLaunchKernelGGL(k_transpose, dim3(cdiv(cols, 32), cdiv(rows, 32)), dim3(256), 0, st, src, rows, cols, dst);
+}
+
+void launch_fold_rows(const float * K, int nk, const int * sel, int t, const float * beta, const float * dir, int H,
+                      int dk, float scale, float * out, hipStream_t st) {
+    if (t <= 0) return;
+    hipLaunchKernelGGL(k_fold_rows, dim3(grid_cap((long long)t * nk, 256)), dim3(256), 0, st,
+                       K, nk, sel, t, beta, dir, H, dk, scale, out);
+}
+
+void launch_value_columns(const float * Cv, const float * V, int nv, const int * sel, int H, int dv, int t,
+                          float * col, hipStream_t st) {
+    if (t <= 0) return;
+    hipLaunchKernelGGL(k_value_columns, dim3(grid_cap((long long)H * dv * t, 256)), dim3(256), 0, st,
+                       Cv, V, nv, sel, H, dv, t, col);
+}
+
+void launch_gather_qref(const float * K, long long ldK, int nk, int q0, int nq, int H, int dk, int L, float * out,
+                        hipStream_t st) {
+    if (L <= 0) return;
+    hipLaunchKernelGGL(k_gather_qref, dim3(grid_cap((long long)H * nq * dk, 256), L), dim3(256), 0, st,
+                       K, ldK, nk, q0, nq, H, dk, out);
+}
+
+void launch_iota(int * p, long long n, hipStream_t st) {
+    if (n <= 0) return;
+    hipLaunchKernelGGL(k_iota, dim3(cdiv(n, 256)), dim3(256), 0, st, p, n);
 }
 
 void launch_gather_cv_rows(const float * Cv, int H, int t, int dv, float * rows, hipStream_t st) {

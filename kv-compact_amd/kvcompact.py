@@ -24,7 +24,7 @@ REPO = HERE.parent
 KV_TYPE_F32, KV_TYPE_F16, KV_TYPE_Q4_0, KV_TYPE_Q4_1, KV_TYPE_Q8_0 = 0, 1, 2, 3, 8
 KV_TYPE_BF16 = 30   # extension: bfloat16 rows (no reference counterpart)
 KV_TOKEN_ANSWER, KV_TOKEN_THINKING, KV_TOKEN_TRANSITION = 0, 1, 2
-E_UNSUPPORTED, E_DEVICE, E_SCRATCH = -5, -6, -7
+E_UNSUPPORTED, E_DEVICE, E_SCRATCH, E_CAPACITY = -5, -6, -7, -8
 
 
 class Stats(ctypes.Structure):

@@ -1466,6 +1466,9 @@ static int orc_state_parse(const uint8_t * data, size_t size, uint32_t n_pos, or
                 const uint64_t bytes = (uint64_t)ld->n_embd_v_hdr * cc * ld->v_size_el;
                 if ((uint64_t)(end - p) < bytes) return 0;
                 const size_t n = (size_t)ld->n_embd_v_hdr * cc;
+                /* the flat decode must stay inside the section (a smaller
+                 * v_size_el would make the reference read past it) */
+                if (orc_quant_row_bytes(ld->v_type, (int)n) > bytes) return 0;
                 ld->nv = (int)ld->n_embd_v_hdr;
                 float * tmp = (float *)calloc(n + 1, sizeof(float));
                 convert_to_f32(p, ld->v_type, tmp, n);

@@ -194,3 +194,15 @@ def test_config3_bf16_slice(gpu, orc):
         same(a, b)
         assert np.array_equal(a.K_out, b.K_out)
         assert np.array_equal(a.V_out, b.V_out)
+
+
+def test_many_reference_queries(gpu, orc):
+    """300 query rows (beyond one LDS row-sum slot per thread of a 256-thread
+    block): chunked and unchunked calls equal the oracle."""
+    K, V = kv_cache(3000, 2, 64, 81, channel_scale=True)
+    Q = snapkv_queries(K, 300, 81)
+    for kw in (dict(target_ratio=0.2), dict(target_ratio=0.1, chunk_size=-1, skip_beta=0)):
+        print(f"[case] n_q=300 {kw}", flush=True)
+        a = gpu.compact(K, V, Q, 3000, 300, 2, 64, 64, gpu.params(**kw))
+        b = orc.compact(K, V, Q, 3000, 300, 2, 64, 64, orc.params(**kw))
+        same(a, b)
