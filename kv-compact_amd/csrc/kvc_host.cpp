@@ -143,7 +143,19 @@ bool drain_second_stream(DeviceCtx * ctx, hipStream_t st) {
            hipStreamWaitEvent(st, ctx->refit_join, 0) == hipSuccess;
 }
 
+// Host-forced faults for tests of the error paths, read at every call:
+// KVC_FAULT=alloc fails every workspace allocation (as a failing hipMalloc
+// would, whether or not the arena must grow); KVC_FAULT=launch stops each
+// compaction's kernel sequence before its first launch with a device error.
+bool forced_fault(const char * kind) {
+    const char * e = getenv("KVC_FAULT");
+    if (!e || strcmp(e, kind) != 0) return false;
+    fprintf(stderr, "[kv-compact] forced %s failure (KVC_FAULT=%s)\n", kind, kind);
+    return true;
+}
+
 bool ensure_arena(DeviceCtx * c, size_t bytes) {
+    if (forced_fault("alloc")) return false;
     if (c->arena_cap >= bytes) return true;
     if (c->arena) {
         (void)hipStreamSynchronize(c->stream);
@@ -482,6 +494,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     // the beta fit's PGD steps keep their vectors in LDS
     const bool pgd = !p.skip_beta && p.nnls_method != 0 && p.nnls_pgd_iters > 0;
     if (pgd && 3 * pl.tc_max + pl.nq_max > PGD_LDS_FLOATS) return KV_COMPACT_E_UNSUPPORTED;
+    if (forced_fault("launch")) return KV_COMPACT_E_DEVICE;
     if (!drain_second_stream(ctx, st)) return KV_COMPACT_E_DEVICE;
     Work w{};
     StatWork sw{};
@@ -1638,6 +1651,9 @@ int parse_state(BlobReader & r, uint32_t n_pos, StateLayout & s) {
             s.extra_streams = true;
             return 0;
         }
+        // every cell record takes at least 8 bytes: a count beyond the blob
+        // is malformed (checked before anything is sized by it)
+        if (cc > (r.size - off) / 8) return -2;
         s.cells = cc;
         s.cell_at.resize(cc);
         s.cell_len.resize(cc);
@@ -1652,6 +1668,7 @@ int parse_state(BlobReader & r, uint32_t n_pos, StateLayout & s) {
             s.cell_len[c] = (uint32_t)(off - s.cell_at[c]);
         }
         if (!rd(&s.v_trans, 4) || !rd(&s.n_layer, 4)) return fail();
+        if (s.n_layer > (r.size - off) / 24) return -2;   // two headers of >= 12 bytes per layer
         s.layers.assign(s.n_layer, StateLayer());
         for (uint32_t l = 0; l < s.n_layer; l++) {
             StateLayer & ld = s.layers[l];
@@ -1893,6 +1910,7 @@ StateRun state_compact_impl(const uint8_t * blob, size_t size, bool dev, const k
     int * idx = b.idx, * iota = b.iota;
     uint8_t * stage = b.stage;
 
+    if (forced_fault("launch")) return done(KV_COMPACT_E_DEVICE);
     // 1. decode every layer's K and V into fp32 rows (slot order)
     (void)hipEventRecord(ctx->q_ev[0], st);
     for (int l = 0; l < L; l++) {

@@ -1412,6 +1412,9 @@ static int orc_state_parse(const uint8_t * data, size_t size, uint32_t n_pos, or
         if (!rd(&p, end, &cc, 4)) return 0;
         if (cc == 0) continue;
         if (st > 0) { *extra_streams = 1; return 1; }   /* only stream 0 may hold cells */
+        /* a record takes at least 8 bytes: larger counts are malformed (the
+         * reference would size its cell table first and fail while reading) */
+        if (cc > (size_t)(end - p) / 8) return 0;
         s->cell_count = cc;
         s->pos = (int32_t *)calloc(cc, 4);
         s->ext = (int32_t *)calloc((size_t)cc * 2, 4);
@@ -1432,6 +1435,7 @@ static int orc_state_parse(const uint8_t * data, size_t size, uint32_t n_pos, or
         }
         if (!rd(&p, end, &s->v_trans, 4)) return 0;
         if (!rd(&p, end, &s->n_layer, 4)) return 0;
+        if (s->n_layer > (size_t)(end - p) / 24) return 0;   /* two headers of >= 12 bytes per layer */
         s->layers = (orc_layer *)calloc(s->n_layer ? s->n_layer : 1, sizeof(orc_layer));
         for (uint32_t l = 0; l < s->n_layer; l++) {
             orc_layer * ld = &s->layers[l];

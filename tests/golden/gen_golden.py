@@ -5,6 +5,7 @@ Run in the container that holds the reference checkout, after
 
     python tests/golden/gen_golden.py          (everything)
     python tests/golden/gen_golden.py state    (the state blob cases only)
+    python tests/golden/gen_golden.py replay   (the wrapper call-sequence replay only)
 
 Inputs are regenerated from seeds by tests/kvc_data.py (integer-only
 generator), so each fixture stores only the reference's outputs plus an
@@ -91,9 +92,27 @@ def write_state_fixtures():
     print("wrote", len(STATE_CASES), "state cases")
 
 
+def write_replay_fixtures():
+    """The reference wrapper's call sequence replayed against the compiled
+    reference (tests/bindings_replay.py)."""
+    import bindings_replay as br
+    from kvc_harness import REF_SO
+    lib = br.load(str(REF_SO))
+    out = {}
+    for c in br.REPLAY_CASES:
+        K, V, Q = br.replay_inputs(c["seed"])
+        idx, cv, ksel, st = br.compact(lib, K, V, Q if c["q"] else None, **c["kw"])
+        out[c["name"] + "_indices"] = idx
+        out[c["name"] + "_C_v"] = cv
+        out[c["name"] + "_K_selected"] = ksel
+        out[c["name"] + "_stats"] = np.array([st["avg_cosine_sim"], st["avg_mse"], st["avg_agreement"]], np.float32)
+    np.savez_compressed(HERE / "bindings_replay.npz", **out)
+    print("wrote", len(br.REPLAY_CASES), "replay cases")
+
+
 def main():
-    if len(sys.argv) > 1 and sys.argv[1] == "state":
-        write_state_fixtures()
+    if len(sys.argv) > 1 and sys.argv[1] in ("state", "replay"):
+        (write_state_fixtures if sys.argv[1] == "state" else write_replay_fixtures)()
         return
     ref = load_ref()
     if ref is None:
@@ -173,6 +192,7 @@ def main():
     blocks["f32_to_f16_out"] = np.array([h.ref_f32_to_f16(float(v)) for v in probe], np.uint16)
     np.savez_compressed(HERE / "blocks.npz", **blocks)
     write_state_fixtures()
+    write_replay_fixtures()
     print("wrote", len(out), "cases,", len(QUANT_CASES), "quantized cases, multi-round and blocks")
 
 
