@@ -128,25 +128,27 @@ def roofline(name, model, ms):
 
 
 def host_info() -> dict:
-    """Device and host descriptions for the record, as the box's own tools
-    print them (rocminfo and rocm-smi run as their own processes)."""
-    import subprocess
-    arch, model = "", ""
+    """Device and host descriptions for the record, read from sysfs and /proc
+    (no other program is started: this process may already hold the GPU)."""
+    arch, model, product = "", "", ""
     try:
-        out = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=60).stdout
-        for line in out.splitlines():
-            t = line.strip()
-            if t.startswith("Name:") and "gfx" in t and not arch:
-                arch = t.split(":", 1)[1].strip()
-    except Exception:  # noqa: BLE001
+        for node in sorted(Path("/sys/class/kfd/kfd/topology/nodes").iterdir()):
+            name = (node / "name").read_text().strip() if (node / "name").exists() else ""
+            if name.startswith("gfx"):
+                arch = name
+                for line in (node / "properties").read_text().splitlines():
+                    k, _, v = line.partition(" ")
+                    if k == "device_id" and v.strip().isdigit():
+                        model = f"0x{int(v):04x}"
+                break
+    except OSError:
         pass
     try:
-        out = subprocess.run(["rocm-smi", "--showproductname"], capture_output=True, text=True, timeout=60).stdout
-        for line in out.splitlines():
-            if "Card Model:" in line:
-                model = line.split("Card Model:", 1)[1].strip()
+        for card in sorted(Path("/sys/class/drm").glob("card*/device/product_name")):
+            product = card.read_text().strip()
+            if product:
                 break
-    except Exception:  # noqa: BLE001
+    except OSError:
         pass
     cpu = ""
     try:
@@ -156,7 +158,9 @@ def host_info() -> dict:
                 break
     except OSError:
         pass
-    dev = f"AMD Instinct {arch}" + (f" (PCI device {model})" if model else "")
+    dev = product or f"AMD Instinct {arch}"
+    if model:
+        dev += f" ({arch}, PCI device {model})" if product else f" (PCI device {model})"
     return {"device": dev, "cpu_model": cpu, "host_cpus": os.cpu_count(),
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS", "")}
 
