@@ -1301,9 +1301,9 @@ k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 }
 
 // The greedy pass of one unit, one wave; candidate position p sits in lane
-// p % 64, slot p / 64. grid (units).
-constexpr int DIV_SLOTS = DIV_MAX_CAND / 64;
-
+// p % 64, slot p / 64 (NS slots: the level's capacity is at most 64 NS).
+// grid (units).
+template <int NS>
 __global__ void __launch_bounds__(64)
 k_div_greedy(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ gimp, DivWork dw,
              const int * __restrict__ cand_all, int * __restrict__ sel) {
@@ -1321,14 +1321,27 @@ k_div_greedy(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
     const int * cand = cand_all + (long long)unit * g.Tc_max;
     const float * G = dw.G + (long long)slot_g * dw.cap * dw.cap;
     __shared__ unsigned char taken[DIV_MAX_CAND];   // by candidate position
-    float imp[DIV_SLOTS], pen[DIV_SLOTS], sqn[DIV_SLOTS];
+    float imp[NS], pen[NS], sqn[NS], gv[NS];
     unsigned live = 0;   // bit k: slot k holds an unused candidate
+    // Loads sit under wave-uniform slot guards with clamped indices, never
+    // under a per-lane branch: a load inside a divergent branch is waited for
+    // before the branch ends, which would serialize one memory round trip per
+    // slot. Lanes past the candidates read a valid entry and discard it.
+    const int nsl = (C + 63) >> 6;   // slots holding candidates
+    int ci[NS];
 #pragma unroll
-    for (int k = 0; k < DIV_SLOTS; k++) {
+    for (int k = 0; k < NS; k++) {
+        const int p = min(lane + 64 * k, C - 1);
+        ci[k] = k < nsl ? cand[p] : 0;
+        gv[k] = k < nsl ? G[(long long)p * dw.cap + p] : 0.0f;
+    }
+#pragma unroll
+    for (int k = 0; k < NS; k++) {
         const int p = lane + 64 * k;
         const bool v = p < C;
-        imp[k] = v ? im[cand[p]] : 0.0f;
-        sqn[k] = v ? sqrtf(G[(long long)p * dw.cap + p]) : 0.0f;
+        const float x = k < nsl ? im[ci[k]] : 0.0f;
+        imp[k] = v ? x : 0.0f;
+        sqn[k] = v ? sqrtf(gv[k]) : 0.0f;
         pen[k] = 0.0f;
         if (v) live |= 1u << k;
         taken[p] = 0;
@@ -1339,10 +1352,10 @@ k_div_greedy(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
         float bs = -1e30f;
         int bp = -1;
 #pragma unroll
-        for (int k = 0; k < DIV_SLOTS; k++) {
-            if (live & (1u << k)) {
+        for (int k = 0; k < NS; k++) {
+            if (k < nsl) {
                 const float sc = imp[k] * (1.0f - s * pen[k]);
-                if (sc > bs) { bs = sc; bp = lane + 64 * k; }
+                if (((live >> k) & 1u) && sc > bs) { bs = sc; bp = lane + 64 * k; }
             }
         }
         const unsigned kmax = dpp_reduce_u32<true>(bp >= 0 ? score_key(bs) : 0u);
@@ -1356,13 +1369,17 @@ k_div_greedy(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
             live &= ~(1u << (b >> 6));
             taken[b] = 1;
         }
-        const float nsel = sqrtf(G[(long long)b * dw.cap + b]) + 1e-8f;
         const float * Gb = G + (long long)b * dw.cap;
 #pragma unroll
-        for (int k = 0; k < DIV_SLOTS; k++) {
-            if (live & (1u << k)) {
-                const float cs = Gb[lane + 64 * k] / (nsel * sqn[k] + 1e-8f);
-                if (cs > pen[k]) pen[k] = cs;
+        for (int k = 0; k < NS; k++) gv[k] = k < nsl ? Gb[min(lane + 64 * k, C - 1)] : 0.0f;
+        const float nsel = sqrtf(Gb[b]) + 1e-8f;
+        // every slot's quotient is formed (no divergent branch); only unused
+        // candidates take it
+#pragma unroll
+        for (int k = 0; k < NS; k++) {
+            if (k < nsl) {
+                const float cs = gv[k] / (nsel * sqn[k] + 1e-8f);
+                if (((live >> k) & 1u) && cs > pen[k]) pen[k] = cs;
             }
         }
     }
@@ -4478,7 +4495,11 @@ void launch_div_level(const Geom & g, const Work & w, const DivWork & dw, const 
     const int nt = cdiv(dw.cap, DG_TILE);
     hipLaunchKernelGGL(k_div_candidates, dim3(g.n_chunks, g.L), dim3(256), 0, st, g, w.chunks, w.gimp, dw, w.cand);
     hipLaunchKernelGGL(k_div_gram, dim3(units, nt * (nt + 1) / 2), dim3(256), 0, st, g, w.chunks, K, dw, w.cand);
-    hipLaunchKernelGGL(k_div_greedy, dim3(units), dim3(64), 0, st, g, w.chunks, w.gimp, dw, w.cand, w.sel);
+    if (dw.cap <= 8 * 64)
+        hipLaunchKernelGGL(k_div_greedy<8>, dim3(units), dim3(64), 0, st, g, w.chunks, w.gimp, dw, w.cand, w.sel);
+    else
+        hipLaunchKernelGGL(k_div_greedy<DIV_MAX_CAND / 64>, dim3(units), dim3(64), 0, st, g, w.chunks, w.gimp, dw,
+                           w.cand, w.sel);
 }
 
 void launch_select_topk(const Geom & g, const Work & w, hipStream_t st) {
