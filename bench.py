@@ -276,7 +276,9 @@ def drop_in_mode(lib, L, T, H, d, W, ratio, diversity, seed):
 
 def quantized_mode(dll, lib, hiprt, L, T, H, d, ratio, steps, warmup, seed):
     """Q8_0 and Q4_0 caches of N(0,1) data: the multi-layer quantized device
-    entry (dequantize, compact, requantize) on all layers, inputs resident."""
+    entry (compact, requantize) on all layers, inputs resident; the kernels
+    decode K and V blocks in registers as they load them. The same call with
+    KVC_INPLACE=0 (a whole-cache decode to fp32 first) is reported beside it."""
     sys.path.insert(0, str(REPO / "tests"))
     from kvc_data import quantize_rows
     E = H * d
@@ -303,34 +305,55 @@ def quantized_mode(dll, lib, hiprt, L, T, H, d, ratio, steps, warmup, seed):
                                                          ko.value, vo.value, None)
             if rc != 0:
                 raise RuntimeError(f"kvc_compact_quantized_layers_device returned {rc}")
-        for _ in range(warmup):
-            step()
-        hiprt.synchronize()
-        acc = np.zeros(len(QSTAGES))
-        buf = (ctypes.c_float * len(QSTAGES))()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            step()
-            dll.kvc_stage_times(buf, len(QSTAGES))
-            acc += np.array(buf[:])
-        hiprt.synchronize()
-        ms = (time.perf_counter() - t0) / steps * 1e3
-        acc /= steps
-        dq_bytes = 2 * L * T * (rb + E * 4)                     # read the rows, write fp32
-        rq_bytes = 2 * L * t * (E * 4 + rb)                     # read kept K rows and C_v, write the rows
-        st = dict(zip(QSTAGES, acc))
-        res[name] = {"value": round(T / (ms / 1e3), 1), "unit": "tok/s", "ms_per_step": round(ms, 3),
-                     "row_bytes": rb,
+
+        for mode in ("1", "0"):
+            old_env = os.environ.get("KVC_INPLACE")
+            os.environ["KVC_INPLACE"] = mode
+            try:
+                for _ in range(warmup):
+                    step()
+                hiprt.synchronize()
+                acc = np.zeros(len(QSTAGES))
+                buf = (ctypes.c_float * len(QSTAGES))()
+                t0 = time.perf_counter()
+                for _ in range(steps):
+                    step()
+                    dll.kvc_stage_times(buf, len(QSTAGES))
+                    acc += np.array(buf[:])
+                hiprt.synchronize()
+                ms = (time.perf_counter() - t0) / steps * 1e3
+            finally:
+                if old_env is None:
+                    os.environ.pop("KVC_INPLACE", None)
+                else:
+                    os.environ["KVC_INPLACE"] = old_env
+            acc /= steps
+            st = dict(zip(QSTAGES, acc))
+            if mode == "1":
+                # kept K rows decoded and re-encoded (read and write the rows),
+                # C_v read and its rows written
+                rq_bytes = L * t * (2 * rb + E * 4 + rb)
+                r = {"decode": "in the kernels' loads (no fp32 copy of the cache)",
+                     "value": round(T / (ms / 1e3), 1), "unit": "tok/s", "ms_per_step": round(ms, 3),
+                     "row_bytes": rb, "stage_ms": {k: round(float(v), 3) for k, v in st.items()}}
+            else:
+                dq_bytes = 2 * L * T * (rb + E * 4)             # read the rows, write fp32
+                rq_bytes = 2 * L * t * (E * 4 + rb)             # read kept K rows and C_v, write the rows
+                r = {"decode": "whole-cache pass to fp32 first (KVC_INPLACE=0)",
+                     "value": round(T / (ms / 1e3), 1), "unit": "tok/s", "ms_per_step": round(ms, 3),
                      "stage_ms": {k: round(float(v), 3) for k, v in st.items()},
-                     "dequantize_gb_s": round(dq_bytes / (st["dequantize"] / 1e3) / 1e9, 1) if st["dequantize"] else None,
+                     "dequantize_gb_s": round(dq_bytes / (st["dequantize"] / 1e3) / 1e9, 1)
+                     if st["dequantize"] else None,
                      "dequantize_frac_hbm": round(dq_bytes / (st["dequantize"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
                      if st["dequantize"] else None,
-                     "requantize_gb_s": round(rq_bytes / (st["requantize"] / 1e3) / 1e9, 1) if st["requantize"] else None,
-                     "requantize_frac_hbm": round(rq_bytes / (st["requantize"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
-                     if st["requantize"] else None,
-                     "dequantize_bytes": dq_bytes, "requantize_bytes": rq_bytes}
-        print(f"[bench] quantized {name}: {ms:.1f} ms per step, dequantize {st['dequantize']:.2f} ms, "
-              f"requantize {st['requantize']:.2f} ms", file=sys.stderr, flush=True)
+                     "dequantize_bytes": dq_bytes}
+            r["requantize_gb_s"] = round(rq_bytes / (st["requantize"] / 1e3) / 1e9, 1) if st["requantize"] else None
+            r["requantize_frac_hbm"] = (round(rq_bytes / (st["requantize"] / 1e3) / 1e9 / HBM_PEAK_GBS, 4)
+                                        if st["requantize"] else None)
+            r["requantize_bytes"] = rq_bytes
+            res[name if mode == "1" else name + "_whole_cache"] = r
+            print(f"[bench] quantized {name} inplace={mode}: {ms:.1f} ms per step, dequantize "
+                  f"{st['dequantize']:.2f} ms, requantize {st['requantize']:.2f} ms", file=sys.stderr, flush=True)
         del dKq, dVq, bufs, ko, vo
     return res
 

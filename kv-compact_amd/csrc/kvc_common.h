@@ -31,6 +31,18 @@ struct ChunkDesc {
     int nq;       // reference queries used by the chunk
 };
 
+// A quantized K or V cache read in place: the kernels that read the cache
+// decode each block in registers as they load it (the same products as the
+// whole-cache codec kernels). base == nullptr: the fp32 array is read.
+// Block codecs only (Q8_0, Q4_0): 2-byte fields at even offsets of even row
+// and layer strides.
+struct RowCodec {
+    const uint8_t * base;   // layer 0, row 0
+    long long row_bytes;    // bytes per token row (all heads)
+    long long layer_bytes;  // bytes per layer
+    int type;               // KV_TYPE_Q8_0 (8) or KV_TYPE_Q4_0 (2)
+};
+
 // Geometry of a batch of layers sharing one plan.
 struct Geom {
     int L, T, H, dk, dv;
@@ -42,6 +54,7 @@ struct Geom {
     float ridge;
     float zero_val;             // solution value of a skipped pivot (0 for C_v, eps for the beta weights)
     int lu_masked;              // 1: every register LU takes the masked variant (KVC_LU_MASKED=1, for tests)
+    RowCodec kc, vc;            // in-place quantized K / V (base == nullptr: fp32 K / V)
 };
 
 // Device scratch for one batch (all pointers device memory).

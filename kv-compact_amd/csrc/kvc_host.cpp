@@ -314,8 +314,9 @@ int check_supported(const kv_compact_params & p, int d_v) {
 // ------------------------------------------------------------ batch run
 
 struct BatchIO {
-    const float * K;   // device
-    const float * V;   // device
+    const float * K;   // device (nullptr when kc.base is set)
+    const float * V;   // device (nullptr when vc.base is set)
+    RowCodec kc, vc;   // quantized K / V read in place (base nullptr: K / V above)
     const float * Q;   // device or null
     long long ldK, ldV, ldQ;
     int L, T, n_q, H, dk, dv;
@@ -512,6 +513,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     g.tc_max = pl.tc_max; g.Tc_max = pl.Tc_max;
     g.qmode = pl.qmode; g.nq_global = pl.nq_global;
     g.ldK = io.ldK; g.ldV = io.ldV; g.ldQ = io.ldQ;
+    g.kc = io.kc; g.vc = io.vc;
     g.score_method = p.score_method;
     g.inv_sqrt_dk = 1.0f / sqrtf((float)io.dk);
     g.ridge = p.ridge;
@@ -875,14 +877,44 @@ size_t requant_floats(const QuantIO & qi, int t, int H, int dv) {
     return v8 ? 0 : (size_t)t * H * dv;
 }
 
+// A quantized K or V that the kernels read in place, decoding each block in
+// registers as they load it (no fp32 copy of the cache): Q8_0 and Q4_0 whose
+// 2-byte fields are aligned (even base, row and layer strides); K with d_k a
+// multiple of 32 (whole slabs of the scoring tiles) and, when queries are
+// provided, 16-byte aligned query rows; V with d_v a multiple of 4.
+// KVC_INPLACE=0 sends every cache through the whole-cache decode instead.
+RowCodec inplace_codec(const uint8_t * base, int type, size_t row_bytes, long long layer_bytes, int d, bool is_k,
+                       const float * Q, long long ldQ) {
+    RowCodec rc{};
+    const char * e = getenv("KVC_INPLACE");
+    if (e && e[0] == '0') return rc;
+    if (type != KV_TYPE_Q8_0 && type != KV_TYPE_Q4_0) return rc;
+    if ((reinterpret_cast<uintptr_t>(base) & 1) || (row_bytes & 1) || (layer_bytes & 1)) return rc;
+    if (is_k) {
+        if (d % 32 != 0) return rc;
+        if (Q && ((reinterpret_cast<uintptr_t>(Q) & 15) || (ldQ & 3))) return rc;
+    } else if (d % 4 != 0) {
+        return rc;
+    }
+    rc.base = base;
+    rc.row_bytes = (long long)row_bytes;
+    rc.layer_bytes = layer_bytes;
+    rc.type = type;
+    return rc;
+}
+
 // K_out: the kept rows of the dequantized K (api.cpp:1234-1241); V_out: the
 // refitted rows assembled over heads from C_v (api.cpp:1243-1254).
 void requant_outputs(const QuantIO & qi, const float * Kf, const int * idx, const float * Cv, int L, int T, int t,
-                     int H, int dk, int dv, float * rows_tmp, hipStream_t st) {
+                     int H, int dk, int dv, float * rows_tmp, hipStream_t st, const RowCodec & kc) {
     if (t <= 0) return;
     const int ek = H * dk, ev = H * dv;
     const bool cv_al = (reinterpret_cast<uintptr_t>(Cv) & 15) == 0;
-    if (codec8_ok(qi.k_type, ek)) {
+    if (kc.base) {
+        // K read in place: its kept rows are decoded and re-encoded in one pass
+        launch_requant8(nullptr, 0, 0, idx, t, 0, H, dk, qi.k_type, ek, t, L, qi.Kout, (long long)qi.k_rb,
+                        (long long)t * qi.k_rb, st, kc);
+    } else if (codec8_ok(qi.k_type, ek)) {
         launch_requant8(Kf, (long long)T * ek, ek, idx, t, 0, H, dk, qi.k_type, ek, t, L, qi.Kout,
                         (long long)qi.k_rb, (long long)t * qi.k_rb, st);
     } else {
@@ -1197,13 +1229,20 @@ int kv_compact_quantized(const uint8_t * K_quant, const uint8_t * V_quant, const
     BatchIO io{};
     io.L = 1; io.T = T; io.n_q = n_q; io.H = H; io.dk = d_k; io.dv = d_v;
     io.ldK = (long long)T * ek; io.ldV = (long long)T * ev; io.ldQ = (long long)std::max(n_q, 1) * ek;
+    // K / V read in place (the carve below places the quantized rows at
+    // 256-byte boundaries, so only the strides and shapes decide)
+    const bool k_in = inplace_codec(reinterpret_cast<const uint8_t *>(256), k_type, k_row_bytes, qi.lsKq, d_k, true,
+                                    use_q ? reinterpret_cast<const float *>(qd ? Q_ref_all : nullptr) : nullptr,
+                                    io.ldQ).base != nullptr;
+    const bool v_in = inplace_codec(reinterpret_cast<const uint8_t *>(256), v_type, v_row_bytes, qi.lsVq, d_v, false,
+                                    nullptr, 0).base != nullptr;
     // workspace: quantized rows, fp32 cache, query rows, weights, outputs, requantized rows, batch workspace
     auto carve = [&](Carver & cv, uint8_t *& dKq, uint8_t *& dVq, float *& dK, float *& dV, float *& dQ,
                      float *& dW, float *& tmp) {
         dKq = cv.take<uint8_t>((size_t)T * k_row_bytes);
         dVq = cv.take<uint8_t>((size_t)T * v_row_bytes);
-        dK = cv.take<float>((size_t)T * ek);
-        dV = cv.take<float>((size_t)T * ev);
+        dK = k_in ? nullptr : cv.take<float>((size_t)T * ek);
+        dV = v_in ? nullptr : cv.take<float>((size_t)T * ev);
         dQ = (use_q && !qd) ? cv.take<float>((size_t)n_q * ek) : nullptr;
         dW = have_w ? cv.take<float>(T) : nullptr;
         io.indices = cv.take<int>(std::max(t, 1));
@@ -1227,16 +1266,20 @@ int kv_compact_quantized(const uint8_t * K_quant, const uint8_t * V_quant, const
     if (e == hipSuccess && dQ) e = hipMemcpyAsync(dQ, Q_ref_all, (size_t)n_q * ek * 4, hipMemcpyHostToDevice, st);
     if (e == hipSuccess && dW) e = hipMemcpyAsync(dW, wts.data(), (size_t)T * 4, hipMemcpyHostToDevice, st);
     if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
+    io.Q = use_q ? (qd ? Q_ref_all : dQ) : nullptr;
+    io.kc = k_in ? inplace_codec(dKq, k_type, k_row_bytes, qi.lsKq, d_k, true, io.Q, io.ldQ) : RowCodec{};
+    io.vc = v_in ? inplace_codec(dVq, v_type, v_row_bytes, qi.lsVq, d_v, false, nullptr, 0) : RowCodec{};
+    if (k_in != (io.kc.base != nullptr) || v_in != (io.vc.base != nullptr)) return KV_COMPACT_E_DEVICE;
     (void)hipEventRecord(ctx->q_ev[0], st);
-    dequant_cache(dKq, k_type, k_row_bytes, qi.lsKq, ek, T, 1, dK, st);
-    dequant_cache(dVq, v_type, v_row_bytes, qi.lsVq, ev, T, 1, dV, st);
+    if (!k_in) dequant_cache(dKq, k_type, k_row_bytes, qi.lsKq, ek, T, 1, dK, st);
+    if (!v_in) dequant_cache(dVq, v_type, v_row_bytes, qi.lsVq, ev, T, 1, dV, st);
     (void)hipEventRecord(ctx->q_ev[1], st);
-    io.K = dK; io.V = dV; io.Q = use_q ? (qd ? Q_ref_all : dQ) : nullptr; io.wts = dW;
+    io.K = dK; io.V = dV; io.wts = dW;
     Timing tm;
     rc = run_batch(ctx, st, pl, p, io, cv, &tm);
     if (rc != 0) return rc;
     (void)hipEventRecord(ctx->q_ev[2], st);
-    requant_outputs(qi, dK, io.indices, io.Cv, 1, T, t, H, d_k, d_v, tmp, st);
+    requant_outputs(qi, dK, io.indices, io.Cv, 1, T, t, H, d_k, d_v, tmp, st, io.kc);
     (void)hipEventRecord(ctx->q_ev[3], st);
     std::vector<int> idx(t);
     std::vector<float> beta((size_t)H * t), cvh((size_t)H * t * d_v);
@@ -1492,9 +1535,11 @@ int kvc_compact_quantized_layers_device(const uint8_t * K_quant, const uint8_t *
     io.indices = out->indices; io.beta = out->beta; io.Cv = out->C_v; io.stats = out->stats;
     std::vector<float> wts;
     const bool host_w = rkv_weights(p, T, wts);
+    io.kc = inplace_codec(K_quant, k_type, k_row_bytes, ldKq, d_k, true, io.Q, io.ldQ);
+    io.vc = inplace_codec(V_quant, v_type, v_row_bytes, ldVq, d_v, false, nullptr, 0);
     auto carve = [&](Carver & cv, float *& dK, float *& dV, float *& dW, float *& tmp) {
-        dK = cv.take<float>((size_t)L * T * ek);
-        dV = cv.take<float>((size_t)L * T * ev);
+        dK = io.kc.base ? nullptr : cv.take<float>((size_t)L * T * ek);
+        dV = io.vc.base ? nullptr : cv.take<float>((size_t)L * T * ev);
         dW = host_w ? cv.take<float>(T) : nullptr;
         tmp = cv.take<float>(std::max<size_t>(requant_floats(qi, t, H, d_v), 1));
     };
@@ -1509,14 +1554,14 @@ int kvc_compact_quantized_layers_device(const uint8_t * K_quant, const uint8_t *
     if (dW && hipMemcpyAsync(dW, wts.data(), (size_t)T * 4, hipMemcpyHostToDevice, st) != hipSuccess)
         return KV_COMPACT_E_DEVICE;
     (void)hipEventRecord(ctx->q_ev[0], st);
-    dequant_cache(K_quant, k_type, k_row_bytes, ldKq, ek, T, L, dK, st);
-    dequant_cache(V_quant, v_type, v_row_bytes, ldVq, ev, T, L, dV, st);
+    if (!io.kc.base) dequant_cache(K_quant, k_type, k_row_bytes, ldKq, ek, T, L, dK, st);
+    if (!io.vc.base) dequant_cache(V_quant, v_type, v_row_bytes, ldVq, ev, T, L, dV, st);
     (void)hipEventRecord(ctx->q_ev[1], st);
     io.K = dK; io.V = dV; io.wts = dW;
     rc = run_batch(ctx, st, pl, p, io, cv, nullptr);
     if (rc != 0) return rc;
     (void)hipEventRecord(ctx->q_ev[2], st);
-    requant_outputs(qi, dK, io.indices, io.Cv, L, T, t, H, d_k, d_v, tmp, st);
+    requant_outputs(qi, dK, io.indices, io.Cv, L, T, t, H, d_k, d_v, tmp, st, io.kc);
     (void)hipEventRecord(ctx->q_ev[3], st);
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(st);

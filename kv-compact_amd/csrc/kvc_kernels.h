@@ -61,9 +61,11 @@ void launch_dequant8(const uint8_t * src, int type, long long row_bytes, long lo
                      float * dst, hipStream_t st);
 // mode 0: kept rows idx[l * idx_ls + j] of src (row stride src_ld, layer stride
 // src_ls floats); mode 1: value rows assembled from C_v [L][H][rows][dv]
+// sq.base != nullptr (mode 0): the kept rows are read in place from that
+// quantized cache (src unused) and re-encoded
 void launch_requant8(const float * src, long long src_ls, long long src_ld, const int * idx, long long idx_ls,
                      int mode, int H, int dv, int type, int n_el, int rows, int L, uint8_t * dst, long long row_bytes,
-                     long long dst_ls, hipStream_t st);
+                     long long dst_ls, hipStream_t st, RowCodec sq = RowCodec{});
 // state blobs: [rows][cols] -> [cols][rows]; kept key rows with the beta
 // fold; transposed value columns; the reference-query rows of each head
 void launch_transpose(const float * src, long long rows, long long cols, float * dst, hipStream_t st);

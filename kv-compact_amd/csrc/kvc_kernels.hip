@@ -122,6 +122,102 @@ __device__ __forceinline__ const float * query_row(const Geom & g, const float *
     return K + layer * g.ldK + (long long)(c.start + cheap_pos(qi, c.nq, c.Tc)) * ek;
 }
 
+// In-place quantized rows (RowCodec), decoded with the whole-cache codec's
+// products: Q8_0 d * q, Q4_0 d * (nibble - 8) with adjacent-pair nibbles
+// (state.h:355-375). TYPE (KV_TYPE_Q8_0 = 8 or KV_TYPE_Q4_0 = 2) is fixed per
+// kernel instance; codec_inst picks the instance for a RowCodec (0: fp32).
+__device__ __forceinline__ float f16_to_f32_ref(uint16_t hv);
+
+// f16 bits to f32, exact and without branches: the same bits as
+// f16_to_f32_ref (subnormals are m * 2^-24, a normal f32; Inf and NaN keep
+// their payload; zeros keep their sign)
+__device__ __forceinline__ float f16_bits_f32(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16, e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    const uint32_t sub = __float_as_uint((float)m * 0x1p-24f);
+    const uint32_t nrm = ((e + 112u) << 23) | (m << 13);
+    const uint32_t inf = 0x7F800000u | (m << 13);
+    return __uint_as_float(sign | (e == 0u ? sub : (e == 31u ? inf : nrm)));
+}
+
+inline int codec_inst(const RowCodec & rc) { return rc.base ? rc.type : 0; }
+
+__device__ __forceinline__ const uint8_t * codec_row(const RowCodec & rc, int l, long long r) {
+    return rc.base + l * rc.layer_bytes + r * rc.row_bytes;
+}
+
+// The loads and the decode apart, so that a loader can keep the raw bits in
+// registers while a tile is summed and decode them when it stores the next
+// one: Q8_0 {scale, 2 bytes, 2 bytes}, Q4_0 {scale, 2 bytes}. Elements
+// c .. c + 3 (c a multiple of 4: one block, aligned 2-byte fields) of a row
+// from its first byte.
+struct Raw4 {
+    uint32_t x, y, z, w;
+};
+template <int TYPE>
+__device__ __forceinline__ Raw4 codec_raw4_at(const uint8_t * row, int c) {
+    const int o = c & 31;
+    if constexpr (TYPE == 8) {
+        const uint8_t * bl = row + (c >> 5) * 34;
+        return Raw4{*reinterpret_cast<const uint16_t *>(bl), *reinterpret_cast<const uint16_t *>(bl + 2 + o),
+                    *reinterpret_cast<const uint16_t *>(bl + 4 + o), 0u};
+    } else {
+        const uint8_t * bl = row + (c >> 5) * 18;
+        return Raw4{*reinterpret_cast<const uint16_t *>(bl), *reinterpret_cast<const uint16_t *>(bl + 2 + (o >> 1)),
+                    0u, 0u};
+    }
+}
+template <int TYPE>
+__device__ __forceinline__ Raw4 codec_raw4(const RowCodec & rc, int l, long long r, int c) {
+    return codec_raw4_at<TYPE>(codec_row(rc, l, r), c);
+}
+template <int TYPE>
+__device__ __forceinline__ float4 codec_dec4(const Raw4 & v) {
+    const float d = f16_bits_f32(v.x);
+    if constexpr (TYPE == 8)
+        return make_float4(d * (float)(int8_t)(v.y & 0xFF), d * (float)(int8_t)(v.y >> 8),
+                           d * (float)(int8_t)(v.z & 0xFF), d * (float)(int8_t)(v.z >> 8));
+    else
+        return make_float4(d * ((float)(v.y & 0xF) - 8.0f), d * ((float)((v.y >> 4) & 0xF) - 8.0f),
+                           d * ((float)((v.y >> 8) & 0xF) - 8.0f), d * ((float)((v.y >> 12) & 0xF) - 8.0f));
+}
+template <int TYPE>
+__device__ __forceinline__ float4 codec_load4(const RowCodec & rc, int l, long long r, int c) {
+    return codec_dec4<TYPE>(codec_raw4<TYPE>(rc, l, r, c));
+}
+// element c (any) of row r of layer l
+template <int TYPE>
+__device__ __forceinline__ float codec_load1(const RowCodec & rc, int l, long long r, int c) {
+    const uint8_t * row = codec_row(rc, l, r);
+    const int o = c & 31;
+    if constexpr (TYPE == 8) {
+        const uint8_t * bl = row + (c >> 5) * 34;
+        return f16_bits_f32(*reinterpret_cast<const uint16_t *>(bl)) * (float)(int8_t)bl[2 + o];
+    } else {
+        const uint8_t * bl = row + (c >> 5) * 18;
+        const uint8_t b = bl[2 + (o >> 1)];
+        return f16_bits_f32(*reinterpret_cast<const uint16_t *>(bl)) * ((float)((o & 1) ? (b >> 4) : (b & 0xF)) - 8.0f);
+    }
+}
+// v where keep, else zero bits (per component: a select of the struct goes
+// through memory). Zero bits decode to +0 or -0 in every codec.
+__device__ __forceinline__ Raw4 raw_keep(bool keep, const Raw4 & v) {
+    return Raw4{keep ? v.x : 0u, keep ? v.y : 0u, keep ? v.z : 0u, keep ? v.w : 0u};
+}
+// a 16-byte fp32 load as raw bits, and back
+__device__ __forceinline__ Raw4 f32_raw4(const float * p) {
+    const float4 x = *reinterpret_cast<const float4 *>(p);
+    return Raw4{__float_as_uint(x.x), __float_as_uint(x.y), __float_as_uint(x.z), __float_as_uint(x.w)};
+}
+__device__ __forceinline__ float4 raw_f4(const Raw4 & v) {
+    return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+
+// K row (token index) of reference query qi of chunk c in the cheap modes
+__device__ __forceinline__ long long query_krow(const Geom & g, const ChunkDesc & c, int qi, int qmode) {
+    if (qmode == Q_CHEAP_GLOBAL) return cheap_pos(qi, g.nq_global, g.T);
+    return c.start + cheap_pos(qi, c.nq, c.Tc);
+}
+
 // order-preserving key of a float score (unsigned order = float order; NaN excluded by callers)
 __device__ __forceinline__ unsigned score_key(float x) {
     const unsigned b = __float_as_uint(x);
@@ -184,6 +280,9 @@ __device__ __forceinline__ unsigned dpp_half_max_u32(unsigned x) {
     return x;
 }
 
+// KC: 0, or the codec (8 Q8_0, 2 Q4_0) of a quantized K read in place (g.kc),
+// decoded in registers
+template <int KC>
 __global__ void __launch_bounds__(256)
 k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ K,
          const float * __restrict__ Q, float * __restrict__ S, int Hs, int nq_cap,
@@ -201,8 +300,12 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
     const int tid = threadIdx.x;
     const int tk = tid & 31, tr = tid >> 5;
     const long long ek = (long long)g.H * g.dk;
+    // K read in place from a quantized cache (uniform): the fast path below
+    // decodes its tiles in registers; the host sends such K only when that
+    // path is taken (d_k a multiple of 32, provided queries 16-byte aligned)
+    constexpr bool kcod = KC != 0;
     // key_idx: keys are rows key_idx[layer * t_total + j] (compacted statistics)
-    const float * Kl = K + layer * g.ldK + (key_idx ? 0 : (long long)c.start * ek) + (long long)h * g.dk;
+    const float * Kl = kcod ? nullptr : K + layer * g.ldK + (key_idx ? 0 : (long long)c.start * ek) + (long long)h * g.dk;
     const int * kix = key_idx ? key_idx + (long long)layer * g.t_total : nullptr;
     const float * bh = beta ? beta + ((long long)layer * g.H + h) * g.t_total : nullptr;
     float * Sl = S + layer * s_layer + h * s_head + c.start;
@@ -248,7 +351,8 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
         const long long row = (key < c.Tc) ? (kix ? (long long)kix[key] : (long long)key) : -1;
         kp[u] = (row >= 0) ? Kl + row * ek : nullptr;
     }
-    const bool vec = (g.dk & 3) == 0 && (ek & 3) == 0 && (reinterpret_cast<uintptr_t>(Kl) & 15) == 0 &&
+    const bool vec = (g.dk & 3) == 0 &&
+                     (kcod || ((ek & 3) == 0 && (reinterpret_cast<uintptr_t>(Kl) & 15) == 0)) &&
                      (qmode != Q_PROVIDED || ((reinterpret_cast<uintptr_t>(Q) & 15) == 0 && (g.ldQ & 3) == 0));
     if (vec && g.dk % SC_SLAB == 0) {
         // whole 16-byte slabs: every thread loads rows that exist (keys past
@@ -256,45 +360,65 @@ k_scores(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict
         // sums are not stored), with no branch around the loads, and the next
         // slab is loaded while this one is summed
         const float * kq[4];
+        long long kr[4];   // token rows (quantized K)
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int key = min(key0 + lr + 32 * u, c.Tc - 1);
-            kq[u] = Kl + (kix ? (long long)kix[key] : (long long)key) * ek + ld;
+            kr[u] = kix ? (long long)kix[key] : (long long)c.start + key;
+            kq[u] = kcod ? nullptr : Kl + (kix ? (long long)kix[key] : (long long)key) * ek + ld;
         }
+        const int kc0 = h * g.dk + ld;   // this thread's first element of a quantized row
+        const uint8_t * krp[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) krp[u] = kcod ? codec_row(g.kc, layer, kr[u]) : nullptr;
         // query rows as element offsets from qbase (a pointer kept in LDS
-        // would make the row loads flat ones, which every LDS wait waits for)
+        // would make the row loads flat ones, which every LDS wait waits for),
+        // or as K token rows when they are rows of a quantized K
+        const bool qcod = kcod && qmode != Q_PROVIDED;
         const float * qbase = qmode == Q_PROVIDED ? Q : K;
+        // raw loads (bits kept while a slab is summed), decoded at the LDS store
+        auto kload = [&](int u, int dn) -> Raw4 {
+            return kcod ? codec_raw4_at<KC>(krp[u], kc0 + dn) : f32_raw4(kq[u] + dn);
+        };
         for (int q0 = 0; q0 < nq; q0 += SC_ROWS) {
             __syncthreads();
             if (tid < SC_ROWS) {
-                const int qi = q0 + tid;
-                qoff[tid] = (query_row(g, K, Q, layer, c, qi < nq ? qi : 0, qmode) - qbase) + (long long)h * g.dk;
+                const int qi = q0 + tid, qq = qi < nq ? qi : 0;
+                qoff[tid] = qcod ? query_krow(g, c, qq, qmode)
+                                 : (query_row(g, K, Q, layer, c, qq, qmode) - qbase) + (long long)h * g.dk;
             }
             __syncthreads();
-            const float * qp = qbase + qoff[lr] + ld;
+            const long long qo = qoff[lr];
+            const float * qp = qcod ? nullptr : qbase + qo + ld;
+            const uint8_t * qrp = qcod ? codec_row(g.kc, layer, qo) : nullptr;
+            auto qload = [&](int dn) -> Raw4 {
+                return qcod ? codec_raw4_at<KC>(qrp, kc0 + dn) : f32_raw4(qp + dn);
+            };
             float acc[4][4];
 #pragma unroll
             for (int i = 0; i < 4; i++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) acc[i][j] = 0.0f;
-            float4 kx[4], qx;
+            Raw4 kx[4], qx;
 #pragma unroll
-            for (int u = 0; u < 4; u++) kx[u] = *reinterpret_cast<const float4 *>(kq[u]);
-            qx = *reinterpret_cast<const float4 *>(qp);
+            for (int u = 0; u < 4; u++) kx[u] = kload(u, 0);
+            qx = qload(0);
             for (int d0 = 0; d0 < g.dk; d0 += SC_SLAB) {
                 __syncthreads();
 #pragma unroll
                 for (int u = 0; u < 4; u++) {
                     const int kk = lr + 32 * u;
-                    ks[ld][kk] = kx[u].x; ks[ld + 1][kk] = kx[u].y; ks[ld + 2][kk] = kx[u].z; ks[ld + 3][kk] = kx[u].w;
+                    const float4 k4 = kcod ? codec_dec4<KC>(kx[u]) : raw_f4(kx[u]);
+                    ks[ld][kk] = k4.x; ks[ld + 1][kk] = k4.y; ks[ld + 2][kk] = k4.z; ks[ld + 3][kk] = k4.w;
                 }
-                qs[ld][lr] = qx.x; qs[ld + 1][lr] = qx.y; qs[ld + 2][lr] = qx.z; qs[ld + 3][lr] = qx.w;
+                const float4 q4 = qcod ? codec_dec4<KC>(qx) : raw_f4(qx);
+                qs[ld][lr] = q4.x; qs[ld + 1][lr] = q4.y; qs[ld + 2][lr] = q4.z; qs[ld + 3][lr] = q4.w;
                 __syncthreads();
                 // the next slab (the last one again at the end: no branch)
                 const int dn = min(d0 + SC_SLAB, g.dk - SC_SLAB);
 #pragma unroll
-                for (int u = 0; u < 4; u++) kx[u] = *reinterpret_cast<const float4 *>(kq[u] + dn);
-                qx = *reinterpret_cast<const float4 *>(qp + dn);
+                for (int u = 0; u < 4; u++) kx[u] = kload(u, dn);
+                qx = qload(dn);
                 asm volatile("" ::: "memory");   // keeps the loads ahead of the sums, not sunk to their use
                 // dimension dd + 1 is read from LDS while dd is summed
                 float4 kv = *reinterpret_cast<const float4 *>(&ks[0][4 * tk]);
@@ -592,11 +716,12 @@ constexpr int AS_KT = 32;
 // queries tq + TQ*i (i < QR) and columns tv + TV*k (k < VR) of a QB x VB
 // output block (QB = TQ*QR, VB = TV*VR); every output is a sequential sum
 // over the keys in order.
-template <int QR, int VR, int TV>
+template <int QR, int VR, int TV, int VC>
 __device__ __forceinline__ void attn_sum_tile(const float * __restrict__ a, const float * __restrict__ ascale,
                                               long long a_rs, int nq,
                                               const float * __restrict__ val, long long val_rs, int n,
-                                              int vn, float * __restrict__ out, long long out_rs) {
+                                              int vn, float * __restrict__ out, long long out_rs,
+                                              const RowCodec & vq, int layer, long long vrow0, int ve0) {
     constexpr int TQ = 256 / TV, QB = TQ * QR, VB = TV * VR;
     __shared__ float as[QB][AS_KT + 1];
     __shared__ float vs[AS_KT][VB + 1];
@@ -619,7 +744,11 @@ __device__ __forceinline__ void attn_sum_tile(const float * __restrict__ a, cons
                 }
                 for (int e = threadIdx.x; e < AS_KT * VB; e += 256) {
                     const int jj = e / VB, vv = e % VB;
-                    vs[jj][vv] = (jj < jn && vv < vb) ? val[(long long)(j0 + jj) * val_rs + v0 + vv] : 0.0f;
+                    // (a quantized V: token row vrow0 + j, element ve0 + column)
+                    vs[jj][vv] = (jj < jn && vv < vb)
+                                     ? (VC ? codec_load1<VC>(vq, layer, vrow0 + j0 + jj, ve0 + v0 + vv)
+                                                : val[(long long)(j0 + jj) * val_rs + v0 + vv])
+                                     : 0.0f;
                 }
                 __syncthreads();
                 for (int jj = 0; jj < jn; jj++) {
@@ -656,10 +785,12 @@ __device__ __forceinline__ void attn_sum_tile(const float * __restrict__ a, cons
 // while this one is summed. A zero term leaves a sum unchanged: a sum that
 // starts at +0 never becomes -0 (x + y is -0 only when both are -0), and
 // x + (+0) = x for every other x.
+template <int VC>
 __device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, const float * __restrict__ ascale,
                                              long long a_rs, int nq,
                                              const float * __restrict__ val, long long val_rs, int n,
-                                             float * __restrict__ out, long long out_rs) {
+                                             float * __restrict__ out, long long out_rs,
+                                             const RowCodec & vq, int layer, long long vrow0, int ve0) {
     __shared__ __align__(16) float as[AS_KT][32];
     __shared__ __align__(16) float vs[AS_KT][128];
     const int tid = threadIdx.x, tq = tid >> 5, tv = tid & 31;
@@ -673,6 +804,7 @@ __device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, const
         const float sc = ascale[min(q0 + lq, nq - 1)];
         float ra[4];
         float4 rv[4];
+        Raw4 rq[4];   // (quantized V) raw value bits, decoded at the LDS store
         auto load = [&](int j0) {
 #pragma unroll
             for (int u = 0; u < 4; u++) {
@@ -683,8 +815,12 @@ __device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, const
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int j = j0 + vk + 8 * u;
-                const float4 x = *reinterpret_cast<const float4 *>(val + (long long)min(j, n - 1) * val_rs + vc);
-                rv[u] = j < n ? x : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if constexpr (VC != 0) {
+                    rq[u] = raw_keep(j < n, codec_raw4<VC>(vq, layer, vrow0 + min(j, n - 1), ve0 + vc));
+                } else {
+                    const float4 x = *reinterpret_cast<const float4 *>(val + (long long)min(j, n - 1) * val_rs + vc);
+                    rv[u] = j < n ? x : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                }
             }
         };
         float acc[4][4];
@@ -698,7 +834,8 @@ __device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, const
 #pragma unroll
             for (int u = 0; u < 4; u++) as[lk + u][lq] = ra[u];
 #pragma unroll
-            for (int u = 0; u < 4; u++) *reinterpret_cast<float4 *>(&vs[vk + 8 * u][vc]) = rv[u];
+            for (int u = 0; u < 4; u++)
+                *reinterpret_cast<float4 *>(&vs[vk + 8 * u][vc]) = VC ? codec_dec4<VC>(rq[u]) : rv[u];
             __syncthreads();
             load(j0 + AS_KT);   // past the end: clamped rows, zeros (not used)
             asm volatile("" ::: "memory");   // keeps the loads ahead of the sums
@@ -735,6 +872,7 @@ __device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, const
 // Two kernels, so that each holds only its own LDS tiles: k_refit_target
 // for d_v = 128 with 16-byte aligned value rows (chosen on the host), and
 // k_refit_target_any for every other shape.
+template <int VC>   // 0, or the codec of a quantized V read in place (g.vc)
 __global__ void __launch_bounds__(256)
 k_refit_target(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ A,
                const float * __restrict__ ainv, const float * __restrict__ V, float * __restrict__ Y) {
@@ -743,11 +881,13 @@ k_refit_target(Geom g, const ChunkDesc * __restrict__ chunks, const float * __re
     const long long ev = (long long)g.H * g.dv;
     if (c.nq <= 0 || c.Tc <= 0) return;
     const float * sc = ainv + (((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max;
-    attn_sum_128(A + layer * lS(g) + h * hS(g) + c.start, sc, g.T, c.nq,
-                 V + layer * g.ldV + (long long)c.start * ev + (long long)h * g.dv, ev, c.Tc,
-                 Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv, g.dv);
+    attn_sum_128<VC>(A + layer * lS(g) + h * hS(g) + c.start, sc, g.T, c.nq,
+                 VC ? nullptr : V + layer * g.ldV + (long long)c.start * ev + (long long)h * g.dv, ev, c.Tc,
+                 Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv, g.dv,
+                 g.vc, layer, c.start, h * g.dv);
 }
 
+template <int VC>
 __global__ void __launch_bounds__(256)
 k_refit_target_any(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ A,
                    const float * __restrict__ ainv, const float * __restrict__ V, float * __restrict__ Y) {
@@ -755,9 +895,11 @@ k_refit_target_any(Geom g, const ChunkDesc * __restrict__ chunks, const float * 
     const ChunkDesc c = chunks[c_idx];
     const long long ev = (long long)g.H * g.dv;
     const float * sc = ainv + (((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max;
-    attn_sum_tile<4, 4, 32>(A + layer * lS(g) + h * hS(g) + c.start, sc, g.T, c.nq,
-                            V + layer * g.ldV + (long long)c.start * ev + (long long)h * g.dv, ev, c.Tc, g.dv,
-                            Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv, g.dv);
+    attn_sum_tile<4, 4, 32, VC>(A + layer * lS(g) + h * hS(g) + c.start, sc, g.T, c.nq,
+                            VC ? nullptr : V + layer * g.ldV + (long long)c.start * ev + (long long)h * g.dv,
+                            ev, c.Tc, g.dv,
+                            Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv, g.dv,
+                            g.vc, layer, c.start, h * g.dv);
 }
 
 // ---------------------------------------------------------------------------
@@ -781,6 +923,8 @@ constexpr int SV_QB = 16, SV_VB = 64, SV_KT = 64, SV_THREADS = 256;
 // SIMD at 104 VGPRs) while the original-attention statistics overlap the
 // factorizations
 constexpr int SV_LDS = (2 * SV_QB * (SV_KT + 1) + 2 * SV_KT * SV_VB) * 4;
+// VC: 0, or the codec of a quantized V (mode 1) read in place (g.vc)
+template <int VC>
 __global__ void __launch_bounds__(SV_THREADS) __attribute__((amdgpu_waves_per_eu(5, 8)))
 k_stats_values(Geom g, const float * __restrict__ a_all, const float * __restrict__ ascale, long long a_ls,
                long long a_hs, long long a_rs, int n,
@@ -793,9 +937,11 @@ k_stats_values(Geom g, const float * __restrict__ a_all, const float * __restric
     const float * a = a_all + layer * a_ls + h * a_hs;   // row q at a + q * a_rs
     const float * val;
     long long vrs;
+    // original attention over a quantized V: rows decoded in registers
+    const bool vcod = VC != 0 && mode == 1;
     if (mode == 1) {
         vrs = (long long)g.H * g.dv;
-        val = V + layer * g.ldV + (long long)h * g.dv;
+        val = vcod ? nullptr : V + layer * g.ldV + (long long)h * g.dv;
     } else {
         vrs = g.dv;
         val = Cv + ((long long)layer * g.H + h) * g.t_total * g.dv;
@@ -807,9 +953,9 @@ k_stats_values(Geom g, const float * __restrict__ a_all, const float * __restric
     const int tid = threadIdx.x, tq = tid >> 4, tv = tid & 15;
     const int qa = q0 + tq, vc = v0 + 4 * tv;
     // tile loaders: a: 16 x 64 (4 per thread); val: 64 x 64 (16 per thread, 4 float4)
-    const bool vvec = (g.dv & 3) == 0 && (vrs & 3) == 0 && (reinterpret_cast<uintptr_t>(val) & 15) == 0;
+    const bool vvec = (g.dv & 3) == 0 && (vcod || ((vrs & 3) == 0 && (reinterpret_cast<uintptr_t>(val) & 15) == 0));
     float ra[4];
-    float4 rv[4];
+    Raw4 rv[4];   // raw value bits (a quantized V is decoded at the LDS store)
     // row scales (the weights are a * ascale[row] when ascale is given),
     // applied at the LDS store: a product at the load would make each load
     // wait for its data before the next is issued
@@ -830,16 +976,22 @@ k_stats_values(Geom g, const float * __restrict__ a_all, const float * __restric
         for (int u = 0; u < 4; u++) {
             const int e = tid + SV_THREADS * u, jj = e >> 4, c4 = (e & 15) * 4;
             const int j = j0 + jj, c = v0 + c4;
-            float4 x = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            Raw4 x{0u, 0u, 0u, 0u};
             if (j < n) {
-                const float * src = val + (long long)j * vrs + c;
-                if (vvec && c + 3 < g.dv) {
-                    x = *reinterpret_cast<const float4 *>(src);
+                if (vcod && c + 3 < g.dv) {
+                    x = codec_raw4<VC>(g.vc, layer, j, h * g.dv + c);
+                } else if (vcod) {
+                    // columns past d_v stay zero
                 } else {
-                    if (c < g.dv) x.x = src[0];
-                    if (c + 1 < g.dv) x.y = src[1];
-                    if (c + 2 < g.dv) x.z = src[2];
-                    if (c + 3 < g.dv) x.w = src[3];
+                    const float * src = val + (long long)j * vrs + c;
+                    if (vvec && c + 3 < g.dv) {
+                        x = f32_raw4(src);
+                    } else {
+                        if (c < g.dv) x.x = __float_as_uint(src[0]);
+                        if (c + 1 < g.dv) x.y = __float_as_uint(src[1]);
+                        if (c + 2 < g.dv) x.z = __float_as_uint(src[2]);
+                        if (c + 3 < g.dv) x.w = __float_as_uint(src[3]);
+                    }
                 }
             }
             rv[u] = x;
@@ -854,7 +1006,8 @@ k_stats_values(Geom g, const float * __restrict__ a_all, const float * __restric
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const int e = tid + SV_THREADS * u;
-            *reinterpret_cast<float4 *>(&Vs[b][e >> 4][(e & 15) * 4]) = rv[u];
+            // (zero bits: padded keys and columns, +0 or -0 in every codec)
+            *reinterpret_cast<float4 *>(&Vs[b][e >> 4][(e & 15) * 4]) = vcod ? codec_dec4<VC>(rv[u]) : raw_f4(rv[u]);
         }
     };
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1203,6 +1356,7 @@ k_div_candidates(Geom g, const ChunkDesc * __restrict__ chunks, const float * __
 // sub-tile skips the sums). grid (units, tile pairs).
 constexpr int DG_TILE = 64, DG_SLAB = 32;
 
+template <int KC>   // 0, or the codec of a quantized K read in place (g.kc)
 __global__ void __launch_bounds__(256)
 k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ K, DivWork dw,
            const int * __restrict__ cand_all) {
@@ -1220,7 +1374,8 @@ k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     const ChunkDesc c = chunks[c_idx];
     const int E = g.H * g.dk;
     const int * cand = cand_all + (long long)unit * g.Tc_max;
-    const float * Kl = K + (long long)layer * g.ldK + (long long)c.start * E;
+    constexpr bool kcod = KC != 0;   // rows of a quantized K, decoded in registers
+    const float * Kl = kcod ? nullptr : K + (long long)layer * g.ldK + (long long)c.start * E;
     __shared__ __align__(16) float As[DG_SLAB][DG_TILE + 4];
     __shared__ __align__(16) float Bs[DG_SLAB][DG_TILE + 4];
     // rows from tile ta, columns from tile tb: the partial last tile, if in
@@ -1244,9 +1399,11 @@ k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     // loader: row lr of the tile, dims lq*8 .. lq*8+7 of the slab
     const int lr = tid >> 2, lq = tid & 3;
     const int ra = ta * DG_TILE + lr, rb = tb * DG_TILE + lr;
-    const float * pa = Kl + (long long)cand[ra < C ? ra : C - 1] * E + lq * 8;
-    const float * pb = Kl + (long long)cand[rb < C ? rb : C - 1] * E + lq * 8;
-    const bool vec = (E & 3) == 0 && (reinterpret_cast<uintptr_t>(Kl) & 15) == 0;
+    const long long rra = c.start + cand[ra < C ? ra : C - 1], rrb = c.start + cand[rb < C ? rb : C - 1];
+    const float * pa = kcod ? nullptr : Kl + (rra - c.start) * E + lq * 8;
+    const float * pb = kcod ? nullptr : Kl + (rrb - c.start) * E + lq * 8;
+    // (a quantized row holds whole 32-element blocks: E is a multiple of 32)
+    const bool vec = kcod || ((E & 3) == 0 && (reinterpret_cast<uintptr_t>(Kl) & 15) == 0);
     float acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
@@ -1255,8 +1412,15 @@ k_div_gram(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     for (int d0 = 0; d0 < E; d0 += DG_SLAB) {
         float va[8], vb[8];
         if (vec && d0 + DG_SLAB <= E) {
-            const float4 a0 = *reinterpret_cast<const float4 *>(pa + d0), a1 = *reinterpret_cast<const float4 *>(pa + d0 + 4);
-            const float4 b0 = *reinterpret_cast<const float4 *>(pb + d0), b1 = *reinterpret_cast<const float4 *>(pb + d0 + 4);
+            float4 a0, a1, b0, b1;
+            if (kcod) {
+                const int e0 = d0 + lq * 8;
+                a0 = codec_load4<KC>(g.kc, layer, rra, e0); a1 = codec_load4<KC>(g.kc, layer, rra, e0 + 4);
+                b0 = codec_load4<KC>(g.kc, layer, rrb, e0); b1 = codec_load4<KC>(g.kc, layer, rrb, e0 + 4);
+            } else {
+                a0 = *reinterpret_cast<const float4 *>(pa + d0); a1 = *reinterpret_cast<const float4 *>(pa + d0 + 4);
+                b0 = *reinterpret_cast<const float4 *>(pb + d0); b1 = *reinterpret_cast<const float4 *>(pb + d0 + 4);
+            }
             va[0] = a0.x; va[1] = a0.y; va[2] = a0.z; va[3] = a0.w; va[4] = a1.x; va[5] = a1.y; va[6] = a1.z; va[7] = a1.w;
             vb[0] = b0.x; vb[1] = b0.y; vb[2] = b0.z; vb[3] = b0.w; vb[4] = b1.x; vb[5] = b1.y; vb[6] = b1.z; vb[7] = b1.w;
         } else {
@@ -4243,7 +4407,7 @@ k_dequant8(const uint8_t * __restrict__ src, int type, long long row_bytes, long
 __global__ void __launch_bounds__(256)
 k_requant8(const float * __restrict__ src, long long src_ls, long long src_ld, const int * __restrict__ idx,
            long long idx_ls, int mode, int H, int dv, int type, int n_el, int rows, int L,
-           uint8_t * __restrict__ dst, long long row_bytes, long long dst_ls) {
+           uint8_t * __restrict__ dst, long long row_bytes, long long dst_ls, RowCodec sq) {
     const int n8 = n_el >> 3;
     const long long total = (long long)L * rows * n8;   // a multiple of 4: quads stay whole
     for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < total;
@@ -4251,14 +4415,28 @@ k_requant8(const float * __restrict__ src, long long src_ls, long long src_ld, c
         const long long rr = e / n8;
         const int q = (int)(e - rr * n8);
         const long long l = rr / rows, j = rr - l * rows;
-        const float * x;
-        if (mode == 0) {
-            x = src + l * src_ls + (long long)idx[l * idx_ls + j] * src_ld + 8 * q;
+        float4 a, b;
+        if (mode == 0 && sq.base) {
+            // kept rows of a quantized cache read in place: decoded, then re-encoded
+            const long long r = idx[l * idx_ls + j];
+            if (sq.type == 8) {
+                a = codec_load4<8>(sq, (int)l, r, 8 * q);
+                b = codec_load4<8>(sq, (int)l, r, 8 * q + 4);
+            } else {
+                a = codec_load4<2>(sq, (int)l, r, 8 * q);
+                b = codec_load4<2>(sq, (int)l, r, 8 * q + 4);
+            }
         } else {
-            const int h = (8 * q) / dv, v = 8 * q - h * dv;
-            x = src + (((l * H + h) * rows + j) * dv + v);
+            const float * x;
+            if (mode == 0) {
+                x = src + l * src_ls + (long long)idx[l * idx_ls + j] * src_ld + 8 * q;
+            } else {
+                const int h = (8 * q) / dv, v = 8 * q - h * dv;
+                x = src + (((l * H + h) * rows + j) * dv + v);
+            }
+            a = reinterpret_cast<const float4 *>(x)[0];
+            b = reinterpret_cast<const float4 *>(x)[1];
         }
-        const float4 a = reinterpret_cast<const float4 *>(x)[0], b = reinterpret_cast<const float4 *>(x)[1];
         const float xv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
         uint8_t * o = dst + l * dst_ls + j * row_bytes;
         if (type == 8 || type == 2) {
@@ -4456,8 +4634,19 @@ void launch_scores(const Geom & g, const ChunkDesc * chunks, int n_chunk_units, 
                    long long s_layer, long long s_head, long long s_row, int qmode, hipStream_t st,
                    const int * key_idx, const float * beta, unsigned * tmax) {
     dim3 grid(cdiv(Tc_max, SC_KEYS), n_chunk_units * Hs, g.L);
-    hipLaunchKernelGGL(k_scores, grid, dim3(256), 0, st, g, chunks, K, Q, S, Hs, nq_cap,
-                       s_layer, s_head, s_row, qmode, key_idx, beta, tmax);
+    switch (codec_inst(g.kc)) {
+    case 8:
+        hipLaunchKernelGGL(k_scores<8>, grid, dim3(256), 0, st, g, chunks, K, Q, S, Hs, nq_cap,
+                           s_layer, s_head, s_row, qmode, key_idx, beta, tmax);
+        break;
+    case 2:
+        hipLaunchKernelGGL(k_scores<2>, grid, dim3(256), 0, st, g, chunks, K, Q, S, Hs, nq_cap,
+                           s_layer, s_head, s_row, qmode, key_idx, beta, tmax);
+        break;
+    default:
+        hipLaunchKernelGGL(k_scores<0>, grid, dim3(256), 0, st, g, chunks, K, Q, S, Hs, nq_cap,
+                           s_layer, s_head, s_row, qmode, key_idx, beta, tmax);
+    }
 }
 
 void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st) {
@@ -4472,17 +4661,25 @@ void launch_chunk_softmax(const Geom & g, const Work & w, hipStream_t st) {
                            g, w.chunks, g.score_method != 0 ? w.amax : w.imp, w.sens);
 }
 
+template <int VC>
+void launch_refit_inst(const Geom & g, const Work & w, const float * V, bool v128, hipStream_t st) {
+    const dim3 grid(g.n_chunks * g.H, g.L);
+    if (v128)
+        hipLaunchKernelGGL(k_refit_target<VC>, grid, dim3(256), 0, st, g, w.chunks, w.A, w.ainv, V, w.Y);
+    else
+        hipLaunchKernelGGL(k_refit_target_any<VC>, grid, dim3(256), 0, st, g, w.chunks, w.A, w.ainv, V, w.Y);
+}
+
 void launch_refit_target(const Geom & g, const Work & w, const float * V, hipStream_t st) {
     // every (layer, chunk, head) value row starts 16-byte aligned when V does
-    // and the layer, token and head strides are multiples of four floats
-    const bool v128 = g.dv == 128 && (reinterpret_cast<uintptr_t>(V) & 15) == 0 && (g.ldV & 3) == 0 &&
-                      (((long long)g.H * g.dv) & 3) == 0;
-    if (v128)
-        hipLaunchKernelGGL(k_refit_target, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
-                           g, w.chunks, w.A, w.ainv, V, w.Y);
-    else
-        hipLaunchKernelGGL(k_refit_target_any, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
-                           g, w.chunks, w.A, w.ainv, V, w.Y);
+    // and the layer, token and head strides are multiples of four floats (a
+    // quantized V read in place is decoded four elements at a time)
+    const int vc = codec_inst(g.vc);
+    const bool v128 = g.dv == 128 && (vc || ((reinterpret_cast<uintptr_t>(V) & 15) == 0 && (g.ldV & 3) == 0 &&
+                                              (((long long)g.H * g.dv) & 3) == 0));
+    if (vc == 8) launch_refit_inst<8>(g, w, V, v128, st);
+    else if (vc == 2) launch_refit_inst<2>(g, w, V, v128, st);
+    else launch_refit_inst<0>(g, w, V, v128, st);
 }
 
 void launch_global_importance(const Geom & g, const Work & w, hipStream_t st) {
@@ -4494,7 +4691,12 @@ void launch_div_level(const Geom & g, const Work & w, const DivWork & dw, const 
     const unsigned units = (unsigned)(g.L * g.n_chunks);
     const int nt = cdiv(dw.cap, DG_TILE);
     hipLaunchKernelGGL(k_div_candidates, dim3(g.n_chunks, g.L), dim3(256), 0, st, g, w.chunks, w.gimp, dw, w.cand);
-    hipLaunchKernelGGL(k_div_gram, dim3(units, nt * (nt + 1) / 2), dim3(256), 0, st, g, w.chunks, K, dw, w.cand);
+    const dim3 ggrid(units, nt * (nt + 1) / 2);
+    switch (codec_inst(g.kc)) {
+    case 8: hipLaunchKernelGGL(k_div_gram<8>, ggrid, dim3(256), 0, st, g, w.chunks, K, dw, w.cand); break;
+    case 2: hipLaunchKernelGGL(k_div_gram<2>, ggrid, dim3(256), 0, st, g, w.chunks, K, dw, w.cand); break;
+    default: hipLaunchKernelGGL(k_div_gram<0>, ggrid, dim3(256), 0, st, g, w.chunks, K, dw, w.cand);
+    }
     if (dw.cap <= 8 * 64)
         hipLaunchKernelGGL(k_div_greedy<8>, dim3(units), dim3(64), 0, st, g, w.chunks, w.gimp, dw, w.cand, w.sel);
     else
@@ -4654,8 +4856,20 @@ void launch_stats_original(const Geom & g, const Work & w, const StatWork & sw, 
     }
     hipLaunchKernelGGL(k_row_softmax, dim3(rsm_blocks, g.L), dim3(RSM_THREADS), 0, st,
                        os, g.T, o_ls, o_hs, (long long)g.T, sw.mh, sw.mq, ms, sw.OI);
-    hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), SV_LDS, st,
-                       g, os, sw.OI, o_ls, o_hs, (long long)g.T, g.T, V, nullptr, 1, sw.OO, sw.mh, sw.mq);
+    const dim3 sgrid(sv_blocks, g.L);
+    switch (codec_inst(g.vc)) {
+    case 8:
+        hipLaunchKernelGGL(k_stats_values<8>, sgrid, dim3(SV_THREADS), SV_LDS, st,
+                           g, os, sw.OI, o_ls, o_hs, (long long)g.T, g.T, V, nullptr, 1, sw.OO, sw.mh, sw.mq);
+        break;
+    case 2:
+        hipLaunchKernelGGL(k_stats_values<2>, sgrid, dim3(SV_THREADS), SV_LDS, st,
+                           g, os, sw.OI, o_ls, o_hs, (long long)g.T, g.T, V, nullptr, 1, sw.OO, sw.mh, sw.mq);
+        break;
+    default:
+        hipLaunchKernelGGL(k_stats_values<0>, sgrid, dim3(SV_THREADS), SV_LDS, st,
+                           g, os, sw.OI, o_ls, o_hs, (long long)g.T, g.T, V, nullptr, 1, sw.OO, sw.mh, sw.mq);
+    }
 }
 
 // Compacted attention over the kept keys with beta and C_v (outputs CO), then
@@ -4672,7 +4886,7 @@ void launch_stats_compacted(const Geom & g, const Work & w, const StatWork & sw,
     hipLaunchKernelGGL(k_row_softmax, dim3(rsm_blocks, g.L), dim3(RSM_THREADS), 0, st,
                        sw.CS, g.t_total, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, sw.mh, sw.mq,
                        RowMaxSrc{}, sw.CI);
-    hipLaunchKernelGGL(k_stats_values, dim3(sv_blocks, g.L), dim3(SV_THREADS), SV_LDS, st,
+    hipLaunchKernelGGL(k_stats_values<0>, dim3(sv_blocks, g.L), dim3(SV_THREADS), SV_LDS, st,
                        g, sw.CS, sw.CI, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, g.t_total, V, Cv, 2,
                        sw.CO, sw.mh, sw.mq);
 }
@@ -4720,12 +4934,12 @@ void launch_dequant8(const uint8_t * src, int type, long long row_bytes, long lo
 
 void launch_requant8(const float * src, long long src_ls, long long src_ld, const int * idx, long long idx_ls,
                      int mode, int H, int dv, int type, int n_el, int rows, int L, uint8_t * dst, long long row_bytes,
-                     long long dst_ls, hipStream_t st) {
+                     long long dst_ls, hipStream_t st, RowCodec sq) {
     const long long total = (long long)L * rows * (n_el / 8);
     if (total <= 0) return;
     const long long blocks = std::min<long long>((total + 255) / 256, 1LL << 30);
     hipLaunchKernelGGL(k_requant8, dim3((unsigned)blocks), dim3(256), 0, st,
-                       src, src_ls, src_ld, idx, idx_ls, mode, H, dv, type, n_el, rows, L, dst, row_bytes, dst_ls);
+                       src, src_ls, src_ld, idx, idx_ls, mode, H, dv, type, n_el, rows, L, dst, row_bytes, dst_ls, sq);
 }
 
 void launch_transpose(const float * src, long long rows, long long cols, float * dst, hipStream_t st) {

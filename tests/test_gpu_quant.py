@@ -12,7 +12,9 @@ which test_oracle.py pins against the oracle's row quantizer).
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
+import os
 
 import numpy as np
 import pytest
@@ -107,22 +109,74 @@ def same_device(dv, l, ref, H, d):
     assert np.array_equal(dv["V_out"][l], ref.V_out), "V_out"
 
 
+@contextlib.contextmanager
+def inplace(flag):
+    """KVC_INPLACE=0 sends Q8_0 / Q4_0 caches through the whole-cache decode
+    instead of the kernels' in-register decode; both must give the oracle's
+    outputs."""
+    old = os.environ.get("KVC_INPLACE")
+    os.environ["KVC_INPLACE"] = flag
+    try:
+        yield
+    finally:
+        if old is None:
+            os.environ.pop("KVC_INPLACE", None)
+        else:
+            os.environ["KVC_INPLACE"] = old
+
+
+@pytest.mark.parametrize("mode", ["1", "0"])
 @pytest.mark.parametrize("kt,vt", [(8, 8), (2, 2), (2, 8)])
-def test_config4_chunked(gpu, orc, kt, vt):
-    """8 heads x d = 128, T = 2560 (two 1280-token chunks), both device entries and the host entry."""
+def test_config4_chunked(gpu, orc, kt, vt, mode):
+    """8 heads x d = 128, T = 2560 (two 1280-token chunks), both device entries and the host entry,
+    with K and V decoded in the kernels (mode 1) and by the whole-cache pass (mode 0)."""
     T, H, d = 2560, 8, 128
-    print(f"[quant] config-4 shape T={T} k_type={kt} v_type={vt}", flush=True)
+    print(f"[quant] config-4 shape T={T} k_type={kt} v_type={vt} inplace={mode}", flush=True)
     K, V = kv_cache(T, H, d, 4000 + kt * 10 + vt)
     Kq, Vq = quantize_rows(K, kt), quantize_rows(V, vt)
     pk = dict(target_ratio=0.2, use_cheap_qref=1)
     args = (Kq, Vq, None, kt, vt, Kq.shape[1], Vq.shape[1], T, 0, H, d, d)
     rb, b = orc.quantized(*args, orc.params(**pk))
+    with inplace(mode):
+        ra, a = gpu.quantized(*args, gpu.params(**pk))
+        dv = device_call(gpu, Kq[None], Vq[None], kt, vt, 1, T, H, d, gpu.params(**pk))
+    assert ra == 0 and rb == 0
+    same(a, b)
+    assert np.array_equal(a.K_out, b.K_out) and np.array_equal(a.V_out, b.V_out)
+    same_device(dv, 0, b, H, d)
+
+
+@pytest.mark.parametrize("case", ["given_q_beta", "diversity", "d96"])
+def test_quantized_options(gpu, orc, case):
+    """In-register decode on the other readers of K and V: provided reference
+    queries with the beta fit (scores of a quantized K against fp32 queries),
+    the diversity Gram of quantized key rows, and d = 96 (the general refit
+    tiles and statistics columns past d_v)."""
+    T, H, d = 2560, 8, 128
+    kt, vt = 8, 2
+    pk = dict(target_ratio=0.2)
+    if case == "d96":
+        H, d, kt, vt = 4, 96, 2, 8
+    K, V = kv_cache(T, H, d, 4300 + len(case))
+    Kq, Vq = quantize_rows(K, kt), quantize_rows(V, vt)
+    Q, nq = None, 0
+    if case == "given_q_beta":
+        Kd = dequant_q(Kq, kt)
+        Q = np.ascontiguousarray(Kd[-32:] + np.float32(0.1) * np.random.default_rng(43).standard_normal(
+            (32, H * d), dtype=np.float32), np.float32)
+        nq = 32
+        pk.update(skip_beta=0)
+    else:
+        pk.update(use_cheap_qref=1)
+    if case == "diversity":
+        pk.update(use_diversity=1, diversity_strength=0.5)
+    print(f"[quant] options {case} T={T} H={H} d={d}", flush=True)
+    args = (Kq, Vq, Q, kt, vt, Kq.shape[1], Vq.shape[1], T, nq, H, d, d)
+    rb, b = orc.quantized(*args, orc.params(**pk))
     ra, a = gpu.quantized(*args, gpu.params(**pk))
     assert ra == 0 and rb == 0
     same(a, b)
     assert np.array_equal(a.K_out, b.K_out) and np.array_equal(a.V_out, b.V_out)
-    dv = device_call(gpu, Kq[None], Vq[None], kt, vt, 1, T, H, d, gpu.params(**pk))
-    same_device(dv, 0, b, H, d)
 
 
 def test_quantized_layers_device(gpu, orc):
