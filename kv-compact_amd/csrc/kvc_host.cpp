@@ -860,9 +860,20 @@ void record_codec_times(DeviceCtx * ctx) {
 }
 
 // rows [L][T] of a codec into fp32 [L][T][n_el]
+// The coalesced codec kernels read and write the 2-byte fields of Q8_0, Q4_0,
+// F16 and BF16 rows as 2-byte accesses: they need even addresses (row strides
+// of these codecs are even; base and layer strides are the caller's). Other
+// layouts go through the per-row kernels, which move single bytes.
+bool two_byte_ok(int type, const void * base, long long ls) {
+    if (type != KV_TYPE_Q8_0 && type != KV_TYPE_Q4_0 && type != KV_TYPE_F16 && type != KV_TYPE_BF16) return true;
+    return ((reinterpret_cast<uintptr_t>(base) | (uintptr_t)ls) & 1) == 0;
+}
+
 void dequant_cache(const uint8_t * src, int type, size_t rb, long long ls, int n_el, int T, int L, float * dst,
                    hipStream_t st) {
-    if (codec8_ok(type, n_el)) {
+    // (the coalesced kernel assembles F16 / BF16 / F32 elements from bytes)
+    const bool even = ((reinterpret_cast<uintptr_t>(src) | (uintptr_t)ls | (uintptr_t)rb) & 1) == 0;
+    if (codec8_ok(type, n_el) && (even || (type != KV_TYPE_Q8_0 && type != KV_TYPE_Q4_0))) {
         launch_dequant8(src, type, (long long)rb, ls, n_el, T, L, dst, st);
         return;
     }
@@ -910,11 +921,13 @@ void requant_outputs(const QuantIO & qi, const float * Kf, const int * idx, cons
     if (t <= 0) return;
     const int ek = H * dk, ev = H * dv;
     const bool cv_al = (reinterpret_cast<uintptr_t>(Cv) & 15) == 0;
+    const bool k_even = two_byte_ok(qi.k_type, qi.Kout, 0), v_even = two_byte_ok(qi.v_type, qi.Vout, 0);
     if (kc.base) {
         // K read in place: its kept rows are decoded and re-encoded in one pass
+        // (in place only with an even K_out)
         launch_requant8(nullptr, 0, 0, idx, t, 0, H, dk, qi.k_type, ek, t, L, qi.Kout, (long long)qi.k_rb,
                         (long long)t * qi.k_rb, st, kc);
-    } else if (codec8_ok(qi.k_type, ek)) {
+    } else if (codec8_ok(qi.k_type, ek) && k_even) {
         launch_requant8(Kf, (long long)T * ek, ek, idx, t, 0, H, dk, qi.k_type, ek, t, L, qi.Kout,
                         (long long)qi.k_rb, (long long)t * qi.k_rb, st);
     } else {
@@ -922,7 +935,7 @@ void requant_outputs(const QuantIO & qi, const float * Kf, const int * idx, cons
             launch_quant_rows(Kf + (long long)l * T * ek, ek, idx + (long long)l * t, qi.k_type, ek, t,
                               qi.Kout + (long long)l * t * qi.k_rb, (long long)qi.k_rb, st);
     }
-    if (codec8_ok(qi.v_type, ev) && dv % 8 == 0 && cv_al) {
+    if (codec8_ok(qi.v_type, ev) && dv % 8 == 0 && cv_al && v_even) {
         launch_requant8(Cv, 0, 0, nullptr, 0, 1, H, dv, qi.v_type, ev, t, L, qi.Vout, (long long)qi.v_rb,
                         (long long)t * qi.v_rb, st);
     } else {
@@ -1535,7 +1548,9 @@ int kvc_compact_quantized_layers_device(const uint8_t * K_quant, const uint8_t *
     io.indices = out->indices; io.beta = out->beta; io.Cv = out->C_v; io.stats = out->stats;
     std::vector<float> wts;
     const bool host_w = rkv_weights(p, T, wts);
-    io.kc = inplace_codec(K_quant, k_type, k_row_bytes, ldKq, d_k, true, io.Q, io.ldQ);
+    // (the kept rows of an in-place K are re-encoded with 2-byte stores: even K_out)
+    io.kc = two_byte_ok(k_type, K_out, 0) ? inplace_codec(K_quant, k_type, k_row_bytes, ldKq, d_k, true, io.Q, io.ldQ)
+                                          : RowCodec{};
     io.vc = inplace_codec(V_quant, v_type, v_row_bytes, ldVq, d_v, false, nullptr, 0);
     auto carve = [&](Carver & cv, float *& dK, float *& dV, float *& dW, float *& tmp) {
         dK = io.kc.base ? nullptr : cv.take<float>((size_t)L * T * ek);

@@ -238,3 +238,48 @@ def test_config4_full_size(gpu, typ):
         assert np.array_equal(quantize_rows(kept, typ), dv["K_out"][l][j])
         vrows = dv["C_v"][l][:, j, :].transpose(1, 0, 2).reshape(len(j), E)
         assert np.array_equal(quantize_rows(vrows, typ), dv["V_out"][l][j])
+
+
+def test_quantized_odd_layout(gpu, orc):
+    """Odd layer strides and odd output addresses (caller layouts the 2-byte
+    codec accesses cannot take): K and V go through the byte-wise decode and
+    the kept rows through the byte-wise encode; outputs equal the oracle's."""
+    import hiprt
+    L, T, H, d, kt, vt = 2, 1536, 4, 64, 8, 2
+    print(f"[quant] odd layout L={L} T={T} H={H} d={d}", flush=True)
+    krb, vrb = H * d // 32 * ROW_BYTES[kt], H * d // 32 * ROW_BYTES[vt]
+    lsk, lsv = T * krb + 1, T * vrb + 3
+    Kq = np.zeros(L * lsk, np.uint8)
+    Vq = np.zeros(L * lsv, np.uint8)
+    per = []
+    for l in range(L):
+        K, V = kv_cache(T, H, d, 4400 + l)
+        kq, vq = quantize_rows(K, kt), quantize_rows(V, vt)
+        Kq[l * lsk:l * lsk + T * krb] = kq.reshape(-1)
+        Vq[l * lsv:l * lsv + T * vrb] = vq.reshape(-1)
+        per.append((kq, vq))
+    p = gpu.params(target_ratio=0.2, use_cheap_qref=1)
+    dll = gpu.dll
+    t, _ = kc.plan(dll, T, 0, False, p)
+    dKq, dVq = hiprt.DevBuf(Kq.nbytes), hiprt.DevBuf(Vq.nbytes)
+    dKq.upload(Kq)
+    dVq.upload(Vq)
+    idx, beta, cv, st = (hiprt.DevBuf(n * 4) for n in (L * t, L * H * t, L * H * t * d, L * 3))
+    ko, vo = hiprt.DevBuf(L * t * krb + 16), hiprt.DevBuf(L * t * vrb + 16)
+    out = kc.DeviceOut(idx.value, beta.value, cv.value, st.value)
+    rc = dll.kvc_compact_quantized_layers_device(dKq.value, dVq.value, None, L, kt, vt, krb, vrb, T, 0, H, d, d,
+                                                 lsk, lsv, 0, ctypes.byref(p), ctypes.byref(out),
+                                                 ko.value + 1, vo.value + 3, None)
+    assert rc == 0
+    dv = dict(t=t, indices=idx.download(np.int32, L * t).reshape(L, t),
+              beta=beta.download(np.float32, L * H * t).reshape(L, H, t),
+              C_v=cv.download(np.float32, L * H * t * d).reshape(L, H, t, d),
+              stats=st.download(np.float32, L * 3).reshape(L, 3),
+              K_out=ko.download(np.uint8, L * t * krb + 16)[1:1 + L * t * krb].reshape(L, t, krb),
+              V_out=vo.download(np.uint8, L * t * vrb + 16)[3:3 + L * t * vrb].reshape(L, t, vrb))
+    for l in range(L):
+        kq, vq = per[l]
+        rb, b = orc.quantized(kq, vq, None, kt, vt, krb, vrb, T, 0, H, d, d, orc.params(target_ratio=0.2,
+                                                                                     use_cheap_qref=1))
+        assert rb == 0
+        same_device(dv, l, b, H, d)
