@@ -358,6 +358,45 @@ def quantized_mode(dll, lib, hiprt, L, T, H, d, ratio, steps, warmup, seed):
     return res
 
 
+def state_mode(dll, hiprt, L, T, H, d, ratio, steps, warmup, seed):
+    """A llama.cpp sequence state blob (F16 K and V rows, L layers x H heads x
+    d) compacted by kvc_state_compact_device: parse, score every layer with the
+    default reference queries (the last max(16, T/4) keys), one top-t across
+    layers and heads, per-head value refit and beta directions, blob written
+    back; device blob in, device blob out."""
+    sys.path.insert(0, str(REPO / "tests"))
+    from kvc_data import T_F16, state_blob
+    c = dict(T=T, L=L, H=H, dk=d, dv=d, kt=T_F16, vt=T_F16, vtrans=0, seed=seed, ratio=ratio)
+    blob = state_blob(c)
+    p, keep = kc.state_params(ratio, H)
+    f = dll.kvc_state_compact_device
+    f.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(kc.StateParams), ctypes.c_void_p,
+                  ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t), ctypes.c_void_p, ctypes.c_void_p]
+    f.restype = ctypes.c_int
+    src, dst = hiprt.DevBuf(len(blob)), hiprt.DevBuf(len(blob))
+    src.upload(np.frombuffer(blob, np.uint8))
+    n = ctypes.c_size_t(0)
+
+    def step():
+        rc = f(src.value, len(blob), ctypes.byref(p), dst.value, len(blob), ctypes.byref(n), None, None)
+        if rc != 0:
+            raise RuntimeError(f"kvc_state_compact_device returned {rc}")
+    for _ in range(warmup):
+        step()
+    hiprt.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    hiprt.synchronize()
+    ms = (time.perf_counter() - t0) / steps * 1e3
+    t = max(1, int(np.float32(T) * np.float32(ratio)))
+    del keep
+    return {"workload": f"{L} layers x {H} KV heads x d={d}, {T} cells, F16 rows, keep {ratio:g} "
+                        f"({t} cells, one set for all layers), default reference queries ({max(16, T // 4)})",
+            "ms_per_call": round(ms, 3), "cells_per_s": round(T / (ms / 1e3), 1),
+            "blob_bytes_in": len(blob), "blob_bytes_out": int(n.value)}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -486,6 +525,8 @@ def main():
     extras = {}
     if not a.no_extras:
         extras["quantized"] = quantized_mode(dll, lib, hiprt, 32, 32768, H, d, a.ratio, a.steps, a.warmup, a.seed + 7)
+        extras["state_blob"] = state_mode(dll, hiprt, 32, 2048, H, d, a.ratio, 3, 1, a.seed + 11)
+        print(f"[bench] state blob: {extras['state_blob']}", file=sys.stderr, flush=True)
         extras["drop_in_host_pointers"] = drop_in_mode(lib, L, T, H, d, W, a.ratio, a.diversity, a.seed)
         print(f"[bench] drop-in mode: {extras['drop_in_host_pointers']}", file=sys.stderr, flush=True)
         extras["config1"] = config1_point(lib, 101)

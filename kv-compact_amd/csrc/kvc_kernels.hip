@@ -2031,15 +2031,22 @@ __device__ __forceinline__ long long rhs_at(int n, int p, int i, int v) {
     return (long long)n * n + (n <= 256 ? (long long)i * p + v : (long long)v * n + i);
 }
 
-// one block per system; X (nq x n) and Y (nq x p) staged in (dynamic) LDS
-// when they fit its budget
+// X (nq x n) and Y (nq x p) staged in (dynamic) LDS as rows X | Y of width
+// wp = round_up(n + p, 4); 4 x 4 output tiles per thread over the block tile
+// grid, upper-triangular tiles only for X^T X (a sequential dot product is
+// symmetric bit for bit: the mirror entry is written from the same sum).
+// When all nq rows fit the LDS budget, one block per system takes every
+// tile. Otherwise (large systems: the unchunked refits of state blobs) the
+// rows come through the LDS in slabs of ks and each thread keeps two tiles'
+// sums across the slabs (k ascending throughout), the system's tiles spread
+// over gridDim.z blocks, 512 tiles per block and pass. Rows wider than the
+// budget allows (ks < 8): one output per thread straight from global memory.
 constexpr int LB_LDS_FLOATS = 40960;   // 160 KB
+constexpr int LB_TPT = 2;              // tiles per thread and pass (slab mode)
 
-// Staged X | Y (rows of width wp = round_up(n + p, 4)): 4 x 4 output tiles per
-// thread over the block tile grid, upper-triangular tiles only for X^T X
-// (a sequential dot product is symmetric bit for bit: the mirror entry is
-// written from the same sum). Without staging (too large for LDS): one
-// output per thread straight from global memory.
+// SLAB: the instance for systems whose rows do not all fit (the launcher's
+// choice), so that the other keeps its registers
+template <bool SLAB>
 __global__ void __launch_bounds__(256)
 k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ X,
            const float * __restrict__ Y, float * __restrict__ aug, const long long * __restrict__ aug_off,
@@ -2055,7 +2062,10 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     const float * Yh = Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv;
     extern __shared__ __align__(16) float xs[];
     const int wp = (w + 3) & ~3;
-    if ((long long)nq * wp > lds_floats) {
+    const bool whole = (long long)nq * wp <= lds_floats;
+    const int ks = whole ? nq : lds_floats / wp;   // rows per slab
+    if (!whole && ks < 8) {
+        if (blockIdx.z != 0) return;
         // column-major: entry (row i, column j) at Ag[j * n + i]
         const long long total = (long long)n * w;
         for (long long e = skip_m ? (long long)n * n + threadIdx.x : threadIdx.x; e < total; e += blockDim.x) {
@@ -2071,51 +2081,48 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
         }
         return;
     }
-    // xs[k][0..n) = X row k, xs[k][n..n+p) = Y row k, zero padding to wp
+    // rows k0 .. k0 + kn - 1 into xs: xs[k][0..n) = X row, xs[k][n..n+p) = Y row, zero padding to wp
     const bool v4 = (n & 3) == 0 && (p & 3) == 0 && (g.t_total & 3) == 0 && (g.dv & 3) == 0 &&
                     (reinterpret_cast<uintptr_t>(Xh) & 15) == 0 && (reinterpret_cast<uintptr_t>(Yh) & 15) == 0;
-    if (v4) {
-        // 16-byte pieces with no branch around the loads (w = wp here)
-        const int n4 = n >> 2, p4 = p >> 2;
-        for (int q = threadIdx.x; q < nq * n4; q += blockDim.x) {
-            const int k = q / n4, j4 = q - k * n4;
-            *reinterpret_cast<float4 *>(&xs[k * wp + 4 * j4]) =
-                *reinterpret_cast<const float4 *>(Xh + (long long)k * g.t_total + 4 * j4);
+    auto stage = [&](int k0, int kn) {
+        if (v4) {
+            // 16-byte pieces with no branch around the loads (w = wp here)
+            const int n4 = n >> 2, p4 = p >> 2;
+            for (int q = threadIdx.x; q < kn * n4; q += blockDim.x) {
+                const int k = q / n4, j4 = q - k * n4;
+                *reinterpret_cast<float4 *>(&xs[k * wp + 4 * j4]) =
+                    *reinterpret_cast<const float4 *>(Xh + (long long)(k0 + k) * g.t_total + 4 * j4);
+            }
+            for (int q = threadIdx.x; q < kn * p4; q += blockDim.x) {
+                const int k = q / p4, j4 = q - k * p4;
+                *reinterpret_cast<float4 *>(&xs[k * wp + n + 4 * j4]) =
+                    *reinterpret_cast<const float4 *>(Yh + (long long)(k0 + k) * g.dv + 4 * j4);
+            }
+        } else {
+            for (int e = threadIdx.x; e < kn * wp; e += blockDim.x) {
+                const int k = e / wp, j = e % wp;
+                float v = 0.0f;
+                if (j < n) v = Xh[(long long)(k0 + k) * g.t_total + j];
+                else if (j < w) v = Yh[(long long)(k0 + k) * g.dv + (j - n)];
+                xs[e] = v;
+            }
         }
-        for (int q = threadIdx.x; q < nq * p4; q += blockDim.x) {
-            const int k = q / p4, j4 = q - k * p4;
-            *reinterpret_cast<float4 *>(&xs[k * wp + n + 4 * j4]) =
-                *reinterpret_cast<const float4 *>(Yh + (long long)k * g.dv + 4 * j4);
-        }
-    } else {
-        for (int e = threadIdx.x; e < nq * wp; e += blockDim.x) {
-            const int k = e / wp, j = e % wp;
-            float v = 0.0f;
-            if (j < n) v = Xh[(long long)k * g.t_total + j];
-            else if (j < w) v = Yh[(long long)k * g.dv + (j - n)];
-            xs[e] = v;
-        }
-    }
-    __syncthreads();
+    };
     const int nbi = (n + 3) >> 2, nbw = wp >> 2;
     // 16-byte stores need n, p multiples of 4, B row-major and an aligned base
     const bool vec = (n & 3) == 0 && (p & 3) == 0 && n <= 256 && (reinterpret_cast<uintptr_t>(Ag) & 15) == 0;
-    // one 4 x 4 output tile; the sums run over k ascending
-    auto tile = [&](int ib, int jb) {
+    // a 4 x 4 tile's sums over the staged rows 0 .. kn - 1 (k ascending),
+    // continuing acc
+    auto tile_acc = [&](float (&acc)[4][4], int ib, int jb, int kn) {
         const int i0 = 4 * ib, j0 = 4 * jb;
-        float acc[4][4];
-#pragma unroll
-        for (int a = 0; a < 4; a++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
         // row k + 1 is read from LDS while row k is summed (the last row
         // again at the end: no branch around the reads)
         float4 xi = *reinterpret_cast<const float4 *>(&xs[i0]);
         float4 xj = *reinterpret_cast<const float4 *>(&xs[j0]);
-        for (int k = 0; k < nq; k++) {
-            const int kn = min(k + 1, nq - 1);
-            const float4 xin = *reinterpret_cast<const float4 *>(&xs[kn * wp + i0]);
-            const float4 xjn = *reinterpret_cast<const float4 *>(&xs[kn * wp + j0]);
+        for (int k = 0; k < kn; k++) {
+            const int kk = min(k + 1, kn - 1);
+            const float4 xin = *reinterpret_cast<const float4 *>(&xs[kk * wp + i0]);
+            const float4 xjn = *reinterpret_cast<const float4 *>(&xs[kk * wp + j0]);
             __builtin_amdgcn_sched_barrier(0);
             const float vi[4] = {xi.x, xi.y, xi.z, xi.w}, vj[4] = {xj.x, xj.y, xj.z, xj.w};
 #pragma unroll
@@ -2126,6 +2133,9 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             xi = xin;
             xj = xjn;
         }
+    };
+    auto tile_store = [&](float (&acc)[4][4], int ib, int jb) {
+        const int i0 = 4 * ib, j0 = 4 * jb;
         if (vec && i0 + 3 < n && j0 + 3 < w && (j0 + 3 < n || j0 >= n)) {
             // whole tile inside M or inside B: 16-byte stores
             if (j0 < n) {
@@ -2167,23 +2177,74 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             }
         }
     };
-    // tiles holding columns of M (upper triangle only): consecutive threads
-    // take consecutive row blocks (column-major stores)
-    const int nbm = nbi;   // column blocks that hold at least one column of M
-    if (!skip_m) {
-        for (int e = threadIdx.x; e < nbi * nbm; e += blockDim.x) {
-            const int jb = e / nbi, ib = e % nbi;
-            if (ib > jb) continue;
-            tile(ib, jb);
+    // the tiles: those holding columns of M (upper triangle; column blocks
+    // jb < nbm, consecutive row blocks to consecutive threads: column-major
+    // stores), or with M left to the LU only the block that also holds the
+    // first columns of B; then the tiles of B alone
+    const int nbm = nbi, nbr = nbw - nbm;
+    const int nmt = skip_m ? ((n & 3) ? nbi : 0) : nbi * nbm;
+    const int njobs = nmt + nbi * nbr;
+    // job -> tile (ib, jb); false: none (below the diagonal)
+    auto job_tile = [&](int e, int & ib, int & jb) -> bool {
+        if (e < nmt) {
+            if (skip_m) { ib = e; jb = nbm - 1; return true; }
+            jb = e / nbi;
+            ib = e % nbi;
+            return ib <= jb;
         }
-    } else if (n & 3) {
-        // the last M column block also holds the first columns of B
-        for (int ib = threadIdx.x; ib < nbi; ib += blockDim.x) tile(ib, nbm - 1);
+        e -= nmt;
+        ib = e / nbr;
+        jb = nbm + e % nbr;
+        return true;
+    };
+    if (!SLAB || whole) {
+        if (blockIdx.z != 0 || !whole) return;
+        stage(0, nq);
+        __syncthreads();
+        for (int e = threadIdx.x; e < njobs; e += blockDim.x) {
+            int ib, jb;
+            if (!job_tile(e, ib, jb)) continue;
+            float acc[4][4];
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) acc[a][b] = 0.0f;
+            tile_acc(acc, ib, jb, nq);
+            tile_store(acc, ib, jb);
+        }
+        return;
     }
-    // tiles of B alone: consecutive threads take consecutive column blocks
-    // (row-major stores when n <= 256)
-    const int nbr = nbw - nbm;
-    for (int e = threadIdx.x; e < nbi * nbr; e += blockDim.x) tile(e / nbr, nbm + e % nbr);
+    // slab mode: passes of LB_TPT * 256 jobs per block; every thread of the
+    // block runs the same passes and slabs (the barriers are uniform)
+    if constexpr (SLAB) {
+    const int per_pass = LB_TPT * (int)blockDim.x;
+    for (int p0 = (int)blockIdx.z * per_pass; p0 < njobs; p0 += (int)gridDim.z * per_pass) {
+        int tib[LB_TPT], tjb[LB_TPT];
+        bool act[LB_TPT];
+        float acc[LB_TPT][4][4];
+#pragma unroll
+        for (int u = 0; u < LB_TPT; u++) {
+            const int e = p0 + u * (int)blockDim.x + (int)threadIdx.x;
+            act[u] = e < njobs && job_tile(e, tib[u], tjb[u]);
+#pragma unroll
+            for (int a = 0; a < 4; a++)
+#pragma unroll
+                for (int b = 0; b < 4; b++) acc[u][a][b] = 0.0f;
+        }
+        for (int k0 = 0; k0 < nq; k0 += ks) {
+            const int kn = min(ks, nq - k0);
+            __syncthreads();   // the previous slab is read
+            stage(k0, kn);
+            __syncthreads();
+#pragma unroll
+            for (int u = 0; u < LB_TPT; u++)
+                if (act[u]) tile_acc(acc[u], tib[u], tjb[u], kn);
+        }
+#pragma unroll
+        for (int u = 0; u < LB_TPT; u++)
+            if (act[u]) tile_store(acc[u], tib[u], tjb[u]);
+    }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -4785,14 +4846,29 @@ void launch_ls_build(const Geom & g, const Work & w, hipStream_t st, bool m_by_l
     // dynamic LDS beyond 64 KB needs the kernel attribute (once per process)
     static int lds_cap = -1;
     if (lds_cap < 0)
-        lds_cap = hipFuncSetAttribute(reinterpret_cast<const void *>(k_ls_build),
+        lds_cap = hipFuncSetAttribute(reinterpret_cast<const void *>(k_ls_build<false>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                      LB_LDS_FLOATS * (int)sizeof(float)) == hipSuccess
+                                      LB_LDS_FLOATS * (int)sizeof(float)) == hipSuccess &&
+                          hipFuncSetAttribute(reinterpret_cast<const void *>(k_ls_build<true>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              LB_LDS_FLOATS * (int)sizeof(float)) == hipSuccess
                       ? LB_LDS_FLOATS : 16384;
     const long long need = (long long)g.nq_max * ((g.tc_max + g.dv + 3) & ~3);
-    const int lds_floats = need <= lds_cap ? (int)need : 0;
-    hipLaunchKernelGGL(k_ls_build, dim3(g.n_chunks * g.H, g.L), dim3(256), (size_t)lds_floats * sizeof(float), st,
-                       g, w.chunks, w.X, w.Y, w.aug, w.aug_off, lds_floats, m_by_lu ? 1 : 0);
+    // every system's rows fit: one block per system; else slabs of rows
+    // through the whole budget, the tiles of a system over enough blocks to
+    // give the GPU about 2048 of them
+    const int wmax = (g.tc_max + g.dv + 3) & ~3;
+    // (slabs of at least 8 rows in about 40 KB: four blocks per CU)
+    const int lds_floats = need <= lds_cap ? (int)need : std::min(lds_cap, std::max(8 * wmax, 10240));
+    const long long systems = (long long)g.n_chunks * g.H * g.L;
+    const int nz = need <= lds_cap ? 1 : (int)std::max<long long>(1, std::min<long long>(64, (2048 + systems - 1) / systems));
+    if (need <= lds_cap)
+        hipLaunchKernelGGL(k_ls_build<false>, dim3(g.n_chunks * g.H, g.L), dim3(256), (size_t)lds_floats * sizeof(float),
+                           st, g, w.chunks, w.X, w.Y, w.aug, w.aug_off, lds_floats, m_by_lu ? 1 : 0);
+    else
+        hipLaunchKernelGGL(k_ls_build<true>, dim3(g.n_chunks * g.H, g.L, nz), dim3(256),
+                           (size_t)lds_floats * sizeof(float), st, g, w.chunks, w.X, w.Y, w.aug, w.aug_off, lds_floats,
+                           m_by_lu ? 1 : 0);
 }
 
 void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st, bool m_by_lu) {
