@@ -3718,7 +3718,155 @@ __device__ void ge_solve_block(float * __restrict__ a, int n, int p, float * __r
 
 constexpr int GE_LDS_FLOATS = 8192;
 
-__global__ void __launch_bounds__(256)
+// The same elimination in panels of pb steps (systems with n > 256): each
+// element of [M | B] receives the same sequence of row swaps and updates
+// a -= f * u, in step order, as in ge_solve_block, but the trailing columns
+// are read and written once per panel instead of once per step.
+//  1. Panel: columns c0 .. c0 + pb - 1, rows c0 .. n - 1, in LDS (P, one
+//     column of nr = n - c0 rows each). Per step c: the pivot search over
+//     column c (rows > c; the largest |a| that is not NaN, the first such row
+//     on ties, taken only when it exceeds |a[c][c]| and that is not NaN), the
+//     swap of rows c and mr in the panel, and, unless |pivot| < 1e-12 (a
+//     skipped step), the multipliers F[s][r] = a[r][c] / pivot (rows r > c)
+//     and their update of the panel's later columns. The panel's rows c0 ..
+//     c0 + pb - 1 are final and go back to memory (the rows below the
+//     diagonal are never read again).
+//  2. Trailing columns c0 + pb .. w - 1 (the rest of M, then B), TW at a
+//     time in LDS: each panel step applied in order, the row swap and then,
+//     unless skipped, a[r][j] -= F[s][r] * a[c][j] for the rows r > c.
+// Then the back substitution of ge_solve_block. Dynamic LDS: 3 pb nr floats
+// (P, F and the trailing tile, TW = pb columns).
+__device__ void ge_solve_blocked(float * __restrict__ a, int n, int p, float * __restrict__ x, long long ldx,
+                                 float zero_val, float * __restrict__ lds, int pb) {
+    const int w = n + p, nt = blockDim.x, tid = threadIdx.x;
+    __shared__ float bv[32];
+    __shared__ int bi[32];
+    __shared__ int s_mr[32];
+    __shared__ unsigned char s_skip[32];
+    for (int c0 = 0; c0 < n; c0 += pb) {
+        const int np = min(pb, n - c0), nr = n - c0;
+        float * P = lds;                    // P[jj * nr + (r - c0)]
+        float * F = lds + pb * nr;          // F[s * nr + (r - c0)]
+        float * Tt = lds + 2 * pb * nr;     // trailing tile, same layout as P
+        __syncthreads();
+        for (int e = tid; e < np * nr; e += nt) {
+            const int jj = e / nr, rr = e - jj * nr;
+            P[e] = a[(long long)(c0 + jj) * n + c0 + rr];
+        }
+        __syncthreads();
+        for (int s = 0; s < np; s++) {
+            const int c = c0 + s;
+            const float * Pc = P + s * nr;
+            // pivot search (as in ge_solve_block)
+            float best = -1.0f;
+            int brow = 0x7fffffff;
+            for (int r = c + 1 + tid; r < n; r += nt) {
+                const float v = fabsf(Pc[r - c0]);
+                if (v == v && v > best) { best = v; brow = r; }
+            }
+            for (int o = 32; o > 0; o >>= 1) {
+                const float ov = __shfl_xor(best, o);
+                const int orow = __shfl_xor(brow, o);
+                if (ov > best || (ov == best && orow < brow)) { best = ov; brow = orow; }
+            }
+            if ((tid & 63) == 0) { bv[tid >> 6] = best; bi[tid >> 6] = brow; }
+            __syncthreads();
+            if (tid == 0) {
+                float b = bv[0];
+                int r = bi[0];
+                for (int i = 1; i < (nt >> 6); i++)
+                    if (bv[i] > b || (bv[i] == b && bi[i] < r)) { b = bv[i]; r = bi[i]; }
+                const float a0 = fabsf(Pc[s]);
+                s_mr[s] = (a0 == a0 && b > a0) ? r : c;
+            }
+            __syncthreads();
+            const int mr = s_mr[s];
+            if (mr != c) {
+                for (int jj = tid; jj < np; jj += nt) {
+                    float * col = P + jj * nr;
+                    const float t0 = col[s];
+                    col[s] = col[mr - c0];
+                    col[mr - c0] = t0;
+                }
+            }
+            __syncthreads();
+            const float piv = Pc[s];
+            const bool skip = fabsf(piv) < 1e-12f;
+            if (tid == 0) s_skip[s] = skip ? 1 : 0;
+            if (!skip) {
+                for (int r = c + 1 + tid; r < n; r += nt) F[s * nr + (r - c0)] = Pc[r - c0] / piv;
+                __syncthreads();
+                const int rows = n - c - 1;
+                for (int e = tid; e < (np - s - 1) * rows; e += nt) {
+                    const int jj = s + 1 + e / rows, rr = c + 1 - c0 + e % rows;
+                    float * col = P + jj * nr;
+                    col[rr] = col[rr] - F[s * nr + rr] * col[s];
+                }
+            }
+            __syncthreads();
+        }
+        // the panel's rows c0 .. c0 + np - 1 are final
+        for (int e = tid; e < np * np; e += nt) {
+            const int jj = e / np, rr = e - jj * np;
+            a[(long long)(c0 + jj) * n + c0 + rr] = P[jj * nr + rr];
+        }
+        // trailing columns, pb at a time
+        for (int j0 = c0 + np; j0 < w; j0 += pb) {
+            const int nj = min(pb, w - j0);
+            __syncthreads();
+            for (int e = tid; e < nj * nr; e += nt) {
+                const int jj = e / nr, rr = e - jj * nr;
+                Tt[e] = a[(long long)(j0 + jj) * n + c0 + rr];
+            }
+            __syncthreads();
+            for (int s = 0; s < np; s++) {
+                const int c = c0 + s, mr = s_mr[s];
+                if (mr != c) {
+                    for (int jj = tid; jj < nj; jj += nt) {
+                        float * col = Tt + jj * nr;
+                        const float t0 = col[s];
+                        col[s] = col[mr - c0];
+                        col[mr - c0] = t0;
+                    }
+                    __syncthreads();
+                }
+                if (!s_skip[s]) {
+                    const int rows = n - c - 1;
+                    for (int e = tid; e < nj * rows; e += nt) {
+                        const int jj = e / rows, rr = c + 1 - c0 + e % rows;
+                        float * col = Tt + jj * nr;
+                        col[rr] = col[rr] - F[s * nr + rr] * col[s];
+                    }
+                    __syncthreads();
+                }
+            }
+            for (int e = tid; e < nj * nr; e += nt) {
+                const int jj = e / nr, rr = e - jj * nr;
+                a[(long long)(j0 + jj) * n + c0 + rr] = Tt[e];
+            }
+        }
+    }
+    __syncthreads();
+    for (int col = n - 1; col >= 0; col--) {
+        const float piv = a[(long long)col * n + col];
+        if (fabsf(piv) < 1e-12f) {
+            for (int j = tid; j < p; j += nt) x[(long long)col * ldx + j] = zero_val;
+        } else {
+            for (int j = tid; j < p; j += nt) {
+                float v = a[(long long)(n + j) * n + col];
+                for (int r = col + 1; r < n; r++) v -= a[(long long)r * n + col] * x[(long long)r * ldx + j];
+                x[(long long)col * ldx + j] = v / piv;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// panel width for n rows in GE_BLK_LDS floats (3 pb n), or 0: too large
+constexpr int GE_BLK_LDS = 40960 - 256;
+__host__ __device__ inline int ge_panel(int n) { return std::min(32, GE_BLK_LDS / (3 * n)); }
+
+__global__ void __launch_bounds__(512)
 k_ge_general(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__ aug,
              const long long * __restrict__ aug_off, float * __restrict__ Cv, float * __restrict__ gtmp) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
@@ -3727,13 +3875,19 @@ k_ge_general(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__
     const long long sys = ((long long)layer * g.n_chunks + c_idx) * g.H + h;
     float * Ag = aug + aug_off[sys];
     float * x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
-    __shared__ float s_buf[GE_LDS_FLOATS];
+    extern __shared__ __align__(16) float ge_dyn[];
     const int n = c.tc, w = n + g.dv;
+    const int pb = ge_panel(n);
+    if (pb >= 1) {
+        ge_solve_blocked(Ag, n, g.dv, x, g.dv, g.zero_val, ge_dyn, pb);
+        return;
+    }
+    // (rows beyond the panel budget: step by step, the factors in LDS or in gtmp)
     float * prow;
     float * fac;
     if (w + n <= GE_LDS_FLOATS) {
-        prow = s_buf;
-        fac = s_buf + w;
+        prow = ge_dyn;
+        fac = ge_dyn + w;
     } else {
         prow = gtmp + sys * (long long)(2 * g.tc_max + g.dv);
         fac = prow + g.tc_max + g.dv;
@@ -4901,9 +5055,20 @@ void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st)
     }
     hipLaunchKernelGGL(k_ge_solve, dim3(systems, cdiv(g.dv, 64)), dim3(64), 0, st,
                        g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, w.Bt, Cv, old_solve ? 0 : 1);
-    if (g.tc_max > RG_ROWS)
-        hipLaunchKernelGGL(k_ge_general, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
+    if (g.tc_max > RG_ROWS) {
+        // dynamic LDS: the largest system's panels (3 pb n floats), or the
+        // step-by-step factors; the attribute once per process
+        static int ge_lds_ok = -1;
+        if (ge_lds_ok < 0)
+            ge_lds_ok = hipFuncSetAttribute(reinterpret_cast<const void *>(k_ge_general),
+                                            hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            GE_BLK_LDS * (int)sizeof(float)) == hipSuccess;
+        const int pb = ge_panel(g.tc_max);
+        size_t lds = pb >= 1 ? (size_t)3 * pb * g.tc_max * sizeof(float) : (size_t)GE_LDS_FLOATS * sizeof(float);
+        if (!ge_lds_ok && lds > 65536) lds = 0;   // (reported by the launch)
+        hipLaunchKernelGGL(k_ge_general, dim3(g.n_chunks * g.H, g.L), dim3(512), lds, st,
                            g, w.chunks, w.aug, w.aug_off, Cv, w.gtmp);
+    }
 }
 
 // Original attention of the sampled queries over all T (outputs OO): needs
