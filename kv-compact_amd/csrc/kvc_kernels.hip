@@ -1678,14 +1678,23 @@ k_refine_step(Geom g, const ChunkDesc * __restrict__ chunks, const float * __res
 // (api.cpp:833-840); aug = [X^T X + ridge I | X^T Y] (math.h:465-504),
 // both sums sequential over the query index.
 // ---------------------------------------------------------------------------
-// 32 rows x t_c columns at a time in LDS: gather S[:, sel] + beta, row maxima
-// (one wave per row, the reference's scan semantics), exponentials, the
-// sequential row sums (one thread per row over LDS), then X = e * inv.
-constexpr int LSX_ROWS = 32, LSX_COLS = 256;
+// Up to 32 rows x t_c columns at a time in LDS: gather S[:, sel] + beta, row
+// maxima (one wave per row, the reference's scan semantics), exponentials,
+// the sequential row sums (one thread per row over LDS), then X = e * inv.
+// The dynamic LDS holds the chunk's selection and beta (2 t_c floats), then
+// the rows at a stride of t_c + 1 floats; it is sized for the largest chunk
+// (at most LSX_LDS_BYTES), and a chunk for which not even one row fits goes
+// row by row through global memory.
+constexpr int LSX_ROWS = 32, LSX_LDS_BYTES = 60 * 1024;
+
+__host__ __device__ inline int lsx_rows(int t, int lds_floats) {
+    return min(LSX_ROWS, (lds_floats - 2 * t) / (t + 1));
+}
 
 __global__ void __launch_bounds__(256)
 k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ S,
-             const int * __restrict__ sel, const float * __restrict__ beta, float * __restrict__ X) {
+             const int * __restrict__ sel, const float * __restrict__ beta, float * __restrict__ X,
+             int lds_floats) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const int t = c.tc, nq = c.nq;
@@ -1697,7 +1706,8 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     __shared__ uint64_t etab[32];
     if (tid < 32) etab[tid] = c_exp2_tab[tid];   // visible after the barriers below
-    if (t > LSX_COLS) {
+    const int rows = lsx_rows(t, lds_floats);
+    if (rows < 1) {
         // large chunks: row by row through global memory
         __shared__ float red[16];
         __shared__ float rmax1, rinv1;
@@ -1722,17 +1732,19 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
         }
         return;
     }
-    __shared__ float xs[LSX_ROWS][LSX_COLS + 1];
+    extern __shared__ float lsx_dyn[];
     __shared__ float rmax[LSX_ROWS], rinv[LSX_ROWS];
-    __shared__ int sls[LSX_COLS];
-    __shared__ float bs[LSX_COLS];
+    int * sls = reinterpret_cast<int *>(lsx_dyn);
+    float * bs = lsx_dyn + t;
+    float * xs = lsx_dyn + 2 * t;
+    const int ld = t + 1;
     for (int j = tid; j < t; j += blockDim.x) {
         sls[j] = sl[j];
         bs[j] = bh[j];
     }
     __syncthreads();
-    for (int r0 = 0; r0 < nq; r0 += LSX_ROWS) {
-        const int nr = min(LSX_ROWS, nq - r0);
+    for (int r0 = 0; r0 < nq; r0 += rows) {
+        const int nr = min(rows, nq - r0);
         // gather: eight rows' loads per thread in flight
         for (int j = tid; j < t; j += blockDim.x) {
             const int sj = sls[j];
@@ -1744,7 +1756,7 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
                     if (rb + u < nr) v[u] = Sh[(long long)(r0 + rb + u) * g.T + sj];
 #pragma unroll
                 for (int u = 0; u < 8; u++)
-                    if (rb + u < nr) xs[rb + u][j] = v[u] + bj;
+                    if (rb + u < nr) xs[(rb + u) * ld + j] = v[u] + bj;
             }
         }
         __syncthreads();
@@ -1753,19 +1765,17 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
         for (int r = wv; r < nr; r += 4) {
             float m = -INFINITY;
             for (int j = lane; j < t; j += 64) {
-                const float v = xs[r][j];
+                const float v = xs[r * ld + j];
                 if (v == v && v > m) m = v;
             }
             const unsigned k = dpp_reduce_u32<true>(score_key(m));
             const float mm = __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-            const float a0 = xs[r][0];
+            const float a0 = xs[r * ld];
             if (lane == 0) rmax[r] = (a0 != a0) ? a0 : ((mm > a0) ? mm : a0);
         }
         __syncthreads();
-        for (int e = tid; e < nr * LSX_COLS; e += blockDim.x) {
-            const int r = e / LSX_COLS, j = e % LSX_COLS;
-            if (j < t) xs[r][j] = expf_ref(xs[r][j] - rmax[r], etab);
-        }
+        for (int r = 0; r < nr; r++)
+            for (int j = tid; j < t; j += blockDim.x) xs[r * ld + j] = expf_ref(xs[r * ld + j] - rmax[r], etab);
         __syncthreads();
         if (tid < nr) {
             float sum = 0.0f;
@@ -1773,18 +1783,18 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
             for (; j + 16 <= t; j += 16) {   // 16 reads in flight, then the adds in order
                 float e[16];
 #pragma unroll
-                for (int k = 0; k < 16; k++) e[k] = xs[tid][j + k];
+                for (int k = 0; k < 16; k++) e[k] = xs[tid * ld + j + k];
 #pragma unroll
                 for (int k = 0; k < 16; k++) sum += e[k];
             }
-            for (; j < t; j++) sum += xs[tid][j];
+            for (; j < t; j++) sum += xs[tid * ld + j];
             rinv[tid] = 1.0f / (sum + 1e-12f);
         }
         __syncthreads();
         for (int r = 0; r < nr; r++) {
             const float iv = rinv[r];
             float * xr = Xh + (long long)(r0 + r) * g.t_total;
-            for (int j = tid; j < t; j += blockDim.x) xr[j] = xs[r][j] * iv;
+            for (int j = tid; j < t; j += blockDim.x) xr[j] = xs[r * ld + j] * iv;
         }
         __syncthreads();
     }
@@ -4960,8 +4970,12 @@ void launch_refine_step(const Geom & g, const Work & w, hipStream_t st) {
 }
 
 void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st) {
-    hipLaunchKernelGGL(k_ls_softmax, dim3(g.n_chunks * g.H, g.L), dim3(256), 0, st,
-                       g, w.chunks, w.S, w.sel, beta, w.X);
+    // LDS for the largest chunk's rows (every smaller chunk then fits as many)
+    const int W = g.tc_max;
+    const int rows = lsx_rows(W, LSX_LDS_BYTES / 4);
+    const size_t bytes = rows >= 1 ? sizeof(float) * (2 * (size_t)W + (size_t)rows * (W + 1)) : LSX_LDS_BYTES;
+    hipLaunchKernelGGL(k_ls_softmax, dim3(g.n_chunks * g.H, g.L), dim3(256), bytes, st,
+                       g, w.chunks, w.S, w.sel, beta, w.X, (int)(bytes / sizeof(float)));
 }
 
 void launch_gather_exp(const Geom & g, const Work & w, hipStream_t st) {
