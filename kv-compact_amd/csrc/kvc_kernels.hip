@@ -2032,9 +2032,10 @@ k_nnls_lh(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restric
 // of B across 64 columns at a time; column-major (B transposed) for larger
 // ones, whose general elimination swaps rows in place. For p == 1 both are
 // the same.
-// The register LU forms M = X^T X from X itself when X (nq x n) fits the LDS
-// of its step ring (lu_x_fits, defined with the LU's constants below): then
-// k_ls_build writes B only.
+// The register LU forms M = X^T X from X itself, staging X through the LDS of
+// its step ring in slabs of rows, when X has at most LU_X_MAXQ rows
+// (lu_x_fits, defined with the LU's constants below): then k_ls_build writes
+// B only.
 __device__ __forceinline__ bool lu_x_fits(int n, int nq);
 
 __device__ __forceinline__ long long rhs_at(int n, int p, int i, int v) {
@@ -2304,10 +2305,12 @@ constexpr int RG_THREADS = RG_WAVES * 64;
 constexpr int LU_RING = 32;          // > 17 outstanding steps
 constexpr int LU_TROWS = 32;         // rows per pass of the transposed output write
 constexpr int LU_SPIN_LIMIT = 1 << 22;   // polls per wave over the whole factorization
-constexpr int LU_X_FLOATS = LU_RING * 64 * 4;   // X staged in the ring's LDS: nq * n <= LU_X_FLOATS
+constexpr int LU_X_FLOATS = LU_RING * 64 * 4;   // X staged in the ring's LDS, LU_X_FLOATS / n rows at a time
+constexpr int LU_X_MAXQ = 1024;                 // rows of X beyond which k_ls_build forms M
 
-// X (nq x n) fits the ring's LDS, and the system the register LU
-__device__ __forceinline__ bool lu_x_fits(int n, int nq) { return n <= RG_ROWS && nq >= 1 && nq * n <= LU_X_FLOATS; }
+// the register LU forms M from X: a system it factors, and X of at most
+// LU_X_MAXQ rows (staged through the ring's LDS in slabs of rows)
+__device__ __forceinline__ bool lu_x_fits(int n, int nq) { return n <= RG_ROWS && nq >= 1 && nq <= LU_X_MAXQ; }
 
 struct LuShared {
     union {
@@ -2622,15 +2625,12 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
     if (X && lu_x_fits(n, c.nq)) {
         // M = X^T X (+ ridge on the diagonal) formed here, k_ls_build having
         // left it out: each entry the same sequential sum over the rows of X
-        // (k ascending from +0), the ridge added after it, X staged in LDS
+        // (k ascending from +0, kept in registers across the slabs of rows
+        // staged in LDS), the ridge added after it
         const int nq = c.nq;
+        const int kb = LU_X_FLOATS / n;   // rows per slab (at least 32)
         const long long hsX = (long long)g.nq_max * g.t_total;
         const float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
-        for (int e = tid; e < nq * n; e += RG_THREADS) {
-            const int k = e / n, i = e - k * n;
-            sh.u.xs[e] = Xh[(long long)k * g.t_total + i];
-        }
-        __syncthreads();
         int cc[RG_COLS];
 #pragma unroll
         for (int q = 0; q < RG_COLS; q++) cc[q] = min(w + RG_WAVES * q, n - 1);
@@ -2641,17 +2641,26 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
 #pragma unroll
             for (int q = 0; q < RG_COLS; q++) a[s][q] = 0.0f;
         }
-        for (int k = 0; k < nq; k++) {
-            const float * xk = sh.u.xs + k * n;
-            float xr[RG_SLOTS], xc[RG_COLS];
+        for (int k0 = 0; k0 < nq; k0 += kb) {
+            const int nk = min(kb, nq - k0);
+            if (k0 > 0) __syncthreads();   // the previous slab has been read
+            for (int e = tid; e < nk * n; e += RG_THREADS) {
+                const int k = e / n, i = e - k * n;
+                sh.u.xs[e] = Xh[(long long)(k0 + k) * g.t_total + i];
+            }
+            __syncthreads();
+            for (int k = 0; k < nk; k++) {
+                const float * xk = sh.u.xs + k * n;
+                float xr[RG_SLOTS], xc[RG_COLS];
 #pragma unroll
-            for (int s = 0; s < RG_SLOTS; s++) xr[s] = xk[min(lane + 64 * s, n - 1)];
+                for (int s = 0; s < RG_SLOTS; s++) xr[s] = xk[min(lane + 64 * s, n - 1)];
 #pragma unroll
-            for (int q = 0; q < RG_COLS; q++) xc[q] = xk[cc[q]];
+                for (int q = 0; q < RG_COLS; q++) xc[q] = xk[cc[q]];
 #pragma unroll
-            for (int s = 0; s < RG_SLOTS; s++)
+                for (int s = 0; s < RG_SLOTS; s++)
 #pragma unroll
-                for (int q = 0; q < RG_COLS; q++) a[s][q] = a[s][q] + xr[s] * xc[q];
+                    for (int q = 0; q < RG_COLS; q++) a[s][q] = a[s][q] + xr[s] * xc[q];
+            }
         }
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++) {
