@@ -3750,11 +3750,20 @@ constexpr int GE_LDS_FLOATS = 8192;
 //     and their update of the panel's later columns. The panel's rows c0 ..
 //     c0 + pb - 1 are final and go back to memory (the rows below the
 //     diagonal are never read again).
-//  2. Trailing columns c0 + pb .. w - 1 (the rest of M, then B), TW at a
-//     time in LDS: each panel step applied in order, the row swap and then,
-//     unless skipped, a[r][j] -= F[s][r] * a[c][j] for the rows r > c.
+//  2. Trailing columns c0 + pb .. w - 1 (the rest of M, then B), each by 16
+//     lanes of one wave in an LDS column of its own: each panel step applied
+//     in order, the row swap and then, unless skipped, a[r][j] -= F[s][r] *
+//     a[c][j] for the rows r > c.
 // Then the back substitution of ge_solve_block. Dynamic LDS: 3 pb nr floats
-// (P, F and the trailing tile, TW = pb columns).
+// (P, F and min(pb, blockDim.x / 16) trailing columns).
+// Order this wave's LDS accesses around the call in program order (the
+// hardware completes one wave's LDS operations in order; this keeps the
+// compiler from moving them across).
+__device__ __forceinline__ void lds_wave_order() {
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+}
+
 __device__ void ge_solve_blocked(float * __restrict__ a, int n, int p, float * __restrict__ x, long long ldx,
                                  float zero_val, float * __restrict__ lds, int pb) {
     const int w = n + p, nt = blockDim.x, tid = threadIdx.x;
@@ -3815,11 +3824,11 @@ __device__ void ge_solve_blocked(float * __restrict__ a, int n, int p, float * _
             if (!skip) {
                 for (int r = c + 1 + tid; r < n; r += nt) F[s * nr + (r - c0)] = Pc[r - c0] / piv;
                 __syncthreads();
-                const int rows = n - c - 1;
-                for (int e = tid; e < (np - s - 1) * rows; e += nt) {
-                    const int jj = s + 1 + e / rows, rr = c + 1 - c0 + e % rows;
+                // 16 lanes per column, rows strided by 16
+                for (int jj = s + 1 + (tid >> 4); jj < np; jj += nt >> 4) {
                     float * col = P + jj * nr;
-                    col[rr] = col[rr] - F[s * nr + rr] * col[s];
+                    const float u = col[s];
+                    for (int rr = c + 1 - c0 + (tid & 15); rr < nr; rr += 16) col[rr] = col[rr] - F[s * nr + rr] * u;
                 }
             }
             __syncthreads();
@@ -3829,41 +3838,39 @@ __device__ void ge_solve_blocked(float * __restrict__ a, int n, int p, float * _
             const int jj = e / np, rr = e - jj * np;
             a[(long long)(c0 + jj) * n + c0 + rr] = P[jj * nr + rr];
         }
-        // trailing columns, pb at a time
-        for (int j0 = c0 + np; j0 < w; j0 += pb) {
-            const int nj = min(pb, w - j0);
-            __syncthreads();
-            for (int e = tid; e < nj * nr; e += nt) {
-                const int jj = e / nr, rr = e - jj * nr;
-                Tt[e] = a[(long long)(j0 + jj) * n + c0 + rr];
-            }
-            __syncthreads();
-            for (int s = 0; s < np; s++) {
-                const int c = c0 + s, mr = s_mr[s];
-                if (mr != c) {
-                    for (int jj = tid; jj < nj; jj += nt) {
-                        float * col = Tt + jj * nr;
-                        const float t0 = col[s];
-                        col[s] = col[mr - c0];
-                        col[mr - c0] = t0;
+        // trailing columns: each column by the 16 lanes of one column group
+        // (rows strided by 16) in its own LDS column; the lanes of a group
+        // are in one wave, whose LDS accesses complete in program order, so
+        // the panel's steps need no block barrier here
+        {
+            const int cg = tid >> 4, cr = tid & 15, ngr = min(nt >> 4, pb);
+            float * col = Tt + cg * nr;
+            for (int j = c0 + np + cg; cg < ngr && j < w; j += ngr) {
+                float * aj = a + (long long)j * n + c0;
+                for (int rr = cr; rr < nr; rr += 16) col[rr] = aj[rr];
+                lds_wave_order();
+                for (int s = 0; s < np; s++) {
+                    const int c = c0 + s, mr = s_mr[s];
+                    if (mr != c) {
+                        if (cr == 0) {
+                            const float t0 = col[s];
+                            col[s] = col[mr - c0];
+                            col[mr - c0] = t0;
+                        }
+                        lds_wave_order();
                     }
-                    __syncthreads();
-                }
-                if (!s_skip[s]) {
-                    const int rows = n - c - 1;
-                    for (int e = tid; e < nj * rows; e += nt) {
-                        const int jj = e / rows, rr = c + 1 - c0 + e % rows;
-                        float * col = Tt + jj * nr;
-                        col[rr] = col[rr] - F[s * nr + rr] * col[s];
+                    if (!s_skip[s]) {
+                        const float u = col[s];
+                        const float * Fs = F + s * nr;
+                        for (int rr = c + 1 - c0 + cr; rr < nr; rr += 16) col[rr] = col[rr] - Fs[rr] * u;
+                        lds_wave_order();
                     }
-                    __syncthreads();
                 }
-            }
-            for (int e = tid; e < nj * nr; e += nt) {
-                const int jj = e / nr, rr = e - jj * nr;
-                a[(long long)(j0 + jj) * n + c0 + rr] = Tt[e];
+                for (int rr = cr; rr < nr; rr += 16) aj[rr] = col[rr];
+                lds_wave_order();
             }
         }
+        __syncthreads();
     }
     __syncthreads();
     for (int col = n - 1; col >= 0; col--) {
@@ -5035,11 +5042,13 @@ void launch_ls_build(const Geom & g, const Work & w, hipStream_t st, bool m_by_l
     // through the whole budget, the tiles of a system over enough blocks to
     // give the GPU about 2048 of them
     const int wmax = (g.tc_max + g.dv + 3) & ~3;
-    // (slabs of at least 8 rows in about 40 KB: four blocks per CU)
-    const int lds_floats = need <= lds_cap ? (int)need : std::min(lds_cap, std::max(8 * wmax, 10240));
+    // (slabs of at least 8 rows in about 40 KB: four blocks per CU; whole
+    // systems only up to 48 KB, three blocks per CU)
+    const bool whole = need <= std::min(lds_cap, 12288);
+    const int lds_floats = whole ? (int)need : std::min(lds_cap, std::max(8 * wmax, 10240));
     const long long systems = (long long)g.n_chunks * g.H * g.L;
-    const int nz = need <= lds_cap ? 1 : (int)std::max<long long>(1, std::min<long long>(64, (2048 + systems - 1) / systems));
-    if (need <= lds_cap)
+    const int nz = whole ? 1 : (int)std::max<long long>(1, std::min<long long>(64, (2048 + systems - 1) / systems));
+    if (whole)
         hipLaunchKernelGGL(k_ls_build<false>, dim3(g.n_chunks * g.H, g.L), dim3(256), (size_t)lds_floats * sizeof(float),
                            st, g, w.chunks, w.X, w.Y, w.aug, w.aug_off, lds_floats, m_by_lu ? 1 : 0);
     else

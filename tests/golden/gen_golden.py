@@ -6,6 +6,7 @@ Run in the container that holds the reference checkout, after
     python tests/golden/gen_golden.py          (everything)
     python tests/golden/gen_golden.py state    (the state blob cases only)
     python tests/golden/gen_golden.py replay   (the wrapper call-sequence replay only)
+    python tests/golden/gen_golden.py case NAME   (one case of the catalogue)
 
 Inputs are regenerated from seeds by tests/kvc_data.py (integer-only
 generator), so each fixture stores only the reference's outputs plus an
@@ -117,14 +118,19 @@ def main():
     ref = load_ref()
     if ref is None:
         raise SystemExit("oracle/_ref/libkvref.so missing: run `make -C oracle ref` first")
+    one = sys.argv[2] if len(sys.argv) > 2 and sys.argv[1] == "case" else None
     out = {}
     for c in CASES:
+        if one is not None and c["name"] != one:
+            continue
         inp = make_case(c)
         r = run_case(ref, c, inp)
         np.savez_compressed(HERE / f"case_{c['name']}.npz", indices=r.indices.astype(np.int32),
                             beta=r.beta, C_v=r.C_v, stats=stats_arr(r.stats),
                             input_checksum=np.uint64(checksum(*inp[:3])))
         out[c["name"]] = r.t
+    if one is not None:
+        return
     for c in QUANT_CASES:
         K, V, Kq, Vq = quant_inputs(ref, c)
         kr, vr = Kq.shape[1], Vq.shape[1]

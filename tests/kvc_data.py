@@ -158,6 +158,9 @@ CASES = [
          params=dict(target_ratio=0.5)),
     dict(name="unchunked_big_t", T=700, H=1, d=32, seed=20, qref="random", n_q=16,
          params=dict(target_ratio=0.5, chunk_size=-1)),
+    # t = 600: the general elimination's panels narrower than 32 columns
+    dict(name="unchunked_t600", T=1200, H=2, d=16, seed=21, qref="random", n_q=24,
+         params=dict(target_ratio=0.5, chunk_size=-1)),
 ]
 
 CASE_BY_NAME = {c["name"]: c for c in CASES}
