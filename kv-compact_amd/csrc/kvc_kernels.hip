@@ -3833,10 +3833,13 @@ __device__ void ge_solve_blocked(float * __restrict__ a, int n, int p, float * _
             }
             __syncthreads();
         }
-        // the panel's rows c0 .. c0 + np - 1 are final
+        // the panel's rows c0 .. c0 + np - 1 are final: U in place on and
+        // above the diagonal, and each U row also transposed below it (the
+        // multipliers there are dead), so that row i's entries right of the
+        // diagonal lie contiguously at a[i n + i + 1 ..]
         for (int e = tid; e < np * np; e += nt) {
             const int jj = e / np, rr = e - jj * np;
-            a[(long long)(c0 + jj) * n + c0 + rr] = P[jj * nr + rr];
+            a[(long long)(c0 + jj) * n + c0 + rr] = rr <= jj ? P[jj * nr + rr] : P[rr * nr + jj];
         }
         // trailing columns: each column by the 16 lanes of one column group
         // (rows strided by 16) in its own LDS column; the lanes of a group
@@ -3867,10 +3870,88 @@ __device__ void ge_solve_blocked(float * __restrict__ a, int n, int p, float * _
                     }
                 }
                 for (int rr = cr; rr < nr; rr += 16) aj[rr] = col[rr];
+                if (j < n)   // U rows c0 .. c0 + np - 1, transposed below the diagonal
+                    for (int rr = cr; rr < np; rr += 16) a[(long long)(c0 + rr) * n + j] = col[rr];
                 lds_wave_order();
             }
         }
         __syncthreads();
+    }
+    // back substitution (the order of ge_solve_block's) from LDS, in passes
+    // of pc right-hand-side columns: the pass's y, then x in place, at
+    // xl[r (pc + 1) + j]; U row col (contiguous at a[col n + col ..]) in one
+    // of two LDS rows, the next row loaded by the whole block while this one
+    // is solved
+    const int pc_max = min(3 * pb - 3, nt);   // n (pc + 1) + 2 n <= 3 pb n
+    if (pc_max >= 1) {
+        const int passes = (p + pc_max - 1) / pc_max, pc = (p + passes - 1) / passes, ldl = pc + 1;
+        float * ub = lds;
+        float * xl = lds + 2 * n;
+        constexpr int PF = 4;
+        for (int j0 = 0; j0 < p; j0 += pc) {
+            const int nc = min(pc, p - j0);
+            __syncthreads();
+            for (int e = tid; e < nc * n; e += nt) {
+                const int j = e / n, r = e - j * n;
+                xl[r * ldl + j] = a[(long long)(n + j0 + j) * n + r];
+            }
+            if (tid == 0) ub[((n - 1) & 1) * n + n - 1] = a[(long long)(n - 1) * n + n - 1];
+            __syncthreads();
+            for (int col = n - 1; col >= 0; col--) {
+                // row col - 1 (entries col - 1 .. n - 1) toward the other buffer
+                const int nld = col > 0 ? n - col + 1 : 0;
+                const float * src = a + (long long)(col - 1) * n + (col - 1);
+                float * dst = ub + ((col - 1) & 1) * n + (col - 1);
+                const bool pf = nld <= PF * nt;
+                float pre[PF];
+#pragma unroll
+                for (int k = 0; k < PF; k++) pre[k] = (pf && tid + k * nt < nld) ? src[tid + k * nt] : 0.0f;
+                if (tid < nc) {
+                    const float * u = ub + (col & 1) * n;
+                    const float piv = u[col];
+                    float v = zero_val;
+                    if (!(fabsf(piv) < 1e-12f)) {
+                        v = xl[col * ldl + tid];
+                        // terms in order, eight at a time, the next eight's
+                        // reads issued before this eight's arithmetic
+                        int r = col + 1;
+                        if (r + 8 <= n) {
+                            float uc[8], xc[8];
+#pragma unroll
+                            for (int k = 0; k < 8; k++) { uc[k] = u[r + k]; xc[k] = xl[(r + k) * ldl + tid]; }
+                            for (; r + 16 <= n; r += 8) {
+                                float un[8], xn[8];
+#pragma unroll
+                                for (int k = 0; k < 8; k++) { un[k] = u[r + 8 + k]; xn[k] = xl[(r + 8 + k) * ldl + tid]; }
+#pragma unroll
+                                for (int k = 0; k < 8; k++) v -= uc[k] * xc[k];
+#pragma unroll
+                                for (int k = 0; k < 8; k++) { uc[k] = un[k]; xc[k] = xn[k]; }
+                            }
+#pragma unroll
+                            for (int k = 0; k < 8; k++) v -= uc[k] * xc[k];
+                            r += 8;
+                        }
+                        for (; r < n; r++) v -= u[r] * xl[r * ldl + tid];
+                        v = v / piv;
+                    }
+                    xl[col * ldl + tid] = v;
+                }
+                if (pf) {
+#pragma unroll
+                    for (int k = 0; k < PF; k++)
+                        if (tid + k * nt < nld) dst[tid + k * nt] = pre[k];
+                } else {
+                    for (int i = tid; i < nld; i += nt) dst[i] = src[i];
+                }
+                __syncthreads();
+            }
+            for (int e = tid; e < n * nc; e += nt) {
+                const int r = e / nc, j = e - r * nc;
+                x[(long long)r * ldx + j0 + j] = xl[r * ldl + j];
+            }
+        }
+        return;
     }
     __syncthreads();
     for (int col = n - 1; col >= 0; col--) {
@@ -3880,7 +3961,8 @@ __device__ void ge_solve_blocked(float * __restrict__ a, int n, int p, float * _
         } else {
             for (int j = tid; j < p; j += nt) {
                 float v = a[(long long)(n + j) * n + col];
-                for (int r = col + 1; r < n; r++) v -= a[(long long)r * n + col] * x[(long long)r * ldx + j];
+                // U row col, transposed below the diagonal
+                for (int r = col + 1; r < n; r++) v -= a[(long long)col * n + r] * x[(long long)r * ldx + j];
                 x[(long long)col * ldx + j] = v / piv;
             }
         }
@@ -3903,7 +3985,9 @@ k_ge_general(Geom g, const ChunkDesc * __restrict__ chunks, float * __restrict__
     float * x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
     extern __shared__ __align__(16) float ge_dyn[];
     const int n = c.tc, w = n + g.dv;
-    const int pb = ge_panel(n);
+    // the panel width the launch sized the LDS for (3 pb tc_max floats): a
+    // smaller chunk's own width could need more than that
+    const int pb = ge_panel(g.tc_max);
     if (pb >= 1) {
         ge_solve_blocked(Ag, n, g.dv, x, g.dv, g.zero_val, ge_dyn, pb);
         return;
