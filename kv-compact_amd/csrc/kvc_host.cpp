@@ -14,12 +14,14 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <thread>
 #include <vector>
 
 #include "../../include/kv-compact-api.h"
@@ -47,8 +49,19 @@ enum Stage { ST_SCORES, ST_SOFTMAX, ST_REFIT, ST_SELECT, ST_BETA, ST_LS_SOFTMAX,
 // device address, taken once per device with hipGetSymbolAddress.
 static __device__ __align__(256) unsigned char scratch[KVC_NOALLOC_SCRATCH_BYTES];
 
+// Pinned host ring for transfers between pageable host memory and the
+// device: kPinThreads host threads, each with two buffers of kPinBytes.
+constexpr int kPinThreads = 4, kPinBufs = 2 * kPinThreads;
+constexpr size_t kPinBytes = (size_t)8 << 20;
+
 struct DeviceCtx {
     std::mutex mu;
+    // the pinned ring (allocated on the first large host transfer, kept
+    // until the process ends; pin_failed: plain copies instead)
+    void * pin[kPinBufs] = {};
+    hipEvent_t pin_ev[kPinBufs] = {};
+    bool pin_used[kPinBufs] = {};
+    bool pin_ready = false, pin_failed = false;
     bool ready = false;
     char * scratch = nullptr;   // device address of `scratch` on this device (null if unavailable)
     hipStream_t stream = nullptr;
@@ -182,6 +195,103 @@ bool is_device_ptr(const void * p) {
         return false;
     }
     return a.type == hipMemoryTypeDevice;
+}
+
+// One contiguous piece of a transfer between host and device memory.
+struct HostSeg {
+    void * host;
+    void * dev;
+    size_t bytes;
+};
+
+bool pin_ring(DeviceCtx * c) {
+    if (c->pin_ready) return true;
+    if (c->pin_failed) return false;
+    for (int b = 0; b < kPinBufs; b++) {
+        if (hipHostMalloc(&c->pin[b], kPinBytes, hipHostMallocDefault) != hipSuccess ||
+            hipEventCreateWithFlags(&c->pin_ev[b], hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            c->pin_failed = true;
+            return false;
+        }
+    }
+    c->pin_ready = true;
+    return true;
+}
+
+// Copies the segments between pageable host memory and device memory on st,
+// through the pinned ring: thread i moves pieces i, i + kPinThreads, ... (at
+// most kPinBytes each, in segment order) through its two buffers. Host to
+// device: a piece is copied into a buffer once the transfer that last read
+// it has finished, then its transfer is queued on st; the data is on the
+// device once st reaches that point. Device to host (data produced on st):
+// the transfer of a thread's next piece is queued before the previous one is
+// copied out, and the call returns with every piece in host memory. Without
+// the ring (or for a single piece) the segments take plain copies. Returns
+// false on a HIP error.
+bool host_transfer(DeviceCtx * c, const std::vector<HostSeg> & segs, bool to_device, hipStream_t st) {
+    std::vector<HostSeg> pieces;
+    for (const HostSeg & sg : segs) {
+        if (sg.bytes > 0 && is_device_ptr(sg.host)) {
+            // (a device buffer passed where host memory is expected: copied directly)
+            const hipError_t e = to_device ? hipMemcpyAsync(sg.dev, sg.host, sg.bytes, hipMemcpyDefault, st)
+                                           : hipMemcpyAsync(sg.host, sg.dev, sg.bytes, hipMemcpyDefault, st);
+            if (e != hipSuccess) return false;
+            continue;
+        }
+        for (size_t off = 0; off < sg.bytes; off += kPinBytes)
+            pieces.push_back({static_cast<char *>(sg.host) + off, static_cast<char *>(sg.dev) + off,
+                              std::min(kPinBytes, sg.bytes - off)});
+    }
+    if (pieces.size() < 2 || !pin_ring(c)) {
+        for (const HostSeg & pc : pieces) {
+            const hipError_t e = to_device
+                ? hipMemcpyAsync(pc.dev, pc.host, pc.bytes, hipMemcpyHostToDevice, st)
+                : hipMemcpyAsync(pc.host, pc.dev, pc.bytes, hipMemcpyDeviceToHost, st);
+            if (e != hipSuccess) return false;
+        }
+        return to_device || hipStreamSynchronize(st) == hipSuccess;
+    }
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    std::atomic<bool> ok{true};
+    auto worker = [&](int i) {
+        if (hipSetDevice(dev) != hipSuccess) { ok = false; return; }
+        int prev = -1, pb = -1;   // device to host: piece waiting to be copied out, and its buffer
+        int k = 0;
+        for (size_t q = (size_t)i; q < pieces.size() && ok; q += kPinThreads, k++) {
+            const int b = 2 * i + (k & 1);
+            const HostSeg & pc = pieces[q];
+            if (to_device) {
+                if (c->pin_used[b] && hipEventSynchronize(c->pin_ev[b]) != hipSuccess) { ok = false; break; }
+                memcpy(c->pin[b], pc.host, pc.bytes);
+                if (hipMemcpyAsync(pc.dev, c->pin[b], pc.bytes, hipMemcpyHostToDevice, st) != hipSuccess ||
+                    hipEventRecord(c->pin_ev[b], st) != hipSuccess) { ok = false; break; }
+                c->pin_used[b] = true;
+            } else {
+                if (hipMemcpyAsync(c->pin[b], pc.dev, pc.bytes, hipMemcpyDeviceToHost, st) != hipSuccess ||
+                    hipEventRecord(c->pin_ev[b], st) != hipSuccess) { ok = false; break; }
+                c->pin_used[b] = true;
+                if (prev >= 0) {
+                    if (hipEventSynchronize(c->pin_ev[pb]) != hipSuccess) { ok = false; break; }
+                    memcpy(pieces[prev].host, c->pin[pb], pieces[prev].bytes);
+                }
+                prev = (int)q;
+                pb = b;
+            }
+        }
+        if (!to_device && prev >= 0 && ok) {
+            if (hipEventSynchronize(c->pin_ev[pb]) != hipSuccess) ok = false;
+            else memcpy(pieces[prev].host, c->pin[pb], pieces[prev].bytes);
+        }
+    };
+    std::vector<std::thread> th;
+    for (int i = 1; i < kPinThreads; i++) th.emplace_back(worker, i);
+    worker(0);
+    for (std::thread & t : th) t.join();
+    // (device to host: also any direct copies queued above)
+    if (!to_device && ok && hipStreamSynchronize(st) != hipSuccess) ok = false;
+    return ok;
 }
 
 double now_ms() {
@@ -717,18 +827,26 @@ int validate(const float * K, const float * V, const void * res, int T, int n_q,
 }
 
 // Device-resident outputs of one layer copied into a malloc'd host result.
-void fill_result(kv_compact_result * r, int t, int H, int dv, const std::vector<int> & idx,
-                 const std::vector<float> & beta, const std::vector<float> & cv) {
+// The result's arrays (reference ownership: malloc'd, freed by
+// kv_compact_result_free), contents not yet set.
+void alloc_result(kv_compact_result * r, int t, int H, int dv) {
     r->t = t;
     r->n_head_kv = H;
     r->selected_indices = (int *)malloc((size_t)std::max(t, 1) * sizeof(int));
-    memcpy(r->selected_indices, idx.data(), (size_t)t * sizeof(int));
     r->beta = (float **)malloc((size_t)H * sizeof(float *));
     r->C_v = (float **)malloc((size_t)H * sizeof(float *));
     for (int h = 0; h < H; h++) {
         r->beta[h] = (float *)malloc((size_t)std::max(t, 1) * sizeof(float));
-        memcpy(r->beta[h], beta.data() + (size_t)h * t, (size_t)t * sizeof(float));
         r->C_v[h] = (float *)malloc((size_t)std::max(t, 1) * dv * sizeof(float));
+    }
+}
+
+void fill_result(kv_compact_result * r, int t, int H, int dv, const std::vector<int> & idx,
+                 const std::vector<float> & beta, const std::vector<float> & cv) {
+    alloc_result(r, t, H, dv);
+    memcpy(r->selected_indices, idx.data(), (size_t)t * sizeof(int));
+    for (int h = 0; h < H; h++) {
+        memcpy(r->beta[h], beta.data() + (size_t)h * t, (size_t)t * sizeof(float));
         memcpy(r->C_v[h], cv.data() + (size_t)h * t * dv, (size_t)t * dv * sizeof(float));
     }
 }
@@ -781,10 +899,13 @@ int compact_one(const float * K, const float * V, const float * Q, int T, int n_
     io.beta = cv.take<float>((size_t)H * std::max(pl.t_total, 1));
     io.Cv = cv.take<float>((size_t)H * std::max(pl.t_total, 1) * dv);
     io.stats = cv.take<float>(3);
+    // K and V through the pinned ring, the small inputs directly
+    std::vector<HostSeg> up;
+    if (!kd) up.push_back({const_cast<float *>(K), K_dev, (size_t)T * ek * sizeof(float)});
+    if (!vd) up.push_back({const_cast<float *>(V), V_dev, (size_t)T * ev * sizeof(float)});
+    if (!host_transfer(ctx, up, true, st)) return KV_COMPACT_E_DEVICE;
     hipError_t e = hipSuccess;
-    if (!kd) e = hipMemcpyAsync(K_dev, K, (size_t)T * ek * sizeof(float), hipMemcpyHostToDevice, st);
-    if (e == hipSuccess && !vd) e = hipMemcpyAsync(V_dev, V, (size_t)T * ev * sizeof(float), hipMemcpyHostToDevice, st);
-    if (e == hipSuccess && use_q && !qd) e = hipMemcpyAsync(Q_dev, Q, (size_t)n_q * ek * sizeof(float), hipMemcpyHostToDevice, st);
+    if (use_q && !qd) e = hipMemcpyAsync(Q_dev, Q, (size_t)n_q * ek * sizeof(float), hipMemcpyHostToDevice, st);
     if (e == hipSuccess && have_w) e = hipMemcpyAsync(W_dev, wts.data(), (size_t)T * sizeof(float), hipMemcpyHostToDevice, st);
     if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
     io.K = K_dev; io.V = V_dev; io.Q = Q_dev; io.wts = W_dev;
@@ -793,16 +914,22 @@ int compact_one(const float * K, const float * V, const float * Q, int T, int n_
     int rc = run_batch(ctx, st, pl, p, io, cv, &tm);
     if (rc != 0) return rc;
 
+    // results straight into the caller's arrays (C_v through the pinned ring)
     const int t = pl.t_total;
-    std::vector<int> idx(t);
-    std::vector<float> beta((size_t)H * t), cvh((size_t)H * t * dv);
+    alloc_result(res, t, H, dv);
     float stats[3];
-    e = hipMemcpy(idx.data(), io.indices, (size_t)t * sizeof(int), hipMemcpyDeviceToHost);
-    if (e == hipSuccess) e = hipMemcpy(beta.data(), io.beta, beta.size() * sizeof(float), hipMemcpyDeviceToHost);
-    if (e == hipSuccess) e = hipMemcpy(cvh.data(), io.Cv, cvh.size() * sizeof(float), hipMemcpyDeviceToHost);
+    std::vector<HostSeg> down;
+    e = hipMemcpy(res->selected_indices, io.indices, (size_t)t * sizeof(int), hipMemcpyDeviceToHost);
+    for (int h = 0; h < H; h++) {
+        if (e == hipSuccess)
+            e = hipMemcpy(res->beta[h], io.beta + (size_t)h * t, (size_t)t * sizeof(float), hipMemcpyDeviceToHost);
+        down.push_back({res->C_v[h], io.Cv + (size_t)h * t * dv, (size_t)t * dv * sizeof(float)});
+    }
     if (e == hipSuccess) e = hipMemcpy(stats, io.stats, sizeof(stats), hipMemcpyDeviceToHost);
-    if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
-    fill_result(res, t, H, dv, idx, beta, cvh);
+    if (e != hipSuccess || !host_transfer(ctx, down, false, st)) {
+        kv_compact_result_free(res);
+        return KV_COMPACT_E_DEVICE;
+    }
     res->stats.avg_cosine_sim = stats[0];
     res->stats.avg_mse = stats[1];
     res->stats.avg_agreement = stats[2];
@@ -1274,9 +1401,12 @@ int kv_compact_quantized(const uint8_t * K_quant, const uint8_t * V_quant, const
     Carver cv;
     cv.base = ctx->arena;
     carve(cv, dKq, dVq, dK, dV, dQ, dW, tmp);
-    hipError_t e = hipMemcpyAsync(dKq, K_quant, (size_t)T * k_row_bytes, hipMemcpyHostToDevice, st);
-    if (e == hipSuccess) e = hipMemcpyAsync(dVq, V_quant, (size_t)T * v_row_bytes, hipMemcpyHostToDevice, st);
-    if (e == hipSuccess && dQ) e = hipMemcpyAsync(dQ, Q_ref_all, (size_t)n_q * ek * 4, hipMemcpyHostToDevice, st);
+    // the quantized rows through the pinned ring, the small inputs directly
+    const std::vector<HostSeg> up{{const_cast<void *>(static_cast<const void *>(K_quant)), dKq, (size_t)T * k_row_bytes},
+                                  {const_cast<void *>(static_cast<const void *>(V_quant)), dVq, (size_t)T * v_row_bytes}};
+    if (!host_transfer(ctx, up, true, st)) return KV_COMPACT_E_DEVICE;
+    hipError_t e = hipSuccess;
+    if (dQ) e = hipMemcpyAsync(dQ, Q_ref_all, (size_t)n_q * ek * 4, hipMemcpyHostToDevice, st);
     if (e == hipSuccess && dW) e = hipMemcpyAsync(dW, wts.data(), (size_t)T * 4, hipMemcpyHostToDevice, st);
     if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
     io.Q = use_q ? (qd ? Q_ref_all : dQ) : nullptr;
@@ -1294,29 +1424,35 @@ int kv_compact_quantized(const uint8_t * K_quant, const uint8_t * V_quant, const
     (void)hipEventRecord(ctx->q_ev[2], st);
     requant_outputs(qi, dK, io.indices, io.Cv, 1, T, t, H, d_k, d_v, tmp, st, io.kc);
     (void)hipEventRecord(ctx->q_ev[3], st);
-    std::vector<int> idx(t);
-    std::vector<float> beta((size_t)H * t), cvh((size_t)H * t * d_v);
+    // results straight into the caller's arrays (C_v and the requantized
+    // rows through the pinned ring)
     float stats[3];
     result->K_out = (uint8_t *)malloc((size_t)std::max(t, 1) * k_row_bytes);
     result->V_out = (uint8_t *)malloc((size_t)std::max(t, 1) * v_row_bytes);
+    alloc_result(&result->base, t, H, d_v);
     e = hipGetLastError();
-    if (e == hipSuccess) e = hipMemcpyAsync(idx.data(), io.indices, (size_t)t * sizeof(int), hipMemcpyDeviceToHost, st);
-    if (e == hipSuccess) e = hipMemcpyAsync(beta.data(), io.beta, beta.size() * 4, hipMemcpyDeviceToHost, st);
-    if (e == hipSuccess) e = hipMemcpyAsync(cvh.data(), io.Cv, cvh.size() * 4, hipMemcpyDeviceToHost, st);
-    if (e == hipSuccess) e = hipMemcpyAsync(stats, io.stats, sizeof(stats), hipMemcpyDeviceToHost, st);
-    if (e == hipSuccess && t > 0)
-        e = hipMemcpyAsync(result->K_out, qi.Kout, (size_t)t * k_row_bytes, hipMemcpyDeviceToHost, st);
-    if (e == hipSuccess && t > 0)
-        e = hipMemcpyAsync(result->V_out, qi.Vout, (size_t)t * v_row_bytes, hipMemcpyDeviceToHost, st);
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e == hipSuccess) record_codec_times(ctx);
-    if (e != hipSuccess) {
+    if (e == hipSuccess)
+        e = hipMemcpy(result->base.selected_indices, io.indices, (size_t)t * sizeof(int), hipMemcpyDeviceToHost);
+    std::vector<HostSeg> down;
+    for (int h = 0; h < H; h++) {
+        if (e == hipSuccess)
+            e = hipMemcpy(result->base.beta[h], io.beta + (size_t)h * t, (size_t)t * 4, hipMemcpyDeviceToHost);
+        down.push_back({result->base.C_v[h], io.Cv + (size_t)h * t * d_v, (size_t)t * d_v * 4});
+    }
+    if (e == hipSuccess) e = hipMemcpy(stats, io.stats, sizeof(stats), hipMemcpyDeviceToHost);
+    if (t > 0) {
+        down.push_back({result->K_out, qi.Kout, (size_t)t * k_row_bytes});
+        down.push_back({result->V_out, qi.Vout, (size_t)t * v_row_bytes});
+    }
+    if (e != hipSuccess || !host_transfer(ctx, down, false, st)) {
         free(result->K_out);
         free(result->V_out);
         result->K_out = result->V_out = NULL;
+        kv_compact_result_free(&result->base);
         return KV_COMPACT_E_DEVICE;
     }
-    fill_result(&result->base, t, H, d_v, idx, beta, cvh);
     result->base.stats.avg_cosine_sim = stats[0];
     result->base.stats.avg_mse = stats[1];
     result->base.stats.avg_agreement = stats[2];

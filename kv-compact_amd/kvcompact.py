@@ -208,6 +208,10 @@ class Lib:
                            ctypes.byref(params) if params is not None else None, ctypes.byref(r))
         return rc, r
 
+    def free_result(self, r):
+        """kv_compact_result_free on a Result from compact_raw."""
+        self._free(ctypes.byref(r))
+
     def compact(self, K, V, Q, T, n_q, H, d_k, d_v, params=None) -> Compacted:
         rc, r = self.compact_raw(K, V, Q, T, n_q, H, d_k, d_v, params)
         if rc != 0:
