@@ -2097,7 +2097,7 @@ StateRun state_compact_impl(const uint8_t * blob, size_t size, bool dev, const k
     }
     const uint8_t * dblob = blob;
     if (!dev) {
-        if (hipMemcpyAsync(b.blob, blob, size, hipMemcpyHostToDevice, st) != hipSuccess)
+        if (!host_transfer(ctx, {{const_cast<uint8_t *>(blob), b.blob, size}}, true, st))
             return done(KV_COMPACT_E_DEVICE);
         dblob = b.blob;
     }
@@ -2305,8 +2305,7 @@ StateRun state_compact_impl(const uint8_t * blob, size_t size, bool dev, const k
     if (host_out) {
         uint8_t * out = (uint8_t *)malloc(std::max<size_t>(o.total, 1));
         if (!out) return done(-1);
-        if (hipMemcpyAsync(out, stage, o.total, hipMemcpyDeviceToHost, st) != hipSuccess ||
-            hipStreamSynchronize(st) != hipSuccess) {
+        if (!host_transfer(ctx, {{out, stage, o.total}}, false, st)) {
             free(out);
             return done(KV_COMPACT_E_DEVICE);
         }
