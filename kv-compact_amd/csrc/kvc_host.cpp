@@ -221,7 +221,7 @@ bool pin_ring(DeviceCtx * c) {
 
 // Copies the segments between pageable host memory and device memory on st,
 // through the pinned ring: thread i moves pieces i, i + kPinThreads, ... (at
-// most kPinBytes each, in segment order) through its two buffers. Host to
+// most pin_piece_bytes() each, in segment order) through its two buffers. Host to
 // device: a piece is copied into a buffer once the transfer that last read
 // it has finished, then its transfer is queued on st; the data is on the
 // device once st reaches that point. Device to host (data produced on st):
@@ -229,7 +229,18 @@ bool pin_ring(DeviceCtx * c) {
 // copied out, and the call returns with every piece in host memory. Without
 // the ring (or for a single piece) the segments take plain copies. Returns
 // false on a HIP error.
+// Piece size of the pinned transfers: kPinBytes, or KVC_PIN_BYTES (a test
+// switch, read at every call: 4096 .. kPinBytes) to run the ring on small
+// inputs.
+size_t pin_piece_bytes() {
+    const char * e = getenv("KVC_PIN_BYTES");
+    if (!e) return kPinBytes;
+    const long long v = atoll(e);
+    return (v >= 4096 && v <= (long long)kPinBytes) ? (size_t)v : kPinBytes;
+}
+
 bool host_transfer(DeviceCtx * c, const std::vector<HostSeg> & segs, bool to_device, hipStream_t st) {
+    const size_t piece = pin_piece_bytes();
     std::vector<HostSeg> pieces;
     for (const HostSeg & sg : segs) {
         if (sg.bytes > 0 && is_device_ptr(sg.host)) {
@@ -239,9 +250,9 @@ bool host_transfer(DeviceCtx * c, const std::vector<HostSeg> & segs, bool to_dev
             if (e != hipSuccess) return false;
             continue;
         }
-        for (size_t off = 0; off < sg.bytes; off += kPinBytes)
+        for (size_t off = 0; off < sg.bytes; off += piece)
             pieces.push_back({static_cast<char *>(sg.host) + off, static_cast<char *>(sg.dev) + off,
-                              std::min(kPinBytes, sg.bytes - off)});
+                              std::min(piece, sg.bytes - off)});
     }
     if (pieces.size() < 2 || !pin_ring(c)) {
         for (const HostSeg & pc : pieces) {

@@ -161,6 +161,10 @@ CASES = [
     # t = 600: the general elimination's panels narrower than 32 columns
     dict(name="unchunked_t600", T=1200, H=2, d=16, seed=21, qref="random", n_q=24,
          params=dict(target_ratio=0.5, chunk_size=-1)),
+    # t = 600, d_v = 128: the general elimination's back substitution in three
+    # passes of right-hand-side columns (43, 43, 42)
+    dict(name="unchunked_t600_d128", T=1200, H=1, d=128, seed=22, qref="random", n_q=24,
+         params=dict(target_ratio=0.5, chunk_size=-1)),
 ]
 
 CASE_BY_NAME = {c["name"]: c for c in CASES}
