@@ -2,6 +2,10 @@
 
 * One layer of the headline workload (T = 100,000, 8 KV heads, d = 128,
   SnapKV W = 32, keep 0.2, diversity on): every output equal to the oracle's.
+* One layer of the Llama-3-8B-shaped configuration (T = 16,384, its 1,024-key
+  tail chunk included) and one of the long-context configuration (T =
+  100,000, 4 KV heads, d = 256, bf16 storage, keep 0.5 and 0.2): every
+  output equal to the oracle's.
 * One layer with the 1M-token configuration's options (Lawson-Hanson beta,
   diversity, one refinement round, R-KV span weights) at T = 100,000 and
   4 KV heads: every output equal to the oracle's.
@@ -74,6 +78,38 @@ def test_headline_layer_exact(gpu, orc):
     b = orc.compact(K, V, Q, T, 32, H, d, d, orc.params(target_ratio=0.2, use_diversity=1))
     assert a.t == 20000
     same(a, b)
+
+
+def test_config2_layer_exact(gpu, orc):
+    """One layer of the Llama-3-8B-shaped configuration: T = 16,384, 8 KV
+    heads, d = 128, SnapKV W = 32, keep 0.2, diversity on; the plan ends in a
+    1,024-key tail chunk."""
+    T, H, d = 16384, 8, 128
+    K, V, Q = layer(T, H, d, 7004)
+    print("[full] config-2 layer T=16384 H=8 d=128 diversity", flush=True)
+    a = gpu.compact(K, V, Q, T, 32, H, d, d, gpu.params(target_ratio=0.2, use_diversity=1))
+    b = orc.compact(K, V, Q, T, 32, H, d, d, orc.params(target_ratio=0.2, use_diversity=1))
+    same(a, b)
+
+
+@pytest.mark.parametrize("ratio", [0.5, 0.2])
+def test_config3_layer_exact_bf16(gpu, orc, ratio):
+    """One layer of the long-context configuration: T = 100,000, 4 KV heads,
+    d = 256, K and V stored as bf16 (fp32 arithmetic), SnapKV W = 32, keep
+    0.5 and 0.2 with auto-chunking; the kept K rows and C_v rows come back as
+    bf16."""
+    T, H, d = 100000, 4, 256
+    K, V, Q = layer(T, H, d, 7005)
+    print(f"[full] config-3 layer T=100000 H=4 d=256 bf16 ratio={ratio}", flush=True)
+    Kb = np.stack([orc.quantize_row(K[i], kc.KV_TYPE_BF16) for i in range(T)])
+    Vb = np.stack([orc.quantize_row(V[i], kc.KV_TYPE_BF16) for i in range(T)])
+    del K, V
+    args = (Kb, Vb, Q, kc.KV_TYPE_BF16, kc.KV_TYPE_BF16, Kb.shape[1], Vb.shape[1], T, 32, H, d, d)
+    ra, a = gpu.quantized(*args, gpu.params(target_ratio=ratio))
+    rb, b = orc.quantized(*args, orc.params(target_ratio=ratio))
+    assert ra == 0 and rb == 0
+    same(a, b)
+    assert np.array_equal(a.K_out, b.K_out) and np.array_equal(a.V_out, b.V_out)
 
 
 def c5_params(lib, T, s):
