@@ -296,9 +296,16 @@ bool host_transfer(DeviceCtx * c, const std::vector<HostSeg> & segs, bool to_dev
             else memcpy(pieces[prev].host, c->pin[pb], pieces[prev].bytes);
         }
     };
+    // (a worker whose thread cannot be started runs on this one: each moves
+    // only its own pieces through its own buffers)
     std::vector<std::thread> th;
-    for (int i = 1; i < kPinThreads; i++) th.emplace_back(worker, i);
+    int started = 1;
+    try {
+        for (; started < kPinThreads; started++) th.emplace_back(worker, started);
+    } catch (...) {
+    }
     worker(0);
+    for (int i = started; i < kPinThreads; i++) worker(i);
     for (std::thread & t : th) t.join();
     // (device to host: also any direct copies queued above)
     if (!to_device && ok && hipStreamSynchronize(st) != hipSuccess) ok = false;
