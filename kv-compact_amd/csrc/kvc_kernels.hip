@@ -1047,6 +1047,86 @@ k_stats_values(Geom g, const float * __restrict__ a_all, const float * __restric
     }
 }
 
+// The same sums for grids that would leave most CUs idle (one layer): each
+// thread one (query, column) output, so that a block's time is one sequential
+// sum over the keys rather than four; blocks of 16 queries x 16 columns,
+// 64-key tiles of a and val double-buffered in LDS. fp32 values only (a
+// quantized V takes k_stats_values). grid (mh * ceil(mq/16) * ceil(dv/16), L).
+constexpr int SVN_QB = 16, SVN_VB = 16;
+
+__global__ void __launch_bounds__(SV_THREADS)
+k_stats_values_narrow(Geom g, const float * __restrict__ a_all, const float * __restrict__ ascale, long long a_ls,
+                      long long a_hs, long long a_rs, int n, const float * __restrict__ V,
+                      const float * __restrict__ Cv, int mode, float * __restrict__ out_all, int mh, int mq) {
+    const int nqb = (mq + SVN_QB - 1) / SVN_QB, nvb = (g.dv + SVN_VB - 1) / SVN_VB;
+    const int layer = blockIdx.y;
+    const int h = blockIdx.x / (nqb * nvb);
+    const int q0 = ((blockIdx.x / nvb) % nqb) * SVN_QB, v0 = (blockIdx.x % nvb) * SVN_VB;
+    const float * a = a_all + layer * a_ls + h * a_hs;   // row q at a + q * a_rs
+    const float * val;
+    long long vrs;
+    if (mode == 1) {
+        vrs = (long long)g.H * g.dv;
+        val = V + layer * g.ldV + (long long)h * g.dv;
+    } else {
+        vrs = g.dv;
+        val = Cv + ((long long)layer * g.H + h) * g.t_total * g.dv;
+    }
+    float * out = out_all + (((long long)layer * mh + h) * mq) * g.dv;
+    __shared__ float As[2][SVN_QB][SV_KT + 1];
+    __shared__ float Vs[2][SV_KT][SVN_VB];
+    const int tid = threadIdx.x, tq = tid >> 4, tv = tid & 15;
+    // tile loaders: a 16 x 64 and val 64 x 16, four elements per thread each
+    float ra[4], rv[4], sc[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int q = q0 + ((tid + SV_THREADS * u) >> 6);
+        sc[u] = ascale ? ascale[((long long)layer * mh + h) * mq + min(q, mq - 1)] : 1.0f;
+    }
+    auto load = [&](int j0) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int e = tid + SV_THREADS * u, q = q0 + (e >> 6), j = j0 + (e & 63);
+            ra[u] = (q < mq && j < n) ? a[(long long)q * a_rs + j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int e = tid + SV_THREADS * u, j = j0 + (e >> 4), c = v0 + (e & 15);
+            rv[u] = (j < n && c < g.dv) ? val[(long long)j * vrs + c] : 0.0f;
+        }
+    };
+    auto store = [&](int b) {
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int e = tid + SV_THREADS * u;
+            As[b][e >> 6][e & 63] = ra[u] * sc[u];
+            Vs[b][e >> 4][e & 15] = rv[u];
+        }
+    };
+    float acc = 0.0f;
+    const int ntiles = (n + SV_KT - 1) / SV_KT;
+    if (ntiles > 0) {
+        load(0);
+        store(0);
+    }
+    __syncthreads();
+    for (int t = 0; t < ntiles; t++) {
+        const int b = t & 1;
+        if (t + 1 < ntiles) load((t + 1) * SV_KT);
+        const int jn = min(SV_KT, n - t * SV_KT);
+        if (jn == SV_KT) {
+#pragma unroll 8
+            for (int jj = 0; jj < SV_KT; jj++) acc = acc + As[b][tq][jj] * Vs[b][jj][tv];
+        } else {
+            for (int jj = 0; jj < jn; jj++) acc = acc + As[b][tq][jj] * Vs[b][jj][tv];
+        }
+        if (t + 1 < ntiles) store(b ^ 1);
+        __syncthreads();
+    }
+    const int q = q0 + tq, c = v0 + tv;
+    if (q < mq && c < g.dv) out[(long long)q * g.dv + c] = acc;
+}
+
 // ---------------------------------------------------------------------------
 // Head sensitivity (math.h:579-594) of one (layer, chunk, head): over the
 // chunk's keys, the largest of the per-key maxima over queries of the softmax
@@ -4308,7 +4388,7 @@ k_omp_select(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
 // ---------------------------------------------------------------------------
 // In-place row softmax (math.h:83-100) of the statistics rows: row r of a
 // layer is (h = r / mq, q = r % mq) at x + layer * ls + h * hs + q * rs. A
-// block owns RSM_ROWS rows and sweeps them together, one column per thread,
+// block owns ROWS rows and sweeps them together, one column per thread,
 // so that every row's load of a column is in flight at once:
 //  1. maxima: the largest non-NaN value of each row (NaN when row[0] is NaN;
 //     the reference's scan keeps row[0] otherwise unless a value exceeds it),
@@ -4320,8 +4400,10 @@ k_omp_select(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
 //  3. inv = 1 / (sum + 1e-12f): to inv_out[layer][r] when given (the rows stay
 //     unnormalised and their reader forms x * inv, the same product), else
 //     x *= inv in place.
-// grid (ceil(mh * mq / RSM_ROWS), L), RSM_THREADS threads.
-constexpr int RSM_ROWS = 16, RSM_TILE = 256, RSM_THREADS = 64 + RSM_TILE;
+// grid (ceil(mh * mq / ROWS), L), RSM_THREADS threads. ROWS = RSM_ROWS, or
+// RSM_ROWS_FEW when that grid would leave most CUs idle (one layer): each
+// row's sequential sum then shares its block with fewer rows.
+constexpr int RSM_ROWS = 16, RSM_ROWS_FEW = 4, RSM_TILE = 256, RSM_THREADS = 64 + RSM_TILE;
 
 // tile maxima of the main scores (k_scores' tmax), for rows that are rows of S:
 // row (h, q) of a layer at tm + layer * ls + h * hs + q * rs, chunk c's tiles
@@ -4333,20 +4415,21 @@ struct RowMaxSrc {
     long long ls, hs, rs;
 };
 
+template <int ROWS>
 __global__ void __launch_bounds__(RSM_THREADS)
 k_row_softmax(float * __restrict__ x, int n, long long ls, long long hs, long long rs, int mh, int mq,
               RowMaxSrc ms, float * __restrict__ inv_out) {
-    const int layer = blockIdx.y, r0 = blockIdx.x * RSM_ROWS;
-    const int nrows = min(RSM_ROWS, mh * mq - r0);
+    const int layer = blockIdx.y, r0 = blockIdx.x * ROWS;
+    const int nrows = min(ROWS, mh * mq - r0);
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    __shared__ float mx[RSM_ROWS], inv[RSM_ROWS];
-    __shared__ float tile[2][RSM_ROWS][RSM_TILE + 1];
-    __shared__ unsigned red[RSM_THREADS / 64][RSM_ROWS];
+    __shared__ float mx[ROWS], inv[ROWS];
+    __shared__ float tile[2][ROWS][RSM_TILE + 1];
+    __shared__ unsigned red[RSM_THREADS / 64][ROWS];
     __shared__ uint64_t etab[32];
     if (tid < 32) etab[tid] = c_exp2_tab[tid];   // visible after the barriers below
-    float * rowp[RSM_ROWS];
+    float * rowp[ROWS];
 #pragma unroll
-    for (int r = 0; r < RSM_ROWS; r++) {
+    for (int r = 0; r < ROWS; r++) {
         const int rr = r0 + min(r, nrows - 1);
         rowp[r] = x + layer * ls + (long long)(rr / mq) * hs + (long long)(rr % mq) * rs;
     }
@@ -4366,19 +4449,19 @@ k_row_softmax(float * __restrict__ x, int n, long long ls, long long hs, long lo
         }
         __syncthreads();
     } else {
-        float m[RSM_ROWS];
+        float m[ROWS];
 #pragma unroll
-        for (int r = 0; r < RSM_ROWS; r++) m[r] = -INFINITY;
+        for (int r = 0; r < ROWS; r++) m[r] = -INFINITY;
         for (int j = tid; j < n; j += RSM_THREADS) {
-            float v[RSM_ROWS];
+            float v[ROWS];
 #pragma unroll
-            for (int r = 0; r < RSM_ROWS; r++) v[r] = rowp[r][j];
+            for (int r = 0; r < ROWS; r++) v[r] = rowp[r][j];
 #pragma unroll
-            for (int r = 0; r < RSM_ROWS; r++)
+            for (int r = 0; r < ROWS; r++)
                 if (v[r] == v[r] && v[r] > m[r]) m[r] = v[r];
         }
 #pragma unroll
-        for (int r = 0; r < RSM_ROWS; r++) {
+        for (int r = 0; r < ROWS; r++) {
             const unsigned k = dpp_reduce_u32<true>(score_key(m[r]));
             if (lane == 0) red[w][r] = k;
         }
@@ -4397,11 +4480,11 @@ k_row_softmax(float * __restrict__ x, int n, long long ls, long long hs, long lo
     auto compute = [&](int t, int b) {   // threads 64 .. 64 + RSM_TILE - 1
         const int c = tid - 64, j = t * RSM_TILE + c;
         if (j >= n) return;
-        float v[RSM_ROWS];
+        float v[ROWS];
 #pragma unroll
-        for (int r = 0; r < RSM_ROWS; r++) v[r] = rowp[r][j];
+        for (int r = 0; r < ROWS; r++) v[r] = rowp[r][j];
 #pragma unroll
-        for (int r = 0; r < RSM_ROWS; r++) {
+        for (int r = 0; r < ROWS; r++) {
             if (r < nrows) {
                 const float e = expf_ref(v[r] - mx[r], etab);
                 rowp[r][j] = e;
@@ -4439,15 +4522,15 @@ k_row_softmax(float * __restrict__ x, int n, long long ls, long long hs, long lo
     if (inv_out) return;
     __syncthreads();
     // 3. normalisation
-    float iv[RSM_ROWS];
+    float iv[ROWS];
 #pragma unroll
-    for (int r = 0; r < RSM_ROWS; r++) iv[r] = inv[min(r, nrows - 1)];
+    for (int r = 0; r < ROWS; r++) iv[r] = inv[min(r, nrows - 1)];
     for (int j = tid; j < n; j += RSM_THREADS) {
-        float v[RSM_ROWS];
+        float v[ROWS];
 #pragma unroll
-        for (int r = 0; r < RSM_ROWS; r++) v[r] = rowp[r][j];
+        for (int r = 0; r < ROWS; r++) v[r] = rowp[r][j];
 #pragma unroll
-        for (int r = 0; r < RSM_ROWS; r++)
+        for (int r = 0; r < ROWS; r++)
             if (r < nrows) rowp[r][j] = v[r] * iv[r];
     }
 }
@@ -5191,11 +5274,25 @@ void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st)
 // only the main scores (or the statistics' own) and V, so it may run beside
 // the compaction once the main path no longer reads S (row softmax rewrites
 // the rows of S it uses in place).
+// The statistics' sums take the narrow kernel when the wide grid would not
+// give every CU a block.
+bool stats_narrow(const Geom & g, unsigned sv_blocks) { return (long long)sv_blocks * g.L < 256; }
+
+void launch_row_softmax(const Geom & g, float * x, int n, long long ls, long long hs, long long rs, int mh, int mq,
+                        RowMaxSrc ms, float * inv_out, hipStream_t st) {
+    const int rows = mh * mq;
+    if ((long long)cdiv(rows, RSM_ROWS) * g.L < 256)
+        hipLaunchKernelGGL(k_row_softmax<RSM_ROWS_FEW>, dim3(cdiv(rows, RSM_ROWS_FEW), g.L), dim3(RSM_THREADS), 0, st,
+                           x, n, ls, hs, rs, mh, mq, ms, inv_out);
+    else
+        hipLaunchKernelGGL(k_row_softmax<RSM_ROWS>, dim3(cdiv(rows, RSM_ROWS), g.L), dim3(RSM_THREADS), 0, st,
+                           x, n, ls, hs, rs, mh, mq, ms, inv_out);
+}
+
 void launch_stats_original(const Geom & g, const Work & w, const StatWork & sw, const float * K,
                            const float * V, const float * Q, hipStream_t st, float * S_main) {
     const ChunkDesc * whole = w.chunks + g.n_chunks;      // all T keys
     const long long osl = (long long)sw.mh * sw.mq * g.T;
-    const unsigned rsm_blocks = (unsigned)cdiv(sw.mh * sw.mq, RSM_ROWS);
     const unsigned sv_blocks = (unsigned)(sw.mh * cdiv(sw.mq, SV_QB) * cdiv(g.dv, SV_VB));
     // the main path's scores S [L][H][nq_max][T] hold exactly these rows when
     // the statistics use the main query set, else they are computed here
@@ -5219,9 +5316,14 @@ void launch_stats_original(const Geom & g, const Work & w, const StatWork & sw, 
         launch_scores(g, whole, 1, g.T, K, Q, sw.OS, sw.mh, sw.mq, osl, (long long)sw.mq * g.T, g.T, sw.qmode, st,
                       nullptr, nullptr);
     }
-    hipLaunchKernelGGL(k_row_softmax, dim3(rsm_blocks, g.L), dim3(RSM_THREADS), 0, st,
-                       os, g.T, o_ls, o_hs, (long long)g.T, sw.mh, sw.mq, ms, sw.OI);
+    launch_row_softmax(g, os, g.T, o_ls, o_hs, (long long)g.T, sw.mh, sw.mq, ms, sw.OI, st);
     const dim3 sgrid(sv_blocks, g.L);
+    if (codec_inst(g.vc) == 0 && stats_narrow(g, sv_blocks)) {
+        hipLaunchKernelGGL(k_stats_values_narrow, dim3(sw.mh * cdiv(sw.mq, SVN_QB) * cdiv(g.dv, SVN_VB), g.L),
+                           dim3(SV_THREADS), 0, st, g, os, sw.OI, o_ls, o_hs, (long long)g.T, g.T, V, nullptr, 1,
+                           sw.OO, sw.mh, sw.mq);
+        return;
+    }
     switch (codec_inst(g.vc)) {
     case 8:
         hipLaunchKernelGGL(k_stats_values<8>, sgrid, dim3(SV_THREADS), SV_LDS, st,
@@ -5244,16 +5346,19 @@ void launch_stats_compacted(const Geom & g, const Work & w, const StatWork & sw,
                             float * stats, hipStream_t st) {
     const ChunkDesc * kept = w.chunks + g.n_chunks + 1;   // the t_total kept keys
     const long long csl = (long long)sw.mh * sw.mq * g.t_total;
-    const unsigned rsm_blocks = (unsigned)cdiv(sw.mh * sw.mq, RSM_ROWS);
     const unsigned sv_blocks = (unsigned)(sw.mh * cdiv(sw.mq, SV_QB) * cdiv(g.dv, SV_VB));
     launch_scores(g, kept, 1, g.t_total, K, Q, sw.CS, sw.mh, sw.mq, csl, (long long)sw.mq * g.t_total, g.t_total,
                   sw.qmode, st, w.sel, beta);
-    hipLaunchKernelGGL(k_row_softmax, dim3(rsm_blocks, g.L), dim3(RSM_THREADS), 0, st,
-                       sw.CS, g.t_total, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, sw.mh, sw.mq,
-                       RowMaxSrc{}, sw.CI);
-    hipLaunchKernelGGL(k_stats_values<0>, dim3(sv_blocks, g.L), dim3(SV_THREADS), SV_LDS, st,
-                       g, sw.CS, sw.CI, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, g.t_total, V, Cv, 2,
-                       sw.CO, sw.mh, sw.mq);
+    launch_row_softmax(g, sw.CS, g.t_total, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, sw.mh, sw.mq,
+                       RowMaxSrc{}, sw.CI, st);
+    if (stats_narrow(g, sv_blocks))
+        hipLaunchKernelGGL(k_stats_values_narrow, dim3(sw.mh * cdiv(sw.mq, SVN_QB) * cdiv(g.dv, SVN_VB), g.L),
+                           dim3(SV_THREADS), 0, st, g, sw.CS, sw.CI, csl, (long long)sw.mq * g.t_total,
+                           (long long)g.t_total, g.t_total, V, Cv, 2, sw.CO, sw.mh, sw.mq);
+    else
+        hipLaunchKernelGGL(k_stats_values<0>, dim3(sv_blocks, g.L), dim3(SV_THREADS), SV_LDS, st,
+                           g, sw.CS, sw.CI, csl, (long long)sw.mq * g.t_total, (long long)g.t_total, g.t_total, V, Cv,
+                           2, sw.CO, sw.mh, sw.mq);
 }
 
 void launch_stats_final(const Geom & g, const StatWork & sw, float * stats, hipStream_t st) {
