@@ -1185,10 +1185,12 @@ k_global_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float *
 
 // ---------------------------------------------------------------------------
 // Top-t selection (api.cpp:716-744): the set std::partial_sort keeps under
-// "greater importance first" — libstdc++'s heap selection, restated here so
-// that boundary ties resolve to the same members — written ascending.
-// grid = (n_chunks, L). The heap runs on lane 0 over LDS copies (or global
-// scratch for chunks beyond the LDS budget).
+// "greater importance first", written ascending. Without NaN and without a
+// tie across the boundary that set is every candidate at or above the t-th
+// largest importance, found by a block-wide bitwise search; otherwise
+// libstdc++'s heap selection, restated here so that boundary ties resolve to
+// the same members, runs on lane 0 over LDS copies (or global scratch for
+// chunks beyond the LDS budget). grid = (n_chunks, L).
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool heap_less(const float * imp, int a, int b) { return imp[a] > imp[b]; }
 
@@ -1296,9 +1298,52 @@ k_select_topk(Geom g, const ChunkDesc * __restrict__ chunks, const float * __res
     for (int j = threadIdx.x; j < nc; j += blockDim.x) cand[j] = pc + j;
     for (int j = threadIdx.x; j < c.Tc; j += blockDim.x) fl[j] = (j < pc) ? 1 : 0;
     __syncthreads();
-    if (threadIdx.x == 0 && rem > 0) heap_select(cand, rem, nc, im);
-    __syncthreads();
-    for (int j = threadIdx.x; j < rem; j += blockDim.x) fl[cand[j]] = 1;
+    // The set a partial sort keeps is fixed by value unless the boundary
+    // value ties: find the rem-th largest order key K (-0 counted as +0, the
+    // comparator's equality) by a bitwise search over block counts; when no
+    // candidate is NaN and exactly rem candidates reach K, they are the set.
+    // Otherwise (NaN, or a tie across the boundary) the heap selection
+    // decides which of the tied keys stay.
+    bool fast = false;
+    if (rem > 0) {
+        __shared__ int s_wc[4];
+        auto okey = [](float v) {
+            const unsigned u = __float_as_uint(v == 0.0f ? 0.0f : v);
+            return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+        };
+        // candidates with key >= kt (nan: with a NaN importance instead)
+        auto count = [&](unsigned kt, bool nan) {
+            int cnt = 0;
+            for (int j0 = 0; j0 < nc; j0 += blockDim.x) {
+                const int j = j0 + threadIdx.x;
+                const float v = j < nc ? im[pc + j] : 0.0f;
+                const bool pr = j < nc && (nan ? v != v : okey(v) >= kt);
+                cnt += __popcll(__ballot(pr));
+            }
+            if ((threadIdx.x & 63) == 0) s_wc[threadIdx.x >> 6] = cnt;
+            __syncthreads();
+            int tot = 0;
+            for (int i = 0; i < (int)(blockDim.x >> 6); i++) tot += s_wc[i];
+            __syncthreads();
+            return tot;
+        };
+        if (count(0u, true) == 0) {
+            unsigned K = 0u;
+            for (int b = 31; b >= 0; b--) {
+                const unsigned kt = K | (1u << b);
+                if (count(kt, false) >= rem) K = kt;
+            }
+            fast = count(K, false) == rem;
+            if (fast)
+                for (int j = threadIdx.x; j < nc; j += blockDim.x)
+                    if (okey(im[pc + j]) >= K) fl[pc + j] = 1;
+        }
+    }
+    if (!fast) {
+        if (threadIdx.x == 0 && rem > 0) heap_select(cand, rem, nc, im);
+        __syncthreads();
+        for (int j = threadIdx.x; j < rem; j += blockDim.x) fl[cand[j]] = 1;
+    }
     __syncthreads();
     write_flagged(fl, c.Tc, c.start, sel + (long long)layer * g.t_total + c.off);
 }

@@ -55,6 +55,24 @@ def test_case_parity(gpu, orc, name):
     same(run_case(gpu, c, inp), run_case(orc, c, inp))
 
 
+@pytest.mark.parametrize("ratio", [0.25, 0.3, 0.7])
+def test_topk_boundary_ties(gpu, orc, ratio):
+    """Top-t selection (no diversity) with every key row repeated four times:
+    every importance appears four times, so the kept boundary usually splits
+    a group of equal importances and the heap selection's tie order decides
+    (0.25 keeps whole groups, 0.3 and 0.7 split one)."""
+    T, H, d = 1024, 2, 32
+    print(f"[case] topk_boundary_ties ratio={ratio}", flush=True)
+    K0, _ = kv_cache(T // 4, H, d, 41)
+    K = np.ascontiguousarray(np.repeat(K0, 4, axis=0))
+    V, _ = kv_cache(T, H, d, 42)
+    Q = np.ascontiguousarray(np.repeat(K0[-3:], 4, axis=0))
+    p = dict(target_ratio=ratio)
+    a = gpu.compact(K, V, Q, T, 12, H, d, d, gpu.params(**p))
+    b = orc.compact(K, V, Q, T, 12, H, d, d, orc.params(**p))
+    same(a, b)
+
+
 def test_config1_shape(gpu, orc):
     """Single head, T=4096, d=128, 4 outlier channels x8, cheap Q_ref, 50%."""
     K, V = kv_cache(4096, 1, 128, 101, outliers=4)
