@@ -1370,6 +1370,7 @@ k_select_topk(Geom g, const ChunkDesc * __restrict__ chunks, const float * __res
 
 // candidates of one (layer, chunk): ascending positions of the unused keys
 // with importance >= alpha * I_t; grid (n_chunks, L), 256 threads
+constexpr int DC_LDS = 4096;
 __global__ void __launch_bounds__(256)
 k_div_candidates(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ gimp, DivWork dw,
                  int * __restrict__ cand_all) {
@@ -1381,9 +1382,9 @@ k_div_candidates(Geom g, const ChunkDesc * __restrict__ chunks, const float * __
     const int pc = min(c.prefix, c.tc);
     const int need = c.tc - pc;
     const int tid = threadIdx.x;
-    __shared__ int s_cnt, s_bad;
-    __shared__ unsigned s_lo, s_hi;
+    __shared__ int s_bad;
     __shared__ int wsum[4];
+    __shared__ float s_im[DC_LDS];
     if (need <= 0) {   // the prefix fills the chunk: no greedy step
         if (tid == 0) {
             dw.maxnc[unit] = -INFINITY;
@@ -1407,25 +1408,31 @@ k_div_candidates(Geom g, const ChunkDesc * __restrict__ chunks, const float * __
     }
     if (prune) {
         // I_t: the largest bit pattern x with #(imp >= x) >= tc (order of
-        // non-negative floats = order of their bits)
-        if (tid == 0) { s_lo = 0u; s_hi = 0x7f7fffffu; }
-        __syncthreads();
-        for (int it = 0; it < 32; it++) {
-            const unsigned lo = s_lo, hi = s_hi;
-            if (lo >= hi) break;
-            const unsigned mid = lo + (hi - lo + 1u) / 2u;
-            if (tid == 0) s_cnt = 0;
+        // non-negative floats = order of their bits), by bisection over
+        // block counts (a ballot per wave, the waves' counts through LDS;
+        // every thread takes the same bounds); the chunk's importances staged
+        // in LDS when they fit
+        const float * src = im;
+        if (c.Tc <= DC_LDS) {
+            for (int j = tid; j < c.Tc; j += blockDim.x) s_im[j] = im[j];
             __syncthreads();
-            int cnt = 0;
-            for (int j = tid; j < c.Tc; j += blockDim.x) cnt += (__float_as_uint(im[j]) >= mid) ? 1 : 0;
-            atomicAdd(&s_cnt, cnt);
-            __syncthreads();
-            if (tid == 0) {
-                if (s_cnt >= c.tc) s_lo = mid; else s_hi = mid - 1u;
-            }
-            __syncthreads();
+            src = s_im;
         }
-        thr = __uint_as_float(s_lo) * dw.alpha;
+        unsigned lo = 0u, hi = 0x7f7fffffu;
+        for (int it = 0; it < 32 && lo < hi; it++) {
+            const unsigned mid = lo + (hi - lo + 1u) / 2u;
+            int cnt = 0;
+            for (int j0 = 0; j0 < c.Tc; j0 += blockDim.x) {
+                const int j = j0 + tid;
+                cnt += __popcll(__ballot(j < c.Tc && __float_as_uint(src[j < c.Tc ? j : 0]) >= mid));
+            }
+            if ((tid & 63) == 0) wsum[tid >> 6] = cnt;
+            __syncthreads();
+            const int tot = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+            __syncthreads();
+            if (tot >= c.tc) lo = mid; else hi = mid - 1u;
+        }
+        thr = __uint_as_float(lo) * dw.alpha;
     }
     // flags, the largest pruned importance, then an ascending write-out
     int * cand = cand_all + (long long)unit * g.Tc_max;
