@@ -1801,7 +1801,9 @@ struct BlobReader {
             return true;
         }
         if (off < win_off || off + n > win_off + win_len) {
-            const size_t len = std::min(size - off, std::max(n, (size_t)1 << 20));
+            // the first window covers the cell records; later reads are the
+            // layers' headers, megabytes apart: small windows
+            const size_t len = std::min(size - off, std::max(n, win_len == 0 ? (size_t)1 << 20 : (size_t)1 << 16));
             win.resize(len);
             if (hipMemcpy(win.data(), p + off, len, hipMemcpyDeviceToHost) != hipSuccess) {
                 (void)hipGetLastError();
