@@ -96,7 +96,9 @@ int kvc_compact_quantized_device(const uint8_t * K_quant, const uint8_t * V_quan
  * written. */
 int kvc_stage_times(float * out_ms, int n);
 
-/* Release the library's cached device workspace of the current device. */
+/* Release the library's cached device workspace of the current device, and
+ * its pinned host ring for transfers from and to pageable host memory (both
+ * are allocated again by the next call that needs them). */
 void kvc_release_workspace(void);
 
 #ifdef __cplusplus

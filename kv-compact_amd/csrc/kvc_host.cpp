@@ -1767,9 +1767,23 @@ void kvc_release_workspace(void) {
     std::lock_guard<std::mutex> lk(c->mu);
     if (c->arena) {
         (void)hipStreamSynchronize(c->stream);
+        (void)hipStreamSynchronize(c->stream2);
         (void)hipFree(c->arena);
         c->arena = nullptr;
         c->arena_cap = 0;
+    }
+    if (c->pin_ready) {
+        // (a call that failed may have left a transfer from the ring queued)
+        for (int b = 0; b < kPinBufs; b++)
+            if (c->pin_used[b]) (void)hipEventSynchronize(c->pin_ev[b]);
+        for (int b = 0; b < kPinBufs; b++) {
+            (void)hipHostFree(c->pin[b]);
+            (void)hipEventDestroy(c->pin_ev[b]);
+            c->pin[b] = nullptr;
+            c->pin_ev[b] = nullptr;
+            c->pin_used[b] = false;
+        }
+        c->pin_ready = false;
     }
 }
 

@@ -77,6 +77,25 @@ def test_host_compact_in_pieces(gpu, orc, piece):
     same(a, b)
 
 
+def test_release_between_calls(gpu, orc):
+    """kvc_release_workspace frees the device workspace and the pinned ring;
+    the next host-pointer call allocates both again and gives the same
+    results."""
+    T, H, d = 2560, 8, 128
+    print("[transfer] release between calls", flush=True)
+    K, V = kv_cache(T, H, d, 303)
+    Q = snapkv_queries(K, 32, 303)
+    p = dict(target_ratio=0.2)
+    b = orc.compact(K, V, Q, T, 32, H, d, d, orc.params(**p))
+    with pieces(65540):
+        a1 = gpu.compact(K, V, Q, T, 32, H, d, d, gpu.params(**p))
+        gpu.dll.kvc_release_workspace.restype = None
+        gpu.dll.kvc_release_workspace()
+        a2 = gpu.compact(K, V, Q, T, 32, H, d, d, gpu.params(**p))
+    same(a1, b)
+    same(a2, b)
+
+
 def test_host_quantized_in_pieces(gpu, orc):
     """Q8_0 K, Q4_0 V, H = 8, d = 128, T = 2560, cheap queries: the rows go up
     and the requantized rows come back in pieces of 4100 bytes."""
