@@ -20,7 +20,8 @@
  * count, -4 quantized row size mismatch (all as the reference), and the
  * additional codes KV_COMPACT_E_UNSUPPORTED (-5: an option this library
  * does not implement on the GPU) and KV_COMPACT_E_DEVICE (-6: no usable
- * GPU or a HIP runtime failure). There is no CPU fallback.
+ * GPU, a HIP runtime failure, or a failed host allocation of the result).
+ * There is no CPU fallback.
  */
 #pragma once
 

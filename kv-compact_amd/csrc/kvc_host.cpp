@@ -846,27 +846,37 @@ int validate(const float * K, const float * V, const void * res, int T, int n_q,
 
 // Device-resident outputs of one layer copied into a malloc'd host result.
 // The result's arrays (reference ownership: malloc'd, freed by
-// kv_compact_result_free), contents not yet set.
-void alloc_result(kv_compact_result * r, int t, int H, int dv) {
+// kv_compact_result_free), contents not yet set. False (and nothing left
+// allocated) when an allocation fails.
+bool alloc_result(kv_compact_result * r, int t, int H, int dv) {
     r->t = t;
     r->n_head_kv = H;
     r->selected_indices = (int *)malloc((size_t)std::max(t, 1) * sizeof(int));
-    r->beta = (float **)malloc((size_t)H * sizeof(float *));
-    r->C_v = (float **)malloc((size_t)H * sizeof(float *));
-    for (int h = 0; h < H; h++) {
+    r->beta = (float **)calloc((size_t)std::max(H, 1), sizeof(float *));
+    r->C_v = (float **)calloc((size_t)std::max(H, 1), sizeof(float *));
+    bool ok = r->selected_indices && r->beta && r->C_v;
+    for (int h = 0; ok && h < H; h++) {
         r->beta[h] = (float *)malloc((size_t)std::max(t, 1) * sizeof(float));
         r->C_v[h] = (float *)malloc((size_t)std::max(t, 1) * dv * sizeof(float));
+        ok = r->beta[h] && r->C_v[h];
     }
+    if (!ok) {
+        fprintf(stderr, "[kv-compact] host allocation of the result failed\n");
+        if (!r->beta || !r->C_v) r->n_head_kv = 0;   // (entries freed only when both arrays exist)
+        kv_compact_result_free(r);
+    }
+    return ok;
 }
 
-void fill_result(kv_compact_result * r, int t, int H, int dv, const std::vector<int> & idx,
+bool fill_result(kv_compact_result * r, int t, int H, int dv, const std::vector<int> & idx,
                  const std::vector<float> & beta, const std::vector<float> & cv) {
-    alloc_result(r, t, H, dv);
+    if (!alloc_result(r, t, H, dv)) return false;
     memcpy(r->selected_indices, idx.data(), (size_t)t * sizeof(int));
     for (int h = 0; h < H; h++) {
         memcpy(r->beta[h], beta.data() + (size_t)h * t, (size_t)t * sizeof(float));
         memcpy(r->C_v[h], cv.data() + (size_t)h * t * dv, (size_t)t * dv * sizeof(float));
     }
+    return true;
 }
 
 // One layer with host or device inputs; results to host (kv_compact()).
@@ -934,7 +944,7 @@ int compact_one(const float * K, const float * V, const float * Q, int T, int n_
 
     // results straight into the caller's arrays (C_v through the pinned ring)
     const int t = pl.t_total;
-    alloc_result(res, t, H, dv);
+    if (!alloc_result(res, t, H, dv)) return KV_COMPACT_E_DEVICE;
     float stats[3];
     std::vector<HostSeg> down;
     e = hipMemcpy(res->selected_indices, io.indices, (size_t)t * sizeof(int), hipMemcpyDeviceToHost);
@@ -1207,7 +1217,10 @@ int kv_compact_multi_round(const float * K_all, const float * V_all, const float
                 memcpy(b.data() + (size_t)h * nT, rr.beta[h], (size_t)nT * 4);
                 memcpy(c.data() + (size_t)h * nT * d_v, rr.C_v[h], (size_t)nT * d_v * 4);
             }
-            fill_result(result, nT, H, d_v, norig, b, c);
+            if (!fill_result(result, nT, H, d_v, norig, b, c)) {
+                kv_compact_result_free(&rr);
+                return KV_COMPACT_E_DEVICE;
+            }
             result->stats = rr.stats;
         }
         kv_compact_result_free(&rr);
@@ -1447,7 +1460,13 @@ int kv_compact_quantized(const uint8_t * K_quant, const uint8_t * V_quant, const
     float stats[3];
     result->K_out = (uint8_t *)malloc((size_t)std::max(t, 1) * k_row_bytes);
     result->V_out = (uint8_t *)malloc((size_t)std::max(t, 1) * v_row_bytes);
-    alloc_result(&result->base, t, H, d_v);
+    if (!result->K_out || !result->V_out || !alloc_result(&result->base, t, H, d_v)) {
+        free(result->K_out);
+        free(result->V_out);
+        result->K_out = result->V_out = NULL;
+        kv_compact_result_free(&result->base);
+        return KV_COMPACT_E_DEVICE;
+    }
     e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(st);
     if (e == hipSuccess) record_codec_times(ctx);
