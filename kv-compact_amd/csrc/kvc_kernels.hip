@@ -805,21 +805,20 @@ __device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, const
         float ra[4];
         float4 rv[4];
         Raw4 rq[4];   // (quantized V) raw value bits, decoded at the LDS store
+        // loads at clamped (valid) positions with no condition on them; the
+        // row scale and the zeros for keys past n and queries past nq are
+        // applied at the LDS store (a product or a select on a load here
+        // would make each load wait for its data before the tile is summed)
         auto load = [&](int j0) {
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int j = j0 + lk + u;
-                const float x = arow[min(j, n - 1)] * sc;
-                ra[u] = (qok && j < n) ? x : 0.0f;
-            }
+            for (int u = 0; u < 4; u++) ra[u] = arow[min(j0 + lk + u, n - 1)];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
-                const int j = j0 + vk + 8 * u;
+                const int j = min(j0 + vk + 8 * u, n - 1);
                 if constexpr (VC != 0) {
-                    rq[u] = raw_keep(j < n, codec_raw4<VC>(vq, layer, vrow0 + min(j, n - 1), ve0 + vc));
+                    rq[u] = codec_raw4<VC>(vq, layer, vrow0 + j, ve0 + vc);
                 } else {
-                    const float4 x = *reinterpret_cast<const float4 *>(val + (long long)min(j, n - 1) * val_rs + vc);
-                    rv[u] = j < n ? x : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    rv[u] = *reinterpret_cast<const float4 *>(val + (long long)j * val_rs + vc);
                 }
             }
         };
@@ -832,10 +831,18 @@ __device__ __forceinline__ void attn_sum_128(const float * __restrict__ a, const
         for (int j0 = 0; j0 < n; j0 += AS_KT) {
             __syncthreads();
 #pragma unroll
-            for (int u = 0; u < 4; u++) as[lk + u][lq] = ra[u];
+            for (int u = 0; u < 4; u++) {
+                const float x = ra[u] * sc;
+                as[lk + u][lq] = (qok && j0 + lk + u < n) ? x : 0.0f;
+            }
 #pragma unroll
-            for (int u = 0; u < 4; u++)
-                *reinterpret_cast<float4 *>(&vs[vk + 8 * u][vc]) = VC ? codec_dec4<VC>(rq[u]) : rv[u];
+            for (int u = 0; u < 4; u++) {
+                const bool in = j0 + vk + 8 * u < n;
+                float4 x;
+                if constexpr (VC != 0) x = codec_dec4<VC>(raw_keep(in, rq[u]));
+                else x = in ? rv[u] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                *reinterpret_cast<float4 *>(&vs[vk + 8 * u][vc]) = x;
+            }
             __syncthreads();
             load(j0 + AS_KT);   // past the end: clamped rows, zeros (not used)
             asm volatile("" ::: "memory");   // keeps the loads ahead of the sums
