@@ -568,6 +568,17 @@ __device__ __forceinline__ float wave_ref_row_max(const float * row, int n, int 
     return (mm > r0) ? mm : r0;
 }
 
+// Workgroup barrier for data in LDS only: waits for this wave's LDS
+// operations and leaves its global loads and stores in flight (a
+// __syncthreads also waits for those). The empty asm statements keep the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0), vmcnt and expcnt unchanged
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
 // Chunk softmax + per-key importance (math.h:142-248), for up to SOFTMAX_MAXQ rows
 // (two floats per row in dynamic LDS):
 //  1. row maxima, one wave per row;
@@ -617,21 +628,24 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
         }
     }
     __syncthreads();
-    // 2. exponentials and ordered row sums, 32 rows at a time
+    // 2. exponentials and ordered row sums, 32 rows at a time; the next tile's
+    //    scores load while the row sums run (barriers for LDS only)
+    const int kk = tid & 63;
     for (int r0 = 0; r0 < nq; r0 += SM_TROWS) {
         const int nr = min(SM_TROWS, nq - r0);
         float sum = 0.0f;   // row r0 + tid for tid < nr
+        // this thread's rows wv, wv + 4, ... of tile t0, at clamped (in-bounds) rows and keys
+        float sv[SM_TROWS / 4];
+        auto load = [&](int t0) {
+            const int j = t0 + min(kk, min(SM_TILE, n - t0) - 1);
+#pragma unroll
+            for (int u = 0; u < SM_TROWS / 4; u++)
+                sv[u] = Sh[(long long)(r0 + min(wv + 4 * u, nr - 1)) * rs + j];
+        };
+        load(0);
         for (int t0 = 0; t0 < n; t0 += SM_TILE) {
             const int jn = min(SM_TILE, n - t0);
-            const int kk = tid & 63;
             if (kk < jn) {
-                // this thread's rows wv, wv + 4, ...: every load in flight first
-                float sv[SM_TROWS / 4];
-#pragma unroll
-                for (int u = 0; u < SM_TROWS / 4; u++) {
-                    const int rr = wv + 4 * u;
-                    if (rr < nr) sv[u] = Sh[(r0 + rr) * rs + t0 + kk];
-                }
 #pragma unroll
                 for (int u = 0; u < SM_TROWS / 4; u++) {
                     const int rr = wv + 4 * u;
@@ -643,7 +657,8 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
                     }
                 }
             }
-            __syncthreads();
+            lds_barrier();
+            if (t0 + SM_TILE < n) load(t0 + SM_TILE);
             if (tid < nr) {
                 int j = 0;
                 for (; j + 16 <= jn; j += 16) {   // 16 reads in flight, then the adds in order
@@ -655,7 +670,7 @@ k_softmax_importance(Geom g, const ChunkDesc * __restrict__ chunks, const float 
                 }
                 for (; j < jn; j++) sum += eb[tid][j];
             }
-            __syncthreads();
+            lds_barrier();
         }
         if (tid < nr) {
             const int r = r0 + tid;
