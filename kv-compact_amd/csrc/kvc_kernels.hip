@@ -1899,19 +1899,18 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
     __syncthreads();
     for (int r0 = 0; r0 < nq; r0 += rows) {
         const int nr = min(rows, nq - r0);
-        // gather: eight rows' loads per thread in flight
+        // gather: all rows' loads per thread in flight (at clamped rows: in
+        // bounds, the extra ones unused); the LDS caps the block count, so
+        // these registers cost no occupancy
         for (int j = tid; j < t; j += blockDim.x) {
             const int sj = sls[j];
             const float bj = bs[j];
-            for (int rb = 0; rb < nr; rb += 8) {
-                float v[8];
+            float v[LSX_ROWS];
 #pragma unroll
-                for (int u = 0; u < 8; u++)
-                    if (rb + u < nr) v[u] = Sh[(long long)(r0 + rb + u) * g.T + sj];
+            for (int u = 0; u < LSX_ROWS; u++) v[u] = Sh[(long long)(r0 + min(u, nr - 1)) * g.T + sj];
 #pragma unroll
-                for (int u = 0; u < 8; u++)
-                    if (rb + u < nr) xs[(rb + u) * ld + j] = v[u] + bj;
-            }
+            for (int u = 0; u < LSX_ROWS; u++)
+                if (u < nr) xs[u * ld + j] = v[u] + bj;
         }
         __syncthreads();
         // maxima: largest non-NaN value, NaN when the first entry is NaN,
