@@ -2250,17 +2250,27 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
                     (reinterpret_cast<uintptr_t>(Xh) & 15) == 0 && (reinterpret_cast<uintptr_t>(Yh) & 15) == 0;
     auto stage = [&](int k0, int kn) {
         if (v4) {
-            // 16-byte pieces with no branch around the loads (w = wp here)
-            const int n4 = n >> 2, p4 = p >> 2;
-            for (int q = threadIdx.x; q < kn * n4; q += blockDim.x) {
-                const int k = q / n4, j4 = q - k * n4;
-                *reinterpret_cast<float4 *>(&xs[k * wp + 4 * j4]) =
-                    *reinterpret_cast<const float4 *>(Xh + (long long)(k0 + k) * g.t_total + 4 * j4);
-            }
-            for (int q = threadIdx.x; q < kn * p4; q += blockDim.x) {
-                const int k = q / p4, j4 = q - k * p4;
-                *reinterpret_cast<float4 *>(&xs[k * wp + n + 4 * j4]) =
-                    *reinterpret_cast<const float4 *>(Yh + (long long)(k0 + k) * g.dv + 4 * j4);
+            // 16-byte pieces, eight loads per thread in flight before their
+            // LDS stores: pieces q < tx are X's, the rest Y's (w = wp here);
+            // a slot past the end repeats the last piece (the same value to
+            // the same place)
+            const int n4 = n >> 2, p4 = p >> 2, tx = kn * n4, tot = tx + kn * p4;
+            for (int q0 = threadIdx.x; q0 < tot; q0 += 8 * blockDim.x) {
+                float4 v[8];
+                int dst[8];
+#pragma unroll
+                for (int u = 0; u < 8; u++) {
+                    const int q = min(q0 + u * (int)blockDim.x, tot - 1);
+                    const bool isx = q < tx;
+                    const int qq = isx ? q : q - tx, w4 = isx ? n4 : p4;
+                    const int k = qq / w4, j4 = qq - k * w4;
+                    const float * src = isx ? Xh + (long long)(k0 + k) * g.t_total + 4 * j4
+                                            : Yh + (long long)(k0 + k) * g.dv + 4 * j4;
+                    dst[u] = k * wp + (isx ? 0 : n) + 4 * j4;
+                    v[u] = *reinterpret_cast<const float4 *>(src);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; u++) *reinterpret_cast<float4 *>(&xs[dst[u]]) = v[u];
             }
         } else {
             for (int e = threadIdx.x; e < kn * wp; e += blockDim.x) {
