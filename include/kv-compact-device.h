@@ -44,7 +44,7 @@ int kvc_compact_layers_device(const float * K, const float * V, const float * Q_
 
 /* Allocation-free variant of kvc_compact_layers_device (no counterpart in the
  * reference). For callers that cannot allocate device memory (tight serving
- * loops, code under graph capture, harnesses that forbid hipMalloc): same
+ * loops, harnesses that forbid hipMalloc): same
  * arguments, outputs and results bit for bit, but the workspace is a fixed
  * device array of KVC_NOALLOC_SCRATCH_BYTES per GPU that the library holds
  * from load until the process ends, and the call makes no hipMalloc/hipFree
@@ -54,7 +54,9 @@ int kvc_compact_layers_device(const float * K, const float * V, const float * Q_
  * what it reads, and clears its status flag with a kernel): calls on one GPU
  * must not overlap — this library serializes its own calls per device, so
  * overlapping calls can only come from elsewhere (another copy of the library
- * in the process) and would race on the array. */
+ * in the process) and would race on the array. The call is not capturable
+ * into a HIP graph: like kvc_compact_layers_device it synchronizes its
+ * stream and copies a status word to the host before it returns. */
 #define KVC_NOALLOC_SCRATCH_BYTES (64u << 20)
 #define KVC_E_SCRATCH (-7)
 int kvc_compact_layers_device_noalloc(const float * K, const float * V, const float * Q_ref,
@@ -100,6 +102,12 @@ int kvc_stage_times(float * out_ms, int n);
  * its pinned host ring for transfers from and to pageable host memory (both
  * are allocated again by the next call that needs them). */
 void kvc_release_workspace(void);
+
+/* Number of HIP streams, events and pinned host buffers the library holds,
+ * over all devices (no counterpart in the reference). It stays constant
+ * across calls once the library is set up, including calls that fail part
+ * of the way through a set-up; a test of the error paths reads it. */
+int kvc_live_objects(void);
 
 #ifdef __cplusplus
 }

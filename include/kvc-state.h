@@ -33,8 +33,8 @@
  *    bytes, state.h:419, :628);
  *  - more than 8192 reference queries.
  */
-#ifndef KV_COMPACT_STATE_H
-#define KV_COMPACT_STATE_H
+#ifndef KVC_STATE_H
+#define KVC_STATE_H
 
 #include <stddef.h>
 #include <stdint.h>

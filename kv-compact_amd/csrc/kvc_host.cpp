@@ -27,7 +27,7 @@
 #include "../../include/kv-compact-api.h"
 #include "../../include/kv-compact-accel.h"
 #include "../../include/kv-compact-device.h"
-#include "../../include/kv-compact-state.h"
+#include "../../include/kvc-state.h"
 #include "kvc_common.h"
 #include "kvc_kernels.h"
 
@@ -95,7 +95,71 @@ void exp2_table(uint64_t tab[32]) {
     }
 }
 
-// Returns the context of the current device, initialised, or nullptr.
+// HIP streams, events and pinned host buffers the library holds, over all
+// devices (kvc_live_objects): every creation below counts one, every destroy
+// takes one back, so a failure path that leaks shows up in the count.
+std::atomic<int> g_live{0};
+
+bool made(hipError_t e) {
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    g_live++;
+    return true;
+}
+
+template <class H, class F> void drop(H & h, F destroy) {
+    if (!h) return;
+    (void)destroy(h);
+    h = nullptr;
+    g_live--;
+}
+
+// Destroys the streams and events of a context (a device_ctx set-up that
+// failed part of the way, so the next call starts again from nothing).
+void destroy_ctx_objects(DeviceCtx * c) {
+    drop(c->stream, hipStreamDestroy);
+    drop(c->stream2, hipStreamDestroy);
+    drop(c->fork_ev, hipEventDestroy);
+    drop(c->join_ev, hipEventDestroy);
+    drop(c->refit_fork, hipEventDestroy);
+    drop(c->refit_join, hipEventDestroy);
+    for (hipEvent_t & e : c->refit_t) drop(e, hipEventDestroy);
+    for (hipEvent_t & e : c->ev) drop(e, hipEventDestroy);
+    for (hipEvent_t & e : c->q_ev) drop(e, hipEventDestroy);
+}
+
+bool forced_fault(const char * kind);
+
+bool create_ctx_objects(DeviceCtx * c) {
+    uint64_t tab[32];
+    exp2_table(tab);
+    if (set_exp2_table(tab) != hipSuccess) {
+        (void)hipGetLastError();
+        return false;
+    }
+    if (!made(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking)) ||
+        !made(hipStreamCreateWithFlags(&c->stream2, hipStreamNonBlocking)) ||
+        !made(hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming)) ||
+        !made(hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming)))
+        return false;
+    // (KVC_FAULT=init: the set-up fails here, with part of its objects made)
+    if (forced_fault("init")) return false;
+    if (!made(hipEventCreateWithFlags(&c->refit_fork, hipEventDisableTiming)) ||
+        !made(hipEventCreateWithFlags(&c->refit_join, hipEventDisableTiming)))
+        return false;
+    for (hipEvent_t & e : c->refit_t)
+        if (!made(hipEventCreate(&e))) return false;
+    for (hipEvent_t & e : c->ev)
+        if (!made(hipEventCreate(&e))) return false;
+    for (hipEvent_t & e : c->q_ev)
+        if (!made(hipEventCreate(&e))) return false;
+    return true;
+}
+
+// Returns the context of the current device, initialised, or nullptr (then
+// nothing of a partial set-up is kept, and the next call tries again).
 DeviceCtx * device_ctx() {
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
@@ -107,21 +171,10 @@ DeviceCtx * device_ctx() {
     DeviceCtx * c = &g_dev[dev];
     std::lock_guard<std::mutex> lk(g_init_mu);
     if (!c->ready) {
-        uint64_t tab[32];
-        exp2_table(tab);
-        if (set_exp2_table(tab) != hipSuccess) return nullptr;
-        if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
-        if (hipStreamCreateWithFlags(&c->stream2, hipStreamNonBlocking) != hipSuccess) return nullptr;
-        if (hipEventCreateWithFlags(&c->fork_ev, hipEventDisableTiming) != hipSuccess) return nullptr;
-        if (hipEventCreateWithFlags(&c->join_ev, hipEventDisableTiming) != hipSuccess) return nullptr;
-        if (hipEventCreateWithFlags(&c->refit_fork, hipEventDisableTiming) != hipSuccess) return nullptr;
-        if (hipEventCreateWithFlags(&c->refit_join, hipEventDisableTiming) != hipSuccess) return nullptr;
-        for (int i = 0; i < 2; i++)
-            if (hipEventCreate(&c->refit_t[i]) != hipSuccess) return nullptr;
-        for (int i = 0; i <= ST_BATCH_END; i++)
-            if (hipEventCreate(&c->ev[i]) != hipSuccess) return nullptr;
-        for (int i = 0; i < 4; i++)
-            if (hipEventCreate(&c->q_ev[i]) != hipSuccess) return nullptr;
+        if (!create_ctx_objects(c)) {
+            destroy_ctx_objects(c);
+            return nullptr;
+        }
         void * sp = nullptr;
         if (hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)) == hipSuccess) {
             c->scratch = static_cast<char *>(sp);
@@ -204,13 +257,29 @@ struct HostSeg {
     size_t bytes;
 };
 
+// Frees the pinned ring's buffers and events (after any transfer still
+// queued from them).
+void free_pin_ring(DeviceCtx * c) {
+    for (int b = 0; b < kPinBufs; b++)
+        if (c->pin_used[b] && c->pin_ev[b]) (void)hipEventSynchronize(c->pin_ev[b]);
+    for (int b = 0; b < kPinBufs; b++) {
+        drop(c->pin[b], hipHostFree);
+        drop(c->pin_ev[b], hipEventDestroy);
+        c->pin_used[b] = false;
+    }
+    c->pin_ready = false;
+}
+
+// Allocates the ring once; on a failure frees what it made and marks the
+// ring failed (plain copies until kvc_release_workspace clears the mark).
 bool pin_ring(DeviceCtx * c) {
     if (c->pin_ready) return true;
     if (c->pin_failed) return false;
     for (int b = 0; b < kPinBufs; b++) {
-        if (hipHostMalloc(&c->pin[b], kPinBytes, hipHostMallocDefault) != hipSuccess ||
-            hipEventCreateWithFlags(&c->pin_ev[b], hipEventDisableTiming) != hipSuccess) {
-            (void)hipGetLastError();
+        // (KVC_FAULT=pin: the ring fails after its first buffer)
+        if ((b == 1 && forced_fault("pin")) || !made(hipHostMalloc(&c->pin[b], kPinBytes, hipHostMallocDefault)) ||
+            !made(hipEventCreateWithFlags(&c->pin_ev[b], hipEventDisableTiming))) {
+            free_pin_ring(c);
             c->pin_failed = true;
             return false;
         }
@@ -1791,20 +1860,11 @@ void kvc_release_workspace(void) {
         c->arena = nullptr;
         c->arena_cap = 0;
     }
-    if (c->pin_ready) {
-        // (a call that failed may have left a transfer from the ring queued)
-        for (int b = 0; b < kPinBufs; b++)
-            if (c->pin_used[b]) (void)hipEventSynchronize(c->pin_ev[b]);
-        for (int b = 0; b < kPinBufs; b++) {
-            (void)hipHostFree(c->pin[b]);
-            (void)hipEventDestroy(c->pin_ev[b]);
-            c->pin[b] = nullptr;
-            c->pin_ev[b] = nullptr;
-            c->pin_used[b] = false;
-        }
-        c->pin_ready = false;
-    }
+    free_pin_ring(c);
+    c->pin_failed = false;
 }
+
+int kvc_live_objects(void) { return g_live.load(); }
 
 }  // extern "C"
 

@@ -5347,7 +5347,9 @@ void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st)
                                             GE_BLK_LDS * (int)sizeof(float)) == hipSuccess;
         const int pb = ge_panel(g.tc_max);
         size_t lds = pb >= 1 ? (size_t)3 * pb * g.tc_max * sizeof(float) : (size_t)GE_LDS_FLOATS * sizeof(float);
-        if (!ge_lds_ok && lds > 65536) lds = 0;   // (reported by the launch)
+        // without the attribute a launch above 64 KB fails, and run_batch's
+        // error check turns that into -6 (the kernel is never run short of LDS)
+        (void)ge_lds_ok;
         hipLaunchKernelGGL(k_ge_general, dim3(g.n_chunks * g.H, g.L), dim3(512), lds, st,
                            g, w.chunks, w.aug, w.aug_off, Cv, w.gtmp);
     }

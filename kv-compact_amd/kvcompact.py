@@ -324,12 +324,12 @@ def load_product() -> "Lib":
     return Lib(p)
 
 
-# -- llama.cpp state blob compaction (include/kv-compact-state.h) ---------------
+# -- llama.cpp state blob compaction (include/kvc-state.h) ---------------
 LayerFilterFn = ctypes.CFUNCTYPE(_i, _i, _i, _vp)
 
 
 class StateParams(ctypes.Structure):
-    """kvc_state_params (include/kv-compact-state.h)."""
+    """kvc_state_params (include/kvc-state.h)."""
     _fields_ = [
         ("compact_ratio", ctypes.c_float),
         ("n_ref_queries", ctypes.c_int32),
@@ -342,7 +342,7 @@ class StateParams(ctypes.Structure):
 
 
 class StateInfo(ctypes.Structure):
-    """kvc_state_info (include/kv-compact-state.h)."""
+    """kvc_state_info (include/kvc-state.h)."""
     _fields_ = [
         ("n_stream", ctypes.c_uint32),
         ("cell_count", ctypes.c_uint32),

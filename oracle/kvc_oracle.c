@@ -96,6 +96,19 @@ void orc_scores(const float * Q, const float * K, float * S, int n_q, int T,
     for (size_t i = 0; i < (size_t)n_q * T; i++) S[i] *= scale;
 }
 
+/* C[i][j] = sum_l A[i][l] * B[l][j], sequential in l (math.h:70-80), with
+ * B's rows ldb floats apart: the reference's refit target Y_h = A_h V_h over
+ * the head's slice of V (api.cpp:776-781 extracts the slice, then
+ * mat_mul_AB; the same products in the same order). */
+void orc_mat_mul_AB(const float * A, const float * B, float * C, int m, int k, int n, int ldb) {
+    for (int i = 0; i < m; i++)
+        for (int j = 0; j < n; j++) {
+            float acc = 0.0f;
+            for (int l = 0; l < k; l++) acc += A[(size_t)i * k + l] * B[(size_t)l * ldb + j];
+            C[(size_t)i * n + j] = acc;
+        }
+}
+
 /* softmax over rows, math.h:83-100 */
 void orc_softmax_rows(float * x, int m, int n) {
     for (int i = 0; i < m; i++) {

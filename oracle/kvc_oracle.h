@@ -19,7 +19,7 @@
 #include <stddef.h>
 #include <stdint.h>
 #include "../include/kv-compact-api.h"
-#include "../include/kv-compact-state.h"
+#include "../include/kvc-state.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -54,6 +54,7 @@ size_t   orc_quantize_row(const float * src, int type, int n, uint8_t * dst);
 float orc_expf_replica(float x);   /* glibc-expf algorithm restated (see .c) */
 void  orc_scores(const float * Q, const float * K, float * S, int n_q, int T,
                  int d, int stride_q, int stride_k, float scale);
+void  orc_mat_mul_AB(const float * A, const float * B, float * C, int m, int k, int n, int ldb);
 void  orc_softmax_importance(const float * S, float * attn, float * imp,
                              float * exp_out, float * row_sums, int m, int n, int agg);
 void  orc_softmax_rows(float * x, int m, int n);

@@ -46,6 +46,10 @@ void ref_mat_mul_ABt(const float * A, const float * B, float * C, int m, int n, 
     mat_mul_ABt(A, B, C, m, n, k);
 }
 
+void ref_mat_mul_AB(const float * A, const float * B, float * C, int m, int k, int n) {
+    mat_mul_AB(A, B, C, m, k, n);
+}
+
 size_t ref_convert_from_f32(const float * src, int type, uint8_t * dst, int n) {
     return convert_from_f32(src, type, dst, n);
 }

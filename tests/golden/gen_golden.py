@@ -6,6 +6,7 @@ Run in the container that holds the reference checkout, after
     python tests/golden/gen_golden.py          (everything)
     python tests/golden/gen_golden.py state    (the state blob cases only)
     python tests/golden/gen_golden.py replay   (the wrapper call-sequence replay only)
+    python tests/golden/gen_golden.py matmul   (the accelerator GEMMs only)
     python tests/golden/gen_golden.py case NAME   (one case of the catalogue)
 
 Inputs are regenerated from seeds by tests/kvc_data.py (integer-only
@@ -26,7 +27,7 @@ import numpy as np
 HERE = Path(__file__).resolve().parent
 sys.path.insert(0, str(HERE.parent))
 
-from kvc_data import CASES, kv_cache, make_case, normal, uniform  # noqa: E402
+from kvc_data import CASES, kv_cache, make_case, matmul_inputs, normal, uniform  # noqa: E402
 from kvc_harness import REF_HARNESS_SO, kc, load_ref, run_case  # noqa: E402
 
 
@@ -111,9 +112,36 @@ def write_replay_fixtures():
     print("wrote", len(br.REPLAY_CASES), "replay cases")
 
 
+# The reference's two accelerator GEMMs, computed by its CPU path: the
+# scores mat_mul_ABt followed by the scale (api.cpp:619-627) for
+# kv_compact_hip_mat_mul_ABt_scaled, and the refit target's per-head slice of
+# V followed by mat_mul_AB (api.cpp:776-781) for
+# kv_compact_hip_refit_target_all_heads (inputs: kvc_data.matmul_inputs).
+def write_matmul_fixtures():
+    h = ctypes.CDLL(str(REF_HARNESS_SO))
+    fp, ci = ctypes.c_void_p, ctypes.c_int
+    h.ref_mat_mul_ABt.argtypes = [fp, fp, fp, ci, ci, ci]
+    h.ref_mat_mul_AB.argtypes = [fp, fp, fp, ci, ci, ci]
+    (A, B, scale), (W, Vall, H, dv) = matmul_inputs()
+    m, k = A.shape
+    n = B.shape[0]
+    C = np.zeros((m, n), np.float32)
+    h.ref_mat_mul_ABt(A.ctypes.data, B.ctypes.data, C.ctypes.data, m, n, k)
+    C = (C * np.float32(scale)).astype(np.float32)
+    nq, T = W.shape[1], W.shape[2]
+    Y = np.zeros((H, nq, dv), np.float32)
+    for hh in range(H):
+        vh = np.ascontiguousarray(Vall[:, hh * dv:(hh + 1) * dv])
+        W_h = np.ascontiguousarray(W[hh])
+        h.ref_mat_mul_AB(W_h.ctypes.data, vh.ctypes.data, Y[hh].ctypes.data, nq, T, dv)
+    np.savez_compressed(HERE / "matmul.npz", abt_C=C, ab_Y=Y,
+                        in_checksum=np.uint64(checksum(A, B, W, Vall)))
+
+
 def main():
-    if len(sys.argv) > 1 and sys.argv[1] in ("state", "replay"):
-        (write_state_fixtures if sys.argv[1] == "state" else write_replay_fixtures)()
+    if len(sys.argv) > 1 and sys.argv[1] in ("state", "replay", "matmul"):
+        {"state": write_state_fixtures, "replay": write_replay_fixtures,
+         "matmul": write_matmul_fixtures}[sys.argv[1]]()
         return
     ref = load_ref()
     if ref is None:
@@ -199,6 +227,7 @@ def main():
     np.savez_compressed(HERE / "blocks.npz", **blocks)
     write_state_fixtures()
     write_replay_fixtures()
+    write_matmul_fixtures()
     print("wrote", len(out), "cases,", len(QUANT_CASES), "quantized cases, multi-round and blocks")
 
 

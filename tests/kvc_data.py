@@ -35,6 +35,23 @@ def normal(seed: int, shape) -> np.ndarray:
     return (s * 0.8660254037844386).astype(np.float32).reshape(shape)
 
 
+# Inputs of the accelerator GEMM fixtures (tests/golden/matmul.npz): the
+# reference's scores product mat_mul_ABt then the scale, and its refit target
+# mat_mul_AB over each head's slice of V. Shapes no tile divides.
+MATMUL_ABT = (37, 301, 72, 0.117851130)        # m, n, k, scale
+MATMUL_AB = (29, 333, 3, 40)                    # n_q, T, H, d_v
+
+
+def matmul_inputs():
+    """((A, B, scale), (W [H][n_q][T], V_all [T][H*d_v], H, d_v))."""
+    m, n, k, scale = MATMUL_ABT
+    A = normal(901, (m, k)); B = normal(902, (n, k))
+    nq, T, H, dv = MATMUL_AB
+    W = np.abs(normal(903, (H, nq, T))).astype(np.float32)
+    Vall = normal(904, (T, H * dv))
+    return (A, B, scale), (W, Vall, H, dv)
+
+
 def kv_cache(T: int, H: int, d: int, seed: int, outliers: int = 0, channel_scale: bool = False):
     """K, V [T x H*d] float32. outliers: that many key/value channels x8.
     channel_scale: per-channel key scale in [0.25, 4) (log-uniform-like)."""

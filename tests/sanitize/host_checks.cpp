@@ -13,7 +13,7 @@
 
 #include "../../include/kv-compact-api.h"
 #include "../../include/kv-compact-device.h"
-#include "../../include/kv-compact-state.h"
+#include "../../include/kvc-state.h"
 
 static int failures = 0;
 #define CHECK(c)                                                        \

@@ -92,3 +92,74 @@ def test_forced_fault_surfaces_and_clears(gpu, kind):
     b = orc.compact(K, V, Q, T, 16, H, d, d, orc.params(target_ratio=0.2))
     assert np.array_equal(a.indices, b.indices)
     assert np.array_equal(a.C_v.view(np.uint32), b.C_v.view(np.uint32))
+
+
+def _live(gpu):
+    gpu.dll.kvc_live_objects.restype = ctypes.c_int
+    return gpu.dll.kvc_live_objects()
+
+
+def test_pinned_ring_failure_frees_its_buffers(gpu):
+    """KVC_FAULT=pin fails the pinned ring after its first buffer: the host
+    call falls back to plain copies with the same results, the buffer made
+    is freed, and once kvc_release_workspace clears the mark the ring is
+    allocated again."""
+    orc = load_oracle()
+    T, H, d = 1536, 2, 64
+    K, V = kv_cache(T, H, d, 302, channel_scale=True)
+    Q = snapkv_queries(K, 16, 302)
+    ref = orc.compact(K, V, Q, T, 16, H, d, d, orc.params(target_ratio=0.2))
+    gpu.dll.kvc_release_workspace()
+    base = _live(gpu)
+    try:
+        os.environ["KVC_PIN_BYTES"] = "4096"   # the inputs take many pieces
+        os.environ["KVC_FAULT"] = "pin"
+        for _ in range(3):
+            print("[fault] pin kv_compact", flush=True)
+            a = gpu.compact(K, V, Q, T, 16, H, d, d, gpu.params(target_ratio=0.2))
+            assert np.array_equal(a.indices, ref.indices)
+            assert np.array_equal(a.C_v.view(np.uint32), ref.C_v.view(np.uint32))
+            assert _live(gpu) == base, "a failed ring set-up left objects behind"
+        os.environ.pop("KVC_FAULT")
+        gpu.dll.kvc_release_workspace()
+        a = gpu.compact(K, V, Q, T, 16, H, d, d, gpu.params(target_ratio=0.2))
+        assert np.array_equal(a.C_v.view(np.uint32), ref.C_v.view(np.uint32))
+        assert _live(gpu) == base + 16, "the ring (8 buffers, 8 events) was not set up again"
+    finally:
+        os.environ.pop("KVC_FAULT", None)
+        os.environ.pop("KVC_PIN_BYTES", None)
+
+
+_INIT_CHILD = r"""
+import ctypes, os, sys
+sys.path.insert(0, sys.argv[1])
+import kvcompact as kc
+lib = kc.load_product()
+lib.dll.kvc_live_objects.restype = ctypes.c_int
+os.environ["KVC_FAULT"] = "init"
+for i in range(5):
+    assert lib.dll.kv_compact_hip_available() == 0, "set-up succeeded under KVC_FAULT=init"
+    assert lib.dll.kvc_live_objects() == 0, ("objects left by a failed set-up", lib.dll.kvc_live_objects())
+os.environ.pop("KVC_FAULT")
+assert lib.dll.kv_compact_hip_available() == 1
+n = lib.dll.kvc_live_objects()
+assert n > 0
+assert lib.dll.kv_compact_hip_available() == 1 and lib.dll.kvc_live_objects() == n
+print("init-fault child ok", n, flush=True)
+"""
+
+
+def test_device_setup_failure_leaves_nothing(gpu):
+    """KVC_FAULT=init fails the per-device set-up after its streams and first
+    events are made: the call reports no device, every object it made is
+    destroyed (the live count stays 0), and the set-up succeeds once the
+    fault is cleared. The set-up happens once per process, so this runs in a
+    child process of its own."""
+    import subprocess
+    import sys
+    from pathlib import Path
+    pkg = Path(kc.__file__).resolve().parent
+    print("[fault] init child process", flush=True)
+    r = subprocess.run([sys.executable, "-c", _INIT_CHILD, str(pkg)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, (r.stdout[-2000:], r.stderr[-2000:])
+    assert "init-fault child ok" in r.stdout

@@ -148,6 +148,60 @@ def test_accel_plugin_scores(gpu, orc):
         assert np.array_equal(bits(outs[h]), bits(ref)), h
 
 
+def _accel_fixture():
+    from pathlib import Path
+    from kvc_data import matmul_inputs
+    return np.load(Path(__file__).resolve().parent / "golden" / "matmul.npz"), matmul_inputs()
+
+
+def test_accel_plugin_mat_mul_ABt_scaled(gpu, orc):
+    """kv_compact_hip_mat_mul_ABt_scaled (reference accel.h:24, hip:223-257)
+    equals the CPU path's mat_mul_ABt followed by the scale, bit for bit: the
+    reference's fixture and the oracle's sequential product."""
+    g, ((A, B, scale), _) = _accel_fixture()
+    m, k = A.shape
+    n = B.shape[0]
+    f = gpu.dll.kv_compact_hip_mat_mul_ABt_scaled
+    f.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 3 + [ctypes.c_float]
+    C = np.full((m, n), np.nan, np.float32)
+    assert f(A.ctypes.data, B.ctypes.data, C.ctypes.data, m, n, k, float(np.float32(scale))) == 0
+    assert np.array_equal(bits(C), bits(g["abt_C"]))
+    # and an unscaled call at another shape against the oracle
+    from kvc_data import normal
+    A2, B2 = normal(905, (64, 130)), normal(906, (257, 130))
+    C2 = np.zeros((64, 257), np.float32)
+    assert f(A2.ctypes.data, B2.ctypes.data, C2.ctypes.data, 64, 257, 130, 1.0) == 0
+    R2 = np.zeros_like(C2)
+    sc = orc.dll.orc_scores
+    sc.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 5 + [ctypes.c_float]
+    sc(A2.ctypes.data, B2.ctypes.data, R2.ctypes.data, 64, 257, 130, 130, 130, 1.0)
+    assert np.array_equal(bits(C2), bits(R2))
+
+
+def test_accel_plugin_refit_target(gpu, orc):
+    """kv_compact_hip_refit_target_all_heads (reference accel.h:50,
+    hip:372-462; called by api.cpp:762-775) equals the CPU path's per-head
+    mat_mul_AB over V's head slice, bit for bit: the reference's fixture and
+    the oracle's sequential product."""
+    g, (_, (W, Vall, H, dv)) = _accel_fixture()
+    nq, T = W.shape[1], W.shape[2]
+    Ws = [np.ascontiguousarray(W[h]) for h in range(H)]
+    Ys = [np.full((nq, dv), np.nan, np.float32) for _ in range(H)]
+    P = ctypes.POINTER(ctypes.c_float)
+    wa = (P * H)(*[w.ctypes.data_as(P) for w in Ws])
+    ya = (P * H)(*[y.ctypes.data_as(P) for y in Ys])
+    f = gpu.dll.kv_compact_hip_refit_target_all_heads
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int] * 4
+    assert f(ctypes.cast(wa, ctypes.c_void_p), Vall.ctypes.data, ctypes.cast(ya, ctypes.c_void_p), nq, T, H, dv) == 0
+    mm = orc.dll.orc_mat_mul_AB
+    mm.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int] * 4
+    for h in range(H):
+        assert np.array_equal(bits(Ys[h]), bits(g["ab_Y"][h])), h
+        R = np.zeros((nq, dv), np.float32)
+        mm(Ws[h].ctypes.data, Vall[:, h * dv:].ctypes.data, R.ctypes.data, nq, T, dv, H * dv)
+        assert np.array_equal(bits(Ys[h]), bits(R)), h
+
+
 def test_device_batch_api(gpu, orc):
     """Three layers in one device-resident call equal three oracle calls."""
     import hiprt

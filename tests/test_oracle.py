@@ -438,3 +438,31 @@ def test_numpy_quantizers_match_oracle(orc):
             a = quantize_rows(x, typ)
             b = np.stack([orc.quantize_row(x[i], typ) for i in range(x.shape[0])])
             assert np.array_equal(a, b), (typ, s)
+
+
+def test_accel_gemms_match_reference_fixture(orc):
+    """The accelerator exports' CPU counterparts: orc_scores (one head) is the
+    reference's mat_mul_ABt then the scale, orc_mat_mul_AB over a head's slice
+    of V is its extract + mat_mul_AB, bit for bit with the fixture written by
+    the compiled reference; and both are within fp32 rounding of an fp64
+    product (a transposed operand or a dropped term fails that)."""
+    g = np.load(GOLD / "matmul.npz")
+    from kvc_data import matmul_inputs
+    (A, B, scale), (W, Vall, H, dv) = matmul_inputs()
+    assert int(g["in_checksum"]) == checksum(A, B, W, Vall)
+    m, k = A.shape
+    n = B.shape[0]
+    C = np.zeros((m, n), np.float32)
+    _o("orc_scores", fp, fp, fp, ci, ci, ci, ci, ci, cf)(A.ctypes.data, B.ctypes.data, C.ctypes.data, m, n, k, k, k,
+                                                         float(np.float32(scale)))
+    assert np.array_equal(bits(C), bits(g["abt_C"]))
+    exact = (A.astype(np.float64) @ B.astype(np.float64).T) * np.float64(np.float32(scale))
+    assert np.allclose(C, exact, rtol=0, atol=1e-4 * np.abs(exact).max())
+    nq, T = W.shape[1], W.shape[2]
+    f = _o("orc_mat_mul_AB", fp, fp, fp, ci, ci, ci, ci)
+    for h in range(H):
+        Y = np.zeros((nq, dv), np.float32)
+        f(np.ascontiguousarray(W[h]).ctypes.data, Vall[:, h * dv:].ctypes.data, Y.ctypes.data, nq, T, dv, H * dv)
+        assert np.array_equal(bits(Y), bits(g["ab_Y"][h])), h
+        exact = W[h].astype(np.float64) @ Vall[:, h * dv:(h + 1) * dv].astype(np.float64)
+        assert np.allclose(Y, exact, rtol=0, atol=1e-4 * np.abs(exact).max()), h
