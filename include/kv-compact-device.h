@@ -94,8 +94,9 @@ int kvc_compact_quantized_device(const uint8_t * K_quant, const uint8_t * V_quan
  * 7 LU elimination with partial pivoting, 8 forward + back substitution,
  * 9 refinement rounds, 10 quality statistics, and for the quantized entries
  * 11 dequantization of the K and V rows, 12 requantization of the kept K
- * rows and refitted V rows (0 after an unquantized call). Returns the number
- * written. */
+ * rows and refitted V rows (0 after an unquantized call). After a call that
+ * took the fused scoring kernel (KVC_FUSED=1), stage 0 is that kernel and
+ * stages 1 and 2 read 0. Returns the number written. */
 int kvc_stage_times(float * out_ms, int n);
 
 /* Release the library's cached device workspace of the current device, and

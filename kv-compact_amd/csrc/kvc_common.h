@@ -89,6 +89,7 @@ struct Work {
     int   * refine_active; // [L][n_chunks] 1 while the unit's refinement rounds continue
     int   * lu_redo;  // [L][n_chunks][H] 1: the system's LU is redone with masked updates
     ChunkDesc * chunks;  // [n_chunks + 2]; then all T keys, then the kept keys (statistics)
+    float * Qt;       // [L][H][dk][32] transposed reference queries (the fused scoring path), or nullptr
 };
 
 // Diversity selection scratch (api.cpp:175-233). One unit = (layer, chunk).

@@ -501,6 +501,18 @@ void make_plan(int T, int n_q, bool q_given, const kv_compact_params & p, Plan &
     pl.chunks.push_back(whole);
 }
 
+// KVC_FUSED=1 (read at every call) runs the scoring, chunk softmax,
+// importance and refit target as one kernel whose scores never leave the
+// chip (k_score_attend), where the call allows it; same results. It is not
+// the default: holding a chunk's scores in registers leaves one block per CU,
+// and at that occupancy the kernel takes longer (about 14.9 ms at 100k
+// tokens x 32 layers) than the separate kernels with their HBM round trip
+// (scores 5.4 + softmax 2.0 ms, the refit target beside the selection).
+bool fused_enabled() {
+    const char * e = getenv("KVC_FUSED");
+    return e && e[0] == '1';
+}
+
 // Options this library implements; everything else is refused with -5
 // rather than computed differently.
 int check_supported(const kv_compact_params & p, int d_v) {
@@ -582,6 +594,7 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     ww.cand = cv.take<int>(L * nc * (size_t)pl.Tc_max);
     ww.flags = cv.take<unsigned char>(L * nc * (size_t)pl.Tc_max);
     ww.chunks = cv.take<ChunkDesc>(pl.chunks.size());
+    ww.Qt = cv.take<float>(L * H * (size_t)io.dk * 32);
     ww.status = cv.take<int>(1);
     ww.refine_active = cv.take<int>(L * nc);
     ww.lu_redo = cv.take<int>(L * nc * H);
@@ -738,19 +751,34 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     launch_fill_int(w.status, 0, 1, st);
     hipEvent_t * ev = ctx->ev;
     (void)hipEventRecord(ev[0], st);
-    // 1. scores for every (layer, chunk, head)
-    launch_scores(g, w.chunks, pl.n_chunks, pl.Tc_max, io.K, io.Q, w.S, io.H, pl.nq_max,
-                  (long long)io.H * pl.nq_max * io.T, (long long)pl.nq_max * io.T, io.T, pl.qmode, st,
-                  nullptr, nullptr, w.smax);
-    (void)hipEventRecord(ev[ST_SCORES + 1], st);
-    // 2. chunk softmax + per-head importance
-    launch_chunk_softmax(g, w, st);
-    (void)hipEventRecord(ev[ST_SOFTMAX + 1], st);
+    // Scoring, chunk softmax, importance and the refit target in one kernel
+    // whose scores never leave the chip, where the call allows it (the
+    // options that read the scores or weights again later keep them in HBM)
+    const bool fused = p.skip_beta && !p.use_omp && !p.use_sensitivity && p.refine_rounds <= 0 && fused_enabled() &&
+                       score_attend_ok(g, io.K, io.V, io.Q, pl.Tc_max, pl.nq_max, pl.qmode);
+    if (fused) {
+        // the statistics' original scores are rows of S (heads < 4) when they
+        // share the main query set
+        launch_score_attend(g, w, io.K, io.V, io.Q, pl.qmode == pl.stats_qmode ? w.S : nullptr,
+                            std::min(io.H, 4), st);
+        (void)hipEventRecord(ev[ST_SCORES + 1], st);
+        (void)hipEventRecord(ev[ST_SOFTMAX + 1], st);
+    } else {
+        // 1. scores for every (layer, chunk, head)
+        launch_scores(g, w.chunks, pl.n_chunks, pl.Tc_max, io.K, io.Q, w.S, io.H, pl.nq_max,
+                      (long long)io.H * pl.nq_max * io.T, (long long)pl.nq_max * io.T, io.T, pl.qmode, st,
+                      nullptr, nullptr, w.smax);
+        (void)hipEventRecord(ev[ST_SCORES + 1], st);
+        // 2. chunk softmax + per-head importance
+        launch_chunk_softmax(g, w, st);
+        (void)hipEventRecord(ev[ST_SOFTMAX + 1], st);
+    }
     // 3. refit target Y = A V. Only the normal equations read Y, so it runs
     //    on the second stream beside the selection (whose greedy pass is one
     //    short serial chain per unit and leaves the chip mostly idle).
-    const bool refit_fork = ctx->stream2 != nullptr;
-    if (refit_fork) {
+    const bool refit_fork = !fused && ctx->stream2 != nullptr;
+    if (fused) {
+    } else if (refit_fork) {
         if (hipEventRecord(ctx->refit_fork, st) != hipSuccess ||
             hipStreamWaitEvent(ctx->stream2, ctx->refit_fork, 0) != hipSuccess) return KV_COMPACT_E_DEVICE;
         (void)hipEventRecord(ctx->refit_t[0], ctx->stream2);
@@ -808,8 +836,16 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     int rc = fit_beta();
     if (rc) return rc;
     (void)hipEventRecord(ev[ST_BETA + 1], st);
-    // 6. X = softmax(S[:, sel] + beta)
-    launch_ls_softmax(g, w, io.beta, st);
+    // 6. X = softmax(S[:, sel] + beta); without S in HBM, the kept keys'
+    //    scores are computed again (the same sums) into the A buffer
+    if (fused) {
+        launch_scores(g, w.chunks + pl.n_chunks + 1, 1, pl.t_total, io.K, io.Q, w.A, io.H, pl.nq_max,
+                      (long long)io.H * pl.nq_max * pl.t_total, (long long)pl.nq_max * pl.t_total, pl.t_total,
+                      pl.qmode, st, w.sel, nullptr);
+        launch_ls_softmax(g, w, io.beta, st, w.A);
+    } else {
+        launch_ls_softmax(g, w, io.beta, st);
+    }
     (void)hipEventRecord(ev[ST_LS_SOFTMAX + 1], st);
     // The original-attention statistics read S and V only and rewrite the rows
     // of S they use; without refinement rounds the main path reads S no more,
@@ -875,6 +911,9 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         ctx->stage_ms[i] = ms;
     }
     ctx->stage_ms[ST_DEQUANT] = ctx->stage_ms[ST_REQUANT] = 0.0f;
+    // (the fused kernel's time is the scores stage's; the two stages it
+    // absorbs read 0)
+    if (fused) ctx->stage_ms[ST_SOFTMAX] = ctx->stage_ms[ST_REFIT] = 0.0f;
     if (refit_fork) {
         // the refit target's own time on the second stream (it overlaps the selection)
         float ms = 0.0f;

@@ -19,7 +19,18 @@ void launch_fill_int(int * p, int v, long long n, hipStream_t st);
 // fill kernels stand in for hipMemsetAsync (a caller may capture the call in a graph)
 void launch_fill_f32(float * p, float v, long long n, hipStream_t st);
 void launch_refine_step(const Geom & g, const Work & w, hipStream_t st);
-void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st);
+// Ssel (optional): the kept keys' scores [L][H][nq_max][t_total] in place of S[:, sel]
+void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st,
+                       const float * Ssel = nullptr);
+// The scoring, chunk softmax, importance and refit target of a call in one
+// kernel whose scores stay on chip (k_score_attend): chunks of at most 1280
+// keys, at most 32 reference queries shared by every chunk, d_v = 128, fp32
+// K and V with 16-byte aligned rows. S (optional) receives the raw scores of
+// the heads h < mh (and w.smax their tile maxima) for the statistics.
+bool score_attend_ok(const Geom & g, const float * K, const float * V, const float * Q, int Tc_max, int nq_max,
+                     int qmode);
+void launch_score_attend(const Geom & g, const Work & w, const float * K, const float * V, const float * Q,
+                         float * S, int mh, hipStream_t st);
 void launch_gather_exp(const Geom & g, const Work & w, hipStream_t st);
 void launch_nnls_lh(const Geom & g, const Work & w, float * wout, int max_iter, int * status, hipStream_t st);
 void launch_beta_log(float * wb, long long n, hipStream_t st);

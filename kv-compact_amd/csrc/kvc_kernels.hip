@@ -60,6 +60,33 @@ __device__ __forceinline__ float expf_ref(float x, const uint64_t * tab = c_exp2
     return (float)(y * s);
 }
 
+// The same value as expf_ref for every x, computed without branches: the
+// general path always, then the two range results selected (for x below
+// the lower or above the upper limit the general path's value is unused;
+// NaN takes the general path in both forms).
+__device__ __forceinline__ float expf_ref_sel(float x, const uint64_t * tab) {
+    const double N = 32.0;
+    const double inv_ln2_n = 0x1.71547652b82fep+0 * N;
+    const double shift = 0x1.8p+52;
+    const double c0 = 0x1.c6af84b912394p-5 / N / N / N;
+    const double c1 = 0x1.ebfce50fac4f3p-3 / N / N;
+    const double c2 = 0x1.62e42ff0c52d6p-1 / N;
+    double xd = (double)x;
+    double z = inv_ln2_n * xd;
+    double kd = z + shift;
+    uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= shift;
+    double r = __builtin_fma(inv_ln2_n, xd, -kd);
+    uint64_t tb = tab[ki % 32] + (ki << 47);
+    double sc = __longlong_as_double((long long)tb);
+    double p = __builtin_fma(c0, r, c1);
+    double r2 = r * r;
+    double y = __builtin_fma(c2, r, 1.0);
+    y = __builtin_fma(p, r2, y);
+    const float v = (float)(y * sc);
+    return x < -0x1.9fe368p6f ? 0.0f : (x > 0x1.62e42ep6f ? __int_as_float(0x7f800000) : v);
+}
+
 // ---------------------------------------------------------------------------
 // logf as glibc computes it on x86-64 (FMA variant of the ARM optimized-
 // routines method): x = 2^k * z with z in [0x1.66p-1, 0x1.66p0), 16
@@ -922,6 +949,359 @@ k_refit_target_any(Geom g, const ChunkDesc * __restrict__ chunks, const float * 
                             ev, c.Tc, g.dv,
                             Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv, g.dv,
                             g.vc, layer, c.start, h * g.dv);
+}
+
+// ---------------------------------------------------------------------------
+// Scoring, chunk softmax, per-key importance and the refit target in one pass
+// per (layer, chunk, head), the chunk's scores held in registers so that
+// neither the score matrix nor the softmax weights go to HBM (math.h:44-54,
+// 142-248; api.cpp:618-628, 754-783). Thread t owns keys 2t and 2t + 1 of the
+// chunk with all FA_ROWS query rows (64 values), FA_THREADS threads cover
+// FA_KEYS keys; the registers this takes leave one block per CU. Every value
+// is the reference's:
+//   1. s = (sum_d q[d] k[d]) * inv_sqrt_dk, d ascending (the query columns
+//      come from Qt [L][H][d_k][FA_ROWS], uniform over the block: scalar
+//      operands; key rows in 64-byte segments), the same sums k_scores forms;
+//   2. row maxima in the reference's scan semantics (largest non-NaN value,
+//      or row[0] when it is NaN), from wave maxima of the order keys; each
+//      wave's maxima are also the 128-key tile maxima the statistics' row
+//      softmax reads (tmax, as k_scores writes them);
+//   3. e = expf(s - max); row sums in key order: 64-key tiles of e go through
+//      LDS and one thread per row adds them in order; inv = 1/(sum + 1e-12f);
+//   4. a = e * inv; importance per key over the rows in row order (max, sum
+//      of squares then sqrtf(acc * inv_m), or mean), as k_softmax_importance;
+//   5. Y[i][v] = sum_j a[i][j] V[j][v], j ascending: 64-key tiles of a
+//      (key-major) and V through LDS, double-buffered (the owners of the next
+//      tile's keys and waves 8-9 fill it while threads 0..511, 2 rows x 4
+//      columns each, sum this one; d_v = 128).
+// S (optional): the raw scores of the heads h < mh are stored for the
+// statistics (they read rows of S); other heads store nothing.
+// grid (n_chunks * H, L); FA_THREADS threads.
+// ---------------------------------------------------------------------------
+constexpr int FA_THREADS = 640, FA_ROWS = 32, FA_KEYS = 2 * FA_THREADS, FA_TILE = 64;
+constexpr int FA_WAVES = FA_THREADS / 64;
+
+struct FaShared {
+    union {
+        float eb[2][FA_ROWS][FA_TILE + 1];   // e tiles for the ordered row sums
+        struct {
+            float at[2][FA_TILE][FA_ROWS];   // a tiles, key-major
+            float vt[2][FA_TILE][128];       // V tiles
+        } y;
+    } u;
+    unsigned red[FA_WAVES][FA_ROWS];         // per-wave row maxima (order keys)
+    float rmax[FA_ROWS], rinv[FA_ROWS], r0[FA_ROWS];
+    uint64_t etab[32];
+};
+
+__global__ void __launch_bounds__(FA_THREADS)
+k_score_attend(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ K,
+               const float * __restrict__ Qt, const float * __restrict__ V, float * __restrict__ S, int mh,
+               unsigned * __restrict__ tmax, float * __restrict__ imp, float * __restrict__ ainv,
+               float * __restrict__ Y) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const ChunkDesc c = chunks[c_idx];
+    const int n = c.Tc, nq = c.nq;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    __shared__ __align__(16) FaShared sh;
+    if (tid < 32) sh.etab[tid] = c_exp2_tab[tid];   // visible after the barriers below
+    const long long ek = (long long)g.H * g.dk, ev = (long long)g.H * g.dv;
+    const int j0 = 2 * tid;
+    const bool ok0 = j0 < n, ok1 = j0 + 1 < n;
+    // 1. scores (loads at clamped keys; the sums of keys past n are not used)
+    const float * Kl = K + layer * g.ldK + (long long)c.start * ek + (long long)h * g.dk;
+    const float4 * kp0 = reinterpret_cast<const float4 *>(Kl + (long long)min(j0, n - 1) * ek);
+    const float4 * kp1 = reinterpret_cast<const float4 *>(Kl + (long long)min(j0 + 1, n - 1) * ek);
+    const float * qt = Qt + ((long long)layer * g.H + h) * g.dk * FA_ROWS;
+    float s0[FA_ROWS], s1[FA_ROWS];
+#pragma unroll
+    for (int i = 0; i < FA_ROWS; i++) s0[i] = s1[i] = 0.0f;
+    // Each key row in 64-byte segments (16 dimensions, one cache line):
+    // a thread's two segments sit in registers, and the next segment's first
+    // half is loaded once this one's first eight dimensions are summed (its
+    // second half after the rest), so the loads overlap the sums and every
+    // line is read whole. Query column d: uniform scalar operands.
+    const int nst = g.dk >> 4;   // (the host sends d_k % 16 == 0)
+    float4 A[4], B[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        A[k] = kp0[k];
+        B[k] = kp1[k];
+    }
+    for (int st = 0; st < nst; st++) {
+        const int nx = min(st + 1, nst - 1);
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+#pragma unroll
+            for (int dd = 0; dd < 8; dd++) {
+                const int d = 16 * st + 8 * half + dd;
+                const float a = (dd & 4) ? ((dd & 2) ? ((dd & 1) ? A[2 * half + 1].w : A[2 * half + 1].z)
+                                                      : ((dd & 1) ? A[2 * half + 1].y : A[2 * half + 1].x))
+                                         : ((dd & 2) ? ((dd & 1) ? A[2 * half].w : A[2 * half].z)
+                                                      : ((dd & 1) ? A[2 * half].y : A[2 * half].x));
+                const float b = (dd & 4) ? ((dd & 2) ? ((dd & 1) ? B[2 * half + 1].w : B[2 * half + 1].z)
+                                                      : ((dd & 1) ? B[2 * half + 1].y : B[2 * half + 1].x))
+                                         : ((dd & 2) ? ((dd & 1) ? B[2 * half].w : B[2 * half].z)
+                                                      : ((dd & 1) ? B[2 * half].y : B[2 * half].x));
+                const float * qd = qt + (long long)d * FA_ROWS;
+#pragma unroll
+                for (int i = 0; i < FA_ROWS; i++) {
+                    const float q = qd[i];
+                    s0[i] = s0[i] + q * a;
+                    s1[i] = s1[i] + q * b;
+                }
+            }
+            // this half's eight dimensions are summed: the next segment's
+            // same half into their registers
+            A[2 * half] = kp0[4 * nx + 2 * half];
+            A[2 * half + 1] = kp0[4 * nx + 2 * half + 1];
+            B[2 * half] = kp1[4 * nx + 2 * half];
+            B[2 * half + 1] = kp1[4 * nx + 2 * half + 1];
+            asm volatile("" ::: "memory");   // keeps the loads here, ahead of the next sums
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < FA_ROWS; i++) {
+        s0[i] = s0[i] * g.inv_sqrt_dk;
+        s1[i] = s1[i] * g.inv_sqrt_dk;
+    }
+    if (S && h < mh) {
+        float * Sh = S + layer * lS(g) + h * hS(g) + c.start;
+#pragma unroll
+        for (int i = 0; i < FA_ROWS; i++) {
+            if (i < nq) {
+                if (ok0) Sh[(long long)i * g.T + j0] = s0[i];
+                if (ok1) Sh[(long long)i * g.T + j0 + 1] = s1[i];
+            }
+        }
+    }
+    if (tid == 0) {
+#pragma unroll
+        for (int i = 0; i < FA_ROWS; i++) sh.r0[i] = s0[i];
+    }
+    // 2. row maxima: wave maxima of the order keys of the largest non-NaN
+    //    score (fmaxf skips NaN), then over the waves, then row[0]'s rule
+    unsigned mine = 0u;
+#pragma unroll
+    for (int i = 0; i < FA_ROWS; i++) {
+        float m = -INFINITY;
+        if (ok0) m = fmaxf(m, s0[i]);
+        if (ok1) m = fmaxf(m, s1[i]);
+        const unsigned k = dpp_reduce_u32<true>(score_key(m));
+        mine = lane == i ? k : mine;
+    }
+    if (lane < FA_ROWS) {
+        sh.red[wv][lane] = mine;
+        // this wave's 128 keys are one scoring tile of the statistics' row softmax
+        if (tmax && h < mh && lane < nq && 128 * wv < n) {
+            const long long nt = (g.Tc_max + SC_KEYS - 1) / SC_KEYS;
+            tmax[((((long long)layer * g.H + h) * g.nq_max + lane) * g.n_chunks + c_idx) * nt + wv] = mine;
+        }
+    }
+    __syncthreads();
+    if (tid < FA_ROWS) {
+        unsigned k = sh.red[0][tid];
+        for (int w = 1; w < FA_WAVES; w++) k = max(k, sh.red[w][tid]);
+        const float mm = __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+        const float a0 = sh.r0[tid];
+        sh.rmax[tid] = (a0 != a0) ? a0 : ((mm > a0) ? mm : a0);
+    }
+    __syncthreads();
+    // 3. exponentials (rows past nq and keys past n hold 0)
+#pragma unroll
+    for (int i = 0; i < FA_ROWS; i++) {
+        const float m = sh.rmax[i];
+        const float e0 = expf_ref_sel(s0[i] - m, sh.etab), e1 = expf_ref_sel(s1[i] - m, sh.etab);
+        s0[i] = (ok0 && i < nq) ? e0 : 0.0f;
+        s1[i] = (ok1 && i < nq) ? e1 : 0.0f;
+    }
+    //    the row sums in key order: tile p (keys 64 p ..) is written by
+    //    threads 32 p .. 32 p + 31 while thread i < nq adds tile p - 1
+    const int ntile = (n + FA_TILE - 1) / FA_TILE;
+    auto put_e = [&](int p) {
+        const int kk = j0 - FA_TILE * p;
+        if (kk >= 0 && kk < FA_TILE) {
+#pragma unroll
+            for (int i = 0; i < FA_ROWS; i++) {
+                sh.u.eb[p & 1][i][kk] = s0[i];
+                sh.u.eb[p & 1][i][kk + 1] = s1[i];
+            }
+        }
+    };
+    float sum = 0.0f;
+    put_e(0);
+    __syncthreads();
+    for (int p = 0; p < ntile; p++) {
+        if (p + 1 < ntile) put_e(p + 1);
+        if (tid < nq) {
+            const int jn = min(FA_TILE, n - FA_TILE * p);
+            const float * er = &sh.u.eb[p & 1][tid][0];
+            int j = 0;
+            for (; j + 16 <= jn; j += 16) {   // 16 reads in flight, then the adds in order
+                float e[16];
+#pragma unroll
+                for (int k = 0; k < 16; k++) e[k] = er[j + k];
+#pragma unroll
+                for (int k = 0; k < 16; k++) sum += e[k];
+            }
+            for (; j < jn; j++) sum += er[j];
+        }
+        __syncthreads();
+    }
+    if (tid < nq) {
+        const float iv = 1.0f / (sum + 1e-12f);
+        sh.rinv[tid] = iv;
+        ainv[(((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max + tid] = iv;
+    }
+    __syncthreads();
+    // 4. weights and importance, rows in order
+    {
+        const float inv_m = 1.0f / (float)nq;
+        float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < FA_ROWS; i++) {
+            if (i < nq) {
+                const float iv = sh.rinv[i];
+                const float a0 = s0[i] * iv, a1 = s1[i] * iv;
+                s0[i] = a0;
+                s1[i] = a1;
+                if (g.score_method == 0) {
+                    if (a0 > acc0) acc0 = a0;
+                    if (a1 > acc1) acc1 = a1;
+                } else if (g.score_method == 1) {
+                    acc0 += a0 * a0;
+                    acc1 += a1 * a1;
+                } else {
+                    acc0 += a0;
+                    acc1 += a1;
+                }
+            }
+        }
+        if (g.score_method == 1) {
+            acc0 = sqrtf(acc0 * inv_m);
+            acc1 = sqrtf(acc1 * inv_m);
+        } else if (g.score_method == 2) {
+            acc0 *= inv_m;
+            acc1 *= inv_m;
+        }
+        float * imph = imp + ((long long)layer * g.H + h) * g.T + c.start;
+        if (ok0) imph[j0] = acc0;
+        if (ok1) imph[j0 + 1] = acc1;
+    }
+    // 5. Y = A V over 64-key tiles, double-buffered in LDS: the owners of
+    //    tile p + 1 write its weights and waves 8-9 load its V rows (four
+    //    16-byte loads at a time, zeros past n) while threads 0..511 sum tile
+    //    p, each owning rows 2 tq, 2 tq + 1 and columns 4 tv .. 4 tv + 3
+    const float * Vl = V + layer * g.ldV + (long long)c.start * ev + (long long)h * g.dv;
+    const bool yt = tid < 512;
+    const int tq = (tid >> 5) & 15, tv = tid & 31;
+    auto put_a = [&](int p) {
+        const int kk = j0 - FA_TILE * p;
+        if (kk >= 0 && kk < FA_TILE) {
+#pragma unroll
+            for (int i4 = 0; i4 < FA_ROWS / 4; i4++) {
+                *reinterpret_cast<float4 *>(&sh.u.y.at[p & 1][kk][4 * i4]) =
+                    make_float4(s0[4 * i4], s0[4 * i4 + 1], s0[4 * i4 + 2], s0[4 * i4 + 3]);
+                *reinterpret_cast<float4 *>(&sh.u.y.at[p & 1][kk + 1][4 * i4]) =
+                    make_float4(s1[4 * i4], s1[4 * i4 + 1], s1[4 * i4 + 2], s1[4 * i4 + 3]);
+            }
+        }
+    };
+    auto put_v = [&](int p) {   // waves 8-9: 128 threads, 16 rows of 4 keys x 32 columns each, all in flight
+        const int lt = tid - 512, col = 4 * (lt & 31);
+        float4 x[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int kk = (lt >> 5) + 4 * u;
+            x[u] = *reinterpret_cast<const float4 *>(Vl + (long long)min(FA_TILE * p + kk, n - 1) * ev + col);
+        }
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int kk = (lt >> 5) + 4 * u;
+            *reinterpret_cast<float4 *>(&sh.u.y.vt[p & 1][kk][col]) =
+                FA_TILE * p + kk < n ? x[u] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    };
+    float acc[2][4];
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) acc[r][k] = 0.0f;
+    __syncthreads();   // the row sums' tiles (same LDS) have been read
+    put_a(0);
+    if (!yt) put_v(0);
+    __syncthreads();
+    for (int p = 0; p < ntile; p++) {
+        if (p + 1 < ntile) {
+            put_a(p + 1);
+            if (!yt) put_v(p + 1);
+        }
+        if (yt) {
+            // keys in groups of four: the next group's LDS reads are in
+            // flight while this group is summed (keys in order)
+            const float (*at)[FA_ROWS] = sh.u.y.at[p & 1];
+            const float (*vt)[128] = sh.u.y.vt[p & 1];
+            float2 ag[4];
+            float4 vg[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                ag[u] = *reinterpret_cast<const float2 *>(&at[u][2 * tq]);
+                vg[u] = *reinterpret_cast<const float4 *>(&vt[u][4 * tv]);
+            }
+#pragma unroll 4
+            for (int j4 = 0; j4 < FA_TILE; j4 += 4) {
+                float2 an[4];
+                float4 vn[4];
+                const int jn = min(j4 + 4, FA_TILE - 4);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    an[u] = *reinterpret_cast<const float2 *>(&at[jn + u][2 * tq]);
+                    vn[u] = *reinterpret_cast<const float4 *>(&vt[jn + u][4 * tv]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const float aa[2] = {ag[u].x, ag[u].y}, vx[4] = {vg[u].x, vg[u].y, vg[u].z, vg[u].w};
+#pragma unroll
+                    for (int r = 0; r < 2; r++)
+#pragma unroll
+                        for (int k = 0; k < 4; k++) acc[r][k] = acc[r][k] + aa[r] * vx[k];
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    ag[u] = an[u];
+                    vg[u] = vn[u];
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (yt) {
+        float * Yh = Y + ((((long long)layer * g.n_chunks + c_idx) * g.H + h) * g.nq_max) * g.dv;
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int qi = 2 * tq + r;
+            if (qi < nq)
+                *reinterpret_cast<float4 *>(Yh + (long long)qi * g.dv + 4 * tv) =
+                    make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
+        }
+    }
+}
+
+// Qt[l][h][d][i] = component h * d_k + d of query row i (FA_ROWS rows; rows
+// past nq are zero), the transposed query columns k_score_attend reads as
+// uniform operands. grid (H, L), 256 threads.
+__global__ void __launch_bounds__(256)
+k_query_columns(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ K,
+                const float * __restrict__ Q, float * __restrict__ Qt) {
+    const int h = blockIdx.x, layer = blockIdx.y;
+    const ChunkDesc c = chunks[0];
+    float * o = Qt + ((long long)layer * g.H + h) * g.dk * FA_ROWS;
+    for (int e = threadIdx.x; e < g.dk * FA_ROWS; e += blockDim.x) {
+        const int d = e / FA_ROWS, i = e % FA_ROWS;
+        o[e] = i < c.nq ? query_row(g, K, Q, layer, c, i, g.qmode)[(long long)h * g.dk + d] : 0.0f;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1848,11 +2228,15 @@ __host__ __device__ inline int lsx_rows(int t, int lds_floats) {
 __global__ void __launch_bounds__(256)
 k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ S,
              const int * __restrict__ sel, const float * __restrict__ beta, float * __restrict__ X,
-             int lds_floats) {
+             int lds_floats, const float * __restrict__ Ssel) {
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const int t = c.tc, nq = c.nq;
-    const float * Sh = S + layer * lS(g) + h * hS(g);
+    // S[:, sel] from the main scores, or (Ssel) the kept keys' own scores:
+    // row r of the chunk's kept key j at Sr[r * srs + sj]
+    const float * Sh = Ssel ? Ssel + ((long long)layer * g.H + h) * g.nq_max * g.t_total + c.off
+                            : S + layer * lS(g) + h * hS(g);
+    const long long srs = Ssel ? g.t_total : g.T;
     const int * sl = sel + (long long)layer * g.t_total + c.off;
     const float * bh = beta + ((long long)layer * g.H + h) * g.t_total + c.off;
     const long long hsX = (long long)g.nq_max * g.t_total;
@@ -1867,8 +2251,8 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
         __shared__ float rmax1, rinv1;
         for (int r = 0; r < nq; r++) {
             float * xr = Xh + (long long)r * g.t_total;
-            const float * sr = Sh + (long long)r * g.T;
-            for (int j = tid; j < t; j += blockDim.x) xr[j] = sr[sl[j]] + bh[j];
+            const float * sr = Sh + (long long)r * srs;
+            for (int j = tid; j < t; j += blockDim.x) xr[j] = sr[Ssel ? j : sl[j]] + bh[j];
             __syncthreads();
             const float m = ref_row_max(xr, t, red);
             if (tid == 0) rmax1 = m;
@@ -1893,7 +2277,7 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
     float * xs = lsx_dyn + 2 * t;
     const int ld = t + 1;
     for (int j = tid; j < t; j += blockDim.x) {
-        sls[j] = sl[j];
+        sls[j] = Ssel ? j : sl[j];
         bs[j] = bh[j];
     }
     __syncthreads();
@@ -1907,7 +2291,7 @@ k_ls_softmax(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
             const float bj = bs[j];
             float v[LSX_ROWS];
 #pragma unroll
-            for (int u = 0; u < LSX_ROWS; u++) v[u] = Sh[(long long)(r0 + min(u, nr - 1)) * g.T + sj];
+            for (int u = 0; u < LSX_ROWS; u++) v[u] = Sh[(long long)(r0 + min(u, nr - 1)) * srs + sj];
 #pragma unroll
             for (int u = 0; u < LSX_ROWS; u++)
                 if (u < nr) xs[u * ld + j] = v[u] + bj;
@@ -5235,13 +5619,29 @@ void launch_refine_step(const Geom & g, const Work & w, hipStream_t st) {
                        w.flags, w.refine_active);
 }
 
-void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st) {
+void launch_ls_softmax(const Geom & g, const Work & w, const float * beta, hipStream_t st, const float * Ssel) {
     // LDS for the largest chunk's rows (every smaller chunk then fits as many)
     const int W = g.tc_max;
     const int rows = lsx_rows(W, LSX_LDS_BYTES / 4);
     const size_t bytes = rows >= 1 ? sizeof(float) * (2 * (size_t)W + (size_t)rows * (W + 1)) : LSX_LDS_BYTES;
     hipLaunchKernelGGL(k_ls_softmax, dim3(g.n_chunks * g.H, g.L), dim3(256), bytes, st,
-                       g, w.chunks, w.S, w.sel, beta, w.X, (int)(bytes / sizeof(float)));
+                       g, w.chunks, w.S, w.sel, beta, w.X, (int)(bytes / sizeof(float)), Ssel);
+}
+
+bool score_attend_ok(const Geom & g, const float * K, const float * V, const float * Q, int Tc_max, int nq_max,
+                     int qmode) {
+    const auto al16 = [](const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    return Tc_max <= FA_KEYS && nq_max >= 1 && nq_max <= FA_ROWS && qmode != Q_CHEAP_LOCAL && g.dv == 128 &&
+           g.dk >= 16 && (g.dk & 15) == 0 && !g.kc.base && !g.vc.base && K && V && al16(K) && al16(V) &&
+           (g.ldK & 3) == 0 && (g.ldV & 3) == 0 && ((long long)g.H * g.dk & 3) == 0 &&
+           (qmode != Q_PROVIDED || Q);
+}
+
+void launch_score_attend(const Geom & g, const Work & w, const float * K, const float * V, const float * Q,
+                         float * S, int mh, hipStream_t st) {
+    hipLaunchKernelGGL(k_query_columns, dim3(g.H, g.L), dim3(256), 0, st, g, w.chunks, K, Q, w.Qt);
+    hipLaunchKernelGGL(k_score_attend, dim3(g.n_chunks * g.H, g.L), dim3(FA_THREADS), 0, st,
+                       g, w.chunks, K, w.Qt, V, S, mh, S ? w.smax : nullptr, w.imp, w.ainv, w.Y);
 }
 
 void launch_gather_exp(const Geom & g, const Work & w, hipStream_t st) {
