@@ -80,6 +80,9 @@ struct Work {
     float * LU;       // [L][n_chunks][H][256][256] by physical row: multipliers left of the row's
                       // pivot step, its U row from that step on (systems with tc <= 256)
     float * Bt;       // [L][n_chunks][H][256][dv] forward-substituted right-hand sides by logical row
+    float * LU2;      // [L][n_chunks][H][128][128] trailing matrices of the split register LU
+                      // (column-major), or nullptr: no split
+    int   * map2;     // [L][n_chunks][H][128] physical row of each trailing-matrix row
     long long * aug_off; // [L][n_chunks][H] element offsets into aug
     float * gtmp;     // [L][n_chunks][H][tc_max + tc_max + dv] GE factor / pivot-row spill
     int   * cand;     // [L][n_chunks][Tc_max] selection candidates

@@ -20,9 +20,12 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <mutex>
 #include <thread>
 #include <vector>
+
+#include <sys/mman.h>
 
 #include "../../include/kv-compact-api.h"
 #include "../../include/kv-compact-accel.h"
@@ -72,6 +75,10 @@ struct DeviceCtx {
     hipStream_t stream2 = nullptr;
     hipEvent_t fork_ev = nullptr, join_ev = nullptr;
     hipEvent_t refit_fork = nullptr, refit_join = nullptr;
+    // host-pointer calls: V uploads on its own stream while the kernels
+    // that read only K run; v_ev marks its last transfer
+    hipStream_t up_stream = nullptr;
+    hipEvent_t v_ev = nullptr;
     hipEvent_t refit_t[2] = {};   // timing of the refit target on the second stream
     char * arena = nullptr;
     size_t arena_cap = 0;
@@ -125,6 +132,8 @@ void destroy_ctx_objects(DeviceCtx * c) {
     drop(c->join_ev, hipEventDestroy);
     drop(c->refit_fork, hipEventDestroy);
     drop(c->refit_join, hipEventDestroy);
+    drop(c->up_stream, hipStreamDestroy);
+    drop(c->v_ev, hipEventDestroy);
     for (hipEvent_t & e : c->refit_t) drop(e, hipEventDestroy);
     for (hipEvent_t & e : c->ev) drop(e, hipEventDestroy);
     for (hipEvent_t & e : c->q_ev) drop(e, hipEventDestroy);
@@ -147,7 +156,9 @@ bool create_ctx_objects(DeviceCtx * c) {
     // (KVC_FAULT=init: the set-up fails here, with part of its objects made)
     if (forced_fault("init")) return false;
     if (!made(hipEventCreateWithFlags(&c->refit_fork, hipEventDisableTiming)) ||
-        !made(hipEventCreateWithFlags(&c->refit_join, hipEventDisableTiming)))
+        !made(hipEventCreateWithFlags(&c->refit_join, hipEventDisableTiming)) ||
+        !made(hipStreamCreateWithFlags(&c->up_stream, hipStreamNonBlocking)) ||
+        !made(hipEventCreateWithFlags(&c->v_ev, hipEventDisableTiming)))
         return false;
     for (hipEvent_t & e : c->refit_t)
         if (!made(hipEventCreate(&e))) return false;
@@ -590,6 +601,10 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     ww.skip = cv.take<unsigned char>(L * nc * H * (size_t)pl.tc_max);
     ww.LU = cv.take<float>(L * nc * H * ut_rows * ut_rows);
     ww.Bt = cv.take<float>(L * nc * H * ut_rows * dv);
+    // trailing matrices of the split register LU (systems of 129 .. 256 unknowns)
+    const bool split = ut_rows && pl.tc_max > 128;
+    ww.LU2 = split ? cv.take<float>(L * nc * H * 128 * 128) : nullptr;
+    ww.map2 = split ? cv.take<int>(L * nc * H * 128) : nullptr;
     ww.gtmp = cv.take<float>(L * nc * H * (2 * (size_t)pl.tc_max + dv));
     ww.cand = cv.take<int>(L * nc * (size_t)pl.Tc_max);
     ww.flags = cv.take<unsigned char>(L * nc * (size_t)pl.Tc_max);
@@ -695,8 +710,13 @@ int run_diversity(hipStream_t st, const Plan & pl, const kv_compact_params & p, 
     return 0;
 }
 
+// v_ready (host-pointer calls): V may still be arriving. It is called once,
+// before the first kernel that reads V is queued, and returns once st waits
+// for V (0) or an error code; the refit target then runs on st after the
+// kernels that read only K, which overlap the upload of V.
 int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact_params & p,
-              const BatchIO & io, Carver & carver, Timing * tm) {
+              const BatchIO & io, Carver & carver, Timing * tm,
+              const std::function<int()> & v_ready = std::function<int()>()) {
     // the chunk softmax keeps each row's maximum and scale in LDS, OMP its residuals
     if (pl.nq_max > SOFTMAX_MAXQ || (p.use_omp && pl.nq_max > OMP_MAXQ)) return KV_COMPACT_E_UNSUPPORTED;
     // Lawson-Hanson keeps a system's passive set on one wave: refused before
@@ -755,6 +775,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     // whose scores never leave the chip, where the call allows it (the
     // options that read the scores or weights again later keep them in HBM)
     const bool fused = p.skip_beta && !p.use_omp && !p.use_sensitivity && p.refine_rounds <= 0 && fused_enabled() &&
+                       !v_ready &&
                        score_attend_ok(g, io.K, io.V, io.Q, pl.Tc_max, pl.nq_max, pl.qmode);
     if (fused) {
         // the statistics' original scores are rows of S (heads < 4) when they
@@ -776,8 +797,9 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     // 3. refit target Y = A V. Only the normal equations read Y, so it runs
     //    on the second stream beside the selection (whose greedy pass is one
     //    short serial chain per unit and leaves the chip mostly idle).
-    const bool refit_fork = !fused && ctx->stream2 != nullptr;
-    if (fused) {
+    const bool late_v = static_cast<bool>(v_ready);
+    const bool refit_fork = !fused && !late_v && ctx->stream2 != nullptr;
+    if (fused || late_v) {
     } else if (refit_fork) {
         if (hipEventRecord(ctx->refit_fork, st) != hipSuccess ||
             hipStreamWaitEvent(ctx->stream2, ctx->refit_fork, 0) != hipSuccess) return KV_COMPACT_E_DEVICE;
@@ -847,6 +869,16 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         launch_ls_softmax(g, w, io.beta, st);
     }
     (void)hipEventRecord(ev[ST_LS_SOFTMAX + 1], st);
+    // V still arriving: the factorizations, which form their matrices from X
+    // alone (every system's at most 256 x 256, from at most 1024 rows of X),
+    // run before the wait too; the normal equations then write B only
+    const bool lu_first = late_v && pl.tc_max <= 256 && pl.nq_max <= 1024;
+    if (lu_first) launch_ge_lu(g, w, st, true);
+    if (late_v) {
+        rc = v_ready();
+        if (rc) return rc;
+        launch_refit_target(g, w, io.V, st);
+    }
     // The original-attention statistics read S and V only and rewrite the rows
     // of S they use; without refinement rounds the main path reads S no more,
     // so they run from here on the second stream, beside the normal
@@ -863,7 +895,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     if (refit_fork && hipStreamWaitEvent(st, ctx->refit_join, 0) != hipSuccess) return KV_COMPACT_E_DEVICE;
     launch_ls_build(g, w, st, true);
     (void)hipEventRecord(ev[ST_LS_BUILD + 1], st);
-    launch_ge_lu(g, w, st, true);
+    if (!lu_first) launch_ge_lu(g, w, st, true);
     (void)hipEventRecord(ev[ST_LU + 1], st);
     launch_ge_solve(g, w, io.Cv, st);
     (void)hipEventRecord(ev[ST_SOLVE + 1], st);
@@ -952,6 +984,19 @@ int validate(const float * K, const float * V, const void * res, int T, int n_q,
     return 0;
 }
 
+// Host memory for a result array, freeable with free(): arrays of 4 MB or
+// more are aligned to 2 MB and advised for transparent huge pages, so that
+// first-touch faults (and the caller's later free) come per 2 MB rather than
+// per 4 KB page; smaller ones come from malloc.
+void * host_alloc(size_t bytes) {
+    constexpr size_t kHuge = (size_t)2 << 20;
+    if (bytes < 2 * kHuge) return malloc(bytes);
+    void * p = nullptr;
+    if (posix_memalign(&p, kHuge, bytes) != 0) return nullptr;
+    (void)madvise(p, (bytes + kHuge - 1) & ~(kHuge - 1), MADV_HUGEPAGE);
+    return p;
+}
+
 // Device-resident outputs of one layer copied into a malloc'd host result.
 // The result's arrays (reference ownership: malloc'd, freed by
 // kv_compact_result_free), contents not yet set. False (and nothing left
@@ -959,13 +1004,13 @@ int validate(const float * K, const float * V, const void * res, int T, int n_q,
 bool alloc_result(kv_compact_result * r, int t, int H, int dv) {
     r->t = t;
     r->n_head_kv = H;
-    r->selected_indices = (int *)malloc((size_t)std::max(t, 1) * sizeof(int));
+    r->selected_indices = (int *)host_alloc((size_t)std::max(t, 1) * sizeof(int));
     r->beta = (float **)calloc((size_t)std::max(H, 1), sizeof(float *));
     r->C_v = (float **)calloc((size_t)std::max(H, 1), sizeof(float *));
     bool ok = r->selected_indices && r->beta && r->C_v;
     for (int h = 0; ok && h < H; h++) {
-        r->beta[h] = (float *)malloc((size_t)std::max(t, 1) * sizeof(float));
-        r->C_v[h] = (float *)malloc((size_t)std::max(t, 1) * dv * sizeof(float));
+        r->beta[h] = (float *)host_alloc((size_t)std::max(t, 1) * sizeof(float));
+        r->C_v[h] = (float *)host_alloc((size_t)std::max(t, 1) * dv * sizeof(float));
         ok = r->beta[h] && r->C_v[h];
     }
     if (!ok) {
@@ -975,6 +1020,47 @@ bool alloc_result(kv_compact_result * r, int t, int H, int dv) {
     }
     return ok;
 }
+
+// Writes one byte of every page of some host arrays on helper threads, so
+// that the pages are mapped (and zeroed by the kernel) while the device
+// works rather than during the result download. The array contents are set
+// afterwards; join() before anything else writes them.
+class PageToucher {
+public:
+    void add(void * p, size_t bytes) {
+        if (p && bytes) regions_.push_back({static_cast<char *>(p), bytes});
+    }
+    void start(int n_threads) {
+        for (int i = 0; i < n_threads; i++) {
+            try {
+                th_.emplace_back([this, i, n_threads] { touch(i, n_threads); });
+            } catch (...) {
+                touch(i, n_threads);   // (a thread that cannot start: its share runs here)
+            }
+        }
+    }
+    void join() {
+        for (std::thread & t : th_) t.join();
+        th_.clear();
+    }
+    ~PageToucher() { join(); }
+
+private:
+    static constexpr size_t kPage = 4096;
+    // thread i of n: the i-th contiguous part of each array (parts of whole
+    // 2 MB units, so no two threads fault the same huge page)
+    void touch(int i, int n) {
+        constexpr size_t kUnit = (size_t)2 << 20;
+        for (const auto & r : regions_) {
+            const size_t units = (r.second + kUnit - 1) / kUnit;
+            const size_t lo = std::min(r.second, units * i / n * kUnit);
+            const size_t hi = std::min(r.second, units * (i + 1) / n * kUnit);
+            for (size_t o = lo; o < hi; o += kPage) reinterpret_cast<volatile char *>(r.first)[o] = 0;
+        }
+    }
+    std::vector<std::pair<char *, size_t>> regions_;
+    std::vector<std::thread> th_;
+};
 
 bool fill_result(kv_compact_result * r, int t, int H, int dv, const std::vector<int> & idx,
                  const std::vector<float> & beta, const std::vector<float> & cv) {
@@ -988,9 +1074,14 @@ bool fill_result(kv_compact_result * r, int t, int H, int dv, const std::vector<
 }
 
 // One layer with host or device inputs; results to host (kv_compact()).
+// Host inputs: K is uploaded first; V then uploads on a second stream,
+// driven by a helper thread, while the kernels that read only K run
+// (scores, softmax, selection, the compacted softmax), and the kernels that
+// read V wait for its last transfer. The result arrays are allocated at the
+// start and their pages mapped by helper threads meanwhile, so C_v comes
+// back through the pinned ring into memory that is already present.
 int compact_one(const float * K, const float * V, const float * Q, int T, int n_q, int H, int dk, int dv,
-                const kv_compact_params & p, kv_compact_result * res, std::vector<float> * K_keep = nullptr) {
-    (void)K_keep;
+                const kv_compact_params & p, kv_compact_result * res) {
     const double t0 = now_ms();
     DeviceCtx * ctx = device_ctx();
     if (!ctx) return KV_COMPACT_E_DEVICE;
@@ -1024,6 +1115,23 @@ int compact_one(const float * K, const float * V, const float * Q, int T, int n_
     size_t need = workspace_bytes(pl, io, &p, &sizer, nullptr, nullptr);
     if (!ensure_arena(ctx, need)) return KV_COMPACT_E_DEVICE;
 
+    // the result (freed again on every failure below), its pages mapped by
+    // helper threads while the device works
+    const int t = pl.t_total;
+    if (!alloc_result(res, t, H, dv)) return KV_COMPACT_E_DEVICE;
+    struct FreeOnFail {
+        kv_compact_result * r;
+        bool armed = true;
+        ~FreeOnFail() { if (armed) kv_compact_result_free(r); }
+    } guard{res};
+    PageToucher touch;
+    for (int h = 0; h < H; h++) {
+        touch.add(res->C_v[h], (size_t)t * dv * sizeof(float));
+        touch.add(res->beta[h], (size_t)t * sizeof(float));
+    }
+    touch.add(res->selected_indices, (size_t)t * sizeof(int));
+    touch.start(4);
+
     Carver cv;
     cv.base = ctx->arena;
     float * K_dev = kd ? const_cast<float *>(K) : cv.take<float>((size_t)T * ek);
@@ -1035,24 +1143,59 @@ int compact_one(const float * K, const float * V, const float * Q, int T, int n_
     io.beta = cv.take<float>((size_t)H * std::max(pl.t_total, 1));
     io.Cv = cv.take<float>((size_t)H * std::max(pl.t_total, 1) * dv);
     io.stats = cv.take<float>(3);
-    // K and V through the pinned ring, the small inputs directly
-    std::vector<HostSeg> up;
-    if (!kd) up.push_back({const_cast<float *>(K), K_dev, (size_t)T * ek * sizeof(float)});
-    if (!vd) up.push_back({const_cast<float *>(V), V_dev, (size_t)T * ev * sizeof(float)});
-    if (!host_transfer(ctx, up, true, st)) return KV_COMPACT_E_DEVICE;
+    // the small inputs directly, K through the pinned ring on the call's stream
     hipError_t e = hipSuccess;
     if (use_q && !qd) e = hipMemcpyAsync(Q_dev, Q, (size_t)n_q * ek * sizeof(float), hipMemcpyHostToDevice, st);
     if (e == hipSuccess && have_w) e = hipMemcpyAsync(W_dev, wts.data(), (size_t)T * sizeof(float), hipMemcpyHostToDevice, st);
     if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
+    if (!kd && !host_transfer(ctx, {{const_cast<float *>(K), K_dev, (size_t)T * ek * sizeof(float)}}, true, st))
+        return KV_COMPACT_E_DEVICE;
     io.K = K_dev; io.V = V_dev; io.Q = Q_dev; io.wts = W_dev;
 
+    // V on the upload stream from a helper thread (the ring is idle again:
+    // host_transfer has queued every piece of K), unless it is on the device
+    // or the fused scoring kernel (which reads V with K) is asked for
+    std::thread v_thread;
+    std::atomic<int> v_state{vd ? 1 : 0};   // 0 queued in progress, 1 done, -1 failed
+    std::function<int()> v_ready;
+    if (!vd && fused_enabled()) {
+        if (!host_transfer(ctx, {{const_cast<float *>(V), V_dev, (size_t)T * ev * sizeof(float)}}, true, st))
+            return KV_COMPACT_E_DEVICE;
+        v_state = 1;
+    } else if (!vd) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return KV_COMPACT_E_DEVICE;
+        auto upload_v = [ctx, dev, V, V_dev, T, ev, &v_state] {
+            const bool ok = hipSetDevice(dev) == hipSuccess &&
+                            host_transfer(ctx, {{const_cast<float *>(V), V_dev, (size_t)T * ev * sizeof(float)}}, true,
+                                          ctx->up_stream) &&
+                            hipEventRecord(ctx->v_ev, ctx->up_stream) == hipSuccess;
+            v_state = ok ? 1 : -1;
+        };
+        try {
+            v_thread = std::thread(upload_v);
+        } catch (...) {
+            upload_v();   // (no thread: V is queued now, before the kernels)
+        }
+        v_ready = [&]() -> int {
+            if (v_thread.joinable()) v_thread.join();
+            if (v_state != 1 || hipStreamWaitEvent(st, ctx->v_ev, 0) != hipSuccess) return KV_COMPACT_E_DEVICE;
+            return 0;
+        };
+    }
     Timing tm;
-    int rc = run_batch(ctx, st, pl, p, io, cv, &tm);
-    if (rc != 0) return rc;
+    int rc = run_batch(ctx, st, pl, p, io, cv, &tm, v_ready);
+    if (v_thread.joinable()) v_thread.join();   // (run_batch stopped before it needed V)
+    if (rc == 0 && v_state != 1) rc = KV_COMPACT_E_DEVICE;
+    if (rc != 0) {
+        // nothing queued may still read the pinned ring or the arena
+        (void)hipStreamSynchronize(ctx->up_stream);
+        (void)hipStreamSynchronize(st);
+        return rc;
+    }
 
     // results straight into the caller's arrays (C_v through the pinned ring)
-    const int t = pl.t_total;
-    if (!alloc_result(res, t, H, dv)) return KV_COMPACT_E_DEVICE;
+    touch.join();
     float stats[3];
     std::vector<HostSeg> down;
     e = hipMemcpy(res->selected_indices, io.indices, (size_t)t * sizeof(int), hipMemcpyDeviceToHost);
@@ -1062,16 +1205,14 @@ int compact_one(const float * K, const float * V, const float * Q, int T, int n_
         down.push_back({res->C_v[h], io.Cv + (size_t)h * t * dv, (size_t)t * dv * sizeof(float)});
     }
     if (e == hipSuccess) e = hipMemcpy(stats, io.stats, sizeof(stats), hipMemcpyDeviceToHost);
-    if (e != hipSuccess || !host_transfer(ctx, down, false, st)) {
-        kv_compact_result_free(res);
-        return KV_COMPACT_E_DEVICE;
-    }
+    if (e != hipSuccess || !host_transfer(ctx, down, false, st)) return KV_COMPACT_E_DEVICE;
     res->stats.avg_cosine_sim = stats[0];
     res->stats.avg_mse = stats[1];
     res->stats.avg_agreement = stats[2];
     res->stats.scoring_ms = tm.scoring_ms;
     res->stats.nnls_ms = tm.nnls_ms;
     res->stats.elapsed_ms = now_ms() - t0;
+    guard.armed = false;
     return 0;
 }
 

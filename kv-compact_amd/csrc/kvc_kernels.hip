@@ -2854,6 +2854,7 @@ constexpr int LU_TROWS = 32;         // rows per pass of the transposed output w
 constexpr int LU_SPIN_LIMIT = 1 << 22;   // polls per wave over the whole factorization
 constexpr int LU_X_FLOATS = LU_RING * 64 * 4;   // X staged in the ring's LDS, LU_X_FLOATS / n rows at a time
 constexpr int LU_X_MAXQ = 1024;                 // rows of X beyond which k_ls_build forms M
+constexpr int LU_SPLIT = 128;   // k_ge_lu<false, true> takes steps before this; k_ge_lu_tail the rest
 
 // the register LU forms M from X: a system it factors, and X of at most
 // LU_X_MAXQ rows (staged through the ring's LDS in slabs of rows)
@@ -3143,12 +3144,19 @@ __device__ __forceinline__ void lu_steps(LuShared & sh, float (&a)[RG_SLOTS][RG_
 
 // grid (n_chunks * H, L), 1024 threads. MASKED = false: every system, sets
 // redo[sys]; MASKED = true: only the systems with redo[sys] set.
-template <bool MASKED>
+// SPLIT (unmasked only): steps 0 .. 127 only. A system of n > 128 unknowns
+// then leaves its rows not yet chosen as pivots (logical indices 128 ..
+// n - 1) in the columns >= 128 to k_ge_lu_tail, which takes the remaining
+// steps: that trailing matrix goes to T2[sys] column-major (entry (logical
+// row 128 + k, column 128 + j) at j * 128 + k) and the physical row of each
+// of its rows to map2[sys][k]; every other entry is final and written here.
+template <bool MASKED, bool SPLIT = false>
 __global__ void __launch_bounds__(RG_THREADS)
 k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
         const long long * __restrict__ aug_off, const float * __restrict__ X, int * __restrict__ perm_out,
         unsigned char * __restrict__ skip_out, float * __restrict__ LU_all, int * __restrict__ redo,
-        int * __restrict__ status) {
+        int * __restrict__ status, float * __restrict__ T2, int * __restrict__ map2) {
+    static_assert(!(MASKED && SPLIT), "the split factorization is the unmasked one");
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
     const int n = c.tc;
@@ -3254,15 +3262,27 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
         for (int s = 0; s < RG_SLOTS; s++) a[s][0] = col[s];
     }
     int spins = 0;
-    lu_steps<0, MASKED>(sh, a, live, n, w, lane, spins, status);
+    // (SPLIT: the steps before LU_SPLIT only)
+    const int nsteps = SPLIT ? min(n, LU_SPLIT) : n;
+    const bool tail = SPLIT && n > LU_SPLIT;
+    lu_steps<0, MASKED>(sh, a, live, nsteps, w, lane, spins, status);
+    int li[RG_SLOTS] = {0, 0, 0, 0};
+    if (tail) {
+        __syncthreads();   // (the last step's permutation update)
+        const int4 iv = sh.m.p.inv[lane];
+        li[0] = iv.x; li[1] = iv.y; li[2] = iv.z; li[3] = iv.w;
+    }
     if (!MASKED) {
         // a non-finite final entry: some step may have changed a finished row
+        // (SPLIT: the entries final here, columns < 128 and the rows already
+        // chosen as pivots)
         bool bad = false;
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++)
 #pragma unroll
             for (int q = 0; q < RG_COLS; q++)
                 bad = bad || (lane + 64 * s < n && w + RG_WAVES * q < n &&
+                              (!tail || w + RG_WAVES * q < LU_SPLIT || li[s] < LU_SPLIT) &&
                               (__float_as_uint(a[s][q]) & 0x7f800000u) == 0x7f800000u);
         const bool redo_sys = __syncthreads_or(bad);
         if (tid == 0) redo[sys] = redo_sys ? 1 : 0;
@@ -3270,7 +3290,22 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
     } else {
         __syncthreads();
     }
-    if (tid < n) {
+    if (tail) {
+        // the trailing matrix and its rows' physical indices for k_ge_lu_tail
+        float * T = T2 + sys * (long long)(LU_SPLIT * LU_SPLIT);
+#pragma unroll
+        for (int s = 0; s < RG_SLOTS; s++) {
+            if (li[s] >= LU_SPLIT && li[s] < n) {
+#pragma unroll
+                for (int q = LU_SPLIT / RG_WAVES; q < RG_COLS; q++) {
+                    const int j = w + RG_WAVES * q;
+                    if (j < n) T[(unsigned)((j - LU_SPLIT) * LU_SPLIT + li[s] - LU_SPLIT)] = a[s][q];
+                }
+            }
+        }
+        if (tid < n - LU_SPLIT) map2[sys * LU_SPLIT + tid] = sh.m.p.phys[LU_SPLIT + tid];
+    }
+    if (tid < nsteps) {
         const int pl = sh.plog[tid];
         perm_out[sys * (long long)g.tc_max + tid] = pl & 255;
         skip_out[sys * (long long)g.tc_max + tid] = (unsigned char)(pl >> 8);
@@ -3293,7 +3328,9 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
             __syncthreads();
             for (int e = tid; e < LU_TROWS * RG_ROWS; e += RG_THREADS) {
                 const int rr = e / RG_ROWS, j = e % RG_ROWS;
-                if (r0 + rr < n && j < n) LU[(unsigned)((r0 + rr) * RG_ROWS + j)] = sh.u.tile[rr][j];
+                if (r0 + rr < n && j < n &&
+                    (!tail || j < LU_SPLIT || sh.m.e[lu_inv_elem(r0 + rr)] < LU_SPLIT))
+                    LU[(unsigned)((r0 + rr) * RG_ROWS + j)] = sh.u.tile[rr][j];
             }
             __syncthreads();
         }
@@ -3302,6 +3339,367 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
     for (int e = tid; e < n * (RG_ROWS - n); e += RG_THREADS) {
         const int r = e / (RG_ROWS - n), j = n + e % (RG_ROWS - n);
         LU[(unsigned)(r * RG_ROWS + j)] = 0.0f;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// The last steps of the split register LU. k_ge_lu<false, true> stops after
+// step 127; from there a step only changes the rows not yet chosen as pivots
+// (logical indices 128 .. n - 1) in the columns >= 128. That trailing matrix
+// (at most 128 x 128, T2) is factored here, its rows in logical order, with
+// k_ge_lu's pivot rules and update order, in 32 registers per lane of a
+// 512-thread block: lane l holds rows l and l + 64, wave w columns w, w + 8,
+// ... Such a block needs a quarter of the registers of a whole system, so
+// several run on a CU at once and their pivot chains (each a series of
+// dependent reductions, divisions and LDS hand-offs) overlap, where the
+// whole-matrix kernel runs one system per CU.
+// ---------------------------------------------------------------------------
+constexpr int LP_WAVES = 8, LP_THREADS = 64 * LP_WAVES;
+constexpr int LP_Q = LU_SPLIT / LP_WAVES;   // register columns per wave
+constexpr int LP_TROWS = 32;               // rows per pass of the output
+
+struct LtShared {
+    float2 ring[LU_RING][64];              // step c's multipliers in slot c % LU_RING: lane l's two rows
+    float tile[LP_TROWS][LU_SPLIT + 1];    // output staging
+    int plog[LU_SPLIT];                    // step c's pivot row (+256: skipped); -1 until published
+    int inv[2 * 64];                       // logical index of rows l, l + 64 at [2 l], [2 l + 1]
+    int phys[LU_SPLIT];                    // row of each logical index
+    int map[LU_SPLIT];                     // physical row (of the whole system) of each row
+};
+
+// S values of slot c of a ring, the plog entry and the lane's logical row
+// indices, and phys[c + 1], read in this order with one wait (the wave's LDS
+// reads execute in order, so a published plog entry means the rest is too)
+template <int S>
+__device__ __forceinline__ void lp_poll_read(unsigned a_plog, unsigned a_f, unsigned a_inv, unsigned a_phys,
+                                             int & pl, float (&f)[S], int (&li)[S], int & ph) {
+    if constexpr (S == 4) {
+        typedef float v4f __attribute__((ext_vector_type(4)));
+        typedef int v4i __attribute__((ext_vector_type(4)));
+        v4f x;
+        v4i y;
+        asm volatile("ds_read_b32 %0, %4\n\t"
+                     "ds_read_b128 %1, %5\n\t"
+                     "ds_read_b128 %2, %6\n\t"
+                     "ds_read_b32 %3, %7\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(pl), "=&v"(x), "=&v"(y), "=&v"(ph)
+                     : "v"(a_plog), "v"(a_f), "v"(a_inv), "v"(a_phys)
+                     : "memory");
+        f[0] = x[0]; f[1] = x[1]; f[2] = x[2]; f[3] = x[3];
+        li[0] = y[0]; li[1] = y[1]; li[2] = y[2]; li[3] = y[3];
+    } else {
+        typedef float v2f __attribute__((ext_vector_type(2)));
+        typedef int v2i __attribute__((ext_vector_type(2)));
+        v2f x;
+        v2i y;
+        asm volatile("ds_read_b32 %0, %4\n\t"
+                     "ds_read_b64 %1, %5\n\t"
+                     "ds_read_b64 %2, %6\n\t"
+                     "ds_read_b32 %3, %7\n\t"
+                     "s_waitcnt lgkmcnt(0)"
+                     : "=&v"(pl), "=&v"(x), "=&v"(y), "=&v"(ph)
+                     : "v"(a_plog), "v"(a_f), "v"(a_inv), "v"(a_phys)
+                     : "memory");
+        f[0] = x[0]; f[1] = x[1];
+        li[0] = y[0]; li[1] = y[1];
+    }
+}
+
+// v[s] for a uniform s, as selects of values (a conditional of the array
+// elements themselves would select their addresses, and an array read
+// through a selected address is kept in scratch memory)
+template <int S>
+__device__ __forceinline__ float lp_pick(const float (&v)[S], int s) {
+    const float v0 = v[0], v1 = v[1];
+    const float lo = (s & 1) ? v1 : v0;
+    if constexpr (S == 4) {
+        const float v2 = v[2], v3 = v[3];
+        const float hi = (s & 1) ? v3 : v2;
+        return (s & 2) ? hi : lo;
+    } else {
+        return lo;
+    }
+}
+
+// Publish step c1 of a chain from its column col[] (steps < c1 applied):
+// lu_produce's rules (first logical index among the largest |a| of the rows
+// not yet used, the diagonal kept when all are zero, pivots below 1e-12
+// skip the step), for S rows per lane. ring: [LU_RING][64][S]; inv: [64][S].
+template <int S>
+__device__ __forceinline__ void lp_produce(float * ring, int * plog, int * inv, int * phys, float (&col)[S],
+                                           const int (&li)[S], int physc, int c1, int lane) {
+    bool live[S];
+    unsigned key[S];
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        live[s] = li[s] >= c1;
+        key[s] = live[s] ? __float_as_uint(fabsf(col[s])) : 0u;
+    }
+    unsigned km = key[0];
+#pragma unroll
+    for (int s = 1; s < S; s++) km = max(km, key[s]);
+    const unsigned gmax = dpp_reduce_u32<true>(km);
+    int mr, P;
+    if (gmax == 0u) {
+        mr = c1;
+        P = physc;
+    } else {
+        unsigned cand = 0xffffffffu;
+#pragma unroll
+        for (int s = 0; s < S; s++)
+            cand = min(cand, key[s] == gmax ? (((unsigned)li[s] << 8) | (unsigned)(lane + 64 * s)) : 0xffffffffu);
+        const unsigned long long m = __ballot(cand != 0xffffffffu);
+        unsigned v;
+        if ((m & (m - 1)) == 0ull) v = (unsigned)__builtin_amdgcn_readlane((int)cand, __builtin_ctzll(m));
+        else v = dpp_reduce_u32<false>(cand);
+        mr = (int)(v >> 8);
+        P = (int)(v & 255u);
+    }
+    // swap logical c1 and mr: inv[P] = c1, inv[physc] = mr, phys[c1] = P, phys[mr] = physc
+    if (lane < 4) {
+        const int ie = lane == 0 ? P : physc;
+        const int e = lane < 2 ? (ie & 63) * S + (ie >> 6) : (lane == 2 ? c1 : mr);
+        const int v = lane == 0 ? c1 : (lane == 1 ? mr : (lane == 2 ? P : physc));
+        if (lane < 2) inv[e] = v;
+        else phys[e] = v;
+    }
+    const float piv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lp_pick<S>(col, P >> 6)), P & 63));
+    const bool elim = !(fabsf(piv) < 1e-12f);
+    float f[S];
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const bool below = live[s] && (lane + 64 * s) != P;
+        const float q = col[s] / piv;
+        f[s] = (elim && below) ? q : 0.0f;
+        if (below) col[s] = f[s];
+    }
+    float * slot = ring + ((c1 & (LU_RING - 1)) * 64 + lane) * S;
+    if constexpr (S == 4) *reinterpret_cast<float4 *>(slot) = make_float4(f[0], f[1], f[2], f[3]);
+    else *reinterpret_cast<float2 *>(slot) = make_float2(f[0], f[1]);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    if (lane == 0) __hip_atomic_store(&plog[c1], P | (elim ? 0 : 256), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// a[r][q] -= f[r] * a[P][q] for the register columns q >= Q0 (pivot row in
+// slot SL, lane lP): each column's pivot entry read from its lane just
+// before the column is updated
+template <int S, int Q, int SL, int Q0>
+__device__ __forceinline__ void lp_update_from(float (&a)[S][Q], const float (&f)[S], int lP) {
+#pragma unroll
+    for (int q = Q0; q < Q; q++) {
+        const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[SL][q]), lP));
+#pragma unroll
+        for (int s = 0; s < S; s++) a[s][q] = a[s][q] - f[s] * u;
+    }
+}
+
+// one step applied to the register columns q >= Q0 (multiplier 0 off the rows below)
+template <int S, int Q, int Q0>
+__device__ __forceinline__ void lp_apply(float (&a)[S][Q], const float (&f)[S], int P) {
+    if constexpr (Q0 < Q) {
+        const int lP = P & 63;
+        if constexpr (S == 4) {
+            switch (P >> 6) {
+                case 0: lp_update_from<S, Q, 0, Q0>(a, f, lP); break;
+                case 1: lp_update_from<S, Q, 1, Q0>(a, f, lP); break;
+                case 2: lp_update_from<S, Q, 2, Q0>(a, f, lP); break;
+                default: lp_update_from<S, Q, 3, Q0>(a, f, lP); break;
+            }
+        } else {
+            if (P >> 6) lp_update_from<S, Q, 1, Q0>(a, f, lP);
+            else lp_update_from<S, Q, 0, Q0>(a, f, lP);
+        }
+    }
+}
+
+// The owner of column c + 1 (register column QN): a copy of it with step c
+// applied, from which step c + 1 is published
+template <int S, int Q, int QN>
+__device__ __forceinline__ void lp_next_column(float * ring, int * plog, int * inv, int * phys, const float (&a)[S][Q],
+                                               const float (&f)[S], bool skip, int P, const int (&li)[S], int physc,
+                                               int c1, int lane, float (&col)[S]) {
+#pragma unroll
+    for (int s = 0; s < S; s++) col[s] = a[s][QN];
+    if (!skip) {
+        const float u = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lp_pick<S>(col, P >> 6)), P & 63));
+#pragma unroll
+        for (int s = 0; s < S; s++) col[s] = col[s] - f[s] * u;
+    }
+    lp_produce<S>(ring, plog, inv, phys, col, li, physc, c1, lane);
+}
+
+// Step c = LP_WAVES B + i of a chain whose wave-relative column block is B: wait
+// for it, publish step c + 1 if this wave owns column c + 1 (and c + 1 <
+// nlim), apply it to the wave's columns > c (lu_steps' scheme).
+template <int S, int Q, int B>
+__device__ __forceinline__ void lp_step(float * ring, int * plog, int * inv, int * phys, float (&a)[S][Q], int c,
+                                        int nlim, int wv, int lane, int & spins, int * __restrict__ status) {
+    const int i = c - LP_WAVES * B;
+    const int slot = c & (LU_RING - 1);
+    const bool prod = c + 1 < nlim && wv == ((c + 1) & (LP_WAVES - 1));
+    if (prod || wv == ((c + 2) & (LP_WAVES - 1))) __builtin_amdgcn_s_setprio(2);
+    else __builtin_amdgcn_s_setprio(0);
+    int pv;
+    float f[S];
+    int li[S];
+    int physc = 0;
+#pragma unroll
+    for (int s = 0; s < S; s++) li[s] = 0;
+    float * fs = ring + (slot * 64 + lane) * S;
+    if (prod) {
+        for (;;) {
+            int pl;
+            lp_poll_read<S>(lu_lds(&plog[c]), lu_lds(fs), lu_lds(&inv[lane * S]), lu_lds(&phys[c + 1]), pl, f, li,
+                            physc);
+            pv = __builtin_amdgcn_readfirstlane(pl);
+            if (pv >= 0) break;
+            if (++spins > LU_SPIN_LIMIT) {
+                if (lane == 0) atomicOr(status, 2);
+                break;
+            }
+        }
+    } else {
+        for (;;) {
+            pv = __builtin_amdgcn_readfirstlane(
+                __hip_atomic_load(&plog[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+            if (pv >= 0) break;
+            if (++spins > LU_SPIN_LIMIT) {
+                if (lane == 0) atomicOr(status, 2);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+        if constexpr (S == 4) {
+            const float4 v = *reinterpret_cast<const float4 *>(fs);
+            f[0] = v.x; f[1] = v.y; f[2] = v.z; f[3] = v.w;
+        } else {
+            const float2 v = *reinterpret_cast<const float2 *>(fs);
+            f[0] = v.x; f[1] = v.y;
+        }
+    }
+    physc = __builtin_amdgcn_readfirstlane(physc);
+    const int P = pv & 255;
+    const bool skip = (pv & 256) != 0;
+    float col[S];
+#pragma unroll
+    for (int s = 0; s < S; s++) col[s] = 0.0f;
+    if (prod) {
+        __builtin_amdgcn_s_setprio(3);
+        if (wv != 0) lp_next_column<S, Q, B>(ring, plog, inv, phys, a, f, skip, P, li, physc, c + 1, lane, col);
+        else if constexpr (B + 1 < Q)
+            lp_next_column<S, Q, B + 1>(ring, plog, inv, phys, a, f, skip, P, li, physc, c + 1, lane, col);
+        __builtin_amdgcn_s_setprio(2);
+    }
+    if (!skip) {
+        if (wv > i) lp_apply<S, Q, B>(a, f, P);
+        else lp_apply<S, Q, B + 1>(a, f, P);
+    }
+    // (value selects: stores under if / else to two elements would be merged
+    // into one store through a selected address, which keeps the matrix in
+    // scratch memory)
+    const bool put0 = prod && wv != 0;
+#pragma unroll
+    for (int s = 0; s < S; s++) a[s][B] = put0 ? col[s] : a[s][B];
+    if constexpr (B + 1 < Q) {
+        const bool put1 = prod && wv == 0;
+#pragma unroll
+        for (int s = 0; s < S; s++) a[s][B + 1] = put1 ? col[s] : a[s][B + 1];
+    }
+}
+
+// steps LP_WAVES B .. LP_WAVES B + LP_WAVES - 1 (below m)
+template <int B>
+__device__ __forceinline__ void lt_steps(LtShared & sh, float (&b)[2][LP_Q], int m, int w, int lane, int & spins,
+                                         int * __restrict__ status) {
+    for (int i = 0; i < LP_WAVES; i++) {
+        const int c = LP_WAVES * B + i;
+        if (c >= m) break;
+        lp_step<2, LP_Q, B>(&sh.ring[0][0].x, sh.plog, sh.inv, sh.phys, b, c, m, w, lane, spins, status);
+    }
+    if constexpr (B + 1 < LP_Q) {
+        if (LP_WAVES * (B + 1) < m) lt_steps<B + 1>(sh, b, m, w, lane, spins, status);
+    }
+}
+
+// grid (n_chunks * H, L), LP_THREADS threads: the systems of more than 128
+// unknowns that k_ge_lu<false, true> did not flag for the masked kernel
+__global__ void __launch_bounds__(LP_THREADS)
+k_ge_lu_tail(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ T2,
+             const int * __restrict__ map2, int * __restrict__ perm_out, unsigned char * __restrict__ skip_out,
+             float * __restrict__ LU_all, int * __restrict__ redo, int * __restrict__ status) {
+    const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
+    const int n = chunks[c_idx].tc;
+    if (n <= LU_SPLIT || n > RG_ROWS) return;
+    const long long sys = ((long long)layer * g.n_chunks + c_idx) * g.H + h;
+    if (redo[sys] != 0) return;
+    const int m = n - LU_SPLIT;
+    const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    __shared__ LtShared sh;
+    // rows and columns past m hold zeros; those rows are never live and
+    // those columns are never published or written out
+    const float * T = T2 + sys * (long long)(LU_SPLIT * LU_SPLIT);
+    float b[2][LP_Q];
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int q = 0; q < LP_Q; q++) {
+            const int k = lane + 64 * s, j = w + LP_WAVES * q;
+            b[s][q] = (k < m && j < m) ? T[j * LU_SPLIT + k] : 0.0f;
+        }
+    if (tid < LU_SPLIT) {
+        sh.inv[(tid & 63) * 2 + (tid >> 6)] = tid < m ? tid : -1;
+        sh.phys[tid] = tid;
+        sh.plog[tid] = -1;
+        sh.map[tid] = tid < m ? map2[sys * LU_SPLIT + tid] : 0;
+    }
+    __syncthreads();
+    if (w == 0) {
+        float col[2] = {b[0][0], b[1][0]};
+        const int li[2] = {sh.inv[2 * lane], sh.inv[2 * lane + 1]};
+        lp_produce<2>(&sh.ring[0][0].x, sh.plog, sh.inv, sh.phys, col, li, 0, 0, lane);
+        b[0][0] = col[0];
+        b[1][0] = col[1];
+    }
+    int spins = 0;
+    lt_steps<0>(sh, b, m, w, lane, spins, status);
+    __builtin_amdgcn_s_setprio(0);
+    bool bad = false;
+#pragma unroll
+    for (int s = 0; s < 2; s++)
+#pragma unroll
+        for (int q = 0; q < LP_Q; q++)
+            bad = bad || (lane + 64 * s < m && w + LP_WAVES * q < m &&
+                          (__float_as_uint(b[s][q]) & 0x7f800000u) == 0x7f800000u);
+    const bool redo_sys = __syncthreads_or(bad);
+    if (tid == 0) redo[sys] = redo_sys ? 1 : 0;
+    if (redo_sys) return;
+    if (tid < m) {
+        const int pl = sh.plog[tid];
+        perm_out[sys * (long long)g.tc_max + LU_SPLIT + tid] = sh.map[pl & 255];
+        skip_out[sys * (long long)g.tc_max + LU_SPLIT + tid] = (unsigned char)(pl >> 8);
+    }
+    // row k's columns 128 .. n - 1 to its physical row, through LDS
+    float * LU = LU_all + sys * (long long)RG_ROWS * RG_ROWS;
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+#pragma unroll
+        for (int part = 0; part < 64 / LP_TROWS; part++) {
+            const int k0 = 64 * s + LP_TROWS * part;
+            if (k0 >= m) break;
+            const int lr = lane - LP_TROWS * part;
+            if (lr >= 0 && lr < LP_TROWS) {
+#pragma unroll
+                for (int q = 0; q < LP_Q; q++) sh.tile[lr][w + LP_WAVES * q] = b[s][q];
+            }
+            __syncthreads();
+            for (int e = tid; e < LP_TROWS * m; e += LP_THREADS) {
+                const int kk = e / m, j = e - kk * m;
+                if (k0 + kk < m) LU[(unsigned)(sh.map[k0 + kk] * RG_ROWS + LU_SPLIT + j)] = sh.tile[kk][j];
+            }
+            __syncthreads();
+        }
     }
 }
 
@@ -5391,6 +5789,168 @@ k_requant8(const float * __restrict__ src, long long src_ls, long long src_ld, c
 }
 
 // ---------------------------------------------------------------------------
+// Codec row tiles (Q8_0 / Q4_0 rows whose byte length is a multiple of 16,
+// at 16-byte aligned addresses): a block stages up to CT_ROWS whole rows in
+// LDS, and HBM sees only 16-byte pieces, one float4 (or one 16-byte run of
+// encoded bytes) per lane, so every wave instruction reads or writes 1 KB of
+// contiguous memory. The 2-byte scale and code fields are then read or
+// written in LDS. The arithmetic is k_dequant8's and k_requant8's, so the
+// results equal theirs bit for bit; a 32-element block of the encode is
+// spread over 8 lanes of 4 elements, whose largest magnitude is reduced
+// between them (the largest non-NaN |x| from 0: one value in any order).
+// ---------------------------------------------------------------------------
+constexpr int CT_THREADS = 256;
+constexpr int CT_ROWS = 8;
+
+template <int TYPE>
+__device__ __forceinline__ int ct_block_bytes() { return TYPE == 8 ? 34 : 18; }
+
+// copy nr rows (row r at src_row(r), rb bytes, rb % 16 == 0) into LDS at
+// lds + r * rb, four 16-byte loads per thread in flight
+template <class RowPtr>
+__device__ __forceinline__ void ct_stage(uint8_t * lds, int nr, long long rb, RowPtr src_row) {
+    const int pieces = (int)(rb >> 4), n = nr * pieces;
+    for (int p0 = threadIdx.x; p0 < n; p0 += 4 * CT_THREADS) {
+        uint4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int pp = p0 + k * CT_THREADS;
+            if (pp < n) {
+                const int rl = pp / pieces, o = pp - rl * pieces;
+                v[k] = *reinterpret_cast<const uint4 *>(src_row(rl) + 16LL * o);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const int pp = p0 + k * CT_THREADS;
+            if (pp < n) *reinterpret_cast<uint4 *>(lds + 16LL * pp) = v[k];
+        }
+    }
+}
+
+// rows [L][T] of codec TYPE (row stride row_bytes, layer stride src_ls
+// bytes) into dst [L][T][n_el] fp32; grid (ceil(T / CT_ROWS), L): rows
+// j0 .. j0 + nr - 1 of layer blockIdx.y per block
+template <int TYPE>
+__global__ void __launch_bounds__(CT_THREADS)
+k_dequant_tile(const uint8_t * __restrict__ src, long long row_bytes, long long src_ls, int n_el, int T, int L,
+               float * __restrict__ dst) {
+    extern __shared__ __align__(16) uint8_t ct_lds[];
+    const int j0 = blockIdx.x * CT_ROWS, l = blockIdx.y;
+    const int nr = min(CT_ROWS, T - j0);
+    const uint8_t * base = src + l * src_ls + (long long)j0 * row_bytes;
+    ct_stage(ct_lds, nr, row_bytes, [&](int rl) { return base + rl * row_bytes; });
+    __syncthreads();
+    const int n4 = n_el >> 2;
+    float4 * out = reinterpret_cast<float4 *>(dst + ((long long)l * T + j0) * n_el);
+    for (int j = threadIdx.x; j < nr * n4; j += CT_THREADS) {
+        const int rl = j / n4, c = 4 * (j - rl * n4);
+        out[j] = codec_dec4<TYPE>(codec_raw4_at<TYPE>(ct_lds + rl * row_bytes, c));
+    }
+}
+
+// Quantize rows (l, j), j < rows, of L layers into codec OUT (row stride
+// row_bytes, layer stride dst_ls; both multiples of 16). Source row (as in
+// k_requant8): SRC 0: fp32 src + l * src_ls + idx[l * idx_ls + j] * src_ld;
+// SRC 1: the concatenation over heads of Cv[((l * H + h) * rows + j) * dv ..]
+// (dv a multiple of 4); SRC 8 / 2: row idx[l * idx_ls + j] of the codec
+// cache sq (rows of a multiple of 16 bytes), staged in LDS and decoded.
+template <int SRC, int OUT>
+__global__ void __launch_bounds__(CT_THREADS)
+k_requant_tile(const float * __restrict__ src, long long src_ls, long long src_ld, const int * __restrict__ idx,
+               long long idx_ls, int H, int dv, int n_el, int rows, int L, uint8_t * __restrict__ dst,
+               long long row_bytes, long long dst_ls, RowCodec sq) {
+    extern __shared__ __align__(16) uint8_t ct_lds[];
+    uint8_t * outs = ct_lds;                              // nr encoded rows
+    uint8_t * ins = ct_lds + CT_ROWS * row_bytes;         // nr source rows (SRC 8 / 2)
+    const int j0 = blockIdx.x * CT_ROWS, l = blockIdx.y;
+    const int nr = min(CT_ROWS, rows - j0);
+    const int * lidx = idx ? idx + l * idx_ls + j0 : nullptr;
+    if constexpr (SRC == 8 || SRC == 2) {
+        ct_stage(ins, nr, sq.row_bytes, [&](int rl) { return codec_row(sq, l, (long long)lidx[rl]); });
+        __syncthreads();
+    }
+    const int n4 = n_el >> 2;
+    // (nr * n4 is a multiple of 8, so the eight lanes of an encode block run
+    // together.) A thread's float4 of up to CT_BATCH passes are loaded before
+    // any is encoded, so their memory latencies overlap.
+    constexpr int CT_BATCH = 8;
+    const int lane8 = threadIdx.x & 7;
+    for (int b0 = threadIdx.x - lane8; b0 < nr * n4; b0 += CT_BATCH * CT_THREADS) {
+        float4 xs[CT_BATCH];
+#pragma unroll
+        for (int k = 0; k < CT_BATCH; k++) {
+            const int jj = b0 + k * CT_THREADS + lane8;
+            if (jj < nr * n4) {
+                const int rl = jj / n4, c = 4 * (jj - rl * n4);
+                if constexpr (SRC == 0) {
+                    xs[k] = *reinterpret_cast<const float4 *>(src + l * src_ls + (long long)lidx[rl] * src_ld + c);
+                } else if constexpr (SRC == 1) {
+                    const int h = c / dv, v = c - h * dv;
+                    xs[k] = *reinterpret_cast<const float4 *>(
+                        src + ((((long long)l * H + h) * rows + j0 + rl) * dv + v));
+                } else {
+                    xs[k] = codec_dec4<SRC>(codec_raw4_at<SRC>(ins + rl * sq.row_bytes, c));
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < CT_BATCH; k++) {
+            const int jj = b0 + k * CT_THREADS + lane8;
+            if (jj >= nr * n4) break;   // (uniform over the eight lanes of a block)
+            const int rl = jj / n4, c = 4 * (jj - rl * n4);
+            const float xv[4] = {xs[k].x, xs[k].y, xs[k].z, xs[k].w};
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float t = fabsf(xv[i]);
+                if (t > amax) amax = t;
+            }
+#pragma unroll
+            for (int m = 1; m < 8; m <<= 1) {
+                const float o = __shfl_xor(amax, m);
+                amax = o > amax ? o : amax;
+            }
+            const int k8 = (c >> 2) & 7;
+            uint8_t * blk = outs + rl * row_bytes + (c >> 5) * ct_block_bytes<OUT>();
+            if constexpr (OUT == 8) {
+                const float d = amax / 127.0f;
+                const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
+                if (k8 == 0) *reinterpret_cast<uint16_t *>(blk) = f32_to_f16_ref(d);
+                uint16_t * q16 = reinterpret_cast<uint16_t *>(blk + 2 + 4 * k8);
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const uint8_t q0 = (uint8_t)(int8_t)roundf(fmax_std(-128.0f, fmin_std(127.0f, xv[2 * i] * id)));
+                    const uint8_t q1 =
+                        (uint8_t)(int8_t)roundf(fmax_std(-128.0f, fmin_std(127.0f, xv[2 * i + 1] * id)));
+                    q16[i] = (uint16_t)(q0 | ((uint16_t)q1 << 8));
+                }
+            } else {
+                const float d = amax / 7.0f;
+                const float id = (d != 0.0f) ? 7.0f / amax : 0.0f;
+                if (k8 == 0) *reinterpret_cast<uint16_t *>(blk) = f32_to_f16_ref(d);
+                uint8_t by[2];
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const float v0 = xv[2 * u] * id + 8.0f;
+                    const float v1 = xv[2 * u + 1] * id + 8.0f;
+                    const uint8_t q0 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v0)));
+                    const uint8_t q1 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v1)));
+                    by[u] = (uint8_t)(q0 | (q1 << 4));
+                }
+                *reinterpret_cast<uint16_t *>(blk + 2 + 2 * k8) = (uint16_t)(by[0] | ((uint16_t)by[1] << 8));
+            }
+        }
+    }
+    __syncthreads();
+    const int pieces = (int)(row_bytes >> 4);
+    // (the block's rows are consecutive in the output)
+    uint8_t * obase = dst + l * dst_ls + (long long)j0 * row_bytes;
+    for (int pp = threadIdx.x; pp < nr * pieces; pp += CT_THREADS)
+        *reinterpret_cast<uint4 *>(obase + 16LL * pp) = *reinterpret_cast<const uint4 *>(outs + 16 * pp);
+}
+
+// ---------------------------------------------------------------------------
 // llama.cpp state blobs (state.h:425-462, 645-810; kv-compact.cpp:659-685):
 // the layout moves around the compaction itself.
 // ---------------------------------------------------------------------------
@@ -5707,13 +6267,29 @@ void launch_ls_build(const Geom & g, const Work & w, hipStream_t st, bool m_by_l
                            m_by_lu ? 1 : 0);
 }
 
+// KVC_LU_SPLIT=0 (read at every launch) factors every system in one pass of
+// k_ge_lu instead of k_ge_lu<false, true> + k_ge_lu_tail
+static bool lu_split_enabled() {
+    const char * e = getenv("KVC_LU_SPLIT");
+    return !(e && e[0] == '0');
+}
+
 void launch_ge_lu(const Geom & g, const Work & w, hipStream_t st, bool m_by_lu) {
     // unmasked pass over every system, then the masked pass over the flagged ones
     const float * X = m_by_lu ? w.X : nullptr;
-    hipLaunchKernelGGL(k_ge_lu<false>, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
-                       g, w.chunks, w.aug, w.aug_off, X, w.perm, w.skip, w.LU, w.lu_redo, w.status);
-    hipLaunchKernelGGL(k_ge_lu<true>, dim3(g.n_chunks * g.H, g.L), dim3(RG_THREADS), 0, st,
-                       g, w.chunks, w.aug, w.aug_off, X, w.perm, w.skip, w.LU, w.lu_redo, w.status);
+    const dim3 grid(g.n_chunks * g.H, g.L);
+    if (w.LU2 && g.tc_max > LU_SPLIT && lu_split_enabled()) {
+        hipLaunchKernelGGL((k_ge_lu<false, true>), grid, dim3(RG_THREADS), 0, st,
+                           g, w.chunks, w.aug, w.aug_off, X, w.perm, w.skip, w.LU, w.lu_redo, w.status, w.LU2, w.map2);
+        hipLaunchKernelGGL(k_ge_lu_tail, grid, dim3(LP_THREADS), 0, st,
+                           g, w.chunks, w.LU2, w.map2, w.perm, w.skip, w.LU, w.lu_redo, w.status);
+    } else {
+        hipLaunchKernelGGL((k_ge_lu<false, false>), grid, dim3(RG_THREADS), 0, st,
+                           g, w.chunks, w.aug, w.aug_off, X, w.perm, w.skip, w.LU, w.lu_redo, w.status, nullptr,
+                           nullptr);
+    }
+    hipLaunchKernelGGL((k_ge_lu<true, false>), grid, dim3(RG_THREADS), 0, st,
+                       g, w.chunks, w.aug, w.aug_off, X, w.perm, w.skip, w.LU, w.lu_redo, w.status, nullptr, nullptr);
 }
 
 void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st) {
@@ -5877,8 +6453,26 @@ bool codec8_ok(int type, int n_el) {
     return (type == 0 || type == 1 || type == 30) && n_el % 8 == 0;
 }
 
+// Q8_0 / Q4_0 rows that are whole 16-byte pieces at 16-byte aligned addresses
+static bool ct_rows_ok(int type, const void * base, long long row_bytes, long long layer_bytes, int n_el) {
+    return (type == 8 || type == 2) && n_el % 32 == 0 && row_bytes % 16 == 0 && layer_bytes % 16 == 0 &&
+           (reinterpret_cast<uintptr_t>(base) & 15) == 0 && CT_ROWS * row_bytes <= 32768;
+}
+
 void launch_dequant8(const uint8_t * src, int type, long long row_bytes, long long src_ls, int n_el, int T, int L,
                      float * dst, hipStream_t st) {
+    if (ct_rows_ok(type, src, row_bytes, src_ls, n_el) && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+        if ((long long)L * T <= 0) return;
+        const dim3 grid(cdiv(T, CT_ROWS), L);
+        const size_t lds = (size_t)CT_ROWS * row_bytes;
+        if (type == 8)
+            hipLaunchKernelGGL(k_dequant_tile<8>, grid, dim3(CT_THREADS), lds, st, src, row_bytes, src_ls, n_el, T, L,
+                               dst);
+        else
+            hipLaunchKernelGGL(k_dequant_tile<2>, grid, dim3(CT_THREADS), lds, st, src, row_bytes, src_ls, n_el, T, L,
+                               dst);
+        return;
+    }
     // one work item per thread (measured: 5.1 TB/s against 4.0 with the
     // grid capped and a strided loop)
     const long long total = (long long)L * T * (n_el / 8);
@@ -5892,6 +6486,32 @@ void launch_requant8(const float * src, long long src_ls, long long src_ld, cons
                      long long dst_ls, hipStream_t st, RowCodec sq) {
     const long long total = (long long)L * rows * (n_el / 8);
     if (total <= 0) return;
+    const bool src_ok = mode == 1 ? (dv % 4 == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0)
+                      : sq.base   ? ct_rows_ok(sq.type, sq.base, sq.row_bytes, sq.layer_bytes, n_el)
+                                  : ((reinterpret_cast<uintptr_t>(src) | (uintptr_t)(src_ls * 4) |
+                                      (uintptr_t)(src_ld * 4)) & 15) == 0;
+    if (src_ok && ct_rows_ok(type, dst, row_bytes, dst_ls, n_el) &&
+        (!sq.base || CT_ROWS * (row_bytes + sq.row_bytes) <= 65536)) {
+        const dim3 grid(cdiv(rows, CT_ROWS), L);
+        const size_t lds = (size_t)CT_ROWS * (row_bytes + (sq.base ? sq.row_bytes : 0));
+        auto go = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, dim3(CT_THREADS), lds, st, src, src_ls, src_ld, idx, idx_ls,
+                               H, dv, n_el, rows, L, dst, row_bytes, dst_ls, sq);
+        };
+        const int sk = mode == 1 ? 1 : (sq.base ? sq.type : 0);
+        if (type == 8) {
+            if (sk == 0) go(k_requant_tile<0, 8>);
+            else if (sk == 1) go(k_requant_tile<1, 8>);
+            else if (sk == 8) go(k_requant_tile<8, 8>);
+            else go(k_requant_tile<2, 8>);
+        } else {
+            if (sk == 0) go(k_requant_tile<0, 2>);
+            else if (sk == 1) go(k_requant_tile<1, 2>);
+            else if (sk == 8) go(k_requant_tile<8, 2>);
+            else go(k_requant_tile<2, 2>);
+        }
+        return;
+    }
     const long long blocks = std::min<long long>((total + 255) / 256, 1LL << 30);
     hipLaunchKernelGGL(k_requant8, dim3((unsigned)blocks), dim3(256), 0, st,
                        src, src_ls, src_ld, idx, idx_ls, mode, H, dv, type, n_el, rows, L, dst, row_bytes, dst_ls, sq);

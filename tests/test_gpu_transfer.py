@@ -127,3 +127,60 @@ def test_host_state_in_pieces(gpu, orc):
     assert rc == 0 and rc_o == 0, (rc, rc_o)
     assert np.array_equal(sel, sel_o), "kept cells"
     assert out == out_o, "output blob"
+
+
+@pytest.mark.parametrize("where", ["k_device", "v_device", "both_host"])
+def test_host_device_mixes(gpu, orc, where):
+    """kv_compact with K, V or neither already in device memory, diversity on:
+    a host V uploads on its own stream while the kernels that read only K run
+    (the diversity levels synchronise the call's stream meanwhile); results
+    equal the oracle's bit for bit."""
+    import hiprt
+    T, H, d = 2560, 8, 128
+    print(f"[transfer] mixed pointers {where}", flush=True)
+    K, V = kv_cache(T, H, d, 304, channel_scale=True)
+    Q = snapkv_queries(K, 32, 304)
+    p = dict(target_ratio=0.2, use_diversity=1)
+    dK = dV = None
+    Ka, Va = K, V
+    if where == "k_device":
+        dK = hiprt.DevBuf(K.nbytes)
+        dK.upload(K)
+        Ka = dK.value
+    elif where == "v_device":
+        dV = hiprt.DevBuf(V.nbytes)
+        dV.upload(V)
+        Va = dV.value
+    with pieces(65540):
+        a = gpu.compact(Ka, Va, Q, T, 32, H, d, d, gpu.params(**p))
+    b = orc.compact(K, V, Q, T, 32, H, d, d, orc.params(**p))
+    same(a, b)
+    del dK, dV
+
+
+def test_failure_while_v_uploads(gpu, orc):
+    """A call that stops while V is still being uploaded (KVC_FAULT=launch
+    stops it before its first kernel; Lawson-Hanson beta on an unchunked call
+    keeping more than 256 keys is refused with -5) returns its code with the
+    result left empty (no arrays, t = 0), and the next call gives the oracle's
+    results."""
+    T, H, d = 2560, 8, 128
+    print("[transfer] failure while V uploads", flush=True)
+    K, V = kv_cache(T, H, d, 305)
+    Q = snapkv_queries(K, 32, 305)
+    cases = [("launch", dict(target_ratio=0.2), -6),
+             (None, dict(target_ratio=0.2, chunk_size=-1, skip_beta=0, nnls_method=0), -5)]
+    with pieces(65540):
+        for fault, p, want in cases:
+            if fault:
+                os.environ["KVC_FAULT"] = fault
+            try:
+                rc, r = gpu.compact_raw(K, V, Q, T, 32, H, d, d, gpu.params(**p))
+            finally:
+                os.environ.pop("KVC_FAULT", None)
+            assert rc == want, (fault, rc)
+            assert r.t == 0 and r.n_head_kv == 0 and not r.selected_indices and not r.C_v and not r.beta
+            gpu.free_result(r)
+        a = gpu.compact(K, V, Q, T, 32, H, d, d, gpu.params(target_ratio=0.2))
+    b = orc.compact(K, V, Q, T, 32, H, d, d, orc.params(target_ratio=0.2))
+    same(a, b)
