@@ -79,6 +79,7 @@ struct DeviceCtx {
     // that read only K run; v_ev marks its last transfer
     hipStream_t up_stream = nullptr;
     hipEvent_t v_ev = nullptr;
+    hipEvent_t cv_ev = nullptr;   // C_v written (its download, on up_stream, waits for it)
     hipEvent_t refit_t[2] = {};   // timing of the refit target on the second stream
     char * arena = nullptr;
     size_t arena_cap = 0;
@@ -134,6 +135,7 @@ void destroy_ctx_objects(DeviceCtx * c) {
     drop(c->refit_join, hipEventDestroy);
     drop(c->up_stream, hipStreamDestroy);
     drop(c->v_ev, hipEventDestroy);
+    drop(c->cv_ev, hipEventDestroy);
     for (hipEvent_t & e : c->refit_t) drop(e, hipEventDestroy);
     for (hipEvent_t & e : c->ev) drop(e, hipEventDestroy);
     for (hipEvent_t & e : c->q_ev) drop(e, hipEventDestroy);
@@ -158,7 +160,8 @@ bool create_ctx_objects(DeviceCtx * c) {
     if (!made(hipEventCreateWithFlags(&c->refit_fork, hipEventDisableTiming)) ||
         !made(hipEventCreateWithFlags(&c->refit_join, hipEventDisableTiming)) ||
         !made(hipStreamCreateWithFlags(&c->up_stream, hipStreamNonBlocking)) ||
-        !made(hipEventCreateWithFlags(&c->v_ev, hipEventDisableTiming)))
+        !made(hipEventCreateWithFlags(&c->v_ev, hipEventDisableTiming)) ||
+        !made(hipEventCreateWithFlags(&c->cv_ev, hipEventDisableTiming)))
         return false;
     for (hipEvent_t & e : c->refit_t)
         if (!made(hipEventCreate(&e))) return false;
@@ -714,9 +717,12 @@ int run_diversity(hipStream_t st, const Plan & pl, const kv_compact_params & p, 
 // before the first kernel that reads V is queued, and returns once st waits
 // for V (0) or an error code; the refit target then runs on st after the
 // kernels that read only K, which overlap the upload of V.
+// cv_done (host-pointer calls): called once C_v's last writer is queued on
+// st (before the statistics), so that its download can start beside them.
 int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact_params & p,
               const BatchIO & io, Carver & carver, Timing * tm,
-              const std::function<int()> & v_ready = std::function<int()>()) {
+              const std::function<int()> & v_ready = std::function<int()>(),
+              const std::function<void()> & cv_done = std::function<void()>()) {
     // the chunk softmax keeps each row's maximum and scale in LDS, OMP its residuals
     if (pl.nq_max > SOFTMAX_MAXQ || (p.use_omp && pl.nq_max > OMP_MAXQ)) return KV_COMPACT_E_UNSUPPORTED;
     // Lawson-Hanson keeps a system's passive set on one wave: refused before
@@ -915,6 +921,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
         }
     }
     (void)hipEventRecord(ev[ST_REFINE + 1], st);
+    if (cv_done) cv_done();
     // 8. quality statistics against the full call
     // the statistics' original scores are rows of S when both use one query set
     if (!fork) launch_stats_original(g, w, sw, io.K, io.V, io.Q, st, s_main);
@@ -1183,10 +1190,42 @@ int compact_one(const float * K, const float * V, const float * Q, int T, int n_
             return 0;
         };
     }
+    // C_v goes to the caller's arrays through the pinned ring as soon as its
+    // last writer is queued: a helper thread queues the transfers on the
+    // upload stream (after an event on st) while the statistics run
+    std::vector<HostSeg> down;
+    for (int h = 0; h < H; h++)
+        down.push_back({res->C_v[h], io.Cv + (size_t)h * t * dv, (size_t)t * dv * sizeof(float)});
+    std::thread d_thread;
+    std::atomic<int> d_state{0};   // 0 not started, 1 done, -1 failed
+    auto download = [ctx, &down, &d_state, &touch](int dev) {
+        touch.join();   // (the pages are mapped before the ring writes them)
+        const bool ok = hipSetDevice(dev) == hipSuccess && hipStreamWaitEvent(ctx->up_stream, ctx->cv_ev, 0) == hipSuccess &&
+                        host_transfer(ctx, down, false, ctx->up_stream);
+        d_state = ok ? 1 : -1;
+    };
+    std::function<void()> cv_done = [&]() {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipEventRecord(ctx->cv_ev, st) != hipSuccess) {
+            d_state = -1;
+            return;
+        }
+        try {
+            d_thread = std::thread(download, dev);
+        } catch (...) {
+            download(dev);
+        }
+    };
     Timing tm;
-    int rc = run_batch(ctx, st, pl, p, io, cv, &tm, v_ready);
+    int rc = run_batch(ctx, st, pl, p, io, cv, &tm, v_ready, cv_done);
     if (v_thread.joinable()) v_thread.join();   // (run_batch stopped before it needed V)
+    if (d_thread.joinable()) d_thread.join();
     if (rc == 0 && v_state != 1) rc = KV_COMPACT_E_DEVICE;
+    if (rc == 0 && d_state == 0) {
+        touch.join();
+        d_state = host_transfer(ctx, down, false, st) ? 1 : -1;   // (cv_done was not reached)
+    }
+    if (rc == 0 && d_state != 1) rc = KV_COMPACT_E_DEVICE;
     if (rc != 0) {
         // nothing queued may still read the pinned ring or the arena
         (void)hipStreamSynchronize(ctx->up_stream);
@@ -1194,18 +1233,14 @@ int compact_one(const float * K, const float * V, const float * Q, int T, int n_
         return rc;
     }
 
-    // results straight into the caller's arrays (C_v through the pinned ring)
-    touch.join();
+    // the small results
     float stats[3];
-    std::vector<HostSeg> down;
     e = hipMemcpy(res->selected_indices, io.indices, (size_t)t * sizeof(int), hipMemcpyDeviceToHost);
-    for (int h = 0; h < H; h++) {
+    for (int h = 0; h < H; h++)
         if (e == hipSuccess)
             e = hipMemcpy(res->beta[h], io.beta + (size_t)h * t, (size_t)t * sizeof(float), hipMemcpyDeviceToHost);
-        down.push_back({res->C_v[h], io.Cv + (size_t)h * t * dv, (size_t)t * dv * sizeof(float)});
-    }
     if (e == hipSuccess) e = hipMemcpy(stats, io.stats, sizeof(stats), hipMemcpyDeviceToHost);
-    if (e != hipSuccess || !host_transfer(ctx, down, false, st)) return KV_COMPACT_E_DEVICE;
+    if (e != hipSuccess) return KV_COMPACT_E_DEVICE;
     res->stats.avg_cosine_sim = stats[0];
     res->stats.avg_mse = stats[1];
     res->stats.avg_agreement = stats[2];

@@ -2854,6 +2854,9 @@ constexpr int LU_TROWS = 32;         // rows per pass of the transposed output w
 constexpr int LU_SPIN_LIMIT = 1 << 22;   // polls per wave over the whole factorization
 constexpr int LU_X_FLOATS = LU_RING * 64 * 4;   // X staged in the ring's LDS, LU_X_FLOATS / n rows at a time
 constexpr int LU_X_MAXQ = 1024;                 // rows of X beyond which k_ls_build forms M
+#ifndef LU_POLL_SLEEP
+#define LU_POLL_SLEEP 1   // s_sleep units (64 clocks) between polls of a wave with slack
+#endif
 constexpr int LU_SPLIT = 128;   // k_ge_lu<false, true> takes steps before this; k_ge_lu_tail the rest
 
 // the register LU forms M from X: a system it factors, and X of at most
@@ -3104,7 +3107,12 @@ __device__ __forceinline__ void lu_steps(LuShared & sh, float (&a)[RG_SLOTS][RG_
                     if (lane == 0) atomicOr(status, 2);
                     break;
                 }
-                __builtin_amdgcn_s_sleep(1);
+                // (the owner of column c + 2 publishes next after the
+                // producer; the others have a step or more of slack and
+                // wait longer between polls, which leaves the issue slots
+                // of their SIMDs to the waves doing the work)
+                if (w == ((c + 2) & (RG_COLS - 1))) __builtin_amdgcn_s_sleep(1);
+                else __builtin_amdgcn_s_sleep(LU_POLL_SLEEP);
             }
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
             f4 = sh.u.fm[slot][lane];
@@ -3568,7 +3576,8 @@ __device__ __forceinline__ void lp_step(float * ring, int * plog, int * inv, int
                 if (lane == 0) atomicOr(status, 2);
                 break;
             }
-            __builtin_amdgcn_s_sleep(1);
+            if (wv == ((c + 2) & (LP_WAVES - 1))) __builtin_amdgcn_s_sleep(1);
+            else __builtin_amdgcn_s_sleep(LU_POLL_SLEEP);
         }
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
         if constexpr (S == 4) {
@@ -5789,21 +5798,16 @@ k_requant8(const float * __restrict__ src, long long src_ls, long long src_ld, c
 }
 
 // ---------------------------------------------------------------------------
-// Codec row tiles (Q8_0 / Q4_0 rows whose byte length is a multiple of 16,
-// at 16-byte aligned addresses): a block stages up to CT_ROWS whole rows in
-// LDS, and HBM sees only 16-byte pieces, one float4 (or one 16-byte run of
-// encoded bytes) per lane, so every wave instruction reads or writes 1 KB of
-// contiguous memory. The 2-byte scale and code fields are then read or
-// written in LDS. The arithmetic is k_dequant8's and k_requant8's, so the
-// results equal theirs bit for bit; a 32-element block of the encode is
-// spread over 8 lanes of 4 elements, whose largest magnitude is reduced
-// between them (the largest non-NaN |x| from 0: one value in any order).
+// Codec row tiles for the whole-cache decode (Q8_0 / Q4_0 rows whose byte
+// length is a multiple of 16, at 16-byte aligned addresses): a block stages
+// up to CT_ROWS whole rows in LDS, so HBM sees only 16-byte pieces, and
+// writes one float4 per lane: every wave instruction reads or writes 1 KB
+// of contiguous memory. The 2-byte scale and code fields are read in LDS,
+// with the in-register decoders' products (codec_dec4, k_dequant8's values
+// bit for bit).
 // ---------------------------------------------------------------------------
 constexpr int CT_THREADS = 256;
 constexpr int CT_ROWS = 8;
-
-template <int TYPE>
-__device__ __forceinline__ int ct_block_bytes() { return TYPE == 8 ? 34 : 18; }
 
 // copy nr rows (row r at src_row(r), rb bytes, rb % 16 == 0) into LDS at
 // lds + r * rb, four 16-byte loads per thread in flight
@@ -5847,107 +5851,6 @@ k_dequant_tile(const uint8_t * __restrict__ src, long long row_bytes, long long 
         const int rl = j / n4, c = 4 * (j - rl * n4);
         out[j] = codec_dec4<TYPE>(codec_raw4_at<TYPE>(ct_lds + rl * row_bytes, c));
     }
-}
-
-// Quantize rows (l, j), j < rows, of L layers into codec OUT (row stride
-// row_bytes, layer stride dst_ls; both multiples of 16). Source row (as in
-// k_requant8): SRC 0: fp32 src + l * src_ls + idx[l * idx_ls + j] * src_ld;
-// SRC 1: the concatenation over heads of Cv[((l * H + h) * rows + j) * dv ..]
-// (dv a multiple of 4); SRC 8 / 2: row idx[l * idx_ls + j] of the codec
-// cache sq (rows of a multiple of 16 bytes), staged in LDS and decoded.
-template <int SRC, int OUT>
-__global__ void __launch_bounds__(CT_THREADS)
-k_requant_tile(const float * __restrict__ src, long long src_ls, long long src_ld, const int * __restrict__ idx,
-               long long idx_ls, int H, int dv, int n_el, int rows, int L, uint8_t * __restrict__ dst,
-               long long row_bytes, long long dst_ls, RowCodec sq) {
-    extern __shared__ __align__(16) uint8_t ct_lds[];
-    uint8_t * outs = ct_lds;                              // nr encoded rows
-    uint8_t * ins = ct_lds + CT_ROWS * row_bytes;         // nr source rows (SRC 8 / 2)
-    const int j0 = blockIdx.x * CT_ROWS, l = blockIdx.y;
-    const int nr = min(CT_ROWS, rows - j0);
-    const int * lidx = idx ? idx + l * idx_ls + j0 : nullptr;
-    if constexpr (SRC == 8 || SRC == 2) {
-        ct_stage(ins, nr, sq.row_bytes, [&](int rl) { return codec_row(sq, l, (long long)lidx[rl]); });
-        __syncthreads();
-    }
-    const int n4 = n_el >> 2;
-    // (nr * n4 is a multiple of 8, so the eight lanes of an encode block run
-    // together.) A thread's float4 of up to CT_BATCH passes are loaded before
-    // any is encoded, so their memory latencies overlap.
-    constexpr int CT_BATCH = 8;
-    const int lane8 = threadIdx.x & 7;
-    for (int b0 = threadIdx.x - lane8; b0 < nr * n4; b0 += CT_BATCH * CT_THREADS) {
-        float4 xs[CT_BATCH];
-#pragma unroll
-        for (int k = 0; k < CT_BATCH; k++) {
-            const int jj = b0 + k * CT_THREADS + lane8;
-            if (jj < nr * n4) {
-                const int rl = jj / n4, c = 4 * (jj - rl * n4);
-                if constexpr (SRC == 0) {
-                    xs[k] = *reinterpret_cast<const float4 *>(src + l * src_ls + (long long)lidx[rl] * src_ld + c);
-                } else if constexpr (SRC == 1) {
-                    const int h = c / dv, v = c - h * dv;
-                    xs[k] = *reinterpret_cast<const float4 *>(
-                        src + ((((long long)l * H + h) * rows + j0 + rl) * dv + v));
-                } else {
-                    xs[k] = codec_dec4<SRC>(codec_raw4_at<SRC>(ins + rl * sq.row_bytes, c));
-                }
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < CT_BATCH; k++) {
-            const int jj = b0 + k * CT_THREADS + lane8;
-            if (jj >= nr * n4) break;   // (uniform over the eight lanes of a block)
-            const int rl = jj / n4, c = 4 * (jj - rl * n4);
-            const float xv[4] = {xs[k].x, xs[k].y, xs[k].z, xs[k].w};
-            float amax = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const float t = fabsf(xv[i]);
-                if (t > amax) amax = t;
-            }
-#pragma unroll
-            for (int m = 1; m < 8; m <<= 1) {
-                const float o = __shfl_xor(amax, m);
-                amax = o > amax ? o : amax;
-            }
-            const int k8 = (c >> 2) & 7;
-            uint8_t * blk = outs + rl * row_bytes + (c >> 5) * ct_block_bytes<OUT>();
-            if constexpr (OUT == 8) {
-                const float d = amax / 127.0f;
-                const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
-                if (k8 == 0) *reinterpret_cast<uint16_t *>(blk) = f32_to_f16_ref(d);
-                uint16_t * q16 = reinterpret_cast<uint16_t *>(blk + 2 + 4 * k8);
-#pragma unroll
-                for (int i = 0; i < 2; i++) {
-                    const uint8_t q0 = (uint8_t)(int8_t)roundf(fmax_std(-128.0f, fmin_std(127.0f, xv[2 * i] * id)));
-                    const uint8_t q1 =
-                        (uint8_t)(int8_t)roundf(fmax_std(-128.0f, fmin_std(127.0f, xv[2 * i + 1] * id)));
-                    q16[i] = (uint16_t)(q0 | ((uint16_t)q1 << 8));
-                }
-            } else {
-                const float d = amax / 7.0f;
-                const float id = (d != 0.0f) ? 7.0f / amax : 0.0f;
-                if (k8 == 0) *reinterpret_cast<uint16_t *>(blk) = f32_to_f16_ref(d);
-                uint8_t by[2];
-#pragma unroll
-                for (int u = 0; u < 2; u++) {
-                    const float v0 = xv[2 * u] * id + 8.0f;
-                    const float v1 = xv[2 * u + 1] * id + 8.0f;
-                    const uint8_t q0 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v0)));
-                    const uint8_t q1 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v1)));
-                    by[u] = (uint8_t)(q0 | (q1 << 4));
-                }
-                *reinterpret_cast<uint16_t *>(blk + 2 + 2 * k8) = (uint16_t)(by[0] | ((uint16_t)by[1] << 8));
-            }
-        }
-    }
-    __syncthreads();
-    const int pieces = (int)(row_bytes >> 4);
-    // (the block's rows are consecutive in the output)
-    uint8_t * obase = dst + l * dst_ls + (long long)j0 * row_bytes;
-    for (int pp = threadIdx.x; pp < nr * pieces; pp += CT_THREADS)
-        *reinterpret_cast<uint4 *>(obase + 16LL * pp) = *reinterpret_cast<const uint4 *>(outs + 16 * pp);
 }
 
 // ---------------------------------------------------------------------------
@@ -6486,32 +6389,6 @@ void launch_requant8(const float * src, long long src_ls, long long src_ld, cons
                      long long dst_ls, hipStream_t st, RowCodec sq) {
     const long long total = (long long)L * rows * (n_el / 8);
     if (total <= 0) return;
-    const bool src_ok = mode == 1 ? (dv % 4 == 0 && (reinterpret_cast<uintptr_t>(src) & 15) == 0)
-                      : sq.base   ? ct_rows_ok(sq.type, sq.base, sq.row_bytes, sq.layer_bytes, n_el)
-                                  : ((reinterpret_cast<uintptr_t>(src) | (uintptr_t)(src_ls * 4) |
-                                      (uintptr_t)(src_ld * 4)) & 15) == 0;
-    if (src_ok && ct_rows_ok(type, dst, row_bytes, dst_ls, n_el) &&
-        (!sq.base || CT_ROWS * (row_bytes + sq.row_bytes) <= 65536)) {
-        const dim3 grid(cdiv(rows, CT_ROWS), L);
-        const size_t lds = (size_t)CT_ROWS * (row_bytes + (sq.base ? sq.row_bytes : 0));
-        auto go = [&](auto kern) {
-            hipLaunchKernelGGL(kern, grid, dim3(CT_THREADS), lds, st, src, src_ls, src_ld, idx, idx_ls,
-                               H, dv, n_el, rows, L, dst, row_bytes, dst_ls, sq);
-        };
-        const int sk = mode == 1 ? 1 : (sq.base ? sq.type : 0);
-        if (type == 8) {
-            if (sk == 0) go(k_requant_tile<0, 8>);
-            else if (sk == 1) go(k_requant_tile<1, 8>);
-            else if (sk == 8) go(k_requant_tile<8, 8>);
-            else go(k_requant_tile<2, 8>);
-        } else {
-            if (sk == 0) go(k_requant_tile<0, 2>);
-            else if (sk == 1) go(k_requant_tile<1, 2>);
-            else if (sk == 8) go(k_requant_tile<8, 2>);
-            else go(k_requant_tile<2, 2>);
-        }
-        return;
-    }
     const long long blocks = std::min<long long>((total + 255) / 256, 1LL << 30);
     hipLaunchKernelGGL(k_requant8, dim3((unsigned)blocks), dim3(256), 0, st,
                        src, src_ls, src_ld, idx, idx_ls, mode, H, dv, type, n_el, rows, L, dst, row_bytes, dst_ls, sq);
