@@ -54,7 +54,8 @@ STAGE_KERNELS = {"scores": "k_scores", "chunk_softmax_importance": "k_softmax_im
                  "selection": "k_global_importance + k_select_topk (or k_div_candidates + k_div_gram + k_div_greedy)",
                  "beta_fit": "k_gather_exp + k_ls_build + k_ge_lu + k_ge_solve (or k_nnls_lh) + k_beta_log",
                  "compacted_softmax": "k_ls_softmax", "normal_equations": "k_ls_build",
-                 "lu_factorization": "k_ge_lu", "substitution": "k_ge_subst",
+                 "lu_factorization": "k_ge_lu<false, true> (steps 0-127) + k_ge_lu_tail (the rest)",
+                 "substitution": "k_ge_subst",
                  "refinement": "k_refine_step + the beta and C_v refit per round",
                  "quality_stats": "k_scores + k_row_softmax + k_stats_sum + k_stats_final"}
 
@@ -187,39 +188,86 @@ def cpu_baseline(K, V, Q, T, H, d, ratio, L_total, diversity):
 
 
 def _pmc_per_dispatch(path: Path) -> dict:
-    """kernel -> (dispatches, {counter: mean value per dispatch}) from a rocprofv3 csv"""
+    """kernel -> (dispatches, {counter: mean value per dispatch}, mean ms per
+    dispatch) from a rocprofv3 --pmc csv"""
     import csv
-    tot, disp = {}, {}
+    tot, disp, dur = {}, {}, {}
     with open(path) as f:
         for r in csv.DictReader(f):
-            k = r["Kernel_Name"].split("(")[0]
+            k = r["Kernel_Name"].split("(")[0].replace("void ", "")
             c = tot.setdefault(k, {})
             c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
             disp.setdefault(k, set()).add(r["Dispatch_Id"])
-    return {k: (len(disp[k]), {c: v / len(disp[k]) for c, v in tot[k].items()}) for k in tot}
+            dur.setdefault(k, {})[r["Dispatch_Id"]] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6
+    return {k: (len(disp[k]), {c: v / len(disp[k]) for c, v in tot[k].items()},
+                sum(dur[k].values()) / len(dur[k])) for k in tot}
+
+
+# The counter passes of one bench step (each its own rocprofv3 run; at most 4
+# TCC and 8 SQ counters per pass on this GPU):
+PMC_PASSES = {
+    "rd": "TCC_EA0_RDREQ_128B_sum TCC_EA0_RDREQ_64B_sum TCC_EA0_RDREQ_32B_sum TCC_EA0_RDREQ_sum",
+    "wr": "TCC_EA0_WRREQ_sum TCC_EA0_WRREQ_64B_sum GRBM_GUI_ACTIVE",
+    "v1": "SQ_INSTS_VALU SQ_ACTIVE_INST_VALU SQ_THREAD_CYCLES_VALU SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_INSTS_LDS "
+          "SQ_ACTIVE_INST_LDS SQ_LDS_BANK_CONFLICT GRBM_GUI_ACTIVE",
+    "v2": "SQ_WAIT_INST_ANY SQ_WAIT_ANY SQ_ACTIVE_INST_ANY SQ_INSTS_SALU SQ_ACTIVE_INST_SCA SQ_INSTS_SMEM SQ_WAVES "
+          "SQ_INSTS_VMEM_RD GRBM_GUI_ACTIVE",
+}
+N_XCD, N_SIMD = 8, 1024   # MI355X: GRBM_GUI_ACTIVE sums the 8 XCDs' clocks; 256 CUs x 4 SIMDs
+
+
+def _read_bytes(c: dict) -> float:
+    # L2 -> fabric read requests resolved by size (the FETCH_SIZE expression
+    # counts a 128-byte request as 64 bytes on this GPU)
+    return (c.get("TCC_EA0_RDREQ_128B_sum", 0.0) * 128 + c.get("TCC_EA0_RDREQ_64B_sum", 0.0) * 64 +
+            c.get("TCC_EA0_RDREQ_32B_sum", 0.0) * 32)
+
+
+def _write_bytes(c: dict) -> float:
+    w64 = c.get("TCC_EA0_WRREQ_64B_sum", 0.0)
+    return (c.get("TCC_EA0_WRREQ_sum", 0.0) - w64) * 32 + w64 * 64
 
 
 def summarize_pmc(d: Path) -> dict:
-    """HBM bytes per dispatch of every kernel of one bench step: FETCH_SIZE and
-    WRITE_SIZE (KiB per dispatch) divided by what the same counter reads per
-    byte for the runtime's copy kernel moving a known number of bytes."""
+    """Per-kernel HBM bytes and instruction counters of one bench step, from
+    the counter passes PMC_PASSES under d/<pass>/, with the byte formulas
+    checked on the runtime's copy kernel moving a known number of bytes
+    (d/crd, d/cwr; the size in d/crd.log)."""
     calib = None
-    for line in (d / "cf.log").read_text().splitlines() if (d / "cf.log").exists() else []:
+    for line in (d / "crd.log").read_text().splitlines() if (d / "crd.log").exists() else []:
         if line.startswith("{") and "copy_calibration_bytes" in line:
             calib = json.loads(line)["copy_calibration_bytes"]
-    if calib is None:
-        raise SystemExit(f"no copy calibration log under {d}")
-    cf = _pmc_per_dispatch(d / "cf" / "run_counter_collection.csv")["__amd_rocclr_copyBuffer"][1]["FETCH_SIZE"]
-    cw = _pmc_per_dispatch(d / "cw" / "run_counter_collection.csv")["__amd_rocclr_copyBuffer"][1]["WRITE_SIZE"]
-    f_fac, w_fac = cf * 1024.0 / calib, cw * 1024.0 / calib
-    bf = _pmc_per_dispatch(d / "bf" / "run_counter_collection.csv")
-    bw = _pmc_per_dispatch(d / "bw" / "run_counter_collection.csv")
-    out = {"copy_bytes": calib, "fetch_factor": round(f_fac, 6), "write_factor": round(w_fac, 6), "kernels": {}}
-    for k, (n, c) in bf.items():
-        fk = c.get("FETCH_SIZE", 0.0)
-        wk = bw.get(k, (0, {}))[1].get("WRITE_SIZE", 0.0)
-        out["kernels"][k] = {"dispatches": n, "fetch_kib": round(fk, 1), "write_kib": round(wk, 1),
-                             "hbm_bytes": int(fk * 1024.0 / f_fac + wk * 1024.0 / w_fac)}
+    out = {"passes": PMC_PASSES, "kernels": {}}
+    if calib:
+        cr = _pmc_per_dispatch(d / "crd" / "run_counter_collection.csv")["__amd_rocclr_copyBuffer"][1]
+        cw = _pmc_per_dispatch(d / "cwr" / "run_counter_collection.csv")["__amd_rocclr_copyBuffer"][1]
+        out["copy_check"] = {"bytes": calib, "read_bytes_counted": _read_bytes(cr),
+                             "write_bytes_counted": _write_bytes(cw)}
+    P = {n: _pmc_per_dispatch(d / n / "run_counter_collection.csv") for n in PMC_PASSES}
+    for k, (n, c, ms) in P["rd"].items():
+        w = P["wr"].get(k, (0, {}, 0.0))[1]
+        v1 = P["v1"].get(k, (0, {}, 0.0))[1]
+        v2 = P["v2"].get(k, (0, {}, 0.0))[1]
+        rb, wb = _read_bytes(c), _write_bytes(w)
+        cyc = v1.get("GRBM_GUI_ACTIVE", 0.0) / N_XCD   # the dispatch's clocks
+        e = {"dispatches": n, "ms": round(ms, 4), "read_bytes": int(rb), "write_bytes": int(wb),
+             "hbm_bytes": int(rb + wb), "hbm_gbs": round((rb + wb) / (ms * 1e6), 1) if ms else None}
+        if cyc and v1:
+            e["valu_insts"] = int(v1.get("SQ_INSTS_VALU", 0.0))
+            # wave64 VALU instructions issued per SIMD per clock (two issue
+            # per four clocks from different waves at most for fp32 work)
+            e["valu_issue_per_simd_clock"] = round(v1.get("SQ_INSTS_VALU", 0.0) / (N_SIMD * cyc), 4)
+            e["valu_lane_util"] = round(v1.get("SQ_THREAD_CYCLES_VALU", 0.0) /
+                                        max(1.0, 64 * v1.get("SQ_ACTIVE_INST_VALU", 0.0)), 3)
+            e["lds_insts"] = int(v1.get("SQ_INSTS_LDS", 0.0))
+            e["lds_bank_conflict_frac"] = round(v1.get("SQ_LDS_BANK_CONFLICT", 0.0) /
+                                                max(1.0, v1.get("SQ_ACTIVE_INST_LDS", 0.0)), 4)
+        if v2:
+            wc = max(1.0, v2.get("SQ_WAVE_CYCLES", v1.get("SQ_WAVE_CYCLES", 1.0)))
+            e["salu_insts"] = int(v2.get("SQ_INSTS_SALU", 0.0))
+            e["wave_wait_frac"] = round(v2.get("SQ_WAIT_ANY", 0.0) / wc, 3)
+            e["wave_issue_wait_frac"] = round(v2.get("SQ_WAIT_INST_ANY", 0.0) / wc, 3)
+        out["kernels"][k] = e
     return out
 
 
@@ -518,13 +566,15 @@ def main():
     # FETCH_SIZE / WRITE_SIZE summary of this exact workload (copy-calibrated)
     prof = REPO / "profiles" / "hbm_traffic_100k_32layer_pmc.json"
     headline = (L, T, H, d, W, a.ratio, a.diversity) == (32, 100000, 8, 128, 32, 0.2, 1)
-    # the profiler's name of the stage's kernel (the LU's is the unmasked
-    # template instance, the one every system of this workload runs)
-    kname = {"lu_factorization": "void kvc::k_ge_lu<false>"}.get(dom, "kvc::" + STAGE_KERNELS[dom])
+    # the profiler's names of the stage's kernels (the LU: the whole-matrix
+    # kernel's split instance for steps 0-127, then the trailing-matrix
+    # kernel; every system of this workload runs these two)
+    knames = {"lu_factorization": ["kvc::k_ge_lu<false, true>", "kvc::k_ge_lu_tail"]}.get(
+        dom, ["kvc::" + STAGE_KERNELS[dom]])
     if headline and prof.exists():
-        kern = json.loads(prof.read_text())["kernels"].get(kname)
-        if kern:
-            roof["traffic"] = kern["hbm_bytes"]
+        kern = json.loads(prof.read_text())["kernels"]
+        if all(k in kern for k in knames):
+            roof["traffic"] = sum(kern[k]["hbm_bytes"] for k in knames)
             roof["traffic_source"] = str(prof.relative_to(REPO))
     stats = st.download(np.float32, L * 3).reshape(L, 3)
     del dK, dV, dQ, idx, beta, cv, st
