@@ -2850,7 +2850,7 @@ k_ls_build(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 constexpr int RG_ROWS = 256, RG_WAVES = 16, RG_COLS = 16, RG_SLOTS = 4;
 constexpr int RG_THREADS = RG_WAVES * 64;
 constexpr int LU_RING = 32;          // > 17 outstanding steps
-constexpr int LU_TROWS = 32;         // rows per pass of the transposed output write
+constexpr int LU_TROWS = 64;         // rows per pass of the transposed output write
 constexpr int LU_SPIN_LIMIT = 1 << 22;   // polls per wave over the whole factorization
 constexpr int LU_X_FLOATS = LU_RING * 64 * 4;   // X staged in the ring's LDS, LU_X_FLOATS / n rows at a time
 constexpr int LU_X_MAXQ = 1024;                 // rows of X beyond which k_ls_build forms M
@@ -2858,18 +2858,22 @@ constexpr int LU_X_MAXQ = 1024;                 // rows of X beyond which k_ls_b
 #define LU_POLL_SLEEP 1   // s_sleep units (64 clocks) between polls of a wave with slack
 #endif
 constexpr int LU_SPLIT = 128;   // k_ge_lu<false, true> takes steps before this; k_ge_lu_tail the rest
+// wave priorities in the register LU: the owners of the next LU_PRIO_HI
+// steps at 2, of the steps up to LU_PRIO_MID ahead at 1
+#ifndef LU_PRIO_HI
+#define LU_PRIO_HI 4
+#endif
+#ifndef LU_PRIO_MID
+#define LU_PRIO_MID 12
+#endif
 
 // the register LU forms M from X: a system it factors, and X of at most
 // LU_X_MAXQ rows (staged through the ring's LDS in slabs of rows)
 __device__ __forceinline__ bool lu_x_fits(int n, int nq) { return n <= RG_ROWS && nq >= 1 && nq <= LU_X_MAXQ; }
 
+// (the small arrays first: their fixed addresses stay within the 16-bit
+// offset field of the LDS instructions)
 struct LuShared {
-    union {
-        float4 fm[LU_RING][64];      // step c's multipliers in slot c % LU_RING: lane l's four rows
-        float tile[LU_TROWS][RG_ROWS + 1];   // output staging at the end
-        float xs[LU_X_FLOATS];       // X (nq x n) while the matrix is formed, when M comes from X
-    } u;
-    static_assert(sizeof(float) * LU_X_FLOATS <= sizeof(float4) * LU_RING * 64, "X staging exceeds the ring");
     int plog[RG_ROWS];               // step c's pivot row (+256: skipped); -1 until published
     union {
         struct {
@@ -2878,6 +2882,12 @@ struct LuShared {
         } p;
         int e[2 * RG_ROWS];          // the same as one array: inv entries, then phys
     } m;
+    union {
+        float4 fm[LU_RING][64];      // step c's multipliers in slot c % LU_RING: lane l's four rows
+        float tile[LU_TROWS][RG_ROWS + 1];   // output staging at the end
+        float xs[LU_X_FLOATS];       // X (nq x n) while the matrix is formed, when M comes from X
+    } u;
+    static_assert(sizeof(float) * LU_X_FLOATS <= sizeof(float4) * LU_RING * 64, "X staging exceeds the ring");
 };
 
 __device__ __forceinline__ int lu_inv_elem(int r) { return (r & 63) * 4 + (r >> 6); }
@@ -2919,11 +2929,13 @@ __device__ __forceinline__ float lu_pick(const float (&v)[RG_SLOTS], int s) {
     return (s & 2) ? hi : lo;
 }
 
+// Floating-point class tests (one v_cmp_class each, no branches). The class
+// masks: bit 0 signalling NaN, 1 quiet NaN, 2 -inf, 5 -0, 9 +inf.
+constexpr int FP_CLASS_NONFINITE = 0x207;   // NaN or +-inf
+constexpr int FP_CLASS_UNSAFE = 0x227;      // NaN, +-inf or -0
 // -0, +-inf or NaN
-__device__ __forceinline__ bool lu_unsafe(float x) {
-    const unsigned b = __float_as_uint(x);
-    return b == 0x80000000u || (b & 0x7f800000u) == 0x7f800000u;
-}
+__device__ __forceinline__ bool lu_unsafe(float x) { return __builtin_amdgcn_classf(x, FP_CLASS_UNSAFE); }
+__device__ __forceinline__ bool lu_nonfinite(float x) { return __builtin_amdgcn_classf(x, FP_CLASS_NONFINITE); }
 
 // Publish step c1 from its column's values col[] (steps < c1 applied), given
 // the logical indices iv of this lane's rows (negative for rows past n) and
@@ -3027,8 +3039,11 @@ __device__ __forceinline__ void lu_next_column(LuShared & sh, const float (&a)[R
 // u[q] = a[P][q] for the register columns q >= Q0 (pivot row in slot S, lane lP)
 template <int S, int Q0>
 __device__ __forceinline__ void lu_read_row(const float (&a)[RG_SLOTS][RG_COLS], int lP, float (&u)[RG_COLS]) {
+    // each column's pivot entry broadcast from lane lP by ds_bpermute, so
+    // that the multiplies read VGPRs only: fp32 multiplies with an SGPR
+    // operand (a v_readlane result) issue at about half the rate
 #pragma unroll
-    for (int q = Q0; q < RG_COLS; q++) u[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[S][q]), lP));
+    for (int q = Q0; q < RG_COLS; q++) u[q] = __int_as_float(__builtin_amdgcn_ds_bpermute(lP << 2, __float_as_int(a[S][q])));
 }
 
 // Apply one step to the register columns q >= Q0: a[r][q] -= f[r] * a[P][q],
@@ -3071,10 +3086,15 @@ __device__ __forceinline__ void lu_steps(LuShared & sh, float (&a)[RG_SLOTS][RG_
         if (c >= n) break;   // (a break, not a return: one exit path keeps the register assignment)
         const int slot = c & (LU_RING - 1);
         const bool prod = c + 1 < n && w == ((c + 1) & (RG_COLS - 1));
-        // the owners of columns c + 1 and c + 2 run ahead of the others on
-        // their SIMDs: the first publishes step c + 1 now, the second must be
-        // through step c by the time step c + 1 appears
-        if (prod || w == ((c + 2) & (RG_COLS - 1))) __builtin_amdgcn_s_setprio(2);
+        // the owners of the next columns run ahead of the others on their
+        // SIMDs: the owner of c + 1 publishes step c + 1 now, the owner of
+        // c + 2 must be through step c by the time step c + 1 appears, and
+        // waves that own a column a few steps ahead work off the updates they
+        // still owe before their turn comes (at equal priority the SIMDs
+        // favour older waves, and the younger ones would fall behind)
+        const int ahead = (w - c) & (RG_COLS - 1);   // this wave next publishes step c + ahead
+        if (ahead != 0 && ahead <= LU_PRIO_HI) __builtin_amdgcn_s_setprio(2);
+        else if (ahead != 0 && ahead <= LU_PRIO_MID) __builtin_amdgcn_s_setprio(1);
         else __builtin_amdgcn_s_setprio(0);
         // wait for step c (bounded: past the limit the wave stops waiting and
         // reports through *status, which the host turns into a device error).
@@ -3204,12 +3224,35 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
 #pragma unroll
             for (int q = 0; q < RG_COLS; q++) a[s][q] = 0.0f;
         }
+        // rows of X as 16-byte pieces copied straight to LDS when they allow
+        // it (global_load_lds: no registers, every piece of a slab in flight
+        // at once; a wave's 64 pieces land contiguously at the LDS address
+        // given for its first lane). The masked variant, at its register
+        // limit, keeps the plain loads.
+        const bool x4 = !MASKED && (n & 3) == 0 && (g.t_total & 3) == 0 &&
+                        (reinterpret_cast<uintptr_t>(Xh) & 15) == 0;
         for (int k0 = 0; k0 < nq; k0 += kb) {
             const int nk = min(kb, nq - k0);
             if (k0 > 0) __syncthreads();   // the previous slab has been read
-            for (int e = tid; e < nk * n; e += RG_THREADS) {
-                const int k = e / n, i = e - k * n;
-                sh.u.xs[e] = Xh[(long long)(k0 + k) * g.t_total + i];
+            if (x4) {
+                constexpr int PER = LU_X_FLOATS / 4 / RG_THREADS;
+                const int n4 = n >> 2, tot4 = (nk * n) >> 2;
+#pragma unroll
+                for (int u = 0; u < PER; u++) {
+                    const int base = u * RG_THREADS + 64 * w;   // this wave's first piece
+                    const int e4 = base + lane;
+                    if (e4 < tot4) {
+                        const int k = e4 / n4, i4 = e4 - k * n4;
+                        __builtin_amdgcn_global_load_lds(
+                            static_cast<const void *>(Xh + (long long)(k0 + k) * g.t_total + 4 * i4),
+                            (__attribute__((address_space(3))) void *)(sh.u.xs + 4 * base), 16, 0, 0);
+                    }
+                }
+            } else {
+                for (int e = tid; e < nk * n; e += RG_THREADS) {
+                    const int k = e / n, i = e - k * n;
+                    sh.u.xs[e] = Xh[(long long)(k0 + k) * g.t_total + i];
+                }
             }
             __syncthreads();
             for (int k = 0; k < nk; k++) {
@@ -3231,7 +3274,7 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
 #pragma unroll
             for (int q = 0; q < RG_COLS; q++) {
                 if (rc == cc[q]) a[s][q] = a[s][q] + g.ridge;
-                if (!MASKED) unsafe = unsafe || lu_unsafe(a[s][q]);
+                if (!MASKED) unsafe |= lu_unsafe(a[s][q]);
             }
         }
         __syncthreads();   // X is dead: the LDS becomes the step ring
@@ -3244,7 +3287,7 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
 #pragma unroll
             for (int q = 0; q < RG_COLS; q++) {
                 a[s][q] = A[(unsigned)(min(w + RG_WAVES * q, n - 1) * n + rc)];
-                if (!MASKED) unsafe = unsafe || lu_unsafe(a[s][q]);
+                if (!MASKED) unsafe |= lu_unsafe(a[s][q]);
             }
         }
     }
@@ -3284,14 +3327,19 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
         // a non-finite final entry: some step may have changed a finished row
         // (SPLIT: the entries final here, columns < 128 and the rows already
         // chosen as pivots)
+        // (bitwise operators only: short-circuit ones compile to a branch per entry)
         bool bad = false;
 #pragma unroll
-        for (int s = 0; s < RG_SLOTS; s++)
+        for (int s = 0; s < RG_SLOTS; s++) {
+            const bool rin = lane + 64 * s < n;
+            const bool rfin = rin & (!tail | (li[s] < LU_SPLIT));
 #pragma unroll
-            for (int q = 0; q < RG_COLS; q++)
-                bad = bad || (lane + 64 * s < n && w + RG_WAVES * q < n &&
-                              (!tail || w + RG_WAVES * q < LU_SPLIT || li[s] < LU_SPLIT) &&
-                              (__float_as_uint(a[s][q]) & 0x7f800000u) == 0x7f800000u);
+            for (int q = 0; q < RG_COLS; q++) {
+                // (column w + 16 q is below LU_SPLIT exactly when q is)
+                const bool use = (w + RG_WAVES * q < n) & (q < LU_SPLIT / RG_WAVES ? rin : rfin);
+                bad |= use & lu_nonfinite(a[s][q]);
+            }
+        }
         const bool redo_sys = __syncthreads_or(bad);
         if (tid == 0) redo[sys] = redo_sys ? 1 : 0;
         if (redo_sys) return;
@@ -3319,22 +3367,24 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
         skip_out[sys * (long long)g.tc_max + tid] = (unsigned char)(pl >> 8);
     }
     // every entry is final in registers: multipliers left of each row's pivot
-    // step, U from it on; rows go out through LDS, LU_TROWS at a time, as
+    // step, U from it on; rows go out through LDS, TR at a time (LU_TROWS; 32 in the masked
+    // variant, whose registers are at their limit), as
     // contiguous row segments of 256 entries, zero past column n (the
     // substitution reads whole blocks of a row without guards)
+    constexpr int TR = MASKED ? 32 : LU_TROWS;
 #pragma unroll
     for (int s = 0; s < RG_SLOTS; s++) {
 #pragma unroll
-        for (int half = 0; half < 64 / LU_TROWS; half++) {
-            const int r0 = 64 * s + LU_TROWS * half;
+        for (int half = 0; half < 64 / TR; half++) {
+            const int r0 = 64 * s + TR * half;
             if (r0 >= n) break;
-            const int lr = lane - LU_TROWS * half;
-            if (lr >= 0 && lr < LU_TROWS) {
+            const int lr = lane - TR * half;
+            if (lr >= 0 && lr < TR) {
 #pragma unroll
                 for (int q = 0; q < RG_COLS; q++) sh.u.tile[lr][w + RG_WAVES * q] = a[s][q];
             }
             __syncthreads();
-            for (int e = tid; e < LU_TROWS * RG_ROWS; e += RG_THREADS) {
+            for (int e = tid; e < TR * RG_ROWS; e += RG_THREADS) {
                 const int rr = e / RG_ROWS, j = e % RG_ROWS;
                 if (r0 + rr < n && j < n &&
                     (!tail || j < LU_SPLIT || sh.m.e[lu_inv_elem(r0 + rr)] < LU_SPLIT))
@@ -3491,7 +3541,8 @@ __device__ __forceinline__ void lp_produce(float * ring, int * plog, int * inv, 
 
 // a[r][q] -= f[r] * a[P][q] for the register columns q >= Q0 (pivot row in
 // slot SL, lane lP): each column's pivot entry read from its lane just
-// before the column is updated
+// before the column is updated (v_readlane: the ds_bpermute broadcast of
+// k_ge_lu needs registers that would cost this kernel a block per CU)
 template <int S, int Q, int SL, int Q0>
 __device__ __forceinline__ void lp_update_from(float (&a)[S][Q], const float (&f)[S], int lP) {
 #pragma unroll
@@ -3679,8 +3730,7 @@ k_ge_lu_tail(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
     for (int s = 0; s < 2; s++)
 #pragma unroll
         for (int q = 0; q < LP_Q; q++)
-            bad = bad || (lane + 64 * s < m && w + LP_WAVES * q < m &&
-                          (__float_as_uint(b[s][q]) & 0x7f800000u) == 0x7f800000u);
+            bad |= (lane + 64 * s < m) & (w + LP_WAVES * q < m) & lu_nonfinite(b[s][q]);
     const bool redo_sys = __syncthreads_or(bad);
     if (tid == 0) redo[sys] = redo_sys ? 1 : 0;
     if (redo_sys) return;
