@@ -2888,6 +2888,7 @@ struct LuShared {
         float xs[LU_X_FLOATS];       // X (nq x n) while the matrix is formed, when M comes from X
     } u;
     static_assert(sizeof(float) * LU_X_FLOATS <= sizeof(float4) * LU_RING * 64, "X staging exceeds the ring");
+    static_assert(2 * LU_X_FLOATS <= LU_TROWS * (RG_ROWS + 1), "X and its column-grouped copy exceed the union");
 };
 
 __device__ __forceinline__ int lu_inv_elem(int r) { return (r & 63) * 4 + (r >> 6); }
@@ -3037,13 +3038,20 @@ __device__ __forceinline__ void lu_next_column(LuShared & sh, const float (&a)[R
 }
 
 // u[q] = a[P][q] for the register columns q >= Q0 (pivot row in slot S, lane lP)
-template <int S, int Q0>
+template <int S, int Q0, bool MASKED>
 __device__ __forceinline__ void lu_read_row(const float (&a)[RG_SLOTS][RG_COLS], int lP, float (&u)[RG_COLS]) {
-    // each column's pivot entry broadcast from lane lP by ds_bpermute, so
-    // that the multiplies read VGPRs only: fp32 multiplies with an SGPR
-    // operand (a v_readlane result) issue at about half the rate
+    if constexpr (!MASKED) {
+        // each column's pivot entry broadcast from lane lP by ds_bpermute, so
+        // that the multiplies read VGPRs only: fp32 multiplies with an SGPR
+        // operand (a v_readlane result) issue at about half the rate
 #pragma unroll
-    for (int q = Q0; q < RG_COLS; q++) u[q] = __int_as_float(__builtin_amdgcn_ds_bpermute(lP << 2, __float_as_int(a[S][q])));
+        for (int q = Q0; q < RG_COLS; q++)
+            u[q] = __int_as_float(__builtin_amdgcn_ds_bpermute(lP << 2, __float_as_int(a[S][q])));
+    } else {
+        // (the masked variant, at its register limit, reads them into SGPRs)
+#pragma unroll
+        for (int q = Q0; q < RG_COLS; q++) u[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a[S][q]), lP));
+    }
 }
 
 // Apply one step to the register columns q >= Q0: a[r][q] -= f[r] * a[P][q],
@@ -3055,10 +3063,10 @@ __device__ __forceinline__ void lu_apply_any(float (&a)[RG_SLOTS][RG_COLS], cons
         const int lP = P & 63;
         float u[RG_COLS];
         switch (P >> 6) {
-            case 0: lu_read_row<0, Q0>(a, lP, u); break;
-            case 1: lu_read_row<1, Q0>(a, lP, u); break;
-            case 2: lu_read_row<2, Q0>(a, lP, u); break;
-            default: lu_read_row<3, Q0>(a, lP, u); break;
+            case 0: lu_read_row<0, Q0, MASKED>(a, lP, u); break;
+            case 1: lu_read_row<1, Q0, MASKED>(a, lP, u); break;
+            case 2: lu_read_row<2, Q0, MASKED>(a, lP, u); break;
+            default: lu_read_row<3, Q0, MASKED>(a, lP, u); break;
         }
 #pragma unroll
         for (int s = 0; s < RG_SLOTS; s++) {
@@ -3211,7 +3219,10 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
         // (k ascending from +0, kept in registers across the slabs of rows
         // staged in LDS), the ridge added after it
         const int nq = c.nq;
-        const int kb = LU_X_FLOATS / n;   // rows per slab (at least 32)
+        // rows per slab: at least 32; at most 32 with the second copy of the
+        // slab (256 columns a row)
+        constexpr bool XP = !MASKED;
+        const int kb = XP ? LU_X_FLOATS / RG_ROWS : LU_X_FLOATS / n;
         const long long hsX = (long long)g.nq_max * g.t_total;
         const float * Xh = X + (long long)layer * g.H * hsX + h * hsX + c.off;
         int cc[RG_COLS];
@@ -3255,13 +3266,34 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
                 }
             }
             __syncthreads();
+            // (unmasked) a second copy of the slab with each wave's 16 columns
+            // side by side (entry (k, w + 16 q) at k * 256 + 16 w + q, clamped
+            // like cc), so that a wave reads its column values as four
+            // broadcast 16-byte reads per row of X
+            float * xp = sh.u.xs + LU_X_FLOATS;
+            if constexpr (XP) {
+                for (int e = tid; e < nk * RG_ROWS; e += RG_THREADS) {
+                    const int k = e >> 8, p = e & 255;
+                    xp[e] = sh.u.xs[k * n + min((p >> 4) + RG_WAVES * (p & 15), n - 1)];
+                }
+                __syncthreads();
+            }
             for (int k = 0; k < nk; k++) {
                 const float * xk = sh.u.xs + k * n;
                 float xr[RG_SLOTS], xc[RG_COLS];
 #pragma unroll
                 for (int s = 0; s < RG_SLOTS; s++) xr[s] = xk[min(lane + 64 * s, n - 1)];
+                if constexpr (XP) {
+                    const float4 * xq = reinterpret_cast<const float4 *>(xp + k * RG_ROWS + 16 * w);
 #pragma unroll
-                for (int q = 0; q < RG_COLS; q++) xc[q] = xk[cc[q]];
+                    for (int i = 0; i < RG_COLS / 4; i++) {
+                        const float4 v = xq[i];
+                        xc[4 * i] = v.x; xc[4 * i + 1] = v.y; xc[4 * i + 2] = v.z; xc[4 * i + 3] = v.w;
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < RG_COLS; q++) xc[q] = xk[cc[q]];
+                }
 #pragma unroll
                 for (int s = 0; s < RG_SLOTS; s++)
 #pragma unroll
@@ -3384,11 +3416,25 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
                 for (int q = 0; q < RG_COLS; q++) sh.u.tile[lr][w + RG_WAVES * q] = a[s][q];
             }
             __syncthreads();
-            for (int e = tid; e < TR * RG_ROWS; e += RG_THREADS) {
-                const int rr = e / RG_ROWS, j = e % RG_ROWS;
-                if (r0 + rr < n && j < n &&
-                    (!tail || j < LU_SPLIT || sh.m.e[lu_inv_elem(r0 + rr)] < LU_SPLIT))
-                    LU[(unsigned)((r0 + rr) * RG_ROWS + j)] = sh.u.tile[rr][j];
+            // four entries a thread, one 16-byte store (a group never straddles
+            // column 128; the last one of a row with n % 4 != 0 goes entry by
+            // entry); the masked variant stores entry by entry
+            if constexpr (MASKED) {
+                for (int e = tid; e < TR * RG_ROWS; e += RG_THREADS) {
+                    const int rr = e / RG_ROWS, j = e % RG_ROWS;
+                    if (r0 + rr < n && j < n) LU[(unsigned)((r0 + rr) * RG_ROWS + j)] = sh.u.tile[rr][j];
+                }
+            } else for (int e4 = tid; e4 < TR * RG_ROWS / 4; e4 += RG_THREADS) {
+                const int rr = e4 >> 6, j = (e4 & 63) * 4, r = r0 + rr;
+                if (r < n && j < n && (!tail || j < LU_SPLIT || sh.m.e[lu_inv_elem(r)] < LU_SPLIT)) {
+                    const float * t = &sh.u.tile[rr][j];
+                    float * o = LU + (unsigned)(r * RG_ROWS + j);
+                    if (j + 4 <= n) {
+                        *reinterpret_cast<float4 *>(o) = make_float4(t[0], t[1], t[2], t[3]);
+                    } else {
+                        for (int k = 0; k < n - j; k++) o[k] = t[k];
+                    }
+                }
             }
             __syncthreads();
         }
