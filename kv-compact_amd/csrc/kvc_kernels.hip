@@ -3731,7 +3731,8 @@ __device__ __forceinline__ void lt_steps(LtShared & sh, float (&b)[2][LP_Q], int
 
 // grid (n_chunks * H, L), LP_THREADS threads: the systems of more than 128
 // unknowns that k_ge_lu<false, true> did not flag for the masked kernel
-__global__ void __launch_bounds__(LP_THREADS)
+// (at most 64 VGPRs: eight waves per SIMD, four systems per CU)
+__global__ void __launch_bounds__(LP_THREADS, 8)
 k_ge_lu_tail(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ T2,
              const int * __restrict__ map2, int * __restrict__ perm_out, unsigned char * __restrict__ skip_out,
              float * __restrict__ LU_all, int * __restrict__ redo, int * __restrict__ status) {
@@ -5893,6 +5894,154 @@ k_requant8(const float * __restrict__ src, long long src_ls, long long src_ld, c
     }
 }
 
+// The same encodings (Q8_0 / Q4_0, the same arithmetic as k_requant8) one
+// wave per row, for rows whose encoded bytes are whole 16-byte pieces at
+// 16-byte aligned addresses. A row goes in chunks of up to 1024 elements:
+// lane l takes elements 16 l .. 16 l + 15 of the chunk (half a 32-element
+// block; the block's amax comes from the lane pair), writes its scale and
+// codes into the wave's LDS copy of the chunk's encoded bytes, and the wave
+// stores that copy as 16-byte pieces. Sources: MODE 0 gathered fp32 rows
+// (src + l src_ls + idx[l idx_ls + j] src_ld), MODE 1 C_v [L][H][rows][dv],
+// MODE 2 kept rows of a quantized cache (sq, rows staged into LDS as 16-byte
+// pieces and decoded there).
+constexpr int RQ_WAVES = 4;
+constexpr int RQ_CHUNK = 1024;                 // elements per chunk
+constexpr int RQ_BYTES = RQ_CHUNK / 32 * 34;   // encoded bytes of a chunk, at most (Q8_0)
+
+template <int TYPE, int MODE>
+__global__ void __launch_bounds__(64 * RQ_WAVES)
+k_requant_rows(const float * __restrict__ src, long long src_ls, long long src_ld, const int * __restrict__ idx,
+               long long idx_ls, int H, int dv, int n_el, int rows, int L, uint8_t * __restrict__ dst,
+               long long row_bytes, long long dst_ls, RowCodec sq) {
+    constexpr int BB = TYPE == 8 ? 34 : 18;    // bytes per block
+    __shared__ __align__(16) uint8_t st_out[RQ_WAVES][RQ_BYTES];
+    __shared__ __align__(16) uint8_t st_in[MODE == 2 ? RQ_WAVES : 1][MODE == 2 ? RQ_BYTES : 16];
+    const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    uint8_t * so = st_out[w];
+    const long long nrows = (long long)L * rows;
+    const long long step = (long long)gridDim.x * RQ_WAVES;
+    // the raw source of one chunk of row rw (MODE 2: 16-byte pieces lane and
+    // lane + 64 of the encoded row; else the lane's 16 values)
+    auto fetch = [&](long long rw, int c0, float (&x)[16], uint4 & raw0, uint4 & raw1) {
+        const int l = (int)(rw / rows);
+        const long long j = rw - (long long)l * rows;
+        const int ce = min(RQ_CHUNK, n_el - c0);
+        if constexpr (MODE == 2) {
+            const uint8_t * irow = codec_row(sq, l, idx[l * idx_ls + j]) + c0 / 32 * BB;
+            const int np = ce / 32 * BB / 16;
+            if (lane < np) raw0 = *reinterpret_cast<const uint4 *>(irow + 16 * lane);
+            if (lane + 64 < np) raw1 = *reinterpret_cast<const uint4 *>(irow + 16 * (lane + 64));
+        } else {
+            const float * xs;
+            if constexpr (MODE == 0) {
+                xs = src + l * src_ls + (long long)idx[l * idx_ls + j] * src_ld + c0 + 16 * lane;
+            } else {
+                const int e = c0 + 16 * lane, h = e / dv, v = e - h * dv;
+                xs = src + (((long long)l * H + h) * rows + j) * dv + v;
+            }
+            const bool on = lane < ce / 16;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 v = on ? reinterpret_cast<const float4 *>(xs)[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+            }
+        }
+    };
+    // encode one chunk of row rw from its fetched source and store it
+    auto put = [&](long long rw, int c0, float (&x)[16], const uint4 & raw0, const uint4 & raw1) {
+        const int l = (int)(rw / rows);
+        const long long j = rw - (long long)l * rows;
+        const int ce = min(RQ_CHUNK, n_el - c0);   // a multiple of 256
+        const int nb = ce / 32 * BB;                // encoded bytes (a multiple of 16)
+        const bool on = lane < ce / 16;
+        if constexpr (MODE == 2) {
+            uint8_t * si = st_in[w];
+            if (lane < nb / 16) *reinterpret_cast<uint4 *>(si + 16 * lane) = raw0;
+            if (lane + 64 < nb / 16) *reinterpret_cast<uint4 *>(si + 16 * (lane + 64)) = raw1;
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront", "local");
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 v = on ? codec_dec4<TYPE>(codec_raw4_at<TYPE>(si, 16 * lane + 4 * i))
+                                    : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+            }
+        }
+        float amax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const float t = fabsf(x[i]);
+            if (t > amax) amax = t;
+        }
+        const float o1 = __shfl_xor(amax, 1);
+        amax = o1 > amax ? o1 : amax;
+        const int b = lane >> 1, half = lane & 1;
+        uint16_t * ob = reinterpret_cast<uint16_t *>(so + b * BB);   // 2-byte aligned
+        if (on) {
+            if constexpr (TYPE == 8) {
+                const float d = amax / 127.0f;
+                const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
+                if (half == 0) ob[0] = f32_to_f16_ref(d);
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const uint8_t q0 = (uint8_t)(int8_t)roundf(fmax_std(-128.0f, fmin_std(127.0f, x[2 * i] * id)));
+                    const uint8_t q1 = (uint8_t)(int8_t)roundf(fmax_std(-128.0f, fmin_std(127.0f, x[2 * i + 1] * id)));
+                    ob[1 + 8 * half + i] = (uint16_t)(q0 | ((uint16_t)q1 << 8));
+                }
+            } else {
+                const float d = amax / 7.0f;
+                const float id = (d != 0.0f) ? 7.0f / amax : 0.0f;
+                if (half == 0) ob[0] = f32_to_f16_ref(d);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    uint8_t by[2];
+#pragma unroll
+                    for (int u = 0; u < 2; u++) {
+                        const float v0 = x[4 * i + 2 * u] * id + 8.0f;
+                        const float v1 = x[4 * i + 2 * u + 1] * id + 8.0f;
+                        const uint8_t q0 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v0)));
+                        const uint8_t q1 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v1)));
+                        by[u] = (uint8_t)(q0 | (q1 << 4));
+                    }
+                    ob[1 + 4 * half + i] = (uint16_t)(by[0] | ((uint16_t)by[1] << 8));
+                }
+            }
+        }
+        // the wave's LDS writes are done before its reads of the copy
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront", "local");
+        uint8_t * orow = dst + l * dst_ls + j * row_bytes + c0 / 32 * BB;
+        for (int p = lane; p < nb / 16; p += 64)
+            *reinterpret_cast<uint4 *>(orow + 16 * p) = *reinterpret_cast<const uint4 *>(so + 16 * p);
+        // (the copies are rewritten for the next chunk or row only after these reads)
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront", "local");
+    };
+    const long long rw0 = (long long)blockIdx.x * RQ_WAVES + w;
+    float x[16];
+    uint4 raw0 = make_uint4(0, 0, 0, 0), raw1 = raw0;
+    if (n_el <= RQ_CHUNK) {
+        // one chunk a row: the next row's source is fetched before this row is encoded
+        float xn[16];
+        uint4 rn0 = raw0, rn1 = raw0;
+        if (rw0 < nrows) fetch(rw0, 0, xn, rn0, rn1);
+        for (long long rw = rw0; rw < nrows; rw += step) {
+#pragma unroll
+            for (int i = 0; i < 16; i++) x[i] = xn[i];
+            raw0 = rn0;
+            raw1 = rn1;
+            if (rw + step < nrows) fetch(rw + step, 0, xn, rn0, rn1);
+            put(rw, 0, x, raw0, raw1);
+        }
+    } else {
+        for (long long rw = rw0; rw < nrows; rw += step)
+            for (int c0 = 0; c0 < n_el; c0 += RQ_CHUNK) {
+                fetch(rw, c0, x, raw0, raw1);
+                put(rw, c0, x, raw0, raw1);
+            }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Codec row tiles for the whole-cache decode (Q8_0 / Q4_0 rows whose byte
 // length is a multiple of 16, at 16-byte aligned addresses): a block stages
@@ -6485,6 +6634,35 @@ void launch_requant8(const float * src, long long src_ls, long long src_ld, cons
                      long long dst_ls, hipStream_t st, RowCodec sq) {
     const long long total = (long long)L * rows * (n_el / 8);
     if (total <= 0) return;
+    // one wave per row where the encoded rows are whole 16-byte pieces
+    auto a16 = [](const void * p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    if ((type == 8 || type == 2) && n_el % 256 == 0 && row_bytes % 16 == 0 && dst_ls % 16 == 0 && a16(dst)) {
+        int m = -1;
+        if (mode == 0 && sq.base) {
+            if (sq.type == type && sq.row_bytes % 16 == 0 && sq.layer_bytes % 16 == 0 && a16(sq.base)) m = 2;
+        } else if (mode == 0) {
+            if (a16(src) && src_ls % 4 == 0 && src_ld % 4 == 0) m = 0;
+        } else if (a16(src) && dv % 16 == 0) {
+            m = 1;
+        }
+        if (m >= 0) {
+            const long long nrows = (long long)L * rows;
+            // (one row a wave: measured faster than a grid of 2048 blocks whose
+            // waves fetch each next row while they encode the current one)
+            const dim3 grid((unsigned)std::min<long long>((nrows + RQ_WAVES - 1) / RQ_WAVES, 1LL << 20));
+            const dim3 blk(64 * RQ_WAVES);
+#define KVC_RQ(T_, M_)                                                                                           \
+    hipLaunchKernelGGL((k_requant_rows<T_, M_>), grid, blk, 0, st, src, src_ls, src_ld, idx, idx_ls, H, dv, n_el, \
+                       rows, L, dst, row_bytes, dst_ls, sq)
+            if (type == 8) {
+                if (m == 0) KVC_RQ(8, 0); else if (m == 1) KVC_RQ(8, 1); else KVC_RQ(8, 2);
+            } else {
+                if (m == 0) KVC_RQ(2, 0); else if (m == 1) KVC_RQ(2, 1); else KVC_RQ(2, 2);
+            }
+#undef KVC_RQ
+            return;
+        }
+    }
     const long long blocks = std::min<long long>((total + 255) / 256, 1LL << 30);
     hipLaunchKernelGGL(k_requant8, dim3((unsigned)blocks), dim3(256), 0, st,
                        src, src_ls, src_ld, idx, idx_ls, mode, H, dv, type, n_el, rows, L, dst, row_bytes, dst_ls, sq);
