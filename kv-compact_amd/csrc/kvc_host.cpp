@@ -602,7 +602,9 @@ size_t workspace_bytes(const Plan & pl, const BatchIO & io, const kv_compact_par
     for (int c = 0; c < pl.n_chunks; c++) tc_min = std::min(tc_min, pl.chunks[c].tc);
     const size_t ut_rows = tc_min <= 256 ? 256 : 0;
     ww.skip = cv.take<unsigned char>(L * nc * H * (size_t)pl.tc_max);
-    ww.LU = cv.take<float>(L * nc * H * ut_rows * ut_rows);
+    // (one row of padding: the back substitution's U-row loads run up to 247
+    // entries past a row's end, values it never uses)
+    ww.LU = cv.take<float>(L * nc * H * ut_rows * ut_rows + (ut_rows ? 256 : 0));
     ww.Bt = cv.take<float>(L * nc * H * ut_rows * dv);
     // trailing matrices of the split register LU (systems of 129 .. 256 unknowns)
     const bool split = ut_rows && pl.tc_max > 128;

@@ -4343,10 +4343,15 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 //    one in the last block; once solved groups fill the stack the oldest
 //    moves to the LDS slot of the y group just consumed.
 // Between the passes the blocks are permuted statically into the backward's
-// order. Rows of L and U are the same for every lane of a wave and come
-// through scalar loads. The forward pass sums four rows side by side
-// (independent chains); the backward pass is one chain per column (each row's
-// sum starts with the row solved just before it). Rows past n are processed
+// order. Entries of L and U are the same for every lane of a wave: they come
+// in vector loads that replicate sixteen of them in each 16-lane row, and a
+// DPP broadcast folds each into the multiply that uses it (an SGPR operand,
+// which a scalar load would give, costs the multiply as much issue time, and
+// scalar loads return out of order, so a pipeline of them waits on all at
+// once; vector loads return in order and run several blocks ahead). The
+// forward pass sums the eight rows of a group side by side (independent
+// chains); the backward pass is one chain per column (each row's sum starts
+// with the row solved just before it). Rows past n are processed
 // as zero rows: their values stay zero and the factor array holds zeros in
 // their columns, so their terms (0 * 0 subtracted from a sum that is never -0)
 // change nothing and the sums need no guards.
@@ -4372,11 +4377,16 @@ __device__ __forceinline__ void sb_wait_scalar() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-// perm[i] for a uniform i, from the lanes' entries (perm[l + 64 s] in slot s)
+// slot s of the lanes' permutation entries (perm[l + 64 s] in lane l), for a
+// uniform s; masks rather than a select chain, which the compiler may turn
+// into an indexed private array
+__device__ __forceinline__ int sb_pvslot(const int (&pv)[4], int s) {
+    return (pv[0] & -(int)(s == 0)) | (pv[1] & -(int)(s == 1)) | (pv[2] & -(int)(s == 2)) | (pv[3] & -(int)(s == 3));
+}
+
+// perm[i] for a uniform i, from the lanes' entries
 __device__ __forceinline__ int sb_perm(const int (&pv)[4], int i) {
-    const int s = i >> 6;
-    const int v = s == 0 ? pv[0] : s == 1 ? pv[1] : s == 2 ? pv[2] : pv[3];
-    return __builtin_amdgcn_readlane(v, i & 63);
+    return __builtin_amdgcn_readlane(sb_pvslot(pv, i >> 6), i & 63);
 }
 
 // push a group onto the register stack
@@ -4389,126 +4399,145 @@ __device__ __forceinline__ void sb_push(float (&R)[SB_RG][SB_G], const float (&g
     for (int j = 0; j < SB_G; j++) R[0][j] = g[j];
 }
 
-// val[t] -= l[t][j] * y[j] for the four rows t, j ascending
-__device__ __forceinline__ void sb_fterms(float (&val)[4], const float (&l)[4][4], const float * y) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        float pr[4];
-#pragma unroll
-        for (int t = 0; t < 4; t++) pr[t] = l[t][j] * y[j];
-#pragma unroll
-        for (int t = 0; t < 4; t++) val[t] = val[t] - pr[t];
-    }
+// lane L of each 16-lane row of v, in every lane (DPP row_newbcast, folded
+// into the instruction that uses it)
+template <int L>
+__device__ __forceinline__ float sb_bc(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xf, 0xf, false));
 }
 
-// Forward pass for four rows r0 .. r0+3 of group gi (r0 = 8 gi, or 8 gi + 4
-// for the second half): the steps of every earlier group, then (second half)
-// the first half's four steps, then the half's own steps. ya: the first
-// half's results.
-template <bool SECOND>
-__device__ __forceinline__ void sb_fhalf(float (&val)[4], const float (&R)[SB_RG][SB_G], float (*zl)[64],
-                                         const float * const (&lr)[4], const float (&ya)[4], int gi, int lane) {
-    int cnt = min(gi, SB_RG);
-    // (opaque to the compiler, so that each half tests its own copy rather
-    // than keeping the other half's test results alive)
-    asm volatile("" : "+s"(cnt));
-    // register groups, oldest first: block m holds group cnt - 1 - m
-    float lc[4][4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) sb_load(lc[t], lr[t], 0);
-#pragma unroll
-    for (int m = SB_RG - 1; m >= 0; m--) {
-        if (m >= cnt) continue;
-        const int k0 = SB_G * (cnt - 1 - m);
-        // steps k0 .. k0 + 3 (lc), then k0 + 4 .. k0 + 7
-        sb_wait_scalar();
-        float ln[4][4];
-#pragma unroll
-        for (int t = 0; t < 4; t++) sb_load(ln[t], lr[t], k0 + 4);
-        __builtin_amdgcn_sched_barrier(0);
-        sb_fterms(val, lc, &R[m][0]);
-        sb_wait_scalar();
-#pragma unroll
-        for (int t = 0; t < 4; t++) sb_load(lc[t], lr[t], k0 + 8);   // the next group's steps
-        __builtin_amdgcn_sched_barrier(0);
-        sb_fterms(val, ln, &R[m][4]);
-    }
-    // LDS groups SB_RG .. gi - 1 (lc holds their first four steps when there are any)
-    for (int G = SB_RG; G < gi; G++) {
-        const int k0 = SB_G * G;
-        float y[SB_G];
-#pragma unroll
-        for (int j = 0; j < SB_G; j++) y[j] = zl[SB_G * (G - SB_RG) + j][lane];
-        sb_wait_scalar();
-        float ln[4][4];
-#pragma unroll
-        for (int t = 0; t < 4; t++) sb_load(ln[t], lr[t], k0 + 4);
-        __builtin_amdgcn_sched_barrier(0);
-        sb_fterms(val, lc, y);
-        sb_wait_scalar();
-#pragma unroll
-        for (int t = 0; t < 4; t++) sb_load(lc[t], lr[t], min(k0 + 8, RG_ROWS - 4));
-        __builtin_amdgcn_sched_barrier(0);
-        sb_fterms(val, ln, y + 4);
-    }
-    // this group's steps: the first half's rows (second half only), then the
-    // half's own rows in order; lc holds the entries of steps 8 gi .. 8 gi + 3
-    sb_wait_scalar();
-    const int g0 = SB_G * gi;
-    if (SECOND) {
-        sb_fterms(val, lc, ya);
-#pragma unroll
-        for (int t = 0; t < 4; t++) sb_load(lc[t], lr[t], g0 + 4);
-        sb_wait_scalar();
-    }
-    // (lc: the entries of the half's own steps)
-#pragma unroll
-    for (int t = 1; t < 4; t++) {
-#pragma unroll
-        for (int r = 0; r < t; r++) val[t] = val[t] - lc[t][r] * val[r];
-    }
+// Forward pass: the eight rows of a group side by side (eight independent
+// sums share each y value). The entries of the eight L rows for the eight
+// steps of one earlier group come in one 16-byte vector load per lane: lane l
+// of every 16-lane row loads entries 8 G + 4 (l & 1) .. + 3 of row
+// (l & 15) >> 1, so component q holds L[t][8 G + 4 j4 + q] in lane 2 t + j4
+// of each 16-lane row, and a DPP broadcast folds it into the multiply. Vector
+// loads return in order, so the loads run SB_FD groups ahead of the
+// arithmetic (SB_FD + 1 buffers: a block issues its load into the buffer
+// the block before it used, then works on its own) with no wait beyond the
+// one for the group being used.
+constexpr int SB_FD = 2;
+constexpr int SB_FB = SB_FD + 1;
+constexpr int SB_FSINK = 11;   // the block of the load sequence that issues the cache warm-up loads
+
+__device__ __forceinline__ float4 sb_fload(const float * __restrict__ LU, unsigned off) {
+    return *reinterpret_cast<const float4 *>(LU + off);
 }
 
-// one group of the forward pass: its eight results in yg (zero past n)
+// L[T][8 G + J] from the group's load, in every lane
+template <int J, int T>
+__device__ __forceinline__ float sb_fl(const float4 & b) {
+    constexpr int q = J & 3;
+    return sb_bc<2 * T + (J >> 2)>(q == 0 ? b.x : q == 1 ? b.y : q == 2 ? b.z : b.w);
+}
+
+// val[t] -= L[t][8 G + J] * y for the eight rows t
+template <int J, int... T>
+__device__ __forceinline__ void sb_fstep(float (&val)[SB_G], const float4 & b, float y,
+                                         std::integer_sequence<int, T...>) {
+    float pr[SB_G];
+    ((pr[T] = sb_fl<J, T>(b) * y), ...);
+    ((val[T] = val[T] - pr[T]), ...);
+}
+
+// the eight steps of one earlier group, ascending
+template <int... J>
+__device__ __forceinline__ void sb_fterms(float (&val)[SB_G], const float4 & b, const float * y,
+                                          std::integer_sequence<int, J...>) {
+    (sb_fstep<J>(val, b, y[J], std::make_integer_sequence<int, SB_G>{}), ...);
+}
+
+// the group's own steps: row T takes steps 8 gi + R, R < T, ascending, from
+// the rows finished before it
+template <int T, int... R>
+__device__ __forceinline__ void sb_ftri_row(float (&val)[SB_G], const float4 & b, std::integer_sequence<int, R...>) {
+    ((val[T] = val[T] - sb_fl<R, T>(b) * val[R]), ...);
+}
+template <int... T>
+__device__ __forceinline__ void sb_ftri(float (&val)[SB_G], const float4 & b, std::integer_sequence<int, T...>) {
+    (sb_ftri_row<T>(val, b, std::make_integer_sequence<int, T>{}), ...);
+}
+
+// one group of the forward pass: its eight results in yg (zero past n). Rows
+// 8 gi .. 8 gi + 7 take the steps of every earlier group (the register
+// stack oldest first, then the LDS groups), then the group's own steps.
 __device__ __forceinline__ void sb_fgroup(float (&yg)[SB_G], const float (&R)[SB_RG][SB_G], float (*zl)[64],
                                           const float * __restrict__ LU, const float * __restrict__ B,
                                           const int (&pv)[4], int gi, int n, int p, int vc, int lane, float & pf) {
-    if (SB_G * gi < n) {
-        // the next group's eight L rows into the caches (lane l: line l & 15
-        // of row l >> 4 of each half; the value only feeds the sink)
-        {
-            const int r = min(SB_G * (gi + 1) + (lane >> 4), n - 1);
-            const int r2 = min(SB_G * (gi + 1) + 4 + (lane >> 4), n - 1);
-            const int pr = __builtin_amdgcn_ds_bpermute(4 * (r & 63), r < 64 ? pv[0] : r < 128 ? pv[1] : r < 192 ? pv[2] : pv[3]);
-            const int pr2 = __builtin_amdgcn_ds_bpermute(4 * (r2 & 63), r2 < 64 ? pv[0] : r2 < 128 ? pv[1] : r2 < 192 ? pv[2] : pv[3]);
-            pf = fmaxf(pf, LU[(unsigned)(pr * RG_ROWS + 16 * (lane & 15))]);
-            pf = fmaxf(pf, LU[(unsigned)(pr2 * RG_ROWS + 16 * (lane & 15))]);
-        }
-        float ya[4], yb[4];
-        const float * lr[4];
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int pr = sb_perm(pv, min(SB_G * gi + t, n - 1));
-            lr[t] = LU + (unsigned)(pr * RG_ROWS);
-            ya[t] = B[(unsigned)(pr * p + vc)];
-        }
-        sb_fhalf<false>(ya, R, zl, lr, ya, gi, lane);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int pr = sb_perm(pv, min(SB_G * gi + 4 + t, n - 1));
-            lr[t] = LU + (unsigned)(pr * RG_ROWS);
-            yb[t] = B[(unsigned)(pr * p + vc)];
-        }
-        sb_fhalf<true>(yb, R, zl, lr, ya, gi, lane);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            yg[t] = SB_G * gi + t < n ? ya[t] : 0.0f;
-            yg[4 + t] = SB_G * gi + 4 + t < n ? yb[t] : 0.0f;
-        }
-    } else {
+    if (SB_G * gi >= n) {
 #pragma unroll
         for (int j = 0; j < SB_G; j++) yg[j] = 0.0f;
+        return;
     }
+    // the lane's L row for the group's loads (rows past n read row n - 1,
+    // whose results are discarded); the group's rows share one 64-row slot
+    // of the permutation
+    const int rt = min(SB_G * gi + ((lane & 15) >> 1), n - 1);
+    const int prow = __builtin_amdgcn_ds_bpermute(4 * (rt & 63), sb_pvslot(pv, gi >> 3));
+    const unsigned vb = (unsigned)(prow * RG_ROWS + 4 * (lane & 1));
+    float val[SB_G];
+#pragma unroll
+    for (int t = 0; t < SB_G; t++) {
+        const int pr = sb_perm(pv, min(SB_G * gi + t, n - 1));
+        val[t] = B[(unsigned)(pr * p + vc)];
+    }
+    int cnt = min(gi, SB_RG);
+    // (opaque to the compiler, so that each block tests it afresh rather than
+    // keeping 23 comparison results alive)
+    asm volatile("" : "+s"(cnt));
+    // Register groups, oldest first: block m holds group cnt - 1 - m. Block m
+    // uses buffer m % SB_FB, which block m + SB_FD loaded: every block,
+    // m = SB_RG + SB_FD - 1 .. 0, first loads the group SB_FD blocks on (its
+    // index clamped to 0 .. gi) into the buffer of block m + 1, then (m <
+    // cnt) works on its own. The blocks not in use load too, so that every
+    // path through the sequence issues the same loads and each wait is for
+    // exactly the load it needs. The last loads go past the register groups:
+    // to the LDS groups, or to group gi (the group's own steps).
+    float4 fb[SB_FB];
+    float w[3];
+#pragma unroll
+    for (int m = SB_RG + SB_FD - 1; m >= 0; m--) {
+        const int G = min(max(cnt - 1 - m + SB_FD, 0), gi);
+        fb[(m + 1) % SB_FB] = sb_fload(LU, vb + SB_G * G);
+        if (m == SB_FSINK) {
+            // the next group's eight L rows (lane l: line l & 15 of row
+            // l >> 4 of each half) and right-hand-side rows (lane l: 64 bytes
+            // of row l >> 3) into the caches, so that its first loads hit
+            // them; the values only feed the sink, at the end of the group.
+            // Issued here, mid-sequence, because the loads after them in the
+            // in-order queue are not waited for until several blocks on.
+            const int r = min(SB_G * (gi + 1) + (lane >> 4), n - 1);
+            const int r2 = min(SB_G * (gi + 1) + 4 + (lane >> 4), n - 1);
+            const int r3 = min(SB_G * (gi + 1) + (lane >> 3), n - 1);
+            const int pr = __builtin_amdgcn_ds_bpermute(4 * (r & 63), sb_pvslot(pv, r >> 6));
+            const int pr2 = __builtin_amdgcn_ds_bpermute(4 * (r2 & 63), sb_pvslot(pv, r2 >> 6));
+            const int pr3 = __builtin_amdgcn_ds_bpermute(4 * (r3 & 63), sb_pvslot(pv, r3 >> 6));
+            w[0] = LU[(unsigned)(pr * RG_ROWS + 16 * (lane & 15))];
+            w[1] = LU[(unsigned)(pr2 * RG_ROWS + 16 * (lane & 15))];
+            w[2] = B[(unsigned)(pr3 * p + min(16 * (lane & 7), p - 1))];
+        }
+        if (m < SB_RG && m < cnt)
+            sb_fterms(val, fb[m % SB_FB], &R[m][0], std::make_integer_sequence<int, SB_G>{});
+    }
+    // blocks 1 and 0 loaded groups cnt and cnt + 1 (clamped to gi) into
+    // buffers 2 and 1; the LDS groups SB_RG .. gi - 1 (present only when the
+    // stack is full) continue the sequence, and the group after the last
+    // one, gi, ends in cur
+    static_assert(SB_FD == 2 && SB_FB == 3, "the buffer rotation assumes two groups in flight");
+    float4 cur = fb[2], nxt = fb[1];
+    for (int G = SB_RG; G < gi; G++) {
+        const float4 fre = sb_fload(LU, vb + SB_G * min(G + SB_FD, gi));
+        float y[SB_G];
+#pragma unroll
+        for (int j = 0; j < SB_G; j++) y[j] = zl[SB_G * (G - SB_RG) + j][lane];
+        sb_fterms(val, cur, y, std::make_integer_sequence<int, SB_G>{});
+        cur = nxt;
+        nxt = fre;
+    }
+    sb_ftri(val, cur, std::make_integer_sequence<int, SB_G>{});
+#pragma unroll
+    for (int t = 0; t < SB_G; t++) yg[t] = SB_G * gi + t < n ? val[t] : 0.0f;
+    pf = fmaxf(pf, fmaxf(w[0], fmaxf(w[1], w[2])));
 }
 
 __device__ __forceinline__ void sb_forward(float (&R)[SB_RG][SB_G], float (*zl)[64], const float * __restrict__ LU,
@@ -4530,17 +4559,24 @@ __device__ __forceinline__ void sb_forward(float (&R)[SB_RG][SB_G], float (*zl)[
 
 // Backward pass. On entry block m holds y group SB_LG + m and LDS slot s y
 // group s; on exit block m holds x group m and LDS slot s x group SB_RG + s.
-// lane L of each 16-lane row of v, in every lane (DPP row_newbcast, folded
-// into the instruction that uses it)
-template <int L>
-__device__ __forceinline__ float sb_bc(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xf, 0xf, false));
-}
+// A row's U entries come in vector loads from its group's first column g0,
+// sixteen entries per register (register i: entries g0 + 16 i + 0..15, each
+// in every 16-lane row), and a DPP broadcast folds each into its multiply.
+// Registers 0..11 cover the register blocks (entries g0 + 8 .. g0 + 191),
+// 12..15 the LDS slots (g0 + 192 .. g0 + 255). Loads past the row's end
+// (g0 + 16 i + 15 > 255, at most 247 entries) read the next physical row, or
+// for the last row of the last system the factor array's padding; those
+// entries are never used. One address per row, the registers at immediate
+// offsets. The next row's entries load while a row runs.
+constexpr int SB_US = RG_ROWS / 16;
 
-// backward pass: a U row from its group's first column g0, sixteen entries
-// per register (register i: entries g0 + 16 i + 0..15, each in every 16-lane
-// row), far enough for the register blocks (entries g0 .. g0 + 207)
-constexpr int SB_US = (SB_G * (SB_RG + 2) + 15) / 16;
+__device__ __forceinline__ void sb_uload(float (&us)[SB_US], const float * __restrict__ LU, const int (&pv)[4],
+                                         int col, int lane) {
+    const int g0 = col & ~(SB_G - 1);
+    const float * __restrict__ rp = LU + (unsigned)(sb_perm(pv, col) * RG_ROWS + g0 + (lane & 15));
+#pragma unroll
+    for (int i = 0; i < SB_US; i++) us[i] = rp[16 * i];
+}
 
 // products of register block M (entries g0 + 8 (M + 1) + J) with its results
 template <int M, int... J>
@@ -4563,6 +4599,22 @@ __device__ __forceinline__ void sb_bblocks(float & val, const float (&us)[SB_US]
                                            int nxr, std::integer_sequence<int, M...>) {
     (sb_bblock<M>(val, us, R, nxr), ...);
 }
+// LDS slot gb + D (solved group gb + SB_RG + D, entries g0 + 8 (SB_RG + D) + J)
+template <int D, int... J>
+__device__ __forceinline__ void sb_bslot(float & val, const float (&us)[SB_US], float (*zl)[64], int gb, int lane,
+                                         std::integer_sequence<int, J...>) {
+    if (gb + D < SB_LG) {
+        float x[SB_G], pr[SB_G];
+        ((x[J] = zl[SB_G * (gb + D) + J][lane]), ...);
+        ((pr[J] = sb_bc<(SB_G * (SB_RG + D) + J) % 16>(us[(SB_G * (SB_RG + D) + J) / 16]) * x[J]), ...);
+        ((val = val - pr[J]), ...);
+    }
+}
+template <int... D>
+__device__ __forceinline__ void sb_bslots(float & val, const float (&us)[SB_US], float (*zl)[64], int gb, int lane,
+                                          std::integer_sequence<int, D...>) {
+    (sb_bslot<D + 1>(val, us, zl, gb, lane, std::make_integer_sequence<int, SB_G>{}), ...);
+}
 // the rows above col in its group (entries g0 + J, J > k), ascending
 template <int... J>
 __device__ __forceinline__ void sb_bgroup_terms(float & val, float us0, const float (&xw)[SB_G], int k,
@@ -4570,10 +4622,12 @@ __device__ __forceinline__ void sb_bgroup_terms(float & val, float us0, const fl
     ((val = J > k ? val - sb_bc<J>(us0) * xw[J] : val), ...);
 }
 
-// one group of the backward pass: its results xw from its y values yw
+// one group of the backward pass: its results xw from its y values yw; us
+// holds the U entries of the group's first row (the highest one below n) on
+// entry and those of the next group's first row on exit
 __device__ __forceinline__ void sb_bgroup(float (&xw)[SB_G], const float (&yw)[SB_G], const float (&R)[SB_RG][SB_G],
                                           float (*zl)[64], const float * __restrict__ LU, const int (&pv)[4],
-                                          int gb, int n, float zero_val, int lane, float & pf) {
+                                          int gb, int n, float zero_val, int lane, float (&us)[SB_US]) {
         const int nx = min(SB_NG - 1 - gb, SB_RG);   // solved groups in registers
         // the group's y values, read by row through the LDS window after the
         // stored rows
@@ -4584,13 +4638,10 @@ __device__ __forceinline__ void sb_bgroup(float (&xw)[SB_G], const float (&yw)[S
         const int g0 = SB_G * gb;
         for (int col = min(g0 + SB_G, n) - 1; col >= g0; col--) {
             const int k = col - g0;
-            const float * __restrict__ ur = LU + (unsigned)(sb_perm(pv, col) * RG_ROWS);
-            // the next row's sixteen 64-byte lines into the caches while
-            // this row runs (one load; the value only feeds the sink)
-            pf = fmaxf(pf, LU[(unsigned)(sb_perm(pv, max(col - 1, 0)) * RG_ROWS + 16 * (lane & 15))]);
-            float us[SB_US];
-#pragma unroll
-            for (int i = 0; i < SB_US; i++) us[i] = ur[min(g0 + 16 * i + (lane & 15), RG_ROWS - 1)];
+            // the next row's entries (the next group's first row after the
+            // last one here) while this row runs
+            float un[SB_US];
+            sb_uload(un, LU, pv, max(col - 1, 0), lane);
             const float yk = zl[SB_LDS + k][lane];
             const float piv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(us[0]), k));
             float val = zero_val;
@@ -4603,28 +4654,26 @@ __device__ __forceinline__ void sb_bgroup(float (&xw)[SB_G], const float (&yw)[S
                 asm volatile("" : "+s"(nxr));
                 sb_bblocks(val, us, R, nxr, std::make_integer_sequence<int, SB_RG>{});
                 // solved groups gb + SB_RG + 1 .. 31 in LDS slots gb + 1 .. SB_LG - 1
-                for (int s = gb + 1; s < SB_LG; s++) {
-                    float uc[SB_G];
-                    sb_load(uc, ur, SB_G * (s + SB_RG));
-                    sb_wait_scalar();
-#pragma unroll
-                    for (int j = 0; j < SB_G; j++) val = val - uc[j] * zl[SB_G * s + j][lane];
-                }
+                sb_bslots(val, us, zl, gb, lane, std::make_integer_sequence<int, SB_LG - 1>{});
                 val = val / piv;
             }
 #pragma unroll
             for (int j = 0; j < SB_G; j++) xw[j] = k == j ? val : xw[j];
+#pragma unroll
+            for (int i = 0; i < SB_US; i++) us[i] = un[i];
         }
 }
 
 __device__ __forceinline__ void sb_backward(float (&R)[SB_RG][SB_G], float (*zl)[64], const float * __restrict__ LU,
-                                            const int (&pv)[4], int n, float zero_val, int lane, float & pf) {
+                                            const int (&pv)[4], int n, float zero_val, int lane) {
+    float us[SB_US];
+    sb_uload(us, LU, pv, n - 1, lane);
     // groups 31 .. SB_LG: y from the bottom block, which the pushed result replaces
     for (int gb = SB_NG - 1; gb >= SB_LG; gb--) {
         float yw[SB_G], xw[SB_G];
 #pragma unroll
         for (int j = 0; j < SB_G; j++) yw[j] = R[SB_RG - 1][j];
-        sb_bgroup(xw, yw, R, zl, LU, pv, gb, n, zero_val, lane, pf);
+        sb_bgroup(xw, yw, R, zl, LU, pv, gb, n, zero_val, lane, us);
         sb_push(R, xw);
     }
     // groups SB_LG - 1 .. 0: y from LDS; the oldest solved group moves to its slot
@@ -4632,7 +4681,7 @@ __device__ __forceinline__ void sb_backward(float (&R)[SB_RG][SB_G], float (*zl)
         float yw[SB_G], xw[SB_G];
 #pragma unroll
         for (int j = 0; j < SB_G; j++) yw[j] = zl[SB_G * gb + j][lane];
-        sb_bgroup(xw, yw, R, zl, LU, pv, gb, n, zero_val, lane, pf);
+        sb_bgroup(xw, yw, R, zl, LU, pv, gb, n, zero_val, lane, us);
 #pragma unroll
         for (int j = 0; j < SB_G; j++) zl[SB_G * gb + j][lane] = R[SB_RG - 1][j];
         sb_push(R, xw);
@@ -4705,7 +4754,7 @@ k_ge_subst(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 #pragma unroll
             for (int j = 0; j < SB_G; j++) R[m][j] = Q[m][j];
     }
-    sb_backward(R, zl, LU, pv, n, g.zero_val, lane, pf);
+    sb_backward(R, zl, LU, pv, n, g.zero_val, lane);
     zl[SB_LDS][lane] = pf;   // (the window row is dead by now)
     // block m = x group m, LDS slot s = x group 24 + s
     if (act) {
