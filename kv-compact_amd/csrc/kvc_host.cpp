@@ -896,7 +896,7 @@ int run_batch(DeviceCtx * ctx, hipStream_t st, const Plan & pl, const kv_compact
     if (fork) {
         if (hipEventRecord(ctx->fork_ev, st) != hipSuccess ||
             hipStreamWaitEvent(ctx->stream2, ctx->fork_ev, 0) != hipSuccess) return KV_COMPACT_E_DEVICE;
-        launch_stats_original(g, w, sw, io.K, io.V, io.Q, ctx->stream2, s_main);
+        launch_stats_original(g, w, sw, io.K, io.V, io.Q, ctx->stream2, s_main, true);
         if (hipEventRecord(ctx->join_ev, ctx->stream2) != hipSuccess) return KV_COMPACT_E_DEVICE;
     }
     // 7. normal equations and their solution

@@ -55,8 +55,11 @@ void launch_stats(const Geom & g, const Work & w, const StatWork & sw, const flo
                   float * stats, hipStream_t st, float * S_main = nullptr);
 // the same in parts: original attention (needs S and V only), compacted
 // attention, then the statistics (needs both)
+// beside_lu: it runs on a second stream beside the factorizations, so the
+// sums with V take the form that shares a CU with a factorization block
 void launch_stats_original(const Geom & g, const Work & w, const StatWork & sw, const float * K,
-                           const float * V, const float * Q, hipStream_t st, float * S_main);
+                           const float * V, const float * Q, hipStream_t st, float * S_main,
+                           bool beside_lu = false);
 void launch_stats_compacted(const Geom & g, const Work & w, const StatWork & sw, const float * K,
                             const float * V, const float * Q, const float * beta, const float * Cv,
                             float * stats, hipStream_t st);

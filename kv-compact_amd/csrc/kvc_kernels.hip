@@ -130,6 +130,13 @@ __device__ __forceinline__ float logf_ref(float x) {
     return (float)y;
 }
 
+// lane L of each 16-lane row of v, in every lane (DPP row_newbcast, folded
+// into the instruction that uses it)
+template <int L>
+__device__ __forceinline__ float sb_bc(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xf, 0xf, false));
+}
+
 // cheap reference-query row (api.cpp:140-151): quadratic spacing over n rows
 __device__ __forceinline__ int cheap_pos(int qi, int n, int T) {
     float f = (float)(qi + 1) / (float)(n + 1);
@@ -1316,14 +1323,12 @@ k_query_columns(Geom g, const ChunkDesc * __restrict__ chunks, const float * __r
 // ---------------------------------------------------------------------------
 constexpr int SV_QB = 16, SV_VB = 64, SV_KT = 64, SV_THREADS = 256;
 
-// at most 96 VGPRs (five waves per SIMD), so that a block fits on a CU
-// beside a k_ge_lu block (four waves per SIMD at up to 104 VGPRs) while the
-// original-attention statistics overlap the factorizations
 // LDS: As[2][SV_QB][SV_KT + 1] then Vs[2][SV_KT][SV_VB] (SV_LDS bytes), given
-// at launch, so that the compiler holds the kernel to 96 VGPRs (five waves
-// per SIMD): a block then fits on a CU beside a k_ge_lu block (four waves per
-// SIMD at 104 VGPRs) while the original-attention statistics overlap the
-// factorizations
+// at launch. At 80-86 VGPRs a block does not fit on a CU beside a k_ge_lu
+// block (four waves per SIMD at 112 VGPRs leave 64): beside the
+// factorizations the sums over an fp32 V take k_stats_values_lean, which
+// does; this kernel serves the compacted statistics, a quantized V, and the
+// calls that run the statistics after the solve.
 constexpr int SV_LDS = (2 * SV_QB * (SV_KT + 1) + 2 * SV_KT * SV_VB) * 4;
 // VC: 0, or the codec of a quantized V (mode 1) read in place (g.vc)
 template <int VC>
@@ -1527,6 +1532,106 @@ k_stats_values_narrow(Geom g, const float * __restrict__ a_all, const float * __
     }
     const int q = q0 + tq, c = v0 + tv;
     if (q < mq && c < g.dv) out[(long long)q * g.dv + c] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// The original-attention sums (the k_stats_values arithmetic for mode 1 and
+// an fp32 V: out[q][v] = sum_j (a[q][j] * ascale[q]) * V[j][v], j ascending)
+// in a form that fits on a CU beside a k_ge_lu block, whose four waves per
+// SIMD leave 32 VGPRs a lane, most of the VALU's issue slots and 90 KB of LDS:
+// at most 32 VGPRs, one wave per SIMD, 48 KB of LDS. A block of four waves
+// owns 32 queries x 64 columns of one (layer, head); a wave owns eight
+// queries, lane = column, so each lane keeps eight independent sums. Tiles of
+// 64 keys are copied to LDS with global_load_lds (no registers: each wave
+// copies 16 rows of V, one 256-byte row an instruction, and its own eight
+// weight rows), the next tile while the current one is summed. A lane reads
+// the weight of query (l & 15) >> 1 for key jj + (l & 1) (l: its lane in the
+// 16-lane row), scales it, and DPP broadcasts take each query's weight into
+// the multiplies. Keys past the last whole tile come straight from memory.
+// Offsets are 32-bit, the weight rows 16-byte aligned: the host checks both.
+// grid (mh * ceil(mq / 32) * (dv / 64), L), dv a multiple of 64.
+// ---------------------------------------------------------------------------
+constexpr int SL_QW = 8, SL_QB = 4 * SL_QW, SL_KT = 64;
+constexpr int SL_LDS = (2 * SL_KT * 64 + 4 * 2 * SL_QW * SL_KT) * 4;   // V tiles, then each wave's weight tiles
+
+// key K of a pair: the weight of query Q sits in lane 2 Q + K of each
+// 16-lane row of w
+template <int K, int... Q>
+__device__ __forceinline__ void sl_key(float (&acc)[SL_QW], float w, float v, std::integer_sequence<int, Q...>) {
+    ((acc[Q] = acc[Q] + sb_bc<2 * Q + K>(w) * v), ...);
+    // (one key's products at a time: the kernel has few registers)
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <class T>
+__device__ __forceinline__ const T * sl_at(const T * base, unsigned byte_off) {
+    return reinterpret_cast<const T *>(reinterpret_cast<const char *>(base) + byte_off);
+}
+
+__global__ void __launch_bounds__(256)
+k_stats_values_lean(Geom g, const float * __restrict__ a_all, const float * __restrict__ ascale, long long a_ls,
+                    long long a_hs, long long a_rs, int n, const float * __restrict__ V,
+                    float * __restrict__ out_all, int mh, int mq) {
+    const int nqb = (mq + SL_QB - 1) / SL_QB, nvb = g.dv / 64;
+    const int layer = blockIdx.y;
+    const int h = blockIdx.x / (nqb * nvb);
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int q0 = ((blockIdx.x / nvb) % nqb) * SL_QB + SL_QW * wv, c = (blockIdx.x % nvb) * 64 + lane;
+    // the lane's weight row (rows past mq read row mq - 1; their sums are not
+    // stored) and scale
+    const int ql = min(q0 + ((lane & 15) >> 1), mq - 1);
+    const float * __restrict__ ab = a_all + layer * a_ls + h * a_hs;
+    const float sc = ascale ? ascale[((long long)layer * mh + h) * mq + ql] : 1.0f;
+    const float * __restrict__ vb = V + layer * g.ldV + (long long)h * g.dv;
+    const unsigned vrs4 = (unsigned)(g.H * g.dv) * 4u;   // bytes from one key's row of V to the next
+    extern __shared__ __align__(16) float sl_lds[];
+    float (*Vs)[SL_KT][64] = reinterpret_cast<float (*)[SL_KT][64]>(sl_lds);
+    float (*Ws)[SL_QW][SL_KT] = reinterpret_cast<float (*)[SL_QW][SL_KT]>(sl_lds + 2 * SL_KT * 64) + 2 * wv;
+    auto issue = [&](int t) {
+        const int b = t & 1;
+        const unsigned j0 = (unsigned)t * SL_KT;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const unsigned jj = 16u * wv + k;
+            __builtin_amdgcn_global_load_lds(static_cast<const void *>(sl_at(vb, (j0 + jj) * vrs4 + 4u * c)),
+                                             (__attribute__((address_space(3))) void *)&Vs[b][jj][0], 4, 0, 0);
+        }
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int q = min(q0 + 4 * r + (lane >> 4), mq - 1);
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void *>(sl_at(ab, 4u * (unsigned)(q * a_rs + j0 + 4 * (lane & 15)))),
+                (__attribute__((address_space(3))) void *)&Ws[b][4 * r][0], 16, 0, 0);
+        }
+    };
+    float acc[SL_QW];
+#pragma unroll
+    for (int q = 0; q < SL_QW; q++) acc[q] = 0.0f;
+    const int ntf = n / SL_KT;
+    if (ntf > 0) issue(0);
+    __syncthreads();   // (waits for the copies)
+    for (int t = 0; t < ntf; t++) {
+        const int b = t & 1;
+        if (t + 1 < ntf) issue(t + 1);
+#pragma unroll 2
+        for (int jj = 0; jj < SL_KT; jj += 2) {
+            const float w = Ws[b][(lane & 15) >> 1][jj + (lane & 1)] * sc;
+            const float v0 = Vs[b][jj][lane], v1 = Vs[b][jj + 1][lane];
+            sl_key<0>(acc, w, v0, std::make_integer_sequence<int, SL_QW>{});
+            sl_key<1>(acc, w, v1, std::make_integer_sequence<int, SL_QW>{});
+        }
+        __syncthreads();   // tile t + 1 has landed; every wave is done with tile t
+    }
+    // the keys past the last whole tile
+    const unsigned ao = (unsigned)(ql * a_rs);
+    for (int j = ntf * SL_KT; j < n; j++) {
+        const float w = ab[ao + (unsigned)j] * sc;
+        sl_key<0>(acc, w, *sl_at(vb, (unsigned)j * vrs4 + 4u * c), std::make_integer_sequence<int, SL_QW>{});
+    }
+    float * out = out_all + (((long long)layer * mh + h) * mq) * g.dv;
+#pragma unroll
+    for (int q = 0; q < SL_QW; q++)
+        if (q0 + q < mq) out[(long long)(q0 + q) * g.dv + c] = acc[q];
 }
 
 // ---------------------------------------------------------------------------
@@ -3186,12 +3291,12 @@ __device__ __forceinline__ void lu_steps(LuShared & sh, float (&a)[RG_SLOTS][RG_
 // steps: that trailing matrix goes to T2[sys] column-major (entry (logical
 // row 128 + k, column 128 + j) at j * 128 + k) and the physical row of each
 // of its rows to map2[sys][k]; every other entry is final and written here.
-template <bool MASKED, bool SPLIT = false>
-__global__ void __launch_bounds__(RG_THREADS)
-k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
-        const long long * __restrict__ aug_off, const float * __restrict__ X, int * __restrict__ perm_out,
-        unsigned char * __restrict__ skip_out, float * __restrict__ LU_all, int * __restrict__ redo,
-        int * __restrict__ status, float * __restrict__ T2, int * __restrict__ map2) {
+template <bool MASKED, bool SPLIT>
+__device__ __forceinline__ void
+ge_lu_body(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
+           const long long * __restrict__ aug_off, const float * __restrict__ X, int * __restrict__ perm_out,
+           unsigned char * __restrict__ skip_out, float * __restrict__ LU_all, int * __restrict__ redo,
+           int * __restrict__ status, float * __restrict__ T2, int * __restrict__ map2) {
     static_assert(!(MASKED && SPLIT), "the split factorization is the unmasked one");
     const int c_idx = blockIdx.x / g.H, h = blockIdx.x % g.H, layer = blockIdx.y;
     const ChunkDesc c = chunks[c_idx];
@@ -3444,6 +3549,36 @@ k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict_
         const int r = e / (RG_ROWS - n), j = n + e % (RG_ROWS - n);
         LU[(unsigned)(r * RG_ROWS + j)] = 0.0f;
     }
+}
+
+// The kernels. The unmasked ones are held to 112 VGPRs (amdgpu_num_vgpr
+// counts a register pair on this GPU, so 56), one under what they use
+// unconstrained and spill-free: four waves per SIMD then leave 64 VGPRs a
+// lane, which lets a block of the original-attention statistics run on the
+// same CU. The masked kernel keeps its registers.
+template <bool MASKED, bool SPLIT = false>
+__global__ void __launch_bounds__(RG_THREADS)
+k_ge_lu(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
+        const long long * __restrict__ aug_off, const float * __restrict__ X, int * __restrict__ perm_out,
+        unsigned char * __restrict__ skip_out, float * __restrict__ LU_all, int * __restrict__ redo,
+        int * __restrict__ status, float * __restrict__ T2, int * __restrict__ map2) {
+    ge_lu_body<MASKED, SPLIT>(g, chunks, aug, aug_off, X, perm_out, skip_out, LU_all, redo, status, T2, map2);
+}
+template <>
+__global__ void __launch_bounds__(RG_THREADS) __attribute__((amdgpu_num_vgpr(56)))
+k_ge_lu<false, true>(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
+        const long long * __restrict__ aug_off, const float * __restrict__ X, int * __restrict__ perm_out,
+        unsigned char * __restrict__ skip_out, float * __restrict__ LU_all, int * __restrict__ redo,
+        int * __restrict__ status, float * __restrict__ T2, int * __restrict__ map2) {
+    ge_lu_body<false, true>(g, chunks, aug, aug_off, X, perm_out, skip_out, LU_all, redo, status, T2, map2);
+}
+template <>
+__global__ void __launch_bounds__(RG_THREADS) __attribute__((amdgpu_num_vgpr(56)))
+k_ge_lu<false, false>(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
+        const long long * __restrict__ aug_off, const float * __restrict__ X, int * __restrict__ perm_out,
+        unsigned char * __restrict__ skip_out, float * __restrict__ LU_all, int * __restrict__ redo,
+        int * __restrict__ status, float * __restrict__ T2, int * __restrict__ map2) {
+    ge_lu_body<false, false>(g, chunks, aug, aug_off, X, perm_out, skip_out, LU_all, redo, status, T2, map2);
 }
 
 // ---------------------------------------------------------------------------
@@ -4397,13 +4532,6 @@ __device__ __forceinline__ void sb_push(float (&R)[SB_RG][SB_G], const float (&g
         for (int j = 0; j < SB_G; j++) R[m][j] = R[m - 1][j];
 #pragma unroll
     for (int j = 0; j < SB_G; j++) R[0][j] = g[j];
-}
-
-// lane L of each 16-lane row of v, in every lane (DPP row_newbcast, folded
-// into the instruction that uses it)
-template <int L>
-__device__ __forceinline__ float sb_bc(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x150 + L, 0xf, 0xf, false));
 }
 
 // Forward pass: the eight rows of a group side by side (eight independent
@@ -5422,7 +5550,10 @@ k_omp_select(Geom g, const ChunkDesc * __restrict__ chunks, const float * __rest
 //     x *= inv in place.
 // grid (ceil(mh * mq / ROWS), L), RSM_THREADS threads. ROWS = RSM_ROWS, or
 // RSM_ROWS_FEW when that grid would leave most CUs idle (one layer): each
-// row's sequential sum then shares its block with fewer rows.
+// row's sequential sum then shares its block with fewer rows. RSM_ROWS_FEW
+// also for the original-attention rows beside the factorizations: at 32
+// VGPRs its blocks share CUs with k_ge_lu blocks, where the 70 of RSM_ROWS
+// would keep them off the CUs they hold.
 constexpr int RSM_ROWS = 16, RSM_ROWS_FEW = 4, RSM_TILE = 256, RSM_THREADS = 64 + RSM_TILE;
 
 // tile maxima of the main scores (k_scores' tmax), for rows that are rows of S:
@@ -6537,9 +6668,9 @@ void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st)
 bool stats_narrow(const Geom & g, unsigned sv_blocks) { return (long long)sv_blocks * g.L < 256; }
 
 void launch_row_softmax(const Geom & g, float * x, int n, long long ls, long long hs, long long rs, int mh, int mq,
-                        RowMaxSrc ms, float * inv_out, hipStream_t st) {
+                        RowMaxSrc ms, float * inv_out, hipStream_t st, bool beside_lu = false) {
     const int rows = mh * mq;
-    if ((long long)cdiv(rows, RSM_ROWS) * g.L < 256)
+    if (beside_lu || (long long)cdiv(rows, RSM_ROWS) * g.L < 256)
         hipLaunchKernelGGL(k_row_softmax<RSM_ROWS_FEW>, dim3(cdiv(rows, RSM_ROWS_FEW), g.L), dim3(RSM_THREADS), 0, st,
                            x, n, ls, hs, rs, mh, mq, ms, inv_out);
     else
@@ -6548,7 +6679,7 @@ void launch_row_softmax(const Geom & g, float * x, int n, long long ls, long lon
 }
 
 void launch_stats_original(const Geom & g, const Work & w, const StatWork & sw, const float * K,
-                           const float * V, const float * Q, hipStream_t st, float * S_main) {
+                           const float * V, const float * Q, hipStream_t st, float * S_main, bool beside_lu) {
     const ChunkDesc * whole = w.chunks + g.n_chunks;      // all T keys
     const long long osl = (long long)sw.mh * sw.mq * g.T;
     const unsigned sv_blocks = (unsigned)(sw.mh * cdiv(sw.mq, SV_QB) * cdiv(g.dv, SV_VB));
@@ -6574,12 +6705,24 @@ void launch_stats_original(const Geom & g, const Work & w, const StatWork & sw, 
         launch_scores(g, whole, 1, g.T, K, Q, sw.OS, sw.mh, sw.mq, osl, (long long)sw.mq * g.T, g.T, sw.qmode, st,
                       nullptr, nullptr);
     }
-    launch_row_softmax(g, os, g.T, o_ls, o_hs, (long long)g.T, sw.mh, sw.mq, ms, sw.OI, st);
+    launch_row_softmax(g, os, g.T, o_ls, o_hs, (long long)g.T, sw.mh, sw.mq, ms, sw.OI, st, beside_lu);
     const dim3 sgrid(sv_blocks, g.L);
     if (codec_inst(g.vc) == 0 && stats_narrow(g, sv_blocks)) {
         hipLaunchKernelGGL(k_stats_values_narrow, dim3(sw.mh * cdiv(sw.mq, SVN_QB) * cdiv(g.dv, SVN_VB), g.L),
                            dim3(SV_THREADS), 0, st, g, os, sw.OI, o_ls, o_hs, (long long)g.T, g.T, V, nullptr, 1,
                            sw.OO, sw.mh, sw.mq);
+        return;
+    }
+    // beside the factorizations: the form that shares a CU with a k_ge_lu
+    // block (fp32 V, whole 64-column blocks, 16-byte aligned weight rows,
+    // 32-bit offsets)
+    const bool lean = beside_lu && codec_inst(g.vc) == 0 && g.dv % 64 == 0 && g.T % 4 == 0 &&
+                      o_ls % 4 == 0 && o_hs % 4 == 0 && (reinterpret_cast<uintptr_t>(os) & 15) == 0 &&
+                      ((long long)g.T + SL_KT) * g.H * g.dv * 4 < (1ll << 31) &&
+                      (long long)sw.mq * g.T * 4 < (1ll << 31);
+    if (lean) {
+        hipLaunchKernelGGL(k_stats_values_lean, dim3(sw.mh * cdiv(sw.mq, SL_QB) * (g.dv / 64), g.L), dim3(256),
+                           SL_LDS, st, g, os, sw.OI, o_ls, o_hs, (long long)g.T, g.T, V, sw.OO, sw.mh, sw.mq);
         return;
     }
     switch (codec_inst(g.vc)) {
