@@ -4466,7 +4466,8 @@ k_ge_solve(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
 // system in one block, two waves per SIMD. A column's 256 values sit in 32
 // groups of eight rows: 23 groups in registers, 9 in LDS (the most that lets
 // two waves share a SIMD with nothing spilled: the 23 groups take 184 of 256
-// registers, and four blocks' LDS fill the CU's 160 KB). Registers are only
+// registers, and a tenth group in LDS would leave room for three blocks of
+// four on the CU's 160 KB). Registers are only
 // indexed statically, so they form a stack: a new group enters at block 0 and
 // the others move down one block. Each pass reads the stack in a fixed order
 // with a uniform guard per block:
@@ -4495,7 +4496,8 @@ constexpr int SB_G = 8;                     // rows per group (and entries per b
 constexpr int SB_NG = RG_ROWS / SB_G;       // groups of a column
 constexpr int SB_RG = 23;                   // groups held in registers
 constexpr int SB_LG = SB_NG - SB_RG;        // groups held in LDS
-constexpr int SB_LDS = SB_LG * SB_G;        // stored LDS rows per lane (plus an eight-row window)
+constexpr int SB_LDS = SB_LG * SB_G;        // stored LDS rows per lane
+constexpr int SB_LROWS = SB_LDS + 1;        // plus one row for the sink of the cache warm-up loads
 
 // N consecutive entries of a row of the factor array (uniform address: scalar loads)
 template <int N>
@@ -4743,53 +4745,58 @@ __device__ __forceinline__ void sb_bslots(float & val, const float (&us)[SB_US],
                                           std::integer_sequence<int, D...>) {
     (sb_bslot<D + 1>(val, us, zl, gb, lane, std::make_integer_sequence<int, SB_G>{}), ...);
 }
-// the rows above col in its group (entries g0 + J, J > k), ascending
-template <int... J>
-__device__ __forceinline__ void sb_bgroup_terms(float & val, float us0, const float (&xw)[SB_G], int k,
+// the rows above row K of its group (entries g0 + J, J > K), ascending
+template <int K, int... J>
+__device__ __forceinline__ void sb_bgroup_terms(float & val, float us0, const float (&xw)[SB_G],
                                                 std::integer_sequence<int, J...>) {
-    ((val = J > k ? val - sb_bc<J>(us0) * xw[J] : val), ...);
+    ((J > K ? (void)(val = val - sb_bc<J>(us0) * xw[J]) : (void)0), ...);
 }
 
-// one group of the backward pass: its results xw from its y values yw; us
-// holds the U entries of the group's first row (the highest one below n) on
-// entry and those of the next group's first row on exit
+// row K of group gb (logical row 8 gb + K; nothing past n): its result into
+// xw[K]. us holds the row's U entries on entry and the next row's on exit.
+template <int K>
+__device__ __forceinline__ void sb_brow(float (&xw)[SB_G], float yk, const float (&R)[SB_RG][SB_G], float (*zl)[64],
+                                        const float * __restrict__ LU, const int (&pv)[4], int gb, int nx, int n,
+                                        float zero_val, int lane, float (&us)[SB_US]) {
+    const int col = SB_G * gb + K;
+    if (col >= n) return;
+    // the next row's entries (the next group's first row after row 0) while
+    // this row runs
+    float un[SB_US];
+    sb_uload(un, LU, pv, max(col - 1, 0), lane);
+    const float piv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(us[0]), K));
+    float val = zero_val;
+    if (!(fabsf(piv) < 1e-12f)) {
+        val = yk;
+        sb_bgroup_terms<K>(val, us[0], xw, std::make_integer_sequence<int, SB_G>{});
+        // solved groups in registers, newest (lowest rows) first (nx opaque:
+        // tested per row, not kept from the row before)
+        int nxr = nx;
+        asm volatile("" : "+s"(nxr));
+        sb_bblocks(val, us, R, nxr, std::make_integer_sequence<int, SB_RG>{});
+        // solved groups gb + SB_RG + 1 .. 31 in LDS slots gb + 1 .. SB_LG - 1
+        sb_bslots(val, us, zl, gb, lane, std::make_integer_sequence<int, SB_LG - 1>{});
+        val = val / piv;
+    }
+    xw[K] = val;
+#pragma unroll
+    for (int i = 0; i < SB_US; i++) us[i] = un[i];
+}
+
+// one group of the backward pass: its results xw from its y values yw, the
+// rows from the last (the highest below n) to the first, each unrolled so
+// that its place in the group is a constant (its y value a register); us
+// holds the U entries of the group's first row on entry and those of the
+// next group's first row on exit
+template <int... K>
 __device__ __forceinline__ void sb_bgroup(float (&xw)[SB_G], const float (&yw)[SB_G], const float (&R)[SB_RG][SB_G],
                                           float (*zl)[64], const float * __restrict__ LU, const int (&pv)[4],
-                                          int gb, int n, float zero_val, int lane, float (&us)[SB_US]) {
-        const int nx = min(SB_NG - 1 - gb, SB_RG);   // solved groups in registers
-        // the group's y values, read by row through the LDS window after the
-        // stored rows
+                                          int gb, int n, float zero_val, int lane, float (&us)[SB_US],
+                                          std::integer_sequence<int, K...>) {
+    const int nx = min(SB_NG - 1 - gb, SB_RG);   // solved groups in registers
 #pragma unroll
-        for (int j = 0; j < SB_G; j++) zl[SB_LDS + j][lane] = yw[j];
-#pragma unroll
-        for (int j = 0; j < SB_G; j++) xw[j] = 0.0f;
-        const int g0 = SB_G * gb;
-        for (int col = min(g0 + SB_G, n) - 1; col >= g0; col--) {
-            const int k = col - g0;
-            // the next row's entries (the next group's first row after the
-            // last one here) while this row runs
-            float un[SB_US];
-            sb_uload(un, LU, pv, max(col - 1, 0), lane);
-            const float yk = zl[SB_LDS + k][lane];
-            const float piv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(us[0]), k));
-            float val = zero_val;
-            if (!(fabsf(piv) < 1e-12f)) {
-                val = yk;
-                sb_bgroup_terms(val, us[0], xw, k, std::make_integer_sequence<int, SB_G>{});
-                // solved groups in registers, newest (lowest rows) first (nx
-                // opaque: tested per row, not kept from the row before)
-                int nxr = nx;
-                asm volatile("" : "+s"(nxr));
-                sb_bblocks(val, us, R, nxr, std::make_integer_sequence<int, SB_RG>{});
-                // solved groups gb + SB_RG + 1 .. 31 in LDS slots gb + 1 .. SB_LG - 1
-                sb_bslots(val, us, zl, gb, lane, std::make_integer_sequence<int, SB_LG - 1>{});
-                val = val / piv;
-            }
-#pragma unroll
-            for (int j = 0; j < SB_G; j++) xw[j] = k == j ? val : xw[j];
-#pragma unroll
-            for (int i = 0; i < SB_US; i++) us[i] = un[i];
-        }
+    for (int j = 0; j < SB_G; j++) xw[j] = 0.0f;
+    (sb_brow<SB_G - 1 - K>(xw, yw[SB_G - 1 - K], R, zl, LU, pv, gb, nx, n, zero_val, lane, us), ...);
 }
 
 __device__ __forceinline__ void sb_backward(float (&R)[SB_RG][SB_G], float (*zl)[64], const float * __restrict__ LU,
@@ -4801,7 +4808,7 @@ __device__ __forceinline__ void sb_backward(float (&R)[SB_RG][SB_G], float (*zl)
         float yw[SB_G], xw[SB_G];
 #pragma unroll
         for (int j = 0; j < SB_G; j++) yw[j] = R[SB_RG - 1][j];
-        sb_bgroup(xw, yw, R, zl, LU, pv, gb, n, zero_val, lane, us);
+        sb_bgroup(xw, yw, R, zl, LU, pv, gb, n, zero_val, lane, us, std::make_integer_sequence<int, SB_G>{});
         sb_push(R, xw);
     }
     // groups SB_LG - 1 .. 0: y from LDS; the oldest solved group moves to its slot
@@ -4809,14 +4816,14 @@ __device__ __forceinline__ void sb_backward(float (&R)[SB_RG][SB_G], float (*zl)
         float yw[SB_G], xw[SB_G];
 #pragma unroll
         for (int j = 0; j < SB_G; j++) yw[j] = zl[SB_G * gb + j][lane];
-        sb_bgroup(xw, yw, R, zl, LU, pv, gb, n, zero_val, lane, us);
+        sb_bgroup(xw, yw, R, zl, LU, pv, gb, n, zero_val, lane, us, std::make_integer_sequence<int, SB_G>{});
 #pragma unroll
         for (int j = 0; j < SB_G; j++) zl[SB_G * gb + j][lane] = R[SB_RG - 1][j];
         sb_push(R, xw);
     }
 }
 
-// grid (systems), block 64 * ceil(p / 64); dynamic LDS SB_LDS + SB_G rows x
+// grid (systems), block 64 * ceil(p / 64); dynamic LDS SB_LROWS rows x
 // 64 lanes per wave
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
 k_ge_subst(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restrict__ aug,
@@ -4835,7 +4842,7 @@ k_ge_subst(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
     const float * __restrict__ B = aug + aug_off[sysl] + (long long)n * n;   // row-major RHS [r][v]
     float * __restrict__ x = Cv + (((long long)layer * g.H + h) * g.t_total + c.off) * g.dv;
     extern __shared__ float sb_lds[];
-    float (*zl)[64] = reinterpret_cast<float (*)[64]>(sb_lds + (size_t)wv * (SB_LDS + SB_G) * 64);
+    float (*zl)[64] = reinterpret_cast<float (*)[64]>(sb_lds + (size_t)wv * SB_LROWS * 64);
     // permutation by logical row (lane l holds rows l, l + 64, ...); a system
     // with a skipped step is left to k_ge_solve
     int pv[4];
@@ -4883,7 +4890,7 @@ k_ge_subst(Geom g, const ChunkDesc * __restrict__ chunks, const float * __restri
             for (int j = 0; j < SB_G; j++) R[m][j] = Q[m][j];
     }
     sb_backward(R, zl, LU, pv, n, g.zero_val, lane);
-    zl[SB_LDS][lane] = pf;   // (the window row is dead by now)
+    zl[SB_LDS][lane] = pf;
     // block m = x group m, LDS slot s = x group 24 + s
     if (act) {
 #pragma unroll
@@ -6630,12 +6637,12 @@ void launch_ge_solve(const Geom & g, const Work & w, float * Cv, hipStream_t st)
     }();
     if (!old_solve) {
         const unsigned nw = cdiv(g.dv, 64);
-        const size_t lds = (size_t)nw * (SB_LDS + SB_G) * 64 * sizeof(float);
+        const size_t lds = (size_t)nw * SB_LROWS * 64 * sizeof(float);
         static int lds_ok = -1;
         if (lds_ok < 0)
             lds_ok = hipFuncSetAttribute(reinterpret_cast<const void *>(k_ge_subst),
                                          hipFuncAttributeMaxDynamicSharedMemorySize,
-                                         4 * (SB_LDS + SB_G) * 64 * (int)sizeof(float)) == hipSuccess;
+                                         4 * SB_LROWS * 64 * (int)sizeof(float)) == hipSuccess;
         hipLaunchKernelGGL(k_ge_subst, dim3(systems), dim3(64 * nw), lds, st,
                            g, w.chunks, w.aug, w.aug_off, w.perm, w.skip, w.LU, Cv);
     }
