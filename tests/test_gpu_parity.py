@@ -245,6 +245,22 @@ def test_mixed_chunk_sizes(gpu, orc):
     same(a, b)
 
 
+@pytest.mark.parametrize("T,H,d,nq", [(1000, 2, 64, 12), (1300, 3, 128, 20)])
+def test_stats_partial_query_groups(gpu, orc, T, H, d, nq):
+    """The original-attention statistics' sums that run beside the
+    factorization (d_v a multiple of 64, T a multiple of 4), with query
+    counts that fill only part of a wave's eight sums (12: the second wave
+    half used; 20: the third) and a last key tile of 40 or 20 keys; three
+    heads leave one of the four statistics heads unused."""
+    K, V = kv_cache(T, H, d, 45 + H)
+    Q = snapkv_queries(K, nq, 45 + H)
+    p = dict(target_ratio=0.2)
+    print(f"[case] stats_partial T={T} H={H} d={d} nq={nq}", flush=True)
+    a = gpu.compact(K, V, Q, T, nq, H, d, d, gpu.params(**p))
+    b = orc.compact(K, V, Q, T, nq, H, d, d, orc.params(**p))
+    same(a, b)
+
+
 def test_config3_bf16_slice(gpu, orc):
     """Long-context shape: 4 KV heads x d=256 with bf16 storage (K/V rows
     rounded to bf16, passed as KV_TYPE_BF16), two 1280-token chunks, keep 0.5
