@@ -4591,9 +4591,22 @@ __device__ __forceinline__ void sb_ftri(float (&val)[SB_G], const float4 & b, st
 // one group of the forward pass: its eight results in yg (zero past n). Rows
 // 8 gi .. 8 gi + 7 take the steps of every earlier group (the register
 // stack oldest first, then the LDS groups), then the group's own steps.
+// rows 8 gi .. 8 gi + 7 of the right-hand sides (rows past n read row n - 1)
+__device__ __forceinline__ void sb_bload(float (&b)[SB_G], const float * __restrict__ B, const int (&pv)[4], int gi,
+                                         int n, int p, int vc) {
+#pragma unroll
+    for (int t = 0; t < SB_G; t++) {
+        const int pr = sb_perm(pv, min(SB_G * gi + t, n - 1));
+        b[t] = B[(unsigned)(pr * p + vc)];
+    }
+}
+
+// bn: this group's right-hand-side values on entry (loaded during the group
+// before), the next group's on exit
 __device__ __forceinline__ void sb_fgroup(float (&yg)[SB_G], const float (&R)[SB_RG][SB_G], float (*zl)[64],
                                           const float * __restrict__ LU, const float * __restrict__ B,
-                                          const int (&pv)[4], int gi, int n, int p, int vc, int lane, float & pf) {
+                                          const int (&pv)[4], int gi, int n, int p, int vc, int lane, float & pf,
+                                          float (&bn)[SB_G]) {
     if (SB_G * gi >= n) {
 #pragma unroll
         for (int j = 0; j < SB_G; j++) yg[j] = 0.0f;
@@ -4607,10 +4620,7 @@ __device__ __forceinline__ void sb_fgroup(float (&yg)[SB_G], const float (&R)[SB
     const unsigned vb = (unsigned)(prow * RG_ROWS + 4 * (lane & 1));
     float val[SB_G];
 #pragma unroll
-    for (int t = 0; t < SB_G; t++) {
-        const int pr = sb_perm(pv, min(SB_G * gi + t, n - 1));
-        val[t] = B[(unsigned)(pr * p + vc)];
-    }
+    for (int t = 0; t < SB_G; t++) val[t] = bn[t];
     int cnt = min(gi, SB_RG);
     // (opaque to the compiler, so that each block tests it afresh rather than
     // keeping 23 comparison results alive)
@@ -4624,27 +4634,25 @@ __device__ __forceinline__ void sb_fgroup(float (&yg)[SB_G], const float (&R)[SB
     // exactly the load it needs. The last loads go past the register groups:
     // to the LDS groups, or to group gi (the group's own steps).
     float4 fb[SB_FB];
-    float w[3];
+    float w[2], bnext[SB_G];
 #pragma unroll
     for (int m = SB_RG + SB_FD - 1; m >= 0; m--) {
         const int G = min(max(cnt - 1 - m + SB_FD, 0), gi);
         fb[(m + 1) % SB_FB] = sb_fload(LU, vb + SB_G * G);
         if (m == SB_FSINK) {
-            // the next group's eight L rows (lane l: line l & 15 of row
-            // l >> 4 of each half) and right-hand-side rows (lane l: 64 bytes
-            // of row l >> 3) into the caches, so that its first loads hit
-            // them; the values only feed the sink, at the end of the group.
-            // Issued here, mid-sequence, because the loads after them in the
+            // the next group's eight L rows into the caches (lane l: line
+            // l & 15 of row l >> 4 of each half; the values only feed the
+            // sink, at the end of the group), so that its first loads hit
+            // them, and its right-hand-side values into registers. Issued
+            // here, mid-sequence, because the loads after them in the
             // in-order queue are not waited for until several blocks on.
             const int r = min(SB_G * (gi + 1) + (lane >> 4), n - 1);
             const int r2 = min(SB_G * (gi + 1) + 4 + (lane >> 4), n - 1);
-            const int r3 = min(SB_G * (gi + 1) + (lane >> 3), n - 1);
             const int pr = __builtin_amdgcn_ds_bpermute(4 * (r & 63), sb_pvslot(pv, r >> 6));
             const int pr2 = __builtin_amdgcn_ds_bpermute(4 * (r2 & 63), sb_pvslot(pv, r2 >> 6));
-            const int pr3 = __builtin_amdgcn_ds_bpermute(4 * (r3 & 63), sb_pvslot(pv, r3 >> 6));
             w[0] = LU[(unsigned)(pr * RG_ROWS + 16 * (lane & 15))];
             w[1] = LU[(unsigned)(pr2 * RG_ROWS + 16 * (lane & 15))];
-            w[2] = B[(unsigned)(pr3 * p + min(16 * (lane & 7), p - 1))];
+            sb_bload(bnext, B, pv, min(gi + 1, SB_NG - 1), n, p, vc);
         }
         if (m < SB_RG && m < cnt)
             sb_fterms(val, fb[m % SB_FB], &R[m][0], std::make_integer_sequence<int, SB_G>{});
@@ -4667,21 +4675,25 @@ __device__ __forceinline__ void sb_fgroup(float (&yg)[SB_G], const float (&R)[SB
     sb_ftri(val, cur, std::make_integer_sequence<int, SB_G>{});
 #pragma unroll
     for (int t = 0; t < SB_G; t++) yg[t] = SB_G * gi + t < n ? val[t] : 0.0f;
-    pf = fmaxf(pf, fmaxf(w[0], fmaxf(w[1], w[2])));
+    pf = fmaxf(pf, fmaxf(w[0], w[1]));
+#pragma unroll
+    for (int t = 0; t < SB_G; t++) bn[t] = bnext[t];
 }
 
 __device__ __forceinline__ void sb_forward(float (&R)[SB_RG][SB_G], float (*zl)[64], const float * __restrict__ LU,
                                            const float * __restrict__ B, const int (&pv)[4], int n, int p, int vc,
                                            int lane, float & pf) {
     // groups 0 .. SB_RG - 1 onto the register stack, the rest into LDS
+    float bn[SB_G];
+    sb_bload(bn, B, pv, 0, n, p, vc);
     for (int gi = 0; gi < SB_RG; gi++) {
         float yg[SB_G];
-        sb_fgroup(yg, R, zl, LU, B, pv, gi, n, p, vc, lane, pf);
+        sb_fgroup(yg, R, zl, LU, B, pv, gi, n, p, vc, lane, pf, bn);
         sb_push(R, yg);
     }
     for (int gi = SB_RG; gi < SB_NG; gi++) {
         float yg[SB_G];
-        sb_fgroup(yg, R, zl, LU, B, pv, gi, n, p, vc, lane, pf);
+        sb_fgroup(yg, R, zl, LU, B, pv, gi, n, p, vc, lane, pf, bn);
 #pragma unroll
         for (int j = 0; j < SB_G; j++) zl[SB_G * (gi - SB_RG) + j][lane] = yg[j];
     }
