@@ -6093,6 +6093,66 @@ k_requant8(const float * __restrict__ src, long long src_ls, long long src_ld, c
     }
 }
 
+// roundf (halves away from zero) for |y| < 2^23, as
+// trunc(y + copysign(0.5 - 2^-25, y)): three instructions instead of six.
+// Equal to roundf bit for bit on every float of that range (checked
+// exhaustively: adding 0.5 - 2^-25 carries into the next integer exactly
+// when the fraction is at least one half); a NaN gives a NaN.
+__device__ __forceinline__ float roundf_small(float y) {
+    return truncf(y + copysignf(0x1.fffffep-2f, y));
+}
+
+// One wave encodes up to 1024 elements of a row (32 blocks, Q8_0 or Q4_0,
+// the reference's arithmetic, state.h:528-567): lane l holds elements
+// 16 l .. 16 l + 15 in x (half of block l / 2; the block's amax comes from
+// the lane pair), and lanes with `on` write the block's scale and their codes
+// at so + (l / 2) * bytes-per-block. Every lane of the wave calls it.
+template <int TYPE>
+__device__ __forceinline__ void rq_encode16(const float (&x)[16], bool on, int lane, uint8_t * so) {
+    constexpr int BB = TYPE == 8 ? 34 : 18;    // bytes per block
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float t = fabsf(x[i]);
+        if (t > amax) amax = t;
+    }
+    const float o1 = __shfl_xor(amax, 1);
+    amax = o1 > amax ? o1 : amax;
+    const int b = lane >> 1, half = lane & 1;
+    uint16_t * ob = reinterpret_cast<uint16_t *>(so + b * BB);   // 2-byte aligned
+    if (on) {
+        if constexpr (TYPE == 8) {
+            const float d = amax / 127.0f;
+            const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
+            if (half == 0) ob[0] = f32_to_f16_ref(d);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint8_t q0 = (uint8_t)(int8_t)roundf_small(fmax_std(-128.0f, fmin_std(127.0f, x[2 * i] * id)));
+                const uint8_t q1 =
+                    (uint8_t)(int8_t)roundf_small(fmax_std(-128.0f, fmin_std(127.0f, x[2 * i + 1] * id)));
+                ob[1 + 8 * half + i] = (uint16_t)(q0 | ((uint16_t)q1 << 8));
+            }
+        } else {
+            const float d = amax / 7.0f;
+            const float id = (d != 0.0f) ? 7.0f / amax : 0.0f;
+            if (half == 0) ob[0] = f32_to_f16_ref(d);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint8_t by[2];
+#pragma unroll
+                for (int u = 0; u < 2; u++) {
+                    const float v0 = x[4 * i + 2 * u] * id + 8.0f;
+                    const float v1 = x[4 * i + 2 * u + 1] * id + 8.0f;
+                    const uint8_t q0 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf_small(v0)));
+                    const uint8_t q1 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf_small(v1)));
+                    by[u] = (uint8_t)(q0 | (q1 << 4));
+                }
+                ob[1 + 4 * half + i] = (uint16_t)(by[0] | ((uint16_t)by[1] << 8));
+            }
+        }
+    }
+}
+
 // The same encodings (Q8_0 / Q4_0, the same arithmetic as k_requant8) one
 // wave per row, for rows whose encoded bytes are whole 16-byte pieces at
 // 16-byte aligned addresses. A row goes in chunks of up to 1024 elements:
@@ -6166,46 +6226,7 @@ k_requant_rows(const float * __restrict__ src, long long src_ls, long long src_l
                 x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
             }
         }
-        float amax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const float t = fabsf(x[i]);
-            if (t > amax) amax = t;
-        }
-        const float o1 = __shfl_xor(amax, 1);
-        amax = o1 > amax ? o1 : amax;
-        const int b = lane >> 1, half = lane & 1;
-        uint16_t * ob = reinterpret_cast<uint16_t *>(so + b * BB);   // 2-byte aligned
-        if (on) {
-            if constexpr (TYPE == 8) {
-                const float d = amax / 127.0f;
-                const float id = (d != 0.0f) ? 127.0f / amax : 0.0f;
-                if (half == 0) ob[0] = f32_to_f16_ref(d);
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    const uint8_t q0 = (uint8_t)(int8_t)roundf(fmax_std(-128.0f, fmin_std(127.0f, x[2 * i] * id)));
-                    const uint8_t q1 = (uint8_t)(int8_t)roundf(fmax_std(-128.0f, fmin_std(127.0f, x[2 * i + 1] * id)));
-                    ob[1 + 8 * half + i] = (uint16_t)(q0 | ((uint16_t)q1 << 8));
-                }
-            } else {
-                const float d = amax / 7.0f;
-                const float id = (d != 0.0f) ? 7.0f / amax : 0.0f;
-                if (half == 0) ob[0] = f32_to_f16_ref(d);
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    uint8_t by[2];
-#pragma unroll
-                    for (int u = 0; u < 2; u++) {
-                        const float v0 = x[4 * i + 2 * u] * id + 8.0f;
-                        const float v1 = x[4 * i + 2 * u + 1] * id + 8.0f;
-                        const uint8_t q0 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v0)));
-                        const uint8_t q1 = (uint8_t)fmax_std(0.0f, fmin_std(15.0f, roundf(v1)));
-                        by[u] = (uint8_t)(q0 | (q1 << 4));
-                    }
-                    ob[1 + 4 * half + i] = (uint16_t)(by[0] | ((uint16_t)by[1] << 8));
-                }
-            }
-        }
+        rq_encode16<TYPE>(x, on, lane, so);
         // the wave's LDS writes are done before its reads of the copy
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront", "local");
@@ -6254,25 +6275,24 @@ constexpr int CT_THREADS = 256;
 constexpr int CT_ROWS = 8;
 
 // copy nr rows (row r at src_row(r), rb bytes, rb % 16 == 0) into LDS at
-// lds + r * rb, four 16-byte loads per thread in flight
+// lds + r * rb, four 16-byte loads per thread in flight. No load or store
+// sits under a per-lane condition (under one, the loads were compiled into
+// one at a time, each waited for): a piece index past the last stands for
+// the last piece, read again and stored again with the same bytes.
 template <class RowPtr>
 __device__ __forceinline__ void ct_stage(uint8_t * lds, int nr, long long rb, RowPtr src_row) {
     const int pieces = (int)(rb >> 4), n = nr * pieces;
     for (int p0 = threadIdx.x; p0 < n; p0 += 4 * CT_THREADS) {
+        int pp[4];
         uint4 v[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            const int pp = p0 + k * CT_THREADS;
-            if (pp < n) {
-                const int rl = pp / pieces, o = pp - rl * pieces;
-                v[k] = *reinterpret_cast<const uint4 *>(src_row(rl) + 16LL * o);
-            }
+            pp[k] = min(p0 + k * CT_THREADS, n - 1);
+            const int rl = pp[k] / pieces, o = pp[k] - rl * pieces;
+            v[k] = *reinterpret_cast<const uint4 *>(src_row(rl) + 16LL * o);
         }
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
-            const int pp = p0 + k * CT_THREADS;
-            if (pp < n) *reinterpret_cast<uint4 *>(lds + 16LL * pp) = v[k];
-        }
+        for (int k = 0; k < 4; k++) *reinterpret_cast<uint4 *>(lds + 16LL * pp[k]) = v[k];
     }
 }
 
@@ -6294,6 +6314,112 @@ k_dequant_tile(const uint8_t * __restrict__ src, long long row_bytes, long long 
     for (int j = threadIdx.x; j < nr * n4; j += CT_THREADS) {
         const int rl = j / n4, c = 4 * (j - rl * n4);
         out[j] = codec_dec4<TYPE>(codec_raw4_at<TYPE>(ct_lds + rl * row_bytes, c));
+    }
+}
+
+// Whether decoding a block and encoding it again gives back its own bytes,
+// which holds for every block the encoder writes. Q8_0: with the scale d a
+// positive normal f16 and the largest |q| exactly 127 (no q = -128), the
+// decoded x = d q are exact (an 11-bit by 8-bit product), amax = 127 d, the
+// new scale amax / 127 = d exactly (the same f16 bits), the inverse
+// 127 / amax = fl(1 / d), and x fl(1 / d) = q (1 + e), |e| < 2^-22, which the
+// clamp keeps and roundf takes back to q. Q4_0: the same with x = d (q - 8),
+// every q in 1..15 and the largest |q - 8| exactly 7 (amax = 7 d), so
+// x fl(1 / d) + 8 rounds back to q. Lane l tests half l & 1 of block l / 2
+// of the encoded row at `row`; its pair's result is merged in, so each lane
+// answers for the whole block (lanes without `on` answer true). Every lane
+// of the wave calls it.
+template <int TYPE>
+__device__ __forceinline__ bool recode_is_identity(const uint8_t * row, bool on, int lane) {
+    constexpr int BB = TYPE == 8 ? 34 : 18;
+    const int half = lane & 1;
+    const uint8_t * bl = row + (lane >> 1) * BB;
+    int bad = 0, ext = 1;   // (lanes without `on`)
+    bool scale_ok = true;
+    if (on) {
+        const uint32_t sb = *reinterpret_cast<const uint16_t *>(bl);
+        scale_ok = sb >= 0x0400u && sb <= 0x7BFFu;
+        ext = 0;
+        if constexpr (TYPE == 8) {
+            const uint16_t * c = reinterpret_cast<const uint16_t *>(bl + 2 + 16 * half);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint32_t w = c[i];
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const uint32_t q = (w >> (8 * k)) & 0xFFu;
+                    bad |= q == 0x80u;
+                    ext |= (q == 0x7Fu) | (q == 0x81u);
+                }
+            }
+        } else {
+            const uint16_t * c = reinterpret_cast<const uint16_t *>(bl + 2 + 8 * half);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t w = c[i];
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t q = (w >> (4 * k)) & 0xFu;
+                    bad |= q == 0u;
+                    ext |= (q == 1u) | (q == 15u);
+                }
+            }
+        }
+    }
+    bad |= __shfl_xor(bad, 1);
+    ext |= __shfl_xor(ext, 1);
+    return scale_ok && !bad && ext;
+}
+
+// Kept rows of a quantized cache decoded and re-encoded (the bytes of
+// k_requant_rows MODE 2) a tile of rows at a time, for rows of at most 1024
+// elements: the block gathers nrb whole rows (through idx) into LDS with
+// ct_stage, 16-byte pieces, each wave decodes its rows there and writes the
+// encoding over them (the wave issues all its reads of a row before its
+// first write, since every code depends on the block's amax; a row whose
+// blocks all pass recode_is_identity is left as it is), and the block
+// stores the tile as 16-byte pieces. grid ceil(L * rows / nrb), nrb * (the
+// encoded row bytes) <= RC_LDS, nrb <= CT_THREADS.
+constexpr int RC_LDS = 16384;
+
+template <int TYPE>
+__global__ void __launch_bounds__(CT_THREADS)
+k_recode_tile(const int * __restrict__ idx, long long idx_ls, int n_el, int rows, int L, int nrb,
+              uint8_t * __restrict__ dst, long long row_bytes, long long dst_ls, RowCodec sq) {
+    constexpr int BB = TYPE == 8 ? 34 : 18;
+    __shared__ __align__(16) uint8_t lds[RC_LDS];
+    __shared__ long long srco[CT_THREADS], dsto[CT_THREADS];   // byte offsets from sq.base and dst
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+    const long long nrows = (long long)L * rows, r0 = (long long)blockIdx.x * nrb;
+    const int nr = (int)min((long long)nrb, nrows - r0);
+    const int nb = n_el / 32 * BB, np = nb / 16;
+    if (tid < nr) {
+        const long long rw = r0 + tid;
+        const int l = (int)(rw / rows);
+        const long long j = rw - (long long)l * rows;
+        srco[tid] = l * sq.layer_bytes + idx[l * idx_ls + j] * sq.row_bytes;
+        dsto[tid] = l * dst_ls + j * row_bytes;
+    }
+    __syncthreads();
+    ct_stage(lds, nr, nb, [&](int rl) { return sq.base + srco[rl]; });
+    __syncthreads();
+    const bool on = lane < n_el / 16;
+    for (int rl = w; rl < nr; rl += CT_THREADS / 64) {
+        uint8_t * row = lds + rl * nb;
+        if (__all(recode_is_identity<TYPE>(row, on, lane))) continue;
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 v = on ? codec_dec4<TYPE>(codec_raw4_at<TYPE>(row, 16 * lane + 4 * i))
+                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            x[4 * i] = v.x; x[4 * i + 1] = v.y; x[4 * i + 2] = v.z; x[4 * i + 3] = v.w;
+        }
+        rq_encode16<TYPE>(x, on, lane, row);
+    }
+    __syncthreads();
+    for (int p = tid; p < nr * np; p += CT_THREADS) {
+        const int rl = p / np, o = p - rl * np;
+        *reinterpret_cast<uint4 *>(dst + dsto[rl] + 16 * o) = *reinterpret_cast<const uint4 *>(lds + 16 * p);
     }
 }
 
@@ -6855,6 +6981,18 @@ void launch_requant8(const float * src, long long src_ls, long long src_ld, cons
             if (a16(src) && src_ls % 4 == 0 && src_ld % 4 == 0) m = 0;
         } else if (a16(src) && dv % 16 == 0) {
             m = 1;
+        }
+        if (m == 2 && n_el <= RQ_CHUNK) {
+            const int nb = n_el / 32 * (type == 8 ? 34 : 18);
+            const int nrb = std::min(CT_THREADS, RC_LDS / nb);
+            const dim3 grid((unsigned)((L * (long long)rows + nrb - 1) / nrb));
+            if (type == 8)
+                hipLaunchKernelGGL(k_recode_tile<8>, grid, dim3(CT_THREADS), 0, st, idx, idx_ls, n_el, rows, L, nrb,
+                                   dst, row_bytes, dst_ls, sq);
+            else
+                hipLaunchKernelGGL(k_recode_tile<2>, grid, dim3(CT_THREADS), 0, st, idx, idx_ls, n_el, rows, L, nrb,
+                                   dst, row_bytes, dst_ls, sq);
+            return;
         }
         if (m >= 0) {
             const long long nrows = (long long)L * rows;

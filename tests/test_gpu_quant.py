@@ -196,6 +196,58 @@ def test_quantized_layers_device(gpu, orc):
         same_device(dv, l, b, H, d)
 
 
+@pytest.mark.parametrize("kt", [8, 2])
+def test_recode_noncanonical_blocks(gpu, orc, kt):
+    """K blocks the encoder never writes, spread over the cache beside ordinary
+    ones: negative, zero and subnormal scales; Q8_0 codes of -128 or with a
+    largest |q| under 127; Q4_0 codes of 0 or with a largest |q - 8| under 7.
+    The kept K rows are decoded and encoded again in place on the GPU, where
+    rows whose blocks all come back unchanged are left as they are; every
+    output must still equal the oracle's decode and encode (state.h:355-375,
+    state.h:528-567) bit for bit."""
+    L, T, H, d, vt = 2, 2560, 8, 128, 8
+    bb = ROW_BYTES[kt]
+    nb = H * d // 32
+    rng = np.random.default_rng(4300 + kt)
+    Kq = np.empty((L, T, nb * bb), np.uint8)
+    Vq = np.empty((L, T, nb * ROW_BYTES[vt]), np.uint8)
+    for l in range(L):
+        K, V = kv_cache(T, H, d, 4310 + l)
+        Kq[l], Vq[l] = quantize_rows(K, kt), quantize_rows(V, vt)
+    blk = Kq.reshape(L, T, nb, bb)
+    kind = rng.integers(0, 10, size=(L, T, nb))          # 0-4 the odd blocks, 5-9 left as written
+    scale = blk[..., 0].astype(np.uint16) | (blk[..., 1].astype(np.uint16) << 8)
+    scale = np.where(kind == 0, scale | 0x8000, scale)
+    scale = np.where(kind == 1, 0, scale)
+    scale = np.where(kind == 2, rng.integers(1, 0x400, size=scale.shape), scale).astype(np.uint16)
+    blk[..., 0] = scale & 0xFF
+    blk[..., 1] = scale >> 8
+    codes = blk[..., 2:]
+    pos = rng.integers(0, bb - 2, size=(L, T, nb))
+    if kt == 8:
+        q = codes.view(np.int8)
+        hit = (kind == 3)[..., None] & (np.arange(bb - 2) == pos[..., None])
+        q[...] = np.where(hit, np.int8(-128), q)
+        q[...] = np.where((kind == 4)[..., None], q >> 1, q)
+    else:
+        lo, hi = codes & 0xF, codes >> 4
+        hit = (kind == 3)[..., None] & (np.arange(bb - 2) == pos[..., None])
+        lo = np.where(hit, 0, lo)
+        shrink = (kind == 4)[..., None]
+        lo = np.where(shrink, 8 + ((lo.astype(np.int16) - 8) >> 1), lo)
+        hi = np.where(shrink, 8 + ((hi.astype(np.int16) - 8) >> 1), hi)
+        codes[...] = (lo | (hi << 4)).astype(np.uint8)
+    print(f"[quant] non-canonical K blocks kt={kt} L={L} T={T}", flush=True)
+    pk = dict(target_ratio=0.2, use_cheap_qref=1)
+    dv = device_call(gpu, Kq, Vq, kt, vt, L, T, H, d, gpu.params(**pk))
+    for l in range(L):
+        kept = kind[l][dv["indices"][l]]
+        assert all((kept == k).any() for k in range(10)), "every kind of block among the kept rows"
+        rb, b = orc.quantized(Kq[l], Vq[l], None, kt, vt, Kq.shape[2], Vq.shape[2], T, 0, H, d, d, orc.params(**pk))
+        assert rb == 0
+        same_device(dv, l, b, H, d)
+
+
 @pytest.mark.parametrize("typ", [8, 2])
 def test_config4_full_size(gpu, typ):
     """32 layers x 8 heads x d = 128, T = 32,768 in one device call (Q8_0 or Q4_0 keys and values)."""

@@ -440,6 +440,71 @@ def test_numpy_quantizers_match_oracle(orc):
             assert np.array_equal(a, b), (typ, s)
 
 
+def recode_identity_blocks(rows: np.ndarray, typ: int) -> np.ndarray:
+    """The GPU's test for Q8_0 / Q4_0 blocks that decode-then-encode returns
+    unchanged (k_recode_tile skips such rows): a positive normal f16 scale,
+    Q8_0 codes with no -128 and a largest |q| of 127, Q4_0 codes with no 0 and
+    a largest |q - 8| of 7. Per block of each row."""
+    bb = 34 if typ == 8 else 18
+    bl = rows.reshape(rows.shape[0], -1, bb)
+    s = bl[..., 0].astype(np.uint32) | (bl[..., 1].astype(np.uint32) << 8)
+    ok = (s >= 0x400) & (s <= 0x7BFF)
+    c = bl[..., 2:]
+    if typ == 8:
+        return ok & ~(c == 0x80).any(-1) & ((c == 0x7F) | (c == 0x81)).any(-1)
+    n = np.concatenate([c & 0xF, c >> 4], axis=-1)
+    return ok & ~(n == 0).any(-1) & ((n == 1) | (n == 15)).any(-1)
+
+
+@pytest.mark.parametrize("typ", [8, 2])
+def test_recode_identity_blocks(orc, typ):
+    """Every block that passes the GPU's identity test comes back byte for
+    byte from the oracle's decode (state.h:355-375) and encode
+    (state.h:528-567); the encoder's own blocks pass it, and blocks that fail
+    it are re-encoded to other bytes often enough that the test has teeth.
+    Scales cover the normal f16 range to its ends (0x0400, 0x7BFF)."""
+    bb, n_el = (34 if typ == 8 else 18), 256
+    nbk = n_el // 32
+    rng = np.random.default_rng(77 + typ)
+    rows = []
+    for s in range(6):   # encoder output over many magnitudes
+        x = (normal(900 + s, (64, n_el)) * np.float32(10.0 ** (2 * s - 6))).astype(np.float32)
+        rows += [orc.quantize_row(x[i], typ) for i in range(x.shape[0])]
+    # hand-made blocks: random codes, an extreme code forced in most of them,
+    # scales drawn from both ends of the normal range and everywhere else
+    ends = np.array([0x0001, 0x03FF, 0x0400, 0x0401, 0x7BFE, 0x7BFF, 0x7C00, 0x8400, 0x0000], np.uint16)
+    for _ in range(384):
+        bl = rng.integers(0, 256, size=(nbk, bb)).astype(np.uint8)
+        sc = np.where(rng.random(nbk) < 0.5, rng.choice(ends, nbk), rng.integers(0x0400, 0x7C00, nbk)).astype(np.uint16)
+        bl[:, 0], bl[:, 1] = sc & 0xFF, sc >> 8
+        for k in range(nbk):
+            if typ == 8:
+                q = rng.integers(-127, 128, size=32).astype(np.int8)
+                if rng.random() < 0.8:
+                    q[rng.integers(32)] = rng.choice([127, -127])
+                if rng.random() < 0.1:
+                    q[rng.integers(32)] = -128
+                bl[k, 2:] = q.view(np.uint8)
+            else:
+                n = rng.integers(1, 16, size=32).astype(np.uint8)
+                if rng.random() < 0.8:
+                    n[rng.integers(32)] = rng.choice([1, 15])
+                else:
+                    n = np.clip(n, 2, 14).astype(np.uint8)
+                if rng.random() < 0.1:
+                    n[rng.integers(32)] = 0
+                bl[k, 2:] = n[0::2] | (n[1::2] << 4)
+        rows.append(bl.reshape(-1))
+    rows = np.stack(rows)
+    ident = recode_identity_blocks(rows, typ)
+    back = np.stack([orc.quantize_row(orc.dequantize_row(r, typ, n_el), typ) for r in rows])
+    same = (back.reshape(rows.shape[0], nbk, bb) == rows.reshape(rows.shape[0], nbk, bb)).all(-1)
+    assert same[ident].all(), "a block that passes the test changed on decode and encode"
+    assert ident[128:384].all(), "the encoder's own blocks with normal f16 scales pass the test"
+    assert not ident[:64].any(), "(scales of 1e-6 data are f16 subnormals or zero)"
+    assert ident[384:].sum() > 500 and (~same[384:]).sum() > 500
+
+
 def test_accel_gemms_match_reference_fixture(orc):
     """The accelerator exports' CPU counterparts: orc_scores (one head) is the
     reference's mat_mul_ABt then the scale, orc_mat_mul_AB over a head's slice
