@@ -505,6 +505,25 @@ def test_recode_identity_blocks(orc, typ):
     assert ident[384:].sum() > 500 and (~same[384:]).sum() > 500
 
 
+def test_round_by_add_and_truncate():
+    """The GPU row encoder's roundf: trunc(y + copysign(0.5 - 2^-25, y)) equals
+    roundf (floor(|y| + 0.5) with y's sign) on every float with |y| < 2^23,
+    exhaustively for y >= 0 and on every negative float below 2^-1 and from
+    2^6 to 2^7 (the rounding of the sum is symmetric in the sign)."""
+    c = np.float32(0.49999997)
+    assert c == np.float32(0.5) - np.float32(2.0 ** -25)
+    step = 1 << 24
+    for b0 in range(0, 0x4B000000, step):
+        y = np.arange(b0, b0 + step, dtype=np.uint32).view(np.float32)
+        want = np.floor(y.astype(np.float64) + 0.5).astype(np.float32)
+        assert np.array_equal(np.trunc(y + c), want), hex(b0)
+    for lo, hi in ((0x80000000, 0xBF000000), (0xC2800000, 0xC3000000)):
+        y = np.arange(lo, hi, 4093, dtype=np.uint32).view(np.float32)
+        want = -np.floor(-y.astype(np.float64) + 0.5).astype(np.float32)
+        got = np.trunc(y + np.copysign(c, y))
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), hex(lo)
+
+
 def test_accel_gemms_match_reference_fixture(orc):
     """The accelerator exports' CPU counterparts: orc_scores (one head) is the
     reference's mat_mul_ABt then the scale, orc_mat_mul_AB over a head's slice
