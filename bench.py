@@ -243,11 +243,13 @@ def summarize_pmc(d: Path) -> dict:
         cw = _pmc_per_dispatch(d / "cwr" / "run_counter_collection.csv")["__amd_rocclr_copyBuffer"][1]
         out["copy_check"] = {"bytes": calib, "read_bytes_counted": _read_bytes(cr),
                              "write_bytes_counted": _write_bytes(cw)}
-    P = {n: _pmc_per_dispatch(d / n / "run_counter_collection.csv") for n in PMC_PASSES}
+    # (passes that were not run are left out: bytes alone need rd and wr)
+    P = {n: _pmc_per_dispatch(d / n / "run_counter_collection.csv") for n in PMC_PASSES
+         if (d / n / "run_counter_collection.csv").exists()}
     for k, (n, c, ms) in P["rd"].items():
-        w = P["wr"].get(k, (0, {}, 0.0))[1]
-        v1 = P["v1"].get(k, (0, {}, 0.0))[1]
-        v2 = P["v2"].get(k, (0, {}, 0.0))[1]
+        w = P.get("wr", {}).get(k, (0, {}, 0.0))[1]
+        v1 = P.get("v1", {}).get(k, (0, {}, 0.0))[1]
+        v2 = P.get("v2", {}).get(k, (0, {}, 0.0))[1]
         rb, wb = _read_bytes(c), _write_bytes(w)
         cyc = v1.get("GRBM_GUI_ACTIVE", 0.0) / N_XCD   # the dispatch's clocks
         e = {"dispatches": n, "ms": round(ms, 4), "read_bytes": int(rb), "write_bytes": int(wb),
@@ -475,6 +477,9 @@ def main():
                     help="summarise rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE csv runs under DIR "
                          "(cf/, cw/: copy calibration; bf/, bw/: one bench step) into per-kernel HBM "
                          "bytes per dispatch, printed as JSON, and exit")
+    ap.add_argument("--quantized-only", action="store_true",
+                    help="only time the quantized-cache record (32 layers, T=32768, Q8_0 and Q4_0, "
+                         "decoded in the kernels' loads and by a whole-cache pass), print it as JSON and exit")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only copy BYTES device-to-device once (the reference kernel for scaling "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE readings) and exit")
@@ -502,6 +507,10 @@ def main():
     dll = kc.bind_device_api(lib.dll)
     if not dll.kv_compact_hip_available():
         raise SystemExit("no usable GPU")
+    if a.quantized_only:
+        print(json.dumps({"quantized": quantized_mode(dll, lib, hiprt, 32, 32768, a.heads, a.dim, a.ratio, a.steps,
+                                                      a.warmup, a.seed + 7)}), flush=True)
+        return
     L, T, H, d, W = a.layers, a.T, a.heads, a.dim, a.window
     E = H * d
     p = lib.params(target_ratio=a.ratio, use_diversity=a.diversity)
