@@ -501,7 +501,17 @@ def main():
         hiprt.synchronize()
         hiprt.check(hiprt.hip().hipMemcpy(dst.value, src.value, a.copy_calibration, hiprt.D2D), "hipMemcpy D2D")
         hiprt.synchronize()
-        print(json.dumps({"copy_calibration_bytes": a.copy_calibration}), flush=True)
+        # the same copy timed (10 back to back): the rate a plain device copy
+        # reaches on this GPU, reading and writing BYTES each
+        e0, e1 = hiprt.Event(), hiprt.Event()
+        e0.record()
+        for _ in range(10):
+            hiprt.check(hiprt.hip().hipMemcpyAsync(dst.value, src.value, a.copy_calibration, hiprt.D2D, None),
+                        "hipMemcpyAsync D2D")
+        e1.record()
+        ms = e0.elapsed_ms(e1) / 10
+        print(json.dumps({"copy_calibration_bytes": a.copy_calibration, "copy_ms": round(ms, 4),
+                          "copy_gb_s": round(2 * a.copy_calibration / (ms * 1e6), 1)}), flush=True)
         return
     lib = kc.load_product()
     dll = kc.bind_device_api(lib.dll)
